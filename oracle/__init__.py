@@ -1,0 +1,231 @@
+"""ctypes binding of the CPU oracle (oracle/libhyq_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, never by the product package. The C sources
+restate the reference's algorithms; hyq_oracle.h lists what pins each one.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libhyq_oracle.so")
+
+F32, F16, Q8_0, Q4_K, Q6_K, Q2_0C, STQ1_0 = 0, 1, 8, 12, 14, 40, 42
+NAMES = {"F32": F32, "F16": F16, "Q8_0": Q8_0, "Q4_K": Q4_K, "Q6_K": Q6_K,
+         "Q2_0C": Q2_0C, "STQ1_0": STQ1_0}
+BLOCK_LEN = {F32: 1, F16: 1, Q8_0: 32, Q4_K: 256, Q6_K: 256, Q2_0C: 512, STQ1_0: 256}
+BLOCK_BYTES = {F32: 4, F16: 2, Q8_0: 34, Q4_K: 144, Q6_K: 210, Q2_0C: 130, STQ1_0: 42}
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+P = ctypes.c_void_p
+SZ = ctypes.c_size_t
+
+
+def _declare(L: ctypes.CDLL) -> None:
+    sig = {
+        "hyqo_block_len": (ctypes.c_int, [ctypes.c_int]),
+        "hyqo_block_bytes": (ctypes.c_int, [ctypes.c_int]),
+        "hyqo_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+        "hyqo_decode": (ctypes.c_int, [ctypes.c_int, P, SZ, P, SZ]),
+        "hyqo_q8_quantize": (None, [P, SZ, P, P]),
+        "hyqo_q8_deinterleave_q2c": (None, [P, SZ, P]),
+        "hyqo_row_isums": (ctypes.c_int, [ctypes.c_int, P, SZ, P, P]),
+        "hyqo_isums_per_row": (ctypes.c_int, [ctypes.c_int, SZ]),
+        "hyqo_gemv_q8_f64": (None, [ctypes.c_int, P, SZ, SZ, P, P, P, P]),
+        "hyqo_gemv_q8_bruteforce": (None, [ctypes.c_int, P, SZ, SZ, P, P, P, P]),
+        "hyqo_dot": (ctypes.c_float, [P, P, SZ]),
+        "hyqo_dot_scalar": (ctypes.c_float, [P, P, SZ]),
+        "hyqo_row_dot_f32": (ctypes.c_float, [ctypes.c_int, P, SZ, P]),
+        "hyqo_matmul": (ctypes.c_int, [ctypes.c_int, P, SZ, SZ, P, SZ, P, ctypes.c_int]),
+        "hyqo_gate_up_silu": (ctypes.c_int, [ctypes.c_int, P, P, SZ, SZ, P, P, ctypes.c_int]),
+        "hyqo_matmul_f64": (None, [ctypes.c_int, P, SZ, SZ, P, SZ, P, P]),
+        "hyqo_chunk_rows": (SZ, [SZ, ctypes.c_int]),
+        "hyqo_route": (None, [P, P, SZ, SZ, ctypes.c_int, ctypes.c_float, P, P]),
+        "hyqo_moe_experts": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, P, P, P, SZ, SZ, SZ,
+                                            P, SZ, P, P, P, SZ, P, ctypes.c_int]),
+        "hyqo_rms_norm_into": (None, [P, P, SZ, ctypes.c_float, P]),
+        "hyqo_rms_norm_rows": (None, [P, P, SZ, SZ, ctypes.c_float]),
+        "hyqo_rope_tables": (None, [SZ, ctypes.c_float, SZ, P, P]),
+        "hyqo_rope": (None, [P, SZ, SZ, P, P]),
+        "hyqo_attention": (None, [P, P, P, SZ, SZ, SZ, SZ, P]),
+        "hyqo_decode_step": (ctypes.c_int, [P, P, P, SZ, SZ, ctypes.c_int, ctypes.c_int, P,
+                                            ctypes.c_int]),
+        "hyqo_argmax": (ctypes.c_int, [P, SZ]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def row_bytes(dtype: int, cols: int) -> int:
+    return cols // BLOCK_LEN[dtype] * BLOCK_BYTES[dtype]
+
+
+def decode(dtype: int, data: np.ndarray | bytes, n: int | None = None) -> np.ndarray:
+    buf = np.frombuffer(bytes(data), dtype=np.uint8) if not isinstance(data, np.ndarray) else data
+    buf = np.ascontiguousarray(buf, dtype=np.uint8)
+    if n is None:
+        n = buf.size // BLOCK_BYTES[dtype] * BLOCK_LEN[dtype]
+    out = np.empty(n, dtype=np.float32)
+    rc = lib().hyqo_decode(dtype, _p(buf), buf.size, _p(out), n)
+    if rc != 0:
+        raise ValueError(f"decode: invalid shape for dtype {dtype}")
+    return out
+
+
+def q8_quantize(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    q = np.empty(x.size, dtype=np.int8)
+    s = np.empty((x.size + 255) // 256, dtype=np.float32)
+    lib().hyqo_q8_quantize(_p(x), x.size, _p(q), _p(s))
+    return q, s
+
+
+def q8_deinterleave_q2c(q: np.ndarray) -> np.ndarray:
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    out = np.empty_like(q)
+    lib().hyqo_q8_deinterleave_q2c(_p(q), q.size, _p(out))
+    return out
+
+
+def row_isums(dtype: int, row: np.ndarray, cols: int, q: np.ndarray) -> np.ndarray:
+    per = lib().hyqo_isums_per_row(dtype, cols)
+    out = np.empty(per, dtype=np.int32)
+    row = np.ascontiguousarray(row, dtype=np.uint8)
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    n = lib().hyqo_row_isums(dtype, _p(row), cols, _p(q), _p(out))
+    assert n == per
+    return out
+
+
+def isums(dtype: int, w: np.ndarray, rows: int, cols: int, q: np.ndarray) -> np.ndarray:
+    rb = row_bytes(dtype, cols)
+    w = np.ascontiguousarray(w, dtype=np.uint8).reshape(rows, rb)
+    return np.stack([row_isums(dtype, w[r], cols, q) for r in range(rows)])
+
+
+def gemv_q8_f64(dtype: int, w: np.ndarray, rows: int, cols: int, q: np.ndarray,
+                s: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    y = np.empty(rows, dtype=np.float64)
+    mag = np.empty(rows, dtype=np.float64)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    lib().hyqo_gemv_q8_f64(dtype, _p(w), rows, cols, _p(q), _p(s), _p(y), _p(mag))
+    return y, mag
+
+
+def gemv_q8_bruteforce(dtype: int, w: np.ndarray, rows: int, cols: int, q: np.ndarray,
+                       s: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    y = np.empty(rows, dtype=np.float64)
+    mag = np.empty(rows, dtype=np.float64)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    lib().hyqo_gemv_q8_bruteforce(dtype, _p(w), rows, cols, _p(q), _p(s), _p(y), _p(mag))
+    return y, mag
+
+
+def dot(a: np.ndarray, b: np.ndarray) -> float:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    return lib().hyqo_dot(_p(a), _p(b), a.size)
+
+
+def dot_scalar(a: np.ndarray, b: np.ndarray) -> float:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    return lib().hyqo_dot_scalar(_p(a), _p(b), a.size)
+
+
+def row_dot_f32(dtype: int, row: np.ndarray, cols: int, x: np.ndarray) -> float:
+    row = np.ascontiguousarray(row, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return lib().hyqo_row_dot_f32(dtype, _p(row), cols, _p(x))
+
+
+def matmul(dtype: int, w: np.ndarray, rows: int, cols: int, x: np.ndarray, batch: int,
+           threads: int = 0) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(batch * rows, dtype=np.float32)
+    rc = lib().hyqo_matmul(dtype, _p(w), rows, cols, _p(x), batch, _p(y), threads)
+    if rc != 0:
+        raise ValueError("matmul: invalid shape")
+    return y.reshape(batch, rows)
+
+
+def gate_up_silu(dtype: int, gate: np.ndarray, up: np.ndarray, rows: int, cols: int,
+                 x: np.ndarray, threads: int = 0) -> np.ndarray:
+    y = np.empty(rows, dtype=np.float32)
+    gate = np.ascontiguousarray(gate, dtype=np.uint8)
+    up = np.ascontiguousarray(up, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rc = lib().hyqo_gate_up_silu(dtype, _p(gate), _p(up), rows, cols, _p(x), _p(y), threads)
+    if rc != 0:
+        raise ValueError("gate_up_silu: invalid shape")
+    return y
+
+
+def matmul_f64(dtype: int, w: np.ndarray, rows: int, cols: int, x: np.ndarray,
+               batch: int) -> tuple[np.ndarray, np.ndarray]:
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(batch * rows, dtype=np.float64)
+    mag = np.empty(batch * rows, dtype=np.float64)
+    lib().hyqo_matmul_f64(dtype, _p(w), rows, cols, _p(x), batch, _p(y), _p(mag))
+    return y.reshape(batch, rows), mag.reshape(batch, rows)
+
+
+def route(logits: np.ndarray, bias: np.ndarray, used: int, normalize: bool,
+          scale: float) -> list[tuple[int, float]]:
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    bias = np.ascontiguousarray(bias, dtype=np.float32)
+    idx = np.empty(used, dtype=np.int32)
+    w = np.empty(used, dtype=np.float32)
+    lib().hyqo_route(_p(logits), _p(bias), logits.size, used, int(normalize), scale,
+                     _p(idx), _p(w))
+    return [(int(i), float(v)) for i, v in zip(idx, w)]
+
+
+def moe_experts(dtype_gate: int, dtype_down: int, gate: np.ndarray, up: np.ndarray,
+                down: np.ndarray, experts: int, hidden: int, mid: int, x: np.ndarray,
+                pairs_token: np.ndarray, pairs_expert: np.ndarray, pairs_weight: np.ndarray,
+                out: np.ndarray, threads: int = 0) -> np.ndarray:
+    gate = np.ascontiguousarray(gate, dtype=np.uint8)
+    up = np.ascontiguousarray(up, dtype=np.uint8)
+    down = np.ascontiguousarray(down, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    pt = np.ascontiguousarray(pairs_token, dtype=np.int32)
+    pe = np.ascontiguousarray(pairs_expert, dtype=np.int32)
+    pw = np.ascontiguousarray(pairs_weight, dtype=np.float32)
+    out = np.ascontiguousarray(out, dtype=np.float32).copy()
+    tokens = x.size // hidden
+    lib().hyqo_moe_experts(dtype_gate, dtype_down, _p(gate), _p(up), _p(down), experts, hidden,
+                           mid, _p(x), tokens, _p(pt), _p(pe), _p(pw), pt.size, _p(out),
+                           threads)
+    return out

@@ -1,0 +1,203 @@
+/*
+ * CPU oracle, part 2: the batch-1 decode step of the dense Hunyuan graph
+ * (src/model.rs:374-546) around the quantized matmuls.
+ *
+ * TEST INFRASTRUCTURE ONLY (checker and CPU baseline). Two arms:
+ *   int8_path = 0  the x86 path: f32 activations through Weight::matmul /
+ *                  matmul_gate_up_silu (src/model.rs:418-422, 473-474, 503,
+ *                  535-537). This is the CPU baseline of the decode step.
+ *   int8_path = 1  the int8 path the reference takes with SDOT
+ *                  (src/model.rs:403-416, 461-471, 487-501, 522-531): every
+ *                  matmul input is Q8-quantized and each output is the exact
+ *                  value of the integer formula rounded once to f32.
+ * The glue follows the x86 arms of rms_norm_into (src/model.rs:785-830),
+ * rms_norm (:832-870), rope_with_cache (:874-917), attention_into
+ * (:949-1035) and add (:1043-1077).
+ */
+#include "hyq_oracle.h"
+#include "hyq_oracle_step.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+static size_t rb_of(int dtype, size_t cols)
+{
+    return cols / (size_t)hyqo_block_len(dtype) * (size_t)hyqo_block_bytes(dtype);
+}
+
+void hyqo_rms_norm_into(const float *x, const float *w, size_t n, float eps, float *out)
+{
+    float variance = hyqo_dot(x, x, n) / (float)n;
+    float scale = 1.0f / sqrtf(variance + eps);
+    for (size_t i = 0; i < n; ++i) out[i] = x[i] * scale * w[i];
+}
+
+void hyqo_rms_norm_rows(float *x, const float *w, size_t total, size_t wlen, float eps)
+{
+    for (size_t r = 0; r + wlen <= total; r += wlen) {
+        float *row = x + r;
+        float variance = hyqo_dot(row, row, wlen) / (float)wlen;
+        float scale = 1.0f / sqrtf(variance + eps);
+        for (size_t i = 0; i < wlen; ++i) row[i] = row[i] * scale * w[i];
+    }
+}
+
+void hyqo_rope_tables(size_t head_dim, float base, size_t pos, float *cos_s, float *sin_s)
+{
+    size_t half = head_dim / 2;
+    float p = (float)pos;
+    for (size_t j = 0; j < half; ++j) {
+        float freq = powf(base, -2.0f * (float)j / (float)head_dim); /* src/model.rs:263-269 */
+        float a = p * freq;
+        sin_s[j] = sinf(a);
+        cos_s[j] = cosf(a);
+    }
+}
+
+void hyqo_rope(float *values, size_t heads, size_t dim, const float *cos_s, const float *sin_s)
+{
+    size_t half = dim / 2;
+    for (size_t h = 0; h < heads; ++h) {
+        float *head = values + h * dim;
+        for (size_t j = 0; j < half; ++j) {
+            float a = head[j], b = head[j + half];
+            head[j] = a * cos_s[j] - b * sin_s[j];
+            head[j + half] = a * sin_s[j] + b * cos_s[j];
+        }
+    }
+}
+
+void hyqo_attention(const float *q, const float *keys, const float *values, size_t heads,
+                    size_t kv_heads, size_t dim, size_t visible, float *out)
+{
+    size_t kv_width = kv_heads * dim;
+    size_t repeats = heads / kv_heads;
+    float scale = 1.0f / sqrtf((float)dim);
+    float *scores = (float *)malloc(sizeof(float) * (visible ? visible : 1));
+    memset(out, 0, sizeof(float) * heads * dim);
+    for (size_t h = 0; h < heads; ++h) {
+        size_t kvh = h / repeats;
+        const float *query = q + h * dim;
+        for (size_t p = 0; p < visible; ++p)
+            scores[p] = hyqo_dot(query, keys + p * kv_width + kvh * dim, dim) * scale;
+        float max = -INFINITY;
+        for (size_t p = 0; p < visible; ++p) max = fmaxf(max, scores[p]);
+        float sum = 0.f;
+        for (size_t p = 0; p < visible; ++p) {
+            scores[p] = expf(scores[p] - max);
+            sum += scores[p];
+        }
+        float inv = 1.0f / sum;
+        float *o = out + h * dim;
+        for (size_t p = 0; p < visible; ++p) {
+            float pr = scores[p] * inv;
+            const float *v = values + p * kv_width + kvh * dim;
+            for (size_t i = 0; i < dim; ++i) o[i] += pr * v[i];
+        }
+    }
+    free(scores);
+}
+
+/* One int8-path GEMV: y = round_f32(exact integer formula) (see hyq_oracle.h). */
+static void gemv_int8(int dtype, const uint8_t *w, size_t rows, size_t cols, const float *x,
+                      float *y)
+{
+    int8_t *q = (int8_t *)malloc(cols);
+    float *s = (float *)malloc(sizeof(float) * (cols / 256 + 1));
+    double *yd = (double *)malloc(sizeof(double) * rows);
+    hyqo_q8_quantize(x, cols, q, s);
+    hyqo_gemv_q8_f64(dtype, w, rows, cols, q, s, yd, NULL);
+    for (size_t r = 0; r < rows; ++r) y[r] = (float)yd[r];
+    free(q);
+    free(s);
+    free(yd);
+}
+
+static void linear(const hyqo_model *m, int dtype, const uint8_t *w, size_t rows, size_t cols,
+                   const float *x, float *y, int int8_path, int threads)
+{
+    if (int8_path)
+        gemv_int8(dtype, w, rows, cols, x, y);
+    else
+        hyqo_matmul(dtype, w, rows, cols, x, 1, y, threads);
+    (void)m;
+}
+
+int hyqo_decode_step(const hyqo_model *m, float *kcache, float *vcache, size_t ctx, size_t pos,
+                     int token, int int8_path, float *logits, int threads)
+{
+    size_t H = (size_t)m->hidden, D = (size_t)m->head_dim;
+    size_t qlen = (size_t)m->heads * D, kvw = (size_t)m->kv_heads * D, F = (size_t)m->ffn;
+    if (pos >= ctx || token < 0 || token >= m->vocab) return -1;
+    float *hidden = (float *)malloc(sizeof(float) * H);
+    float *xn = (float *)malloc(sizeof(float) * H);
+    float *q = (float *)malloc(sizeof(float) * qlen);
+    float *k = (float *)malloc(sizeof(float) * kvw);
+    float *v = (float *)malloc(sizeof(float) * kvw);
+    float *att = (float *)malloc(sizeof(float) * qlen);
+    float *proj = (float *)malloc(sizeof(float) * H);
+    float *gate = (float *)malloc(sizeof(float) * F);
+    float *up = (float *)malloc(sizeof(float) * F);
+    float cos_s[512], sin_s[512];
+
+    /* embedding.row_into (src/model.rs:376) */
+    size_t erb = rb_of(m->dtype_embed, H);
+    hyqo_decode(m->dtype_embed, m->embed + (size_t)token * erb, erb, hidden, H);
+    hyqo_rope_tables(D, m->rope_base, pos, cos_s, sin_s);
+
+    for (int l = 0; l < m->layers; ++l) {
+        float *kc = kcache + (size_t)l * ctx * kvw;
+        float *vc = vcache + (size_t)l * ctx * kvw;
+        hyqo_rms_norm_into(hidden, m->attn_norm[l], H, m->eps, xn);
+        linear(m, m->dtype_linear, m->wq[l], qlen, H, xn, q, int8_path, threads);
+        linear(m, m->dtype_linear, m->wk[l], kvw, H, xn, k, int8_path, threads);
+        linear(m, m->dtype_linear, m->wv[l], kvw, H, xn, v, int8_path, threads);
+        /* dense order: RoPE, then per-head Q/K RMSNorm (src/model.rs:425-446) */
+        hyqo_rope(q, (size_t)m->heads, D, cos_s, sin_s);
+        hyqo_rope(k, (size_t)m->kv_heads, D, cos_s, sin_s);
+        hyqo_rms_norm_rows(q, m->q_norm[l], qlen, D, m->eps);
+        hyqo_rms_norm_rows(k, m->k_norm[l], kvw, D, m->eps);
+        memcpy(kc + pos * kvw, k, sizeof(float) * kvw);
+        memcpy(vc + pos * kvw, v, sizeof(float) * kvw);
+        hyqo_attention(q, kc, vc, (size_t)m->heads, (size_t)m->kv_heads, D, pos + 1, att);
+        linear(m, m->dtype_linear, m->wo[l], H, qlen, att, proj, int8_path, threads);
+        for (size_t i = 0; i < H; ++i) hidden[i] += proj[i];
+        hyqo_rms_norm_into(hidden, m->ffn_norm[l], H, m->eps, xn);
+        if (int8_path) {
+            gemv_int8(m->dtype_linear, m->wgate[l], F, H, xn, gate);
+            gemv_int8(m->dtype_linear, m->wup[l], F, H, xn, up);
+            for (size_t i = 0; i < F; ++i) {
+                float g = gate[i];
+                float silu = g / (1.0f + expf(-g));
+                gate[i] = silu * up[i];
+            }
+        } else {
+            hyqo_gate_up_silu(m->dtype_linear, m->wgate[l], m->wup[l], F, H, xn, gate, threads);
+        }
+        linear(m, m->dtype_linear, m->wdown[l], H, F, gate, proj, int8_path, threads);
+        for (size_t i = 0; i < H; ++i) hidden[i] += proj[i];
+    }
+    hyqo_rms_norm_rows(hidden, m->output_norm, H, H, m->eps);
+    linear(m, m->dtype_embed, m->embed, (size_t)m->vocab, H, hidden, logits, int8_path, threads);
+
+    free(hidden);
+    free(xn);
+    free(q);
+    free(k);
+    free(v);
+    free(att);
+    free(proj);
+    free(gate);
+    free(up);
+    return 0;
+}
+
+int hyqo_argmax(const float *x, size_t n)
+{
+    /* greedy sampling (src/generation.rs:281-290): first maximum wins */
+    size_t best = 0;
+    for (size_t i = 1; i < n; ++i)
+        if (x[i] > x[best]) best = i;
+    return (int)best;
+}

@@ -1,0 +1,41 @@
+/* CPU oracle, part 2: decode-step glue (test infrastructure only). */
+#ifndef HYQ_ORACLE_STEP_H
+#define HYQ_ORACLE_STEP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Weights of a dense Hunyuan model (src/model.rs:49-76), packed GGUF bytes.
+ * The embedding doubles as the output matrix (tied, src/model.rs:194-202). */
+typedef struct {
+    int layers, hidden, heads, kv_heads, head_dim, ffn, vocab;
+    float rope_base, eps;
+    int dtype_linear, dtype_embed;
+    const uint8_t *embed;
+    const float *output_norm;
+    const uint8_t *const *wq, *const *wk, *const *wv, *const *wo;
+    const uint8_t *const *wgate, *const *wup, *const *wdown;
+    const float *const *attn_norm, *const *ffn_norm, *const *q_norm, *const *k_norm;
+} hyqo_model;
+
+void hyqo_rms_norm_into(const float *x, const float *w, size_t n, float eps, float *out);
+void hyqo_rms_norm_rows(float *x, const float *w, size_t total, size_t wlen, float eps);
+void hyqo_rope_tables(size_t head_dim, float base, size_t pos, float *cos_s, float *sin_s);
+void hyqo_rope(float *values, size_t heads, size_t dim, const float *cos_s, const float *sin_s);
+void hyqo_attention(const float *q, const float *keys, const float *values, size_t heads,
+                    size_t kv_heads, size_t dim, size_t visible, float *out);
+/* One token through Model::forward_into batch 1 (src/model.rs:374-546).
+ * kcache/vcache are [layers][ctx][kv_heads*head_dim]; the step writes
+ * position `pos` and attends over 0..=pos. */
+int hyqo_decode_step(const hyqo_model *m, float *kcache, float *vcache, size_t ctx, size_t pos,
+                     int token, int int8_path, float *logits, int threads);
+int hyqo_argmax(const float *x, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,87 @@
+"""Seeded synthetic quantized weights for tests and benchmarks.
+
+Block recipes follow the workload descriptions of the quantized matmul path:
+  fp16 scales      |N(0, 0.02)| (Q4_K d and dmin, Q2_0C d, STQ d, Q6_K d,
+                   Q8_0 d), always finite and nonzero unless overridden;
+  Q4_K             6-bit sub-scales and mins uniform 0..63 (packed as the
+                   decoder reads them, src/quant.rs:2441-2451), nibbles uniform;
+  Q2_0C            uniform code bytes;
+  STQ1_0           uniform nibble and sign bytes (exactly 25% zero digits,
+                   fixed by the codebook);
+  Q6_K             uniform ql/qh bytes, uniform int8 sub-scales;
+  Q8_0             uniform int8 quants.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+F32, F16, Q8_0, Q4_K, Q6_K, Q2_0C, STQ1_0 = 0, 1, 8, 12, 14, 40, 42
+BLOCK_LEN = {F32: 1, F16: 1, Q8_0: 32, Q4_K: 256, Q6_K: 256, Q2_0C: 512, STQ1_0: 256}
+BLOCK_BYTES = {F32: 4, F16: 2, Q8_0: 34, Q4_K: 144, Q6_K: 210, Q2_0C: 130, STQ1_0: 42}
+NAMES = {F32: "F32", F16: "F16", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K",
+         Q2_0C: "Q2_0C", STQ1_0: "STQ1_0"}
+QUANT = (Q2_0C, STQ1_0, Q4_K, Q6_K, Q8_0)
+
+
+def row_bytes(dtype: int, cols: int) -> int:
+    return cols // BLOCK_LEN[dtype] * BLOCK_BYTES[dtype]
+
+
+def _f16_scales(rng: np.random.Generator, n: int, sigma: float = 0.02) -> np.ndarray:
+    v = np.abs(rng.normal(0.0, sigma, n)).astype(np.float16)
+    v[v == 0] = np.float16(sigma)
+    return v
+
+
+def random_blocks(dtype: int, nblocks: int, seed: int = 0) -> np.ndarray:
+    """nblocks packed blocks of dtype as a flat uint8 array."""
+    rng = np.random.default_rng(seed)
+    bb = BLOCK_BYTES[dtype]
+    b = rng.integers(0, 256, size=(nblocks, bb), dtype=np.uint8)
+    if dtype == Q2_0C:
+        b[:, 0:2] = _f16_scales(rng, nblocks).view(np.uint8).reshape(nblocks, 2)
+    elif dtype == STQ1_0:
+        b[:, 40:42] = _f16_scales(rng, nblocks).view(np.uint8).reshape(nblocks, 2)
+    elif dtype == Q8_0:
+        b[:, 0:2] = _f16_scales(rng, nblocks).view(np.uint8).reshape(nblocks, 2)
+    elif dtype == Q6_K:
+        b[:, 208:210] = _f16_scales(rng, nblocks).view(np.uint8).reshape(nblocks, 2)
+    elif dtype == Q4_K:
+        b[:, 0:2] = _f16_scales(rng, nblocks).view(np.uint8).reshape(nblocks, 2)
+        b[:, 2:4] = _f16_scales(rng, nblocks).view(np.uint8).reshape(nblocks, 2)
+        s = rng.integers(0, 64, size=(nblocks, 8), dtype=np.uint8)
+        m = rng.integers(0, 64, size=(nblocks, 8), dtype=np.uint8)
+        b[:, 4:16] = pack_q4k_scales(s, m)
+    elif dtype == F32:
+        b = rng.normal(0, 1, nblocks).astype(np.float32).view(np.uint8).reshape(nblocks, 4)
+    elif dtype == F16:
+        b = rng.normal(0, 1, nblocks).astype(np.float16).view(np.uint8).reshape(nblocks, 2)
+    return np.ascontiguousarray(b).reshape(-1)
+
+
+def pack_q4k_scales(s: np.ndarray, m: np.ndarray) -> np.ndarray:
+    """Inverse of the 6-bit unpacking of src/quant.rs:2441-2451 (per row of 8)."""
+    n = s.shape[0]
+    out = np.zeros((n, 12), dtype=np.uint8)
+    for j in range(4):
+        out[:, j] = (s[:, j] & 63) | ((s[:, j + 4] >> 4) << 6)
+        out[:, j + 4] = (m[:, j] & 63) | ((m[:, j + 4] >> 4) << 6)
+        out[:, j + 8] = (s[:, j + 4] & 15) | ((m[:, j + 4] & 15) << 4)
+    return out
+
+
+def random_matrix(dtype: int, rows: int, cols: int, seed: int = 0) -> np.ndarray:
+    nb = rows * cols // BLOCK_LEN[dtype]
+    return random_blocks(dtype, nb, seed)
+
+
+def set_block_scale(dtype: int, blocks: np.ndarray, value: float, dmin: float | None = None):
+    """Overwrite every block's fp16 scale (and Q4_K dmin) in place."""
+    bb = BLOCK_BYTES[dtype]
+    b = blocks.reshape(-1, bb)
+    h = np.array([value], dtype=np.float16).view(np.uint8)
+    off = {Q2_0C: 0, STQ1_0: 40, Q8_0: 0, Q6_K: 208, Q4_K: 0}[dtype]
+    b[:, off:off + 2] = h
+    if dtype == Q4_K and dmin is not None:
+        b[:, 2:4] = np.array([dmin], dtype=np.float16).view(np.uint8)
+    return blocks
