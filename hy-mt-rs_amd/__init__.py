@@ -1,0 +1,321 @@
+"""Python binding of libhyq (include/hyq.h): MI355X quantized matmuls for hy-mt-rs.
+
+Mirrors the reference's quantized-tensor interface (src/quant.rs):
+``Weight.matmul``, ``Weight.gemv_qkv``, ``Weight.matmul_gate_up_silu``,
+``Weight.expert``, ``Weight.row``, ``decode`` and the int8 ``Q8`` buffers,
+with the same argument meanings and the same failures (ValueError where the
+reference's ``ensure!`` fails). Every call runs the HIP kernels of libhyq.so;
+there is no CPU fallback: importing without the built library, or calling
+without a GPU, raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libhyq.so")
+
+F32, F16, Q8_0, Q4_K, Q6_K, Q2_0C, STQ1_0 = 0, 1, 8, 12, 14, 40, 42
+DTYPES = {"F32": F32, "F16": F16, "Q8_0": Q8_0, "Q4_K": Q4_K, "Q6_K": Q6_K,
+          "Q2_0C": Q2_0C, "STQ1_0": STQ1_0}
+OK, EINVAL, EDTYPE, EDEVICE, ENOMEM = 0, -1, -2, -3, -4
+
+# Every exported symbol of include/hyq.h with its ctypes signature.
+P = ctypes.c_void_p
+SZ = ctypes.c_size_t
+I = ctypes.c_int
+SIGNATURES = {
+    "hyq_last_error": (ctypes.c_char_p, []),
+    "hyq_block_len": (I, [I]),
+    "hyq_block_bytes": (I, [I]),
+    "hyq_ctx_create": (I, [I, ctypes.POINTER(P)]),
+    "hyq_ctx_destroy": (None, [P]),
+    "hyq_ctx_stream": (P, [P]),
+    "hyq_sync": (I, [P]),
+    "hyq_device_alloc": (I, [P, SZ, ctypes.POINTER(P)]),
+    "hyq_device_free": (I, [P, P]),
+    "hyq_memcpy_h2d": (I, [P, P, P, SZ]),
+    "hyq_memcpy_d2h": (I, [P, P, P, SZ]),
+    "hyq_memcpy_d2d": (I, [P, P, P, SZ]),
+    "hyq_weight_upload": (I, [P, I, P, SZ, P, I, ctypes.POINTER(P)]),
+    "hyq_weight_expert": (I, [P, SZ, ctypes.POINTER(P)]),
+    "hyq_weight_release": (None, [P]),
+    "hyq_weight_info": (I, [P, ctypes.POINTER(I), P, ctypes.POINTER(I)]),
+    "hyq_matmul": (I, [P, P, P, SZ, P]),
+    "hyq_gemv_qkv": (I, [P, P, P, P, P, P, P, P]),
+    "hyq_gate_up_silu": (I, [P, P, P, P, P]),
+    "hyq_decode": (I, [P, I, P, SZ, P, SZ]),
+    "hyq_weight_row": (I, [P, P, SZ, P, SZ]),
+    "hyq_q8_create": (I, [P, SZ, ctypes.POINTER(P)]),
+    "hyq_q8_release": (None, [P]),
+    "hyq_q8_buffers": (I, [P, ctypes.POINTER(P), ctypes.POINTER(P), ctypes.POINTER(SZ)]),
+    "hyq_quantize_q8_d": (I, [P, P, SZ, P]),
+    "hyq_gemv_q8_d": (I, [P, P, P, P, P]),
+    "hyq_gemv_qkv_q8_d": (I, [P, P, P, P, P, P, P, P]),
+    "hyq_gate_up_silu_q8_d": (I, [P, P, P, P, P]),
+    "hyq_isums_per_row": (I, [I, SZ]),
+    "hyq_gemv_isums_d": (I, [P, P, P, P]),
+    "hyq_matmul_d": (I, [P, P, P, SZ, P]),
+    "hyq_dequant_rows_d": (I, [P, P, SZ, SZ, P]),
+    "hyq_decode_d": (I, [P, I, P, SZ, P, SZ]),
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libhyq.so (built by build.py / __graft_entry__.build())."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: run hy-mt-rs_amd/build.py first")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+class HyqError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"hyq error {code}: {msg}")
+        self.code = code
+
+
+def check(rc: int) -> None:
+    if rc == OK:
+        return
+    msg = lib().hyq_last_error().decode(errors="replace")
+    if rc in (EINVAL, EDTYPE):
+        raise ValueError(f"hyq error {rc}: {msg}")
+    raise HyqError(rc, msg)
+
+
+def _ptr(a: np.ndarray) -> int:
+    if not a.flags["C_CONTIGUOUS"]:
+        raise ValueError("array must be C-contiguous")
+    return a.ctypes.data
+
+
+def row_bytes(dtype: int, cols: int) -> int:
+    return cols // lib().hyq_block_len(dtype) * lib().hyq_block_bytes(dtype)
+
+
+class Context:
+    """One device and one HIP stream (include/hyq.h: hyq_ctx)."""
+
+    def __init__(self, device: int = 0):
+        h = P()
+        check(lib().hyq_ctx_create(device, ctypes.byref(h)))
+        self.handle = h.value
+        self.device = device
+
+    @property
+    def stream(self) -> int:
+        return lib().hyq_ctx_stream(self.handle)
+
+    def sync(self) -> None:
+        check(lib().hyq_sync(self.handle))
+
+    def close(self) -> None:
+        if self.handle:
+            lib().hyq_ctx_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def decode(self, dtype: int, data, n: int | None = None) -> np.ndarray:
+        """decode (src/quant.rs:1066) on the device."""
+        buf = np.ascontiguousarray(np.frombuffer(bytes(data), np.uint8)
+                                   if not isinstance(data, np.ndarray) else data, np.uint8)
+        if n is None:
+            n = buf.size // lib().hyq_block_bytes(dtype) * lib().hyq_block_len(dtype)
+        out = np.empty(n, np.float32)
+        check(lib().hyq_decode(self.handle, dtype, _ptr(buf), buf.size, _ptr(out), n))
+        return out
+
+    def array(self, a: np.ndarray) -> "DeviceArray":
+        """A device copy of a numpy array."""
+        return DeviceArray.from_host(self, a)
+
+    def empty(self, shape, dtype) -> "DeviceArray":
+        return DeviceArray(self, shape, dtype)
+
+    def upload(self, dtype: int, data: np.ndarray, dims: tuple[int, ...]) -> "Weight":
+        return Weight.upload(self, dtype, data, dims)
+
+    def q8(self, n: int) -> "Q8":
+        return Q8(self, n)
+
+
+class DeviceArray:
+    """A device buffer owned through the C ABI (hyq_device_alloc)."""
+
+    def __init__(self, ctx: Context, shape, dtype):
+        self.ctx = ctx
+        self.shape = tuple(shape) if isinstance(shape, (tuple, list)) else (int(shape),)
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape)) * self.dtype.itemsize
+        h = P()
+        check(lib().hyq_device_alloc(ctx.handle, self.nbytes, ctypes.byref(h)))
+        self.ptr = h.value
+
+    @classmethod
+    def from_host(cls, ctx: Context, a: np.ndarray) -> "DeviceArray":
+        a = np.ascontiguousarray(a)
+        d = cls(ctx, a.shape, a.dtype)
+        d.copy_from(a)
+        return d
+
+    def copy_from(self, a: np.ndarray) -> None:
+        a = np.ascontiguousarray(a, self.dtype)
+        if a.nbytes != self.nbytes:
+            raise ValueError("size mismatch")
+        check(lib().hyq_memcpy_h2d(self.ctx.handle, self.ptr, _ptr(a), self.nbytes))
+
+    def numpy(self) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype)
+        check(lib().hyq_memcpy_d2h(self.ctx.handle, _ptr(out), self.ptr, self.nbytes))
+        return out
+
+    def free(self) -> None:
+        if self.ptr and self.ctx.handle:
+            lib().hyq_device_free(self.ctx.handle, self.ptr)
+        self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Weight:
+    """A packed quantized tensor on the device (src/quant.rs:65-154)."""
+
+    def __init__(self, ctx: Context, handle: int, parent: "Weight | None" = None):
+        self.ctx = ctx
+        self.handle = handle
+        self._parent = parent
+        dt = I()
+        dims = (ctypes.c_uint64 * 3)()
+        rank = I()
+        check(lib().hyq_weight_info(handle, ctypes.byref(dt), ctypes.cast(dims, P),
+                                    ctypes.byref(rank)))
+        self.dtype = dt.value
+        self.rank = rank.value
+        self.dims = tuple(int(d) for d in dims[:self.rank])
+
+    @classmethod
+    def upload(cls, ctx: Context, dtype: int, data: np.ndarray, dims) -> "Weight":
+        buf = np.ascontiguousarray(data, np.uint8)
+        d = (ctypes.c_uint64 * 3)(*[int(v) for v in dims], *([1] * (3 - len(dims))))
+        h = P()
+        check(lib().hyq_weight_upload(ctx.handle, dtype, _ptr(buf), buf.size, ctypes.cast(d, P),
+                                      len(dims), ctypes.byref(h)))
+        return cls(ctx, h.value)
+
+    def shape(self) -> tuple[int, ...]:
+        return self.dims
+
+    @property
+    def cols(self) -> int:
+        return self.dims[0]
+
+    @property
+    def rows(self) -> int:
+        return self.dims[1]
+
+    def release(self) -> None:
+        if self.handle:
+            lib().hyq_weight_release(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
+
+    def expert(self, index: int) -> "Weight":
+        """Weight::expert (src/quant.rs:144-154): a no-copy view."""
+        h = P()
+        check(lib().hyq_weight_expert(self.handle, index, ctypes.byref(h)))
+        return Weight(self.ctx, h.value, parent=self)
+
+    def matmul(self, x: np.ndarray, batch: int) -> np.ndarray:
+        """Weight::matmul (src/quant.rs:159): x [batch*cols] -> [batch*rows]."""
+        x = np.ascontiguousarray(x, np.float32)
+        if x.size != batch * self.cols:
+            raise ValueError("invalid activation shape")
+        y = np.empty(batch * self.rows, np.float32)
+        check(lib().hyq_matmul(self.ctx.handle, self.handle, _ptr(x), batch, _ptr(y)))
+        return y
+
+    @staticmethod
+    def gemv_qkv(q: "Weight", k: "Weight", v: "Weight", x: np.ndarray):
+        """Weight::gemv_qkv (src/quant.rs:658)."""
+        x = np.ascontiguousarray(x, np.float32)
+        if x.size != q.cols:
+            raise ValueError("invalid activation shape for qkv")
+        yq, yk, yv = (np.empty(w.rows, np.float32) for w in (q, k, v))
+        check(lib().hyq_gemv_qkv(q.ctx.handle, q.handle, k.handle, v.handle, _ptr(x), _ptr(yq),
+                                 _ptr(yk), _ptr(yv)))
+        return yq, yk, yv
+
+    def matmul_gate_up_silu(self, up: "Weight", x: np.ndarray) -> np.ndarray:
+        """Weight::matmul_gate_up_silu (src/quant.rs:724)."""
+        x = np.ascontiguousarray(x, np.float32)
+        if x.size != self.cols:
+            raise ValueError("invalid activation shape for gate_up_silu")
+        y = np.empty(self.rows, np.float32)
+        check(lib().hyq_gate_up_silu(self.ctx.handle, self.handle, up.handle, _ptr(x), _ptr(y)))
+        return y
+
+    def row(self, index: int) -> np.ndarray:
+        """Weight::row (src/quant.rs:106)."""
+        out = np.empty(self.cols, np.float32)
+        check(lib().hyq_weight_row(self.ctx.handle, self.handle, index, _ptr(out), out.size))
+        return out
+
+
+class Q8:
+    """Device int8 activations with per-256 scales (src/quant.rs:861-941)."""
+
+    def __init__(self, ctx: Context, n: int):
+        self.ctx = ctx
+        h = P()
+        check(lib().hyq_q8_create(ctx.handle, n, ctypes.byref(h)))
+        self.handle = h.value
+        self.n = n
+        q, s, nn = P(), P(), SZ()
+        check(lib().hyq_q8_buffers(self.handle, ctypes.byref(q), ctypes.byref(s),
+                                   ctypes.byref(nn)))
+        self.values_ptr, self.scales_ptr = q.value, s.value
+
+    def release(self) -> None:
+        if self.handle:
+            lib().hyq_q8_release(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
+
+    def quantize_into(self, x_dev_ptr: int) -> None:
+        check(lib().hyq_quantize_q8_d(self.ctx.handle, x_dev_ptr, self.n, self.handle))
+
+
+def isums_per_row(dtype: int, cols: int) -> int:
+    return lib().hyq_isums_per_row(dtype, cols)

@@ -1,0 +1,339 @@
+// Per-format group kernels of the int8 GEMV on gfx950.
+//
+// One lane owns one 256-weight group of one row at a time: it loads the
+// group's planes with 16-byte loads, expands the codes to int8 bytes in
+// registers and accumulates v_dot4_i32_i8 products against 64 dwords of Q8
+// activations held in registers. Code offsets (Q2_0C's 2c-3, STQ's code-1,
+// Q6_K's q-32, Q4_K's mins) are folded into one multiply by a precomputed
+// activation sum instead of being applied per weight.
+//
+// Each `dot` returns the group's f32 contribution and, when EMIT is set,
+// writes the group's integer block sums in the granularity the reference's
+// SDOT kernels accumulate them (see hyq.h, hyq_gemv_isums_d).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "hyq_internal.hpp"
+
+namespace hyq {
+
+__device__ __forceinline__ float h2f(uint16_t b)
+{
+    _Float16 h;
+    __builtin_memcpy(&h, &b, 2);
+    return (float)h;
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, int b, int c)
+{
+    return __builtin_amdgcn_sdot4((int)a, b, c, false);
+}
+
+// ---------------------------------------------------------------------------
+// Q2_0C: 512-weight blocks, two 256-weight groups (halves) per block.
+// isum_half = sum (2c-3) q = 2 sum c q - 3 sum q   (src/quant.rs:1891-1951)
+// contribution = f32(isum) * (d * s_g)             (src/quant.rs:1896,1922)
+// ---------------------------------------------------------------------------
+struct GroupQ2C {
+    static constexpr int ISUMS = 1;
+    struct Data {
+        uint4 w[4];
+        uint16_t d;
+    };
+    __device__ __forceinline__ static void load(Data &D, const WView &w, int row, int g)
+    {
+        size_t blk = (size_t)row * w.nb + (g >> 1);
+        const uint4 *p = reinterpret_cast<const uint4 *>(w.p0 + blk * 128 + (g & 1) * 64);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) D.w[u] = p[u];
+        D.d = reinterpret_cast<const uint16_t *>(w.p1)[blk];
+    }
+    template <bool EMIT>
+    __device__ __forceinline__ static float dot(const Data &D, const int *act, const Q8View &x,
+                                                int g, int32_t *out)
+    {
+        int raw = 0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t c[4] = {D.w[u].x, D.w[u].y, D.w[u].z, D.w[u].w};
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                raw = sdot4(c[m] & 0x03030303u, act[16 * u + m], raw);
+                raw = sdot4((c[m] >> 2) & 0x03030303u, act[16 * u + 4 + m], raw);
+                raw = sdot4((c[m] >> 4) & 0x03030303u, act[16 * u + 8 + m], raw);
+                raw = sdot4((c[m] >> 6) & 0x03030303u, act[16 * u + 12 + m], raw);
+            }
+        }
+        int isum = 2 * raw - 3 * x.sum256[g];
+        if (EMIT) out[0] = isum;
+        return (float)isum * (h2f(D.d) * x.s[g]);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// STQ1_0: 256-weight blocks of 64 groups of 4 ternary digits (codebook).
+// isum_block = sum digit q = sum code q - sum q      (src/quant.rs:1511-1556)
+// contribution = f32(isum) * (d * s_g)               (src/quant.rs:1512,1555)
+// ---------------------------------------------------------------------------
+struct GroupSTQ {
+    static constexpr int ISUMS = 1;
+    struct Data {
+        uint4 nib[2];
+        uint2 sgn;
+        uint16_t d;
+    };
+    __device__ __forceinline__ static void load(Data &D, const WView &w, int row, int g)
+    {
+        size_t blk = (size_t)row * w.nb + g;
+        const uint4 *p = reinterpret_cast<const uint4 *>(w.p0 + blk * 32);
+        D.nib[0] = p[0];
+        D.nib[1] = p[1];
+        D.sgn = reinterpret_cast<const uint2 *>(w.p1)[blk];
+        D.d = reinterpret_cast<const uint16_t *>(w.p2)[blk];
+    }
+    // 5-bit index bytes (sign<<4 | nibble) -> codebook bytes, four at a time.
+    __device__ __forceinline__ static uint32_t lut(uint32_t idx)
+    {
+        // STQ_CODEBOOK (src/quant.rs:1081-1084) packed 4 entries per dword,
+        // little endian; v_perm_b32 selects bytes 0-3 from its second operand
+        // and 4-7 from its first.
+        constexpr uint32_t CB0 = 0x092989a9u, CB1 = 0x062686a6u, CB2 = 0x121a929au,
+                           CB3 = 0x424a626au, CB4 = 0xa1812101u, CB5 = 0xa4842404u,
+                           CB6 = 0x98901810u, CB7 = 0x68604840u;
+        uint32_t sel = idx & 0x07070707u;
+        uint32_t r0 = __builtin_amdgcn_perm(CB1, CB0, sel);
+        uint32_t r1 = __builtin_amdgcn_perm(CB3, CB2, sel);
+        uint32_t r2 = __builtin_amdgcn_perm(CB5, CB4, sel);
+        uint32_t r3 = __builtin_amdgcn_perm(CB7, CB6, sel);
+        uint32_t b3 = (idx >> 3) & 0x01010101u;
+        uint32_t m3 = (b3 << 8) - b3;
+        uint32_t b4 = (idx >> 4) & 0x01010101u;
+        uint32_t m4 = (b4 << 8) - b4;
+        uint32_t lo = (r1 & m3) | (r0 & ~m3);
+        uint32_t hi = (r3 & m3) | (r2 & ~m3);
+        return (hi & m4) | (lo & ~m4);
+    }
+    template <bool EMIT>
+    __device__ __forceinline__ static float dot(const Data &D, const int *act, const Q8View &x,
+                                                int g, int32_t *out)
+    {
+        const uint32_t nib[8] = {D.nib[0].x, D.nib[0].y, D.nib[0].z, D.nib[0].w,
+                                 D.nib[1].x, D.nib[1].y, D.nib[1].z, D.nib[1].w};
+        const uint32_t sg[2] = {D.sgn.x, D.sgn.y};
+        int raw = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+#pragma unroll
+            for (int qi = 0; qi < 4; ++qi) {
+                const uint32_t dw = nib[2 * c + (qi >> 1)];
+                const uint32_t nb = (qi & 1) ? (dw >> 4) & 0x0F0F0F0Fu : dw & 0x0F0F0F0Fu;
+                const int q = (c & 1) * 4 + qi; // quad index inside the sign dword
+                const uint32_t S = sg[c >> 1];
+                const uint32_t sb = (q <= 4 ? (S << (4 - q)) : (S >> (q - 4))) & 0x10101010u;
+                const uint32_t e = lut(nb | sb);
+#pragma unroll
+                for (int p = 0; p < 4; ++p)
+                    raw = sdot4((e >> (2 * p)) & 0x03030303u, act[16 * c + 4 * p + qi], raw);
+            }
+        }
+        int isum = raw - x.sum256[g];
+        if (EMIT) out[0] = isum;
+        return (float)isum * (h2f(D.d) * x.s[g]);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Q4_K: 256-weight superblocks, 8 sub-blocks of 32 with 6-bit scale s_j and
+// min m_j (src/quant.rs:2437-2461). Integer form (no reference int path):
+//   A = sum_j s_j * sum(q * a),  B = sum_j m_j * sum(a)
+//   contribution = s_g * (d * f32(A) - dmin * f32(B))
+// which equals the decoder's d*s_j*q - dmin*m_j dotted with the Q8 values.
+// ---------------------------------------------------------------------------
+struct GroupQ4K {
+    static constexpr int ISUMS = 2;
+    struct Data {
+        uint4 qs[8];
+        uint4 meta;
+    };
+    __device__ __forceinline__ static void load(Data &D, const WView &w, int row, int g)
+    {
+        size_t blk = (size_t)row * w.nb + g;
+        const uint4 *p = reinterpret_cast<const uint4 *>(w.p0 + blk * 128);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) D.qs[i] = p[i];
+        D.meta = reinterpret_cast<const uint4 *>(w.p1)[blk];
+    }
+    template <bool EMIT>
+    __device__ __forceinline__ static float dot(const Data &D, const int *act, const Q8View &x,
+                                                int g, int32_t *out)
+    {
+        uint32_t q[32];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            q[4 * i] = D.qs[i].x;
+            q[4 * i + 1] = D.qs[i].y;
+            q[4 * i + 2] = D.qs[i].z;
+            q[4 * i + 3] = D.qs[i].w;
+        }
+        const uint32_t m0 = D.meta.x, m1 = D.meta.y, m2 = D.meta.z, m3 = D.meta.w;
+        const uint8_t sc[12] = {
+            (uint8_t)m1,         (uint8_t)(m1 >> 8),  (uint8_t)(m1 >> 16), (uint8_t)(m1 >> 24),
+            (uint8_t)m2,         (uint8_t)(m2 >> 8),  (uint8_t)(m2 >> 16), (uint8_t)(m2 >> 24),
+            (uint8_t)m3,         (uint8_t)(m3 >> 8),  (uint8_t)(m3 >> 16), (uint8_t)(m3 >> 24)};
+        int A = 0, B = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            int s, m;
+            if (j < 4) {
+                s = sc[j] & 63;
+                m = sc[j + 4] & 63;
+            } else {
+                s = (sc[j + 4] & 15) | ((sc[j - 4] >> 6) << 4);
+                m = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
+            }
+            const int grp = j >> 1, hi = j & 1;
+            int qx = 0;
+#pragma unroll
+            for (int i4 = 0; i4 < 8; ++i4) {
+                const uint32_t dw = q[8 * grp + i4];
+                const uint32_t nb = hi ? (dw >> 4) & 0x0F0F0F0Fu : dw & 0x0F0F0F0Fu;
+                qx = sdot4(nb, act[16 * grp + 8 * hi + i4], qx);
+            }
+            A += s * qx;
+            B += m * x.sum32[8 * g + j];
+        }
+        if (EMIT) {
+            out[0] = A;
+            out[1] = B;
+        }
+        const float d = h2f((uint16_t)m0), dmin = h2f((uint16_t)(m0 >> 16));
+        return x.s[g] * (d * (float)A - dmin * (float)B);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Q6_K: 256-weight blocks, 16 planes of 16 weights with int8 sub-scales.
+// isum_plane = sum (q6 - 32) a = sum q6 a - 32 sum a  (src/quant.rs:2257-2330)
+// contribution = sum_k f32(isum_k) * ((d * s_g) * sc_k)   (src/quant.rs:2258,2281)
+// ---------------------------------------------------------------------------
+struct GroupQ6K {
+    static constexpr int ISUMS = 16;
+    struct Data {
+        uint4 q[12];
+        uint4 sc;
+        uint16_t d;
+    };
+    __device__ __forceinline__ static void load(Data &D, const WView &w, int row, int g)
+    {
+        size_t blk = (size_t)row * w.nb + g;
+        const uint4 *p = reinterpret_cast<const uint4 *>(w.p0 + blk * 192);
+#pragma unroll
+        for (int i = 0; i < 12; ++i) D.q[i] = p[i];
+        D.sc = reinterpret_cast<const uint4 *>(w.p1)[blk];
+        D.d = reinterpret_cast<const uint16_t *>(w.p2)[blk];
+    }
+    template <bool EMIT>
+    __device__ __forceinline__ static float dot(const Data &D, const int *act, const Q8View &x,
+                                                int g, int32_t *out)
+    {
+        uint32_t v[48];
+#pragma unroll
+        for (int i = 0; i < 12; ++i) {
+            v[4 * i] = D.q[i].x;
+            v[4 * i + 1] = D.q[i].y;
+            v[4 * i + 2] = D.q[i].z;
+            v[4 * i + 3] = D.q[i].w;
+        }
+        const uint32_t *ql = v;      // 32 dwords
+        const uint32_t *qh = v + 32; // 16 dwords
+        const uint32_t scw[4] = {D.sc.x, D.sc.y, D.sc.z, D.sc.w};
+        const float dd = h2f(D.d) * x.s[g];
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                int r0 = 0, r1 = 0, r2 = 0, r3 = 0;
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    const uint32_t L0 = ql[16 * c + 4 * h + i4];
+                    const uint32_t L1 = ql[16 * c + 8 + 4 * h + i4];
+                    const uint32_t H = qh[8 * c + 4 * h + i4];
+                    const uint32_t q0 = (L0 & 0x0F0F0F0Fu) | ((H << 4) & 0x30303030u);
+                    const uint32_t q1 = (L1 & 0x0F0F0F0Fu) | ((H << 2) & 0x30303030u);
+                    const uint32_t q2 = ((L0 >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u);
+                    const uint32_t q3 = ((L1 >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u);
+                    r0 = sdot4(q0, act[32 * c + 0 + 4 * h + i4], r0);
+                    r1 = sdot4(q1, act[32 * c + 8 + 4 * h + i4], r1);
+                    r2 = sdot4(q2, act[32 * c + 16 + 4 * h + i4], r2);
+                    r3 = sdot4(q3, act[32 * c + 24 + 4 * h + i4], r3);
+                }
+                const int rr[4] = {r0, r1, r2, r3};
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    const int k = 8 * c + 2 * p + h; // plane = sub-scale index
+                    const int isum = rr[p] - 32 * x.sum16[16 * g + k];
+                    if (EMIT) out[k] = isum;
+                    const int8_t s8 = (int8_t)(scw[k >> 2] >> (8 * (k & 3)));
+                    acc += (float)isum * (dd * (float)s8);
+                }
+            }
+        }
+        return acc;
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Q8_0: 32-weight blocks, eight per 256-weight group (no reference int path):
+// isum_b = sum qw q;  contribution = sum_b f32(isum_b) * (d_b * s_g)
+// ---------------------------------------------------------------------------
+struct GroupQ80 {
+    static constexpr int ISUMS = 8;
+    struct Data {
+        uint4 q[16];
+        uint4 d;
+    };
+    __device__ __forceinline__ static void load(Data &D, const WView &w, int row, int g)
+    {
+        size_t blk = (size_t)row * w.nb + 8 * g;
+        const uint4 *p = reinterpret_cast<const uint4 *>(w.p0 + blk * 32);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) D.q[i] = p[i];
+        D.d = *reinterpret_cast<const uint4 *>(w.p1 + blk * 2);
+    }
+    template <bool EMIT>
+    __device__ __forceinline__ static float dot(const Data &D, const int *act, const Q8View &x,
+                                                int g, int32_t *out)
+    {
+        const uint32_t dw[4] = {D.d.x, D.d.y, D.d.z, D.d.w};
+        const float sg = x.s[g];
+        float acc = 0.f;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            const uint4 a = D.q[2 * b], c = D.q[2 * b + 1];
+            int r = 0;
+            r = sdot4(a.x, act[8 * b + 0], r);
+            r = sdot4(a.y, act[8 * b + 1], r);
+            r = sdot4(a.z, act[8 * b + 2], r);
+            r = sdot4(a.w, act[8 * b + 3], r);
+            r = sdot4(c.x, act[8 * b + 4], r);
+            r = sdot4(c.y, act[8 * b + 5], r);
+            r = sdot4(c.z, act[8 * b + 6], r);
+            r = sdot4(c.w, act[8 * b + 7], r);
+            if (EMIT) out[b] = r;
+            const float d = h2f((uint16_t)(dw[b >> 1] >> (16 * (b & 1))));
+            acc += (float)r * (d * sg);
+        }
+        return acc;
+    }
+};
+
+template <int F> struct GroupOf;
+template <> struct GroupOf<Q2_0C> { using T = GroupQ2C; };
+template <> struct GroupOf<STQ1_0> { using T = GroupSTQ; };
+template <> struct GroupOf<Q4_K> { using T = GroupQ4K; };
+template <> struct GroupOf<Q6_K> { using T = GroupQ6K; };
+template <> struct GroupOf<Q8_0> { using T = GroupQ80; };
+
+} // namespace hyq

@@ -1,0 +1,129 @@
+// Internal types shared by the HIP kernels and the C ABI implementation.
+//
+// Device layout of a quantized weight ("planes"). A GGUF block interleaves
+// scales with quants at 34/42/130/144/210-byte strides, which leaves the
+// quants 2-byte aligned. At upload every block is split into planes, each a
+// [rows][blocks][bytes] array starting on a 256-byte boundary, so that a lane
+// loads its quants with 16-byte (dwordx4) loads. The total byte count equals
+// the GGUF byte count: the layout moves bytes, it never widens them.
+//
+//   format   plane 0 (per block)           plane 1            plane 2
+//   Q2_0C    128 B codes (bit-permuted)    2 B d (fp16)       -
+//   STQ1_0   32 B nibbles (regrouped)      8 B signs (regr.)  2 B d
+//   Q4_K     128 B qs (GGUF order)         16 B d,dmin,scales -
+//   Q6_K     192 B ql|qh (GGUF order)      16 B int8 scales   2 B d
+//   Q8_0     32 B int8 quants              2 B d              -
+//   F32/F16  raw values                    -                  -
+//
+// Q2_0C codes: within each 64-weight unit (16 bytes), device byte 4m+t holds
+// in bits 2k..2k+1 the code of weight 16k+4m+t, so that
+// (dword_m >> 2k) & 0x03030303 yields the codes of 4 consecutive weights
+// 16k+4m..16k+4m+3 (GGUF packs weight i of the unit at byte i/4, bits 2(i%4)).
+//
+// STQ1_0 nibbles: 16 groups of a 64-weight chunk c occupy 8 bytes; byte
+// 8c+4h+t holds group 16c+8h+t in its low nibble and group 16c+8h+4+t in its
+// high nibble (the GGUF order is two consecutive groups per byte). Signs: the
+// 32 groups of chunks 2j and 2j+1 occupy dword j; bit q+8t is the sign of
+// group 16(2j+q/4)+4(q%4)+t, so that (S >> q) & 0x01010101 lines up the signs
+// of 4 consecutive groups with 4 bytes.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+namespace hyq {
+
+enum Fmt : int {
+    F32 = 0,
+    F16 = 1,
+    Q8_0 = 8,
+    Q4_K = 12,
+    Q6_K = 14,
+    Q2_0C = 40,
+    STQ1_0 = 42
+};
+
+// DType::block_len / block_bytes (src/quant.rs:43-62).
+inline constexpr int block_len(int f)
+{
+    return f == F32 || f == F16 ? 1 : f == Q8_0 ? 32 : f == Q2_0C ? 512
+           : (f == Q4_K || f == Q6_K || f == STQ1_0) ? 256 : -1;
+}
+inline constexpr int block_bytes(int f)
+{
+    return f == F32 ? 4 : f == F16 ? 2 : f == Q4_K ? 144 : f == Q6_K ? 210 : f == Q8_0 ? 34
+           : f == Q2_0C ? 130 : f == STQ1_0 ? 42 : -1;
+}
+// Bytes per block in each device plane.
+inline constexpr int plane_bytes(int f, int p)
+{
+    switch (f) {
+    case Q2_0C: return p == 0 ? 128 : p == 1 ? 2 : 0;
+    case STQ1_0: return p == 0 ? 32 : p == 1 ? 8 : 2;
+    case Q4_K: return p == 0 ? 128 : p == 1 ? 16 : 0;
+    case Q6_K: return p == 0 ? 192 : p == 1 ? 16 : 2;
+    case Q8_0: return p == 0 ? 32 : p == 1 ? 2 : 0;
+    case F32: return p == 0 ? 4 : 0;
+    case F16: return p == 0 ? 2 : 0;
+    default: return 0;
+    }
+}
+inline constexpr bool is_quant(int f)
+{
+    return f == Q8_0 || f == Q4_K || f == Q6_K || f == Q2_0C || f == STQ1_0;
+}
+
+// A weight (or a view of one expert) on the device: rows x cols, nb blocks
+// per row, plane pointers at this view's first row.
+struct WView {
+    const uint8_t *p0;
+    const uint8_t *p1;
+    const uint8_t *p2;
+    int rows;
+    int nb;
+};
+
+// Q8 activations on the device (src/quant.rs:861-865) plus integer sums of
+// the int8 values over 16-, 32- and 256-element spans (the kernels use them
+// to fold the code offsets of Q2_0C, STQ1_0, Q4_K mins and Q6_K's -32).
+struct Q8View {
+    const int8_t *q;
+    const float *s;
+    const int32_t *sum16;
+    const int32_t *sum32;
+    const int32_t *sum256;
+    int n;
+};
+
+enum GemvMode : int { GEMV_PLAIN = 0, GEMV_SILU = 1, GEMV_MULTI = 2, GEMV_ISUMS = 3 };
+
+struct GemvSeg {
+    WView w;
+    float *y;
+    int row_start; // first row of this segment in the concatenated row space
+};
+
+struct GemvArgs {
+    GemvSeg seg[3];   // PLAIN/ISUMS: seg[0]; SILU: seg[0]=gate, seg[1]=up; MULTI: up to 3
+    int nseg;
+    int rows_total;   // rows in the launch's row space
+    int groups;       // cols / 256
+    Q8View x;
+    const float *residual; // PLAIN: y = residual + W x when non-null
+    int32_t *isums;        // ISUMS output
+};
+
+// Kernel launchers (defined in the .hip files). All return hipError_t as int.
+int launch_repack(int fmt, const uint8_t *gguf, size_t nblocks, int nb_per_row, uint8_t *p0,
+                  uint8_t *p1, uint8_t *p2, void *stream);
+int launch_quantize_q8(const float *x, int n, int8_t *q, float *s, int32_t *sum16,
+                       int32_t *sum32, int32_t *sum256, void *stream);
+int launch_gemv(int fmt, int mode, const GemvArgs &args, void *stream);
+int launch_dequant_rows(int fmt, WView w, int row0, int nrows, int cols, float *out,
+                        void *stream);
+int launch_decode_gguf(int fmt, const uint8_t *bytes, size_t nblocks, float *out, void *stream);
+int launch_gemm_f16(int fmt, WView w, int cols, const float *x, int batch, float *y,
+                    void *stream);
+int isums_per_group(int fmt);
+
+} // namespace hyq

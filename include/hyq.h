@@ -1,0 +1,156 @@
+/*
+ * hyq: MI355X (gfx950) quantized matrix products for hy-mt-rs.
+ *
+ * A C ABI over hand-written HIP kernels. It replaces the bodies of the
+ * reference's quantized-tensor interface (Rust, src/quant.rs) so that the
+ * GGUF reader, tokenizer, KV cache, sampler and server stay unchanged. Each
+ * declaration names the reference item it stands in for.
+ *
+ * Conventions
+ *   - Return value: HYQ_OK (0) or a negative HYQ_E* code; hyq_last_error()
+ *     gives a thread-local message. Shape/length violations return
+ *     HYQ_EINVAL, the reference's `ensure!` arms (src/quant.rs:160-166,
+ *     :665-671, :726-730, :1067-1076); an unsupported format/op pair returns
+ *     HYQ_EDTYPE. No call has undefined behaviour on bad sizes.
+ *   - Host-pointer calls (x, y, bytes in host memory) are synchronous, as the
+ *     reference returns owned Vecs. Calls ending in _d take device pointers
+ *     and are asynchronous on the context's stream (hyq_sync waits).
+ *   - Shapes follow GGUF: dims[0] is the input width (cols), dims[1] the
+ *     output rows, dims[2] the expert count (src/gguf.rs:32, quant.rs:161).
+ *   - Activations are row-major [batch, cols]; outputs are [batch, rows].
+ *   - A hyq_ctx is one device plus one HIP stream; use one per host thread.
+ *     A hyq_weight is immutable after upload and may be shared by contexts
+ *     of the same device.
+ */
+#ifndef HYQ_H
+#define HYQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* DType ids after GGUF profile resolution (src/quant.rs:17-63). 40/42 are the
+ * Tencent legacy ids, valid only under their profiles (src/quant.rs:37-38). */
+typedef enum {
+    HYQ_F32 = 0,
+    HYQ_F16 = 1,
+    HYQ_Q8_0 = 8,
+    HYQ_Q4_K = 12,
+    HYQ_Q6_K = 14,
+    HYQ_Q2_0C = 40,
+    HYQ_STQ1_0 = 42
+} hyq_dtype;
+
+enum {
+    HYQ_OK = 0,
+    HYQ_EINVAL = -1,  /* bad shape, length, index or null pointer */
+    HYQ_EDTYPE = -2,  /* format not supported by this operation */
+    HYQ_EDEVICE = -3, /* HIP runtime error */
+    HYQ_ENOMEM = -4   /* device allocation failed */
+};
+
+typedef struct hyq_ctx hyq_ctx;
+typedef struct hyq_weight hyq_weight;
+typedef struct hyq_q8 hyq_q8;
+
+/* Thread-local description of the last failure on this thread. */
+const char *hyq_last_error(void);
+/* DType::block_len / block_bytes (src/quant.rs:43-62); -1 if unknown. */
+int hyq_block_len(int dtype);
+int hyq_block_bytes(int dtype);
+
+/* ---- context: the device and stream a rayon pool stood for ---- */
+int hyq_ctx_create(int device, hyq_ctx **out);
+void hyq_ctx_destroy(hyq_ctx *ctx);
+/* The context's hipStream_t, for callers that enqueue their own work. */
+void *hyq_ctx_stream(hyq_ctx *ctx);
+int hyq_sync(hyq_ctx *ctx);
+
+/* ---- device buffers for the _d entry points (no reference counterpart: the
+ * reference is host-only; a host that drives the device-pointer calls needs
+ * them). Copies are ordered on the context stream; the h2d/d2h calls return
+ * after the copy completed. ---- */
+int hyq_device_alloc(hyq_ctx *ctx, size_t bytes, void **ptr_d);
+int hyq_device_free(hyq_ctx *ctx, void *ptr_d);
+int hyq_memcpy_h2d(hyq_ctx *ctx, void *dst_d, const void *src, size_t bytes);
+int hyq_memcpy_d2h(hyq_ctx *ctx, void *dst, const void *src_d, size_t bytes);
+int hyq_memcpy_d2d(hyq_ctx *ctx, void *dst_d, const void *src_d, size_t bytes);
+
+/* ---- weights: Weight::new over the mmap (src/quant.rs:65-97) ----
+ * Copies gguf_bytes (byte_len == rows*row_bytes*experts) to the device and
+ * re-lays it out for the kernels (same byte count); the host buffer may be
+ * unmapped afterwards. rank 2: dims = {cols, rows}; rank 3: {cols, rows, E}. */
+int hyq_weight_upload(hyq_ctx *ctx, int dtype, const uint8_t *gguf_bytes, size_t byte_len,
+                      const uint64_t *dims, int rank, hyq_weight **out);
+/* Weight::expert (src/quant.rs:144-154): a no-copy view of expert e. */
+int hyq_weight_expert(const hyq_weight *w, size_t e, hyq_weight **view);
+void hyq_weight_release(hyq_weight *w);
+/* Weight::shape / dtype (src/quant.rs:75-80). dims must hold 3 entries. */
+int hyq_weight_info(const hyq_weight *w, int *dtype, uint64_t *dims, int *rank);
+
+/* ---- host-pointer products (synchronous) ---- */
+
+/* Weight::matmul (src/quant.rs:159-344). batch == 1 runs the int8 GEMV
+ * (x quantized to Q8 as Q8::quantize_into, src/quant.rs:904-922);
+ * batch > 1 runs the f16-MFMA GEMM (weights dequantized to f16 in LDS). */
+int hyq_matmul(hyq_ctx *ctx, const hyq_weight *w, const float *x, size_t batch, float *y);
+/* Weight::gemv_qkv (src/quant.rs:658-721): one Q8 and one launch for all three. */
+int hyq_gemv_qkv(hyq_ctx *ctx, const hyq_weight *q, const hyq_weight *k, const hyq_weight *v,
+                 const float *x, float *yq, float *yk, float *yv);
+/* Weight::matmul_gate_up_silu (src/quant.rs:724-841): y = silu(gate x) * (up x). */
+int hyq_gate_up_silu(hyq_ctx *ctx, const hyq_weight *gate, const hyq_weight *up,
+                     const float *x, float *y);
+/* decode (src/quant.rs:1066-1079) on the device: n values from whole blocks. */
+int hyq_decode(hyq_ctx *ctx, int dtype, const uint8_t *bytes, size_t byte_len, float *out,
+               size_t n);
+/* Weight::row_into (src/quant.rs:123-142): decode one row (cols values). */
+int hyq_weight_row(hyq_ctx *ctx, const hyq_weight *w, size_t row, float *out, size_t n);
+
+/* ---- device-pointer products (asynchronous on the context stream) ---- */
+
+/* Q8::new (src/quant.rs:896-902): int8 activations of length n with one f32
+ * scale per 256 values, plus the per-16/32/256 integer sums the kernels use. */
+int hyq_q8_create(hyq_ctx *ctx, size_t n, hyq_q8 **out);
+void hyq_q8_release(hyq_q8 *q8);
+/* Device addresses of the int8 values [n] and scales [ceil(n/256)]. */
+int hyq_q8_buffers(const hyq_q8 *q8, int8_t **values_d, float **scales_d, size_t *n);
+/* Q8::quantize_into (src/quant.rs:904-922). */
+int hyq_quantize_q8_d(hyq_ctx *ctx, const float *x_d, size_t n, hyq_q8 *q8);
+/* Weight::gemv_q8_fast (src/quant.rs:354-357); y = residual + W x when
+ * residual_d is non-null (the `add` that follows, src/model.rs:476, :512). */
+int hyq_gemv_q8_d(hyq_ctx *ctx, const hyq_weight *w, const hyq_q8 *x, const float *residual_d,
+                  float *y_d);
+/* Weight::gemv_qkv_fast (src/quant.rs:441-538). */
+int hyq_gemv_qkv_q8_d(hyq_ctx *ctx, const hyq_weight *q, const hyq_weight *k,
+                      const hyq_weight *v, const hyq_q8 *x, float *yq_d, float *yk_d,
+                      float *yv_d);
+/* Weight::matmul_gate_up_silu_fast (src/quant.rs:540-651). */
+int hyq_gate_up_silu_q8_d(hyq_ctx *ctx, const hyq_weight *gate, const hyq_weight *up,
+                          const hyq_q8 *x, float *y_d);
+/* The integer block sums of the int8 GEMV (isums_d is [rows][per_row] int32,
+ * per_row from hyq_isums_per_row), from the same device code as
+ * hyq_gemv_q8_d. Granularity as the reference's SDOT kernels accumulate:
+ * STQ1_0 one per block (src/quant.rs:1511-1556), Q2_0C two per block
+ * (:1891-1951), Q6_K sixteen per block (:2257-2330); Q4_K (A, B) and Q8_0 one
+ * per 32-block are this library's definitions (no reference int path). */
+int hyq_isums_per_row(int dtype, size_t cols);
+int hyq_gemv_isums_d(hyq_ctx *ctx, const hyq_weight *w, const hyq_q8 *x, int32_t *isums_d);
+/* Weight::matmul for batch >= 2 on device buffers: x_d [batch, cols] f32,
+ * y_d [batch, rows] f32 (src/quant.rs:272-344). */
+int hyq_matmul_d(hyq_ctx *ctx, const hyq_weight *w, const float *x_d, size_t batch,
+                 float *y_d);
+/* decode of rows [row0, row0+nrows) to f32 on the device (Weight::row_into /
+ * to_vec, src/quant.rs:99-142). */
+int hyq_dequant_rows_d(hyq_ctx *ctx, const hyq_weight *w, size_t row0, size_t nrows,
+                       float *out_d);
+/* decode of raw GGUF block bytes already on the device. */
+int hyq_decode_d(hyq_ctx *ctx, int dtype, const uint8_t *bytes_d, size_t byte_len,
+                 float *out_d, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
