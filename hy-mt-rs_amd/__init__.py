@@ -61,7 +61,29 @@ SIGNATURES = {
     "hyq_matmul_d": (I, [P, P, P, SZ, P]),
     "hyq_dequant_rows_d": (I, [P, P, SZ, SZ, P]),
     "hyq_decode_d": (I, [P, I, P, SZ, P, SZ]),
+    "hyq_embed_row_d": (I, [P, P, P, P]),
+    "hyq_rms_norm_q8_d": (I, [P, P, P, SZ, ctypes.c_float, P, P]),
+    "hyq_rope_norm_append_d": (I, [P, P, P, P, P, P, P, P, SZ, SZ, SZ, ctypes.c_float, P, P]),
+    "hyq_attention_scratch_floats": (SZ, [SZ, SZ]),
+    "hyq_attention_d": (I, [P, P, P, P, P, SZ, SZ, SZ, SZ, P, P, P]),
+    "hyq_argmax_d": (I, [P, P, SZ, P, P]),
+    "hyq_dense_create": (I, [P, P, SZ, ctypes.POINTER(P)]),
+    "hyq_dense_destroy": (None, [P]),
+    "hyq_dense_set_layer": (I, [P, I, P, P, P, P, P, P, P, P, P, P, P]),
+    "hyq_dense_set_output": (I, [P, P, P, P]),
+    "hyq_dense_load_kv": (I, [P, I, SZ, P, P]),
+    "hyq_dense_set_position": (I, [P, SZ]),
+    "hyq_dense_get_position": (I, [P, ctypes.POINTER(SZ)]),
+    "hyq_dense_forward": (I, [P, ctypes.c_int32, P, P]),
+    "hyq_dense_generate": (I, [P, ctypes.c_int32, SZ, I, P]),
 }
+
+
+class DenseConfig(ctypes.Structure):
+    """hyq_dense_config: the Config fields the decode step uses (src/model.rs:29-40)."""
+    _fields_ = [("layers", I), ("hidden", I), ("heads", I), ("kv_heads", I),
+                ("head_dim", I), ("ffn", I), ("vocab", I), ("rope_base", ctypes.c_float),
+                ("rms_eps", ctypes.c_float)]
 
 _lib = None
 
@@ -319,3 +341,74 @@ class Q8:
 
 def isums_per_row(dtype: int, cols: int) -> int:
     return lib().hyq_isums_per_row(dtype, cols)
+
+
+class DenseDecoder:
+    """Batch-1 decode of the dense graph on the device (Model::forward_into,
+    src/model.rs:374-546, plus greedy sampling). Weights are borrowed
+    ``Weight`` objects; norm vectors are f32 numpy arrays."""
+
+    def __init__(self, ctx: Context, cfg: DenseConfig, context: int):
+        self.ctx = ctx
+        self.cfg = cfg
+        h = P()
+        check(lib().hyq_dense_create(ctx.handle, ctypes.byref(cfg), context, ctypes.byref(h)))
+        self.handle = h.value
+        self._keep = []
+
+    def close(self) -> None:
+        if self.handle:
+            lib().hyq_dense_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_layer(self, layer: int, q, k, v, o, gate, up, down, attn_norm, ffn_norm,
+                  q_norm, k_norm) -> None:
+        norms = [np.ascontiguousarray(a, np.float32) for a in (attn_norm, ffn_norm, q_norm,
+                                                               k_norm)]
+        check(lib().hyq_dense_set_layer(self.handle, layer, q.handle, k.handle, v.handle,
+                                        o.handle, gate.handle, up.handle, down.handle,
+                                        *[_ptr(a) for a in norms]))
+        self._keep.extend([q, k, v, o, gate, up, down])
+
+    def set_output(self, embedding, output, output_norm) -> None:
+        on = np.ascontiguousarray(output_norm, np.float32)
+        check(lib().hyq_dense_set_output(self.handle, embedding.handle, output.handle, _ptr(on)))
+        self._keep.extend([embedding, output])
+
+    def load_kv(self, layer: int, keys: np.ndarray, values: np.ndarray) -> None:
+        keys = np.ascontiguousarray(keys, np.float32)
+        values = np.ascontiguousarray(values, np.float32)
+        kvw = self.cfg.kv_heads * self.cfg.head_dim
+        if keys.size != values.size or keys.size % kvw:
+            raise ValueError("keys/values must be [positions, kv_heads*head_dim]")
+        check(lib().hyq_dense_load_kv(self.handle, layer, keys.size // kvw, _ptr(keys),
+                                      _ptr(values)))
+
+    @property
+    def position(self) -> int:
+        p = SZ()
+        check(lib().hyq_dense_get_position(self.handle, ctypes.byref(p)))
+        return p.value
+
+    @position.setter
+    def position(self, pos: int) -> None:
+        check(lib().hyq_dense_set_position(self.handle, pos))
+
+    def forward(self, token: int, want_logits: bool = True):
+        logits = np.empty(self.cfg.vocab, np.float32) if want_logits else None
+        nxt = ctypes.c_int32()
+        check(lib().hyq_dense_forward(self.handle, token,
+                                      _ptr(logits) if logits is not None else None,
+                                      ctypes.byref(nxt)))
+        return logits, nxt.value
+
+    def generate(self, token: int, steps: int, use_graph: bool = True) -> np.ndarray:
+        out = np.empty(steps, np.int32)
+        check(lib().hyq_dense_generate(self.handle, token, steps, int(use_graph), _ptr(out)))
+        return out

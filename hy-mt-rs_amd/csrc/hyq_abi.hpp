@@ -1,0 +1,132 @@
+// Internal state behind the C ABI handles, shared by hyq_api.cpp and
+// hyq_dense.cpp (not installed; include/hyq.h is the public boundary).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <memory>
+#include <string>
+
+#include "../../include/hyq.h"
+#include "hyq_internal.hpp"
+
+namespace hyq {
+
+// Records a thread-local message for hyq_last_error and returns code.
+int fail(int code, const char *fmt, ...);
+int hip_fail(hipError_t e, const char *what);
+
+#define HYQ_HIP(call, what)                                                                    \
+    do {                                                                                       \
+        hipError_t e_ = (call);                                                                \
+        if (e_ != hipSuccess) return ::hyq::hip_fail(e_, what);                                \
+    } while (0)
+
+#define HYQ_LAUNCH(call, what)                                                                 \
+    do {                                                                                       \
+        int e_ = (call);                                                                       \
+        if (e_ != 0) return ::hyq::hip_fail((hipError_t)e_, what);                             \
+    } while (0)
+
+// Makes the context's device current for the scope of one call.
+struct DeviceGuard {
+    int prev = -1;
+    bool ok = true;
+    explicit DeviceGuard(int dev)
+    {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) ok = hipSetDevice(dev) == hipSuccess;
+    }
+    ~DeviceGuard()
+    {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+struct DeviceBuffer {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+    int device = 0;
+    DeviceBuffer() = default;
+    DeviceBuffer(const DeviceBuffer &) = delete;
+    DeviceBuffer &operator=(const DeviceBuffer &) = delete;
+    ~DeviceBuffer()
+    {
+        if (ptr) {
+            DeviceGuard g(device);
+            (void)hipFree(ptr);
+        }
+    }
+    int alloc(int dev, size_t n)
+    {
+        device = dev;
+        bytes = n;
+        hipError_t e = hipMalloc(&ptr, n ? n : 1);
+        if (e != hipSuccess) {
+            ptr = nullptr;
+            return hip_fail(e, "hipMalloc");
+        }
+        return HYQ_OK;
+    }
+};
+
+// Grow-only device scratch owned by a context.
+struct Scratch {
+    std::unique_ptr<DeviceBuffer> buf;
+    int reserve(int device, size_t bytes)
+    {
+        if (buf && buf->bytes >= bytes) return HYQ_OK;
+        buf.reset();
+        auto b = std::make_unique<DeviceBuffer>();
+        int rc = b->alloc(device, align_up(bytes < 4096 ? 4096 : bytes, 4096));
+        if (rc) return rc;
+        buf = std::move(b);
+        return HYQ_OK;
+    }
+    void *ptr() const { return buf ? buf->ptr : nullptr; }
+};
+
+// Non-owning Q8 buffers (a hyq_q8 or a prefix of the context's own).
+struct Q8Ref {
+    int8_t *q = nullptr;
+    float *s = nullptr;
+    int32_t *sum16 = nullptr, *sum32 = nullptr, *sum256 = nullptr;
+    size_t n = 0;
+    Q8View view() const { return Q8View{q, s, sum16, sum32, sum256, (int)n}; }
+    Q8Ref prefix(size_t len) const
+    {
+        Q8Ref r = *this;
+        r.n = len;
+        return r;
+    }
+};
+
+int q8_alloc(int device, size_t n, hyq_q8 **out);
+
+} // namespace hyq
+
+struct hyq_q8 {
+    std::unique_ptr<hyq::DeviceBuffer> mem;
+    int device = 0;
+    hyq::Q8Ref ref;
+};
+
+struct hyq_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hyq::Scratch x, y, bytes;
+    hyq_q8 *q8 = nullptr; // grown on demand for host-pointer calls
+};
+
+struct hyq_weight {
+    std::shared_ptr<hyq::DeviceBuffer> storage;
+    int dtype = 0;
+    int rank = 2;
+    uint64_t dims[3] = {0, 0, 1};
+    size_t cols = 0, rows = 0;
+    int device = 0;
+    hyq::WView view{};
+};

@@ -13,16 +13,14 @@
 #include <string>
 #include <vector>
 
-#include "../../include/hyq.h"
-#include "hyq_internal.hpp"
+#include "hyq_abi.hpp"
 
 using namespace hyq;
 
-// ---------------------------------------------------------------------------
-// errors
-// ---------------------------------------------------------------------------
+namespace hyq {
 namespace {
 thread_local std::string g_last_error;
+}
 
 int fail(int code, const char *fmt, ...)
 {
@@ -41,113 +39,6 @@ int hip_fail(hipError_t e, const char *what)
                 hipGetErrorString(e));
 }
 
-#define HYQ_HIP(call, what)                                                                    \
-    do {                                                                                       \
-        hipError_t e_ = (call);                                                                \
-        if (e_ != hipSuccess) return hip_fail(e_, what);                                       \
-    } while (0)
-
-#define HYQ_LAUNCH(call, what)                                                                 \
-    do {                                                                                       \
-        int e_ = (call);                                                                       \
-        if (e_ != 0) return hip_fail((hipError_t)e_, what);                                    \
-    } while (0)
-
-// Makes the context's device current for the scope of one call.
-struct DeviceGuard {
-    int prev = -1;
-    bool ok = true;
-    explicit DeviceGuard(int dev)
-    {
-        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
-        if (prev != dev) ok = hipSetDevice(dev) == hipSuccess;
-    }
-    ~DeviceGuard()
-    {
-        int cur = -1;
-        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
-    }
-};
-
-size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
-
-struct DeviceBuffer {
-    void *ptr = nullptr;
-    size_t bytes = 0;
-    int device = 0;
-    ~DeviceBuffer()
-    {
-        if (ptr) {
-            DeviceGuard g(device);
-            (void)hipFree(ptr);
-        }
-    }
-};
-
-// Grow-only device scratch owned by a context.
-struct Scratch {
-    std::unique_ptr<DeviceBuffer> buf;
-    int reserve(int device, size_t bytes)
-    {
-        if (buf && buf->bytes >= bytes) return HYQ_OK;
-        buf.reset();
-        auto b = std::make_unique<DeviceBuffer>();
-        b->device = device;
-        b->bytes = align_up(bytes < 4096 ? 4096 : bytes, 4096);
-        hipError_t e = hipMalloc(&b->ptr, b->bytes);
-        if (e != hipSuccess) {
-            b->ptr = nullptr;
-            return hip_fail(e, "hipMalloc(scratch)");
-        }
-        buf = std::move(b);
-        return HYQ_OK;
-    }
-    void *ptr() const { return buf ? buf->ptr : nullptr; }
-};
-} // namespace
-
-namespace {
-// Non-owning Q8 buffers (a hyq_q8 or a prefix of the context's own).
-struct Q8Ref {
-    int8_t *q = nullptr;
-    float *s = nullptr;
-    int32_t *sum16 = nullptr, *sum32 = nullptr, *sum256 = nullptr;
-    size_t n = 0;
-    Q8View view() const { return Q8View{q, s, sum16, sum32, sum256, (int)n}; }
-    Q8Ref prefix(size_t len) const
-    {
-        Q8Ref r = *this;
-        r.n = len;
-        return r;
-    }
-};
-} // namespace
-
-struct hyq_q8 {
-    std::unique_ptr<DeviceBuffer> mem;
-    int device = 0;
-    Q8Ref ref;
-};
-
-struct hyq_ctx {
-    int device = 0;
-    hipStream_t stream = nullptr;
-    Scratch x, y, bytes;
-    hyq_q8 *q8 = nullptr; // grown on demand for host-pointer calls
-};
-
-struct hyq_weight {
-    std::shared_ptr<DeviceBuffer> storage;
-    int dtype = 0;
-    int rank = 2;
-    uint64_t dims[3] = {0, 0, 1};
-    size_t cols = 0, rows = 0;
-    int device = 0;
-    WView view{};
-};
-
-namespace {
-
 int q8_alloc(int device, size_t n, hyq_q8 **out)
 {
     auto q = std::make_unique<hyq_q8>();
@@ -160,13 +51,8 @@ int q8_alloc(int device, size_t n, hyq_q8 **out)
     const size_t off_256 = off_32 + align_up(n32 * 4, 256);
     const size_t total = off_256 + align_up(ng * 4, 256);
     q->mem = std::make_unique<DeviceBuffer>();
-    q->mem->device = device;
-    q->mem->bytes = total;
-    hipError_t e = hipMalloc(&q->mem->ptr, total);
-    if (e != hipSuccess) {
-        q->mem->ptr = nullptr;
-        return hip_fail(e, "hipMalloc(q8)");
-    }
+    int rc = q->mem->alloc(device, total);
+    if (rc) return rc;
     uint8_t *base = (uint8_t *)q->mem->ptr;
     q->ref.q = (int8_t *)base;
     q->ref.s = (float *)(base + off_s);
@@ -176,6 +62,10 @@ int q8_alloc(int device, size_t n, hyq_q8 **out)
     *out = q.release();
     return HYQ_OK;
 }
+
+} // namespace hyq
+
+namespace {
 
 // The context's own Q8 buffers, grown on demand, as a prefix of length n.
 int ctx_q8(hyq_ctx *ctx, size_t n, Q8Ref *out)
@@ -337,7 +227,7 @@ int check_ctx_weight(hyq_ctx *ctx, const hyq_weight *w, const char *who)
 // ---------------------------------------------------------------------------
 extern "C" {
 
-const char *hyq_last_error(void) { return g_last_error.c_str(); }
+const char *hyq_last_error(void) { return hyq::g_last_error.c_str(); }
 int hyq_block_len(int dtype) { return dtype_known(dtype) ? block_len(dtype) : -1; }
 int hyq_block_bytes(int dtype) { return dtype_known(dtype) ? block_bytes(dtype) : -1; }
 

@@ -1,0 +1,557 @@
+// Decode-step glue entry points and the dense batch-1 decoder of the C ABI.
+//
+// hyq_dense composes, per token, the same kernels the reference's
+// Model::forward_into batch-1 arm calls per layer (src/model.rs:394-513):
+// rms_norm -> Q8 -> fused QKV GEMV -> RoPE + Q/K norm + KV append ->
+// attention -> Q8 -> attn_output GEMV (+ residual) -> rms_norm -> Q8 ->
+// gate/up SiLU GEMV -> Q8 -> down GEMV (+ residual); then output norm ->
+// Q8 -> lm_head GEMV -> argmax. Position and token stay in device memory, so
+// one step is captured once as a HIP graph and replayed per token.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "hyq_abi.hpp"
+#include "hyq_step.hpp"
+
+using namespace hyq;
+
+namespace {
+
+int check_ctx(hyq_ctx *ctx, const char *who)
+{
+    if (!ctx) return fail(HYQ_EINVAL, "%s: null context", who);
+    return HYQ_OK;
+}
+
+GemvArgs gemv_args(const hyq_weight *w, const Q8Ref &x, float *y, const float *residual)
+{
+    GemvArgs a{};
+    a.nseg = 1;
+    a.seg[0].w = w->view;
+    a.seg[0].y = y;
+    a.rows_total = (int)w->rows;
+    a.groups = (int)(w->cols / 256);
+    a.x = x.view();
+    a.residual = residual;
+    return a;
+}
+
+bool int8_ok(const hyq_weight *w)
+{
+    return w && w->rank == 2 && is_quant(w->dtype) && w->cols % 256 == 0 && w->cols <= 240 * 256;
+}
+
+} // namespace
+
+// ---------------------------------------------------------------------------
+// glue entry points
+// ---------------------------------------------------------------------------
+extern "C" {
+
+int hyq_embed_row_d(hyq_ctx *ctx, const hyq_weight *w, const int32_t *token_d, float *out_d)
+{
+    int rc = check_ctx(ctx, "embed_row");
+    if (rc) return rc;
+    if (!w || !token_d || !out_d) return fail(HYQ_EINVAL, "embed_row: null argument");
+    if (w->rank != 2) return fail(HYQ_EINVAL, "embed_row: weight is not a matrix");
+    DeviceGuard g(ctx->device);
+    HYQ_LAUNCH(launch_embed_row(w->dtype, w->view, (int)w->cols, token_d, out_d, ctx->stream),
+               "embed_row");
+    return HYQ_OK;
+}
+
+int hyq_rms_norm_q8_d(hyq_ctx *ctx, const float *x_d, const float *w_d, size_t n, float eps,
+                      float *y_d, hyq_q8 *out)
+{
+    int rc = check_ctx(ctx, "rms_norm_q8");
+    if (rc) return rc;
+    if (!x_d || !w_d || !out) return fail(HYQ_EINVAL, "rms_norm_q8: null argument");
+    if (n == 0 || n != out->ref.n) return fail(HYQ_EINVAL, "rms_norm_q8: length %zu", n);
+    DeviceGuard g(ctx->device);
+    const Q8Ref &q = out->ref;
+    HYQ_LAUNCH(launch_rms_norm_q8(x_d, w_d, (int)n, eps, y_d, q.q, q.s, q.sum16, q.sum32,
+                                  q.sum256, ctx->stream),
+               "rms_norm_q8");
+    return HYQ_OK;
+}
+
+int hyq_rope_norm_append_d(hyq_ctx *ctx, float *q_d, const float *k_d, const float *v_d,
+                           const float *q_norm_d, const float *k_norm_d, const float *freq_d,
+                           const int32_t *pos_d, size_t heads, size_t kv_heads, size_t head_dim,
+                           float eps, float *kcache_d, float *vcache_d)
+{
+    int rc = check_ctx(ctx, "rope_norm_append");
+    if (rc) return rc;
+    if (!q_d || !k_d || !v_d || !q_norm_d || !k_norm_d || !freq_d || !pos_d || !kcache_d ||
+        !vcache_d)
+        return fail(HYQ_EINVAL, "rope_norm_append: null argument");
+    if (head_dim != 128 || heads == 0 || kv_heads == 0 || heads % kv_heads)
+        return fail(HYQ_EINVAL, "rope_norm_append: heads %zu/%zu of dim %zu", heads, kv_heads,
+                    head_dim);
+    DeviceGuard g(ctx->device);
+    HYQ_LAUNCH(launch_rope_norm_kv(q_d, k_d, v_d, q_norm_d, k_norm_d, freq_d, pos_d, (int)heads,
+                                   (int)kv_heads, (int)head_dim, eps, kcache_d, vcache_d,
+                                   ctx->stream),
+               "rope_norm_append");
+    return HYQ_OK;
+}
+
+size_t hyq_attention_scratch_floats(size_t context, size_t heads)
+{
+    return (size_t)attention_splits((int)context) * heads * (128 + 2);
+}
+
+int hyq_attention_d(hyq_ctx *ctx, const float *q_d, const float *kcache_d,
+                    const float *vcache_d, const int32_t *pos_d, size_t context, size_t heads,
+                    size_t kv_heads, size_t head_dim, float *scratch_d, float *out_d,
+                    hyq_q8 *out_q8)
+{
+    int rc = check_ctx(ctx, "attention");
+    if (rc) return rc;
+    if (!q_d || !kcache_d || !vcache_d || !pos_d || !scratch_d)
+        return fail(HYQ_EINVAL, "attention: null argument");
+    if (head_dim != 128 || heads == 0 || kv_heads == 0 || heads % kv_heads || context == 0 ||
+        context > (1u << 24))
+        return fail(HYQ_EINVAL, "attention: unsupported shape");
+    if (out_q8 && out_q8->ref.n != heads * head_dim)
+        return fail(HYQ_EINVAL, "attention: Q8 length %zu != %zu", out_q8->ref.n,
+                    heads * head_dim);
+    DeviceGuard g(ctx->device);
+    const Q8Ref q = out_q8 ? out_q8->ref : Q8Ref{};
+    HYQ_LAUNCH(launch_attention(q_d, kcache_d, vcache_d, pos_d, (int)context, (int)heads,
+                                (int)kv_heads, scratch_d, out_d, q.q, q.s, q.sum16, q.sum32,
+                                q.sum256, ctx->stream),
+               "attention");
+    return HYQ_OK;
+}
+
+int hyq_argmax_d(hyq_ctx *ctx, const float *x_d, size_t n, float *scratch_d, int32_t *token_d)
+{
+    int rc = check_ctx(ctx, "argmax");
+    if (rc) return rc;
+    if (!x_d || !scratch_d || !token_d || n == 0 || n > 0x7fffffff)
+        return fail(HYQ_EINVAL, "argmax: bad argument");
+    DeviceGuard g(ctx->device);
+    HYQ_LAUNCH(launch_argmax(x_d, (int)n, scratch_d, (int *)(scratch_d + 64), token_d, nullptr,
+                             nullptr, ctx->stream),
+               "argmax");
+    return HYQ_OK;
+}
+
+} // extern "C"
+
+// ---------------------------------------------------------------------------
+// dense decoder
+// ---------------------------------------------------------------------------
+struct hyq_dense {
+    hyq_ctx *ctx = nullptr;
+    hyq_dense_config cfg{};
+    size_t context = 0;
+    size_t pos_host = 0;
+    struct Layer {
+        const hyq_weight *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
+        const hyq_weight *gate = nullptr, *up = nullptr, *down = nullptr;
+        float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+    };
+    std::vector<Layer> layers;
+    const hyq_weight *embedding = nullptr, *output = nullptr;
+    float *output_norm = nullptr;
+
+    DeviceBuffer mem;       // norms, freq, activations, scratch, state
+    DeviceBuffer kv;        // [layers][2][context][kv_heads*head_dim]
+    hyq_q8 *q8h = nullptr;  // hidden-width activations
+    hyq_q8 *q8a = nullptr;  // attention output
+    hyq_q8 *q8f = nullptr;  // FFN-width activations
+    float *freq = nullptr, *hidden = nullptr, *qb = nullptr, *kb = nullptr, *vb = nullptr;
+    float *gb = nullptr, *logits = nullptr, *att_scratch = nullptr, *argmax_scratch = nullptr;
+    int32_t *token = nullptr, *history = nullptr;
+    StepState *state = nullptr;
+    size_t history_cap = 0;
+    std::unique_ptr<DeviceBuffer> history_mem;
+
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+
+    ~hyq_dense()
+    {
+        if (exec) (void)hipGraphExecDestroy(exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        delete q8h;
+        delete q8a;
+        delete q8f;
+    }
+    size_t kvw() const { return (size_t)cfg.kv_heads * cfg.head_dim; }
+    float *kcache(int l) { return (float *)kv.ptr + (size_t)l * 2 * context * kvw(); }
+    float *vcache(int l) { return kcache(l) + context * kvw(); }
+    void drop_graph()
+    {
+        if (exec) (void)hipGraphExecDestroy(exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        exec = nullptr;
+        graph = nullptr;
+    }
+};
+
+namespace {
+
+int enqueue_step(hyq_dense *m)
+{
+    const hyq_dense_config &c = m->cfg;
+    hipStream_t st = m->ctx->stream;
+    const int qlen = c.heads * c.head_dim;
+    HYQ_LAUNCH(launch_embed_row(m->embedding->dtype, m->embedding->view, c.hidden, m->token,
+                                m->hidden, st),
+               "embed_row");
+    const Q8Ref &h8 = m->q8h->ref, &a8 = m->q8a->ref, &f8 = m->q8f->ref;
+    const int *pos = &m->state->pos;
+    for (int l = 0; l < c.layers; ++l) {
+        const hyq_dense::Layer &L = m->layers[l];
+        HYQ_LAUNCH(launch_rms_norm_q8(m->hidden, L.attn_norm, c.hidden, c.rms_eps, nullptr, h8.q,
+                                      h8.s, h8.sum16, h8.sum32, h8.sum256, st),
+                   "rms_norm_q8");
+        {
+            GemvArgs a = gemv_args(L.q, h8, m->qb, nullptr);
+            const hyq_weight *ws[3] = {L.q, L.k, L.v};
+            float *ys[3] = {m->qb, m->kb, m->vb};
+            int start = 0;
+            for (int i = 0; i < 3; ++i) {
+                a.seg[i].w = ws[i]->view;
+                a.seg[i].y = ys[i];
+                a.seg[i].row_start = start;
+                start += (int)ws[i]->rows;
+            }
+            a.nseg = 3;
+            a.rows_total = start;
+            HYQ_LAUNCH(launch_gemv(L.q->dtype, GEMV_MULTI, a, st), "gemv_qkv");
+        }
+        HYQ_LAUNCH(launch_rope_norm_kv(m->qb, m->kb, m->vb, L.q_norm, L.k_norm, m->freq, pos,
+                                       c.heads, c.kv_heads, c.head_dim, c.rms_eps, m->kcache(l),
+                                       m->vcache(l), st),
+                   "rope_norm_kv");
+        HYQ_LAUNCH(launch_attention(m->qb, m->kcache(l), m->vcache(l), pos, (int)m->context,
+                                    c.heads, c.kv_heads, m->att_scratch, nullptr, a8.q, a8.s,
+                                    a8.sum16, a8.sum32, a8.sum256, st),
+                   "attention");
+        HYQ_LAUNCH(launch_gemv(L.o->dtype, GEMV_PLAIN, gemv_args(L.o, a8, m->hidden, m->hidden),
+                               st),
+                   "gemv_attn_output");
+        HYQ_LAUNCH(launch_rms_norm_q8(m->hidden, L.ffn_norm, c.hidden, c.rms_eps, nullptr, h8.q,
+                                      h8.s, h8.sum16, h8.sum32, h8.sum256, st),
+                   "rms_norm_q8");
+        {
+            GemvArgs a = gemv_args(L.gate, h8, m->gb, nullptr);
+            a.nseg = 2;
+            a.seg[1].w = L.up->view;
+            HYQ_LAUNCH(launch_gemv(L.gate->dtype, GEMV_SILU, a, st), "gemv_gate_up_silu");
+        }
+        HYQ_LAUNCH(launch_quantize_q8(m->gb, c.ffn, f8.q, f8.s, f8.sum16, f8.sum32, f8.sum256, st),
+                   "quantize_q8");
+        HYQ_LAUNCH(launch_gemv(L.down->dtype, GEMV_PLAIN,
+                               gemv_args(L.down, f8, m->hidden, m->hidden), st),
+                   "gemv_down");
+    }
+    HYQ_LAUNCH(launch_rms_norm_q8(m->hidden, m->output_norm, c.hidden, c.rms_eps, nullptr, h8.q,
+                                  h8.s, h8.sum16, h8.sum32, h8.sum256, st),
+               "rms_norm_q8");
+    HYQ_LAUNCH(launch_gemv(m->output->dtype, GEMV_PLAIN,
+                           gemv_args(m->output, h8, m->logits, nullptr), st),
+               "gemv_lm_head");
+    HYQ_LAUNCH(launch_argmax(m->logits, c.vocab, m->argmax_scratch,
+                             (int *)(m->argmax_scratch + 64), m->token, m->state, m->history, st),
+               "argmax");
+    (void)qlen;
+    return HYQ_OK;
+}
+
+int ready(hyq_dense *m)
+{
+    for (size_t l = 0; l < m->layers.size(); ++l)
+        if (!m->layers[l].q) return fail(HYQ_EINVAL, "dense: layer %zu has no weights", l);
+    if (!m->embedding || !m->output) return fail(HYQ_EINVAL, "dense: output weights not set");
+    return HYQ_OK;
+}
+
+int write_state(hyq_dense *m, int32_t token, int step, int cap)
+{
+    StepState s{(int)m->pos_host, step, cap, 0};
+    HYQ_HIP(hipMemcpyAsync(m->state, &s, sizeof s, hipMemcpyHostToDevice, m->ctx->stream),
+            "hipMemcpy(state)");
+    HYQ_HIP(hipMemcpyAsync(m->token, &token, sizeof token, hipMemcpyHostToDevice,
+                           m->ctx->stream),
+            "hipMemcpy(token)");
+    return HYQ_OK;
+}
+
+} // namespace
+
+extern "C" {
+
+int hyq_dense_create(hyq_ctx *ctx, const hyq_dense_config *cfg, size_t context, hyq_dense **out)
+{
+    int rc = check_ctx(ctx, "dense_create");
+    if (rc) return rc;
+    if (!cfg || !out) return fail(HYQ_EINVAL, "dense_create: null argument");
+    const hyq_dense_config &c = *cfg;
+    if (c.layers <= 0 || c.layers > 1024 || c.hidden <= 0 || c.vocab <= 0 || c.ffn <= 0)
+        return fail(HYQ_EINVAL, "invalid model dimensions");
+    if (c.heads <= 0 || c.kv_heads <= 0 || c.heads % c.kv_heads)
+        return fail(HYQ_EINVAL, "invalid grouped-query head counts");
+    if (c.head_dim != 128) return fail(HYQ_EINVAL, "dense: head_dim %d (128 supported)", c.head_dim);
+    if (c.hidden % 256 || c.ffn % 256 || (c.heads * c.head_dim) % 256)
+        return fail(HYQ_EINVAL, "dense: widths must be multiples of 256");
+    if (!(c.rope_base > 0.f) || !(c.rms_eps > 0.f))
+        return fail(HYQ_EINVAL, "invalid context, RoPE, or RMS settings");
+    if (context == 0 || context > (1u << 22)) return fail(HYQ_EINVAL, "dense: context %zu", context);
+    DeviceGuard g(ctx->device);
+
+    auto m = std::make_unique<hyq_dense>();
+    m->ctx = ctx;
+    m->cfg = c;
+    m->context = context;
+    m->layers.resize((size_t)c.layers);
+    const size_t H = (size_t)c.hidden, F = (size_t)c.ffn, D = (size_t)c.head_dim;
+    const size_t QL = (size_t)c.heads * D, KV = (size_t)c.kv_heads * D, V = (size_t)c.vocab;
+    // one arena: norms (per layer 2*H + 2*D, plus H), freq, activations, scratch
+    size_t off = 0;
+    auto take = [&](size_t floats) {
+        size_t o = off;
+        off += align_up(floats * 4, 256);
+        return o;
+    };
+    const size_t o_norms = take((size_t)c.layers * (2 * H + 2 * D) + H);
+    const size_t o_freq = take(D / 2);
+    const size_t o_hidden = take(H), o_q = take(QL), o_k = take(KV), o_v = take(KV);
+    const size_t o_g = take(F), o_logits = take(V);
+    const size_t o_att = take(hyq_attention_scratch_floats(context, (size_t)c.heads));
+    const size_t o_arg = take(128), o_tok = take(4), o_state = take(4);
+    rc = m->mem.alloc(ctx->device, off);
+    if (rc) return rc;
+    uint8_t *base = (uint8_t *)m->mem.ptr;
+    float *norms = (float *)(base + o_norms);
+    for (int l = 0; l < c.layers; ++l) {
+        float *p = norms + (size_t)l * (2 * H + 2 * D);
+        m->layers[l].attn_norm = p;
+        m->layers[l].ffn_norm = p + H;
+        m->layers[l].q_norm = p + 2 * H;
+        m->layers[l].k_norm = p + 2 * H + D;
+    }
+    m->output_norm = norms + (size_t)c.layers * (2 * H + 2 * D);
+    m->freq = (float *)(base + o_freq);
+    m->hidden = (float *)(base + o_hidden);
+    m->qb = (float *)(base + o_q);
+    m->kb = (float *)(base + o_k);
+    m->vb = (float *)(base + o_v);
+    m->gb = (float *)(base + o_g);
+    m->logits = (float *)(base + o_logits);
+    m->att_scratch = (float *)(base + o_att);
+    m->argmax_scratch = (float *)(base + o_arg);
+    m->token = (int32_t *)(base + o_tok);
+    m->state = (StepState *)(base + o_state);
+    // rope_frequencies (src/model.rs:263-269): base^(-2j/head_dim) in f32
+    std::vector<float> freq(D / 2);
+    for (size_t j = 0; j < D / 2; ++j)
+        freq[j] = std::pow(c.rope_base, -2.0f * (float)j / (float)D);
+    HYQ_HIP(hipMemcpy(m->freq, freq.data(), freq.size() * 4, hipMemcpyHostToDevice),
+            "hipMemcpy(freq)");
+    rc = m->kv.alloc(ctx->device, (size_t)c.layers * 2 * context * KV * 4);
+    if (rc) return rc;
+    HYQ_HIP(hipMemset(m->kv.ptr, 0, m->kv.bytes), "hipMemset(kv)");
+    rc = q8_alloc(ctx->device, H, &m->q8h);
+    if (!rc) rc = q8_alloc(ctx->device, QL, &m->q8a);
+    if (!rc) rc = q8_alloc(ctx->device, F, &m->q8f);
+    if (rc) return rc;
+    if ((rc = write_state(m.get(), 0, 0, 0))) return rc;
+    HYQ_HIP(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    *out = m.release();
+    return HYQ_OK;
+}
+
+void hyq_dense_destroy(hyq_dense *m)
+{
+    if (!m) return;
+    DeviceGuard g(m->ctx->device);
+    (void)hipStreamSynchronize(m->ctx->stream);
+    delete m;
+}
+
+static int check_weight(const hyq_dense *m, const hyq_weight *w, size_t cols, size_t rows,
+                        const char *name)
+{
+    if (!w) return fail(HYQ_EINVAL, "dense: null %s weight", name);
+    if (w->device != m->ctx->device) return fail(HYQ_EINVAL, "dense: %s on another device", name);
+    if (w->rank != 2 || w->cols != cols || w->rows != rows)
+        return fail(HYQ_EINVAL, "%s: expected GGUF shape [%zu, %zu], got [%zu, %zu]", name, cols,
+                    rows, w->cols, w->rows);
+    if (!int8_ok(w)) return fail(HYQ_EDTYPE, "%s: dtype %d has no int8 path", name, w->dtype);
+    return HYQ_OK;
+}
+
+int hyq_dense_set_layer(hyq_dense *m, int layer, const hyq_weight *q, const hyq_weight *k,
+                        const hyq_weight *v, const hyq_weight *o, const hyq_weight *gate,
+                        const hyq_weight *up, const hyq_weight *down, const float *attn_norm,
+                        const float *ffn_norm, const float *q_norm, const float *k_norm)
+{
+    if (!m) return fail(HYQ_EINVAL, "dense_set_layer: null decoder");
+    const hyq_dense_config &c = m->cfg;
+    if (layer < 0 || layer >= c.layers) return fail(HYQ_EINVAL, "dense: layer %d", layer);
+    const size_t H = c.hidden, F = c.ffn, QL = (size_t)c.heads * c.head_dim,
+                 KV = (size_t)c.kv_heads * c.head_dim, D = c.head_dim;
+    int rc = check_weight(m, q, H, QL, "attn_q");
+    if (!rc) rc = check_weight(m, k, H, KV, "attn_k");
+    if (!rc) rc = check_weight(m, v, H, KV, "attn_v");
+    if (!rc) rc = check_weight(m, o, QL, H, "attn_output");
+    if (!rc) rc = check_weight(m, gate, H, F, "ffn_gate");
+    if (!rc) rc = check_weight(m, up, H, F, "ffn_up");
+    if (!rc) rc = check_weight(m, down, F, H, "ffn_down");
+    if (rc) return rc;
+    if (!(q->dtype == k->dtype && k->dtype == v->dtype))
+        return fail(HYQ_EDTYPE, "dense: q/k/v formats differ");
+    if (gate->dtype != up->dtype) return fail(HYQ_EDTYPE, "dense: gate/up formats differ");
+    if (!attn_norm || !ffn_norm || !q_norm || !k_norm)
+        return fail(HYQ_EINVAL, "dense: null norm vector");
+    for (const float *vec : {attn_norm, ffn_norm})
+        for (size_t i = 0; i < H; ++i)
+            if (!std::isfinite(vec[i])) return fail(HYQ_EINVAL, "non-finite normalization tensor");
+    DeviceGuard g(m->ctx->device);
+    hyq_dense::Layer &L = m->layers[layer];
+    L.q = q;
+    L.k = k;
+    L.v = v;
+    L.o = o;
+    L.gate = gate;
+    L.up = up;
+    L.down = down;
+    HYQ_HIP(hipMemcpy(L.attn_norm, attn_norm, H * 4, hipMemcpyHostToDevice), "hipMemcpy");
+    HYQ_HIP(hipMemcpy(L.ffn_norm, ffn_norm, H * 4, hipMemcpyHostToDevice), "hipMemcpy");
+    HYQ_HIP(hipMemcpy(L.q_norm, q_norm, D * 4, hipMemcpyHostToDevice), "hipMemcpy");
+    HYQ_HIP(hipMemcpy(L.k_norm, k_norm, D * 4, hipMemcpyHostToDevice), "hipMemcpy");
+    m->drop_graph();
+    return HYQ_OK;
+}
+
+int hyq_dense_set_output(hyq_dense *m, const hyq_weight *embedding, const hyq_weight *output,
+                         const float *output_norm)
+{
+    if (!m) return fail(HYQ_EINVAL, "dense_set_output: null decoder");
+    const hyq_dense_config &c = m->cfg;
+    int rc = check_weight(m, output, c.hidden, c.vocab, "output");
+    if (rc) return rc;
+    if (!embedding || embedding->rank != 2 || embedding->cols != (size_t)c.hidden ||
+        embedding->rows != (size_t)c.vocab)
+        return fail(HYQ_EINVAL, "token_embd: shape mismatch");
+    if (!output_norm) return fail(HYQ_EINVAL, "dense: null output norm");
+    DeviceGuard g(m->ctx->device);
+    m->embedding = embedding;
+    m->output = output;
+    HYQ_HIP(hipMemcpy(m->output_norm, output_norm, (size_t)c.hidden * 4, hipMemcpyHostToDevice),
+            "hipMemcpy");
+    m->drop_graph();
+    return HYQ_OK;
+}
+
+int hyq_dense_load_kv(hyq_dense *m, int layer, size_t positions, const float *keys,
+                      const float *values)
+{
+    if (!m || !keys || !values) return fail(HYQ_EINVAL, "dense_load_kv: null argument");
+    if (layer < 0 || layer >= m->cfg.layers) return fail(HYQ_EINVAL, "dense: layer %d", layer);
+    if (positions > m->context) return fail(HYQ_EINVAL, "context limit exceeded");
+    DeviceGuard g(m->ctx->device);
+    const size_t bytes = positions * m->kvw() * 4;
+    HYQ_HIP(hipMemcpy(m->kcache(layer), keys, bytes, hipMemcpyHostToDevice), "hipMemcpy(k)");
+    HYQ_HIP(hipMemcpy(m->vcache(layer), values, bytes, hipMemcpyHostToDevice), "hipMemcpy(v)");
+    return HYQ_OK;
+}
+
+int hyq_dense_set_position(hyq_dense *m, size_t position)
+{
+    if (!m) return fail(HYQ_EINVAL, "dense_set_position: null decoder");
+    if (position > m->context) return fail(HYQ_EINVAL, "context limit exceeded");
+    m->pos_host = position;
+    return HYQ_OK;
+}
+
+int hyq_dense_get_position(hyq_dense *m, size_t *position)
+{
+    if (!m || !position) return fail(HYQ_EINVAL, "dense_get_position: null argument");
+    *position = m->pos_host;
+    return HYQ_OK;
+}
+
+int hyq_dense_forward(hyq_dense *m, int32_t token, float *logits, int32_t *next)
+{
+    if (!m) return fail(HYQ_EINVAL, "dense_forward: null decoder");
+    int rc = ready(m);
+    if (rc) return rc;
+    if (token < 0 || token >= m->cfg.vocab) return fail(HYQ_EINVAL, "input token outside vocabulary");
+    if (m->pos_host + 1 > m->context) return fail(HYQ_EINVAL, "context limit exceeded");
+    DeviceGuard g(m->ctx->device);
+    if ((rc = write_state(m, token, 0, 0))) return rc;
+    if ((rc = enqueue_step(m))) return rc;
+    if (logits)
+        HYQ_HIP(hipMemcpyAsync(logits, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost,
+                               m->ctx->stream),
+                "hipMemcpy(logits)");
+    int32_t nt = 0;
+    HYQ_HIP(hipMemcpyAsync(&nt, m->token, 4, hipMemcpyDeviceToHost, m->ctx->stream),
+            "hipMemcpy(token)");
+    HYQ_HIP(hipStreamSynchronize(m->ctx->stream), "hipStreamSynchronize");
+    m->pos_host += 1;
+    if (next) *next = nt;
+    return HYQ_OK;
+}
+
+int hyq_dense_generate(hyq_dense *m, int32_t token, size_t steps, int use_graph, int32_t *tokens)
+{
+    if (!m) return fail(HYQ_EINVAL, "dense_generate: null decoder");
+    int rc = ready(m);
+    if (rc) return rc;
+    if (token < 0 || token >= m->cfg.vocab) return fail(HYQ_EINVAL, "input token outside vocabulary");
+    if (steps == 0) return HYQ_OK;
+    if (!tokens) return fail(HYQ_EINVAL, "dense_generate: null output");
+    if (m->pos_host + steps > m->context) return fail(HYQ_EINVAL, "context limit exceeded");
+    DeviceGuard g(m->ctx->device);
+    hipStream_t st = m->ctx->stream;
+    if (m->history_cap < steps) {
+        m->drop_graph(); // the graph bakes the history address in
+        m->history_mem.reset();
+        m->history = nullptr;
+        m->history_cap = 0;
+        auto buf = std::make_unique<DeviceBuffer>();
+        if ((rc = buf->alloc(m->ctx->device, steps * 4))) return rc;
+        m->history_mem = std::move(buf);
+        m->history = (int32_t *)m->history_mem->ptr;
+        m->history_cap = steps;
+    }
+    if ((rc = write_state(m, token, 0, (int)steps))) return rc;
+    if (use_graph) {
+        if (!m->exec) {
+            HYQ_HIP(hipStreamSynchronize(st), "hipStreamSynchronize");
+            HYQ_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "BeginCapture");
+            rc = enqueue_step(m);
+            hipGraph_t graph = nullptr;
+            hipError_t e = hipStreamEndCapture(st, &graph);
+            if (rc) {
+                if (graph) (void)hipGraphDestroy(graph);
+                return rc;
+            }
+            if (e != hipSuccess) return hip_fail(e, "EndCapture");
+            m->graph = graph;
+            HYQ_HIP(hipGraphInstantiate(&m->exec, m->graph, nullptr, nullptr, 0),
+                    "hipGraphInstantiate");
+        }
+        for (size_t i = 0; i < steps; ++i) HYQ_HIP(hipGraphLaunch(m->exec, st), "hipGraphLaunch");
+    } else {
+        for (size_t i = 0; i < steps; ++i)
+            if ((rc = enqueue_step(m))) return rc;
+    }
+    HYQ_HIP(hipMemcpyAsync(tokens, m->history, steps * 4, hipMemcpyDeviceToHost, st),
+            "hipMemcpy(tokens)");
+    HYQ_HIP(hipStreamSynchronize(st), "hipStreamSynchronize");
+    m->pos_host += steps;
+    return HYQ_OK;
+}
+
+} // extern "C"

@@ -1,36 +1,12 @@
-// Q8 activation quantizer (Q8::quantize_into, src/quant.rs:904-922, with
-// max_abs_neon :869-892 and quantize_group_neon :965-991) for gfx950.
-//
-// One 256-thread workgroup per 256-value group: a wave-then-LDS max of |x|,
-// scale = max/127 and inverse = 127/max (both IEEE divisions, or 0/0 for an
-// all-zero group), q = saturate_i8(round_half_even(x * inverse)) over whole
-// 16-value steps and clamp(round_half_away(x * inverse), -127, 127) over a
-// group's tail, as the NEON body and its scalar tail do. The same kernel
-// writes the integer sums of q over 16-, 32- and 256-value spans that the
-// GEMV kernels use to fold code offsets (exact integers, so order-free).
+// Q8 activation quantizer kernel (Q8::quantize_into, src/quant.rs:904-922)
+// for gfx950; the arithmetic lives in hyq_q8.hpp.
 #include <hip/hip_runtime.h>
 
-#include "hyq_internal.hpp"
+#include "hyq_q8.hpp"
 
 namespace hyq {
 
 namespace {
-
-__device__ __forceinline__ int sat_rne(float v)
-{
-    if (v != v) return 0;
-    float r = __builtin_rintf(v);
-    r = fminf(fmaxf(r, -128.f), 127.f);
-    return (int)r;
-}
-
-__device__ __forceinline__ int tail_round(float v)
-{
-    if (v != v) return 0;
-    float r = roundf(v);
-    r = fminf(fmaxf(r, -127.f), 127.f);
-    return (int)r;
-}
 
 __global__ __launch_bounds__(256) void quantize_q8_kernel(const float *__restrict__ x, int n,
                                                           int8_t *__restrict__ q,
@@ -39,43 +15,11 @@ __global__ __launch_bounds__(256) void quantize_q8_kernel(const float *__restric
                                                           int32_t *__restrict__ sum32,
                                                           int32_t *__restrict__ sum256)
 {
-    __shared__ float wmax[4];
-    __shared__ int wsum[4];
     const int g = blockIdx.x;
-    const int base = g * 256;
-    const int len = min(256, n - base);
+    const int len = min(256, n - g * 256);
     const int t = threadIdx.x;
-    const float v = t < len ? x[base + t] : 0.f;
-
-    float m = fabsf(v);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    if ((t & 63) == 0) wmax[t >> 6] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-
-    float scale = 0.f, inverse = 0.f;
-    if (m > 0.f) {
-        scale = m / 127.f;
-        inverse = 127.f / m;
-    }
-    const int vec = len / 16 * 16;
-    int qi = 0;
-    if (t < vec) qi = sat_rne(v * inverse);
-    else if (t < len) qi = tail_round(v * inverse);
-    if (t < len) q[base + t] = (int8_t)qi;
-    if (t == 0) s[g] = scale;
-
-    int a = qi;
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) a += __shfl_xor(a, off, 64);
-    if ((t & 15) == 0 && t < len) sum16[(base + t) >> 4] = a;
-    a += __shfl_xor(a, 16, 64);
-    if ((t & 31) == 0 && t < len) sum32[(base + t) >> 5] = a;
-    a += __shfl_xor(a, 32, 64);
-    if ((t & 63) == 0) wsum[t >> 6] = a;
-    __syncthreads();
-    if (t == 0) sum256[g] = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    const float v = t < len ? x[g * 256 + t] : 0.f;
+    q8_quantize_group(v, g, len, q, s, sum16, sum32, sum256);
 }
 
 } // namespace

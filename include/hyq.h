@@ -150,6 +150,76 @@ int hyq_dequant_rows_d(hyq_ctx *ctx, const hyq_weight *w, size_t row0, size_t nr
 int hyq_decode_d(hyq_ctx *ctx, int dtype, const uint8_t *bytes_d, size_t byte_len,
                  float *out_d, size_t n);
 
+/* ---- batch-1 decode-step glue (device pointers, asynchronous) ----
+ * Positions and token ids are read from device memory so that a caller can
+ * capture a whole step in a HIP graph and replay it. */
+
+/* Weight::row_into (src/quant.rs:123-142) with the row index in device memory. */
+int hyq_embed_row_d(hyq_ctx *ctx, const hyq_weight *w, const int32_t *token_d, float *out_d);
+/* rms_norm_into (src/model.rs:785-830) fused with Q8::quantize_into: the
+ * normalized row y = x * (1/sqrt(mean(x^2)+eps)) * w goes to `out` as Q8 and,
+ * when y_d is non-null, as f32. n must equal out's length. */
+int hyq_rms_norm_q8_d(hyq_ctx *ctx, const float *x_d, const float *w_d, size_t n, float eps,
+                      float *y_d, hyq_q8 *out);
+/* For one token at position *pos_d: rope_with_cache on q and k (NeoX halves,
+ * src/model.rs:874-917), then the dense order's per-head rms_norm of q and k
+ * (src/model.rs:425-446), then KvCache::append (src/model.rs:650-669) of k and
+ * v into row *pos_d of kcache/vcache ([context][kv_heads*head_dim] f32).
+ * q is updated in place. freq_d[j] = rope_base^(-2j/head_dim). head_dim 128. */
+int hyq_rope_norm_append_d(hyq_ctx *ctx, float *q_d, const float *k_d, const float *v_d,
+                           const float *q_norm_d, const float *k_norm_d, const float *freq_d,
+                           const int32_t *pos_d, size_t heads, size_t kv_heads, size_t head_dim,
+                           float eps, float *kcache_d, float *vcache_d);
+/* attention_into (src/model.rs:949-1035) for one query token over cache rows
+ * 0..=*pos_d (grouped-query, head_dim 128, scale 1/sqrt(128)). out_d
+ * [heads*128] f32 and/or out_q8 (quantized for the output projection) may be
+ * null. scratch_d holds hyq_attention_scratch_floats(context, heads) floats. */
+size_t hyq_attention_scratch_floats(size_t context, size_t heads);
+int hyq_attention_d(hyq_ctx *ctx, const float *q_d, const float *kcache_d,
+                    const float *vcache_d, const int32_t *pos_d, size_t context, size_t heads,
+                    size_t kv_heads, size_t head_dim, float *scratch_d, float *out_d,
+                    hyq_q8 *out_q8);
+/* Greedy sampling (src/generation.rs:281-290): index of the first maximum.
+ * scratch_d holds 128 floats. */
+int hyq_argmax_d(hyq_ctx *ctx, const float *x_d, size_t n, float *scratch_d, int32_t *token_d);
+
+/* ---- dense decoder: Model::forward_into at batch 1 (src/model.rs:374-546)
+ * for the hunyuan-dense graph, device-resident, KV cache in HBM ---- */
+typedef struct {
+    int layers, hidden, heads, kv_heads, head_dim, ffn, vocab;
+    float rope_base, rms_eps;
+} hyq_dense_config;
+typedef struct hyq_dense hyq_dense;
+
+/* Model::new_session (src/model.rs:287-322) with `context` cached positions. */
+int hyq_dense_create(hyq_ctx *ctx, const hyq_dense_config *cfg, size_t context,
+                     hyq_dense **out);
+void hyq_dense_destroy(hyq_dense *m);
+/* Layer weights (borrowed: they must outlive the decoder) and f32 norm vectors
+ * (copied), as Model::from_gguf binds them (src/model.rs:204-258). */
+int hyq_dense_set_layer(hyq_dense *m, int layer, const hyq_weight *q, const hyq_weight *k,
+                        const hyq_weight *v, const hyq_weight *o, const hyq_weight *gate,
+                        const hyq_weight *up, const hyq_weight *down, const float *attn_norm,
+                        const float *ffn_norm, const float *q_norm, const float *k_norm);
+/* token_embd / output (tied when the same weight, src/model.rs:194-202). */
+int hyq_dense_set_output(hyq_dense *m, const hyq_weight *embedding, const hyq_weight *output,
+                         const float *output_norm);
+/* Writes cached keys/values [positions][kv_heads*head_dim] of one layer. */
+int hyq_dense_load_kv(hyq_dense *m, int layer, size_t positions, const float *keys,
+                      const float *values);
+int hyq_dense_set_position(hyq_dense *m, size_t position);
+int hyq_dense_get_position(hyq_dense *m, size_t *position);
+/* One token through the model (Model::forward_into, batch 1): appends its
+ * K/V at the current position, advances it, and returns the logits (if
+ * non-null) and the greedy next token (if non-null). */
+int hyq_dense_forward(hyq_dense *m, int32_t token, float *logits, int32_t *next);
+/* Greedy decoding (Generator::generate at temperature 0 and repetition
+ * penalty 1): feeds `token`, then each argmax, for `steps` steps; tokens[i]
+ * is the argmax after step i. use_graph = 1 replays one captured HIP graph
+ * per step; 0 launches the same kernels one by one. */
+int hyq_dense_generate(hyq_dense *m, int32_t token, size_t steps, int use_graph,
+                       int32_t *tokens);
+
 #ifdef __cplusplus
 }
 #endif

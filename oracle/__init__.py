@@ -229,3 +229,50 @@ def moe_experts(dtype_gate: int, dtype_down: int, gate: np.ndarray, up: np.ndarr
                            mid, _p(x), tokens, _p(pt), _p(pe), _p(pw), pt.size, _p(out),
                            threads)
     return out
+
+
+class _Model(ctypes.Structure):
+    _fields_ = [("layers", ctypes.c_int), ("hidden", ctypes.c_int), ("heads", ctypes.c_int),
+                ("kv_heads", ctypes.c_int), ("head_dim", ctypes.c_int), ("ffn", ctypes.c_int),
+                ("vocab", ctypes.c_int), ("rope_base", ctypes.c_float),
+                ("eps", ctypes.c_float), ("dtype_linear", ctypes.c_int),
+                ("dtype_embed", ctypes.c_int), ("embed", P), ("output", P), ("output_norm", P),
+                ("wq", P), ("wk", P), ("wv", P), ("wo", P), ("wgate", P), ("wup", P),
+                ("wdown", P), ("attn_norm", P), ("ffn_norm", P), ("q_norm", P),
+                ("k_norm", P)]
+
+
+class DenseOracle:
+    """Model::forward_into batch 1 on the CPU (oracle/hyq_oracle_step.c) over a
+    synthetic model dict (tests/synth.py:make_dense_model)."""
+
+    def __init__(self, model: dict):
+        self.model = model
+        c = model["cfg"]
+        L = model["layers"]
+        self._arrays = []
+
+        def ptrs(key):
+            arr = (P * len(L))(*[_p(layer[key]) for layer in L])
+            self._arrays.append(arr)
+            return ctypes.cast(arr, P)
+
+        self.m = _Model(c["layers"], c["hidden"], c["heads"], c["kv_heads"], c["head_dim"],
+                        c["ffn"], c["vocab"], c["rope_base"], c["rms_eps"], model["linear"],
+                        model["embed_dtype"], _p(model["embed"]),
+                        _p(model["output"]) if "output" in model else None,
+                        _p(model["output_norm"]),
+                        ptrs("q"), ptrs("k"), ptrs("v"), ptrs("o"), ptrs("gate"), ptrs("up"),
+                        ptrs("down"), ptrs("attn_norm"), ptrs("ffn_norm"), ptrs("q_norm"),
+                        ptrs("k_norm"))
+
+    def step(self, kcache: np.ndarray, vcache: np.ndarray, pos: int, token: int,
+             int8_path: bool, threads: int = 0) -> np.ndarray:
+        assert kcache.flags["C_CONTIGUOUS"] and vcache.flags["C_CONTIGUOUS"]
+        ctx = kcache.shape[1]
+        logits = np.empty(self.model["cfg"]["vocab"], np.float32)
+        rc = lib().hyqo_decode_step(ctypes.byref(self.m), _p(kcache), _p(vcache), ctx, pos,
+                                    token, int(int8_path), _p(logits), threads)
+        if rc != 0:
+            raise ValueError("decode_step: bad position or token")
+        return logits

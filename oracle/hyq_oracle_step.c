@@ -179,7 +179,8 @@ int hyqo_decode_step(const hyqo_model *m, float *kcache, float *vcache, size_t c
         for (size_t i = 0; i < H; ++i) hidden[i] += proj[i];
     }
     hyqo_rms_norm_rows(hidden, m->output_norm, H, H, m->eps);
-    linear(m, m->dtype_embed, m->embed, (size_t)m->vocab, H, hidden, logits, int8_path, threads);
+    linear(m, m->dtype_embed, m->output ? m->output : m->embed, (size_t)m->vocab, H, hidden,
+           logits, int8_path, threads);
 
     free(hidden);
     free(xn);

@@ -16,6 +16,7 @@ typedef struct {
     float rope_base, eps;
     int dtype_linear, dtype_embed;
     const uint8_t *embed;
+    const uint8_t *output; /* NULL: tied to embed */
     const float *output_norm;
     const uint8_t *const *wq, *const *wk, *const *wv, *const *wo;
     const uint8_t *const *wgate, *const *wup, *const *wdown;

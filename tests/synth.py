@@ -85,3 +85,75 @@ def set_block_scale(dtype: int, blocks: np.ndarray, value: float, dmin: float | 
     if dtype == Q4_K and dmin is not None:
         b[:, 2:4] = np.array([dmin], dtype=np.float16).view(np.uint8)
     return blocks
+
+
+# ---------------------------------------------------------------------------
+# Synthetic dense model (random-init weights of the hunyuan-dense shape)
+# ---------------------------------------------------------------------------
+DENSE_1P8B = dict(layers=32, hidden=2048, heads=16, kv_heads=4, head_dim=128, ffn=6144,
+                  vocab=120818, rope_base=11158840.0, rms_eps=1e-5)
+
+
+def make_dense_model(cfg: dict, linear: int = Q2_0C, embed: int = Q6_K, seed: int = 0) -> dict:
+    """Packed GGUF bytes for every matrix plus f32 norms ~ N(1, 0.02).
+    The output matrix is tied to the embedding (src/model.rs:194-202)."""
+    rng = np.random.default_rng(seed)
+    H, F, D = cfg["hidden"], cfg["ffn"], cfg["head_dim"]
+    QL, KV = cfg["heads"] * D, cfg["kv_heads"] * D
+    layers = []
+    for l in range(cfg["layers"]):
+        s = seed * 1000 + l * 10
+        layers.append(dict(
+            q=random_matrix(linear, QL, H, s + 1), k=random_matrix(linear, KV, H, s + 2),
+            v=random_matrix(linear, KV, H, s + 3), o=random_matrix(linear, H, QL, s + 4),
+            gate=random_matrix(linear, F, H, s + 5), up=random_matrix(linear, F, H, s + 6),
+            down=random_matrix(linear, H, F, s + 7),
+            attn_norm=rng.normal(1, 0.02, H).astype(np.float32),
+            ffn_norm=rng.normal(1, 0.02, H).astype(np.float32),
+            q_norm=rng.normal(1, 0.02, D).astype(np.float32),
+            k_norm=rng.normal(1, 0.02, D).astype(np.float32)))
+    return dict(cfg=dict(cfg), linear=linear, embed_dtype=embed, layers=layers,
+                embed=random_matrix(embed, cfg["vocab"], H, seed * 1000 + 999),
+                output_norm=rng.normal(1, 0.02, H).astype(np.float32))
+
+
+def make_kv_cache(cfg: dict, context: int, prefilled: int, seed: int = 0):
+    """f32 K/V caches [layers][context][kv_heads*head_dim], N(0,1) up to prefilled."""
+    rng = np.random.default_rng(seed + 12345)
+    kvw = cfg["kv_heads"] * cfg["head_dim"]
+    k = np.zeros((cfg["layers"], context, kvw), np.float32)
+    v = np.zeros((cfg["layers"], context, kvw), np.float32)
+    k[:, :prefilled] = rng.standard_normal((cfg["layers"], prefilled, kvw), np.float32)
+    v[:, :prefilled] = rng.standard_normal((cfg["layers"], prefilled, kvw), np.float32)
+    return k, v
+
+
+def dense_weight_bytes(model: dict) -> int:
+    """Packed weight bytes one decode step streams (tied embedding read once)."""
+    total = sum(a.size for L in model["layers"] for n, a in L.items()
+                if a.dtype == np.uint8)
+    return total + model["embed"].size
+
+
+def load_dense(hyq, ctx, model: dict, context: int):
+    """Upload a synthetic model into a hyq DenseDecoder (weights kept alive on it)."""
+    c = model["cfg"]
+    cfg = hyq.DenseConfig(c["layers"], c["hidden"], c["heads"], c["kv_heads"], c["head_dim"],
+                          c["ffn"], c["vocab"], c["rope_base"], c["rms_eps"])
+    dec = hyq.DenseDecoder(ctx, cfg, context)
+    H, F, D = c["hidden"], c["ffn"], c["head_dim"]
+    QL, KV = c["heads"] * D, c["kv_heads"] * D
+    lin = model["linear"]
+    for l, L in enumerate(model["layers"]):
+        W = dict(q=ctx.upload(lin, L["q"], (H, QL)), k=ctx.upload(lin, L["k"], (H, KV)),
+                 v=ctx.upload(lin, L["v"], (H, KV)), o=ctx.upload(lin, L["o"], (QL, H)),
+                 gate=ctx.upload(lin, L["gate"], (H, F)), up=ctx.upload(lin, L["up"], (H, F)),
+                 down=ctx.upload(lin, L["down"], (F, H)))
+        dec.set_layer(l, W["q"], W["k"], W["v"], W["o"], W["gate"], W["up"], W["down"],
+                      L["attn_norm"], L["ffn_norm"], L["q_norm"], L["k_norm"])
+    E = ctx.upload(model["embed_dtype"], model["embed"], (H, c["vocab"]))
+    O = E
+    if "output" in model:
+        O = ctx.upload(model["embed_dtype"], model["output"], (H, c["vocab"]))
+    dec.set_output(E, O, model["output_norm"])
+    return dec
