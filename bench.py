@@ -1,0 +1,277 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized matmul path on one MI355X.
+
+Headline (the `value`): greedy decode tokens/s of a random-init 1.8B 2Bit
+model (32 layers, hidden 2048, 16/4 heads of 128, SwiGLU 6144, Q2_0C
+linears, tied Q6_K embedding/lm_head of 120818 rows, RMSNorm eps 1e-5, RoPE
+base 11158840) with an f32 KV cache pre-filled to 1024 positions of N(0,1).
+A step is one decode token (one replay of the captured HIP graph of the
+whole forward pass plus argmax); warmup W and timed K steps run at positions
+1024 .. 1024+W+K-1 (128 positions at the defaults).
+
+Also reported, from live HIP-event timings on the context stream:
+  roofline      the GEMV kernel with the largest time share of a decode
+                step, measured over the decode step's own weights;
+  gemv          GB/s of every matrix of the GEMV workloads (Q4_K [6144x2048];
+                the 1.8B Q2_0C/STQ1_0 set; Q6_K lm_head), weights rotated
+                over >= 1 GiB so that reads come from HBM, not the 256 MB
+                Infinity Cache;
+  cpu_baseline  the reference's x86 decode step (f32 activations, scalar
+                Q2_0C row dot, AVX2 dot; oracle/hyq_oracle_step.c), timed on
+                this host's cores on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "decode tok/s 1.8B Q2_0C; quant GEMV HBM GB/s as % of ~8 TB/s peak"
+PREFILLED = 1024
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Events:
+    """hipEvent timing on a given stream (the HIP runtime libhyq links)."""
+
+    def __init__(self, stream: int):
+        self.hip = ctypes.CDLL("libamdhip64.so.7")
+        self.stream = ctypes.c_void_p(stream)
+
+    def _ev(self):
+        e = ctypes.c_void_p()
+        assert self.hip.hipEventCreate(ctypes.byref(e)) == 0
+        return e
+
+    def time_ms(self, fn, iters: int) -> float:
+        """Average ms per call of fn(i) over iters calls (after one untimed call)."""
+        s, e = self._ev(), self._ev()
+        fn(0)
+        self.hip.hipEventRecord(s, self.stream)
+        for i in range(iters):
+            fn(i)
+        self.hip.hipEventRecord(e, self.stream)
+        self.hip.hipEventSynchronize(e)
+        ms = ctypes.c_float()
+        self.hip.hipEventElapsedTime(ctypes.byref(ms), s, e)
+        self.hip.hipEventDestroy(s)
+        self.hip.hipEventDestroy(e)
+        return ms.value / iters
+
+
+def gemv_rate(hyq, ctx, ev, dtype, rows, cols, seed=1, min_bytes=1 << 30):
+    """Standalone int8 GEMV: (us per launch, algorithmic GB/s), HBM-resident."""
+    from synth import random_matrix
+    base = random_matrix(dtype, rows, cols, seed=seed)
+    copies = int(min(64, max(1, np.ceil(min_bytes / base.size))))
+    Ws = [ctx.upload(dtype, base, (cols, rows)) for _ in range(copies)]
+    x = np.random.default_rng(seed).normal(0, 1, cols).astype(np.float32)
+    q8 = ctx.q8(cols)
+    xd = ctx.array(x)
+    q8.quantize_into(xd.ptr)
+    y = ctx.empty(rows, np.float32)
+    L = hyq.lib()
+
+    def launch(i):
+        L.hyq_gemv_q8_d(ctx.handle, Ws[i % copies].handle, q8.handle, None, y.ptr)
+
+    ms = ev.time_ms(launch, max(64, 4 * copies))
+    alg = base.size + cols + 4 * (cols // 256) + 4 * rows
+    for W in Ws:
+        W.release()
+    return ms * 1e3, alg / (ms * 1e-3) / 1e9
+
+
+def decode_kernel_table(hyq, ctx, ev, dec_weights, model):
+    """Per-launch time of each GEMV of the decode step over the model's own 32
+    layers of weights (the step's memory behaviour), plus its time per step."""
+    c = model["cfg"]
+    L = hyq.lib()
+    H, F = c["hidden"], c["ffn"]
+    QL = c["heads"] * c["head_dim"]
+    KV = c["kv_heads"] * c["head_dim"]
+    q8h, q8a, q8f = ctx.q8(H), ctx.q8(QL), ctx.q8(F)
+    rng = np.random.default_rng(0)
+    for q8, n in ((q8h, H), (q8a, QL), (q8f, F)):
+        q8.quantize_into(ctx.array(rng.normal(0, 1, n).astype(np.float32)).ptr)
+    yq, yk, yv = ctx.empty(QL, np.float32), ctx.empty(KV, np.float32), ctx.empty(KV, np.float32)
+    yh, yf = ctx.empty(H, np.float32), ctx.empty(F, np.float32)
+    yl = ctx.empty(c["vocab"], np.float32)
+    layers = dec_weights["layers"]
+    n = len(layers)
+    b = lambda key: model["layers"][0][key].size  # noqa: E731
+    rows = {
+        "gemv_qkv": (lambda i: L.hyq_gemv_qkv_q8_d(ctx.handle, layers[i % n]["q"].handle,
+                                                   layers[i % n]["k"].handle,
+                                                   layers[i % n]["v"].handle, q8h.handle,
+                                                   yq.ptr, yk.ptr, yv.ptr),
+                     b("q") + b("k") + b("v") + H + 4 * H // 256 + 4 * (QL + 2 * KV), n),
+        "gemv_attn_out": (lambda i: L.hyq_gemv_q8_d(ctx.handle, layers[i % n]["o"].handle,
+                                                    q8a.handle, yh.ptr, yh.ptr),
+                          b("o") + QL + 4 * QL // 256 + 8 * H, n),
+        "gemv_gate_up_silu": (lambda i: L.hyq_gate_up_silu_q8_d(
+            ctx.handle, layers[i % n]["gate"].handle, layers[i % n]["up"].handle, q8h.handle,
+            yf.ptr), b("gate") + b("up") + H + 4 * H // 256 + 4 * F, n),
+        "gemv_down": (lambda i: L.hyq_gemv_q8_d(ctx.handle, layers[i % n]["down"].handle,
+                                                q8f.handle, yh.ptr, yh.ptr),
+                      b("down") + F + 4 * F // 256 + 8 * H, n),
+        "gemv_lm_head": (lambda i: L.hyq_gemv_q8_d(ctx.handle, dec_weights["embed"].handle,
+                                                   q8h.handle, None, yl.ptr),
+                         model["embed"].size + H + 4 * H // 256 + 4 * c["vocab"], 1),
+    }
+    table = {}
+    for name, (fn, alg, per_step) in rows.items():
+        ms = ev.time_ms(fn, 4 * n if per_step > 1 else 40)
+        table[name] = dict(us=round(ms * 1e3, 3), bytes=int(alg), per_step=per_step,
+                           GBs=round(alg / (ms * 1e-3) / 1e9, 1),
+                           us_per_step=round(ms * 1e3 * per_step, 2))
+    return table
+
+
+def cpu_baseline(model, kv, steps: int):
+    import oracle as O
+    o = O.DenseOracle(model)
+    k, v = kv
+    threads = O.lib().hyqo_max_threads()
+    pos = PREFILLED
+    o.step(k, v, pos, 5, int8_path=False)  # warm
+    t = time.perf_counter()
+    tok = 5
+    for i in range(steps):
+        logits = o.step(k, v, pos + 1 + i, tok, int8_path=False)
+        tok = int(np.argmax(logits))
+    dt = time.perf_counter() - t
+    return dict(value=round(steps / dt, 3), unit="tok/s", cores=threads, kind="port",
+                sample=f"{steps} greedy decode tokens at positions {pos + 1}.."
+                       f"{pos + steps} (after 1 warm-up token) of the same synthetic 1.8B "
+                       f"2Bit model and KV cache, x86 path of Model::forward_into "
+                       f"(f32 activations) restated in C, {threads} OpenMP threads")
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=120)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-gemv", action="store_true", help="skip the standalone GEMV table")
+    ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--no-graph", action="store_true",
+                    help="launch the step's kernels one by one instead of replaying a HIP "
+                         "graph (for profilers that cannot follow graph capture)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(the path has no multi-GPU runtime in this build)", file=sys.stderr)
+        return 2
+    import __graft_entry__ as ge
+    from synth import DENSE_1P8B, Q2_0C, Q4_K, Q6_K, STQ1_0, load_dense, make_dense_model, \
+        make_kv_cache
+
+    hyq = ge.package()
+    cfg = DENSE_1P8B
+    context = PREFILLED + args.warmup + args.steps + 1
+    log("building the synthetic 1.8B 2Bit model")
+    model = make_dense_model(cfg, linear=Q2_0C, embed=Q6_K, seed=0)
+    kv = make_kv_cache(cfg, context, PREFILLED, seed=0)
+
+    ctx = hyq.Context(0)
+    ev = Events(ctx.stream)
+    dec = load_dense(hyq, ctx, model, context)
+    for l in range(cfg["layers"]):
+        dec.load_kv(l, kv[0][l, :PREFILLED], kv[1][l, :PREFILLED])
+    dec.position = PREFILLED
+    log("decoding")
+    use_graph = not args.no_graph
+    toks = dec.generate(1, args.warmup, use_graph=use_graph) if args.warmup else [1]
+    t0 = time.perf_counter()
+    toks = dec.generate(int(toks[-1]), args.steps, use_graph=use_graph)
+    dt = time.perf_counter() - t0
+    tok_s = args.steps / dt
+    log(f"decode: {tok_s:.1f} tok/s ({dt / args.steps * 1e3:.3f} ms/token)")
+
+    # kernel table over the decode step's own weights
+    dec_weights = dict(layers=[], embed=None)
+    keep = dec._keep
+    for l in range(cfg["layers"]):
+        q, k, v, o, g, u, d = keep[7 * l:7 * l + 7]
+        dec_weights["layers"].append(dict(q=q, k=k, v=v, o=o, gate=g, up=u, down=d))
+    dec_weights["embed"] = keep[7 * cfg["layers"]]
+    table = decode_kernel_table(hyq, ctx, ev, dec_weights, model)
+    dom = max(table, key=lambda n: table[n]["us_per_step"])
+    dk = table[dom]
+    achieved = dk["bytes"] / (dk["us"] * 1e-6) / 1e9
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", f"{dom}_traffic.json")
+    if os.path.exists(tf):
+        with open(tf) as f:
+            traffic = json.load(f).get("bytes_per_launch")
+    roofline = dict(kernel=dom, bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS,
+                    unit="GB/s", frac=round(achieved / HBM_PEAK_GBS, 4), traffic=traffic,
+                    algorithmic_bytes=dk["bytes"], avg_us=dk["us"])
+
+    gemv = {}
+    if not args.no_gemv:
+        for name, (dt_, rows, cols) in {
+            "C1_Q4_K_6144x2048": (Q4_K, 6144, 2048),
+            "C2_Q2_0C_qkv_3072x2048": (Q2_0C, 3072, 2048),
+            "C2_Q2_0C_attn_out_2048x2048": (Q2_0C, 2048, 2048),
+            "C2_Q2_0C_gate_up_12288x2048": (Q2_0C, 12288, 2048),
+            "C2_Q2_0C_down_2048x6144": (Q2_0C, 2048, 6144),
+            "C2_STQ1_0_qkv_3072x2048": (STQ1_0, 3072, 2048),
+            "C2_STQ1_0_attn_out_2048x2048": (STQ1_0, 2048, 2048),
+            "C2_STQ1_0_gate_up_12288x2048": (STQ1_0, 12288, 2048),
+            "C2_STQ1_0_down_2048x6144": (STQ1_0, 2048, 6144),
+            "C2_Q6_K_lm_head_120818x2048": (Q6_K, 120818, 2048),
+        }.items():
+            us, gbs = gemv_rate(hyq, ctx, ev, dt_, rows, cols)
+            gemv[name] = dict(us=round(us, 3), GBs=round(gbs, 1),
+                              frac=round(gbs / HBM_PEAK_GBS, 4))
+            log(f"{name}: {us:.2f} us {gbs:.0f} GB/s")
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline")
+        cpu = cpu_baseline(model, kv, args.cpu_steps)
+
+    out = {
+        "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(dt / args.steps * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "1.8B 2Bit greedy decode, batch 1, Q2_0C linears, Q6_K tied "
+                               "embedding/lm_head, f32 KV cache pre-filled to 1024 positions",
+                   "layers": cfg["layers"], "hidden": cfg["hidden"], "heads": cfg["heads"],
+                   "kv_heads": cfg["kv_heads"], "ffn": cfg["ffn"], "vocab": cfg["vocab"],
+                   "positions": [PREFILLED + args.warmup,
+                                 PREFILLED + args.warmup + args.steps - 1],
+                   "graph": use_graph},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "decode_kernels": table,
+        "gemv": gemv,
+        "reference_published": {"value": 86.86, "unit": "tok/s",
+                                "note": "Apple M2 Pro 8 threads, real weights, ~14-18 "
+                                        "positions (docs/validation.md:70); not this config"},
+    }
+    print(json.dumps(out), flush=True)
+    dec.close()
+    ctx.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -113,8 +113,9 @@ int hyq_attention_d(hyq_ctx *ctx, const float *q_d, const float *kcache_d,
     if (rc) return rc;
     if (!q_d || !kcache_d || !vcache_d || !pos_d || !scratch_d)
         return fail(HYQ_EINVAL, "attention: null argument");
+    // the combine stages 6 floats per 32-position slice in LDS (<= 48 KiB)
     if (head_dim != 128 || heads == 0 || kv_heads == 0 || heads % kv_heads || context == 0 ||
-        context > (1u << 24))
+        context > 65536)
         return fail(HYQ_EINVAL, "attention: unsupported shape");
     if (out_q8 && out_q8->ref.n != heads * head_dim)
         return fail(HYQ_EINVAL, "attention: Q8 length %zu != %zu", out_q8->ref.n,
@@ -304,7 +305,7 @@ int hyq_dense_create(hyq_ctx *ctx, const hyq_dense_config *cfg, size_t context, 
         return fail(HYQ_EINVAL, "dense: widths must be multiples of 256");
     if (!(c.rope_base > 0.f) || !(c.rms_eps > 0.f))
         return fail(HYQ_EINVAL, "invalid context, RoPE, or RMS settings");
-    if (context == 0 || context > (1u << 22)) return fail(HYQ_EINVAL, "dense: context %zu", context);
+    if (context == 0 || context > 65536) return fail(HYQ_EINVAL, "dense: context %zu", context);
     DeviceGuard g(ctx->device);
 
     auto m = std::make_unique<hyq_dense>();

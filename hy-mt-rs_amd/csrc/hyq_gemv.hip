@@ -44,14 +44,6 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     extern __shared__ int lds[];
 
     const int groups = a.groups;
-    {
-        const int4 *src = reinterpret_cast<const int4 *>(a.x.q);
-        int4 *dst = reinterpret_cast<int4 *>(lds);
-        for (int i = threadIdx.x; i < groups * 16; i += blockDim.x)
-            dst[(i >> 4) * (SLOT_INTS / 4) + (i & 15)] = src[i];
-    }
-    __syncthreads();
-
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int sub = lane & 7;
@@ -75,6 +67,28 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
         lrow[i] = r - a.seg[s].row_start;
     }
 
+    typename G::Data d[NR];
+    typename G::Data d2[MODE == GEMV_SILU ? NR : 1];
+    auto load_group = [&](int g) {
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            if (!valid[i]) continue;
+            const WView &w = MODE == GEMV_MULTI ? a.seg[seg[i]].w : a.seg[0].w;
+            G::load(d[i], w, lrow[i], g);
+            if (MODE == GEMV_SILU) G::load(d2[i], a.seg[1].w, lrow[i], g);
+        }
+    };
+    // The first group's weights do not depend on the activations: put their
+    // loads in flight before staging the Q8 row, so both latencies overlap.
+    if (sub < groups) load_group(sub);
+    {
+        const int4 *src = reinterpret_cast<const int4 *>(a.x.q);
+        int4 *dst = reinterpret_cast<int4 *>(lds);
+        for (int i = threadIdx.x; i < groups * 16; i += blockDim.x)
+            dst[(i >> 4) * (SLOT_INTS / 4) + (i & 15)] = src[i];
+    }
+    __syncthreads();
+
     float acc[NR];
     float acc2[NR];
 #pragma unroll
@@ -93,15 +107,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
                 act[4 * j + 3] = v.w;
             }
         }
-        typename G::Data d[NR];
-        typename G::Data d2[MODE == GEMV_SILU ? NR : 1];
-#pragma unroll
-        for (int i = 0; i < NR; ++i) {
-            if (!valid[i]) continue;
-            const WView &w = MODE == GEMV_MULTI ? a.seg[seg[i]].w : a.seg[0].w;
-            G::load(d[i], w, lrow[i], g);
-            if (MODE == GEMV_SILU) G::load(d2[i], a.seg[1].w, lrow[i], g);
-        }
+        if (g != sub) load_group(g);
 #pragma unroll
         for (int i = 0; i < NR; ++i) {
             if (!valid[i]) continue;

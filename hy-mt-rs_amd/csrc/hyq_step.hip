@@ -60,7 +60,26 @@ __global__ __launch_bounds__(256) void rms_norm_q8_kernel(const float *__restric
     __shared__ float part[4];
     const int t = threadIdx.x;
     float ss = 0.f;
-    for (int i = t; i < n; i += 256) ss += x[i] * x[i];
+    if ((reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+        // all of this thread's float4 loads in flight together
+        const float4 *x4 = reinterpret_cast<const float4 *>(x);
+        const int n4 = n / 4;
+        int i = t;
+        for (; i + 768 < n4; i += 1024) {
+            const float4 a = x4[i], b = x4[i + 256], c = x4[i + 512], d = x4[i + 768];
+            ss += (a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w) +
+                  (b.x * b.x + b.y * b.y + b.z * b.z + b.w * b.w) +
+                  (c.x * c.x + c.y * c.y + c.z * c.z + c.w * c.w) +
+                  (d.x * d.x + d.y * d.y + d.z * d.z + d.w * d.w);
+        }
+        for (; i < n4; i += 256) {
+            const float4 a = x4[i];
+            ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+        }
+        for (int j = n4 * 4 + t; j < n; j += 256) ss += x[j] * x[j];
+    } else {
+        for (int i = t; i < n; i += 256) ss += x[i] * x[i];
+    }
     ss = wave_sum(ss);
     if ((t & 63) == 0) part[t >> 6] = ss;
     __syncthreads();
@@ -133,20 +152,23 @@ __global__ void rope_norm_kv_kernel(float *__restrict__ q, const float *__restri
 
 // ---- attention over positions 0..=pos, split into ATT_CHUNK-position slices ----
 // Grid (splits, kv_heads); wave w of a workgroup serves query head
-// kvh*rep + w (rep = heads/kv_heads <= 4). K and V of the slice are staged in
-// LDS (K rows padded to 129 floats: conflict-free per-lane row reads). Two
-// lanes share one position's 128-wide dot, then the wave forms the slice's
-// max, exp-sum and exp-weighted V sum; a combine kernel merges the slices.
+// kvh*rep + hh0 + w for hh0 = 0, 4, ... (rep = heads/kv_heads). The slice's K
+// and V rows are fetched with all loads in flight at once (4 float4 of each
+// per thread), then staged in LDS (K rows padded to 129 floats). Two lanes
+// share one position's 128-wide dot; the wave then forms the slice's max,
+// exp-sum and exp-weighted V sum; attn_combine merges the slices.
 constexpr int ATT_CHUNK = 32;
+constexpr int ATT_D = 128;
 
 __global__ __launch_bounds__(256) void attn_partial_kernel(
     const float *__restrict__ q, const float *__restrict__ kcache,
     const float *__restrict__ vcache, const int *__restrict__ pos_p, int heads, int kvh,
     float scale, float *__restrict__ part, int splits)
 {
-    constexpr int D = 128;
+    constexpr int D = ATT_D;
     __shared__ float Ks[ATT_CHUNK][D + 1];
-    __shared__ float Vs[ATT_CHUNK][D];
+    __shared__ float4 Vs[ATT_CHUNK][D / 4];
+    __shared__ float Qs[4][D];
     const int split = blockIdx.x, kh = blockIdx.y;
     const int visible = *pos_p + 1;
     const int p0 = split * ATT_CHUNK;
@@ -155,81 +177,148 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const size_t kvw = (size_t)kvh * D;
     if (n <= 0) {
-        for (int hh = wave; hh < rep; hh += 4) {
-            float *o = part + ((size_t)(kh * rep + hh) * splits + split) * (D + 2);
-            if (lane == 0) {
-                o[0] = -INFINITY;
-                o[1] = 0.f;
-            }
+        for (int i = t; i < rep; i += 256) {
+            float *o = part + ((size_t)(kh * rep + i) * splits + split) * (D + 2);
+            o[0] = -INFINITY;
+            o[1] = 0.f;
         }
         return;
     }
-    for (int i = t; i < ATT_CHUNK * D; i += 256) {
-        const int p = i / D, d = i % D;
-        float kv = 0.f, vv = 0.f;
+    float4 kr[4], vr[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int idx = t + 256 * j; // float4 index in the 32 x 128 slice
+        const int p = idx >> 5, d4 = idx & 31;
         if (p < n) {
-            const size_t off = (size_t)(p0 + p) * kvw + (size_t)kh * D + d;
-            kv = kcache[off];
-            vv = vcache[off];
+            const size_t off = (size_t)(p0 + p) * kvw + (size_t)kh * D + 4 * d4;
+            kr[j] = *reinterpret_cast<const float4 *>(kcache + off);
+            vr[j] = *reinterpret_cast<const float4 *>(vcache + off);
+        } else {
+            kr[j] = vr[j] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        Ks[p][d] = kv;
-        Vs[p][d] = vv;
     }
-    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int idx = t + 256 * j;
+        const int p = idx >> 5, d4 = idx & 31;
+        Ks[p][4 * d4] = kr[j].x;
+        Ks[p][4 * d4 + 1] = kr[j].y;
+        Ks[p][4 * d4 + 2] = kr[j].z;
+        Ks[p][4 * d4 + 3] = kr[j].w;
+        Vs[p][d4] = vr[j];
+    }
     const int p = lane & 31, hf = lane >> 5;
-    for (int hh = wave; hh < rep; hh += 4) {
-        const int h = kh * rep + hh;
-        const float *qh = q + (size_t)h * D + hf * 64;
-        float dot = 0.f;
-#pragma unroll 8
-        for (int d = 0; d < 64; ++d) dot += qh[d] * Ks[p][hf * 64 + d];
-        dot += __shfl_xor(dot, 32, 64);
-        const float sc = p < n ? dot * scale : -INFINITY;
-        const float m = wave_max(sc);
-        const float e = p < n ? expf(sc - m) : 0.f;
-        const float sum = wave_sum(e) * 0.5f; // each position is held by two lanes
-        float a0 = 0.f, a1 = 0.f;
-        for (int pp = 0; pp < n; ++pp) {
-            const float ep = __shfl(e, pp, 64);
-            a0 += ep * Vs[pp][lane];
-            a1 += ep * Vs[pp][lane + 64];
+    for (int hh0 = 0; hh0 < rep; hh0 += 4) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int i = t + 256 * j, hq = i / D;
+            if (hh0 + hq < rep) Qs[hq][i % D] = q[(size_t)(kh * rep + hh0 + hq) * D + i % D];
         }
-        float *o = part + ((size_t)h * splits + split) * (D + 2);
-        if (lane == 0) {
-            o[0] = m;
-            o[1] = sum;
+        __syncthreads();
+        const int hh = hh0 + wave;
+        if (hh < rep) {
+            const int h = kh * rep + hh;
+            float dot = 0.f;
+#pragma unroll 16
+            for (int d = 0; d < 64; ++d) dot += Qs[wave][hf * 64 + d] * Ks[p][hf * 64 + d];
+            dot += __shfl_xor(dot, 32, 64);
+            const float sc = p < n ? dot * scale : -INFINITY;
+            const float m = wave_max(sc);
+            const float e = p < n ? expf(sc - m) : 0.f;
+            const float sum = wave_sum(e) * 0.5f; // each position is held by two lanes
+            // lanes 0..31 own output dims 4*lane .. 4*lane+3 of V rows
+            float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int pp = 0; pp < n; ++pp) {
+                const float ep = __shfl(e, pp, 64);
+                const float4 vv = Vs[pp][lane & 31];
+                a.x += ep * vv.x;
+                a.y += ep * vv.y;
+                a.z += ep * vv.z;
+                a.w += ep * vv.w;
+            }
+            float *o = part + ((size_t)h * splits + split) * (D + 2);
+            if (lane == 0) {
+                o[0] = m;
+                o[1] = sum;
+            }
+            if (lane < 32) {
+                o[2 + 4 * lane] = a.x;
+                o[3 + 4 * lane] = a.y;
+                o[4 + 4 * lane] = a.z;
+                o[5 + 4 * lane] = a.w;
+            }
         }
-        o[2 + lane] = a0;
-        o[2 + 64 + lane] = a1;
+        __syncthreads();
     }
 }
 
 // Merges the slices of two heads per workgroup (256 output values = one Q8
-// group) and quantizes the attended vector for the output projection.
+// group) and quantizes the attended vector for the output projection. The
+// per-slice maxima and sums are staged in LDS (dynamic: 6 floats per slice),
+// then every output value sums its slices with independent loads.
 __global__ __launch_bounds__(256) void attn_combine_q8_kernel(
     const float *__restrict__ part, int heads, int splits, float *__restrict__ out, int8_t *q,
     float *s, int32_t *s16, int32_t *s32, int32_t *s256)
 {
-    constexpr int D = 128;
+    constexpr int D = ATT_D;
+    extern __shared__ float st[]; // m[2][S], sum[2][S], w[2][S]
+    __shared__ float den[2];
+    float *sm = st, *ssum = st + 2 * splits, *sw = st + 4 * splits;
     const int t = threadIdx.x;
     const int g = blockIdx.x;
-    const int h = g * 2 + t / D, d = t % D;
+    for (int i = t; i < 2 * splits; i += 256) {
+        const int hl = i / splits, sp = i % splits, h = 2 * g + hl;
+        float m = -INFINITY, sum = 0.f;
+        if (h < heads) {
+            const float *o = part + ((size_t)h * splits + sp) * (D + 2);
+            m = o[0];
+            sum = o[1];
+        }
+        sm[i] = m;
+        ssum[i] = sum;
+    }
+    __syncthreads();
+    // Slices that hold positions have sum >= 1 and form a prefix; the
+    // accumulators of the others were never written and are not read.
+    __shared__ float Mh[2];
+    __shared__ int nvalid;
+    if (t < 2) {
+        float M = -INFINITY;
+        int nv = 0;
+        for (int sp = 0; sp < splits; ++sp)
+            if (ssum[t * splits + sp] > 0.f) {
+                M = fmaxf(M, sm[t * splits + sp]);
+                nv = sp + 1;
+            }
+        Mh[t] = M;
+        if (t == 0) nvalid = nv;
+    }
+    __syncthreads();
+    for (int i = t; i < 2 * splits; i += 256)
+        sw[i] = ssum[i] > 0.f ? expf(sm[i] - Mh[i / splits]) : 0.f;
+    __syncthreads();
+    if (t < 2) {
+        float dsum = 0.f;
+        for (int sp = 0; sp < splits; ++sp) dsum += sw[t * splits + sp] * ssum[t * splits + sp];
+        den[t] = dsum;
+    }
+    __syncthreads();
+    const int hl = t / D, d = t % D, h = 2 * g + hl;
     float v = 0.f;
     if (h < heads) {
-        const float *ph = part + (size_t)h * splits * (D + 2);
-        float M = -INFINITY;
-        for (int sp = 0; sp < splits; ++sp)
-            if (ph[sp * (D + 2) + 1] > 0.f) M = fmaxf(M, ph[sp * (D + 2)]);
-        float num = 0.f, den = 0.f;
-        for (int sp = 0; sp < splits; ++sp) {
-            const float *o = ph + sp * (D + 2);
-            if (o[1] > 0.f) {
-                const float f = expf(o[0] - M);
-                den += f * o[1];
-                num += f * o[2 + d];
-            }
+        const float *ph = part + (size_t)h * splits * (D + 2) + 2 + d;
+        const float *w = sw + hl * splits;
+        float n0 = 0.f, n1 = 0.f, n2 = 0.f, n3 = 0.f;
+        const int nv = nvalid;
+        int sp = 0;
+        for (; sp + 4 <= nv; sp += 4) {
+            n0 += w[sp] * ph[(size_t)sp * (D + 2)];
+            n1 += w[sp + 1] * ph[(size_t)(sp + 1) * (D + 2)];
+            n2 += w[sp + 2] * ph[(size_t)(sp + 2) * (D + 2)];
+            n3 += w[sp + 3] * ph[(size_t)(sp + 3) * (D + 2)];
         }
-        v = num / den;
+        for (; sp < nv; ++sp) n0 += w[sp] * ph[(size_t)sp * (D + 2)];
+        v = ((n0 + n1) + (n2 + n3)) / den[hl];
         if (out) out[h * D + d] = v;
     }
     const int len = min(256, heads * D - g * 256);
@@ -346,8 +435,9 @@ int launch_attention(const float *q, const float *kcache, const float *vcache, c
     hipStream_t st = (hipStream_t)stream;
     hipLaunchKernelGGL(attn_partial_kernel, dim3(splits, kvh), dim3(256), 0, st, q, kcache,
                        vcache, pos, heads, kvh, scale, part, splits);
-    hipLaunchKernelGGL(attn_combine_q8_kernel, dim3((heads * 128 + 255) / 256), dim3(256), 0, st,
-                       part, heads, splits, out, qq, s, s16, s32, s256);
+    hipLaunchKernelGGL(attn_combine_q8_kernel, dim3((heads * 128 + 255) / 256), dim3(256),
+                       (size_t)splits * 6 * sizeof(float), st, part, heads, splits, out, qq, s,
+                       s16, s32, s256);
     return (int)hipGetLastError();
 }
 

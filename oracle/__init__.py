@@ -73,6 +73,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "hyqo_decode_step": (ctypes.c_int, [P, P, P, SZ, SZ, ctypes.c_int, ctypes.c_int, P,
                                             ctypes.c_int]),
         "hyqo_argmax": (ctypes.c_int, [P, SZ]),
+        "hyqo_max_threads": (ctypes.c_int, []),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -21,6 +21,10 @@
 #include <stdlib.h>
 #include <string.h>
 
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
 static size_t rb_of(int dtype, size_t cols)
 {
     return cols / (size_t)hyqo_block_len(dtype) * (size_t)hyqo_block_bytes(dtype);
@@ -74,9 +78,13 @@ void hyqo_attention(const float *q, const float *keys, const float *values, size
     size_t kv_width = kv_heads * dim;
     size_t repeats = heads / kv_heads;
     float scale = 1.0f / sqrtf((float)dim);
-    float *scores = (float *)malloc(sizeof(float) * (visible ? visible : 1));
     memset(out, 0, sizeof(float) * heads * dim);
-    for (size_t h = 0; h < heads; ++h) {
+    /* heads in parallel, as the reference does once past >= 64 (src/model.rs:1024-1034) */
+    long nh = (long)heads;
+#pragma omp parallel for schedule(static) if (visible >= 64)
+    for (long hl = 0; hl < nh; ++hl) {
+        size_t h = (size_t)hl;
+        float *scores = (float *)malloc(sizeof(float) * (visible ? visible : 1));
         size_t kvh = h / repeats;
         const float *query = q + h * dim;
         for (size_t p = 0; p < visible; ++p)
@@ -95,8 +103,17 @@ void hyqo_attention(const float *q, const float *keys, const float *values, size
             const float *v = values + p * kv_width + kvh * dim;
             for (size_t i = 0; i < dim; ++i) o[i] += pr * v[i];
         }
+        free(scores);
     }
-    free(scores);
+}
+
+int hyqo_max_threads(void)
+{
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
 }
 
 /* One int8-path GEMV: y = round_f32(exact integer formula) (see hyq_oracle.h). */

@@ -35,6 +35,8 @@ void hyqo_attention(const float *q, const float *keys, const float *values, size
 int hyqo_decode_step(const hyqo_model *m, float *kcache, float *vcache, size_t ctx, size_t pos,
                      int token, int int8_path, float *logits, int threads);
 int hyqo_argmax(const float *x, size_t n);
+/* OpenMP threads the matmul/attention loops use when threads <= 0. */
+int hyqo_max_threads(void);
 
 #ifdef __cplusplus
 }
