@@ -513,6 +513,11 @@ int hyq_matmul_d(hyq_ctx *ctx, const hyq_weight *w, const float *x_d, size_t bat
         return rc;
     }
     if (!is_quant(w->dtype)) return fail(HYQ_EDTYPE, "matmul: dtype %d has no batched path", w->dtype);
+    // the GEMM walks K in 64-column slices and loads x as float4
+    if (w->cols % 64) return fail(HYQ_EINVAL, "matmul: cols %zu is not a multiple of 64", w->cols);
+    if ((uintptr_t)x_d % 16 || (uintptr_t)y_d % 16)
+        return fail(HYQ_EINVAL, "matmul: device buffers must be 16-byte aligned");
+    if (batch > 0x7fffffff / 2) return fail(HYQ_EINVAL, "matmul: batch %zu too large", batch);
     HYQ_LAUNCH(launch_gemm_f16(w->dtype, w->view, (int)w->cols, x_d, (int)batch, y_d,
                                ctx->stream),
                "gemm_f16");

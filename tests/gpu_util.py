@@ -25,3 +25,17 @@ def device_bytes(hyq, ctx, ptr: int, nbytes: int) -> np.ndarray:
     out = np.empty(nbytes, np.uint8)
     hyq.check(hyq.lib().hyq_memcpy_d2h(ctx.handle, out.ctypes.data, ptr, nbytes))
     return out
+
+
+def check_prefill_path(y: np.ndarray, y_ref: np.ndarray, mag: np.ndarray, label: str = ""):
+    """f16-MFMA tolerance: per element |err| <= 2e-3 * sum|w x| and 2e-3
+    relative in the 2-norm."""
+    y = np.asarray(y, np.float64)
+    err = np.abs(y - y_ref)
+    bad = err > 2e-3 * mag
+    assert not np.any(bad), (
+        f"{label}: {int(bad.sum())} elements exceed 2e-3*mag; worst "
+        f"{float(np.max(err / np.maximum(mag, 1e-30))):.3e}")
+    rel = np.linalg.norm(y - y_ref) / max(np.linalg.norm(y_ref), 1e-30)
+    assert rel <= 2e-3, f"{label}: relative 2-norm error {rel:.3e}"
+    return rel

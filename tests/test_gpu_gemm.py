@@ -1,0 +1,86 @@
+"""GPU parity of the batched (prefill) path: Weight::matmul at batch >= 2
+(src/quant.rs:272-344) through the C ABI against the oracle's f64 brute force
+of decoded weights x f32 activations (oracle/hyq_oracle.c:hyqo_matmul_f64).
+
+Tolerance of the f16-MFMA path (tests/gpu_util.py:check_prefill_path): per
+element |err| <= 2e-3 * sum|w x| (f16 rounding of both operands bounds each
+term's relative error by 2*2^-11 < 1e-3) and 2e-3 relative in the 2-norm."""
+import numpy as np
+import pytest
+
+from gpu_util import check_prefill_path
+from synth import NAMES, Q2_0C, Q4_K, Q6_K, Q8_0, QUANT, STQ1_0, random_matrix, row_bytes
+
+pytestmark = pytest.mark.gpu
+
+
+def _print(*a):
+    print(*a, flush=True)
+
+
+@pytest.mark.parametrize("dtype", QUANT, ids=lambda d: NAMES[d])
+@pytest.mark.parametrize("batch", [2, 7, 8, 130])
+def test_matmul_batched_matches_oracle(gpu_ctx, oracle, dtype, batch):
+    rows, cols = 200, 1024  # a ragged last row tile (200 = 128 + 72)
+    _print("gemm", NAMES[dtype], rows, cols, batch)
+    w = random_matrix(dtype, rows, cols, seed=40 + dtype + batch)
+    x = np.random.default_rng(batch).normal(0, 1, batch * cols).astype(np.float32)
+    W = gpu_ctx.upload(dtype, w, (cols, rows))
+    y = W.matmul(x, batch).reshape(batch, rows)
+    y_ref, mag = oracle.matmul_f64(dtype, w, rows, cols, x, batch)
+    check_prefill_path(y, y_ref, mag, f"{NAMES[dtype]} batch {batch}")
+
+
+@pytest.mark.parametrize("dtype", [Q4_K, Q6_K], ids=lambda d: NAMES[d])
+def test_prefill_7b_k4096_block(gpu_ctx, oracle, dtype):
+    """A 7B-shaped slice: K = 4096, 512 tokens, 384 weight rows."""
+    rows, cols, batch = 384, 4096, 512
+    _print("gemm 7B slice", NAMES[dtype])
+    w = random_matrix(dtype, rows, cols, seed=7)
+    x = np.random.default_rng(7).normal(0, 1, batch * cols).astype(np.float32)
+    y = gpu_ctx.upload(dtype, w, (cols, rows)).matmul(x, batch).reshape(batch, rows)
+    y_ref, mag = oracle.matmul_f64(dtype, w, rows, cols, x, batch)
+    check_prefill_path(y, y_ref, mag, NAMES[dtype])
+
+
+@pytest.mark.parametrize("dtype,rows,cols", [(Q4_K, 14336, 4096), (Q6_K, 4096, 14336),
+                                             (Q4_K, 6144, 4096)],
+                         ids=["gate_up_q4k", "down_q6k", "qkv_q4k"])
+def test_prefill_7b_full_size_sampled_rows(gpu_ctx, oracle, dtype, rows, cols):
+    """Full 7B prefill GEMMs at 512 tokens; a seeded sample of 96 weight rows
+    (all 512 tokens each) is checked against the oracle, which is row-local."""
+    batch = 512
+    _print("gemm full", NAMES[dtype], rows, cols)
+    w = random_matrix(dtype, rows, cols, seed=rows)
+    x = np.random.default_rng(cols).normal(0, 1, batch * cols).astype(np.float32)
+    y = gpu_ctx.upload(dtype, w, (cols, rows)).matmul(x, batch).reshape(batch, rows)
+    assert np.all(np.isfinite(y))
+    rb = row_bytes(dtype, cols)
+    pick = np.sort(np.random.default_rng(5).choice(rows, 96, replace=False))
+    pick[-1] = rows - 1
+    sub = np.concatenate([w[r * rb:(r + 1) * rb] for r in pick])
+    y_ref, mag = oracle.matmul_f64(dtype, sub, len(pick), cols, x, batch)
+    check_prefill_path(y[:, pick], y_ref, mag, NAMES[dtype])
+
+
+def test_batched_rows_are_independent_of_batch(gpu_ctx):
+    """Each token's output row does not depend on the other tokens of the
+    batch (a 128-token tile boundary and a partial tile included)."""
+    rows, cols = 256, 512
+    w = random_matrix(Q4_K, rows, cols, seed=3)
+    x = np.random.default_rng(3).normal(0, 1, 300 * cols).astype(np.float32)
+    W = gpu_ctx.upload(Q4_K, w, (cols, rows))
+    full = W.matmul(x, 300).reshape(300, rows)
+    for lo, hi in ((0, 2), (127, 129), (250, 300)):
+        part = W.matmul(x[lo * cols:hi * cols], hi - lo).reshape(hi - lo, rows)
+        assert np.array_equal(part, full[lo:hi])
+
+
+def test_batched_shape_errors(gpu_ctx):
+    w = random_matrix(Q8_0, 8, 96, seed=0)  # 96 columns: not a multiple of 64
+    W = gpu_ctx.upload(Q8_0, w, (96, 8))
+    with pytest.raises(ValueError):
+        W.matmul(np.zeros(2 * 96, np.float32), 2)
+    W2 = gpu_ctx.upload(Q2_0C, random_matrix(Q2_0C, 8, 512, seed=0), (512, 8))
+    with pytest.raises(ValueError):
+        W2.matmul(np.zeros(3 * 512 - 1, np.float32), 3)
