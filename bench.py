@@ -95,6 +95,28 @@ def gemv_rate(hyq, ctx, ev, dtype, rows, cols, seed=1, min_bytes=1 << 30):
     return ms * 1e3, alg / (ms * 1e-3) / 1e9
 
 
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def prefill_rate(hyq, ctx, ev, dtype, rows, cols, batch, seed=3):
+    """Batched matmul (f16 MFMA): (us per launch, TFLOP/s) at [rows x cols] x
+    [cols x batch], inputs resident in HBM."""
+    from synth import random_matrix
+    w = random_matrix(dtype, rows, cols, seed=seed)
+    W = ctx.upload(dtype, w, (cols, rows))
+    x = ctx.array(np.random.default_rng(seed).normal(0, 1, batch * cols).astype(np.float32))
+    y = ctx.empty(batch * rows, np.float32)
+    L = hyq.lib()
+
+    def launch(i):
+        L.hyq_matmul_d(ctx.handle, W.handle, x.ptr, batch, y.ptr)
+
+    ms = ev.time_ms(launch, 20)
+    flop = 2.0 * rows * cols * batch
+    W.release()
+    return ms * 1e3, flop / (ms * 1e-3) / 1e12
+
+
 def decode_kernel_table(hyq, ctx, ev, dec_weights, model):
     """Per-launch time of each GEMV of the decode step over the model's own 32
     layers of weights (the step's memory behaviour), plus its time per step."""
@@ -168,6 +190,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-gemv", action="store_true", help="skip the standalone GEMV table")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="skip the batched (prefill) GEMM table")
     ap.add_argument("--cpu-steps", type=int, default=3)
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the step's kernels one by one instead of replaying a HIP "
@@ -242,6 +266,18 @@ def main() -> int:
                               frac=round(gbs / HBM_PEAK_GBS, 4))
             log(f"{name}: {us:.2f} us {gbs:.0f} GB/s")
 
+    prefill = {}
+    if not args.no_prefill:
+        for name, (dt_, rows, cols) in {
+            "C4_Q4_K_gate_up_14336x4096x512": (Q4_K, 14336, 4096),
+            "C4_Q6_K_down_4096x14336x512": (Q6_K, 4096, 14336),
+            "C4_Q4_K_qkv_6144x4096x512": (Q4_K, 6144, 4096),
+        }.items():
+            us, tf = prefill_rate(hyq, ctx, ev, dt_, rows, cols, 512)
+            prefill[name] = dict(us=round(us, 2), TFLOPs=round(tf, 1),
+                                 frac=round(tf / MFMA_F16_PEAK_TFLOPS, 4))
+            log(f"{name}: {us:.1f} us {tf:.0f} TFLOP/s")
+
     cpu = None
     if not args.no_cpu:
         log("cpu baseline")
@@ -263,6 +299,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "decode_kernels": table,
         "gemv": gemv,
+        "prefill": prefill,
         "reference_published": {"value": 86.86, "unit": "tok/s",
                                 "note": "Apple M2 Pro 8 threads, real weights, ~14-18 "
                                         "positions (docs/validation.md:70); not this config"},

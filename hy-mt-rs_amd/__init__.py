@@ -60,6 +60,9 @@ SIGNATURES = {
     "hyq_gemv_isums_d": (I, [P, P, P, P]),
     "hyq_matmul_d": (I, [P, P, P, SZ, P]),
     "hyq_dequant_rows_d": (I, [P, P, SZ, SZ, P]),
+    "hyq_moe_scratch_bytes": (SZ, [SZ, SZ, SZ, SZ, SZ]),
+    "hyq_moe_experts_d": (I, [P, P, P, P, P, SZ, P, P, P, SZ, P, SZ, P]),
+    "hyq_moe_experts": (I, [P, P, P, P, P, SZ, P, P, P, SZ, P]),
     "hyq_decode_d": (I, [P, I, P, SZ, P, SZ]),
     "hyq_embed_row_d": (I, [P, P, P, P]),
     "hyq_rms_norm_q8_d": (I, [P, P, P, SZ, ctypes.c_float, P, P]),
@@ -337,6 +340,28 @@ class Q8:
 
     def quantize_into(self, x_dev_ptr: int) -> None:
         check(lib().hyq_quantize_q8_d(self.ctx.handle, x_dev_ptr, self.n, self.handle))
+
+
+def moe_experts(gate: "Weight", up: "Weight", down: "Weight", x: np.ndarray, tokens: int,
+                pair_token, pair_expert, pair_weight, out: np.ndarray) -> np.ndarray:
+    """Expert loop of Moe::forward (src/model.rs:699-725): returns ``out`` plus,
+    per token and in ascending expert order, weight * DenseFfn_e(x[token]).
+    ``out`` [tokens*hidden] is the seed (the shared expert's output)."""
+    x = np.ascontiguousarray(x, np.float32)
+    hidden = gate.dims[0]
+    if x.size != tokens * hidden:
+        raise ValueError("invalid activation shape")
+    pt = np.ascontiguousarray(pair_token, np.int32)
+    pe = np.ascontiguousarray(pair_expert, np.int32)
+    pw = np.ascontiguousarray(pair_weight, np.float32)
+    if not (pt.size == pe.size == pw.size):
+        raise ValueError("routing lists differ in length")
+    res = np.array(out, np.float32, copy=True).reshape(-1)
+    if res.size != tokens * hidden:
+        raise ValueError("invalid output shape")
+    check(lib().hyq_moe_experts(gate.ctx.handle, gate.handle, up.handle, down.handle, _ptr(x),
+                                tokens, _ptr(pt), _ptr(pe), _ptr(pw), pt.size, _ptr(res)))
+    return res
 
 
 def isums_per_row(dtype: int, cols: int) -> int:

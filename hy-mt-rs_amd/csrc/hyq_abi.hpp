@@ -117,7 +117,7 @@ struct hyq_q8 {
 struct hyq_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
-    hyq::Scratch x, y, bytes;
+    hyq::Scratch x, y, bytes, xh, moe;
     hyq_q8 *q8 = nullptr; // grown on demand for host-pointer calls
 };
 

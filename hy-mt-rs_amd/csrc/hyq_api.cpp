@@ -256,6 +256,8 @@ void hyq_ctx_destroy(hyq_ctx *ctx)
     ctx->x.buf.reset();
     ctx->y.buf.reset();
     ctx->bytes.buf.reset();
+    ctx->xh.buf.reset();
+    ctx->moe.buf.reset();
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
@@ -517,8 +519,14 @@ int hyq_matmul_d(hyq_ctx *ctx, const hyq_weight *w, const float *x_d, size_t bat
     if (w->cols % 64) return fail(HYQ_EINVAL, "matmul: cols %zu is not a multiple of 64", w->cols);
     if ((uintptr_t)x_d % 16 || (uintptr_t)y_d % 16)
         return fail(HYQ_EINVAL, "matmul: device buffers must be 16-byte aligned");
-    if (batch > 0x7fffffff / 2) return fail(HYQ_EINVAL, "matmul: batch %zu too large", batch);
-    HYQ_LAUNCH(launch_gemm_f16(w->dtype, w->view, (int)w->cols, x_d, (int)batch, y_d,
+    if (batch > 65535) return fail(HYQ_EINVAL, "matmul: batch %zu exceeds 65535", batch);
+    const size_t xh_bytes = align_up(batch * w->cols * 2, 256);
+    rc = ctx->xh.reserve(ctx->device, xh_bytes + batch * 4);
+    if (rc) return rc;
+    _Float16 *xh = (_Float16 *)ctx->xh.ptr();
+    float *rscale = (float *)((uint8_t *)ctx->xh.ptr() + xh_bytes);
+    HYQ_LAUNCH(launch_to_f16(x_d, (int)batch, (int)w->cols, xh, rscale, ctx->stream), "to_f16");
+    HYQ_LAUNCH(launch_gemm_f16(w->dtype, w->view, (int)w->cols, xh, rscale, (int)batch, y_d,
                                ctx->stream),
                "gemm_f16");
     return HYQ_OK;

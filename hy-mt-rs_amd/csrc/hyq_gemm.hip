@@ -1,15 +1,21 @@
-// Batched matmul (Weight::matmul batch >= 2, src/quant.rs:272-344) for
-// gfx950: Y[batch, rows] = X[batch, cols] W^T with weight tiles dequantized
-// to f16 in LDS and v_mfma_f32_32x32x16_f16 accumulating in f32 (the tile
-// engine is in hyq_tile.hpp).
+// Batched products on gfx950 with the f16-MFMA tile engine of hyq_tile.hpp:
+//   gemm_f16      Weight::matmul at batch >= 2 (src/quant.rs:272-344):
+//                 Y[batch, rows] = X[batch, cols] W^T;
+//   moe_*         Moe::forward's expert loop (src/model.rs:699-725): token
+//                 rows grouped by expert, each expert's DenseFfn as a
+//                 gate/up GEMM with the SiLU product in its epilogue and a
+//                 down GEMM, then the routed sum in ascending expert order.
 //
-// Tile order is XCD-aware: workgroups are dispatched round-robin over the 8
-// XCDs, so workgroup b runs on XCD b % 8; tile index (b % 8) * per + b / 8
-// gives each XCD a contiguous range of tiles, and the BN-token tiles of one
-// weight row block land on the same XCD and share its L2.
+// Activations are rounded to f16 once (to_f16 / the gate-up epilogue) and
+// read by the tiles as f16. Tile order is XCD-aware: workgroups are
+// dispatched round-robin over the 8 XCDs, so workgroup b runs on XCD b % 8;
+// tile (b % 8) * per + b / 8 gives each XCD a contiguous range of tiles, and
+// the tiles sharing one weight row block land on the same XCD and its L2.
 #include <hip/hip_runtime.h>
 
 #include "hyq_tile.hpp"
+
+#pragma clang fp contract(off)
 
 namespace hyq {
 
@@ -17,46 +23,86 @@ namespace {
 
 using namespace tile;
 
+__device__ __forceinline__ int xcd_tile(int total)
+{
+    const int per = (total + 7) / 8;
+    return (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+}
+
+// One workgroup per row: xh[r][k] = f16(x[src][k] * 2^-e) and rscale[r] =
+// 2^e, where e = ceil(log2(max_k |x[src][k]|)) - 14 puts the row's largest
+// magnitude at or below 2^14, so no value overflows f16 or drops into its
+// subnormals; the power-of-two scale is exact and the GEMM epilogues multiply
+// it back. src = r, or ptok[order[r]] when order is given; rows r >= *count
+// (when count is given) are left alone. A row with a zero, infinite or NaN
+// maximum keeps scale 1 (and its infinities / NaNs propagate).
+__global__ __launch_bounds__(256) void rows_to_f16_kernel(const float *__restrict__ x, int K,
+                                                          const int *__restrict__ order,
+                                                          const int *__restrict__ ptok,
+                                                          const int *__restrict__ count,
+                                                          _Float16 *__restrict__ xh,
+                                                          float *__restrict__ rscale)
+{
+    __shared__ float wmax[4];
+    const int r = blockIdx.x;
+    if (count && r >= *count) return;
+    const size_t src = order ? (size_t)ptok[order[r]] : (size_t)r;
+    const float4 *x4 = reinterpret_cast<const float4 *>(x + src * K);
+    const int t = threadIdx.x, n4 = K / 4;
+    float m = 0.f;
+    for (int i = t; i < n4; i += 256) {
+        const float4 v = x4[i];
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        if (v.x != v.x || v.y != v.y || v.z != v.z || v.w != v.w) m = INFINITY;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if ((t & 63) == 0) wmax[t >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    int e = 0;
+    if (m > 0.f && m < INFINITY) {
+        int ex;
+        const float fr = frexpf(m, &ex); // m = fr * 2^ex, fr in [0.5, 1)
+        e = (fr == 0.5f ? ex - 1 : ex) - 14;
+        e = max(-110, min(114, e)); // both 2^e and 2^-e stay normal floats
+    }
+    const float inv = ldexpf(1.0f, -e);
+    if (t == 0) rscale[r] = ldexpf(1.0f, e);
+    _Float16 *o = xh + (size_t)r * K;
+    for (int i = t; i < n4; i += 256) {
+        const float4 v = x4[i];
+        const half2v a = __builtin_convertvector((float2v){v.x * inv, v.y * inv}, half2v);
+        const half2v b = __builtin_convertvector((float2v){v.z * inv, v.w * inv}, half2v);
+        *reinterpret_cast<half2v *>(o + 4 * i) = a;
+        *reinterpret_cast<half2v *>(o + 4 * i + 2) = b;
+    }
+}
+
 template <int F>
 __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(WView w, int M, int K,
-                                                          const float *__restrict__ x, int N,
+                                                          const _Float16 *__restrict__ xh,
+                                                          const float *__restrict__ rscale, int N,
                                                           float *__restrict__ y, int mtiles,
                                                           int ntiles)
 {
-    __shared__ __attribute__((aligned(16))) _Float16 Ws[BM * LDK];
-    __shared__ __attribute__((aligned(16))) _Float16 Xs[BN * LDK];
-    const int total = mtiles * ntiles;
-    const int per = (total + 7) / 8;
-    const int T = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
-    if (T >= total) return;
+    __shared__ __attribute__((aligned(16))) _Float16 lds[4 * TILE_HALVES];
+    const int T = xcd_tile(mtiles * ntiles);
+    if (T >= mtiles * ntiles) return;
     const int m0 = (T / ntiles) * BM, n0 = (T % ntiles) * BN;
-    const int t = threadIdx.x, wave = t >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int drow = t >> 1, dh = t & 1;
-    const bool row_ok = m0 + drow < M;
+    const int wave = threadIdx.x >> 6, wm = wave >> 1, wn = wave & 1;
 
     f32x16 acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
-
-    auto xrow = [&](int r) -> const float * {
-        const int n = n0 + r;
-        return n < N ? x + (size_t)n * K : nullptr;
+    zero_acc(acc);
+    auto wsrc = [&](int lrow, WView &v, int &row) {
+        v = w;
+        row = m0 + lrow < M ? m0 + lrow : -1;
     };
-    for (int k0 = 0; k0 < K; k0 += BK) {
-        float4 xv[8];
-        load_x(xrow, k0, xv);
-        if (row_ok) Deq<F>::run(w, m0 + drow, k0, dh, Ws + drow * LDK);
-        else zero_half(Ws + drow * LDK, dh);
-        store_x(Xs, xv);
-        __syncthreads();
-        mma_step(Ws, Xs, wm, wn, acc);
-        __syncthreads();
-    }
+    auto xrow = [&](int r) -> const _Float16 * {
+        return n0 + r < N ? xh + (size_t)(n0 + r) * K : nullptr;
+    };
+    auto arow = [&](int i) { return wm * 64 + 32 * i; };
+    k_loop<F>(wsrc, xrow, arow, K, wn, lds, acc);
 
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -65,38 +111,274 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(WView w, int M, int K,
             const int n = n0 + acc_col(wn, j);
             if (n >= N) continue;
             float *yr = y + (size_t)n * M;
+            const float sc = rscale[n];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const int m = m0 + acc_row(wm, i, 4 * g);
+                const int m = m0 + arow(i) + acc_row_in_block(4 * g);
                 if (m + 3 < M && (M & 3) == 0) {
                     *reinterpret_cast<float4 *>(yr + m) =
-                        make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                                    acc[i][j][4 * g + 3]);
+                        make_float4(acc[i][j][4 * g] * sc, acc[i][j][4 * g + 1] * sc,
+                                    acc[i][j][4 * g + 2] * sc, acc[i][j][4 * g + 3] * sc);
                 } else {
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        if (m + e < M) yr[m + e] = acc[i][j][4 * g + e];
+                        if (m + e < M) yr[m + e] = acc[i][j][4 * g + e] * sc;
                 }
             }
         }
 }
 
+// ---------------------------------------------------------------------------
+// MoE planning: one workgroup groups the routed (token, expert) pairs.
+//   order[q]   pair at position q of the expert-grouped sequence (experts
+//              ascending; inside an expert, pairs in input order - the order
+//              in which Moe::forward pushes assignments, src/model.rs:694-697)
+//   eoff[e]    first position of expert e (eoff[E] = valid pairs)
+//   tiles[i]   (expert, chunk) of every BN-token chunk of a non-empty expert
+//   toff/tlist for each token, its positions q in ascending expert order
+//              (the order the scatter-add visits them, src/model.rs:700-722)
+// Pairs whose token or expert is out of range are dropped.
+// ---------------------------------------------------------------------------
+constexpr int PLAN_MAX = 4096; // experts and tokens per call
+
+// Exclusive scan of cnt[0..n) in LDS into off[0..n] (global), 256 threads.
+__device__ void block_exclusive_scan(const int *cnt, int n, int *off, int *lsum)
+{
+    const int t = threadIdx.x;
+    const int per = (n + 255) / 256;
+    const int lo = t * per, hi = min(n, lo + per);
+    int s = 0;
+    for (int i = lo; i < hi; ++i) s += cnt[i];
+    lsum[t] = s;
+    __syncthreads();
+    for (int d = 1; d < 256; d <<= 1) {
+        const int v = t >= d ? lsum[t - d] : 0;
+        __syncthreads();
+        lsum[t] += v;
+        __syncthreads();
+    }
+    int run = lsum[t] - s;
+    for (int i = lo; i < hi; ++i) {
+        off[i] = run;
+        run += cnt[i];
+    }
+    if (t == 255) off[n] = lsum[255];
+    __syncthreads();
+}
+
+// Stable counting sort: for i in [0, n), rank[i] = number of j < i with
+// key(j) == key(i), plus the running count of key(i) from earlier chunks;
+// cnt[k] ends as the total count of key k. key < 0 = skipped.
+template <class KeyFn>
+__device__ void stable_rank(const KeyFn &key, int n, int *cnt, int nkeys, int *rank, int *lkey)
+{
+    const int t = threadIdx.x;
+    for (int i = t; i < nkeys; i += 256) cnt[i] = 0;
+    __syncthreads();
+    for (int base = 0; base < n; base += 256) {
+        const int i = base + t;
+        const int k = i < n ? key(i) : -1;
+        lkey[t] = k;
+        __syncthreads();
+        if (k >= 0) {
+            int r = 0;
+            for (int j = 0; j < t; ++j) r += lkey[j] == k;
+            rank[i] = cnt[k] + r;
+        }
+        __syncthreads();
+        if (k >= 0) atomicAdd(&cnt[k], 1);
+        __syncthreads();
+    }
+}
+
+__global__ __launch_bounds__(256) void moe_plan_kernel(const int *__restrict__ ptok,
+                                                       const int *__restrict__ pexp, int P, int T,
+                                                       int E, int *eoff, int *order, int *rank,
+                                                       int *toff, int *tlist, int *tiles,
+                                                       int *ntiles)
+{
+    __shared__ int cnt[PLAN_MAX];
+    __shared__ int lkey[256];
+    __shared__ int lsum[256];
+    const int t = threadIdx.x;
+    auto ekey = [&](int p) {
+        const int tok = ptok[p], e = pexp[p];
+        return (tok >= 0 && tok < T && e >= 0 && e < E) ? e : -1;
+    };
+    // group pairs by expert (stable)
+    stable_rank(ekey, P, cnt, E, rank, lkey);
+    block_exclusive_scan(cnt, E, eoff, lsum);
+    for (int p = t; p < P; p += 256) {
+        const int e = ekey(p);
+        if (e >= 0) order[eoff[e] + rank[p]] = p;
+    }
+    // BN-token chunks of every expert
+    for (int e = t; e < E; e += 256) cnt[e] = (cnt[e] + BN - 1) / BN;
+    __syncthreads();
+    block_exclusive_scan(cnt, E, rank, lsum); // rank[0..E] reused as chunk offsets
+    for (int e = t; e < E; e += 256)
+        for (int c = 0; c < cnt[e]; ++c) {
+            tiles[2 * (rank[e] + c)] = e;
+            tiles[2 * (rank[e] + c) + 1] = c;
+        }
+    if (t == 0) *ntiles = rank[E];
+    __syncthreads();
+    // for each token, its positions in ascending expert order
+    const int nv = eoff[E];
+    auto tkey = [&](int q) { return ptok[order[q]]; };
+    stable_rank(tkey, nv, cnt, T, rank, lkey);
+    block_exclusive_scan(cnt, T, toff, lsum);
+    for (int q = t; q < nv; q += 256) tlist[toff[tkey(q)] + rank[q]] = q;
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u)
+{
+    // (g / (1 + exp(-g))) * u, DenseFfn::forward (src/model.rs:680-682)
+    return (g / (1.0f + expf(-g))) * u;
+}
+
+// Gate and up of one expert chunk: LDS rows 0..63 dequantize gate rows
+// m0..m0+63 and rows 64..127 the same rows of up; wave (wm, wn) holds gate
+// rows 32*wm.. in acc[0] and the matching up rows in acc[1], so the SiLU
+// product pairs registers one to one. H[q][m] = silu(g) * u in f32, with g
+// and u scaled back by the token row's activation scale.
+template <int F>
+__global__ __launch_bounds__(256, 2) void moe_gate_up_kernel(
+    WView gate, WView up, int mid, int K, const int *__restrict__ eoff,
+    const int *__restrict__ tiles, const int *__restrict__ ntiles,
+    const _Float16 *__restrict__ xg, const float *__restrict__ xscale, float *__restrict__ H,
+    int mtiles, int max_tiles)
+{
+    __shared__ __attribute__((aligned(16))) _Float16 lds[4 * TILE_HALVES];
+    const int T = xcd_tile(mtiles * max_tiles);
+    if (T >= mtiles * max_tiles) return;
+    const int ti = T / mtiles, mt = T % mtiles;
+    if (ti >= *ntiles) return;
+    const int e = tiles[2 * ti], c = tiles[2 * ti + 1];
+    const int nb = eoff[e] + c * BN;
+    const int cnt = min(BN, eoff[e + 1] - nb);
+    const int m0 = mt * 64;
+    const int wave = threadIdx.x >> 6, wm = wave >> 1, wn = wave & 1;
+
+    f32x16 acc[2][2];
+    zero_acc(acc);
+    auto wsrc = [&](int lrow, WView &v, int &row) {
+        const int m = m0 + (lrow & 63);
+        v = lrow < 64 ? gate : up;
+        row = m < mid ? e * mid + m : -1;
+    };
+    auto xrow = [&](int r) -> const _Float16 * {
+        return r < cnt ? xg + (size_t)(nb + r) * K : nullptr;
+    };
+    auto arow = [&](int i) { return 64 * i + 32 * wm; };
+    k_loop<F>(wsrc, xrow, arow, K, wn, lds, acc);
+
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int r = acc_col(wn, j);
+        if (r >= cnt) continue;
+        float *hr = H + (size_t)(nb + r) * mid;
+        const float sc = xscale[nb + r];
+#pragma unroll
+        for (int e4 = 0; e4 < 16; ++e4) {
+            const int m = m0 + 32 * wm + acc_row_in_block(e4);
+            if (m < mid) hr[m] = silu_mul(acc[0][j][e4] * sc, acc[1][j][e4] * sc);
+        }
+    }
+}
+
+// Down of one expert chunk: outp[q][m] = down_e[m] . H[q] (H in f16 with its
+// row scale).
+template <int F>
+__global__ __launch_bounds__(256, 2) void moe_down_kernel(
+    WView down, int hidden, int K, const int *__restrict__ eoff, const int *__restrict__ tiles,
+    const int *__restrict__ ntiles, const _Float16 *__restrict__ H,
+    const float *__restrict__ hscale, float *__restrict__ outp, int mtiles, int max_tiles)
+{
+    __shared__ __attribute__((aligned(16))) _Float16 lds[4 * TILE_HALVES];
+    const int T = xcd_tile(mtiles * max_tiles);
+    if (T >= mtiles * max_tiles) return;
+    const int ti = T / mtiles, mt = T % mtiles;
+    if (ti >= *ntiles) return;
+    const int e = tiles[2 * ti], c = tiles[2 * ti + 1];
+    const int nb = eoff[e] + c * BN;
+    const int cnt = min(BN, eoff[e + 1] - nb);
+    const int m0 = mt * BM;
+    const int wave = threadIdx.x >> 6, wm = wave >> 1, wn = wave & 1;
+
+    f32x16 acc[2][2];
+    zero_acc(acc);
+    auto wsrc = [&](int lrow, WView &v, int &row) {
+        v = down;
+        row = m0 + lrow < hidden ? e * hidden + m0 + lrow : -1;
+    };
+    auto xrow = [&](int r) -> const _Float16 * {
+        return r < cnt ? H + (size_t)(nb + r) * K : nullptr;
+    };
+    auto arow = [&](int i) { return wm * 64 + 32 * i; };
+    k_loop<F>(wsrc, xrow, arow, K, wn, lds, acc);
+
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int r = acc_col(wn, j);
+            if (r >= cnt) continue;
+            float *orow = outp + (size_t)(nb + r) * hidden;
+            const float sc = hscale[nb + r];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int m = m0 + arow(i) + acc_row_in_block(4 * g);
+#pragma unroll
+                for (int e4 = 0; e4 < 4; ++e4)
+                    if (m + e4 < hidden) orow[m + e4] = acc[i][j][4 * g + e4] * sc;
+            }
+        }
+}
+
+// out[t][i] += w * value[i] per routed pair of token t, experts ascending
+// (src/model.rs:715-722), as separate rounded products and sums.
+__global__ __launch_bounds__(256) void moe_combine_kernel(float *__restrict__ out, int hidden,
+                                                          const int *__restrict__ toff,
+                                                          const int *__restrict__ tlist,
+                                                          const int *__restrict__ order,
+                                                          const float *__restrict__ pw,
+                                                          const float *__restrict__ outp)
+{
+    const int t = blockIdx.y;
+    const int col = blockIdx.x * 256 + threadIdx.x;
+    if (col >= hidden) return;
+    float acc = out[(size_t)t * hidden + col];
+    for (int i = toff[t]; i < toff[t + 1]; ++i) {
+        const int q = tlist[i];
+        acc = acc + pw[order[q]] * outp[(size_t)q * hidden + col];
+    }
+    out[(size_t)t * hidden + col] = acc;
+}
+
 } // namespace
 
-int launch_gemm_f16(int fmt, WView w, int cols, const float *x, int batch, float *y,
-                    void *stream)
+int launch_to_f16(const float *x, int rows, int K, _Float16 *xh, float *rscale, void *stream)
+{
+    if (rows <= 0) return 0;
+    hipLaunchKernelGGL(rows_to_f16_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream, x, K,
+                       nullptr, nullptr, nullptr, xh, rscale);
+    return (int)hipGetLastError();
+}
+
+int launch_gemm_f16(int fmt, WView w, int cols, const _Float16 *xh, const float *rscale,
+                    int batch, float *y, void *stream)
 {
     if (cols % BK) return (int)hipErrorInvalidValue;
     const int M = w.rows;
     const int mtiles = (M + BM - 1) / BM, ntiles = (batch + BN - 1) / BN;
-    const int total = mtiles * ntiles;
-    const int per = (total + 7) / 8;
+    const int per = (mtiles * ntiles + 7) / 8;
     dim3 grid(8 * per), block(256);
     hipStream_t st = (hipStream_t)stream;
 #define HYQ_GEMM(F)                                                                            \
     case F:                                                                                    \
-        hipLaunchKernelGGL(gemm_f16_kernel<F>, grid, block, 0, st, w, M, cols, x, batch, y,     \
-                           mtiles, ntiles);                                                    \
+        hipLaunchKernelGGL(gemm_f16_kernel<F>, grid, block, 0, st, w, M, cols, xh, rscale,      \
+                           batch, y, mtiles, ntiles);                                          \
         break;
     switch (fmt) {
         HYQ_GEMM(Q4_K)
@@ -107,6 +389,101 @@ int launch_gemm_f16(int fmt, WView w, int cols, const float *x, int batch, float
     default: return (int)hipErrorInvalidValue;
     }
 #undef HYQ_GEMM
+    return (int)hipGetLastError();
+}
+
+MoeLayout moe_layout(int tokens, int npairs, int experts, int hidden, int mid)
+{
+    MoeLayout L{};
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off += (bytes + 255) / 256 * 256;
+        return o;
+    };
+    L.max_tiles = npairs / BN + (experts < npairs ? experts : npairs) + 1;
+    L.eoff = take(4 * ((size_t)experts + 1));
+    L.order = take(4 * (size_t)npairs);
+    L.rank = take(4 * ((size_t)npairs + experts + tokens + 1));
+    L.toff = take(4 * ((size_t)tokens + 1));
+    L.tlist = take(4 * (size_t)npairs);
+    L.tiles = take(8 * (size_t)L.max_tiles);
+    L.ntiles = take(4);
+    L.xg = take(2 * (size_t)npairs * hidden);
+    L.xscale = take(4 * (size_t)npairs);
+    L.h32 = take(4 * (size_t)npairs * mid);
+    L.h = take(2 * (size_t)npairs * mid);
+    L.hscale = take(4 * (size_t)npairs);
+    L.outp = take(4 * (size_t)npairs * hidden);
+    L.bytes = off;
+    return L;
+}
+
+int moe_plan_max() { return PLAN_MAX; }
+
+int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int hidden, int mid,
+               const float *x, int tokens, const int *ptok, const int *pexp, const float *pw,
+               int npairs, int experts, uint8_t *scratch, const MoeLayout &L, float *out,
+               void *stream)
+{
+    if (hidden % BK || mid % BK || hidden % 4 || tokens > PLAN_MAX || experts > PLAN_MAX)
+        return (int)hipErrorInvalidValue;
+    hipStream_t st = (hipStream_t)stream;
+    int *eoff = (int *)(scratch + L.eoff), *order = (int *)(scratch + L.order);
+    int *rank = (int *)(scratch + L.rank), *toff = (int *)(scratch + L.toff);
+    int *tlist = (int *)(scratch + L.tlist), *tiles = (int *)(scratch + L.tiles);
+    int *ntiles = (int *)(scratch + L.ntiles);
+    _Float16 *xg = (_Float16 *)(scratch + L.xg), *H = (_Float16 *)(scratch + L.h);
+    float *xscale = (float *)(scratch + L.xscale), *hscale = (float *)(scratch + L.hscale);
+    float *h32 = (float *)(scratch + L.h32), *outp = (float *)(scratch + L.outp);
+    if (npairs == 0) return 0;
+
+    hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, ptok, pexp, npairs, tokens,
+                       experts, eoff, order, rank, toff, tlist, tiles, ntiles);
+    hipLaunchKernelGGL(rows_to_f16_kernel, dim3(npairs), dim3(256), 0, st, x, hidden, order,
+                       ptok, eoff + experts, xg, xscale);
+    {
+        const int mtiles = (mid + 63) / 64;
+        const int per = (mtiles * L.max_tiles + 7) / 8;
+        dim3 grid(8 * per), block(256);
+#define HYQ_MOE_GU(F)                                                                          \
+    case F:                                                                                    \
+        hipLaunchKernelGGL(moe_gate_up_kernel<F>, grid, block, 0, st, gate, up, mid, hidden,   \
+                           eoff, tiles, ntiles, xg, xscale, h32, mtiles, L.max_tiles);         \
+        break;
+        switch (fmt_gu) {
+            HYQ_MOE_GU(Q4_K)
+            HYQ_MOE_GU(Q6_K)
+            HYQ_MOE_GU(Q8_0)
+            HYQ_MOE_GU(Q2_0C)
+            HYQ_MOE_GU(STQ1_0)
+        default: return (int)hipErrorInvalidValue;
+        }
+#undef HYQ_MOE_GU
+    }
+    hipLaunchKernelGGL(rows_to_f16_kernel, dim3(npairs), dim3(256), 0, st, h32, mid, nullptr,
+                       nullptr, eoff + experts, H, hscale);
+    {
+        const int mtiles = (hidden + BM - 1) / BM;
+        const int per = (mtiles * L.max_tiles + 7) / 8;
+        dim3 grid(8 * per), block(256);
+#define HYQ_MOE_DN(F)                                                                          \
+    case F:                                                                                    \
+        hipLaunchKernelGGL(moe_down_kernel<F>, grid, block, 0, st, down, hidden, mid, eoff,     \
+                           tiles, ntiles, H, hscale, outp, mtiles, L.max_tiles);               \
+        break;
+        switch (fmt_down) {
+            HYQ_MOE_DN(Q4_K)
+            HYQ_MOE_DN(Q6_K)
+            HYQ_MOE_DN(Q8_0)
+            HYQ_MOE_DN(Q2_0C)
+            HYQ_MOE_DN(STQ1_0)
+        default: return (int)hipErrorInvalidValue;
+        }
+#undef HYQ_MOE_DN
+    }
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((hidden + 255) / 256, tokens), dim3(256), 0, st,
+                       out, hidden, toff, tlist, order, pw, outp);
     return (int)hipGetLastError();
 }
 

@@ -122,8 +122,25 @@ int launch_gemv(int fmt, int mode, const GemvArgs &args, void *stream);
 int launch_dequant_rows(int fmt, WView w, int row0, int nrows, int cols, float *out,
                         void *stream);
 int launch_decode_gguf(int fmt, const uint8_t *bytes, size_t nblocks, float *out, void *stream);
-int launch_gemm_f16(int fmt, WView w, int cols, const float *x, int batch, float *y,
-                    void *stream);
+// Batched products (hyq_gemm.hip): x [rows][K] f32 -> f16 with a power-of-two
+// scale per row (rscale), then the f16-MFMA GEMM
+// y[batch][w.rows] = rscale[batch] * (xh[batch][cols] W^T).
+int launch_to_f16(const float *x, int rows, int K, _Float16 *xh, float *rscale, void *stream);
+int launch_gemm_f16(int fmt, WView w, int cols, const _Float16 *xh, const float *rscale,
+                    int batch, float *y, void *stream);
+
+// Byte offsets of the MoE scratch regions (hyq_gemm.hip: moe_layout).
+struct MoeLayout {
+    size_t eoff, order, rank, toff, tlist, tiles, ntiles, xg, xscale, h32, h, hscale, outp, bytes;
+    int max_tiles;
+};
+MoeLayout moe_layout(int tokens, int npairs, int experts, int hidden, int mid);
+int moe_plan_max();
+// Expert loop of Moe::forward: gate/up/down are the whole [E] expert stacks.
+int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int hidden, int mid,
+               const float *x, int tokens, const int *ptok, const int *pexp, const float *pw,
+               int npairs, int experts, uint8_t *scratch, const MoeLayout &L, float *out,
+               void *stream);
 int isums_per_group(int fmt);
 
 } // namespace hyq

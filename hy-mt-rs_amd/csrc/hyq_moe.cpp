@@ -1,0 +1,143 @@
+// C ABI of the MoE expert products (include/hyq.h: hyq_moe_*): the expert
+// loop of Moe::forward (src/model.rs:699-725) on one device. The router
+// matmul, route() and the shared expert stay with the caller, as in the
+// reference they run before the loop and seed its output.
+#include <hip/hip_runtime.h>
+
+#include <vector>
+
+#include "hyq_abi.hpp"
+
+using namespace hyq;
+
+namespace {
+
+struct MoeShape {
+    size_t hidden, mid, experts;
+};
+
+int check_experts(hyq_ctx *ctx, const hyq_weight *gate, const hyq_weight *up,
+                  const hyq_weight *down, MoeShape *out)
+{
+    if (!ctx) return fail(HYQ_EINVAL, "moe: null context");
+    if (!gate || !up || !down) return fail(HYQ_EINVAL, "moe: null expert weight");
+    for (const hyq_weight *w : {gate, up, down}) {
+        if (w->rank != 3) return fail(HYQ_EINVAL, "moe: expert weights must have rank 3");
+        if (w->device != ctx->device) return fail(HYQ_EINVAL, "moe: weight on another device");
+        if (!is_quant(w->dtype)) return fail(HYQ_EDTYPE, "moe: dtype %d has no batched path", w->dtype);
+    }
+    const size_t hidden = gate->dims[0], mid = gate->dims[1], E = gate->dims[2];
+    if (up->dims[0] != hidden || up->dims[1] != mid || up->dims[2] != E)
+        return fail(HYQ_EINVAL, "moe: up shape differs from gate");
+    if (down->dims[0] != mid || down->dims[1] != hidden || down->dims[2] != E)
+        return fail(HYQ_EINVAL, "moe: down must be [mid, hidden, experts]");
+    if (gate->dtype != up->dtype) return fail(HYQ_EDTYPE, "moe: gate and up formats differ");
+    if (hidden % 64 || mid % 64)
+        return fail(HYQ_EINVAL, "moe: hidden %zu and mid %zu must be multiples of 64", hidden, mid);
+    if (E > (size_t)moe_plan_max())
+        return fail(HYQ_EINVAL, "moe: %zu experts exceed %d", E, moe_plan_max());
+    *out = MoeShape{hidden, mid, E};
+    return HYQ_OK;
+}
+
+int check_counts(size_t tokens, size_t npairs)
+{
+    if (tokens == 0 || tokens > (size_t)moe_plan_max())
+        return fail(HYQ_EINVAL, "moe: %zu tokens (1..%d per call)", tokens, moe_plan_max());
+    if (npairs > 65535) return fail(HYQ_EINVAL, "moe: %zu pairs exceed 65535", npairs);
+    return HYQ_OK;
+}
+
+} // namespace
+
+extern "C" {
+
+size_t hyq_moe_scratch_bytes(size_t tokens, size_t npairs, size_t experts, size_t hidden,
+                             size_t mid)
+{
+    if (tokens > (size_t)moe_plan_max() || npairs > 65535 || experts > (size_t)moe_plan_max() ||
+        hidden > (1u << 20) || mid > (1u << 20))
+        return 0;
+    return moe_layout((int)tokens, (int)npairs, (int)experts, (int)hidden, (int)mid).bytes;
+}
+
+int hyq_moe_experts_d(hyq_ctx *ctx, const hyq_weight *gate, const hyq_weight *up,
+                      const hyq_weight *down, const float *x_d, size_t tokens,
+                      const int32_t *pair_token_d, const int32_t *pair_expert_d,
+                      const float *pair_weight_d, size_t npairs, void *scratch_d,
+                      size_t scratch_bytes, float *out_d)
+{
+    MoeShape s;
+    int rc = check_experts(ctx, gate, up, down, &s);
+    if (!rc) rc = check_counts(tokens, npairs);
+    if (rc) return rc;
+    if (npairs == 0) return HYQ_OK;
+    if (!x_d || !out_d || !pair_token_d || !pair_expert_d || !pair_weight_d || !scratch_d)
+        return fail(HYQ_EINVAL, "moe: null buffer");
+    if ((uintptr_t)x_d % 16 || (uintptr_t)scratch_d % 256)
+        return fail(HYQ_EINVAL, "moe: x must be 16-byte and scratch 256-byte aligned");
+    const MoeLayout L =
+        moe_layout((int)tokens, (int)npairs, (int)s.experts, (int)s.hidden, (int)s.mid);
+    if (scratch_bytes < L.bytes)
+        return fail(HYQ_EINVAL, "moe: scratch %zu bytes < %zu", scratch_bytes, L.bytes);
+    DeviceGuard g(ctx->device);
+    HYQ_LAUNCH(launch_moe(gate->dtype, down->dtype, gate->view, up->view, down->view,
+                          (int)s.hidden, (int)s.mid, x_d, (int)tokens, pair_token_d,
+                          pair_expert_d, pair_weight_d, (int)npairs, (int)s.experts,
+                          (uint8_t *)scratch_d, L, out_d, ctx->stream),
+               "moe");
+    return HYQ_OK;
+}
+
+int hyq_moe_experts(hyq_ctx *ctx, const hyq_weight *gate, const hyq_weight *up,
+                    const hyq_weight *down, const float *x, size_t tokens,
+                    const int32_t *pair_token, const int32_t *pair_expert,
+                    const float *pair_weight, size_t npairs, float *out)
+{
+    MoeShape s;
+    int rc = check_experts(ctx, gate, up, down, &s);
+    if (!rc) rc = check_counts(tokens, npairs);
+    if (rc) return rc;
+    if (!x || !out) return fail(HYQ_EINVAL, "moe: null buffer");
+    if (npairs && (!pair_token || !pair_expert || !pair_weight))
+        return fail(HYQ_EINVAL, "moe: null routing list");
+    for (size_t p = 0; p < npairs; ++p) {
+        if (pair_token[p] < 0 || (size_t)pair_token[p] >= tokens)
+            return fail(HYQ_EINVAL, "moe: pair %zu names token %d of %zu", p, pair_token[p], tokens);
+        if (pair_expert[p] < 0 || (size_t)pair_expert[p] >= s.experts)
+            return fail(HYQ_EINVAL, "moe: pair %zu names expert %d of %zu", p, pair_expert[p],
+                        s.experts);
+    }
+    if (npairs == 0) return HYQ_OK;
+    DeviceGuard g(ctx->device);
+    const MoeLayout L =
+        moe_layout((int)tokens, (int)npairs, (int)s.experts, (int)s.hidden, (int)s.mid);
+    const size_t xbytes = tokens * s.hidden * 4;
+    const size_t pbytes = align_up(npairs * 4, 256);
+    // x | out | tokens | experts | weights in ctx->x, the plan in ctx->moe
+    rc = ctx->x.reserve(ctx->device, 2 * align_up(xbytes, 256) + 3 * pbytes);
+    if (!rc) rc = ctx->moe.reserve(ctx->device, L.bytes);
+    if (rc) return rc;
+    uint8_t *base = (uint8_t *)ctx->x.ptr();
+    float *xd = (float *)base;
+    float *od = (float *)(base + align_up(xbytes, 256));
+    uint8_t *pd = base + 2 * align_up(xbytes, 256);
+    hipStream_t st = ctx->stream;
+    HYQ_HIP(hipMemcpyAsync(xd, x, xbytes, hipMemcpyHostToDevice, st), "hipMemcpy");
+    HYQ_HIP(hipMemcpyAsync(od, out, xbytes, hipMemcpyHostToDevice, st), "hipMemcpy");
+    HYQ_HIP(hipMemcpyAsync(pd, pair_token, npairs * 4, hipMemcpyHostToDevice, st), "hipMemcpy");
+    HYQ_HIP(hipMemcpyAsync(pd + pbytes, pair_expert, npairs * 4, hipMemcpyHostToDevice, st),
+            "hipMemcpy");
+    HYQ_HIP(hipMemcpyAsync(pd + 2 * pbytes, pair_weight, npairs * 4, hipMemcpyHostToDevice, st),
+            "hipMemcpy");
+    HYQ_LAUNCH(launch_moe(gate->dtype, down->dtype, gate->view, up->view, down->view,
+                          (int)s.hidden, (int)s.mid, xd, (int)tokens, (const int *)pd,
+                          (const int *)(pd + pbytes), (const float *)(pd + 2 * pbytes),
+                          (int)npairs, (int)s.experts, (uint8_t *)ctx->moe.ptr(), L, od, st),
+               "moe");
+    HYQ_HIP(hipMemcpyAsync(out, od, xbytes, hipMemcpyDeviceToHost, st), "hipMemcpy");
+    HYQ_HIP(hipStreamSynchronize(st), "hipStreamSynchronize");
+    return HYQ_OK;
+}
+
+} // extern "C"

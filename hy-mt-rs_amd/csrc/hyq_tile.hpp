@@ -2,17 +2,19 @@
 // Weight::matmul batch >= 2, src/quant.rs:272-344, and the MoE expert
 // products, src/model.rs:699-725).
 //
-// A workgroup of 256 threads (4 waves) owns a BM x BN tile of the product
-// Y^T = W X^T (BM weight rows by BN tokens) and walks K in BK = 64 steps:
-//   1. every thread dequantizes 32 weights of one row (row t/2, half t%2) of
-//      the 64-column slice from the device planes into LDS as f16, with the
-//      reference decoder's f32 arithmetic (decode_unchecked,
-//      src/quant.rs:2405-2486) followed by one f32->f16 rounding;
-//   2. the X slice (f32 activations) is converted to f16 into LDS;
-//   3. each wave multiplies its 64 x 64 sub-tile with 2 x 2
-//      v_mfma_f32_32x32x16_f16 blocks per 16-wide k step, accumulating in f32.
-// LDS rows are padded to 72 halves (144 bytes), so the 16-byte fragment reads
-// of 8 consecutive rows fall on 8 distinct 4-bank windows.
+// A workgroup of 256 threads (4 waves) owns BM = 128 LDS weight rows by
+// BN = 128 tokens and walks K in BK = 64 steps:
+//   1. every thread fetches the packed bytes of 32 weights of one LDS row
+//      (row t/2, half t%2) of the next 64-column slice, and 4 x 16 bytes of
+//      the f16 activation slice, into registers (Raw / XRaw);
+//   2. after the current slice's MFMAs it dequantizes them into the other
+//      LDS buffer with the reference decoder's f32 arithmetic
+//      (decode_unchecked, src/quant.rs:2405-2486) and one f32->f16 rounding;
+//   3. each wave multiplies a 64 x 64 (weight rows x tokens) sub-tile with
+//      2 x 2 v_mfma_f32_32x32x16_f16 blocks per 16-wide k step, in f32.
+// Two LDS buffers let one barrier per step separate writers from readers.
+// LDS rows are padded to 72 halves (144 bytes), so the 16-byte fragment
+// reads of 8 consecutive rows fall on 8 distinct 4-bank windows.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -23,10 +25,12 @@ namespace hyq {
 namespace tile {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float2v __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 128, BN = 128, BK = 64, LDK = BK + 8;
+constexpr int TILE_HALVES = BM * LDK; // one LDS operand buffer (BM == BN)
 
 __device__ __forceinline__ float h2f(uint32_t bits16)
 {
@@ -38,24 +42,30 @@ __device__ __forceinline__ float h2f(uint32_t bits16)
 
 __device__ __forceinline__ uint32_t byte_of(uint32_t dw, int i) { return (dw >> (8 * i)) & 0xffu; }
 
-// 16 halves (32 bytes) to an LDS address aligned to 16 bytes.
-__device__ __forceinline__ void store16(_Float16 *dst, const _Float16 (&v)[16])
+// 16 f32 values rounded to f16 (round to nearest even), stored as 32 bytes
+// at a 16-byte aligned LDS address.
+__device__ __forceinline__ void store16(_Float16 *dst, const float (&v)[16])
 {
     half8 a, b;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        a[i] = v[i];
-        b[i] = v[8 + i];
+    for (int i = 0; i < 4; ++i) {
+        const half2v p = __builtin_convertvector((float2v){v[2 * i], v[2 * i + 1]}, half2v);
+        const half2v q = __builtin_convertvector((float2v){v[8 + 2 * i], v[9 + 2 * i]}, half2v);
+        a[2 * i] = p[0];
+        a[2 * i + 1] = p[1];
+        b[2 * i] = q[0];
+        b[2 * i + 1] = q[1];
     }
     *reinterpret_cast<half8 *>(dst) = a;
     *reinterpret_cast<half8 *>(dst + 8) = b;
 }
 
 // ---------------------------------------------------------------------------
-// Dequantization of 32 weights of `row`, columns [k0, k0 + 64) half h, to
-// dst (the LDS row, indexed by the column offset inside the 64-slice).
-// Which 32 of the 64 columns a thread writes depends on the format; the two
-// halves of a row always cover all 64.
+// Per-format dequantization of 32 weights of one row, columns [k0, k0 + 64)
+// half h, to dst (the LDS row, indexed by column offset inside the slice).
+// Which 32 columns a half writes depends on the format; the two halves of a
+// row always cover all 64. load() only issues global loads; convert() does
+// the arithmetic from registers.
 // ---------------------------------------------------------------------------
 template <int F> struct Deq;
 
@@ -64,46 +74,46 @@ template <int F> struct Deq;
 // sub-block 2c+1); value = (d*s_j)*q - (dmin*m_j). Half h takes bytes
 // 16h..16h+15, i.e. columns 16h.. and 32+16h...
 template <> struct Deq<Q4_K> {
-    __device__ __forceinline__ static void run(const WView &w, int row, int k0, int h,
-                                               _Float16 *dst)
+    struct Raw {
+        uint4 q, meta;
+    };
+    __device__ __forceinline__ static void load(Raw &r, const WView &w, int row, int k0, int h)
     {
         const size_t blk = (size_t)row * w.nb + (k0 >> 8);
         const int c = (k0 >> 6) & 3;
-        const uint4 qv = *reinterpret_cast<const uint4 *>(w.p0 + blk * 128 + 32 * c + 16 * h);
-        const uint4 meta = *reinterpret_cast<const uint4 *>(w.p1 + blk * 16);
-        const float d = h2f(meta.x & 0xffffu), dmin = h2f(meta.x >> 16);
-        // scales[12] = meta.y, meta.z, meta.w (little endian)
-        auto sc = [&](int j) -> int {
-            const uint32_t dw = j < 4 ? meta.y : j < 8 ? meta.z : meta.w;
-            return (int)byte_of(dw, j & 3);
+        r.q = *reinterpret_cast<const uint4 *>(w.p0 + blk * 128 + 32 * c + 16 * h);
+        r.meta = *reinterpret_cast<const uint4 *>(w.p1 + blk * 16);
+    }
+    __device__ __forceinline__ static void scale_min(const uint4 &meta, int j, int &s, int &m)
+    {
+        auto sc = [&](int i) -> int {
+            const uint32_t dw = i < 4 ? meta.y : i < 8 ? meta.z : meta.w;
+            return (int)byte_of(dw, i & 3);
         };
-        int s0, m0, s1, m1;
-        {
-            const int j0 = 2 * c, j1 = 2 * c + 1;
-            if (j0 < 4) {
-                s0 = sc(j0) & 63;
-                m0 = sc(j0 + 4) & 63;
-            } else {
-                s0 = (sc(j0 + 4) & 15) | ((sc(j0 - 4) >> 6) << 4);
-                m0 = (sc(j0 + 4) >> 4) | ((sc(j0) >> 6) << 4);
-            }
-            if (j1 < 4) {
-                s1 = sc(j1) & 63;
-                m1 = sc(j1 + 4) & 63;
-            } else {
-                s1 = (sc(j1 + 4) & 15) | ((sc(j1 - 4) >> 6) << 4);
-                m1 = (sc(j1 + 4) >> 4) | ((sc(j1) >> 6) << 4);
-            }
+        if (j < 4) {
+            s = sc(j) & 63;
+            m = sc(j + 4) & 63;
+        } else {
+            s = (sc(j + 4) & 15) | ((sc(j - 4) >> 6) << 4);
+            m = (sc(j + 4) >> 4) | ((sc(j) >> 6) << 4);
         }
+    }
+    __device__ __forceinline__ static void convert(const Raw &r, int k0, int h, _Float16 *dst)
+    {
+        const int c = (k0 >> 6) & 3;
+        const float d = h2f(r.meta.x & 0xffffu), dmin = h2f(r.meta.x >> 16);
+        int s0, m0, s1, m1;
+        scale_min(r.meta, 2 * c, s0, m0);
+        scale_min(r.meta, 2 * c + 1, s1, m1);
         const float d1a = d * (float)s0, m1a = dmin * (float)m0;
         const float d1b = d * (float)s1, m1b = dmin * (float)m1;
-        const uint32_t q[4] = {qv.x, qv.y, qv.z, qv.w};
-        _Float16 lo[16], hi[16];
+        const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+        float lo[16], hi[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const uint32_t b = byte_of(q[i >> 2], i & 3);
-            lo[i] = (_Float16)(d1a * (float)(b & 15u) - m1a);
-            hi[i] = (_Float16)(d1b * (float)(b >> 4) - m1b);
+            lo[i] = d1a * (float)(b & 15u) - m1a;
+            hi[i] = d1b * (float)(b >> 4) - m1b;
         }
         store16(dst + 16 * h, lo);
         store16(dst + 32 + 16 * h, hi);
@@ -115,32 +125,40 @@ template <> struct Deq<Q4_K> {
 // from qh[hf*16 + i] (bits 2p); value = (d*sc[2p+hf]) * (q - 32). A 64-slice
 // holds planes p0, p0+1 (p0 even); half h takes plane p0 + h.
 template <> struct Deq<Q6_K> {
-    __device__ __forceinline__ static void run(const WView &w, int row, int k0, int h,
-                                               _Float16 *dst)
+    struct Raw {
+        uint4 l0, l1, g0, g1;
+        uint32_t sc, d;
+    };
+    __device__ __forceinline__ static void load(Raw &r, const WView &w, int row, int k0, int h)
     {
         const size_t blk = (size_t)row * w.nb + (k0 >> 8);
         const int kb = k0 & 255, chunk = kb >> 7;
         const int p = 2 * ((kb >> 6) & 1) + h;
         const uint8_t *base = w.p0 + blk * 192;
-        const uint4 l0 = *reinterpret_cast<const uint4 *>(base + chunk * 64 + 32 * h);
-        const uint4 l1 = *reinterpret_cast<const uint4 *>(base + chunk * 64 + 32 * h + 16);
-        const uint4 g0 = *reinterpret_cast<const uint4 *>(base + 128 + chunk * 32);
-        const uint4 g1 = *reinterpret_cast<const uint4 *>(base + 128 + chunk * 32 + 16);
-        const uint16_t scp = *reinterpret_cast<const uint16_t *>(w.p1 + blk * 16 + chunk * 8 + 2 * p);
-        const float d = h2f(*reinterpret_cast<const uint16_t *>(w.p2 + blk * 2));
-        const float s0 = d * (float)(int8_t)(scp & 0xff), s1 = d * (float)(int8_t)(scp >> 8);
-        const uint32_t ql[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
-        const uint32_t qh[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+        r.l0 = *reinterpret_cast<const uint4 *>(base + chunk * 64 + 32 * h);
+        r.l1 = *reinterpret_cast<const uint4 *>(base + chunk * 64 + 32 * h + 16);
+        r.g0 = *reinterpret_cast<const uint4 *>(base + 128 + chunk * 32);
+        r.g1 = *reinterpret_cast<const uint4 *>(base + 128 + chunk * 32 + 16);
+        r.sc = *reinterpret_cast<const uint16_t *>(w.p1 + blk * 16 + chunk * 8 + 2 * p);
+        r.d = *reinterpret_cast<const uint16_t *>(w.p2 + blk * 2);
+    }
+    __device__ __forceinline__ static void convert(const Raw &r, int k0, int h, _Float16 *dst)
+    {
+        const int p = 2 * ((k0 >> 6) & 1) + h;
+        const float d = h2f(r.d);
+        const float s0 = d * (float)(int8_t)(r.sc & 0xff), s1 = d * (float)(int8_t)(r.sc >> 8);
+        const uint32_t ql[8] = {r.l0.x, r.l0.y, r.l0.z, r.l0.w, r.l1.x, r.l1.y, r.l1.z, r.l1.w};
+        const uint32_t qh[8] = {r.g0.x, r.g0.y, r.g0.z, r.g0.w, r.g1.x, r.g1.y, r.g1.z, r.g1.w};
         const int lsh = (p >> 1) * 4, hsh = 2 * p;
-        _Float16 v0[16], v1[16];
+        float v0[16], v1[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const uint32_t a0 = byte_of(ql[i >> 2], i & 3), a1 = byte_of(ql[4 + (i >> 2)], i & 3);
             const uint32_t b0 = byte_of(qh[i >> 2], i & 3), b1 = byte_of(qh[4 + (i >> 2)], i & 3);
             const int q0 = (int)(((a0 >> lsh) & 15u) | (((b0 >> hsh) & 3u) << 4));
             const int q1 = (int)(((a1 >> lsh) & 15u) | (((b1 >> hsh) & 3u) << 4));
-            v0[i] = (_Float16)(s0 * (float)(q0 - 32));
-            v1[i] = (_Float16)(s1 * (float)(q1 - 32));
+            v0[i] = s0 * (float)(q0 - 32);
+            v1[i] = s1 * (float)(q1 - 32);
         }
         store16(dst + 32 * h, v0);
         store16(dst + 32 * h + 16, v1);
@@ -149,19 +167,26 @@ template <> struct Deq<Q6_K> {
 
 // Q8_0 (src/quant.rs:2409-2414): value = d * q; half h takes the 32-block h.
 template <> struct Deq<Q8_0> {
-    __device__ __forceinline__ static void run(const WView &w, int row, int k0, int h,
-                                               _Float16 *dst)
+    struct Raw {
+        uint4 a, b;
+        uint32_t d;
+    };
+    __device__ __forceinline__ static void load(Raw &r, const WView &w, int row, int k0, int h)
     {
         const size_t blk = (size_t)row * w.nb + (k0 >> 5) + h;
-        const uint4 a = *reinterpret_cast<const uint4 *>(w.p0 + blk * 32);
-        const uint4 b = *reinterpret_cast<const uint4 *>(w.p0 + blk * 32 + 16);
-        const float d = h2f(*reinterpret_cast<const uint16_t *>(w.p1 + blk * 2));
-        const uint32_t q[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-        _Float16 v0[16], v1[16];
+        r.a = *reinterpret_cast<const uint4 *>(w.p0 + blk * 32);
+        r.b = *reinterpret_cast<const uint4 *>(w.p0 + blk * 32 + 16);
+        r.d = *reinterpret_cast<const uint16_t *>(w.p1 + blk * 2);
+    }
+    __device__ __forceinline__ static void convert(const Raw &r, int, int h, _Float16 *dst)
+    {
+        const float d = h2f(r.d);
+        const uint32_t q[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+        float v0[16], v1[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            v0[i] = (_Float16)(d * (float)(int8_t)byte_of(q[i >> 2], i & 3));
-            v1[i] = (_Float16)(d * (float)(int8_t)byte_of(q[4 + (i >> 2)], i & 3));
+            v0[i] = d * (float)(int8_t)byte_of(q[i >> 2], i & 3);
+            v1[i] = d * (float)(int8_t)byte_of(q[4 + (i >> 2)], i & 3);
         }
         store16(dst + 32 * h, v0);
         store16(dst + 32 * h + 16, v1);
@@ -172,21 +197,28 @@ template <> struct Deq<Q8_0> {
 // keeps a 64-weight unit in 16 bytes with weight 16k+i in bits 2k of byte i;
 // half h takes k = 2h and 2h+1 (columns 32h..32h+31).
 template <> struct Deq<Q2_0C> {
-    __device__ __forceinline__ static void run(const WView &w, int row, int k0, int h,
-                                               _Float16 *dst)
+    struct Raw {
+        uint4 c;
+        uint32_t d;
+    };
+    __device__ __forceinline__ static void load(Raw &r, const WView &w, int row, int k0, int)
     {
         const size_t blk = (size_t)row * w.nb + (k0 >> 9);
         const int u = (k0 >> 6) & 7;
-        const uint4 cv = *reinterpret_cast<const uint4 *>(w.p0 + blk * 128 + u * 16);
-        const float d = h2f(*reinterpret_cast<const uint16_t *>(w.p1 + blk * 2));
-        const uint32_t cw[4] = {cv.x, cv.y, cv.z, cv.w};
-        _Float16 v0[16], v1[16];
+        r.c = *reinterpret_cast<const uint4 *>(w.p0 + blk * 128 + u * 16);
+        r.d = *reinterpret_cast<const uint16_t *>(w.p1 + blk * 2);
+    }
+    __device__ __forceinline__ static void convert(const Raw &r, int, int h, _Float16 *dst)
+    {
+        const float d = h2f(r.d);
+        const uint32_t cw[4] = {r.c.x, r.c.y, r.c.z, r.c.w};
+        float v0[16], v1[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const uint32_t b = byte_of(cw[i >> 2], i & 3);
             const int c0 = (int)((b >> (4 * h)) & 3u), c1 = (int)((b >> (4 * h + 2)) & 3u);
-            v0[i] = (_Float16)((float)(2 * c0 - 3) * d);
-            v1[i] = (_Float16)((float)(2 * c1 - 3) * d);
+            v0[i] = (float)(2 * c0 - 3) * d;
+            v1[i] = (float)(2 * c1 - 3) * d;
         }
         store16(dst + 32 * h, v0);
         store16(dst + 32 * h + 16, v1);
@@ -198,32 +230,40 @@ template <> struct Deq<Q2_0C> {
 // the digit read from the codebook entry of (sign << 4 | nibble). Half h
 // takes digits 2h and 2h+1. Device planes as in hyq_internal.hpp.
 template <> struct Deq<STQ1_0> {
-    __device__ __forceinline__ static void run(const WView &w, int row, int k0, int h,
-                                               _Float16 *dst)
+    struct Raw {
+        uint2 nib;
+        uint32_t s, d;
+    };
+    __device__ __forceinline__ static void load(Raw &r, const WView &w, int row, int k0, int)
     {
         const size_t blk = (size_t)row * w.nb + (k0 >> 8);
         const int c = (k0 >> 6) & 3;
-        const uint2 nv = *reinterpret_cast<const uint2 *>(w.p0 + blk * 32 + 8 * c);
-        const uint32_t S = *reinterpret_cast<const uint32_t *>(w.p1 + blk * 8 + 4 * (c >> 1));
-        const float d = h2f(*reinterpret_cast<const uint16_t *>(w.p2 + blk * 2));
-        const uint32_t nb[2] = {nv.x, nv.y};
-        _Float16 v0[16], v1[16];
+        r.nib = *reinterpret_cast<const uint2 *>(w.p0 + blk * 32 + 8 * c);
+        r.s = *reinterpret_cast<const uint32_t *>(w.p1 + blk * 8 + 4 * (c >> 1));
+        r.d = *reinterpret_cast<const uint16_t *>(w.p2 + blk * 2);
+    }
+    __device__ __forceinline__ static void convert(const Raw &r, int k0, int h, _Float16 *dst)
+    {
+        const int c = (k0 >> 6) & 3;
+        const float d = h2f(r.d);
+        const uint32_t nb[2] = {r.nib.x, r.nib.y};
+        float v0[16], v1[16];
 #pragma unroll
         for (int gg = 0; gg < 16; ++gg) {
             const int hh = gg >> 3, r8 = gg & 7, t = r8 & 3, hi = r8 >> 2;
             const int code = (int)((byte_of(nb[hh], t) >> (4 * hi)) & 15u);
             const int q = (c & 1) * 4 + (gg >> 2), tq = gg & 3;
-            const int sign = (int)((S >> (q + 8 * tq)) & 1u);
+            const int sign = (int)((r.s >> (q + 8 * tq)) & 1u);
             const int e = dec::kStqCodebook[(sign << 4) | code];
-            v0[gg] = (_Float16)((float)(((e >> (4 * h)) & 3) - 1) * d);
-            v1[gg] = (_Float16)((float)(((e >> (4 * h + 2)) & 3) - 1) * d);
+            v0[gg] = (float)(((e >> (4 * h)) & 3) - 1) * d;
+            v1[gg] = (float)(((e >> (4 * h + 2)) & 3) - 1) * d;
         }
         store16(dst + 32 * h, v0);
         store16(dst + 32 * h + 16, v1);
     }
 };
 
-// Zeros for rows past the end of the weight (each half clears its 32 columns).
+// Zeros for LDS rows past the end of the weight (each half clears 32 columns).
 __device__ __forceinline__ void zero_half(_Float16 *dst, int h)
 {
     const half8 z = {};
@@ -232,38 +272,41 @@ __device__ __forceinline__ void zero_half(_Float16 *dst, int h)
 }
 
 // ---------------------------------------------------------------------------
-// X slice: BN rows (tokens) x 64 columns of f32 -> f16 in LDS. Row r of the
-// tile reads src_row(r) (nullptr = zero row). 2048 float4 per slice, 8 per
-// thread, 16 consecutive threads per 256-byte row segment.
+// Activation slice: BN rows (tokens) x 64 f16 columns, 16 bytes per thread
+// per load: index f = t + 256 i -> row f/8, columns 8*(f%8)...
 // ---------------------------------------------------------------------------
+struct XRaw {
+    uint4 v[4];
+};
+
+// rowp(r): pointer to f16 activation row r of the tile, or nullptr (zeros).
 template <class RowFn>
-__device__ __forceinline__ void load_x(const RowFn &src_row, int k0, float4 (&v)[8])
+__device__ __forceinline__ void load_x(XRaw &x, const RowFn &rowp, int k0)
 {
     const int t = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int f = t + 256 * i, r = f >> 4, c4 = f & 15;
-        const float *p = src_row(r);
-        v[i] = p ? *reinterpret_cast<const float4 *>(p + k0 + 4 * c4)
-                 : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = 0; i < 4; ++i) {
+        const int f = t + 256 * i, r = f >> 3, c8 = f & 7;
+        const _Float16 *p = rowp(r);
+        x.v[i] = p ? *reinterpret_cast<const uint4 *>(p + k0 + 8 * c8) : make_uint4(0, 0, 0, 0);
     }
 }
 
-__device__ __forceinline__ void store_x(_Float16 *Xs, const float4 (&v)[8])
+__device__ __forceinline__ void store_x(_Float16 *Xs, const XRaw &x)
 {
     const int t = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int f = t + 256 * i, r = f >> 4, c4 = f & 15;
-        half4 hv = {(_Float16)v[i].x, (_Float16)v[i].y, (_Float16)v[i].z, (_Float16)v[i].w};
-        *reinterpret_cast<half4 *>(Xs + r * LDK + 4 * c4) = hv;
+    for (int i = 0; i < 4; ++i) {
+        const int f = t + 256 * i, r = f >> 3, c8 = f & 7;
+        *reinterpret_cast<uint4 *>(Xs + r * LDK + 8 * c8) = x.v[i];
     }
 }
 
-// One 64-deep step of the wave's 64 x 64 sub-tile: acc[bi][bj] covers weight
-// rows wm*64 + 32*bi .. and tokens wn*64 + 32*bj ...
-__device__ __forceinline__ void mma_step(const _Float16 *Ws, const _Float16 *Xs, int wm, int wn,
-                                         f32x16 (&acc)[2][2])
+// One 64-deep step: acc[i][j] accumulates LDS weight rows arow(i) + lane%32
+// against tokens wn*64 + 32*j + lane%32.
+template <class ARow>
+__device__ __forceinline__ void mma_step(const _Float16 *Ws, const _Float16 *Xs, const ARow &arow,
+                                         int wn, f32x16 (&acc)[2][2])
 {
     const int lane = threadIdx.x & 63;
     const int r = lane & 31, kq = 8 * (lane >> 5);
@@ -272,7 +315,7 @@ __device__ __forceinline__ void mma_step(const _Float16 *Ws, const _Float16 *Xs,
         half8 a[2], b[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            a[i] = *reinterpret_cast<const half8 *>(Ws + (wm * 64 + 32 * i + r) * LDK + kk + kq);
+            a[i] = *reinterpret_cast<const half8 *>(Ws + (arow(i) + r) * LDK + kk + kq);
             b[i] = *reinterpret_cast<const half8 *>(Xs + (wn * 64 + 32 * i + r) * LDK + kk + kq);
         }
 #pragma unroll
@@ -283,17 +326,71 @@ __device__ __forceinline__ void mma_step(const _Float16 *Ws, const _Float16 *Xs,
     }
 }
 
-// Element (weight row, token) of accumulator register e of block (i, j):
-// v_mfma 32x32 output layout, row = 8*(e/4) + 4*(lane/32) + e%4, col = lane%32.
-__device__ __forceinline__ int acc_row(int wm, int i, int e)
+// v_mfma 32x32 output layout: register e of a block holds row
+// 8*(e/4) + 4*(lane/32) + e%4 and column lane%32 of the block.
+__device__ __forceinline__ int acc_row_in_block(int e)
 {
-    const int lane = threadIdx.x & 63;
-    return wm * 64 + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+    return 8 * (e >> 2) + 4 * ((threadIdx.x & 63) >> 5) + (e & 3);
 }
 __device__ __forceinline__ int acc_col(int wn, int j)
 {
-    const int lane = threadIdx.x & 63;
-    return wn * 64 + 32 * j + (lane & 31);
+    return wn * 64 + 32 * j + (threadIdx.x & 31);
+}
+
+__device__ __forceinline__ void zero_acc(f32x16 (&acc)[2][2])
+{
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+}
+
+// ---------------------------------------------------------------------------
+// The K loop shared by every GEMM kernel. wsrc(lrow, view, row) sets the
+// weight view and row that LDS row lrow dequantizes (row < 0: zeros); xrow(r) the f16
+// activation row of token r of the tile (nullptr = zeros). lds holds
+// 2 * 2 * TILE_HALVES halves.
+// ---------------------------------------------------------------------------
+template <int F, class WSrc, class XRow, class ARow>
+__device__ __forceinline__ void k_loop(const WSrc &wsrc, const XRow &xrow, const ARow &arow,
+                                       int K, int wn, _Float16 *lds, f32x16 (&acc)[2][2])
+{
+    using D = Deq<F>;
+    const int t = threadIdx.x;
+    const int lrow = t >> 1, h = t & 1;
+    WView wv{};
+    int row = -1;
+    wsrc(lrow, wv, row);
+    typename D::Raw raw;
+    XRaw xr;
+    auto fetch = [&](int k0) {
+        if (row >= 0) D::load(raw, wv, row, k0, h);
+        load_x(xr, xrow, k0);
+    };
+    auto put = [&](int k0, int buf) {
+        _Float16 *Ws = lds + buf * 2 * TILE_HALVES;
+        _Float16 *Xs = Ws + TILE_HALVES;
+        if (row >= 0) D::convert(raw, k0, h, Ws + lrow * LDK);
+        else zero_half(Ws + lrow * LDK, h);
+        store_x(Xs, xr);
+    };
+    const int steps = K / BK;
+    fetch(0);
+    put(0, 0);
+    if (steps > 1) fetch(BK);
+    __syncthreads();
+    for (int s = 0; s < steps; ++s) {
+        const int cur = s & 1;
+        const _Float16 *Ws = lds + cur * 2 * TILE_HALVES;
+        mma_step(Ws, Ws + TILE_HALVES, arow, wn, acc);
+        if (s + 1 < steps) {
+            put((s + 1) * BK, cur ^ 1);
+            if (s + 2 < steps) fetch((s + 2) * BK);
+        }
+        __syncthreads();
+    }
 }
 
 } // namespace tile

@@ -142,6 +142,33 @@ int hyq_gemv_isums_d(hyq_ctx *ctx, const hyq_weight *w, const hyq_q8 *x, int32_t
  * y_d [batch, rows] f32 (src/quant.rs:272-344). */
 int hyq_matmul_d(hyq_ctx *ctx, const hyq_weight *w, const float *x_d, size_t batch,
                  float *y_d);
+/* ---- MoE expert products: the expert loop of Moe::forward (src/model.rs:699-725).
+ * gate and up are rank-3 weights {hidden, mid, E}, down is {mid, hidden, E}
+ * (the expert stacks Weight::expert slices, src/quant.rs:144-154). The
+ * routed pairs (token, expert, weight) are what route() returned
+ * (src/model.rs:728-767) for each token; the caller seeds `out` [tokens,
+ * hidden] (the reference seeds it with the shared expert, :699) and this
+ * adds, for every token and in ascending expert order, weight * down_e(
+ * silu(gate_e x) * (up_e x)) (:700-722). Each expert's token group runs as
+ * f16-MFMA GEMMs (DenseFfn::forward at its batch, :672-685). At most 4096
+ * tokens and experts and 65535 pairs per call. ---- */
+size_t hyq_moe_scratch_bytes(size_t tokens, size_t npairs, size_t experts, size_t hidden,
+                             size_t mid);
+/* Device buffers, asynchronous. scratch_d: 256-byte aligned, at least
+ * hyq_moe_scratch_bytes(...) bytes. Pairs naming a token or expert out of
+ * range are skipped. */
+int hyq_moe_experts_d(hyq_ctx *ctx, const hyq_weight *gate, const hyq_weight *up,
+                      const hyq_weight *down, const float *x_d, size_t tokens,
+                      const int32_t *pair_token_d, const int32_t *pair_expert_d,
+                      const float *pair_weight_d, size_t npairs, void *scratch_d,
+                      size_t scratch_bytes, float *out_d);
+/* Host buffers, synchronous; out is read and updated; pairs out of range are
+ * HYQ_EINVAL. */
+int hyq_moe_experts(hyq_ctx *ctx, const hyq_weight *gate, const hyq_weight *up,
+                    const hyq_weight *down, const float *x, size_t tokens,
+                    const int32_t *pair_token, const int32_t *pair_expert,
+                    const float *pair_weight, size_t npairs, float *out);
+
 /* decode of rows [row0, row0+nrows) to f32 on the device (Weight::row_into /
  * to_vec, src/quant.rs:99-142). */
 int hyq_dequant_rows_d(hyq_ctx *ctx, const hyq_weight *w, size_t row0, size_t nrows,

@@ -84,3 +84,20 @@ def test_batched_shape_errors(gpu_ctx):
     W2 = gpu_ctx.upload(Q2_0C, random_matrix(Q2_0C, 8, 512, seed=0), (512, 8))
     with pytest.raises(ValueError):
         W2.matmul(np.zeros(3 * 512 - 1, np.float32), 3)
+
+
+def test_activation_rows_scale_exactly(gpu_ctx):
+    """Activations are rounded to f16 with a power-of-two scale per token row,
+    so scaling a row by 2^k scales its output row by exactly 2^k, far beyond
+    the f16 range (2^40) and below its normals (2^-40)."""
+    rows, cols, batch = 160, 1024, 5
+    w = random_matrix(Q6_K, rows, cols, seed=9)
+    x = np.random.default_rng(9).normal(0, 1, (batch, cols)).astype(np.float32)
+    W = gpu_ctx.upload(Q6_K, w, (cols, rows))
+    base = W.matmul(x.reshape(-1), batch).reshape(batch, rows)
+    k = np.array([40, -40, 0, 17, -3], np.float32)
+    xs = (x * np.exp2(k)[:, None]).astype(np.float32)
+    scaled = W.matmul(xs.reshape(-1), batch).reshape(batch, rows)
+    assert np.array_equal(scaled, (base * np.exp2(k)[:, None]).astype(np.float32))
+    zero = W.matmul(np.zeros(2 * cols, np.float32), 2)
+    assert np.array_equal(zero, np.zeros(2 * rows, np.float32))

@@ -1,0 +1,194 @@
+"""GPU parity of the MoE expert products (the expert loop of Moe::forward,
+src/model.rs:699-725) through the C ABI.
+
+The oracle is a float64 chain per routed pair built from the oracle's
+row-local f64 products (gate and up in f64, silu(g)*u rounded to f32 as the
+reference stores it, down in f64 over that f32 vector), summed per token in
+ascending expert order onto the seed; oracle.moe_experts (the reference's
+x86 f32 path restated) is checked against the same chain. Tolerance of the
+f16-MFMA path: 2e-3 relative in the 2-norm, and per element
+|err| <= 5e-3 * sum_p |w_p| * sum_k |down_e[i,k] h_k| (h carries the f16
+errors of two products and its own f16 rounding)."""
+import numpy as np
+import pytest
+
+from synth import NAMES, Q4_K, Q6_K, Q8_0, Q2_0C, STQ1_0, random_matrix, row_bytes
+
+pytestmark = pytest.mark.gpu
+
+
+def _print(*a):
+    print(*a, flush=True)
+
+
+def softmax_top(logits: np.ndarray, k: int):
+    """Top-k of softmax(logits) (index tie-break), weights renormalized to sum 1."""
+    z = logits.astype(np.float64) - logits.max()
+    p = np.exp(z) / np.exp(z).sum()
+    idx = sorted(range(len(p)), key=lambda i: (-p[i], i))[:k]
+    w = p[idx] / p[idx].sum()
+    return idx, w.astype(np.float32)
+
+
+def routed_pairs(tokens, experts, used, seed):
+    rng = np.random.default_rng(seed)
+    pt, pe, pw = [], [], []
+    for t in range(tokens):
+        idx, w = softmax_top(rng.normal(0, 1, experts).astype(np.float32), used)
+        pt += [t] * used
+        pe += idx
+        pw += list(w)
+    return (np.array(pt, np.int32), np.array(pe, np.int32), np.array(pw, np.float32))
+
+
+def chain_f64(oracle, fg, fd, gate, up, down, hidden, mid, x, pt, pe, pw, seed_out, tokens_of):
+    """f64 reference of out[t] for t in tokens_of, plus its magnitude bound."""
+    gb, db = row_bytes(fg, hidden) * mid, row_bytes(fd, mid) * hidden
+    out = {t: seed_out[t].astype(np.float64).copy() for t in tokens_of}
+    mag = {t: np.zeros(hidden) for t in tokens_of}
+    order = sorted(range(len(pt)), key=lambda p: (pe[p], p))
+    for p in order:
+        t, e, w = int(pt[p]), int(pe[p]), float(pw[p])
+        if t not in out:
+            continue
+        xt = x[t * hidden:(t + 1) * hidden]
+        g, _ = oracle.matmul_f64(fg, gate[e * gb:(e + 1) * gb], mid, hidden, xt, 1)
+        u, _ = oracle.matmul_f64(fg, up[e * gb:(e + 1) * gb], mid, hidden, xt, 1)
+        with np.errstate(over="ignore"):
+            h = (g[0] / (1 + np.exp(-g[0])) * u[0]).astype(np.float32)
+        d, dm = oracle.matmul_f64(fd, down[e * db:(e + 1) * db], hidden, mid, h, 1)
+        out[t] += np.float64(np.float32(w)) * d[0]
+        mag[t] += abs(w) * dm[0]
+    return out, mag
+
+
+def check_moe(got, ref, mag, label):
+    err = np.abs(got.astype(np.float64) - ref)
+    assert np.all(err <= 5e-3 * mag + 1e-6), (
+        f"{label}: worst err/mag {float(np.max(err / np.maximum(mag, 1e-30))):.3e}")
+    rel = np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30)
+    assert rel <= 2e-3, f"{label}: relative 2-norm error {rel:.3e}"
+
+
+@pytest.mark.parametrize("fg,fd", [(Q4_K, Q4_K), (Q4_K, Q6_K), (Q8_0, Q8_0), (Q2_0C, Q2_0C),
+                                   (STQ1_0, STQ1_0)],
+                         ids=lambda f: NAMES[f])
+def test_moe_small_matches_chain(gpu_ctx, hyq, oracle, fg, fd):
+    hidden, mid, experts, tokens, used = 512, 512, 8, 21, 3
+    _print("moe", NAMES[fg], NAMES[fd])
+    gate = random_matrix(fg, experts * mid, hidden, seed=1)
+    up = random_matrix(fg, experts * mid, hidden, seed=2)
+    down = random_matrix(fd, experts * hidden, mid, seed=3)
+    x = np.random.default_rng(4).normal(0, 1, tokens * hidden).astype(np.float32)
+    seed_out = np.random.default_rng(5).normal(0, 1, (tokens, hidden)).astype(np.float32)
+    pt, pe, pw = routed_pairs(tokens, experts, used, seed=6)
+    G = gpu_ctx.upload(fg, gate, (hidden, mid, experts))
+    U = gpu_ctx.upload(fg, up, (hidden, mid, experts))
+    D = gpu_ctx.upload(fd, down, (mid, hidden, experts))
+    got = hyq.moe_experts(G, U, D, x, tokens, pt, pe, pw, seed_out).reshape(tokens, hidden)
+    ref, mag = chain_f64(oracle, fg, fd, gate, up, down, hidden, mid, x, pt, pe, pw, seed_out,
+                         range(tokens))
+    R = np.stack([ref[t] for t in range(tokens)])
+    M = np.stack([mag[t] for t in range(tokens)])
+    check_moe(got, R, M, f"{NAMES[fg]}/{NAMES[fd]}")
+    if fg == fd:
+        # the reference's own x86 f32 path agrees with the f64 chain
+        cpu = oracle.moe_experts(fg, fd, gate, up, down, experts, hidden, mid, x, pt, pe, pw,
+                                 seed_out.reshape(-1), threads=4).reshape(tokens, hidden)
+        assert np.all(np.abs(cpu - R) <= 1e-4 * M + 1e-6)
+
+
+def test_moe_uneven_groups_and_empty_experts(gpu_ctx, hyq, oracle):
+    """One expert with 150 tokens (two 128-token chunks), several empty
+    experts, a token routed to no expert, pairs not grouped by token."""
+    hidden, mid, experts, tokens = 256, 768, 6, 160
+    gate = random_matrix(Q4_K, experts * mid, hidden, seed=11)
+    up = random_matrix(Q4_K, experts * mid, hidden, seed=12)
+    down = random_matrix(Q4_K, experts * hidden, mid, seed=13)
+    x = np.random.default_rng(14).normal(0, 1, tokens * hidden).astype(np.float32)
+    seed_out = np.zeros((tokens, hidden), np.float32)
+    pt = [t for t in range(150)] + [3, 7, 159, 3]
+    pe = [2] * 150 + [5, 5, 0, 0]
+    pw = list(np.random.default_rng(15).uniform(0.1, 1.0, len(pt)))
+    pt, pe, pw = np.array(pt, np.int32), np.array(pe, np.int32), np.array(pw, np.float32)
+    perm = np.random.default_rng(16).permutation(len(pt))
+    pt, pe, pw = pt[perm], pe[perm], pw[perm]
+    G = gpu_ctx.upload(Q4_K, gate, (hidden, mid, experts))
+    U = gpu_ctx.upload(Q4_K, up, (hidden, mid, experts))
+    D = gpu_ctx.upload(Q4_K, down, (mid, hidden, experts))
+    got = hyq.moe_experts(G, U, D, x, tokens, pt, pe, pw, seed_out).reshape(tokens, hidden)
+    ref, mag = chain_f64(oracle, Q4_K, Q4_K, gate, up, down, hidden, mid, x, pt, pe, pw,
+                         seed_out, range(tokens))
+    R = np.stack([ref[t] for t in range(tokens)])
+    M = np.stack([mag[t] for t in range(tokens)])
+    check_moe(got, R, M, "uneven")
+    assert np.all(got[150:159] == 0.0)  # tokens 150..158 are routed nowhere
+
+
+def test_moe_30b_a3b_shape_sampled_tokens(gpu_ctx, hyq, oracle):
+    """64 tokens, top-8 of 64 experts (softmax routing), hidden 2048, mid 1536,
+    Q4_K experts; every token's output is produced, 6 seeded tokens are
+    checked against the f64 chain."""
+    hidden, mid, experts, tokens, used = 2048, 1536, 64, 64, 8
+    _print("moe 30B-A3B shape")
+    gate = random_matrix(Q4_K, experts * mid, hidden, seed=21)
+    up = random_matrix(Q4_K, experts * mid, hidden, seed=22)
+    down = random_matrix(Q4_K, experts * hidden, mid, seed=23)
+    x = np.random.default_rng(24).normal(0, 1, tokens * hidden).astype(np.float32)
+    seed_out = np.random.default_rng(25).normal(0, 1, (tokens, hidden)).astype(np.float32)
+    pt, pe, pw = routed_pairs(tokens, experts, used, seed=26)
+    G = gpu_ctx.upload(Q4_K, gate, (hidden, mid, experts))
+    U = gpu_ctx.upload(Q4_K, up, (hidden, mid, experts))
+    D = gpu_ctx.upload(Q4_K, down, (mid, hidden, experts))
+    got = hyq.moe_experts(G, U, D, x, tokens, pt, pe, pw, seed_out).reshape(tokens, hidden)
+    assert np.all(np.isfinite(got))
+    pick = sorted(np.random.default_rng(27).choice(tokens, 6, replace=False).tolist())
+    ref, mag = chain_f64(oracle, Q4_K, Q4_K, gate, up, down, hidden, mid, x, pt, pe, pw,
+                         seed_out, pick)
+    check_moe(got[pick], np.stack([ref[t] for t in pick]), np.stack([mag[t] for t in pick]),
+              "30B-A3B")
+
+
+def test_moe_device_entry_point_and_rerun(gpu_ctx, hyq):
+    """hyq_moe_experts_d on device buffers equals the host entry point, twice
+    in a row on the same scratch (the second with fewer pairs)."""
+    hidden, mid, experts, tokens = 256, 256, 4, 10
+    gate = random_matrix(Q4_K, experts * mid, hidden, seed=31)
+    up = random_matrix(Q4_K, experts * mid, hidden, seed=32)
+    down = random_matrix(Q4_K, experts * hidden, mid, seed=33)
+    x = np.random.default_rng(34).normal(0, 1, tokens * hidden).astype(np.float32)
+    G = gpu_ctx.upload(Q4_K, gate, (hidden, mid, experts))
+    U = gpu_ctx.upload(Q4_K, up, (hidden, mid, experts))
+    D = gpu_ctx.upload(Q4_K, down, (mid, hidden, experts))
+    L = hyq.lib()
+    nbytes = L.hyq_moe_scratch_bytes(tokens, 20, experts, hidden, mid)
+    scratch = gpu_ctx.empty(nbytes, np.uint8)
+    xd = gpu_ctx.array(x)
+    for npairs in (20, 7):
+        pt, pe, pw = routed_pairs(tokens, experts, 2, seed=npairs)
+        pt, pe, pw = pt[:npairs], pe[:npairs], pw[:npairs]
+        host = hyq.moe_experts(G, U, D, x, tokens, pt, pe, pw,
+                               np.zeros(tokens * hidden, np.float32))
+        od = gpu_ctx.array(np.zeros(tokens * hidden, np.float32))
+        ptd, ped, pwd = gpu_ctx.array(pt), gpu_ctx.array(pe), gpu_ctx.array(pw)
+        hyq.check(L.hyq_moe_experts_d(gpu_ctx.handle, G.handle, U.handle, D.handle, xd.ptr,
+                                      tokens, ptd.ptr, ped.ptr, pwd.ptr, npairs, scratch.ptr,
+                                      nbytes, od.ptr))
+        assert np.array_equal(od.numpy(), host)
+
+
+def test_moe_errors(gpu_ctx, hyq):
+    hidden, mid, experts = 256, 512, 4
+    G = gpu_ctx.upload(Q4_K, random_matrix(Q4_K, experts * mid, hidden, seed=1),
+                       (hidden, mid, experts))
+    D = gpu_ctx.upload(Q4_K, random_matrix(Q4_K, experts * hidden, mid, seed=2),
+                       (mid, hidden, experts))
+    x = np.zeros(2 * hidden, np.float32)
+    out = np.zeros(2 * hidden, np.float32)
+    with pytest.raises(ValueError):  # expert out of range
+        hyq.moe_experts(G, G, D, x, 2, [0], [4], [1.0], out)
+    with pytest.raises(ValueError):  # token out of range
+        hyq.moe_experts(G, G, D, x, 2, [2], [0], [1.0], out)
+    with pytest.raises(ValueError):  # down given where gate is expected
+        hyq.moe_experts(D, G, D, x, 2, [0], [0], [1.0], out)
+    assert np.array_equal(hyq.moe_experts(G, G, D, x, 2, [], [], [], out), out)
