@@ -117,6 +117,52 @@ def prefill_rate(hyq, ctx, ev, dtype, rows, cols, batch, seed=3):
     return ms * 1e3, flop / (ms * 1e-3) / 1e12
 
 
+def moe_rate(hyq, ctx, ev, tokens=64, experts=64, used=8, hidden=2048, mid=1536, seed=5):
+    """MoE layer at 30B-A3B-style shapes: the dense Q8_0 shared projection
+    [2048x2048] seeds the output (batched matmul), then the Q4_K expert loop
+    (softmax top-8 routing of N(0,1) logits, weights renormalized)."""
+    from synth import Q4_K, Q8_0, random_matrix
+    rng = np.random.default_rng(seed)
+    G = ctx.upload(Q4_K, random_matrix(Q4_K, experts * mid, hidden, seed), (hidden, mid, experts))
+    U = ctx.upload(Q4_K, random_matrix(Q4_K, experts * mid, hidden, seed + 1),
+                   (hidden, mid, experts))
+    D = ctx.upload(Q4_K, random_matrix(Q4_K, experts * hidden, mid, seed + 2),
+                   (mid, hidden, experts))
+    S = ctx.upload(Q8_0, random_matrix(Q8_0, hidden, hidden, seed + 3), (hidden, hidden))
+    pt, pe, pw = [], [], []
+    for t in range(tokens):
+        z = rng.normal(0, 1, experts)
+        p = np.exp(z - z.max())
+        p /= p.sum()
+        idx = sorted(range(experts), key=lambda i: (-p[i], i))[:used]
+        pt += [t] * used
+        pe += idx
+        pw += list(p[idx] / p[idx].sum())
+    x = ctx.array(rng.normal(0, 1, tokens * hidden).astype(np.float32))
+    out = ctx.empty(tokens * hidden, np.float32)
+    ptd = ctx.array(np.array(pt, np.int32))
+    ped = ctx.array(np.array(pe, np.int32))
+    pwd = ctx.array(np.array(pw, np.float32))
+    L = hyq.lib()
+    nbytes = L.hyq_moe_scratch_bytes(tokens, len(pt), experts, hidden, mid)
+    scratch = ctx.empty(nbytes, np.uint8)
+
+    def launch(i):
+        L.hyq_matmul_d(ctx.handle, S.handle, x.ptr, tokens, out.ptr)
+        L.hyq_moe_experts_d(ctx.handle, G.handle, U.handle, D.handle, x.ptr, tokens, ptd.ptr,
+                            ped.ptr, pwd.ptr, len(pt), scratch.ptr, nbytes, out.ptr)
+
+    ms = ev.time_ms(launch, 20)
+    touched = len(set(pe))
+    wbytes = touched * (2 * mid * hidden // 256 * 144 + hidden * mid // 256 * 144) + \
+        hidden * hidden // 32 * 34
+    for w in (G, U, D, S):
+        w.release()
+    return dict(us=round(ms * 1e3, 2), experts_touched=touched, weight_bytes=wbytes,
+                GBs=round(wbytes / (ms * 1e-3) / 1e9, 1),
+                frac=round(wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
+
+
 def decode_kernel_table(hyq, ctx, ev, dec_weights, model):
     """Per-launch time of each GEMV of the decode step over the model's own 32
     layers of weights (the step's memory behaviour), plus its time per step."""
@@ -278,6 +324,12 @@ def main() -> int:
                                  frac=round(tf / MFMA_F16_PEAK_TFLOPS, 4))
             log(f"{name}: {us:.1f} us {tf:.0f} TFLOP/s")
 
+    moe = None
+    if not args.no_prefill:
+        moe = moe_rate(hyq, ctx, ev)
+        log(f"C5 MoE layer (64 tokens, top-8 of 64 Q4_K experts + Q8_0 shared): "
+            f"{moe['us']:.1f} us {moe['GBs']:.0f} GB/s")
+
     cpu = None
     if not args.no_cpu:
         log("cpu baseline")
@@ -300,6 +352,7 @@ def main() -> int:
         "decode_kernels": table,
         "gemv": gemv,
         "prefill": prefill,
+        "moe": moe,
         "reference_published": {"value": 86.86, "unit": "tok/s",
                                 "note": "Apple M2 Pro 8 threads, real weights, ~14-18 "
                                         "positions (docs/validation.md:70); not this config"},

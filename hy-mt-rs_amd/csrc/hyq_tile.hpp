@@ -20,6 +20,7 @@
 #include <hip/hip_runtime.h>
 
 #include "hyq_decode.hpp"
+#include "hyq_groups.hpp"
 
 namespace hyq {
 namespace tile {
@@ -64,9 +65,31 @@ __device__ __forceinline__ void store16(_Float16 *dst, const float (&v)[16])
 // Per-format dequantization of 32 weights of one row, columns [k0, k0 + 64)
 // half h, to dst (the LDS row, indexed by column offset inside the slice).
 // Which 32 columns a half writes depends on the format; the two halves of a
-// row always cover all 64. load() only issues global loads; convert() does
-// the arithmetic from registers.
+// row always cover all 64. load() only issues global loads from the row's
+// plane bases (RowPtr, computed once per thread); convert() does the
+// arithmetic from registers.
+//
+// Every value is formed as one fma whose exact result is the decoder's
+// exact value, so the f32 result is bit-identical to decode_unchecked
+// (src/quant.rs:2405-2486), then rounded once to f16: the packed codes are
+// widened with v_cvt_f32_ubyteN (byte n of a dword to f32) and offsets are
+// folded into the fma's addend (q - 32 as s*q + (-32 s), int8 q as
+// d*(q + 128) + (-128 d), 2c - 3 as 2d*c + (-3d)). The products in those
+// addends and multipliers are exact in f32 (at most 24 significant bits).
 // ---------------------------------------------------------------------------
+struct RowPtr {
+    const uint8_t *p0, *p1, *p2;
+};
+
+__device__ __forceinline__ RowPtr row_ptr(const WView &w, int F_p0, int F_p1, int F_p2, int row)
+{
+    const size_t b = (size_t)row * w.nb;
+    return RowPtr{w.p0 + b * F_p0, w.p1 + b * F_p1, w.p2 + b * F_p2};
+}
+
+// byte i of x as f32 (v_cvt_f32_ubyte{i})
+__device__ __forceinline__ float ub(uint32_t x, int i) { return (float)((x >> (8 * i)) & 0xffu); }
+
 template <int F> struct Deq;
 
 // Q4_K (decode_unchecked, src/quant.rs:2437-2461): byte l of a 64-weight
@@ -77,12 +100,15 @@ template <> struct Deq<Q4_K> {
     struct Raw {
         uint4 q, meta;
     };
-    __device__ __forceinline__ static void load(Raw &r, const WView &w, int row, int k0, int h)
+    __device__ __forceinline__ static RowPtr rows(const WView &w, int row)
     {
-        const size_t blk = (size_t)row * w.nb + (k0 >> 8);
-        const int c = (k0 >> 6) & 3;
-        r.q = *reinterpret_cast<const uint4 *>(w.p0 + blk * 128 + 32 * c + 16 * h);
-        r.meta = *reinterpret_cast<const uint4 *>(w.p1 + blk * 16);
+        return row_ptr(w, 128, 16, 0, row);
+    }
+    __device__ __forceinline__ static void load(Raw &r, const RowPtr &p, int k0, int h)
+    {
+        const int blk = k0 >> 8, c = (k0 >> 6) & 3;
+        r.q = *reinterpret_cast<const uint4 *>(p.p0 + blk * 128 + 32 * c + 16 * h);
+        r.meta = *reinterpret_cast<const uint4 *>(p.p1 + blk * 16);
     }
     __device__ __forceinline__ static void scale_min(const uint4 &meta, int j, int &s, int &m)
     {
@@ -98,22 +124,25 @@ template <> struct Deq<Q4_K> {
             m = (sc(j + 4) >> 4) | ((sc(j) >> 6) << 4);
         }
     }
-    __device__ __forceinline__ static void convert(const Raw &r, int k0, int h, _Float16 *dst)
+    __device__ __forceinline__ static void convert(const Raw &r, int u, int h, _Float16 *dst)
     {
-        const int c = (k0 >> 6) & 3;
+        const int c = u;
         const float d = h2f(r.meta.x & 0xffffu), dmin = h2f(r.meta.x >> 16);
         int s0, m0, s1, m1;
         scale_min(r.meta, 2 * c, s0, m0);
         scale_min(r.meta, 2 * c + 1, s1, m1);
-        const float d1a = d * (float)s0, m1a = dmin * (float)m0;
-        const float d1b = d * (float)s1, m1b = dmin * (float)m1;
+        const float d1a = d * (float)s0, nm1a = -(dmin * (float)m0);
+        const float d1b = d * (float)s1, nm1b = -(dmin * (float)m1);
         const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
         float lo[16], hi[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const uint32_t b = byte_of(q[i >> 2], i & 3);
-            lo[i] = d1a * (float)(b & 15u) - m1a;
-            hi[i] = d1b * (float)(b >> 4) - m1b;
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t l = q[w] & 0x0F0F0F0Fu, u = (q[w] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                lo[4 * w + i] = __builtin_fmaf(d1a, ub(l, i), nm1a);
+                hi[4 * w + i] = __builtin_fmaf(d1b, ub(u, i), nm1b);
+            }
         }
         store16(dst + 16 * h, lo);
         store16(dst + 32 + 16 * h, hi);
@@ -129,36 +158,42 @@ template <> struct Deq<Q6_K> {
         uint4 l0, l1, g0, g1;
         uint32_t sc, d;
     };
-    __device__ __forceinline__ static void load(Raw &r, const WView &w, int row, int k0, int h)
+    __device__ __forceinline__ static RowPtr rows(const WView &w, int row)
     {
-        const size_t blk = (size_t)row * w.nb + (k0 >> 8);
-        const int kb = k0 & 255, chunk = kb >> 7;
-        const int p = 2 * ((kb >> 6) & 1) + h;
-        const uint8_t *base = w.p0 + blk * 192;
+        return row_ptr(w, 192, 16, 2, row);
+    }
+    __device__ __forceinline__ static void load(Raw &r, const RowPtr &p, int k0, int h)
+    {
+        const int blk = k0 >> 8, kb = k0 & 255, chunk = kb >> 7;
+        const int pl = 2 * ((kb >> 6) & 1) + h;
+        const uint8_t *base = p.p0 + blk * 192;
         r.l0 = *reinterpret_cast<const uint4 *>(base + chunk * 64 + 32 * h);
         r.l1 = *reinterpret_cast<const uint4 *>(base + chunk * 64 + 32 * h + 16);
         r.g0 = *reinterpret_cast<const uint4 *>(base + 128 + chunk * 32);
         r.g1 = *reinterpret_cast<const uint4 *>(base + 128 + chunk * 32 + 16);
-        r.sc = *reinterpret_cast<const uint16_t *>(w.p1 + blk * 16 + chunk * 8 + 2 * p);
-        r.d = *reinterpret_cast<const uint16_t *>(w.p2 + blk * 2);
+        r.sc = *reinterpret_cast<const uint16_t *>(p.p1 + blk * 16 + chunk * 8 + 2 * pl);
+        r.d = *reinterpret_cast<const uint16_t *>(p.p2 + blk * 2);
     }
-    __device__ __forceinline__ static void convert(const Raw &r, int k0, int h, _Float16 *dst)
+    __device__ __forceinline__ static void convert(const Raw &r, int u, int h, _Float16 *dst)
     {
-        const int p = 2 * ((k0 >> 6) & 1) + h;
+        const int pl = 2 * (u & 1) + h;
         const float d = h2f(r.d);
         const float s0 = d * (float)(int8_t)(r.sc & 0xff), s1 = d * (float)(int8_t)(r.sc >> 8);
+        const float o0 = -32.f * s0, o1 = -32.f * s1;
         const uint32_t ql[8] = {r.l0.x, r.l0.y, r.l0.z, r.l0.w, r.l1.x, r.l1.y, r.l1.z, r.l1.w};
         const uint32_t qh[8] = {r.g0.x, r.g0.y, r.g0.z, r.g0.w, r.g1.x, r.g1.y, r.g1.z, r.g1.w};
-        const int lsh = (p >> 1) * 4, hsh = 2 * p;
+        const int lsh = (pl >> 1) * 4, hsh = 2 * pl;
         float v0[16], v1[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const uint32_t a0 = byte_of(ql[i >> 2], i & 3), a1 = byte_of(ql[4 + (i >> 2)], i & 3);
-            const uint32_t b0 = byte_of(qh[i >> 2], i & 3), b1 = byte_of(qh[4 + (i >> 2)], i & 3);
-            const int q0 = (int)(((a0 >> lsh) & 15u) | (((b0 >> hsh) & 3u) << 4));
-            const int q1 = (int)(((a1 >> lsh) & 15u) | (((b1 >> hsh) & 3u) << 4));
-            v0[i] = s0 * (float)(q0 - 32);
-            v1[i] = s1 * (float)(q1 - 32);
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t qa = ((ql[w] >> lsh) & 0x0F0F0F0Fu) | (((qh[w] >> hsh) & 0x03030303u) << 4);
+            const uint32_t qb =
+                ((ql[4 + w] >> lsh) & 0x0F0F0F0Fu) | (((qh[4 + w] >> hsh) & 0x03030303u) << 4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v0[4 * w + i] = __builtin_fmaf(s0, ub(qa, i), o0);
+                v1[4 * w + i] = __builtin_fmaf(s1, ub(qb, i), o1);
+            }
         }
         store16(dst + 32 * h, v0);
         store16(dst + 32 * h + 16, v1);
@@ -171,22 +206,30 @@ template <> struct Deq<Q8_0> {
         uint4 a, b;
         uint32_t d;
     };
-    __device__ __forceinline__ static void load(Raw &r, const WView &w, int row, int k0, int h)
+    __device__ __forceinline__ static RowPtr rows(const WView &w, int row)
     {
-        const size_t blk = (size_t)row * w.nb + (k0 >> 5) + h;
-        r.a = *reinterpret_cast<const uint4 *>(w.p0 + blk * 32);
-        r.b = *reinterpret_cast<const uint4 *>(w.p0 + blk * 32 + 16);
-        r.d = *reinterpret_cast<const uint16_t *>(w.p1 + blk * 2);
+        return row_ptr(w, 32, 2, 0, row);
+    }
+    __device__ __forceinline__ static void load(Raw &r, const RowPtr &p, int k0, int h)
+    {
+        const int blk = (k0 >> 5) + h;
+        r.a = *reinterpret_cast<const uint4 *>(p.p0 + blk * 32);
+        r.b = *reinterpret_cast<const uint4 *>(p.p0 + blk * 32 + 16);
+        r.d = *reinterpret_cast<const uint16_t *>(p.p1 + blk * 2);
     }
     __device__ __forceinline__ static void convert(const Raw &r, int, int h, _Float16 *dst)
     {
-        const float d = h2f(r.d);
+        const float d = h2f(r.d), o = -128.f * d;
         const uint32_t q[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
         float v0[16], v1[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            v0[i] = d * (float)(int8_t)byte_of(q[i >> 2], i & 3);
-            v1[i] = d * (float)(int8_t)byte_of(q[4 + (i >> 2)], i & 3);
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t qa = q[w] ^ 0x80808080u, qb = q[4 + w] ^ 0x80808080u; // q + 128
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v0[4 * w + i] = __builtin_fmaf(d, ub(qa, i), o);
+                v1[4 * w + i] = __builtin_fmaf(d, ub(qb, i), o);
+            }
         }
         store16(dst + 32 * h, v0);
         store16(dst + 32 * h + 16, v1);
@@ -201,24 +244,30 @@ template <> struct Deq<Q2_0C> {
         uint4 c;
         uint32_t d;
     };
-    __device__ __forceinline__ static void load(Raw &r, const WView &w, int row, int k0, int)
+    __device__ __forceinline__ static RowPtr rows(const WView &w, int row)
     {
-        const size_t blk = (size_t)row * w.nb + (k0 >> 9);
-        const int u = (k0 >> 6) & 7;
-        r.c = *reinterpret_cast<const uint4 *>(w.p0 + blk * 128 + u * 16);
-        r.d = *reinterpret_cast<const uint16_t *>(w.p1 + blk * 2);
+        return row_ptr(w, 128, 2, 0, row);
+    }
+    __device__ __forceinline__ static void load(Raw &r, const RowPtr &p, int k0, int)
+    {
+        const int blk = k0 >> 9, u = (k0 >> 6) & 7;
+        r.c = *reinterpret_cast<const uint4 *>(p.p0 + blk * 128 + u * 16);
+        r.d = *reinterpret_cast<const uint16_t *>(p.p1 + blk * 2);
     }
     __device__ __forceinline__ static void convert(const Raw &r, int, int h, _Float16 *dst)
     {
-        const float d = h2f(r.d);
+        const float d = h2f(r.d), d2 = 2.f * d, o = -3.f * d;
         const uint32_t cw[4] = {r.c.x, r.c.y, r.c.z, r.c.w};
         float v0[16], v1[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const uint32_t b = byte_of(cw[i >> 2], i & 3);
-            const int c0 = (int)((b >> (4 * h)) & 3u), c1 = (int)((b >> (4 * h + 2)) & 3u);
-            v0[i] = (float)(2 * c0 - 3) * d;
-            v1[i] = (float)(2 * c1 - 3) * d;
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t x0 = (cw[w] >> (4 * h)) & 0x03030303u;
+            const uint32_t x1 = (cw[w] >> (4 * h + 2)) & 0x03030303u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v0[4 * w + i] = __builtin_fmaf(d2, ub(x0, i), o);
+                v1[4 * w + i] = __builtin_fmaf(d2, ub(x1, i), o);
+            }
         }
         store16(dst + 32 * h, v0);
         store16(dst + 32 * h + 16, v1);
@@ -228,35 +277,43 @@ template <> struct Deq<Q2_0C> {
 // STQ1_0 (src/quant.rs:1086-1123, 2423-2430): 64-weight chunk c holds 16
 // groups; digit p of group gg is column p*16 + gg, value (digit - 1) * d with
 // the digit read from the codebook entry of (sign << 4 | nibble). Half h
-// takes digits 2h and 2h+1. Device planes as in hyq_internal.hpp.
+// takes digits 2h and 2h+1. Device planes as in hyq_internal.hpp: groups
+// 4j..4j+3 have their nibbles in bytes of dword j/2 (high nibbles for odd j)
+// and their signs at bits (c%2)*4 + j + 8t of the chunk pair's sign dword.
 template <> struct Deq<STQ1_0> {
     struct Raw {
         uint2 nib;
         uint32_t s, d;
     };
-    __device__ __forceinline__ static void load(Raw &r, const WView &w, int row, int k0, int)
+    __device__ __forceinline__ static RowPtr rows(const WView &w, int row)
     {
-        const size_t blk = (size_t)row * w.nb + (k0 >> 8);
-        const int c = (k0 >> 6) & 3;
-        r.nib = *reinterpret_cast<const uint2 *>(w.p0 + blk * 32 + 8 * c);
-        r.s = *reinterpret_cast<const uint32_t *>(w.p1 + blk * 8 + 4 * (c >> 1));
-        r.d = *reinterpret_cast<const uint16_t *>(w.p2 + blk * 2);
+        return row_ptr(w, 32, 8, 2, row);
     }
-    __device__ __forceinline__ static void convert(const Raw &r, int k0, int h, _Float16 *dst)
+    __device__ __forceinline__ static void load(Raw &r, const RowPtr &p, int k0, int)
     {
-        const int c = (k0 >> 6) & 3;
-        const float d = h2f(r.d);
+        const int blk = k0 >> 8, c = (k0 >> 6) & 3;
+        r.nib = *reinterpret_cast<const uint2 *>(p.p0 + blk * 32 + 8 * c);
+        r.s = *reinterpret_cast<const uint32_t *>(p.p1 + blk * 8 + 4 * (c >> 1));
+        r.d = *reinterpret_cast<const uint16_t *>(p.p2 + blk * 2);
+    }
+    __device__ __forceinline__ static void convert(const Raw &r, int u, int h, _Float16 *dst)
+    {
+        const int c = u;
+        const float d = h2f(r.d), o = -d;
         const uint32_t nb[2] = {r.nib.x, r.nib.y};
         float v0[16], v1[16];
 #pragma unroll
-        for (int gg = 0; gg < 16; ++gg) {
-            const int hh = gg >> 3, r8 = gg & 7, t = r8 & 3, hi = r8 >> 2;
-            const int code = (int)((byte_of(nb[hh], t) >> (4 * hi)) & 15u);
-            const int q = (c & 1) * 4 + (gg >> 2), tq = gg & 3;
-            const int sign = (int)((r.s >> (q + 8 * tq)) & 1u);
-            const int e = dec::kStqCodebook[(sign << 4) | code];
-            v0[gg] = (float)(((e >> (4 * h)) & 3) - 1) * d;
-            v1[gg] = (float)(((e >> (4 * h + 2)) & 3) - 1) * d;
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t nibs = (nb[j >> 1] >> (4 * (j & 1))) & 0x0F0F0F0Fu;
+            const uint32_t sb = ((r.s >> ((c & 1) * 4 + j)) & 0x01010101u) << 4;
+            const uint32_t e = GroupSTQ::lut(nibs | sb);
+            const uint32_t da = (e >> (4 * h)) & 0x03030303u;
+            const uint32_t db = (e >> (4 * h + 2)) & 0x03030303u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v0[4 * j + i] = __builtin_fmaf(d, ub(da, i), o);
+                v1[4 * j + i] = __builtin_fmaf(d, ub(db, i), o);
+            }
         }
         store16(dst + 32 * h, v0);
         store16(dst + 32 * h + 16, v1);
@@ -273,33 +330,27 @@ __device__ __forceinline__ void zero_half(_Float16 *dst, int h)
 
 // ---------------------------------------------------------------------------
 // Activation slice: BN rows (tokens) x 64 f16 columns, 16 bytes per thread
-// per load: index f = t + 256 i -> row f/8, columns 8*(f%8)...
+// per load: index f = t + 256 i -> row f/8 = t/8 + 32 i, columns 8*(t%8)...
+// xp[i] is the thread's row pointer for load i (offset by its 8 columns),
+// nullptr for rows past the end (zeros).
 // ---------------------------------------------------------------------------
 struct XRaw {
     uint4 v[4];
 };
 
-// rowp(r): pointer to f16 activation row r of the tile, or nullptr (zeros).
-template <class RowFn>
-__device__ __forceinline__ void load_x(XRaw &x, const RowFn &rowp, int k0)
+__device__ __forceinline__ void load_x(XRaw &x, const _Float16 *const (&xp)[4], int k0)
 {
-    const int t = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int f = t + 256 * i, r = f >> 3, c8 = f & 7;
-        const _Float16 *p = rowp(r);
-        x.v[i] = p ? *reinterpret_cast<const uint4 *>(p + k0 + 8 * c8) : make_uint4(0, 0, 0, 0);
-    }
+    for (int i = 0; i < 4; ++i)
+        x.v[i] = xp[i] ? *reinterpret_cast<const uint4 *>(xp[i] + k0) : make_uint4(0, 0, 0, 0);
 }
 
 __device__ __forceinline__ void store_x(_Float16 *Xs, const XRaw &x)
 {
     const int t = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int f = t + 256 * i, r = f >> 3, c8 = f & 7;
-        *reinterpret_cast<uint4 *>(Xs + r * LDK + 8 * c8) = x.v[i];
-    }
+    for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<uint4 *>(Xs + ((t >> 3) + 32 * i) * LDK + 8 * (t & 7)) = x.v[i];
 }
 
 // One 64-deep step: acc[i][j] accumulates LDS weight rows arow(i) + lane%32
@@ -349,9 +400,11 @@ __device__ __forceinline__ void zero_acc(f32x16 (&acc)[2][2])
 
 // ---------------------------------------------------------------------------
 // The K loop shared by every GEMM kernel. wsrc(lrow, view, row) sets the
-// weight view and row that LDS row lrow dequantizes (row < 0: zeros); xrow(r) the f16
-// activation row of token r of the tile (nullptr = zeros). lds holds
-// 2 * 2 * TILE_HALVES halves.
+// weight view and row that LDS row lrow dequantizes (row < 0: zeros);
+// xrow(r) gives the f16 activation row of token r of the tile (nullptr =
+// zeros); arow(i) the first LDS weight row of the wave's block i. lds holds
+// 2 * 2 * TILE_HALVES halves: buffer b at lds + b * 2 * TILE_HALVES, weights
+// then activations.
 // ---------------------------------------------------------------------------
 template <int F, class WSrc, class XRow, class ARow>
 __device__ __forceinline__ void k_loop(const WSrc &wsrc, const XRow &xrow, const ARow &arow,
@@ -363,18 +416,24 @@ __device__ __forceinline__ void k_loop(const WSrc &wsrc, const XRow &xrow, const
     WView wv{};
     int row = -1;
     wsrc(lrow, wv, row);
+    const RowPtr rp = D::rows(wv, row < 0 ? 0 : row);
+    const _Float16 *xp[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const _Float16 *p = xrow((t >> 3) + 32 * i);
+        xp[i] = p ? p + 8 * (t & 7) : nullptr;
+    }
     typename D::Raw raw;
     XRaw xr;
     auto fetch = [&](int k0) {
-        if (row >= 0) D::load(raw, wv, row, k0, h);
-        load_x(xr, xrow, k0);
+        if (row >= 0) D::load(raw, rp, k0, h);
+        load_x(xr, xp, k0);
     };
-    auto put = [&](int k0, int buf) {
-        _Float16 *Ws = lds + buf * 2 * TILE_HALVES;
-        _Float16 *Xs = Ws + TILE_HALVES;
-        if (row >= 0) D::convert(raw, k0, h, Ws + lrow * LDK);
+    auto put = [&](int k0, int b) {
+        _Float16 *Ws = lds + b * 2 * TILE_HALVES;
+        if (row >= 0) D::convert(raw, (k0 >> 6) & 3, h, Ws + lrow * LDK);
         else zero_half(Ws + lrow * LDK, h);
-        store_x(Xs, xr);
+        store_x(Ws + TILE_HALVES, xr);
     };
     const int steps = K / BK;
     fetch(0);
