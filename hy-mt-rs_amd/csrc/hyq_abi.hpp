@@ -46,16 +46,27 @@ struct DeviceGuard {
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// Weight storage comes from large per-device pool chunks (hyq_pool.cpp):
+// packing a model's tensors into a few big, 2 MiB-aligned allocations keeps
+// them on large-page mappings, so the first touch of a tensor by a kernel
+// does not walk page tables for every few kilobytes.
+struct PoolChunk;
+void *pool_alloc(int device, size_t bytes, PoolChunk **chunk);
+void pool_release(PoolChunk *chunk);
+
 struct DeviceBuffer {
     void *ptr = nullptr;
     size_t bytes = 0;
     int device = 0;
+    PoolChunk *chunk = nullptr; // set when ptr lives in a pool chunk
     DeviceBuffer() = default;
     DeviceBuffer(const DeviceBuffer &) = delete;
     DeviceBuffer &operator=(const DeviceBuffer &) = delete;
     ~DeviceBuffer()
     {
-        if (ptr) {
+        if (chunk) {
+            pool_release(chunk);
+        } else if (ptr) {
             DeviceGuard g(device);
             (void)hipFree(ptr);
         }

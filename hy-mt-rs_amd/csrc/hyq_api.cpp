@@ -347,7 +347,8 @@ int hyq_weight_upload(hyq_ctx *ctx, int dtype, const uint8_t *gguf_bytes, size_t
     auto storage = std::make_shared<DeviceBuffer>();
     storage->device = ctx->device;
     storage->bytes = sz[0] + sz[1] + sz[2];
-    HYQ_HIP(hipMalloc(&storage->ptr, storage->bytes), "hipMalloc(weight)");
+    storage->ptr = pool_alloc(ctx->device, storage->bytes, &storage->chunk);
+    if (!storage->ptr) return fail(HYQ_ENOMEM, "weight pool: out of device memory");
     int rc = ctx->bytes.reserve(ctx->device, byte_len);
     if (rc) return rc;
     uint8_t *stage = (uint8_t *)ctx->bytes.ptr();

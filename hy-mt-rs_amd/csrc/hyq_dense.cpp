@@ -101,7 +101,8 @@ int hyq_rope_norm_append_d(hyq_ctx *ctx, float *q_d, const float *k_d, const flo
 
 size_t hyq_attention_scratch_floats(size_t context, size_t heads)
 {
-    return (size_t)attention_splits((int)context) * heads * (128 + 2);
+    // split partials, and an f32 output row for callers that only want Q8
+    return (size_t)attention_splits((int)context) * heads * PART_STRIDE + heads * 128;
 }
 
 int hyq_attention_d(hyq_ctx *ctx, const float *q_d, const float *kcache_d,
@@ -113,19 +114,24 @@ int hyq_attention_d(hyq_ctx *ctx, const float *q_d, const float *kcache_d,
     if (rc) return rc;
     if (!q_d || !kcache_d || !vcache_d || !pos_d || !scratch_d)
         return fail(HYQ_EINVAL, "attention: null argument");
-    // the combine stages 6 floats per 32-position slice in LDS (<= 48 KiB)
-    if (head_dim != 128 || heads == 0 || kv_heads == 0 || heads % kv_heads || context == 0 ||
-        context > 65536)
+    if (head_dim != 128 || heads == 0 || kv_heads == 0 || heads % kv_heads ||
+        heads / kv_heads > (size_t)ATT_MAX_REP || context == 0 || context > 65536)
         return fail(HYQ_EINVAL, "attention: unsupported shape");
     if (out_q8 && out_q8->ref.n != heads * head_dim)
         return fail(HYQ_EINVAL, "attention: Q8 length %zu != %zu", out_q8->ref.n,
                     heads * head_dim);
     DeviceGuard g(ctx->device);
-    const Q8Ref q = out_q8 ? out_q8->ref : Q8Ref{};
+    const size_t part_floats = (size_t)attention_splits((int)context) * heads * PART_STRIDE;
+    float *out = out_d ? out_d : scratch_d + part_floats;
     HYQ_LAUNCH(launch_attention(q_d, kcache_d, vcache_d, pos_d, (int)context, (int)heads,
-                                (int)kv_heads, scratch_d, out_d, q.q, q.s, q.sum16, q.sum32,
-                                q.sum256, ctx->stream),
+                                (int)kv_heads, scratch_d, out, ctx->stream),
                "attention");
+    if (out_q8) {
+        const Q8Ref &q = out_q8->ref;
+        HYQ_LAUNCH(launch_quantize_q8(out, (int)(heads * head_dim), q.q, q.s, q.sum16, q.sum32,
+                                      q.sum256, ctx->stream),
+                   "quantize_q8");
+    }
     return HYQ_OK;
 }
 
@@ -163,11 +169,9 @@ struct hyq_dense {
 
     DeviceBuffer mem;       // norms, freq, activations, scratch, state
     DeviceBuffer kv;        // [layers][2][context][kv_heads*head_dim]
-    hyq_q8 *q8h = nullptr;  // hidden-width activations
-    hyq_q8 *q8a = nullptr;  // attention output
-    hyq_q8 *q8f = nullptr;  // FFN-width activations
     float *freq = nullptr, *hidden = nullptr, *qb = nullptr, *kb = nullptr, *vb = nullptr;
     float *gb = nullptr, *logits = nullptr, *att_scratch = nullptr, *argmax_scratch = nullptr;
+    float *att_out = nullptr; // merged attention output [heads * head_dim]
     int32_t *token = nullptr, *history = nullptr;
     StepState *state = nullptr;
     size_t history_cap = 0;
@@ -180,9 +184,6 @@ struct hyq_dense {
     {
         if (exec) (void)hipGraphExecDestroy(exec);
         if (graph) (void)hipGraphDestroy(graph);
-        delete q8h;
-        delete q8a;
-        delete q8f;
     }
     size_t kvw() const { return (size_t)cfg.kv_heads * cfg.head_dim; }
     float *kcache(int l) { return (float *)kv.ptr + (size_t)l * 2 * context * kvw(); }
@@ -198,23 +199,40 @@ struct hyq_dense {
 
 namespace {
 
+// One token: embedding row, then per layer five kernels - the QKV GEMV
+// (RMSNorm + Q8 in its input stage), attention (RoPE, Q/K norm, KV append,
+// merge), the output GEMV (Q8 of the attention row in its input stage,
+// residual add), the gate/up GEMV (RMSNorm + Q8, SiLU product) and the down
+// GEMV (Q8 of the SiLU row, residual add) - then the lm_head GEMV (output
+// RMSNorm + Q8) and the argmax.
+GemvArgs staged(const hyq_weight *w, const float *xin, const float *norm, float eps, float *y,
+                const float *residual)
+{
+    GemvArgs a{};
+    a.nseg = 1;
+    a.seg[0].w = w->view;
+    a.seg[0].y = y;
+    a.rows_total = (int)w->rows;
+    a.groups = (int)(w->cols / 256);
+    a.residual = residual;
+    a.xin = xin;
+    a.norm = norm;
+    a.eps = eps;
+    return a;
+}
+
 int enqueue_step(hyq_dense *m)
 {
     const hyq_dense_config &c = m->cfg;
     hipStream_t st = m->ctx->stream;
-    const int qlen = c.heads * c.head_dim;
     HYQ_LAUNCH(launch_embed_row(m->embedding->dtype, m->embedding->view, c.hidden, m->token,
                                 m->hidden, st),
                "embed_row");
-    const Q8Ref &h8 = m->q8h->ref, &a8 = m->q8a->ref, &f8 = m->q8f->ref;
     const int *pos = &m->state->pos;
     for (int l = 0; l < c.layers; ++l) {
         const hyq_dense::Layer &L = m->layers[l];
-        HYQ_LAUNCH(launch_rms_norm_q8(m->hidden, L.attn_norm, c.hidden, c.rms_eps, nullptr, h8.q,
-                                      h8.s, h8.sum16, h8.sum32, h8.sum256, st),
-                   "rms_norm_q8");
         {
-            GemvArgs a = gemv_args(L.q, h8, m->qb, nullptr);
+            GemvArgs a = staged(L.q, m->hidden, L.attn_norm, c.rms_eps, m->qb, nullptr);
             const hyq_weight *ws[3] = {L.q, L.k, L.v};
             float *ys[3] = {m->qb, m->kb, m->vb};
             int start = 0;
@@ -228,42 +246,35 @@ int enqueue_step(hyq_dense *m)
             a.rows_total = start;
             HYQ_LAUNCH(launch_gemv(L.q->dtype, GEMV_MULTI, a, st), "gemv_qkv");
         }
-        HYQ_LAUNCH(launch_rope_norm_kv(m->qb, m->kb, m->vb, L.q_norm, L.k_norm, m->freq, pos,
-                                       c.heads, c.kv_heads, c.head_dim, c.rms_eps, m->kcache(l),
-                                       m->vcache(l), st),
-                   "rope_norm_kv");
-        HYQ_LAUNCH(launch_attention(m->qb, m->kcache(l), m->vcache(l), pos, (int)m->context,
-                                    c.heads, c.kv_heads, m->att_scratch, nullptr, a8.q, a8.s,
-                                    a8.sum16, a8.sum32, a8.sum256, st),
+        HYQ_LAUNCH(launch_attention_rope(m->qb, m->kb, m->vb, L.q_norm, L.k_norm, m->freq,
+                                         c.rms_eps, m->kcache(l), m->vcache(l), pos,
+                                         (int)m->context, c.heads, c.kv_heads, m->att_scratch,
+                                         st),
                    "attention");
-        HYQ_LAUNCH(launch_gemv(L.o->dtype, GEMV_PLAIN, gemv_args(L.o, a8, m->hidden, m->hidden),
-                               st),
+        HYQ_LAUNCH(launch_attention_merge(m->att_scratch, (int)m->context, c.heads, pos,
+                                          m->att_out, st),
+                   "attention_merge");
+        HYQ_LAUNCH(launch_gemv(L.o->dtype, GEMV_PLAIN,
+                               staged(L.o, m->att_out, nullptr, 0.f, m->hidden, m->hidden), st),
                    "gemv_attn_output");
-        HYQ_LAUNCH(launch_rms_norm_q8(m->hidden, L.ffn_norm, c.hidden, c.rms_eps, nullptr, h8.q,
-                                      h8.s, h8.sum16, h8.sum32, h8.sum256, st),
-                   "rms_norm_q8");
         {
-            GemvArgs a = gemv_args(L.gate, h8, m->gb, nullptr);
+            GemvArgs a = staged(L.gate, m->hidden, L.ffn_norm, c.rms_eps, m->gb, nullptr);
             a.nseg = 2;
             a.seg[1].w = L.up->view;
             HYQ_LAUNCH(launch_gemv(L.gate->dtype, GEMV_SILU, a, st), "gemv_gate_up_silu");
         }
-        HYQ_LAUNCH(launch_quantize_q8(m->gb, c.ffn, f8.q, f8.s, f8.sum16, f8.sum32, f8.sum256, st),
-                   "quantize_q8");
         HYQ_LAUNCH(launch_gemv(L.down->dtype, GEMV_PLAIN,
-                               gemv_args(L.down, f8, m->hidden, m->hidden), st),
+                               staged(L.down, m->gb, nullptr, 0.f, m->hidden, m->hidden), st),
                    "gemv_down");
     }
-    HYQ_LAUNCH(launch_rms_norm_q8(m->hidden, m->output_norm, c.hidden, c.rms_eps, nullptr, h8.q,
-                                  h8.s, h8.sum16, h8.sum32, h8.sum256, st),
-               "rms_norm_q8");
     HYQ_LAUNCH(launch_gemv(m->output->dtype, GEMV_PLAIN,
-                           gemv_args(m->output, h8, m->logits, nullptr), st),
+                           staged(m->output, m->hidden, m->output_norm, c.rms_eps, m->logits,
+                                  nullptr),
+                           st),
                "gemv_lm_head");
     HYQ_LAUNCH(launch_argmax(m->logits, c.vocab, m->argmax_scratch,
                              (int *)(m->argmax_scratch + 64), m->token, m->state, m->history, st),
                "argmax");
-    (void)qlen;
     return HYQ_OK;
 }
 
@@ -298,7 +309,8 @@ int hyq_dense_create(hyq_ctx *ctx, const hyq_dense_config *cfg, size_t context, 
     const hyq_dense_config &c = *cfg;
     if (c.layers <= 0 || c.layers > 1024 || c.hidden <= 0 || c.vocab <= 0 || c.ffn <= 0)
         return fail(HYQ_EINVAL, "invalid model dimensions");
-    if (c.heads <= 0 || c.kv_heads <= 0 || c.heads % c.kv_heads)
+    if (c.heads <= 0 || c.kv_heads <= 0 || c.heads % c.kv_heads ||
+        c.heads / c.kv_heads > ATT_MAX_REP)
         return fail(HYQ_EINVAL, "invalid grouped-query head counts");
     if (c.head_dim != 128) return fail(HYQ_EINVAL, "dense: head_dim %d (128 supported)", c.head_dim);
     if (c.hidden % 256 || c.ffn % 256 || (c.heads * c.head_dim) % 256)
@@ -326,7 +338,8 @@ int hyq_dense_create(hyq_ctx *ctx, const hyq_dense_config *cfg, size_t context, 
     const size_t o_freq = take(D / 2);
     const size_t o_hidden = take(H), o_q = take(QL), o_k = take(KV), o_v = take(KV);
     const size_t o_g = take(F), o_logits = take(V);
-    const size_t o_att = take(hyq_attention_scratch_floats(context, (size_t)c.heads));
+    const size_t o_att = take((size_t)attention_splits((int)context) * c.heads * PART_STRIDE);
+    const size_t o_att_out = take(QL);
     const size_t o_arg = take(128), o_tok = take(4), o_state = take(4);
     rc = m->mem.alloc(ctx->device, off);
     if (rc) return rc;
@@ -348,6 +361,7 @@ int hyq_dense_create(hyq_ctx *ctx, const hyq_dense_config *cfg, size_t context, 
     m->gb = (float *)(base + o_g);
     m->logits = (float *)(base + o_logits);
     m->att_scratch = (float *)(base + o_att);
+    m->att_out = (float *)(base + o_att_out);
     m->argmax_scratch = (float *)(base + o_arg);
     m->token = (int32_t *)(base + o_tok);
     m->state = (StepState *)(base + o_state);
@@ -360,10 +374,6 @@ int hyq_dense_create(hyq_ctx *ctx, const hyq_dense_config *cfg, size_t context, 
     rc = m->kv.alloc(ctx->device, (size_t)c.layers * 2 * context * KV * 4);
     if (rc) return rc;
     HYQ_HIP(hipMemset(m->kv.ptr, 0, m->kv.bytes), "hipMemset(kv)");
-    rc = q8_alloc(ctx->device, H, &m->q8h);
-    if (!rc) rc = q8_alloc(ctx->device, QL, &m->q8a);
-    if (!rc) rc = q8_alloc(ctx->device, F, &m->q8f);
-    if (rc) return rc;
     if ((rc = write_state(m.get(), 0, 0, 0))) return rc;
     HYQ_HIP(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     *out = m.release();

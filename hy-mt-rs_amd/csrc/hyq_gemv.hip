@@ -15,6 +15,8 @@
 #include <hip/hip_runtime.h>
 
 #include "hyq_groups.hpp"
+#include "hyq_q8.hpp"
+#include "hyq_wave.hpp"
 
 namespace hyq {
 
@@ -29,15 +31,112 @@ __device__ __forceinline__ float silu_mul(float g, float u)
     return silu * u;
 }
 
-__device__ __forceinline__ float reduce8(float v)
+__device__ __forceinline__ float reduce8(float v) { return wave::sum8(v); }
+
+// The f32 input stage: the workgroup's waves take 256-value groups in turn
+// (group g = wave + 4i; lane l holds values 4l..4l+3) and write the Q8 row to
+// the LDS slots, the group scales and the 16/32/256-value integer sums to
+// the LDS arrays, as Q8::quantize_into (src/quant.rs:904-922) and
+// q8_quantize_group do. With a norm vector the values are rms_norm_into's
+// x * (1/sqrt(mean(x^2) + eps)) * w (src/model.rs:825-829); the sum of
+// squares is formed per group by a fixed DPP/readlane tree (hyq_wave.hpp)
+// and then over the groups in ascending order. Rows of up to 4 * STAGE_REG groups are loaded with all
+// loads in flight at once; longer rows take a loop.
+constexpr int STAGE_REG = 8;
+
+__device__ __forceinline__ float4 scale_by(float4 v, float scale, float4 w)
 {
-    v += __shfl_xor(v, 1, 64);
-    v += __shfl_xor(v, 2, 64);
-    v += __shfl_xor(v, 4, 64);
-    return v;
+    return make_float4(v.x * scale * w.x, v.y * scale * w.y, v.z * scale * w.z,
+                       v.w * scale * w.w);
 }
 
-template <int F, int NR, int MODE>
+__device__ __forceinline__ void quantize_group4(float4 v, int g, int lane, int *slots, float *sc,
+                                                int *s256, int *s16, int *s32)
+{
+    const float m = wave::max64(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    float s = 0.f, inv = 0.f;
+    if (m > 0.f) {
+        s = m / 127.f;
+        inv = 127.f / m;
+    }
+    const int q0 = q8_sat_rne(v.x * inv), q1 = q8_sat_rne(v.y * inv);
+    const int q2 = q8_sat_rne(v.z * inv), q3 = q8_sat_rne(v.w * inv);
+    slots[g * SLOT_INTS + lane] =
+        (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | ((q3 & 0xff) << 24);
+    // integer sums over 16, 32 and 256 values (4, 8 and 64 lanes): exact
+    const int t4 = wave::sum4((q0 + q1) + (q2 + q3));
+    if ((lane & 3) == 0) s16[g * 16 + (lane >> 2)] = t4;
+    const int t8 = t4 + wave::dpp<wave::DPP_HALF_MIRROR>(t4);
+    if ((lane & 7) == 0) s32[g * 8 + (lane >> 3)] = t8;
+    const int t16 = t8 + wave::dpp<wave::DPP_MIRROR>(t8);
+    const int t256 = (wave::lane(t16, 0) + wave::lane(t16, 16)) +
+                     (wave::lane(t16, 32) + wave::lane(t16, 48));
+    if (lane == 0) {
+        s256[g] = t256;
+        sc[g] = s;
+    }
+}
+
+__device__ __forceinline__ float group_ss(float4 v)
+{
+    return wave::sum64((v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w));
+}
+
+template <int IN>
+__device__ __forceinline__ void stage_f32(const GemvArgs &a, int *slots, float *sc, int *s256,
+                                          int *s16, int *s32, float *gss)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int groups = a.groups;
+    const float4 *x4 = reinterpret_cast<const float4 *>(a.xin);
+    const float4 *n4 = reinterpret_cast<const float4 *>(a.norm);
+    auto finish_norm = [&]() {
+        __syncthreads();
+        float ss = 0.f;
+        for (int g = 0; g < groups; ++g) ss += gss[g];
+        return 1.0f / sqrtf(ss / (float)(groups * 256) + a.eps);
+    };
+    if (groups <= 4 * STAGE_REG) {
+        float4 v[STAGE_REG], w[STAGE_REG];
+#pragma unroll
+        for (int i = 0; i < STAGE_REG; ++i)
+            if (wave + 4 * i < groups) {
+                v[i] = x4[(wave + 4 * i) * 64 + lane];
+                if (IN == 2) w[i] = n4[(wave + 4 * i) * 64 + lane];
+            }
+        float scale = 1.f;
+        if (IN == 2) {
+#pragma unroll
+            for (int i = 0; i < STAGE_REG; ++i)
+                if (wave + 4 * i < groups) {
+                    const float s = group_ss(v[i]);
+                    if (lane == 0) gss[wave + 4 * i] = s;
+                }
+            scale = finish_norm();
+        }
+#pragma unroll
+        for (int i = 0; i < STAGE_REG; ++i)
+            if (wave + 4 * i < groups)
+                quantize_group4(IN == 2 ? scale_by(v[i], scale, w[i]) : v[i], wave + 4 * i, lane,
+                                slots, sc, s256, s16, s32);
+        return;
+    }
+    float scale = 1.f;
+    if (IN == 2) {
+        for (int g = wave; g < groups; g += 4) {
+            const float s = group_ss(x4[g * 64 + lane]);
+            if (lane == 0) gss[g] = s;
+        }
+        scale = finish_norm();
+    }
+    for (int g = wave; g < groups; g += 4) {
+        const float4 v = x4[g * 64 + lane];
+        quantize_group4(IN == 2 ? scale_by(v, scale, n4[g * 64 + lane]) : v, g, lane, slots, sc,
+                        s256, s16, s32);
+    }
+}
+
+template <int F, int NR, int MODE, int IN>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
 {
     using G = typename GroupOf<F>::T;
@@ -78,14 +177,39 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
             if (MODE == GEMV_SILU) G::load(d2[i], a.seg[1].w, lrow[i], g);
         }
     };
-    // The first group's weights do not depend on the activations: put their
-    // loads in flight before staging the Q8 row, so both latencies overlap.
-    if (sub < groups) load_group(sub);
-    {
+    // The weights do not depend on the activations: their loads go in flight
+    // before the Q8 row is staged, so both latencies overlap. A plain GEMV
+    // with one row per lane and at most PRELOAD groups per lane issues all
+    // of its groups at once; otherwise the first group is preloaded and the
+    // others load at the top of their iteration.
+    constexpr int PRELOAD = 4;
+    constexpr bool CAN_PRE = NR == 1 && MODE == GEMV_PLAIN;
+    typename G::Data dp[CAN_PRE ? PRELOAD : 1];
+    const bool pre = CAN_PRE && groups <= 8 * PRELOAD;
+    if (pre) {
+#pragma unroll
+        for (int u = 0; u < (CAN_PRE ? PRELOAD : 1); ++u)
+            if (sub + 8 * u < groups && valid[0]) G::load(dp[u], a.seg[0].w, lrow[0], sub + 8 * u);
+    } else if (sub < groups) {
+        load_group(sub);
+    }
+    Q8View xq = a.x;
+    if (IN == 0) {
         const int4 *src = reinterpret_cast<const int4 *>(a.x.q);
         int4 *dst = reinterpret_cast<int4 *>(lds);
         for (int i = threadIdx.x; i < groups * 16; i += blockDim.x)
             dst[(i >> 4) * (SLOT_INTS / 4) + (i & 15)] = src[i];
+    } else {
+        float *sc = reinterpret_cast<float *>(lds + groups * SLOT_INTS);
+        int *s256 = reinterpret_cast<int *>(sc + groups);
+        int *s16 = s256 + groups;
+        int *s32 = s16 + groups * 16;
+        float *gss = reinterpret_cast<float *>(s32 + groups * 8);
+        stage_f32<IN>(a, lds, sc, s256, s16, s32, gss);
+        xq.s = sc;
+        xq.sum256 = s256;
+        xq.sum16 = s16;
+        xq.sum32 = s32;
     }
     __syncthreads();
 
@@ -94,30 +218,42 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
 #pragma unroll
     for (int i = 0; i < NR; ++i) acc[i] = acc2[i] = 0.f;
 
-    for (int g = sub; g < groups; g += 8) {
-        int act[64];
-        {
-            const int4 *s4 = reinterpret_cast<const int4 *>(lds + g * SLOT_INTS);
+    auto stage_act = [&](int g, int (&act)[64]) {
+        const int4 *s4 = reinterpret_cast<const int4 *>(lds + g * SLOT_INTS);
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const int4 v = s4[j];
-                act[4 * j] = v.x;
-                act[4 * j + 1] = v.y;
-                act[4 * j + 2] = v.z;
-                act[4 * j + 3] = v.w;
-            }
+        for (int j = 0; j < 16; ++j) {
+            const int4 v = s4[j];
+            act[4 * j] = v.x;
+            act[4 * j + 1] = v.y;
+            act[4 * j + 2] = v.z;
+            act[4 * j + 3] = v.w;
         }
-        if (g != sub) load_group(g);
+    };
+    if (pre) {
 #pragma unroll
-        for (int i = 0; i < NR; ++i) {
-            if (!valid[i]) continue;
-            if (MODE == GEMV_ISUMS) {
-                int32_t *out = a.isums + ((size_t)lrow[i] * groups + g) * G::ISUMS;
-                acc[i] += G::template dot<true>(d[i], act, a.x, g, out);
-            } else {
-                acc[i] += G::template dot<false>(d[i], act, a.x, g, nullptr);
-                if (MODE == GEMV_SILU)
-                    acc2[i] += G::template dot<false>(d2[i], act, a.x, g, nullptr);
+        for (int u = 0; u < (CAN_PRE ? PRELOAD : 1); ++u) {
+            const int g = sub + 8 * u;
+            if (g >= groups || !valid[0]) continue;
+            int act[64];
+            stage_act(g, act);
+            acc[0] += G::template dot<false>(dp[u], act, xq, g, nullptr);
+        }
+    } else {
+        for (int g = sub; g < groups; g += 8) {
+            int act[64];
+            stage_act(g, act);
+            if (g != sub) load_group(g);
+#pragma unroll
+            for (int i = 0; i < NR; ++i) {
+                if (!valid[i]) continue;
+                if (MODE == GEMV_ISUMS) {
+                    int32_t *out = a.isums + ((size_t)lrow[i] * groups + g) * G::ISUMS;
+                    acc[i] += G::template dot<true>(d[i], act, xq, g, out);
+                } else {
+                    acc[i] += G::template dot<false>(d[i], act, xq, g, nullptr);
+                    if (MODE == GEMV_SILU)
+                        acc2[i] += G::template dot<false>(d2[i], act, xq, g, nullptr);
+                }
             }
         }
     }
@@ -137,27 +273,38 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     }
 }
 
-template <int F, int MODE>
+template <int F, int MODE, int IN>
 int launch_nr(int nr, const GemvArgs &a, dim3 grid, dim3 block, size_t lds, hipStream_t st)
 {
     switch (nr) {
-    case 1: hipLaunchKernelGGL((gemv_kernel<F, 1, MODE>), grid, block, lds, st, a); break;
-    case 2: hipLaunchKernelGGL((gemv_kernel<F, 2, MODE>), grid, block, lds, st, a); break;
-    default: hipLaunchKernelGGL((gemv_kernel<F, 4, MODE>), grid, block, lds, st, a); break;
+    case 1: hipLaunchKernelGGL((gemv_kernel<F, 1, MODE, IN>), grid, block, lds, st, a); break;
+    case 2: hipLaunchKernelGGL((gemv_kernel<F, 2, MODE, IN>), grid, block, lds, st, a); break;
+    default: hipLaunchKernelGGL((gemv_kernel<F, 4, MODE, IN>), grid, block, lds, st, a); break;
     }
     return (int)hipGetLastError();
+}
+
+template <int F, int IN>
+int launch_in(int mode, int nr, const GemvArgs &a, dim3 grid, dim3 block, size_t lds,
+              hipStream_t st)
+{
+    switch (mode) {
+    case GEMV_PLAIN: return launch_nr<F, GEMV_PLAIN, IN>(nr, a, grid, block, lds, st);
+    case GEMV_SILU: return launch_nr<F, GEMV_SILU, IN>(nr, a, grid, block, lds, st);
+    case GEMV_MULTI: return launch_nr<F, GEMV_MULTI, IN>(nr, a, grid, block, lds, st);
+    default:
+        if (IN != 0) return (int)hipErrorInvalidValue;
+        return launch_nr<F, GEMV_ISUMS, 0>(1, a, grid, block, lds, st);
+    }
 }
 
 template <int F>
 int launch_fmt(int mode, int nr, const GemvArgs &a, dim3 grid, dim3 block, size_t lds,
                hipStream_t st)
 {
-    switch (mode) {
-    case GEMV_PLAIN: return launch_nr<F, GEMV_PLAIN>(nr, a, grid, block, lds, st);
-    case GEMV_SILU: return launch_nr<F, GEMV_SILU>(nr, a, grid, block, lds, st);
-    case GEMV_MULTI: return launch_nr<F, GEMV_MULTI>(nr, a, grid, block, lds, st);
-    default: return launch_nr<F, GEMV_ISUMS>(1, a, grid, block, lds, st);
-    }
+    if (!a.xin) return launch_in<F, 0>(mode, nr, a, grid, block, lds, st);
+    if (!a.norm) return launch_in<F, 1>(mode, nr, a, grid, block, lds, st);
+    return launch_in<F, 2>(mode, nr, a, grid, block, lds, st);
 }
 
 } // namespace
@@ -188,9 +335,14 @@ int launch_gemv(int fmt, int mode, const GemvArgs &a, void *stream)
         if (rows >= 8 * nr * 4 * 512) waves = 4;
         else if (rows >= 8 * nr * 2 * 512) waves = 2;
     }
+    // With an f32 input stage every workgroup quantizes the whole input row,
+    // so fewer, wider workgroups (4 waves) share that work.
+    if (a.xin) waves = 4;
     const int rows_per_block = 8 * nr * waves;
     dim3 grid((rows + rows_per_block - 1) / rows_per_block), block(64 * waves);
-    const size_t lds = (size_t)a.groups * SLOT_INTS * 4;
+    // slots, then (input stage) scales, 256/16/32-value sums and group sums of squares
+    const size_t lds = (size_t)a.groups * SLOT_INTS * 4 +
+                       (a.xin ? (size_t)a.groups * (4 + 4 + 64 + 32 + 4) : 0);
     hipStream_t st = (hipStream_t)stream;
     switch (fmt) {
     case Q2_0C: return launch_fmt<Q2_0C>(mode, nr, a, grid, block, lds, st);

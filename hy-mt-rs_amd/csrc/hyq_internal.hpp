@@ -111,6 +111,12 @@ struct GemvArgs {
     Q8View x;
     const float *residual; // PLAIN: y = residual + W x when non-null
     int32_t *isums;        // ISUMS output
+    // f32 input stage (decode step): when xin is set, every workgroup forms
+    // the Q8 activations of xin itself, in LDS, instead of reading x: of
+    // rms_norm(xin) * norm (eps) when norm is set, else of xin.
+    const float *xin;
+    const float *norm;
+    float eps;
 };
 
 // Kernel launchers (defined in the .hip files). All return hipError_t as int.

@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 
 #include "hyq_internal.hpp"
+#include "hyq_wave.hpp"
 
 namespace hyq {
 
@@ -45,9 +46,7 @@ __device__ __forceinline__ void q8_quantize_group(float v, int g, int len, int8_
     __shared__ int wsum[4];
     const int t = threadIdx.x;
     const int base = g * 256;
-    float m = fabsf(v);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    float m = wave::max64(fabsf(v));
     if ((t & 63) == 0) wmax[t >> 6] = m;
     __syncthreads();
     m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
@@ -64,13 +63,13 @@ __device__ __forceinline__ void q8_quantize_group(float v, int g, int len, int8_
     if (t < len) q[base + t] = (int8_t)qi;
     if (t == 0) s[g] = scale;
 
-    int a = qi;
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) a += __shfl_xor(a, off, 64);
-    if ((t & 15) == 0 && t < len) sum16[(base + t) >> 4] = a;
-    a += __shfl_xor(a, 16, 64);
-    if ((t & 31) == 0 && t < len) sum32[(base + t) >> 5] = a;
-    a += __shfl_xor(a, 32, 64);
+    // one value per lane: 16-value sums over rows, 32-value over row pairs
+    const int a16 = wave::sum16(qi);
+    if ((t & 15) == 0 && t < len) sum16[(base + t) >> 4] = a16;
+    const int h0 = wave::lane(a16, 0) + wave::lane(a16, 16);
+    const int h1 = wave::lane(a16, 32) + wave::lane(a16, 48);
+    if ((t & 31) == 0 && t < len) sum32[(base + t) >> 5] = (t & 32) ? h1 : h0;
+    const int a = h0 + h1;
     if ((t & 63) == 0) wsum[t >> 6] = a;
     __syncthreads();
     if (t == 0) sum256[g] = wsum[0] + wsum[1] + wsum[2] + wsum[3];

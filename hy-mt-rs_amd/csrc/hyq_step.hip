@@ -15,24 +15,14 @@
 #include "hyq_decode.hpp"
 #include "hyq_q8.hpp"
 #include "hyq_step.hpp"
+#include "hyq_wave.hpp"
 
 namespace hyq {
 
 namespace {
 
-__device__ __forceinline__ float wave_sum(float v)
-{
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
-__device__ __forceinline__ float wave_max(float v)
-{
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return wave::sum64(v); }
+__device__ __forceinline__ float wave_max(float v) { return wave::max64(v); }
 
 // ---- embedding row (Weight::row_into with a device-resident token id) ----
 template <int F>
@@ -150,179 +140,222 @@ __global__ void rope_norm_kv_kernel(float *__restrict__ q, const float *__restri
     }
 }
 
-// ---- attention over positions 0..=pos, split into ATT_CHUNK-position slices ----
-// Grid (splits, kv_heads); wave w of a workgroup serves query head
-// kvh*rep + hh0 + w for hh0 = 0, 4, ... (rep = heads/kv_heads). The slice's K
-// and V rows are fetched with all loads in flight at once (4 float4 of each
-// per thread), then staged in LDS (K rows padded to 129 floats). Two lanes
-// share one position's 128-wide dot; the wave then forms the slice's max,
-// exp-sum and exp-weighted V sum; attn_combine merges the slices.
-constexpr int ATT_CHUNK = 32;
-constexpr int ATT_D = 128;
+// ---- attention over positions 0..=pos, in splits of `chunk` positions ----
+// Grid (splits, kv_heads); only the splits that hold visible positions do
+// work. A workgroup walks its split in ATT_SUB-position slices: the slice's
+// K and V rows are fetched with all loads in flight at once (8 float4 of
+// each per thread; the next slice's loads are issued before the current one
+// is used) and staged in LDS (K rows padded to 129 floats). Wave w serves
+// query head kvh*rep + w: lane p scores position p of the slice with a
+// 128-wide dot, the wave keeps an online softmax (running max, exp-sum and
+// exp-weighted V sum, lane l owning output dims l and l + 64), and the
+// split's (max, exp-sum, V sum) per query head goes to `part`
+// ([heads][splits][PART_STRIDE]); a merge (attn_merge_kernel, or the output
+// projection's input stage) combines the splits.
+//
+// With `rope` set the workgroup first forms its query heads from the raw
+// projection (rope_with_cache + the dense order's per-head rms_norm,
+// src/model.rs:425-446, 874-917), and the split holding `pos` also forms the
+// new key (RoPE + norm) and value, appends them to the caches
+// (KvCache::append, src/model.rs:650-669) and uses them from LDS.
 
-__global__ __launch_bounds__(256) void attn_partial_kernel(
-    const float *__restrict__ q, const float *__restrict__ kcache,
-    const float *__restrict__ vcache, const int *__restrict__ pos_p, int heads, int kvh,
-    float scale, float *__restrict__ part, int splits)
+// RoPE (NeoX halves j, j+64) of one 128-wide head followed by its rms_norm;
+// lane j of a full wave owns the pair.
+__device__ __forceinline__ void rope_norm_pair(float a, float c2, float cs, float sn, float n0,
+                                               float n1, float eps, float &o0, float &o1)
+{
+    const float r0 = a * cs - c2 * sn;
+    const float r1 = a * sn + c2 * cs;
+    const float ss = wave_sum(r0 * r0 + r1 * r1);
+    const float scale = 1.0f / sqrtf(ss / (float)ATT_D + eps);
+    o0 = r0 * scale * n0;
+    o1 = r1 * scale * n1;
+}
+
+__global__ __launch_bounds__(256) void attn_kernel(
+    bool rope, const float *__restrict__ q, const float *__restrict__ knew,
+    const float *__restrict__ vnew, const float *__restrict__ qn, const float *__restrict__ kn,
+    const float *__restrict__ freq, float eps, float *__restrict__ kcache,
+    float *__restrict__ vcache, const int *__restrict__ pos_p, int heads, int kvh, float scale,
+    float *__restrict__ part, int splits, int chunk)
 {
     constexpr int D = ATT_D;
-    __shared__ float Ks[ATT_CHUNK][D + 1];
-    __shared__ float4 Vs[ATT_CHUNK][D / 4];
-    __shared__ float Qs[4][D];
+    __shared__ float Ks[ATT_SUB][D + 1];
+    __shared__ float Vs[ATT_SUB][D];
+    __shared__ float Qs[ATT_MAX_REP][D];
+    __shared__ float Kn[D];
+    __shared__ float Vn[D];
     const int split = blockIdx.x, kh = blockIdx.y;
-    const int visible = *pos_p + 1;
-    const int p0 = split * ATT_CHUNK;
-    const int n = min(ATT_CHUNK, visible - p0);
+    const int pos = *pos_p;
+    const int visible = pos + 1;
+    const int nact = (visible + chunk - 1) / chunk;
+    if (split >= nact) return;
+    const int p0 = split * chunk;
+    const int n = min(chunk, visible - p0);
     const int rep = heads / kvh;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const size_t kvw = (size_t)kvh * D;
-    if (n <= 0) {
-        for (int i = t; i < rep; i += 256) {
-            float *o = part + ((size_t)(kh * rep + i) * splits + split) * (D + 2);
-            o[0] = -INFINITY;
-            o[1] = 0.f;
-        }
-        return;
+    const float *kbase = kcache + (size_t)p0 * kvw + (size_t)kh * D;
+    const float *vbase = vcache + (size_t)p0 * kvw + (size_t)kh * D;
+    // the new position's row of this head is formed here, not read
+    const int pnew = rope && split == nact - 1 ? pos - p0 : -1;
+    // thread t stages float4 (row t/32 + 8j, column quad t%32), j = 0..7
+    const int r0 = t >> 5, d4 = t & 31;
+    float4 kr[8], vr[8];
+#define HYQ_ATT_LOAD(SB)                                                                       \
+    _Pragma("unroll") for (int j = 0; j < 8; ++j)                                             \
+    {                                                                                          \
+        const int pp = (SB) + r0 + 8 * j;                                                      \
+        if (pp < n && pp != pnew) {                                                            \
+            kr[j] = reinterpret_cast<const float4 *>(kbase + (size_t)pp * kvw)[d4];             \
+            vr[j] = reinterpret_cast<const float4 *>(vbase + (size_t)pp * kvw)[d4];             \
+        } else {                                                                               \
+            kr[j] = vr[j] = make_float4(0.f, 0.f, 0.f, 0.f);                                   \
+        }                                                                                      \
     }
-    float4 kr[4], vr[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int idx = t + 256 * j; // float4 index in the 32 x 128 slice
-        const int p = idx >> 5, d4 = idx & 31;
-        if (p < n) {
-            const size_t off = (size_t)(p0 + p) * kvw + (size_t)kh * D + 4 * d4;
-            kr[j] = *reinterpret_cast<const float4 *>(kcache + off);
-            vr[j] = *reinterpret_cast<const float4 *>(vcache + off);
-        } else {
-            kr[j] = vr[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    HYQ_ATT_LOAD(0)
+    // query head of this wave (rep <= 4: one per wave)
+    const bool has_q = wave < rep;
+    const int hq = kh * rep + wave;
+    if (rope) {
+        // every small load first, then the arithmetic
+        const float fr = freq[lane], qn0 = qn[lane], qn1 = qn[lane + D / 2];
+        float qa = 0.f, qb = 0.f;
+        if (has_q) {
+            qa = q[hq * D + lane];
+            qb = q[hq * D + lane + D / 2];
         }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int idx = t + 256 * j;
-        const int p = idx >> 5, d4 = idx & 31;
-        Ks[p][4 * d4] = kr[j].x;
-        Ks[p][4 * d4 + 1] = kr[j].y;
-        Ks[p][4 * d4 + 2] = kr[j].z;
-        Ks[p][4 * d4 + 3] = kr[j].w;
-        Vs[p][d4] = vr[j];
-    }
-    const int p = lane & 31, hf = lane >> 5;
-    for (int hh0 = 0; hh0 < rep; hh0 += 4) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int i = t + 256 * j, hq = i / D;
-            if (hh0 + hq < rep) Qs[hq][i % D] = q[(size_t)(kh * rep + hh0 + hq) * D + i % D];
+        float ka = 0.f, kb = 0.f, kn0 = 0.f, kn1 = 0.f, va = 0.f, vb = 0.f;
+        if (pnew >= 0 && wave == 0) {
+            ka = knew[kh * D + lane];
+            kb = knew[kh * D + lane + D / 2];
+            kn0 = kn[lane];
+            kn1 = kn[lane + D / 2];
         }
+        if (pnew >= 0 && wave == 1) {
+            va = vnew[kh * D + lane];
+            vb = vnew[kh * D + lane + D / 2];
+        }
+        const float ang = (float)pos * fr;
+        const float cs = cosf(ang), sn = sinf(ang);
+        if (has_q) {
+            float o0, o1;
+            rope_norm_pair(qa, qb, cs, sn, qn0, qn1, eps, o0, o1);
+            Qs[wave][lane] = o0;
+            Qs[wave][lane + D / 2] = o1;
+        }
+        if (pnew >= 0 && wave == 0) {
+            float o0, o1;
+            rope_norm_pair(ka, kb, cs, sn, kn0, kn1, eps, o0, o1);
+            Kn[lane] = o0;
+            Kn[lane + D / 2] = o1;
+            float *kdst = kcache + (size_t)pos * kvw + (size_t)kh * D;
+            kdst[lane] = o0;
+            kdst[lane + D / 2] = o1;
+        }
+        if (pnew >= 0 && wave == 1) {
+            Vn[lane] = va;
+            Vn[lane + D / 2] = vb;
+            float *vdst = vcache + (size_t)pos * kvw + (size_t)kh * D;
+            vdst[lane] = va;
+            vdst[lane + D / 2] = vb;
+        }
+    } else if (has_q) {
+        Qs[wave][lane] = q[hq * D + lane];
+        Qs[wave][lane + D / 2] = q[hq * D + lane + D / 2];
+    }
+    float m_run = -INFINITY, l_run = 0.f, acc0 = 0.f, acc1 = 0.f;
+    for (int sb = 0; sb < n; sb += ATT_SUB) {
+        const int nn = min(ATT_SUB, n - sb);
+        __syncthreads(); // the previous slice's readers are done (and Qs/Kn/Vn are ready)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int pp = r0 + 8 * j;
+            float4 kv = kr[j], vv = vr[j];
+            if (sb + pp == pnew) {
+                kv = make_float4(Kn[4 * d4], Kn[4 * d4 + 1], Kn[4 * d4 + 2], Kn[4 * d4 + 3]);
+                vv = make_float4(Vn[4 * d4], Vn[4 * d4 + 1], Vn[4 * d4 + 2], Vn[4 * d4 + 3]);
+            }
+            Ks[pp][4 * d4] = kv.x;
+            Ks[pp][4 * d4 + 1] = kv.y;
+            Ks[pp][4 * d4 + 2] = kv.z;
+            Ks[pp][4 * d4 + 3] = kv.w;
+            *reinterpret_cast<float4 *>(&Vs[pp][4 * d4]) = vv;
+        }
+        if (sb + ATT_SUB < n) HYQ_ATT_LOAD(sb + ATT_SUB)
         __syncthreads();
-        const int hh = hh0 + wave;
-        if (hh < rep) {
-            const int h = kh * rep + hh;
+        if (has_q) {
             float dot = 0.f;
-#pragma unroll 16
-            for (int d = 0; d < 64; ++d) dot += Qs[wave][hf * 64 + d] * Ks[p][hf * 64 + d];
-            dot += __shfl_xor(dot, 32, 64);
-            const float sc = p < n ? dot * scale : -INFINITY;
-            const float m = wave_max(sc);
-            const float e = p < n ? expf(sc - m) : 0.f;
-            const float sum = wave_sum(e) * 0.5f; // each position is held by two lanes
-            // lanes 0..31 own output dims 4*lane .. 4*lane+3 of V rows
-            float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-            for (int pp = 0; pp < n; ++pp) {
-                const float ep = __shfl(e, pp, 64);
-                const float4 vv = Vs[pp][lane & 31];
-                a.x += ep * vv.x;
-                a.y += ep * vv.y;
-                a.z += ep * vv.z;
-                a.w += ep * vv.w;
+#pragma unroll 32
+            for (int d = 0; d < D; ++d) dot += Qs[wave][d] * Ks[lane][d];
+            const float sc = lane < nn ? dot * scale : -INFINITY;
+            const float m_new = fmaxf(m_run, wave_max(sc));
+            const float corr = expf(m_run - m_new);
+            const float e = lane < nn ? expf(sc - m_new) : 0.f;
+            l_run = l_run * corr + wave_sum(e);
+            float a0 = acc0 * corr, a1 = acc1 * corr;
+#pragma unroll 8
+            for (int pp = 0; pp < nn; ++pp) {
+                const float ep = wave::lane(e, pp);
+                a0 += ep * Vs[pp][lane];
+                a1 += ep * Vs[pp][lane + D / 2];
             }
-            float *o = part + ((size_t)h * splits + split) * (D + 2);
-            if (lane == 0) {
-                o[0] = m;
-                o[1] = sum;
-            }
-            if (lane < 32) {
-                o[2 + 4 * lane] = a.x;
-                o[3 + 4 * lane] = a.y;
-                o[4 + 4 * lane] = a.z;
-                o[5 + 4 * lane] = a.w;
-            }
+            acc0 = a0;
+            acc1 = a1;
+            m_run = m_new;
         }
-        __syncthreads();
+    }
+#undef HYQ_ATT_LOAD
+    if (has_q) {
+        float *o = part + ((size_t)hq * splits + split) * PART_STRIDE;
+        if (lane == 0) {
+            o[0] = m_run;
+            o[1] = l_run;
+        }
+        o[4 + lane] = acc0;
+        o[4 + D / 2 + lane] = acc1;
     }
 }
 
-// Merges the slices of two heads per workgroup (256 output values = one Q8
-// group) and quantizes the attended vector for the output projection. The
-// per-slice maxima and sums are staged in LDS (dynamic: 6 floats per slice),
-// then every output value sums its slices with independent loads.
-__global__ __launch_bounds__(256) void attn_combine_q8_kernel(
-    const float *__restrict__ part, int heads, int splits, float *__restrict__ out, int8_t *q,
-    float *s, int32_t *s16, int32_t *s32, int32_t *s256)
+// Merge of the splits of one head per workgroup (128 threads, one output
+// dim each): out = sum_s exp(m_s - M) acc_s / sum_s exp(m_s - M) l_s with
+// M = max_s m_s; all of a thread's split loads are in flight at once.
+__global__ __launch_bounds__(128) void attn_merge_kernel(const float *__restrict__ part,
+                                                         int splits, int chunk,
+                                                         const int *__restrict__ pos_p,
+                                                         float *__restrict__ out)
 {
-    constexpr int D = ATT_D;
-    extern __shared__ float st[]; // m[2][S], sum[2][S], w[2][S]
-    __shared__ float den[2];
-    float *sm = st, *ssum = st + 2 * splits, *sw = st + 4 * splits;
-    const int t = threadIdx.x;
-    const int g = blockIdx.x;
-    for (int i = t; i < 2 * splits; i += 256) {
-        const int hl = i / splits, sp = i % splits, h = 2 * g + hl;
-        float m = -INFINITY, sum = 0.f;
-        if (h < heads) {
-            const float *o = part + ((size_t)h * splits + sp) * (D + 2);
-            m = o[0];
-            sum = o[1];
+    const int h = blockIdx.x, d = threadIdx.x;
+    const int nact = (*pos_p + chunk) / chunk;
+    const float *ph = part + (size_t)h * splits * PART_STRIDE;
+    float m[ATT_MAX_SPLITS], l[ATT_MAX_SPLITS], a[ATT_MAX_SPLITS];
+#pragma unroll
+    for (int s = 0; s < ATT_MAX_SPLITS; ++s)
+        if (s < nact) {
+            const float *o = ph + (size_t)s * PART_STRIDE;
+            m[s] = o[0];
+            l[s] = o[1];
+            a[s] = o[4 + d];
         }
-        sm[i] = m;
-        ssum[i] = sum;
-    }
-    __syncthreads();
-    // Slices that hold positions have sum >= 1 and form a prefix; the
-    // accumulators of the others were never written and are not read.
-    __shared__ float Mh[2];
-    __shared__ int nvalid;
-    if (t < 2) {
-        float M = -INFINITY;
-        int nv = 0;
-        for (int sp = 0; sp < splits; ++sp)
-            if (ssum[t * splits + sp] > 0.f) {
-                M = fmaxf(M, sm[t * splits + sp]);
-                nv = sp + 1;
-            }
-        Mh[t] = M;
-        if (t == 0) nvalid = nv;
-    }
-    __syncthreads();
-    for (int i = t; i < 2 * splits; i += 256)
-        sw[i] = ssum[i] > 0.f ? expf(sm[i] - Mh[i / splits]) : 0.f;
-    __syncthreads();
-    if (t < 2) {
-        float dsum = 0.f;
-        for (int sp = 0; sp < splits; ++sp) dsum += sw[t * splits + sp] * ssum[t * splits + sp];
-        den[t] = dsum;
-    }
-    __syncthreads();
-    const int hl = t / D, d = t % D, h = 2 * g + hl;
-    float v = 0.f;
-    if (h < heads) {
-        const float *ph = part + (size_t)h * splits * (D + 2) + 2 + d;
-        const float *w = sw + hl * splits;
-        float n0 = 0.f, n1 = 0.f, n2 = 0.f, n3 = 0.f;
-        const int nv = nvalid;
-        int sp = 0;
-        for (; sp + 4 <= nv; sp += 4) {
-            n0 += w[sp] * ph[(size_t)sp * (D + 2)];
-            n1 += w[sp + 1] * ph[(size_t)(sp + 1) * (D + 2)];
-            n2 += w[sp + 2] * ph[(size_t)(sp + 2) * (D + 2)];
-            n3 += w[sp + 3] * ph[(size_t)(sp + 3) * (D + 2)];
+    float M = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < ATT_MAX_SPLITS; ++s)
+        if (s < nact) M = fmaxf(M, m[s]);
+    float den = 0.f, num = 0.f;
+#pragma unroll
+    for (int s = 0; s < ATT_MAX_SPLITS; ++s)
+        if (s < nact) {
+            const float w = expf(m[s] - M);
+            den += w * l[s];
+            num += w * a[s];
         }
-        for (; sp < nv; ++sp) n0 += w[sp] * ph[(size_t)sp * (D + 2)];
-        v = ((n0 + n1) + (n2 + n3)) / den[hl];
-        if (out) out[h * D + d] = v;
-    }
-    const int len = min(256, heads * D - g * 256);
-    if (q) q8_quantize_group(v, g, len, q, s, s16, s32, s256);
+    out[h * ATT_D + d] = num / den;
+}
+
+__global__ void zero_u32_kernel(unsigned *p, int n)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
 }
 
 // ---- greedy argmax: first maximum wins ----
@@ -424,20 +457,59 @@ int launch_rope_norm_kv(float *q, const float *k, const float *v, const float *q
     return (int)hipGetLastError();
 }
 
-int attention_splits(int context) { return (context + ATT_CHUNK - 1) / ATT_CHUNK; }
+int attention_chunk(int context)
+{
+    // ATT_SUB-position multiples, at most ATT_MAX_SPLITS splits
+    const int per = (context + ATT_MAX_SPLITS - 1) / ATT_MAX_SPLITS;
+    return (per + ATT_SUB - 1) / ATT_SUB * ATT_SUB;
+}
+
+int attention_splits(int context)
+{
+    const int c = attention_chunk(context);
+    return (context + c - 1) / c;
+}
+
+int launch_zero_u32(unsigned *p, int n, void *stream)
+{
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(zero_u32_kernel, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream,
+                       p, n);
+    return (int)hipGetLastError();
+}
 
 int launch_attention(const float *q, const float *kcache, const float *vcache, const int *pos,
-                     int context, int heads, int kvh, float *part, float *out, int8_t *qq,
-                     float *s, int32_t *s16, int32_t *s32, int32_t *s256, void *stream)
+                     int context, int heads, int kvh, float *part, float *out, void *stream)
 {
-    const int splits = attention_splits(context);
+    const int splits = attention_splits(context), chunk = attention_chunk(context);
     const float scale = 1.0f / sqrtf(128.0f);
     hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(attn_partial_kernel, dim3(splits, kvh), dim3(256), 0, st, q, kcache,
-                       vcache, pos, heads, kvh, scale, part, splits);
-    hipLaunchKernelGGL(attn_combine_q8_kernel, dim3((heads * 128 + 255) / 256), dim3(256),
-                       (size_t)splits * 6 * sizeof(float), st, part, heads, splits, out, qq, s,
-                       s16, s32, s256);
+    hipLaunchKernelGGL(attn_kernel, dim3(splits, kvh), dim3(256), 0, st, false, q, nullptr,
+                       nullptr, nullptr, nullptr, nullptr, 0.f, const_cast<float *>(kcache),
+                       const_cast<float *>(vcache), pos, heads, kvh, scale, part, splits, chunk);
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(heads), dim3(128), 0, st, part, splits, chunk, pos,
+                       out);
+    return (int)hipGetLastError();
+}
+
+int launch_attention_merge(const float *part, int context, int heads, const int *pos,
+                           float *out, void *stream)
+{
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(heads), dim3(128), 0, (hipStream_t)stream, part,
+                       attention_splits(context), attention_chunk(context), pos, out);
+    return (int)hipGetLastError();
+}
+
+int launch_attention_rope(const float *q, const float *k, const float *v, const float *qn,
+                          const float *kn, const float *freq, float eps, float *kcache,
+                          float *vcache, const int *pos, int context, int heads, int kvh,
+                          float *part, void *stream)
+{
+    const int splits = attention_splits(context), chunk = attention_chunk(context);
+    const float scale = 1.0f / sqrtf(128.0f);
+    hipLaunchKernelGGL(attn_kernel, dim3(splits, kvh), dim3(256), 0, (hipStream_t)stream, true, q,
+                       k, v, qn, kn, freq, eps, kcache, vcache, pos, heads, kvh, scale, part,
+                       splits, chunk);
     return (int)hipGetLastError();
 }
 

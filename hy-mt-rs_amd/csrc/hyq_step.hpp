@@ -22,10 +22,31 @@ int launch_rms_norm_q8(const float *x, const float *w, int n, float eps, float *
 int launch_rope_norm_kv(float *q, const float *k, const float *v, const float *qn,
                         const float *kn, const float *freq, const int *pos, int heads, int kvh,
                         int dim, float eps, float *kcache, float *vcache, void *stream);
+// Attention splits: `chunk` positions each (a multiple of ATT_SUB), at most
+// ATT_MAX_SPLITS; partials are [heads][splits][PART_STRIDE] floats holding
+// (max, exp-sum, -, -, exp-weighted V sum[128]).
+constexpr int ATT_SUB = 64;
+constexpr int ATT_D = 128;
+constexpr int ATT_MAX_SPLITS = 32;
+constexpr int ATT_MAX_REP = 4; // query heads per KV head (one per wave)
+constexpr int PART_STRIDE = 132;
+int attention_chunk(int context);
 int attention_splits(int context);
+int launch_zero_u32(unsigned *p, int n, void *stream);
+// Attention of one query token over cache rows 0..=*pos (q already rotated
+// and normalized), merged into out [heads*128].
 int launch_attention(const float *q, const float *kcache, const float *vcache, const int *pos,
-                     int context, int heads, int kvh, float *part, float *out, int8_t *qq,
-                     float *s, int32_t *s16, int32_t *s32, int32_t *s256, void *stream);
+                     int context, int heads, int kvh, float *part, float *out, void *stream);
+// Merge of the split partials into out [heads*128].
+int launch_attention_merge(const float *part, int context, int heads, const int *pos,
+                           float *out, void *stream);
+// The decode step's attention: RoPE + Q/K norm of the raw projections, KV
+// append at *pos, split partials (merged by the output projection's input
+// stage).
+int launch_attention_rope(const float *q, const float *k, const float *v, const float *qn,
+                          const float *kn, const float *freq, float eps, float *kcache,
+                          float *vcache, const int *pos, int context, int heads, int kvh,
+                          float *part, void *stream);
 int argmax_partials(int n);
 int launch_argmax(const float *x, int n, float *pv, int *pi, int *token, StepState *st,
                   int *history, void *stream);
