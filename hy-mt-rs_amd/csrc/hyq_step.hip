@@ -177,7 +177,7 @@ __global__ __launch_bounds__(256) void attn_kernel(
     const float *__restrict__ vnew, const float *__restrict__ qn, const float *__restrict__ kn,
     const float *__restrict__ freq, float eps, float *__restrict__ kcache,
     float *__restrict__ vcache, const int *__restrict__ pos_p, int heads, int kvh, float scale,
-    float *__restrict__ part, int splits, int chunk)
+    float *__restrict__ part, int splits, int chunk, int context)
 {
     constexpr int D = ATT_D;
     __shared__ float Ks[ATT_SUB][D + 1];
@@ -186,22 +186,32 @@ __global__ __launch_bounds__(256) void attn_kernel(
     __shared__ float Kn[D];
     __shared__ float Vn[D];
     const int split = blockIdx.x, kh = blockIdx.y;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const size_t kvw = (size_t)kvh * D;
+    const int p0 = split * chunk;
+    const float *kbase = kcache + (size_t)p0 * kvw + (size_t)kh * D;
+    const float *vbase = vcache + (size_t)p0 * kvw + (size_t)kh * D;
+    // thread t stages float4 (row t/32 + 8j, column quad t%32), j = 0..7.
+    // The first slice is fetched before the position is known (rows of the
+    // allocated cache, clamped to `context`; rows past the visible ones are
+    // masked out below), so its latency overlaps the position's.
+    const int r0 = t >> 5, d4 = t & 31;
+    float4 kr[8], vr[8];
+    const int rows0 = min(ATT_SUB, context - p0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int pp = min(r0 + 8 * j, rows0 - 1);
+        kr[j] = reinterpret_cast<const float4 *>(kbase + (size_t)pp * kvw)[d4];
+        vr[j] = reinterpret_cast<const float4 *>(vbase + (size_t)pp * kvw)[d4];
+    }
     const int pos = *pos_p;
     const int visible = pos + 1;
     const int nact = (visible + chunk - 1) / chunk;
     if (split >= nact) return;
-    const int p0 = split * chunk;
     const int n = min(chunk, visible - p0);
     const int rep = heads / kvh;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const size_t kvw = (size_t)kvh * D;
-    const float *kbase = kcache + (size_t)p0 * kvw + (size_t)kh * D;
-    const float *vbase = vcache + (size_t)p0 * kvw + (size_t)kh * D;
     // the new position's row of this head is formed here, not read
     const int pnew = rope && split == nact - 1 ? pos - p0 : -1;
-    // thread t stages float4 (row t/32 + 8j, column quad t%32), j = 0..7
-    const int r0 = t >> 5, d4 = t & 31;
-    float4 kr[8], vr[8];
 #define HYQ_ATT_LOAD(SB)                                                                       \
     _Pragma("unroll") for (int j = 0; j < 8; ++j)                                             \
     {                                                                                          \
@@ -213,7 +223,6 @@ __global__ __launch_bounds__(256) void attn_kernel(
             kr[j] = vr[j] = make_float4(0.f, 0.f, 0.f, 0.f);                                   \
         }                                                                                      \
     }
-    HYQ_ATT_LOAD(0)
     // query head of this wave (rep <= 4: one per wave)
     const bool has_q = wave < rep;
     const int hq = kh * rep + wave;
@@ -272,6 +281,7 @@ __global__ __launch_bounds__(256) void attn_kernel(
         for (int j = 0; j < 8; ++j) {
             const int pp = r0 + 8 * j;
             float4 kv = kr[j], vv = vr[j];
+            if (sb + pp >= n) kv = vv = make_float4(0.f, 0.f, 0.f, 0.f);
             if (sb + pp == pnew) {
                 kv = make_float4(Kn[4 * d4], Kn[4 * d4 + 1], Kn[4 * d4 + 2], Kn[4 * d4 + 3]);
                 vv = make_float4(Vn[4 * d4], Vn[4 * d4 + 1], Vn[4 * d4 + 2], Vn[4 * d4 + 3]);
@@ -326,17 +336,19 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(const float *__restrict
                                                          float *__restrict__ out)
 {
     const int h = blockIdx.x, d = threadIdx.x;
-    const int nact = (*pos_p + chunk) / chunk;
     const float *ph = part + (size_t)h * splits * PART_STRIDE;
+    // every split slot is loaded together with the position (the unused
+    // ones are in bounds and ignored), so only one memory round trip is paid
     float m[ATT_MAX_SPLITS], l[ATT_MAX_SPLITS], a[ATT_MAX_SPLITS];
 #pragma unroll
     for (int s = 0; s < ATT_MAX_SPLITS; ++s)
-        if (s < nact) {
+        if (s < splits) {
             const float *o = ph + (size_t)s * PART_STRIDE;
             m[s] = o[0];
             l[s] = o[1];
             a[s] = o[4 + d];
         }
+    const int nact = (*pos_p + chunk) / chunk;
     float M = -INFINITY;
 #pragma unroll
     for (int s = 0; s < ATT_MAX_SPLITS; ++s)
@@ -486,7 +498,8 @@ int launch_attention(const float *q, const float *kcache, const float *vcache, c
     hipStream_t st = (hipStream_t)stream;
     hipLaunchKernelGGL(attn_kernel, dim3(splits, kvh), dim3(256), 0, st, false, q, nullptr,
                        nullptr, nullptr, nullptr, nullptr, 0.f, const_cast<float *>(kcache),
-                       const_cast<float *>(vcache), pos, heads, kvh, scale, part, splits, chunk);
+                       const_cast<float *>(vcache), pos, heads, kvh, scale, part, splits, chunk,
+                       context);
     hipLaunchKernelGGL(attn_merge_kernel, dim3(heads), dim3(128), 0, st, part, splits, chunk, pos,
                        out);
     return (int)hipGetLastError();
@@ -509,7 +522,7 @@ int launch_attention_rope(const float *q, const float *k, const float *v, const 
     const float scale = 1.0f / sqrtf(128.0f);
     hipLaunchKernelGGL(attn_kernel, dim3(splits, kvh), dim3(256), 0, (hipStream_t)stream, true, q,
                        k, v, qn, kn, freq, eps, kcache, vcache, pos, heads, kvh, scale, part,
-                       splits, chunk);
+                       splits, chunk, context);
     return (int)hipGetLastError();
 }
 
