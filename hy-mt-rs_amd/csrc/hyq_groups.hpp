@@ -30,6 +30,32 @@ __device__ __forceinline__ int sdot4(uint32_t a, int b, int c)
     return __builtin_amdgcn_sdot4((int)a, b, c, false);
 }
 
+// A group's loaded words are passed through an empty volatile asm at the
+// top of `dot`, so that no arithmetic on them (f16 scale conversion, scale
+// unpacking) is hoisted to the load: a load issued under a condition would
+// otherwise be followed at once by its conversion, and the wave would wait
+// there for that load and every load issued before it instead of letting
+// them complete behind the input stage.
+__device__ __forceinline__ void hold(uint32_t &v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void hold(uint4 &v)
+{
+    hold(v.x);
+    hold(v.y);
+    hold(v.z);
+    hold(v.w);
+}
+__device__ __forceinline__ void hold(uint2 &v)
+{
+    hold(v.x);
+    hold(v.y);
+}
+__device__ __forceinline__ void hold(uint16_t &v)
+{
+    uint32_t t = v;
+    hold(t);
+    v = (uint16_t)t;
+}
+
 // ---------------------------------------------------------------------------
 // Q2_0C: 512-weight blocks, two 256-weight groups (halves) per block.
 // isum_half = sum (2c-3) q = 2 sum c q - 3 sum q   (src/quant.rs:1891-1951)
@@ -40,6 +66,12 @@ struct GroupQ2C {
     struct Data {
         uint4 w[4];
         uint16_t d;
+        __device__ __forceinline__ void hold_all()
+        {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) hold(w[u]);
+            hold(d);
+        }
     };
     __device__ __forceinline__ static void load(Data &D, const WView &w, int row, int g)
     {
@@ -50,9 +82,11 @@ struct GroupQ2C {
         D.d = reinterpret_cast<const uint16_t *>(w.p1)[blk];
     }
     template <bool EMIT>
-    __device__ __forceinline__ static float dot(const Data &D, const int *act, const Q8View &x,
-                                                int g, int32_t *out)
+    __device__ __forceinline__ static float dot(const Data &Din, const int *act,
+                                                const Q8View &x, int g, int32_t *out)
     {
+        Data D = Din;
+        D.hold_all();
         int raw = 0;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -82,6 +116,13 @@ struct GroupSTQ {
         uint4 nib[2];
         uint2 sgn;
         uint16_t d;
+        __device__ __forceinline__ void hold_all()
+        {
+            hold(nib[0]);
+            hold(nib[1]);
+            hold(sgn);
+            hold(d);
+        }
     };
     __device__ __forceinline__ static void load(Data &D, const WView &w, int row, int g)
     {
@@ -115,9 +156,11 @@ struct GroupSTQ {
         return (hi & m4) | (lo & ~m4);
     }
     template <bool EMIT>
-    __device__ __forceinline__ static float dot(const Data &D, const int *act, const Q8View &x,
-                                                int g, int32_t *out)
+    __device__ __forceinline__ static float dot(const Data &Din, const int *act,
+                                                const Q8View &x, int g, int32_t *out)
     {
+        Data D = Din;
+        D.hold_all();
         const uint32_t nib[8] = {D.nib[0].x, D.nib[0].y, D.nib[0].z, D.nib[0].w,
                                  D.nib[1].x, D.nib[1].y, D.nib[1].z, D.nib[1].w};
         const uint32_t sg[2] = {D.sgn.x, D.sgn.y};
@@ -155,6 +198,12 @@ struct GroupQ4K {
     struct Data {
         uint4 qs[8];
         uint4 meta;
+        __device__ __forceinline__ void hold_all()
+        {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) hold(qs[i]);
+            hold(meta);
+        }
     };
     __device__ __forceinline__ static void load(Data &D, const WView &w, int row, int g)
     {
@@ -165,9 +214,11 @@ struct GroupQ4K {
         D.meta = reinterpret_cast<const uint4 *>(w.p1)[blk];
     }
     template <bool EMIT>
-    __device__ __forceinline__ static float dot(const Data &D, const int *act, const Q8View &x,
-                                                int g, int32_t *out)
+    __device__ __forceinline__ static float dot(const Data &Din, const int *act,
+                                                const Q8View &x, int g, int32_t *out)
     {
+        Data D = Din;
+        D.hold_all();
         uint32_t q[32];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -223,6 +274,13 @@ struct GroupQ6K {
         uint4 q[12];
         uint4 sc;
         uint16_t d;
+        __device__ __forceinline__ void hold_all()
+        {
+#pragma unroll
+            for (int i = 0; i < 12; ++i) hold(q[i]);
+            hold(sc);
+            hold(d);
+        }
     };
     __device__ __forceinline__ static void load(Data &D, const WView &w, int row, int g)
     {
@@ -234,9 +292,11 @@ struct GroupQ6K {
         D.d = reinterpret_cast<const uint16_t *>(w.p2)[blk];
     }
     template <bool EMIT>
-    __device__ __forceinline__ static float dot(const Data &D, const int *act, const Q8View &x,
-                                                int g, int32_t *out)
+    __device__ __forceinline__ static float dot(const Data &Din, const int *act,
+                                                const Q8View &x, int g, int32_t *out)
     {
+        Data D = Din;
+        D.hold_all();
         uint32_t v[48];
 #pragma unroll
         for (int i = 0; i < 12; ++i) {
@@ -293,6 +353,12 @@ struct GroupQ80 {
     struct Data {
         uint4 q[16];
         uint4 d;
+        __device__ __forceinline__ void hold_all()
+        {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) hold(q[i]);
+            hold(d);
+        }
     };
     __device__ __forceinline__ static void load(Data &D, const WView &w, int row, int g)
     {
@@ -303,9 +369,11 @@ struct GroupQ80 {
         D.d = *reinterpret_cast<const uint4 *>(w.p1 + blk * 2);
     }
     template <bool EMIT>
-    __device__ __forceinline__ static float dot(const Data &D, const int *act, const Q8View &x,
-                                                int g, int32_t *out)
+    __device__ __forceinline__ static float dot(const Data &Din, const int *act,
+                                                const Q8View &x, int g, int32_t *out)
     {
+        Data D = Din;
+        D.hold_all();
         const uint32_t dw[4] = {D.d.x, D.d.y, D.d.z, D.d.w};
         const float sg = x.s[g];
         float acc = 0.f;

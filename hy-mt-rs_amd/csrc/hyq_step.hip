@@ -189,12 +189,35 @@ __global__ __launch_bounds__(256) void attn_kernel(
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const size_t kvw = (size_t)kvh * D;
     const int p0 = split * chunk;
+    const int rep = heads / kvh;
+    // query head of this wave (rep <= 4: one per wave); waves past `rep`
+    // read the last head's row (in bounds) and do not use it
+    const bool has_q = wave < rep;
+    const int hq = kh * rep + wave;
+    const int hql = kh * rep + min(wave, rep - 1);
+    // Loads in the order their values are needed, since they complete in
+    // issue order: the small operands (query row, RoPE frequencies, norm
+    // weights, the new key/value rows), then the first slice's K/V rows of
+    // the allocated cache (clamped to `context`; rows past the visible ones
+    // are masked out below), then the position. None of them depends on the
+    // position, so all latencies overlap.
+    const float qa = q[hql * D + lane], qb = q[hql * D + lane + D / 2];
+    float fr = 0.f, qn0 = 0.f, qn1 = 0.f, kn0 = 0.f, kn1 = 0.f;
+    float ka = 0.f, kb = 0.f, va = 0.f, vb = 0.f;
+    if (rope) {
+        fr = freq[lane];
+        qn0 = qn[lane];
+        qn1 = qn[lane + D / 2];
+        kn0 = kn[lane];
+        kn1 = kn[lane + D / 2];
+        ka = knew[kh * D + lane];
+        kb = knew[kh * D + lane + D / 2];
+        va = vnew[kh * D + lane];
+        vb = vnew[kh * D + lane + D / 2];
+    }
     const float *kbase = kcache + (size_t)p0 * kvw + (size_t)kh * D;
     const float *vbase = vcache + (size_t)p0 * kvw + (size_t)kh * D;
-    // thread t stages float4 (row t/32 + 8j, column quad t%32), j = 0..7.
-    // The first slice is fetched before the position is known (rows of the
-    // allocated cache, clamped to `context`; rows past the visible ones are
-    // masked out below), so its latency overlaps the position's.
+    // thread t stages float4 (row t/32 + 8j, column quad t%32), j = 0..7
     const int r0 = t >> 5, d4 = t & 31;
     float4 kr[8], vr[8];
     const int rows0 = min(ATT_SUB, context - p0);
@@ -207,9 +230,17 @@ __global__ __launch_bounds__(256) void attn_kernel(
     const int pos = *pos_p;
     const int visible = pos + 1;
     const int nact = (visible + chunk - 1) / chunk;
-    if (split >= nact) return;
+    if (split >= nact) {
+        // The idle split consumes its loads as well (a store that a valid
+        // position never takes), so the compiler cannot sink them below
+        // this branch and behind the position's latency.
+        float z = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) z += kr[j].x + vr[j].x;
+        if (pos < 0 && z == 0.f) part[0] = z;
+        return;
+    }
     const int n = min(chunk, visible - p0);
-    const int rep = heads / kvh;
     // the new position's row of this head is formed here, not read
     const int pnew = rope && split == nact - 1 ? pos - p0 : -1;
 #define HYQ_ATT_LOAD(SB)                                                                       \
@@ -223,28 +254,7 @@ __global__ __launch_bounds__(256) void attn_kernel(
             kr[j] = vr[j] = make_float4(0.f, 0.f, 0.f, 0.f);                                   \
         }                                                                                      \
     }
-    // query head of this wave (rep <= 4: one per wave)
-    const bool has_q = wave < rep;
-    const int hq = kh * rep + wave;
     if (rope) {
-        // every small load first, then the arithmetic
-        const float fr = freq[lane], qn0 = qn[lane], qn1 = qn[lane + D / 2];
-        float qa = 0.f, qb = 0.f;
-        if (has_q) {
-            qa = q[hq * D + lane];
-            qb = q[hq * D + lane + D / 2];
-        }
-        float ka = 0.f, kb = 0.f, kn0 = 0.f, kn1 = 0.f, va = 0.f, vb = 0.f;
-        if (pnew >= 0 && wave == 0) {
-            ka = knew[kh * D + lane];
-            kb = knew[kh * D + lane + D / 2];
-            kn0 = kn[lane];
-            kn1 = kn[lane + D / 2];
-        }
-        if (pnew >= 0 && wave == 1) {
-            va = vnew[kh * D + lane];
-            vb = vnew[kh * D + lane + D / 2];
-        }
         const float ang = (float)pos * fr;
         const float cs = cosf(ang), sn = sinf(ang);
         if (has_q) {
@@ -270,8 +280,8 @@ __global__ __launch_bounds__(256) void attn_kernel(
             vdst[lane + D / 2] = vb;
         }
     } else if (has_q) {
-        Qs[wave][lane] = q[hq * D + lane];
-        Qs[wave][lane + D / 2] = q[hq * D + lane + D / 2];
+        Qs[wave][lane] = qa;
+        Qs[wave][lane + D / 2] = qb;
     }
     float m_run = -INFINITY, l_run = 0.f, acc0 = 0.f, acc1 = 0.f;
     for (int sb = 0; sb < n; sb += ATT_SUB) {
@@ -304,8 +314,9 @@ __global__ __launch_bounds__(256) void attn_kernel(
             const float e = lane < nn ? expf(sc - m_new) : 0.f;
             l_run = l_run * corr + wave_sum(e);
             float a0 = acc0 * corr, a1 = acc1 * corr;
-#pragma unroll 8
-            for (int pp = 0; pp < nn; ++pp) {
+            // every slice row: rows past `nn` hold zeros and have e = 0
+#pragma unroll
+            for (int pp = 0; pp < ATT_SUB; ++pp) {
                 const float ep = wave::lane(e, pp);
                 a0 += ep * Vs[pp][lane];
                 a1 += ep * Vs[pp][lane + D / 2];
@@ -327,40 +338,35 @@ __global__ __launch_bounds__(256) void attn_kernel(
     }
 }
 
-// Merge of the splits of one head per workgroup (128 threads, one output
-// dim each): out = sum_s exp(m_s - M) acc_s / sum_s exp(m_s - M) l_s with
-// M = max_s m_s; all of a thread's split loads are in flight at once.
+// Merge of the splits of one head per workgroup (128 threads = 2 waves, one
+// output dim each): out = sum_s exp(m_s - M) acc_s / sum_s exp(m_s - M) l_s
+// with M = max_s m_s. Lane s of each wave loads split s's (max, exp-sum) and
+// forms its weight; every thread loads its dim of every split slot (slots
+// past `splits` are clamped into bounds, slots past the visible splits are
+// ignored), all as vector loads issued together with the position's, so one
+// memory round trip is paid. The weights reach the accumulation by readlane.
 __global__ __launch_bounds__(128) void attn_merge_kernel(const float *__restrict__ part,
                                                          int splits, int chunk,
                                                          const int *__restrict__ pos_p,
                                                          float *__restrict__ out)
 {
-    const int h = blockIdx.x, d = threadIdx.x;
+    const int h = blockIdx.x, d = threadIdx.x, lane = d & 63;
     const float *ph = part + (size_t)h * splits * PART_STRIDE;
-    // every split slot is loaded together with the position (the unused
-    // ones are in bounds and ignored), so only one memory round trip is paid
-    float m[ATT_MAX_SPLITS], l[ATT_MAX_SPLITS], a[ATT_MAX_SPLITS];
+    const float2 ml =
+        *reinterpret_cast<const float2 *>(ph + (size_t)min(lane, splits - 1) * PART_STRIDE);
+    float a[ATT_MAX_SPLITS];
 #pragma unroll
     for (int s = 0; s < ATT_MAX_SPLITS; ++s)
-        if (s < splits) {
-            const float *o = ph + (size_t)s * PART_STRIDE;
-            m[s] = o[0];
-            l[s] = o[1];
-            a[s] = o[4 + d];
-        }
+        a[s] = ph[(size_t)min(s, splits - 1) * PART_STRIDE + 4 + d];
     const int nact = (*pos_p + chunk) / chunk;
-    float M = -INFINITY;
+    const bool live = lane < nact;
+    const float M = wave::max64(live ? ml.x : -INFINITY);
+    const float w = live ? expf(ml.x - M) : 0.f;
+    const float den = wave::sum64(w * (live ? ml.y : 0.f));
+    float num = 0.f;
 #pragma unroll
-    for (int s = 0; s < ATT_MAX_SPLITS; ++s)
-        if (s < nact) M = fmaxf(M, m[s]);
-    float den = 0.f, num = 0.f;
-#pragma unroll
-    for (int s = 0; s < ATT_MAX_SPLITS; ++s)
-        if (s < nact) {
-            const float w = expf(m[s] - M);
-            den += w * l[s];
-            num += w * a[s];
-        }
+    for (int s = 0; s < ATT_MAX_SPLITS; ++s) // a select, not a branch: the loads stay hoisted
+        num += wave::lane(w, s) * (s < nact ? a[s] : 0.f);
     out[h * ATT_D + d] = num / den;
 }
 

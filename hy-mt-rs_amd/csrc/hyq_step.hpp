@@ -28,6 +28,7 @@ int launch_rope_norm_kv(float *q, const float *k, const float *v, const float *q
 constexpr int ATT_SUB = 64;
 constexpr int ATT_D = 128;
 constexpr int ATT_MAX_SPLITS = 32;
+static_assert(ATT_MAX_SPLITS <= 64, "the merge holds one split per lane of a wave");
 constexpr int ATT_MAX_REP = 4; // query heads per KV head (one per wave)
 constexpr int PART_STRIDE = 132;
 int attention_chunk(int context);
