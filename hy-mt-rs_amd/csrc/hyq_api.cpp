@@ -122,6 +122,16 @@ int check_q8(const hyq_q8 *x, size_t cols, const char *who)
     return HYQ_OK;
 }
 
+// An f32 row that the GEMV quantizes itself into LDS (one launch, no
+// separate quantize pass): float4-aligned, with the Q8 row and its sums
+// (380 bytes per 256 values) within 60 KiB of LDS.
+constexpr size_t STAGED_MAX_GROUPS = 160;
+
+bool can_stage(const float *x_d, size_t cols)
+{
+    return (uintptr_t)x_d % 16 == 0 && cols % 256 == 0 && cols / 256 <= STAGED_MAX_GROUPS;
+}
+
 GemvArgs base_args(const hyq_weight *w, const Q8Ref &x)
 {
     GemvArgs a{};
@@ -509,6 +519,17 @@ int hyq_matmul_d(hyq_ctx *ctx, const hyq_weight *w, const float *x_d, size_t bat
     if (batch == 1) {
         rc = check_int8_path(w, "matmul");
         if (rc) return rc;
+        if (can_stage(x_d, w->cols)) {
+            GemvArgs a{};
+            a.nseg = 1;
+            a.seg[0].w = w->view;
+            a.seg[0].y = y_d;
+            a.rows_total = (int)w->rows;
+            a.groups = (int)(w->cols / 256);
+            a.xin = x_d;
+            HYQ_LAUNCH(launch_gemv(w->dtype, GEMV_PLAIN, a, ctx->stream), "gemv");
+            return HYQ_OK;
+        }
         Q8Ref q8;
         rc = ctx_q8(ctx, w->cols, &q8);
         if (!rc) rc = quantize_into(ctx, x_d, q8);

@@ -35,16 +35,62 @@ __device__ __forceinline__ float silu_mul(float g, float u)
 
 __device__ __forceinline__ float reduce8(float v) { return wave::sum8(v); }
 
-// The f32 input stage: the workgroup's waves take 256-value groups in turn
-// (group g = wave + 4i; lane l holds values 4l..4l+3) and write the Q8 row to
-// the LDS slots, the group scales and the 16/32/256-value integer sums to
-// the LDS arrays, as Q8::quantize_into (src/quant.rs:904-922) and
-// q8_quantize_group do. With a norm vector the values are rms_norm_into's
-// x * (1/sqrt(mean(x^2) + eps)) * w (src/model.rs:825-829); the sum of
-// squares is formed per group by a fixed DPP/readlane tree (hyq_wave.hpp)
-// and then over the groups in ascending order. Rows of up to 4 * STAGE_REG groups are loaded with all
-// loads in flight at once; longer rows take a loop.
-constexpr int STAGE_REG = 8;
+// The f32 input stage, as Q8::quantize_into (src/quant.rs:904-922) and
+// q8_quantize_group do, writing the Q8 row to the LDS slots and the group
+// scales and 16/32/256-value integer sums to the LDS arrays. Each 32-lane
+// half wave quantizes one 256-value group (lane c holds values 8c..8c+7),
+// so a 256-thread workgroup takes 8 groups per pass: the group maximum and
+// sums are reduced over a 16-lane row by DPP and across the half wave's two
+// rows by v_permlane16_swap, with no readlane or LDS round trip, and the
+// divisions are branch-free. With a norm vector the values are
+// rms_norm_into's x * (1/sqrt(mean(x^2) + eps)) * w (src/model.rs:825-829);
+// the sum of squares is formed per group by a fixed tree and then over the
+// groups in ascending order. Rows of up to 8 * STAGE_PASSES groups are loaded
+// with all loads in flight at once (before the weights'); longer rows take a
+// loop.
+constexpr int STAGE_PASSES = 4;
+
+struct StageRegs {
+    float4 x[STAGE_PASSES][2];
+    float4 w[STAGE_PASSES][2];
+};
+
+// v_permlane16_swap of v with itself: element 0 holds each 32-lane half's
+// even row in both of its rows, element 1 its odd row. The second operand is
+// an opaque copy (empty asm), because the compiler folds a swap of a value
+// with itself to that value.
+__device__ __forceinline__ void swap_rows(int v, int &even, int &odd)
+{
+    int u = v;
+    asm volatile("" : "+v"(u));
+    const auto r = __builtin_amdgcn_permlane16_swap(v, u, false, false);
+    even = r[0];
+    odd = r[1];
+}
+__device__ __forceinline__ float sum_rows(float v)
+{
+    int e, o;
+    swap_rows(__builtin_bit_cast(int, v), e, o);
+    return __builtin_bit_cast(float, e) + __builtin_bit_cast(float, o);
+}
+__device__ __forceinline__ int sum_rows(int v)
+{
+    int e, o;
+    swap_rows(v, e, o);
+    return e + o;
+}
+__device__ __forceinline__ float max_rows(float v)
+{
+    int e, o;
+    swap_rows(__builtin_bit_cast(int, v), e, o);
+    return fmaxf(__builtin_bit_cast(float, e), __builtin_bit_cast(float, o));
+}
+
+__device__ __forceinline__ float sq8(const float4 &a, const float4 &b)
+{
+    return ((a.x * a.x + a.y * a.y) + (a.z * a.z + a.w * a.w)) +
+           ((b.x * b.x + b.y * b.y) + (b.z * b.z + b.w * b.w));
+}
 
 __device__ __forceinline__ float4 scale_by(float4 v, float scale, float4 w)
 {
@@ -52,54 +98,41 @@ __device__ __forceinline__ float4 scale_by(float4 v, float scale, float4 w)
                        v.w * scale * w.w);
 }
 
-__device__ __forceinline__ void quantize_group4(float4 v, int g, int lane, int *slots, float *sc,
-                                                int *s256, int *s16, int *s32)
+__device__ __forceinline__ uint32_t pack4(int q0, int q1, int q2, int q3)
 {
-    const float m = wave::max64(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    float s = 0.f, inv = 0.f;
-    if (m > 0.f) {
-        s = m / 127.f;
-        inv = 127.f / m;
-    }
-    const int q0 = q8_sat_rne(v.x * inv), q1 = q8_sat_rne(v.y * inv);
-    const int q2 = q8_sat_rne(v.z * inv), q3 = q8_sat_rne(v.w * inv);
-    slots[g * SLOT_INTS + lane] =
-        (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | ((q3 & 0xff) << 24);
-    // integer sums over 16, 32 and 256 values (4, 8 and 64 lanes): exact
-    const int t4 = wave::sum4((q0 + q1) + (q2 + q3));
-    if ((lane & 3) == 0) s16[g * 16 + (lane >> 2)] = t4;
-    const int t8 = t4 + wave::dpp<wave::DPP_HALF_MIRROR>(t4);
-    if ((lane & 7) == 0) s32[g * 8 + (lane >> 3)] = t8;
-    const int t16 = t8 + wave::dpp<wave::DPP_MIRROR>(t8);
-    const int t256 = (wave::lane(t16, 0) + wave::lane(t16, 16)) +
-                     (wave::lane(t16, 32) + wave::lane(t16, 48));
-    if (lane == 0) {
-        s256[g] = t256;
+    return (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
+           ((uint32_t)(q3 & 0xff) << 24);
+}
+
+// Group g's 8 values of this lane (c = lane of the half wave).
+__device__ __forceinline__ void quantize_half(float4 a, float4 b, int g, int c, int *slots,
+                                              float *sc, int *s256, int *s16, int *s32)
+{
+    const float la = fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w)));
+    const float lb = fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)));
+    const float m = max_rows(wave::max16(fmaxf(la, lb)));
+    const bool pos = m > 0.f;
+    const float md = pos ? m : 1.f;
+    const float s = pos ? md / 127.f : 0.f;
+    const float inv = pos ? 127.f / md : 0.f;
+    const int q0 = q8_sat_rne(a.x * inv), q1 = q8_sat_rne(a.y * inv);
+    const int q2 = q8_sat_rne(a.z * inv), q3 = q8_sat_rne(a.w * inv);
+    const int q4 = q8_sat_rne(b.x * inv), q5 = q8_sat_rne(b.y * inv);
+    const int q6 = q8_sat_rne(b.z * inv), q7 = q8_sat_rne(b.w * inv);
+    *reinterpret_cast<uint2 *>(slots + g * SLOT_INTS + 2 * c) =
+        make_uint2(pack4(q0, q1, q2, q3), pack4(q4, q5, q6, q7));
+    // integer sums over 16, 32 and 256 values (2, 4 and 32 lanes): exact
+    const int t8 = ((q0 + q1) + (q2 + q3)) + ((q4 + q5) + (q6 + q7));
+    const int t16 = t8 + wave::dpp<wave::DPP_XOR1>(t8);
+    if ((c & 1) == 0) s16[g * 16 + (c >> 1)] = t16;
+    const int t32 = t16 + wave::dpp<wave::DPP_XOR2>(t16);
+    if ((c & 3) == 0) s32[g * 8 + (c >> 2)] = t32;
+    int t = t32 + wave::dpp<wave::DPP_HALF_MIRROR>(t32);
+    t = sum_rows(t + wave::dpp<wave::DPP_MIRROR>(t));
+    if (c == 0) {
+        s256[g] = t;
         sc[g] = s;
     }
-}
-
-__device__ __forceinline__ float group_ss(float4 v)
-{
-    return wave::sum64((v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w));
-}
-
-// Register path (rows of at most 4 * STAGE_REG groups): the loads are
-// issued by stage_load before the weights' (loads complete in issue order,
-// so the stage then waits for its own data only) and consumed by stage_regs.
-template <int IN>
-__device__ __forceinline__ void stage_load(const GemvArgs &a, float4 (&v)[STAGE_REG],
-                                           float4 (&w)[STAGE_REG])
-{
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const float4 *x4 = reinterpret_cast<const float4 *>(a.xin);
-    const float4 *n4 = reinterpret_cast<const float4 *>(a.norm);
-#pragma unroll
-    for (int i = 0; i < STAGE_REG; ++i)
-        if (wave + 4 * i < a.groups) {
-            v[i] = x4[(wave + 4 * i) * 64 + lane];
-            if (IN == 2) w[i] = n4[(wave + 4 * i) * 64 + lane];
-        }
 }
 
 __device__ __forceinline__ float finish_norm(const float *gss, int groups, float eps)
@@ -110,51 +143,85 @@ __device__ __forceinline__ float finish_norm(const float *gss, int groups, float
     return 1.0f / sqrtf(ss / (float)(groups * 256) + eps);
 }
 
+// Register path: the loads are issued by stage_load before the weights'
+// (loads complete in issue order, so the stage then waits for its own data
+// only) and consumed by stage_regs.
 template <int IN>
-__device__ __forceinline__ void stage_regs(const GemvArgs &a, const float4 (&v)[STAGE_REG],
-                                           const float4 (&w)[STAGE_REG], int *slots, float *sc,
-                                           int *s256, int *s16, int *s32, float *gss)
+__device__ __forceinline__ void stage_load(const GemvArgs &a, StageRegs &r)
 {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int hw = threadIdx.x >> 5, c = threadIdx.x & 31;
+    const float4 *x4 = reinterpret_cast<const float4 *>(a.xin);
+    const float4 *n4 = reinterpret_cast<const float4 *>(a.norm);
+#pragma unroll
+    for (int p = 0; p < STAGE_PASSES; ++p) {
+        const int g = 8 * p + hw;
+        if (g < a.groups) {
+            r.x[p][0] = x4[g * 64 + 2 * c];
+            r.x[p][1] = x4[g * 64 + 2 * c + 1];
+            if (IN == 2) {
+                r.w[p][0] = n4[g * 64 + 2 * c];
+                r.w[p][1] = n4[g * 64 + 2 * c + 1];
+            }
+        }
+    }
+}
+
+template <int IN>
+__device__ __forceinline__ void stage_regs(const GemvArgs &a, const StageRegs &r, int *slots,
+                                           float *sc, int *s256, int *s16, int *s32, float *gss)
+{
+    const int hw = threadIdx.x >> 5, c = threadIdx.x & 31;
     const int groups = a.groups;
     float scale = 1.f;
     if (IN == 2) {
 #pragma unroll
-        for (int i = 0; i < STAGE_REG; ++i)
-            if (wave + 4 * i < groups) {
-                const float s = group_ss(v[i]);
-                if (lane == 0) gss[wave + 4 * i] = s;
+        for (int p = 0; p < STAGE_PASSES; ++p) {
+            const int g = 8 * p + hw;
+            if (g < groups) {
+                const float ss = sum_rows(wave::sum16(sq8(r.x[p][0], r.x[p][1])));
+                if (c == 0) gss[g] = ss;
             }
+        }
         scale = finish_norm(gss, groups, a.eps);
     }
 #pragma unroll
-    for (int i = 0; i < STAGE_REG; ++i)
-        if (wave + 4 * i < groups)
-            quantize_group4(IN == 2 ? scale_by(v[i], scale, w[i]) : v[i], wave + 4 * i, lane,
-                            slots, sc, s256, s16, s32);
+    for (int p = 0; p < STAGE_PASSES; ++p) {
+        const int g = 8 * p + hw;
+        if (g < groups) {
+            if (IN == 2)
+                quantize_half(scale_by(r.x[p][0], scale, r.w[p][0]),
+                              scale_by(r.x[p][1], scale, r.w[p][1]), g, c, slots, sc, s256, s16,
+                              s32);
+            else
+                quantize_half(r.x[p][0], r.x[p][1], g, c, slots, sc, s256, s16, s32);
+        }
+    }
 }
 
-// Longer rows: a loop over the groups (loads at the top of each iteration).
+// Longer rows: a loop over the passes (loads at the top of each).
 template <int IN>
 __device__ __forceinline__ void stage_loop(const GemvArgs &a, int *slots, float *sc, int *s256,
                                            int *s16, int *s32, float *gss)
 {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int hw = threadIdx.x >> 5, c = threadIdx.x & 31;
     const int groups = a.groups;
     const float4 *x4 = reinterpret_cast<const float4 *>(a.xin);
     const float4 *n4 = reinterpret_cast<const float4 *>(a.norm);
     float scale = 1.f;
     if (IN == 2) {
-        for (int g = wave; g < groups; g += 4) {
-            const float s = group_ss(x4[g * 64 + lane]);
-            if (lane == 0) gss[g] = s;
+        for (int g = hw; g < groups; g += 8) {
+            const float ss = sum_rows(wave::sum16(sq8(x4[g * 64 + 2 * c], x4[g * 64 + 2 * c + 1])));
+            if (c == 0) gss[g] = ss;
         }
         scale = finish_norm(gss, groups, a.eps);
     }
-    for (int g = wave; g < groups; g += 4) {
-        const float4 v = x4[g * 64 + lane];
-        quantize_group4(IN == 2 ? scale_by(v, scale, n4[g * 64 + lane]) : v, g, lane, slots, sc,
-                        s256, s16, s32);
+    for (int g = hw; g < groups; g += 8) {
+        float4 va = x4[g * 64 + 2 * c], vb = x4[g * 64 + 2 * c + 1];
+        if (IN == 2) {
+            va = scale_by(va, scale, n4[g * 64 + 2 * c]);
+            vb = scale_by(vb, scale, n4[g * 64 + 2 * c + 1]);
+        }
+        quantize_half(va, vb, g, c, slots, sc, s256, s16, s32);
     }
 }
 
@@ -218,11 +285,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     // GEMV with one row per lane and P = ceil(groups / 8) <= 4 issues all P
     // of its groups at once; otherwise the first group is preloaded and the
     // others load at the top of their iteration.
-    float4 sv[STAGE_REG], sw[STAGE_REG];
+    StageRegs sr;
     i32x4 qv[Q8_REG];
-    const bool stage_reg = IN != 0 && groups <= 4 * STAGE_REG;
+    const bool stage_reg = IN != 0 && groups <= 8 * STAGE_PASSES;
     const bool q8_reg = IN == 0 && groups * 16 <= Q8_REG * (int)blockDim.x;
-    if (IN != 0 && stage_reg) stage_load<IN>(a, sv, sw);
+    if (IN != 0 && stage_reg) stage_load<IN>(a, sr);
     if (IN == 0 && q8_reg) {
         // clamped into bounds; the copy to LDS keeps the in-range ones
         const i32x4 *src = reinterpret_cast<const i32x4 *>(a.x.q);
@@ -259,7 +326,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
         int *s16 = s256 + groups;
         int *s32 = s16 + groups * 16;
         float *gss = reinterpret_cast<float *>(s32 + groups * 8);
-        if (stage_reg) stage_regs<IN>(a, sv, sw, lds, sc, s256, s16, s32, gss);
+        if (stage_reg) stage_regs<IN>(a, sr, lds, sc, s256, s16, s32, gss);
         else stage_loop<IN>(a, lds, sc, s256, s16, s32, gss);
         xq.s = sc;
         xq.sum256 = s256;

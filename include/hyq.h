@@ -138,8 +138,11 @@ int hyq_gate_up_silu_q8_d(hyq_ctx *ctx, const hyq_weight *gate, const hyq_weight
  * per 32-block are this library's definitions (no reference int path). */
 int hyq_isums_per_row(int dtype, size_t cols);
 int hyq_gemv_isums_d(hyq_ctx *ctx, const hyq_weight *w, const hyq_q8 *x, int32_t *isums_d);
-/* Weight::matmul for batch >= 2 on device buffers: x_d [batch, cols] f32,
- * y_d [batch, rows] f32 (src/quant.rs:272-344). */
+/* Weight::matmul on device buffers: x_d [batch, cols] f32, y_d [batch, rows]
+ * f32. Batch 1 is the int8 GEMV (src/quant.rs:159-270): a float4-aligned x_d
+ * whose width is a multiple of 256 (at most 40960) is quantized inside the
+ * GEMV launch, bit-identical to hyq_quantize_q8_d followed by hyq_gemv_q8_d;
+ * batch >= 2 is the f16-MFMA GEMM (src/quant.rs:272-344). */
 int hyq_matmul_d(hyq_ctx *ctx, const hyq_weight *w, const float *x_d, size_t batch,
                  float *y_d);
 /* ---- MoE expert products: the expert loop of Moe::forward (src/model.rs:699-725).

@@ -203,6 +203,38 @@ def test_gate_up_silu(gpu_ctx, oracle, dtype):
     check_decode_path(uy, ur, um)
 
 
+@pytest.mark.parametrize("dtype", QUANT, ids=lambda d: NAMES[d])
+@pytest.mark.parametrize("cols", [256, 1536, 2048, 6144, 8704, 16384])
+def test_staged_gemv_equals_quantize_then_gemv(gpu_ctx, hyq, dtype, cols):
+    """hyq_matmul_d at batch 1 quantizes the f32 row inside the GEMV launch
+    (one 32-lane half wave per 256-value group; rows above 32 groups take the
+    looped stage). Its output equals hyq_quantize_q8_d + hyq_gemv_q8_d bit for
+    bit: the same maxima, IEEE divisions, round-half-even and exact integer
+    sums. A row 4 bytes off float4 alignment takes the two-launch path and
+    must agree as well. An all-zero group (scale 0) is included."""
+    if cols % hyq.lib().hyq_block_len(dtype):
+        pytest.skip("width is not a whole number of blocks")
+    rows = 200
+    _print("staged", NAMES[dtype], cols)
+    w = random_matrix(dtype, rows, cols, seed=cols + dtype)
+    rng = np.random.default_rng(cols)
+    x = (rng.normal(0, 1, cols) * rng.choice([1e-3, 1.0, 40.0], cols)).astype(np.float32)
+    x[256:512] = 0.0
+    W = gpu_ctx.upload(dtype, w, (cols, rows))
+    xd = gpu_ctx.array(np.concatenate([x, x[:4]]))
+    xo = gpu_ctx.array(np.concatenate([np.zeros(1, np.float32), x]))  # x at byte offset 4
+    y_staged, y_two, y_off = (gpu_ctx.empty(rows, np.float32) for _ in range(3))
+    L = hyq.lib()
+    hyq.check(L.hyq_matmul_d(gpu_ctx.handle, W.handle, xd.ptr, 1, y_staged.ptr))
+    hyq.check(L.hyq_matmul_d(gpu_ctx.handle, W.handle, xo.ptr + 4, 1, y_off.ptr))
+    q8 = gpu_ctx.q8(cols)
+    q8.quantize_into(xd.ptr)
+    hyq.check(L.hyq_gemv_q8_d(gpu_ctx.handle, W.handle, q8.handle, None, y_two.ptr))
+    a, b, c = y_staged.numpy(), y_two.numpy(), y_off.numpy()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.array_equal(c.view(np.uint32), b.view(np.uint32))
+
+
 def test_residual_epilogue(gpu_ctx, hyq, oracle):
     rows, cols = 2048, 2048
     w = random_matrix(Q2_0C, rows, cols, seed=8)
