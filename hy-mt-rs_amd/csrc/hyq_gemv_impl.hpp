@@ -55,36 +55,9 @@ struct StageRegs {
     float4 w[STAGE_PASSES][2];
 };
 
-// v_permlane16_swap of v with itself: element 0 holds each 32-lane half's
-// even row in both of its rows, element 1 its odd row. The second operand is
-// an opaque copy (empty asm), because the compiler folds a swap of a value
-// with itself to that value.
-__device__ __forceinline__ void swap_rows(int v, int &even, int &odd)
-{
-    int u = v;
-    asm volatile("" : "+v"(u));
-    const auto r = __builtin_amdgcn_permlane16_swap(v, u, false, false);
-    even = r[0];
-    odd = r[1];
-}
-__device__ __forceinline__ float sum_rows(float v)
-{
-    int e, o;
-    swap_rows(__builtin_bit_cast(int, v), e, o);
-    return __builtin_bit_cast(float, e) + __builtin_bit_cast(float, o);
-}
-__device__ __forceinline__ int sum_rows(int v)
-{
-    int e, o;
-    swap_rows(v, e, o);
-    return e + o;
-}
-__device__ __forceinline__ float max_rows(float v)
-{
-    int e, o;
-    swap_rows(__builtin_bit_cast(int, v), e, o);
-    return fmaxf(__builtin_bit_cast(float, e), __builtin_bit_cast(float, o));
-}
+__device__ __forceinline__ float sum_rows(float v) { return wave::sum_rows2(v); }
+__device__ __forceinline__ int sum_rows(int v) { return wave::sum_rows2(v); }
+__device__ __forceinline__ float max_rows(float v) { return wave::max_rows2(v); }
 
 __device__ __forceinline__ float sq8(const float4 &a, const float4 &b)
 {

@@ -141,17 +141,26 @@ __global__ void rope_norm_kv_kernel(float *__restrict__ q, const float *__restri
 }
 
 // ---- attention over positions 0..=pos, in splits of `chunk` positions ----
-// Grid (splits, kv_heads); only the splits that hold visible positions do
-// work. A workgroup walks its split in ATT_SUB-position slices: the slice's
-// K and V rows are fetched with all loads in flight at once (8 float4 of
-// each per thread; the next slice's loads are issued before the current one
-// is used) and staged in LDS (K rows padded to 129 floats). Wave w serves
-// query head kvh*rep + w: lane p scores position p of the slice with a
-// 128-wide dot, the wave keeps an online softmax (running max, exp-sum and
-// exp-weighted V sum, lane l owning output dims l and l + 64), and the
-// split's (max, exp-sum, V sum) per query head goes to `part`
-// ([heads][splits][PART_STRIDE]); a merge (attn_merge_kernel, or the output
-// projection's input stage) combines the splits.
+// Grid (splits, kv_heads), 512 threads (8 waves, two per SIMD); only the
+// splits that hold visible positions do work. Splits are small (32
+// positions at contexts up to 2048) so that many CUs share the VALU work. A
+// workgroup walks its split in ATT_SUB-position slices: thread t fetches
+// float4 t % 32 of slice rows t / 32 and t / 32 + 16 of K and V, all loads in
+// flight at once (the next slice's are issued before the current one is
+// used), and stages them in LDS. The `rep` (<= 4) query heads of the KV head
+// share every LDS read: head h = lane % 4, so the four heads' lanes of a
+// 16-lane LDS pass read the same address.
+//   scores  lane (h, q = lane / 4 % 4) of wave w dots head h with slice row
+//           4w + lane / 16 over dims {4q + 16i .. +3}; row_ror DPP adds the
+//           four quarters.
+//   softmax the slice maximum and exp-sum per head over the wave's 4 rows by
+//           permlane16/32 swaps, then over the 8 waves through LDS; the
+//           workgroup keeps an online softmax (running max, exp-sum and
+//           exp-weighted V sum).
+//   V       lane (h, x = lane / 4) of wave w accumulates dim 16w + x of head h
+//           over the slice rows.
+// The split's (max, exp-sum, V sum) per query head goes to `part`
+// ([heads][splits][PART_STRIDE]) for the merge (attn_merge_kernel).
 //
 // With `rope` set the workgroup first forms its query heads from the raw
 // projection (rope_with_cache + the dense order's per-head rms_norm,
@@ -172,7 +181,10 @@ __device__ __forceinline__ void rope_norm_pair(float a, float c2, float cs, floa
     o1 = r1 * scale * n1;
 }
 
-__global__ __launch_bounds__(256) void attn_kernel(
+constexpr int ATT_WAVES = 8;
+constexpr int ATT_THREADS = 64 * ATT_WAVES;
+
+__global__ __launch_bounds__(ATT_THREADS) void attn_kernel(
     bool rope, const float *__restrict__ q, const float *__restrict__ knew,
     const float *__restrict__ vnew, const float *__restrict__ qn, const float *__restrict__ kn,
     const float *__restrict__ freq, float eps, float *__restrict__ kcache,
@@ -180,20 +192,24 @@ __global__ __launch_bounds__(256) void attn_kernel(
     float *__restrict__ part, int splits, int chunk, int context)
 {
     constexpr int D = ATT_D;
-    __shared__ float Ks[ATT_SUB][D + 1];
-    __shared__ float Vs[ATT_SUB][D];
-    __shared__ float Qs[ATT_MAX_REP][D];
-    __shared__ float Kn[D];
-    __shared__ float Vn[D];
+    static_assert(ATT_SUB == 32 && ATT_WAVES == 8 && ATT_MAX_REP == 4 && D == 128,
+                  "lane roles assume these");
+    // (16-byte aligned: read and written as float4)
+    __shared__ __align__(16) float Ks[ATT_SUB][D + 4];
+    __shared__ __align__(16) float Vs[ATT_SUB][D];
+    __shared__ __align__(16) float Qs[ATT_MAX_REP][D];
+    __shared__ __align__(16) float Kn[D];
+    __shared__ __align__(16) float Vn[D];
+    __shared__ __align__(16) float Es[ATT_MAX_REP][ATT_SUB];     // the slice's exp weights
+    __shared__ __align__(16) float Red[2][ATT_MAX_REP][ATT_WAVES]; // per-wave max / exp-sum
     const int split = blockIdx.x, kh = blockIdx.y;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const size_t kvw = (size_t)kvh * D;
     const int p0 = split * chunk;
     const int rep = heads / kvh;
-    // query head of this wave (rep <= 4: one per wave); waves past `rep`
-    // read the last head's row (in bounds) and do not use it
+    // rope: wave w < rep forms query head w of the group (waves past `rep`
+    // read the last head's row, in bounds, and do not use it)
     const bool has_q = wave < rep;
-    const int hq = kh * rep + wave;
     const int hql = kh * rep + min(wave, rep - 1);
     // Loads in the order their values are needed, since they complete in
     // issue order: the small operands (query row, RoPE frequencies, norm
@@ -201,29 +217,31 @@ __global__ __launch_bounds__(256) void attn_kernel(
     // the allocated cache (clamped to `context`; rows past the visible ones
     // are masked out below), then the position. None of them depends on the
     // position, so all latencies overlap.
-    const float qa = q[hql * D + lane], qb = q[hql * D + lane + D / 2];
-    float fr = 0.f, qn0 = 0.f, qn1 = 0.f, kn0 = 0.f, kn1 = 0.f;
+    float qa = 0.f, qb = 0.f, fr = 0.f, qn0 = 0.f, qn1 = 0.f, kn0 = 0.f, kn1 = 0.f;
     float ka = 0.f, kb = 0.f, va = 0.f, vb = 0.f;
-    if (rope) {
-        fr = freq[lane];
-        qn0 = qn[lane];
-        qn1 = qn[lane + D / 2];
-        kn0 = kn[lane];
-        kn1 = kn[lane + D / 2];
-        ka = knew[kh * D + lane];
-        kb = knew[kh * D + lane + D / 2];
-        va = vnew[kh * D + lane];
-        vb = vnew[kh * D + lane + D / 2];
+    if (wave < ATT_MAX_REP) {
+        qa = q[hql * D + lane];
+        qb = q[hql * D + lane + D / 2];
+        if (rope) {
+            fr = freq[lane];
+            qn0 = qn[lane];
+            qn1 = qn[lane + D / 2];
+            kn0 = kn[lane];
+            kn1 = kn[lane + D / 2];
+            ka = knew[kh * D + lane];
+            kb = knew[kh * D + lane + D / 2];
+            va = vnew[kh * D + lane];
+            vb = vnew[kh * D + lane + D / 2];
+        }
     }
     const float *kbase = kcache + (size_t)p0 * kvw + (size_t)kh * D;
     const float *vbase = vcache + (size_t)p0 * kvw + (size_t)kh * D;
-    // thread t stages float4 (row t/32 + 8j, column quad t%32), j = 0..7
     const int r0 = t >> 5, d4 = t & 31;
-    float4 kr[8], vr[8];
+    float4 kr[2], vr[2];
     const int rows0 = min(ATT_SUB, context - p0);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int pp = min(r0 + 8 * j, rows0 - 1);
+    for (int j = 0; j < 2; ++j) {
+        const int pp = min(r0 + 16 * j, rows0 - 1);
         kr[j] = reinterpret_cast<const float4 *>(kbase + (size_t)pp * kvw)[d4];
         vr[j] = reinterpret_cast<const float4 *>(vbase + (size_t)pp * kvw)[d4];
     }
@@ -234,9 +252,7 @@ __global__ __launch_bounds__(256) void attn_kernel(
         // The idle split consumes its loads as well (a store that a valid
         // position never takes), so the compiler cannot sink them below
         // this branch and behind the position's latency.
-        float z = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) z += kr[j].x + vr[j].x;
+        const float z = (kr[0].x + vr[0].x) + (kr[1].x + vr[1].x);
         if (pos < 0 && z == 0.f) part[0] = z;
         return;
     }
@@ -244,9 +260,9 @@ __global__ __launch_bounds__(256) void attn_kernel(
     // the new position's row of this head is formed here, not read
     const int pnew = rope && split == nact - 1 ? pos - p0 : -1;
 #define HYQ_ATT_LOAD(SB)                                                                       \
-    _Pragma("unroll") for (int j = 0; j < 8; ++j)                                             \
+    _Pragma("unroll") for (int j = 0; j < 2; ++j)                                             \
     {                                                                                          \
-        const int pp = (SB) + r0 + 8 * j;                                                      \
+        const int pp = (SB) + r0 + 16 * j;                                                     \
         if (pp < n && pp != pnew) {                                                            \
             kr[j] = reinterpret_cast<const float4 *>(kbase + (size_t)pp * kvw)[d4];             \
             vr[j] = reinterpret_cast<const float4 *>(vbase + (size_t)pp * kvw)[d4];             \
@@ -254,110 +270,153 @@ __global__ __launch_bounds__(256) void attn_kernel(
             kr[j] = vr[j] = make_float4(0.f, 0.f, 0.f, 0.f);                                   \
         }                                                                                      \
     }
-    if (rope) {
-        const float ang = (float)pos * fr;
-        const float cs = cosf(ang), sn = sinf(ang);
-        if (has_q) {
-            float o0, o1;
-            rope_norm_pair(qa, qb, cs, sn, qn0, qn1, eps, o0, o1);
-            Qs[wave][lane] = o0;
-            Qs[wave][lane + D / 2] = o1;
+    if (wave < ATT_MAX_REP) {
+        if (rope) {
+            const float ang = (float)pos * fr;
+            const float cs = cosf(ang), sn = sinf(ang);
+            if (has_q) {
+                float o0, o1;
+                rope_norm_pair(qa, qb, cs, sn, qn0, qn1, eps, o0, o1);
+                Qs[wave][lane] = o0;
+                Qs[wave][lane + D / 2] = o1;
+            }
+            if (pnew >= 0 && wave == 0) {
+                float o0, o1;
+                rope_norm_pair(ka, kb, cs, sn, kn0, kn1, eps, o0, o1);
+                Kn[lane] = o0;
+                Kn[lane + D / 2] = o1;
+                float *kdst = kcache + (size_t)pos * kvw + (size_t)kh * D;
+                kdst[lane] = o0;
+                kdst[lane + D / 2] = o1;
+            }
+            if (pnew >= 0 && wave == 1) {
+                Vn[lane] = va;
+                Vn[lane + D / 2] = vb;
+                float *vdst = vcache + (size_t)pos * kvw + (size_t)kh * D;
+                vdst[lane] = va;
+                vdst[lane + D / 2] = vb;
+            }
+        } else if (has_q) {
+            Qs[wave][lane] = qa;
+            Qs[wave][lane + D / 2] = qb;
         }
-        if (pnew >= 0 && wave == 0) {
-            float o0, o1;
-            rope_norm_pair(ka, kb, cs, sn, kn0, kn1, eps, o0, o1);
-            Kn[lane] = o0;
-            Kn[lane + D / 2] = o1;
-            float *kdst = kcache + (size_t)pos * kvw + (size_t)kh * D;
-            kdst[lane] = o0;
-            kdst[lane + D / 2] = o1;
-        }
-        if (pnew >= 0 && wave == 1) {
-            Vn[lane] = va;
-            Vn[lane + D / 2] = vb;
-            float *vdst = vcache + (size_t)pos * kvw + (size_t)kh * D;
-            vdst[lane] = va;
-            vdst[lane + D / 2] = vb;
-        }
-    } else if (has_q) {
-        Qs[wave][lane] = qa;
-        Qs[wave][lane + D / 2] = qb;
     }
-    float m_run = -INFINITY, l_run = 0.f, acc0 = 0.f, acc1 = 0.f;
+    // lane roles (see above); heads past `rep` idle
+    const int hl = lane & 3;
+    const bool hq_ok = hl < rep;
+    const int qq = (lane >> 2) & 3;          // score phase: dim quarter
+    const int srow = 4 * wave + (lane >> 4); // score phase: slice row
+    const int vdim = 16 * wave + (lane >> 2); // V phase: output dim
+    float m_run = -INFINITY, l_run = 0.f, acc = 0.f;
     for (int sb = 0; sb < n; sb += ATT_SUB) {
         const int nn = min(ATT_SUB, n - sb);
         __syncthreads(); // the previous slice's readers are done (and Qs/Kn/Vn are ready)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int pp = r0 + 8 * j;
+        for (int j = 0; j < 2; ++j) {
+            const int pp = r0 + 16 * j;
             float4 kv = kr[j], vv = vr[j];
             if (sb + pp >= n) kv = vv = make_float4(0.f, 0.f, 0.f, 0.f);
             if (sb + pp == pnew) {
-                kv = make_float4(Kn[4 * d4], Kn[4 * d4 + 1], Kn[4 * d4 + 2], Kn[4 * d4 + 3]);
-                vv = make_float4(Vn[4 * d4], Vn[4 * d4 + 1], Vn[4 * d4 + 2], Vn[4 * d4 + 3]);
+                kv = *reinterpret_cast<const float4 *>(&Kn[4 * d4]);
+                vv = *reinterpret_cast<const float4 *>(&Vn[4 * d4]);
             }
-            Ks[pp][4 * d4] = kv.x;
-            Ks[pp][4 * d4 + 1] = kv.y;
-            Ks[pp][4 * d4 + 2] = kv.z;
-            Ks[pp][4 * d4 + 3] = kv.w;
+            *reinterpret_cast<float4 *>(&Ks[pp][4 * d4]) = kv;
             *reinterpret_cast<float4 *>(&Vs[pp][4 * d4]) = vv;
         }
         if (sb + ATT_SUB < n) HYQ_ATT_LOAD(sb + ATT_SUB)
         __syncthreads();
-        if (has_q) {
-            float dot = 0.f;
-#pragma unroll 32
-            for (int d = 0; d < D; ++d) dot += Qs[wave][d] * Ks[lane][d];
-            const float sc = lane < nn ? dot * scale : -INFINITY;
-            const float m_new = fmaxf(m_run, wave_max(sc));
-            const float corr = expf(m_run - m_new);
-            const float e = lane < nn ? expf(sc - m_new) : 0.f;
-            l_run = l_run * corr + wave_sum(e);
-            float a0 = acc0 * corr, a1 = acc1 * corr;
-            // every slice row: rows past `nn` hold zeros and have e = 0
+        // scores: four partial dots per lane (explicit fmaf: this file is
+        // compiled without contraction for the decoders), then the quarters
+        // by row_ror
+        float d0 = 0.f, d1 = 0.f, d2 = 0.f, d3 = 0.f;
 #pragma unroll
-            for (int pp = 0; pp < ATT_SUB; ++pp) {
-                const float ep = wave::lane(e, pp);
-                a0 += ep * Vs[pp][lane];
-                a1 += ep * Vs[pp][lane + D / 2];
-            }
-            acc0 = a0;
-            acc1 = a1;
-            m_run = m_new;
+        for (int i = 0; i < D / 16; ++i) {
+            const float4 qv = *reinterpret_cast<const float4 *>(&Qs[hl][4 * qq + 16 * i]);
+            const float4 kv = *reinterpret_cast<const float4 *>(&Ks[srow][4 * qq + 16 * i]);
+            d0 = fmaf(qv.x, kv.x, d0);
+            d1 = fmaf(qv.y, kv.y, d1);
+            d2 = fmaf(qv.z, kv.z, d2);
+            d3 = fmaf(qv.w, kv.w, d3);
         }
+        float dot = (d0 + d1) + (d2 + d3);
+        dot += wave::dpp<wave::DPP_ROR4>(dot);
+        dot += wave::dpp<wave::DPP_ROR8>(dot);
+        const bool live = hq_ok && srow < nn;
+        const float sc = live ? dot * scale : -INFINITY;
+        const float wmax = wave::max_halves(wave::max_rows2(sc));
+        if (lane < ATT_MAX_REP) Red[0][hl][wave] = wmax;
+        __syncthreads();
+        float smax = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < ATT_WAVES; w += 4) {
+            const float4 m4 = *reinterpret_cast<const float4 *>(&Red[0][hl][w]);
+            smax = fmaxf(smax, fmaxf(fmaxf(m4.x, m4.y), fmaxf(m4.z, m4.w)));
+        }
+        const float m_new = fmaxf(m_run, smax);
+        const float corr = expf(m_run - m_new);
+        const float e = live ? expf(sc - m_new) : 0.f;
+        if (qq == 0) Es[hl][srow] = e;
+        const float wsum = wave::sum_halves(wave::sum_rows2(e));
+        if (lane < ATT_MAX_REP) Red[1][hl][wave] = wsum;
+        __syncthreads();
+        float ssum = 0.f;
+#pragma unroll
+        for (int w = 0; w < ATT_WAVES; w += 4) {
+            const float4 s4 = *reinterpret_cast<const float4 *>(&Red[1][hl][w]);
+            ssum += (s4.x + s4.y) + (s4.z + s4.w);
+        }
+        l_run = l_run * corr + ssum;
+        // V over the slice rows (rows past `nn` hold zeros and have e = 0),
+        // even and odd rows in separate sums
+        float ae = 0.f, ao = 0.f;
+#pragma unroll
+        for (int pp = 0; pp < ATT_SUB; pp += 4) {
+            const float4 ev = *reinterpret_cast<const float4 *>(&Es[hl][pp]);
+            ae = fmaf(ev.x, Vs[pp][vdim], ae);
+            ao = fmaf(ev.y, Vs[pp + 1][vdim], ao);
+            ae = fmaf(ev.z, Vs[pp + 2][vdim], ae);
+            ao = fmaf(ev.w, Vs[pp + 3][vdim], ao);
+        }
+        acc = acc * corr + (ae + ao);
+        m_run = m_new;
     }
 #undef HYQ_ATT_LOAD
-    if (has_q) {
-        float *o = part + ((size_t)hq * splits + split) * PART_STRIDE;
-        if (lane == 0) {
+    if (hq_ok) {
+        float *o = part + ((size_t)(kh * rep + hl) * splits + split) * PART_STRIDE;
+        if (wave == 0 && lane < ATT_MAX_REP) {
             o[0] = m_run;
             o[1] = l_run;
         }
-        o[4 + lane] = acc0;
-        o[4 + D / 2 + lane] = acc1;
+        o[4 + vdim] = acc;
     }
 }
 
-// Merge of the splits of one head per workgroup (128 threads = 2 waves, one
-// output dim each): out = sum_s exp(m_s - M) acc_s / sum_s exp(m_s - M) l_s
-// with M = max_s m_s. Lane s of each wave loads split s's (max, exp-sum) and
-// forms its weight; every thread loads its dim of every split slot (slots
-// past `splits` are clamped into bounds, slots past the visible splits are
-// ignored), all as vector loads issued together with the position's, so one
-// memory round trip is paid. The weights reach the accumulation by readlane.
-__global__ __launch_bounds__(128) void attn_merge_kernel(const float *__restrict__ part,
+// Merge of the splits of one head: out = sum_s exp(m_s - M) acc_s /
+// sum_s exp(m_s - M) l_s with M = max_s m_s. Grid (heads, 2), 256 threads:
+// workgroup (h, y) forms dims 64y .. 64y + 63, wave g the splits g, g + 4,
+// ... (lane = dim), and the four waves' sums are added through LDS in a
+// fixed order. Lane s of every wave loads split s's (max, exp-sum) and forms
+// its weight, which reaches the accumulation by readlane. All loads (split
+// slots past `splits` clamped into bounds, slots past the visible splits
+// ignored) are issued together with the position's, so one memory round
+// trip is paid.
+template <int MS>
+__global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict__ part,
                                                          int splits, int chunk,
                                                          const int *__restrict__ pos_p,
                                                          float *__restrict__ out)
 {
-    const int h = blockIdx.x, d = threadIdx.x, lane = d & 63;
+    static_assert(MS % 4 == 0 && MS <= 64, "one split per lane, four waves");
+    __shared__ float red[4][64];
+    const int h = blockIdx.x, lane = threadIdx.x & 63, g = threadIdx.x >> 6;
+    const int d = 64 * blockIdx.y + lane;
     const float *ph = part + (size_t)h * splits * PART_STRIDE;
     const float2 ml =
         *reinterpret_cast<const float2 *>(ph + (size_t)min(lane, splits - 1) * PART_STRIDE);
-    float a[ATT_MAX_SPLITS];
+    float a[MS / 4];
 #pragma unroll
-    for (int s = 0; s < ATT_MAX_SPLITS; ++s)
-        a[s] = ph[(size_t)min(s, splits - 1) * PART_STRIDE + 4 + d];
+    for (int k = 0; k < MS / 4; ++k)
+        a[k] = ph[(size_t)min(g + 4 * k, splits - 1) * PART_STRIDE + 4 + d];
     const int nact = (*pos_p + chunk) / chunk;
     const bool live = lane < nact;
     const float M = wave::max64(live ? ml.x : -INFINITY);
@@ -365,9 +424,11 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(const float *__restrict
     const float den = wave::sum64(w * (live ? ml.y : 0.f));
     float num = 0.f;
 #pragma unroll
-    for (int s = 0; s < ATT_MAX_SPLITS; ++s) // a select, not a branch: the loads stay hoisted
-        num += wave::lane(w, s) * (s < nact ? a[s] : 0.f);
-    out[h * ATT_D + d] = num / den;
+    for (int k = 0; k < MS / 4; ++k) // a select, not a branch: the loads stay hoisted
+        num += wave::lane(w, g + 4 * k) * (g + 4 * k < nact ? a[k] : 0.f);
+    red[g][lane] = num;
+    __syncthreads();
+    if (g == 0) out[h * ATT_D + d] = ((red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane])) / den;
 }
 
 __global__ void zero_u32_kernel(unsigned *p, int n)
@@ -477,7 +538,8 @@ int launch_rope_norm_kv(float *q, const float *k, const float *v, const float *q
 
 int attention_chunk(int context)
 {
-    // ATT_SUB-position multiples, at most ATT_MAX_SPLITS splits
+    // ATT_SUB-position multiples, at most ATT_MAX_SPLITS splits (the merge
+    // holds one split per lane)
     const int per = (context + ATT_MAX_SPLITS - 1) / ATT_MAX_SPLITS;
     return (per + ATT_SUB - 1) / ATT_SUB * ATT_SUB;
 }
@@ -496,26 +558,40 @@ int launch_zero_u32(unsigned *p, int n, void *stream)
     return (int)hipGetLastError();
 }
 
+// The merge, instantiated for the smallest split bound that covers `splits`.
+static void launch_merge(const float *part, int splits, int chunk, int heads, const int *pos,
+                         float *out, hipStream_t st)
+{
+    if (splits <= 16)
+        hipLaunchKernelGGL(attn_merge_kernel<16>, dim3(heads, 2), dim3(256), 0, st, part,
+                           splits, chunk, pos, out);
+    else if (splits <= 32)
+        hipLaunchKernelGGL(attn_merge_kernel<32>, dim3(heads, 2), dim3(256), 0, st, part,
+                           splits, chunk, pos, out);
+    else
+        hipLaunchKernelGGL(attn_merge_kernel<ATT_MAX_SPLITS>, dim3(heads, 2), dim3(256), 0, st,
+                           part, splits, chunk, pos, out);
+}
+
 int launch_attention(const float *q, const float *kcache, const float *vcache, const int *pos,
                      int context, int heads, int kvh, float *part, float *out, void *stream)
 {
     const int splits = attention_splits(context), chunk = attention_chunk(context);
     const float scale = 1.0f / sqrtf(128.0f);
     hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(attn_kernel, dim3(splits, kvh), dim3(256), 0, st, false, q, nullptr,
+    hipLaunchKernelGGL(attn_kernel, dim3(splits, kvh), dim3(ATT_THREADS), 0, st, false, q, nullptr,
                        nullptr, nullptr, nullptr, nullptr, 0.f, const_cast<float *>(kcache),
                        const_cast<float *>(vcache), pos, heads, kvh, scale, part, splits, chunk,
                        context);
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(heads), dim3(128), 0, st, part, splits, chunk, pos,
-                       out);
+    launch_merge(part, splits, chunk, heads, pos, out, st);
     return (int)hipGetLastError();
 }
 
 int launch_attention_merge(const float *part, int context, int heads, const int *pos,
                            float *out, void *stream)
 {
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(heads), dim3(128), 0, (hipStream_t)stream, part,
-                       attention_splits(context), attention_chunk(context), pos, out);
+    launch_merge(part, attention_splits(context), attention_chunk(context), heads, pos, out,
+                 (hipStream_t)stream);
     return (int)hipGetLastError();
 }
 
@@ -526,7 +602,7 @@ int launch_attention_rope(const float *q, const float *k, const float *v, const 
 {
     const int splits = attention_splits(context), chunk = attention_chunk(context);
     const float scale = 1.0f / sqrtf(128.0f);
-    hipLaunchKernelGGL(attn_kernel, dim3(splits, kvh), dim3(256), 0, (hipStream_t)stream, true, q,
+    hipLaunchKernelGGL(attn_kernel, dim3(splits, kvh), dim3(ATT_THREADS), 0, (hipStream_t)stream, true, q,
                        k, v, qn, kn, freq, eps, kcache, vcache, pos, heads, kvh, scale, part,
                        splits, chunk, context);
     return (int)hipGetLastError();

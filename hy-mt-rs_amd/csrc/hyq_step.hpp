@@ -25,9 +25,9 @@ int launch_rope_norm_kv(float *q, const float *k, const float *v, const float *q
 // Attention splits: `chunk` positions each (a multiple of ATT_SUB), at most
 // ATT_MAX_SPLITS; partials are [heads][splits][PART_STRIDE] floats holding
 // (max, exp-sum, -, -, exp-weighted V sum[128]).
-constexpr int ATT_SUB = 64;
+constexpr int ATT_SUB = 32;
 constexpr int ATT_D = 128;
-constexpr int ATT_MAX_SPLITS = 32;
+constexpr int ATT_MAX_SPLITS = 64;
 static_assert(ATT_MAX_SPLITS <= 64, "the merge holds one split per lane of a wave");
 constexpr int ATT_MAX_REP = 4; // query heads per KV head (one per wave)
 constexpr int PART_STRIDE = 132;
@@ -42,8 +42,7 @@ int launch_attention(const float *q, const float *kcache, const float *vcache, c
 int launch_attention_merge(const float *part, int context, int heads, const int *pos,
                            float *out, void *stream);
 // The decode step's attention: RoPE + Q/K norm of the raw projections, KV
-// append at *pos, split partials (merged by the output projection's input
-// stage).
+// append at *pos, split partials (merged by launch_attention_merge).
 int launch_attention_rope(const float *q, const float *k, const float *v, const float *qn,
                           const float *kn, const float *freq, float eps, float *kcache,
                           float *vcache, const int *pos, int context, int heads, int kvh,

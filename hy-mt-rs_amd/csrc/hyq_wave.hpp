@@ -20,6 +20,8 @@ constexpr int DPP_XOR1 = 0xB1;       // quad_perm [1,0,3,2]
 constexpr int DPP_XOR2 = 0x4E;       // quad_perm [2,3,0,1]
 constexpr int DPP_HALF_MIRROR = 0x141;
 constexpr int DPP_MIRROR = 0x140;
+constexpr int DPP_ROR4 = 0x124; // row_ror:4, lane i of a row reads lane (i - 4) mod 16
+constexpr int DPP_ROR8 = 0x128; // row_ror:8
 
 template <int CTRL> __device__ __forceinline__ float dpp(float v)
 {
@@ -76,6 +78,59 @@ __device__ __forceinline__ float max64(float v)
 {
     v = max16(v);
     return fmaxf(fmaxf(lane(v, 0), lane(v, 16)), fmaxf(lane(v, 32), lane(v, 48)));
+}
+
+// v_permlane16_swap / v_permlane32_swap of v with itself. swap16: `even`
+// holds each 32-lane half's even 16-lane row in both of its rows, `odd` its
+// odd row; swap32: `lo` holds lanes 0..31 in both halves, `hi` lanes 32..63.
+// The second operand is an opaque copy (empty asm) because the compiler
+// folds a swap of a value with itself to that value.
+__device__ __forceinline__ void swap16(int v, int &even, int &odd)
+{
+    int u = v;
+    asm volatile("" : "+v"(u));
+    const auto r = __builtin_amdgcn_permlane16_swap(v, u, false, false);
+    even = r[0];
+    odd = r[1];
+}
+__device__ __forceinline__ void swap32(int v, int &lo, int &hi)
+{
+    int u = v;
+    asm volatile("" : "+v"(u));
+    const auto r = __builtin_amdgcn_permlane32_swap(v, u, false, false);
+    lo = r[0];
+    hi = r[1];
+}
+// Sums / maxima over lanes i and i ^ 16 (sum_rows2), i and i ^ 32 (sum_halves)
+__device__ __forceinline__ float sum_rows2(float v)
+{
+    int e, o;
+    swap16(__builtin_bit_cast(int, v), e, o);
+    return __builtin_bit_cast(float, e) + __builtin_bit_cast(float, o);
+}
+__device__ __forceinline__ int sum_rows2(int v)
+{
+    int e, o;
+    swap16(v, e, o);
+    return e + o;
+}
+__device__ __forceinline__ float max_rows2(float v)
+{
+    int e, o;
+    swap16(__builtin_bit_cast(int, v), e, o);
+    return fmaxf(__builtin_bit_cast(float, e), __builtin_bit_cast(float, o));
+}
+__device__ __forceinline__ float sum_halves(float v)
+{
+    int l, h;
+    swap32(__builtin_bit_cast(int, v), l, h);
+    return __builtin_bit_cast(float, l) + __builtin_bit_cast(float, h);
+}
+__device__ __forceinline__ float max_halves(float v)
+{
+    int l, h;
+    swap32(__builtin_bit_cast(int, v), l, h);
+    return fmaxf(__builtin_bit_cast(float, l), __builtin_bit_cast(float, h));
 }
 
 } // namespace wave
