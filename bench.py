@@ -10,15 +10,23 @@ whole forward pass plus argmax); warmup W and timed K steps run at positions
 1024 .. 1024+W+K-1 (128 positions at the defaults).
 
 Also reported, from live HIP-event timings on the context stream:
-  roofline      the GEMV kernel with the largest time share of a decode
-                step, measured over the decode step's own weights;
-  gemv          GB/s of every matrix of the GEMV workloads (Q4_K [6144x2048];
-                the 1.8B Q2_0C/STQ1_0 set; Q6_K lm_head), weights rotated
-                over >= 1 GiB so that reads come from HBM, not the 256 MB
-                Infinity Cache;
-  cpu_baseline  the reference's x86 decode step (f32 activations, scalar
-                Q2_0C row dot, AVX2 dot; oracle/hyq_oracle_step.c), timed on
-                this host's cores on a bounded sample of the same workload.
+  roofline        the kernel with the largest time share of a decode step (the
+                  down-projection GEMV, Q2_0C [2048 x 6144] with its f32 input
+                  stage) launched alone through the C ABI as the very
+                  instantiation the step launches, weights rotated over 512 MiB
+                  and inputs over 64 rows so that both come from HBM:
+                  algorithmic bytes per launch / average launch time; `traffic`
+                  is the counter-measured HBM bytes per launch of the same
+                  kernel (profiles/*_traffic.json);
+  step_hbm        the bytes a token streams (weights + KV cache) / time per token;
+  decode_kernels  the step's other kernels timed the same way;
+  gemv            GB/s of every matrix of the GEMV workloads (Q4_K [6144x2048];
+                  the 1.8B Q2_0C/STQ1_0 set; Q6_K lm_head), Q8 input, weights
+                  rotated over >= 512 MiB;
+  prefill, moe    the batched f16-MFMA GEMM (TFLOP/s) and the MoE expert layer;
+  cpu_baseline    the reference's x86 decode step (f32 activations, scalar
+                  Q2_0C row dot, AVX2 dot; oracle/hyq_oracle_step.c), timed on
+                  this host's cores on a bounded sample of the same workload.
 """
 from __future__ import annotations
 
@@ -36,6 +44,7 @@ sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 HBM_PEAK_GBS = 8000.0
+ROOFLINE_PROFILE = "down_gemv_q2c_2048x6144"
 METRIC = "decode tok/s 1.8B Q2_0C; quant GEMV HBM GB/s as % of ~8 TB/s peak"
 PREFILLED = 1024
 
@@ -72,11 +81,11 @@ class Events:
         return ms.value / iters
 
 
-def gemv_rate(hyq, ctx, ev, dtype, rows, cols, seed=1, min_bytes=1 << 30):
+def gemv_rate(hyq, ctx, ev, dtype, rows, cols, seed=1, min_bytes=512 << 20):
     """Standalone int8 GEMV: (us per launch, algorithmic GB/s), HBM-resident."""
     from synth import random_matrix
     base = random_matrix(dtype, rows, cols, seed=seed)
-    copies = int(min(64, max(1, np.ceil(min_bytes / base.size))))
+    copies = int(min(1024, max(2, np.ceil(min_bytes / base.size))))
     Ws = [ctx.upload(dtype, base, (cols, rows)) for _ in range(copies)]
     x = np.random.default_rng(seed).normal(0, 1, cols).astype(np.float32)
     q8 = ctx.q8(cols)
@@ -163,50 +172,124 @@ def moe_rate(hyq, ctx, ev, tokens=64, experts=64, used=8, hidden=2048, mid=1536,
                 frac=round(wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
 
 
-def decode_kernel_table(hyq, ctx, ev, dec_weights, model):
-    """Per-launch time of each GEMV of the decode step over the model's own 32
-    layers of weights (the step's memory behaviour), plus its time per step."""
+def _upload_rotation(ctx, dtype, blobs, dims, min_bytes):
+    """Device copies of the given GGUF blobs, cycled until they hold >= min_bytes."""
+    out, total, i = [], 0, 0
+    while total < min_bytes or i < len(blobs):
+        b = blobs[i % len(blobs)]
+        out.append(ctx.upload(dtype, b, dims))
+        total += b.size
+        i += 1
+    return out
+
+
+def step_kernel_table(hyq, ctx, ev, model, kv, pos):
+    """Per-launch time (HIP events on the context stream) of the decode step's
+    kernels launched in isolation through the C ABI, each with its operands
+    rotated over more memory than the 256 MB Infinity Cache holds (512 MiB of
+    weights, 64 inputs), so that they
+    come from HBM as they do in the step (a token streams ~0.8 GB).
+
+    `same_kernel` marks rows whose ABI call launches the very instantiation the
+    step launches (same format, shape, input stage and preload depth); the
+    others are the nearest ABI path (noted in `launch`)."""
+    c = model["cfg"]
+    L = hyq.lib()
+    H, F, D = c["hidden"], c["ffn"], c["head_dim"]
+    QL, KVW = c["heads"] * D, c["kv_heads"] * D
+    lin = model["linear"]
+    rng = np.random.default_rng(1)
+    table = {}
+
+    def staged_gemv(name, key, rows, cols, per_step, note, min_bytes=512 << 20):
+        blobs = [model["layers"][l][key] for l in range(c["layers"])]
+        Ws = _upload_rotation(ctx, lin, blobs, (cols, rows), min_bytes)
+        xs = [ctx.array(rng.normal(0, 1, cols).astype(np.float32)) for _ in range(64)]
+        y = ctx.empty(rows, np.float32)
+        n = len(Ws)
+
+        def launch(i):
+            L.hyq_matmul_d(ctx.handle, Ws[i % n].handle, xs[i % 64].ptr, 1, y.ptr)
+
+        ms = ev.time_ms(launch, 2 * n)
+        alg = blobs[0].size + 4 * cols + 4 * rows
+        table[name] = dict(us=round(ms * 1e3, 3), bytes=int(alg), per_step=per_step,
+                           GBs=round(alg / (ms * 1e-3) / 1e9, 1),
+                           us_per_step=round(ms * 1e3 * per_step, 2), same_kernel=True,
+                           launch=note)
+        for W in Ws:
+            W.release()
+
+    staged_gemv("down", "down", H, F, c["layers"],
+                "hyq_matmul_d batch 1: Q2_0C [2048 x 6144], f32 input quantized in the "
+                "launch (the step adds the residual in the same kernel)")
+    staged_gemv("attn_output", "o", H, QL, c["layers"],
+                "hyq_matmul_d batch 1: Q2_0C [2048 x 2048], f32 input quantized in the launch")
+
+    # attention (+ split merge) over the prefilled cache at the bench's positions
+    ctxlen = kv[0].shape[1]
+    ks = [ctx.array(np.ascontiguousarray(kv[0][l % c["layers"]])) for l in range(64)]
+    vs = [ctx.array(np.ascontiguousarray(kv[1][l % c["layers"]])) for l in range(64)]
+    qd = ctx.array(rng.normal(0, 1, QL).astype(np.float32))
+    posd = ctx.array(np.array([pos], np.int32))
+    scratch = ctx.empty(L.hyq_attention_scratch_floats(ctxlen, c["heads"]), np.float32)
+    out = ctx.empty(QL, np.float32)
+
+    def att(i):
+        L.hyq_attention_d(ctx.handle, qd.ptr, ks[i % 64].ptr, vs[i % 64].ptr, posd.ptr, ctxlen,
+                          c["heads"], c["kv_heads"], D, scratch.ptr, out.ptr, None)
+
+    ms = ev.time_ms(att, 256)
+    alg = 2 * (pos + 1) * KVW * 4 + QL * 4 + QL * 4
+    table["attention"] = dict(us=round(ms * 1e3, 3), bytes=int(alg), per_step=c["layers"],
+                              GBs=round(alg / (ms * 1e-3) / 1e9, 1),
+                              us_per_step=round(ms * 1e3 * c["layers"], 2), same_kernel=False,
+                              launch="hyq_attention_d: split attention + merge (the step's "
+                                     "attention kernel also applies RoPE, the q/k norms and the "
+                                     "KV append)")
+    del ks, vs
+
+    # lm_head: the tied Q6_K matrix (203 MB), two copies alternating
+    E = [ctx.upload(model["embed_dtype"], model["embed"], (H, c["vocab"])) for _ in range(2)]
+    xs = [ctx.array(rng.normal(0, 1, H).astype(np.float32)) for _ in range(2)]
+    yl = ctx.empty(c["vocab"], np.float32)
+
+    def head(i):
+        L.hyq_matmul_d(ctx.handle, E[i % 2].handle, xs[i % 2].ptr, 1, yl.ptr)
+
+    ms = ev.time_ms(head, 40)
+    alg = model["embed"].size + 4 * H + 4 * c["vocab"]
+    table["lm_head"] = dict(us=round(ms * 1e3, 3), bytes=int(alg), per_step=1,
+                            GBs=round(alg / (ms * 1e-3) / 1e9, 1), us_per_step=round(ms * 1e3, 2),
+                            same_kernel=False,
+                            launch="hyq_matmul_d batch 1: Q6_K [120818 x 2048], f32 input "
+                                   "quantized in the launch (the step also applies the output "
+                                   "RMSNorm in it)")
+    for W in E:
+        W.release()
+    return table
+
+
+def roofline_loop(hyq, ctx, ev, model, iters):
+    """The roofline kernel alone (for counter runs): the down-projection GEMV
+    as step_kernel_table times it, then one 256 MiB device copy whose HBM
+    traffic is known (the scale of the FETCH_SIZE / WRITE_SIZE counters)."""
     c = model["cfg"]
     L = hyq.lib()
     H, F = c["hidden"], c["ffn"]
-    QL = c["heads"] * c["head_dim"]
-    KV = c["kv_heads"] * c["head_dim"]
-    q8h, q8a, q8f = ctx.q8(H), ctx.q8(QL), ctx.q8(F)
-    rng = np.random.default_rng(0)
-    for q8, n in ((q8h, H), (q8a, QL), (q8f, F)):
-        q8.quantize_into(ctx.array(rng.normal(0, 1, n).astype(np.float32)).ptr)
-    yq, yk, yv = ctx.empty(QL, np.float32), ctx.empty(KV, np.float32), ctx.empty(KV, np.float32)
-    yh, yf = ctx.empty(H, np.float32), ctx.empty(F, np.float32)
-    yl = ctx.empty(c["vocab"], np.float32)
-    layers = dec_weights["layers"]
-    n = len(layers)
-    b = lambda key: model["layers"][0][key].size  # noqa: E731
-    rows = {
-        "gemv_qkv": (lambda i: L.hyq_gemv_qkv_q8_d(ctx.handle, layers[i % n]["q"].handle,
-                                                   layers[i % n]["k"].handle,
-                                                   layers[i % n]["v"].handle, q8h.handle,
-                                                   yq.ptr, yk.ptr, yv.ptr),
-                     b("q") + b("k") + b("v") + H + 4 * H // 256 + 4 * (QL + 2 * KV), n),
-        "gemv_attn_out": (lambda i: L.hyq_gemv_q8_d(ctx.handle, layers[i % n]["o"].handle,
-                                                    q8a.handle, yh.ptr, yh.ptr),
-                          b("o") + QL + 4 * QL // 256 + 8 * H, n),
-        "gemv_gate_up_silu": (lambda i: L.hyq_gate_up_silu_q8_d(
-            ctx.handle, layers[i % n]["gate"].handle, layers[i % n]["up"].handle, q8h.handle,
-            yf.ptr), b("gate") + b("up") + H + 4 * H // 256 + 4 * F, n),
-        "gemv_down": (lambda i: L.hyq_gemv_q8_d(ctx.handle, layers[i % n]["down"].handle,
-                                                q8f.handle, yh.ptr, yh.ptr),
-                      b("down") + F + 4 * F // 256 + 8 * H, n),
-        "gemv_lm_head": (lambda i: L.hyq_gemv_q8_d(ctx.handle, dec_weights["embed"].handle,
-                                                   q8h.handle, None, yl.ptr),
-                         model["embed"].size + H + 4 * H // 256 + 4 * c["vocab"], 1),
-    }
-    table = {}
-    for name, (fn, alg, per_step) in rows.items():
-        ms = ev.time_ms(fn, 4 * n if per_step > 1 else 40)
-        table[name] = dict(us=round(ms * 1e3, 3), bytes=int(alg), per_step=per_step,
-                           GBs=round(alg / (ms * 1e-3) / 1e9, 1),
-                           us_per_step=round(ms * 1e3 * per_step, 2))
-    return table
+    rng = np.random.default_rng(1)
+    blobs = [model["layers"][l]["down"] for l in range(c["layers"])]
+    Ws = _upload_rotation(ctx, model["linear"], blobs, (F, H), 512 << 20)
+    xs = [ctx.array(rng.normal(0, 1, F).astype(np.float32)) for _ in range(64)]
+    y = ctx.empty(H, np.float32)
+    n = len(Ws)
+    ms = ev.time_ms(lambda i: L.hyq_matmul_d(ctx.handle, Ws[i % n].handle, xs[i % 64].ptr, 1,
+                                             y.ptr), iters)
+    nb = 256 << 20
+    a, b = ctx.empty(nb, np.uint8), ctx.empty(nb, np.uint8)
+    hyq.check(L.hyq_memcpy_d2d(ctx.handle, b.ptr, a.ptr, nb))
+    ctx.sync()
+    return ms * 1e3
 
 
 def cpu_baseline(model, kv, steps: int):
@@ -239,6 +322,9 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the batched (prefill) GEMM table")
     ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="run only the roofline kernel loop and a 256 MiB copy (for hardware "
+                         "counter runs), print its time and exit")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the step's kernels one by one instead of replaying a HIP "
                          "graph (for profilers that cannot follow graph capture)")
@@ -248,8 +334,8 @@ def main() -> int:
               "(the path has no multi-GPU runtime in this build)", file=sys.stderr)
         return 2
     import __graft_entry__ as ge
-    from synth import DENSE_1P8B, Q2_0C, Q4_K, Q6_K, STQ1_0, load_dense, make_dense_model, \
-        make_kv_cache
+    from synth import DENSE_1P8B, Q2_0C, Q4_K, Q6_K, STQ1_0, dense_weight_bytes, load_dense, \
+        make_dense_model, make_kv_cache
 
     hyq = ge.package()
     cfg = DENSE_1P8B
@@ -260,6 +346,11 @@ def main() -> int:
 
     ctx = hyq.Context(0)
     ev = Events(ctx.stream)
+    if args.roofline_only:
+        us = roofline_loop(hyq, ctx, ev, model, max(args.steps, 64))
+        print(json.dumps({"kernel": "down", "avg_us": round(us, 3)}), flush=True)
+        ctx.close()
+        return 0
     dec = load_dense(hyq, ctx, model, context)
     for l in range(cfg["layers"]):
         dec.load_kv(l, kv[0][l, :PREFILLED], kv[1][l, :PREFILLED])
@@ -273,25 +364,27 @@ def main() -> int:
     tok_s = args.steps / dt
     log(f"decode: {tok_s:.1f} tok/s ({dt / args.steps * 1e3:.3f} ms/token)")
 
-    # kernel table over the decode step's own weights
-    dec_weights = dict(layers=[], embed=None)
-    keep = dec._keep
-    for l in range(cfg["layers"]):
-        q, k, v, o, g, u, d = keep[7 * l:7 * l + 7]
-        dec_weights["layers"].append(dict(q=q, k=k, v=v, o=o, gate=g, up=u, down=d))
-    dec_weights["embed"] = keep[7 * cfg["layers"]]
-    table = decode_kernel_table(hyq, ctx, ev, dec_weights, model)
-    dom = max(table, key=lambda n: table[n]["us_per_step"])
+    # the step's kernels, each timed alone with HBM-resident operands
+    table = step_kernel_table(hyq, ctx, ev, model, kv, PREFILLED + args.warmup)
+    dom = max((n for n in table if table[n]["same_kernel"]),
+              key=lambda n: table[n]["us_per_step"])
     dk = table[dom]
     achieved = dk["bytes"] / (dk["us"] * 1e-6) / 1e9
     traffic = None
-    tf = os.path.join(ROOT, "profiles", f"{dom}_traffic.json")
+    tf = os.path.join(ROOT, "profiles", f"{ROOFLINE_PROFILE}_traffic.json")
     if os.path.exists(tf):
         with open(tf) as f:
             traffic = json.load(f).get("bytes_per_launch")
-    roofline = dict(kernel=dom, bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS,
-                    unit="GB/s", frac=round(achieved / HBM_PEAK_GBS, 4), traffic=traffic,
-                    algorithmic_bytes=dk["bytes"], avg_us=dk["us"])
+    roofline = dict(kernel=f"{dom}: {dk['launch']}", bound="hbm", achieved=round(achieved, 1),
+                    peak=HBM_PEAK_GBS, unit="GB/s", frac=round(achieved / HBM_PEAK_GBS, 4),
+                    traffic=traffic, algorithmic_bytes=dk["bytes"], avg_us=dk["us"])
+    # the whole step against the same peak: bytes a token streams from HBM
+    kvw = cfg["kv_heads"] * cfg["head_dim"]
+    mid = PREFILLED + args.warmup + args.steps // 2
+    step_bytes = dense_weight_bytes(model) + cfg["layers"] * 2 * (mid + 1) * kvw * 4
+    step = dict(bytes_per_token=int(step_bytes),
+                GBs=round(step_bytes * tok_s / 1e9, 1),
+                frac=round(step_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4))
 
     gemv = {}
     if not args.no_gemv:
@@ -349,6 +442,7 @@ def main() -> int:
                    "graph": use_graph},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "step_hbm": step,
         "decode_kernels": table,
         "gemv": gemv,
         "prefill": prefill,
