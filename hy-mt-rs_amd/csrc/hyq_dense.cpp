@@ -172,6 +172,12 @@ struct hyq_dense {
     float *freq = nullptr, *hidden = nullptr, *qb = nullptr, *kb = nullptr, *vb = nullptr;
     float *gb = nullptr, *logits = nullptr, *att_scratch = nullptr, *argmax_scratch = nullptr;
     float *att_out = nullptr; // merged attention output [heads * head_dim]
+    // The down projection runs as `down_ks` K slices writing partial rows
+    // [down_ks][hidden]; the next layer's QKV stage (or the lm_head's) adds
+    // them to the hidden row it normalizes, and the attention output adds
+    // them to its residual, which materializes the hidden row again.
+    float *parts = nullptr;
+    int down_ks = 1;
     int32_t *token = nullptr, *history = nullptr;
     StepState *state = nullptr;
     size_t history_cap = 0;
@@ -205,6 +211,15 @@ namespace {
 // residual add), the gate/up GEMV (RMSNorm + Q8, SiLU product) and the down
 // GEMV (Q8 of the SiLU row, residual add) - then the lm_head GEMV (output
 // RMSNorm + Q8) and the argmax.
+// K slices of the down projection: the most (up to GEMV_MAX_PARTS) that
+// leave every slice at least 8 whole groups (one per sub-lane).
+int down_kslices(int groups)
+{
+    for (int k = GEMV_MAX_PARTS; k > 1; --k)
+        if (groups % k == 0 && groups / k >= 8) return k;
+    return 1;
+}
+
 GemvArgs staged(const hyq_weight *w, const float *xin, const float *norm, float eps, float *y,
                 const float *residual)
 {
@@ -229,10 +244,16 @@ int enqueue_step(hyq_dense *m)
                                 m->hidden, st),
                "embed_row");
     const int *pos = &m->state->pos;
+    const int ks = m->down_ks;
     for (int l = 0; l < c.layers; ++l) {
         const hyq_dense::Layer &L = m->layers[l];
+        // the previous layer's down projection left `ks` partial rows
+        const int np = l > 0 && ks > 1 ? ks : 0;
         {
             GemvArgs a = staged(L.q, m->hidden, L.attn_norm, c.rms_eps, m->qb, nullptr);
+            a.sparts = m->parts;
+            a.nsparts = np;
+            a.parts_stride = c.hidden;
             const hyq_weight *ws[3] = {L.q, L.k, L.v};
             float *ys[3] = {m->qb, m->kb, m->vb};
             int start = 0;
@@ -254,24 +275,37 @@ int enqueue_step(hyq_dense *m)
         HYQ_LAUNCH(launch_attention_merge(m->att_scratch, (int)m->context, c.heads, pos,
                                           m->att_out, st),
                    "attention_merge");
-        HYQ_LAUNCH(launch_gemv(L.o->dtype, GEMV_PLAIN,
-                               staged(L.o, m->att_out, nullptr, 0.f, m->hidden, m->hidden), st),
-                   "gemv_attn_output");
+        {
+            GemvArgs a = staged(L.o, m->att_out, nullptr, 0.f, m->hidden, m->hidden);
+            a.rparts = m->parts;
+            a.nrparts = np;
+            a.parts_stride = c.hidden;
+            HYQ_LAUNCH(launch_gemv(L.o->dtype, GEMV_PLAIN, a, st), "gemv_attn_output");
+        }
         {
             GemvArgs a = staged(L.gate, m->hidden, L.ffn_norm, c.rms_eps, m->gb, nullptr);
             a.nseg = 2;
             a.seg[1].w = L.up->view;
             HYQ_LAUNCH(launch_gemv(L.gate->dtype, GEMV_SILU, a, st), "gemv_gate_up_silu");
         }
-        HYQ_LAUNCH(launch_gemv(L.down->dtype, GEMV_PLAIN,
-                               staged(L.down, m->gb, nullptr, 0.f, m->hidden, m->hidden), st),
-                   "gemv_down");
+        if (ks > 1) {
+            GemvArgs a = staged(L.down, m->gb, nullptr, 0.f, m->parts, nullptr);
+            a.groups /= ks;
+            a.kslices = ks;
+            HYQ_LAUNCH(launch_gemv(L.down->dtype, GEMV_PLAIN, a, st), "gemv_down");
+        } else {
+            HYQ_LAUNCH(launch_gemv(L.down->dtype, GEMV_PLAIN,
+                                   staged(L.down, m->gb, nullptr, 0.f, m->hidden, m->hidden), st),
+                       "gemv_down");
+        }
     }
-    HYQ_LAUNCH(launch_gemv(m->output->dtype, GEMV_PLAIN,
-                           staged(m->output, m->hidden, m->output_norm, c.rms_eps, m->logits,
-                                  nullptr),
-                           st),
-               "gemv_lm_head");
+    {
+        GemvArgs a = staged(m->output, m->hidden, m->output_norm, c.rms_eps, m->logits, nullptr);
+        a.sparts = m->parts;
+        a.nsparts = c.layers > 0 && ks > 1 ? ks : 0;
+        a.parts_stride = c.hidden;
+        HYQ_LAUNCH(launch_gemv(m->output->dtype, GEMV_PLAIN, a, st), "gemv_lm_head");
+    }
     HYQ_LAUNCH(launch_argmax(m->logits, c.vocab, m->argmax_scratch,
                              (int *)(m->argmax_scratch + 64), m->token, m->state, m->history, st),
                "argmax");
@@ -340,6 +374,7 @@ int hyq_dense_create(hyq_ctx *ctx, const hyq_dense_config *cfg, size_t context, 
     const size_t o_g = take(F), o_logits = take(V);
     const size_t o_att = take((size_t)attention_splits((int)context) * c.heads * PART_STRIDE);
     const size_t o_att_out = take(QL);
+    const size_t o_parts = take((size_t)GEMV_MAX_PARTS * H);
     const size_t o_arg = take(128), o_tok = take(4), o_state = take(4);
     rc = m->mem.alloc(ctx->device, off);
     if (rc) return rc;
@@ -362,6 +397,8 @@ int hyq_dense_create(hyq_ctx *ctx, const hyq_dense_config *cfg, size_t context, 
     m->logits = (float *)(base + o_logits);
     m->att_scratch = (float *)(base + o_att);
     m->att_out = (float *)(base + o_att_out);
+    m->parts = (float *)(base + o_parts);
+    m->down_ks = down_kslices((int)(F / 256));
     m->argmax_scratch = (float *)(base + o_arg);
     m->token = (int32_t *)(base + o_tok);
     m->state = (StepState *)(base + o_state);

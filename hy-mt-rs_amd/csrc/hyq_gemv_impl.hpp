@@ -53,7 +53,13 @@ constexpr int STAGE_PASSES = 4;
 struct StageRegs {
     float4 x[STAGE_PASSES][2];
     float4 w[STAGE_PASSES][2];
+    float4 pt[GEMV_MAX_PARTS][2]; // partial rows of pass 0 (rows of <= 8 groups)
 };
+
+__device__ __forceinline__ float4 add4(float4 v, float4 p)
+{
+    return make_float4(v.x + p.x, v.y + p.y, v.z + p.z, v.w + p.w);
+}
 
 __device__ __forceinline__ float sum_rows(float v) { return wave::sum_rows2(v); }
 __device__ __forceinline__ int sum_rows(int v) { return wave::sum_rows2(v); }
@@ -120,11 +126,12 @@ __device__ __forceinline__ float finish_norm(const float *gss, int groups, float
 // (loads complete in issue order, so the stage then waits for its own data
 // only) and consumed by stage_regs.
 template <int IN>
-__device__ __forceinline__ void stage_load(const GemvArgs &a, StageRegs &r)
+__device__ __forceinline__ void stage_load(const GemvArgs &a, const float *xin, const float *norm,
+                                           StageRegs &r)
 {
     const int hw = threadIdx.x >> 5, c = threadIdx.x & 31;
-    const float4 *x4 = reinterpret_cast<const float4 *>(a.xin);
-    const float4 *n4 = reinterpret_cast<const float4 *>(a.norm);
+    const float4 *x4 = reinterpret_cast<const float4 *>(xin);
+    const float4 *n4 = reinterpret_cast<const float4 *>(norm);
 #pragma unroll
     for (int p = 0; p < STAGE_PASSES; ++p) {
         const int g = 8 * p + hw;
@@ -137,14 +144,32 @@ __device__ __forceinline__ void stage_load(const GemvArgs &a, StageRegs &r)
             }
         }
     }
+    if (a.nsparts > 0 && hw < a.groups) {
+#pragma unroll
+        for (int k = 0; k < GEMV_MAX_PARTS; ++k)
+            if (k < a.nsparts) {
+                const float4 *p4 =
+                    reinterpret_cast<const float4 *>(a.sparts + (size_t)k * a.parts_stride);
+                r.pt[k][0] = p4[hw * 64 + 2 * c];
+                r.pt[k][1] = p4[hw * 64 + 2 * c + 1];
+            }
+    }
 }
 
 template <int IN>
-__device__ __forceinline__ void stage_regs(const GemvArgs &a, const StageRegs &r, int *slots,
+__device__ __forceinline__ void stage_regs(const GemvArgs &a, StageRegs &r, int *slots,
                                            float *sc, int *s256, int *s16, int *s32, float *gss)
 {
     const int hw = threadIdx.x >> 5, c = threadIdx.x & 31;
     const int groups = a.groups;
+    if (a.nsparts > 0 && hw < groups) {
+#pragma unroll
+        for (int k = 0; k < GEMV_MAX_PARTS; ++k)
+            if (k < a.nsparts) {
+                r.x[0][0] = add4(r.x[0][0], r.pt[k][0]);
+                r.x[0][1] = add4(r.x[0][1], r.pt[k][1]);
+            }
+    }
     float scale = 1.f;
     if (IN == 2) {
 #pragma unroll
@@ -173,23 +198,37 @@ __device__ __forceinline__ void stage_regs(const GemvArgs &a, const StageRegs &r
 
 // Longer rows: a loop over the passes (loads at the top of each).
 template <int IN>
-__device__ __forceinline__ void stage_loop(const GemvArgs &a, int *slots, float *sc, int *s256,
-                                           int *s16, int *s32, float *gss)
+__device__ __forceinline__ void stage_loop(const GemvArgs &a, const float *xin, const float *norm,
+                                           int *slots, float *sc, int *s256, int *s16, int *s32,
+                                           float *gss)
 {
     const int hw = threadIdx.x >> 5, c = threadIdx.x & 31;
     const int groups = a.groups;
-    const float4 *x4 = reinterpret_cast<const float4 *>(a.xin);
-    const float4 *n4 = reinterpret_cast<const float4 *>(a.norm);
+    const float4 *x4 = reinterpret_cast<const float4 *>(xin);
+    const float4 *n4 = reinterpret_cast<const float4 *>(norm);
+    // the input pair of lane c of group g, with the partial rows added
+    auto input = [&](int g, float4 &va, float4 &vb) {
+        va = x4[g * 64 + 2 * c];
+        vb = x4[g * 64 + 2 * c + 1];
+        for (int k = 0; k < a.nsparts; ++k) {
+            const float4 *p4 = reinterpret_cast<const float4 *>(a.sparts + (size_t)k * a.parts_stride);
+            va = add4(va, p4[g * 64 + 2 * c]);
+            vb = add4(vb, p4[g * 64 + 2 * c + 1]);
+        }
+    };
     float scale = 1.f;
     if (IN == 2) {
         for (int g = hw; g < groups; g += 8) {
-            const float ss = sum_rows(wave::sum16(sq8(x4[g * 64 + 2 * c], x4[g * 64 + 2 * c + 1])));
+            float4 va, vb;
+            input(g, va, vb);
+            const float ss = sum_rows(wave::sum16(sq8(va, vb)));
             if (c == 0) gss[g] = ss;
         }
         scale = finish_norm(gss, groups, a.eps);
     }
     for (int g = hw; g < groups; g += 8) {
-        float4 va = x4[g * 64 + 2 * c], vb = x4[g * 64 + 2 * c + 1];
+        float4 va, vb;
+        input(g, va, vb);
         if (IN == 2) {
             va = scale_by(va, scale, n4[g * 64 + 2 * c]);
             vb = scale_by(vb, scale, n4[g * 64 + 2 * c + 1]);
@@ -218,6 +257,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     const int rset = lane >> 3;
     const int nwaves = blockDim.x >> 6;
     const int row0 = ((blockIdx.x * nwaves + wave) * 8 + rset) * NR;
+    // K slice of this workgroup row (kslices > 1: plain mode, f32 input
+    // without norm or partial rows): groups [gbase, gbase + groups)
+    const int gbase = blockIdx.y * groups;
+    const float *xin = a.xin + (size_t)gbase * 256;
 
     // Resolve each row of this lane to (segment, local row).
     int seg[NR], lrow[NR];
@@ -246,8 +289,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
 #pragma unroll
         for (int i = 0; i < NR; ++i) {
             const WView &w = MODE == GEMV_MULTI ? a.seg[seg[i]].w : a.seg[0].w;
-            G::load(d[i], w, lrowc[i], g);
-            if (MODE == GEMV_SILU) G::load(d2[i], a.seg[1].w, lrowc[i], g);
+            G::load(d[i], w, lrowc[i], gbase + g);
+            if (MODE == GEMV_SILU) G::load(d2[i], a.seg[1].w, lrowc[i], gbase + g);
         }
     };
     // The activation row's loads are issued first, then the weights' (which
@@ -260,9 +303,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     // others load at the top of their iteration.
     StageRegs sr;
     i32x4 qv[Q8_REG];
-    const bool stage_reg = IN != 0 && groups <= 8 * STAGE_PASSES;
+    const bool stage_reg = IN != 0 && groups <= 8 * STAGE_PASSES && (a.nsparts == 0 || groups <= 8);
     const bool q8_reg = IN == 0 && groups * 16 <= Q8_REG * (int)blockDim.x;
-    if (IN != 0 && stage_reg) stage_load<IN>(a, sr);
+    if (IN != 0 && stage_reg) stage_load<IN>(a, xin, a.norm, sr);
     if (IN == 0 && q8_reg) {
         // clamped into bounds; the copy to LDS keeps the in-range ones
         const i32x4 *src = reinterpret_cast<const i32x4 *>(a.x.q);
@@ -274,7 +317,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     typename G::Data dp[P > 0 ? P : 1];
     if (P > 0) {
 #pragma unroll
-        for (int u = 0; u < P; ++u) G::load(dp[u], a.seg[0].w, lrowc[0], min(sub + 8 * u, groups - 1));
+        for (int u = 0; u < P; ++u)
+            G::load(dp[u], a.seg[0].w, lrowc[0], gbase + min(sub + 8 * u, groups - 1));
     } else {
         load_group(min(sub, groups - 1));
     }
@@ -300,7 +344,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
         int *s32 = s16 + groups * 16;
         float *gss = reinterpret_cast<float *>(s32 + groups * 8);
         if (stage_reg) stage_regs<IN>(a, sr, lds, sc, s256, s16, s32, gss);
-        else stage_loop<IN>(a, lds, sc, s256, s16, s32, gss);
+        else stage_loop<IN>(a, xin, a.norm, lds, sc, s256, s16, s32, gss);
         xq.s = sc;
         xq.sum256 = s256;
         xq.sum16 = s16;
@@ -363,7 +407,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
         } else if (MODE == GEMV_MULTI) {
             a.seg[seg[i]].y[lrow[i]] = v;
         } else {
-            a.seg[0].y[lrow[i]] = a.residual ? a.residual[lrow[i]] + v : v;
+            if (a.kslices > 1) {
+                a.seg[0].y[(size_t)blockIdx.y * a.rows_total + lrow[i]] = v;
+            } else {
+                float r = a.residual ? a.residual[lrow[i]] : 0.f;
+#pragma unroll
+                for (int k = 0; k < GEMV_MAX_PARTS; ++k)
+                    if (k < a.nrparts) r += a.rparts[(size_t)k * a.parts_stride + lrow[i]];
+                a.seg[0].y[lrow[i]] = a.residual || a.nrparts ? r + v : v;
+            }
         }
     }
 }
@@ -424,7 +476,13 @@ template <int F> int launch_gemv_format(int mode, const GemvArgs &a, void *strea
     // so fewer, wider workgroups (4 waves) share that work.
     if (a.xin) waves = 4;
     const int rows_per_block = 8 * nr * waves;
-    dim3 grid((rows + rows_per_block - 1) / rows_per_block), block(64 * waves);
+    const int ks = a.kslices > 1 ? a.kslices : 1;
+    // a K split is a plain GEMV of an f32 row without norm, residual or
+    // partial-row inputs (each slice writes its own partial row)
+    if (ks > 1 && (mode != GEMV_PLAIN || !a.xin || a.norm || a.residual || a.nsparts || a.nrparts))
+        return (int)hipErrorInvalidValue;
+    if (a.nsparts > GEMV_MAX_PARTS || a.nrparts > GEMV_MAX_PARTS) return (int)hipErrorInvalidValue;
+    dim3 grid((rows + rows_per_block - 1) / rows_per_block, ks), block(64 * waves);
     // slots, then (input stage) scales, 256/16/32-value sums and group sums of squares
     const size_t lds = (size_t)a.groups * SLOT_INTS * 4 +
                        (a.xin ? (size_t)a.groups * (4 + 4 + 64 + 32 + 4) : 0);

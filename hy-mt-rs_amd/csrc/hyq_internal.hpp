@@ -117,7 +117,22 @@ struct GemvArgs {
     const float *xin;
     const float *norm;
     float eps;
+    // K split (plain mode with an f32 input stage): kslices > 1 launches
+    // kslices workgroup rows; row s covers groups [s*groups, (s+1)*groups) of
+    // every matrix row and writes its partial product to
+    // seg[0].y + s * rows_total (no residual).
+    int kslices;
+    // Partial rows (a K split's output) added, in order, to the f32 input of
+    // the stage (sparts) and to the residual of the epilogue (rparts):
+    // ((v + p[0]) + p[1]) + ... with p[k] = parts + k * parts_stride; at most
+    // GEMV_MAX_PARTS of them.
+    const float *sparts;
+    int nsparts;
+    const float *rparts;
+    int nrparts;
+    int parts_stride;
 };
+constexpr int GEMV_MAX_PARTS = 4;
 
 // Kernel launchers (defined in the .hip files). All return hipError_t as int.
 int launch_repack(int fmt, const uint8_t *gguf, size_t nblocks, int nb_per_row, uint8_t *p0,
