@@ -11,14 +11,18 @@ whole forward pass plus argmax); warmup W and timed K steps run at positions
 
 Also reported, from live HIP-event timings on the context stream:
   roofline        the kernel with the largest time share of a decode step (the
-                  down-projection GEMV, Q2_0C [2048 x 6144] with its f32 input
-                  stage) launched alone through the C ABI as the very
-                  instantiation the step launches, weights rotated over 512 MiB
-                  and inputs over 64 rows so that both come from HBM:
+                  Q2_0C GEMV with its f32 input stage that the step runs for the
+                  attention output and, as three K slices, for the down
+                  projection), launched alone through the C ABI as the very
+                  instantiation the step launches, on the attention-output
+                  shape [2048 x 2048], weights rotated over 512 MiB and inputs
+                  over 64 rows so that both come from HBM:
                   algorithmic bytes per launch / average launch time; `traffic`
                   is the counter-measured HBM bytes per launch of the same
                   kernel (profiles/*_traffic.json);
   step_hbm        the bytes a token streams (weights + KV cache) / time per token;
+  device_copy_GBs (in roofline) a 1 GiB device-to-device copy's read + write
+                  bytes / time, the practical HBM ceiling beside the peak;
   decode_kernels  the step's other kernels timed the same way;
   gemv            GB/s of every matrix of the GEMV workloads (Q4_K [6144x2048];
                   the 1.8B Q2_0C/STQ1_0 set; Q6_K lm_head), Q8 input, weights
@@ -44,7 +48,7 @@ sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 HBM_PEAK_GBS = 8000.0
-ROOFLINE_PROFILE = "down_gemv_q2c_2048x6144"
+ROOFLINE_PROFILE = "attn_out_gemv_q2c_2048x2048"
 METRIC = "decode tok/s 1.8B Q2_0C; quant GEMV HBM GB/s as % of ~8 TB/s peak"
 PREFILLED = 1024
 
@@ -201,7 +205,7 @@ def step_kernel_table(hyq, ctx, ev, model, kv, pos):
     rng = np.random.default_rng(1)
     table = {}
 
-    def staged_gemv(name, key, rows, cols, per_step, note, min_bytes=512 << 20):
+    def staged_gemv(name, key, rows, cols, per_step, note, min_bytes=512 << 20, same=True):
         blobs = [model["layers"][l][key] for l in range(c["layers"])]
         Ws = _upload_rotation(ctx, lin, blobs, (cols, rows), min_bytes)
         xs = [ctx.array(rng.normal(0, 1, cols).astype(np.float32)) for _ in range(64)]
@@ -215,16 +219,19 @@ def step_kernel_table(hyq, ctx, ev, model, kv, pos):
         alg = blobs[0].size + 4 * cols + 4 * rows
         table[name] = dict(us=round(ms * 1e3, 3), bytes=int(alg), per_step=per_step,
                            GBs=round(alg / (ms * 1e-3) / 1e9, 1),
-                           us_per_step=round(ms * 1e3 * per_step, 2), same_kernel=True,
+                           us_per_step=round(ms * 1e3 * per_step, 2), same_kernel=same,
                            launch=note)
         for W in Ws:
             W.release()
 
+    staged_gemv("attn_output", "o", H, QL, 4 * c["layers"],
+                "hyq_matmul_d batch 1: Q2_0C [2048 x 2048], f32 input quantized in the launch; "
+                "the step launches this kernel for the attention output (+ residual) and, as "
+                "three K slices of 2048, for the down projection (per_step counts both, in "
+                "units of this launch's work)")
     staged_gemv("down", "down", H, F, c["layers"],
-                "hyq_matmul_d batch 1: Q2_0C [2048 x 6144], f32 input quantized in the "
-                "launch (the step adds the residual in the same kernel)")
-    staged_gemv("attn_output", "o", H, QL, c["layers"],
-                "hyq_matmul_d batch 1: Q2_0C [2048 x 2048], f32 input quantized in the launch")
+                "hyq_matmul_d batch 1: Q2_0C [2048 x 6144] as one launch (the step splits it "
+                "into three K slices of the attention-output kernel instead)", same=False)
 
     # attention (+ split merge) over the prefilled cache at the bench's positions
     ctxlen = kv[0].shape[1]
@@ -270,17 +277,29 @@ def step_kernel_table(hyq, ctx, ev, model, kv, pos):
     return table
 
 
+def copy_rate(hyq, ctx, ev, nbytes=1 << 30):
+    """Device-to-device copy bandwidth on the context stream (read + write
+    bytes / time), the practical HBM ceiling beside the 8 TB/s peak."""
+    L = hyq.lib()
+    a, b = ctx.empty(nbytes, np.uint8), ctx.empty(nbytes, np.uint8)
+    ms = ev.time_ms(lambda i: hyq.check(L.hyq_memcpy_d2d(ctx.handle, b.ptr, a.ptr, nbytes)), 10)
+    a.free()
+    b.free()
+    return dict(bytes=2 * nbytes, ms=round(ms, 4), GBs=round(2 * nbytes / (ms * 1e-3) / 1e9, 1))
+
+
 def roofline_loop(hyq, ctx, ev, model, iters):
-    """The roofline kernel alone (for counter runs): the down-projection GEMV
+    """The roofline kernel alone (for counter runs): the attention-output GEMV
     as step_kernel_table times it, then one 256 MiB device copy whose HBM
     traffic is known (the scale of the FETCH_SIZE / WRITE_SIZE counters)."""
     c = model["cfg"]
     L = hyq.lib()
-    H, F = c["hidden"], c["ffn"]
+    H = c["hidden"]
+    QL = c["heads"] * c["head_dim"]
     rng = np.random.default_rng(1)
-    blobs = [model["layers"][l]["down"] for l in range(c["layers"])]
-    Ws = _upload_rotation(ctx, model["linear"], blobs, (F, H), 512 << 20)
-    xs = [ctx.array(rng.normal(0, 1, F).astype(np.float32)) for _ in range(64)]
+    blobs = [model["layers"][l]["o"] for l in range(c["layers"])]
+    Ws = _upload_rotation(ctx, model["linear"], blobs, (QL, H), 512 << 20)
+    xs = [ctx.array(rng.normal(0, 1, QL).astype(np.float32)) for _ in range(64)]
     y = ctx.empty(H, np.float32)
     n = len(Ws)
     ms = ev.time_ms(lambda i: L.hyq_matmul_d(ctx.handle, Ws[i % n].handle, xs[i % 64].ptr, 1,
@@ -348,7 +367,7 @@ def main() -> int:
     ev = Events(ctx.stream)
     if args.roofline_only:
         us = roofline_loop(hyq, ctx, ev, model, max(args.steps, 64))
-        print(json.dumps({"kernel": "down", "avg_us": round(us, 3)}), flush=True)
+        print(json.dumps({"kernel": "attn_output", "avg_us": round(us, 3)}), flush=True)
         ctx.close()
         return 0
     dec = load_dense(hyq, ctx, model, context)
@@ -378,6 +397,8 @@ def main() -> int:
     roofline = dict(kernel=f"{dom}: {dk['launch']}", bound="hbm", achieved=round(achieved, 1),
                     peak=HBM_PEAK_GBS, unit="GB/s", frac=round(achieved / HBM_PEAK_GBS, 4),
                     traffic=traffic, algorithmic_bytes=dk["bytes"], avg_us=dk["us"])
+    copy = copy_rate(hyq, ctx, ev)
+    roofline["device_copy_GBs"] = copy["GBs"]
     # the whole step against the same peak: bytes a token streams from HBM
     kvw = cfg["kv_heads"] * cfg["head_dim"]
     mid = PREFILLED + args.warmup + args.steps // 2

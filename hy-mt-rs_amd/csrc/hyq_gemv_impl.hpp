@@ -244,19 +244,32 @@ constexpr int Q8_REG = 8;
 // registers here)
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
+// Half-group mode (HALF_GEMV<F, NR, MODE, IN>): 16 lanes share a row and
+// each 256-weight group goes to two of them (lane 2i + h takes half h of
+// group i + 8k), so a workgroup covers 16 rows with half the per-lane work;
+// the two halves' integer sums meet by DPP before the group's one float
+// product, which keeps the result bit-identical to the full-group mode.
+template <int F, int NR, int MODE, int IN>
+constexpr bool HALF_GEMV = HasHalf<F>::value && IN != 0 && NR == 1 && MODE != GEMV_ISUMS;
+
 template <int F, int NR, int MODE, int IN, int P>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
 {
     using G = typename GroupOf<F>::T;
+    constexpr bool H = HALF_GEMV<F, NR, MODE, IN>;
+    using Dt = typename GemvData<G, H>::T;
+    constexpr int SUBL = H ? 16 : 8; // lanes per row
     extern __shared__ int lds[];
 
     const int groups = a.groups;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int sub = lane & 7;
-    const int rset = lane >> 3;
+    const int sub = lane & (SUBL - 1);
+    const int gi = H ? sub >> 1 : sub; // first group of this lane
+    const int hh = H ? sub & 1 : 0;    // half of the group (half-group mode)
+    const int rset = lane / SUBL;
     const int nwaves = blockDim.x >> 6;
-    const int row0 = ((blockIdx.x * nwaves + wave) * 8 + rset) * NR;
+    const int row0 = ((blockIdx.x * nwaves + wave) * (64 / SUBL) + rset) * NR;
     // K slice of this workgroup row (kslices > 1: plain mode, f32 input
     // without norm or partial rows): groups [gbase, gbase + groups)
     const int gbase = blockIdx.y * groups;
@@ -283,14 +296,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
 #pragma unroll
     for (int i = 0; i < NR; ++i) lrowc[i] = valid[i] ? lrow[i] : 0;
 
-    typename G::Data d[NR];
-    typename G::Data d2[MODE == GEMV_SILU ? NR : 1];
+    auto load = [&](Dt &D, const WView &w, int row, int g) {
+        if constexpr (H) G::load_half(D, w, row, gbase + g, hh);
+        else G::load(D, w, row, gbase + g);
+    };
+    Dt d[NR];
+    Dt d2[MODE == GEMV_SILU ? NR : 1];
     auto load_group = [&](int g) {
 #pragma unroll
         for (int i = 0; i < NR; ++i) {
             const WView &w = MODE == GEMV_MULTI ? a.seg[seg[i]].w : a.seg[0].w;
-            G::load(d[i], w, lrowc[i], gbase + g);
-            if (MODE == GEMV_SILU) G::load(d2[i], a.seg[1].w, lrowc[i], gbase + g);
+            load(d[i], w, lrowc[i], g);
+            if (MODE == GEMV_SILU) load(d2[i], a.seg[1].w, lrowc[i], g);
         }
     };
     // The activation row's loads are issued first, then the weights' (which
@@ -314,13 +331,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
             qv[j] = src[min((int)threadIdx.x + j * (int)blockDim.x, groups * 16 - 1)];
     }
     static_assert(P == 0 || (NR == 1 && MODE == GEMV_PLAIN), "preload: plain, one row per lane");
-    typename G::Data dp[P > 0 ? P : 1];
+    Dt dp[P > 0 ? P : 1];
     if (P > 0) {
 #pragma unroll
-        for (int u = 0; u < P; ++u)
-            G::load(dp[u], a.seg[0].w, lrowc[0], gbase + min(sub + 8 * u, groups - 1));
+        for (int u = 0; u < P; ++u) load(dp[u], a.seg[0].w, lrowc[0], min(gi + 8 * u, groups - 1));
     } else {
-        load_group(min(sub, groups - 1));
+        load_group(min(gi, groups - 1));
     }
     Q8View xq = a.x;
     if (IN == 0) {
@@ -357,10 +373,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
 #pragma unroll
     for (int i = 0; i < NR; ++i) acc[i] = acc2[i] = 0.f;
 
-    auto stage_act = [&](int g, int (&act)[64]) {
-        const int4 *s4 = reinterpret_cast<const int4 *>(lds + g * SLOT_INTS);
+    // the lane's activation dwords of group g: the whole slot (64), or half
+    // hh of it (32) in half-group mode
+    constexpr int NACT = H ? 32 : 64;
+    auto stage_act = [&](int g, int (&act)[NACT]) {
+        const int4 *s4 = reinterpret_cast<const int4 *>(lds + g * SLOT_INTS + hh * 32);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
+        for (int j = 0; j < NACT / 4; ++j) {
             const int4 v = s4[j];
             act[4 * j] = v.x;
             act[4 * j + 1] = v.y;
@@ -368,30 +387,46 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
             act[4 * j + 3] = v.w;
         }
     };
+    // acc plus group g's contribution of one matrix row. Half-group mode:
+    // the two halves' integer sums meet by DPP and lane hh == 0 accumulates
+    // the group (as the full-group mode of the same format does, one fused
+    // multiply-add per group), lane hh == 1 keeps zero.
+    auto accum = [&](float acc, const Dt &D, const int (&act)[NACT], int g) -> float {
+        if constexpr (H) {
+            int is = G::isum_half(D, act, xq, g, hh);
+            is += wave::dpp<wave::DPP_XOR1>(is);
+            const float r = G::finish_acc(acc, is, D.d, xq, g);
+            return hh ? acc : r;
+        } else if constexpr (HasHalf<F>::value) {
+            return G::dot_acc(acc, D, act, xq, g);
+        } else {
+            return acc + G::template dot<false>(D, act, xq, g, nullptr);
+        }
+    };
     if (P > 0) {
 #pragma unroll
         for (int u = 0; u < P; ++u) {
-            const int g = sub + 8 * u;
+            const int g = gi + 8 * u;
+            // (uniform over each pair of half lanes, so the DPP partner is live)
             if (g >= groups || !valid[0]) continue;
-            int act[64];
+            int act[NACT];
             stage_act(g, act);
-            acc[0] += G::template dot<false>(dp[u], act, xq, g, nullptr);
+            acc[0] = accum(acc[0], dp[u], act, g);
         }
     } else {
-        for (int g = sub; g < groups; g += 8) {
-            int act[64];
+        for (int g = gi; g < groups; g += 8) {
+            int act[NACT];
             stage_act(g, act);
-            if (g != sub) load_group(g);
+            if (g != gi) load_group(g);
 #pragma unroll
             for (int i = 0; i < NR; ++i) {
                 if (!valid[i]) continue;
-                if (MODE == GEMV_ISUMS) {
+                if constexpr (MODE == GEMV_ISUMS && !H) {
                     int32_t *out = a.isums + ((size_t)lrow[i] * groups + g) * G::ISUMS;
                     acc[i] += G::template dot<true>(d[i], act, xq, g, out);
                 } else {
-                    acc[i] += G::template dot<false>(d[i], act, xq, g, nullptr);
-                    if (MODE == GEMV_SILU)
-                        acc2[i] += G::template dot<false>(d2[i], act, xq, g, nullptr);
+                    acc[i] = accum(acc[i], d[i], act, g);
+                    if (MODE == GEMV_SILU) acc2[i] = accum(acc2[i], d2[i], act, g);
                 }
             }
         }
@@ -399,8 +434,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
 
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
-        const float v = reduce8(acc[i]);
-        const float v2 = MODE == GEMV_SILU ? reduce8(acc2[i]) : 0.f;
+        const float v = H ? wave::sum16(acc[i]) : reduce8(acc[i]);
+        const float v2 = MODE == GEMV_SILU ? (H ? wave::sum16(acc2[i]) : reduce8(acc2[i])) : 0.f;
         if (sub != 0 || !valid[i] || MODE == GEMV_ISUMS) continue;
         if (MODE == GEMV_SILU) {
             a.seg[0].y[lrow[i]] = silu_mul(v, v2);
@@ -475,7 +510,9 @@ template <int F> int launch_gemv_format(int mode, const GemvArgs &a, void *strea
     // With an f32 input stage every workgroup quantizes the whole input row,
     // so fewer, wider workgroups (4 waves) share that work.
     if (a.xin) waves = 4;
-    const int rows_per_block = 8 * nr * waves;
+    // half-group mode (Q2_0C, f32 stage, one row per lane): 4 rows per wave
+    const bool half = HasHalf<F>::value && a.xin && nr == 1 && mode != GEMV_ISUMS;
+    const int rows_per_block = (half ? 4 : 8) * nr * waves;
     const int ks = a.kslices > 1 ? a.kslices : 1;
     // a K split is a plain GEMV of an f32 row without norm, residual or
     // partial-row inputs (each slice writes its own partial row)

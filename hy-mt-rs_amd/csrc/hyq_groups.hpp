@@ -103,6 +103,78 @@ struct GroupQ2C {
         if (EMIT) out[0] = isum;
         return (float)isum * (h2f(D.d) * x.s[g]);
     }
+
+    // Half of a group (weights 128h .. 128h + 127: code units 2h, 2h + 1) for
+    // the GEMV that gives each 256-weight group to two lanes. A half's
+    // integer sum 2 sum(c q) - 3 sum(q) over its 128 values adds exactly to
+    // the group's, so the two halves' sums are added (as integers) before
+    // the one float product of `finish`, which is the whole group's.
+    struct Half {
+        uint4 w[2];
+        uint16_t d;
+        __device__ __forceinline__ void hold_all()
+        {
+            hold(w[0]);
+            hold(w[1]);
+            hold(d);
+        }
+    };
+    __device__ __forceinline__ static void load_half(Half &D, const WView &w, int row, int g,
+                                                     int h)
+    {
+        size_t blk = (size_t)row * w.nb + (g >> 1);
+        const uint4 *p = reinterpret_cast<const uint4 *>(w.p0 + blk * 128 + (g & 1) * 64);
+        D.w[0] = p[2 * h];
+        D.w[1] = p[2 * h + 1];
+        D.d = reinterpret_cast<const uint16_t *>(w.p1)[blk];
+    }
+    // act: the half's 32 activation dwords (values 128h .. 128h + 127)
+    __device__ __forceinline__ static int isum_half(const Half &Din, const int *act,
+                                                    const Q8View &x, int g, int h)
+    {
+        Half D = Din;
+        D.hold_all();
+        int raw = 0;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const uint32_t c[4] = {D.w[u].x, D.w[u].y, D.w[u].z, D.w[u].w};
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                raw = sdot4(c[m] & 0x03030303u, act[16 * u + m], raw);
+                raw = sdot4((c[m] >> 2) & 0x03030303u, act[16 * u + 4 + m], raw);
+                raw = sdot4((c[m] >> 4) & 0x03030303u, act[16 * u + 8 + m], raw);
+                raw = sdot4((c[m] >> 6) & 0x03030303u, act[16 * u + 12 + m], raw);
+            }
+        }
+        const int *s32 = x.sum32 + g * 8 + 4 * h;
+        return 2 * raw - 3 * ((s32[0] + s32[1]) + (s32[2] + s32[3]));
+    }
+    // acc + f32(isum) * (d * s_g) as one fused multiply-add, the form both
+    // GEMV modes accumulate groups in
+    __device__ __forceinline__ static float finish_acc(float acc, int isum, uint16_t d,
+                                                       const Q8View &x, int g)
+    {
+        return fmaf(h2f(d) * x.s[g], (float)isum, acc);
+    }
+    __device__ __forceinline__ static float dot_acc(float acc, const Data &Din, const int *act,
+                                                    const Q8View &x, int g)
+    {
+        Data D = Din;
+        D.hold_all();
+        int raw = 0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t c[4] = {D.w[u].x, D.w[u].y, D.w[u].z, D.w[u].w};
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                raw = sdot4(c[m] & 0x03030303u, act[16 * u + m], raw);
+                raw = sdot4((c[m] >> 2) & 0x03030303u, act[16 * u + 4 + m], raw);
+                raw = sdot4((c[m] >> 4) & 0x03030303u, act[16 * u + 8 + m], raw);
+                raw = sdot4((c[m] >> 6) & 0x03030303u, act[16 * u + 12 + m], raw);
+            }
+        }
+        return finish_acc(acc, 2 * raw - 3 * x.sum256[g], D.d, x, g);
+    }
 };
 
 // ---------------------------------------------------------------------------
@@ -398,6 +470,11 @@ struct GroupQ80 {
 };
 
 template <int F> struct GroupOf;
+// Formats whose GEMV can give each group to two lanes (GroupX::Half).
+template <int F> struct HasHalf { static constexpr bool value = false; };
+template <> struct HasHalf<Q2_0C> { static constexpr bool value = true; };
+template <class G, bool H> struct GemvData { using T = typename G::Data; };
+template <class G> struct GemvData<G, true> { using T = typename G::Half; };
 template <> struct GroupOf<Q2_0C> { using T = GroupQ2C; };
 template <> struct GroupOf<STQ1_0> { using T = GroupSTQ; };
 template <> struct GroupOf<Q4_K> { using T = GroupQ4K; };
