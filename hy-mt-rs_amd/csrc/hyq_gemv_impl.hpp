@@ -249,14 +249,15 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 // group i + 8k), so a workgroup covers 16 rows with half the per-lane work;
 // the two halves' integer sums meet by DPP before the group's one float
 // product, which keeps the result bit-identical to the full-group mode.
+constexpr int HALF_MAX_WORKGROUPS = 256;
 template <int F, int NR, int MODE, int IN>
 constexpr bool HALF_GEMV = HasHalf<F>::value && IN != 0 && NR == 1 && MODE != GEMV_ISUMS;
 
-template <int F, int NR, int MODE, int IN, int P>
+template <int F, int NR, int MODE, int IN, int P, bool H>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
 {
+    static_assert(!H || HALF_GEMV<F, NR, MODE, IN>, "half-group mode: see HALF_GEMV");
     using G = typename GroupOf<F>::T;
-    constexpr bool H = HALF_GEMV<F, NR, MODE, IN>;
     using Dt = typename GemvData<G, H>::T;
     constexpr int SUBL = H ? 16 : 8; // lanes per row
     extern __shared__ int lds[];
@@ -455,39 +456,55 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     }
 }
 
-template <int F, int MODE, int IN>
+template <int F, int MODE, int IN, bool H>
 int launch_nr(int nr, int pre, const GemvArgs &a, dim3 grid, dim3 block, size_t lds,
               hipStream_t st)
 {
-    if constexpr (MODE == GEMV_PLAIN) {
-        if (nr == 1) switch (pre) {
-        case 1: hipLaunchKernelGGL((gemv_kernel<F, 1, MODE, IN, 1>), grid, block, lds, st, a); break;
-        case 2: hipLaunchKernelGGL((gemv_kernel<F, 1, MODE, IN, 2>), grid, block, lds, st, a); break;
-        case 3: hipLaunchKernelGGL((gemv_kernel<F, 1, MODE, IN, 3>), grid, block, lds, st, a); break;
-        case 4: hipLaunchKernelGGL((gemv_kernel<F, 1, MODE, IN, 4>), grid, block, lds, st, a); break;
-        default: hipLaunchKernelGGL((gemv_kernel<F, 1, MODE, IN, 0>), grid, block, lds, st, a); break;
+    if constexpr (H) {
+        // half-group kernels: one row per lane (preloads in plain mode)
+        if constexpr (MODE == GEMV_PLAIN) {
+            switch (pre) {
+            case 1: hipLaunchKernelGGL((gemv_kernel<F, 1, MODE, IN, 1, true>), grid, block, lds, st, a); break;
+            case 2: hipLaunchKernelGGL((gemv_kernel<F, 1, MODE, IN, 2, true>), grid, block, lds, st, a); break;
+            case 3: hipLaunchKernelGGL((gemv_kernel<F, 1, MODE, IN, 3, true>), grid, block, lds, st, a); break;
+            case 4: hipLaunchKernelGGL((gemv_kernel<F, 1, MODE, IN, 4, true>), grid, block, lds, st, a); break;
+            default: hipLaunchKernelGGL((gemv_kernel<F, 1, MODE, IN, 0, true>), grid, block, lds, st, a); break;
+            }
+        } else {
+            hipLaunchKernelGGL((gemv_kernel<F, 1, MODE, IN, 0, true>), grid, block, lds, st, a);
         }
-        if (nr == 1) return (int)hipGetLastError();
+        return (int)hipGetLastError();
+    } else {
+        if constexpr (MODE == GEMV_PLAIN) {
+            if (nr == 1) switch (pre) {
+            case 1: hipLaunchKernelGGL((gemv_kernel<F, 1, MODE, IN, 1, false>), grid, block, lds, st, a); break;
+            case 2: hipLaunchKernelGGL((gemv_kernel<F, 1, MODE, IN, 2, false>), grid, block, lds, st, a); break;
+            case 3: hipLaunchKernelGGL((gemv_kernel<F, 1, MODE, IN, 3, false>), grid, block, lds, st, a); break;
+            case 4: hipLaunchKernelGGL((gemv_kernel<F, 1, MODE, IN, 4, false>), grid, block, lds, st, a); break;
+            default: hipLaunchKernelGGL((gemv_kernel<F, 1, MODE, IN, 0, false>), grid, block, lds, st, a); break;
+            }
+            if (nr == 1) return (int)hipGetLastError();
+        }
+        switch (nr) {
+        case 1: hipLaunchKernelGGL((gemv_kernel<F, 1, MODE, IN, 0, false>), grid, block, lds, st, a); break;
+        case 2: hipLaunchKernelGGL((gemv_kernel<F, 2, MODE, IN, 0, false>), grid, block, lds, st, a); break;
+        default: hipLaunchKernelGGL((gemv_kernel<F, 4, MODE, IN, 0, false>), grid, block, lds, st, a); break;
+        }
+        return (int)hipGetLastError();
     }
-    switch (nr) {
-    case 1: hipLaunchKernelGGL((gemv_kernel<F, 1, MODE, IN, 0>), grid, block, lds, st, a); break;
-    case 2: hipLaunchKernelGGL((gemv_kernel<F, 2, MODE, IN, 0>), grid, block, lds, st, a); break;
-    default: hipLaunchKernelGGL((gemv_kernel<F, 4, MODE, IN, 0>), grid, block, lds, st, a); break;
-    }
-    return (int)hipGetLastError();
 }
 
-template <int F, int IN>
+template <int F, int IN, bool H>
 int launch_in(int mode, int nr, int pre, const GemvArgs &a, dim3 grid, dim3 block, size_t lds,
               hipStream_t st)
 {
     switch (mode) {
-    case GEMV_PLAIN: return launch_nr<F, GEMV_PLAIN, IN>(nr, pre, a, grid, block, lds, st);
-    case GEMV_SILU: return launch_nr<F, GEMV_SILU, IN>(nr, 0, a, grid, block, lds, st);
-    case GEMV_MULTI: return launch_nr<F, GEMV_MULTI, IN>(nr, 0, a, grid, block, lds, st);
+    case GEMV_PLAIN: return launch_nr<F, GEMV_PLAIN, IN, H>(nr, pre, a, grid, block, lds, st);
+    case GEMV_SILU: return launch_nr<F, GEMV_SILU, IN, H>(nr, 0, a, grid, block, lds, st);
+    case GEMV_MULTI: return launch_nr<F, GEMV_MULTI, IN, H>(nr, 0, a, grid, block, lds, st);
     default:
-        if (IN != 0) return (int)hipErrorInvalidValue;
-        return launch_nr<F, GEMV_ISUMS, 0>(1, 0, a, grid, block, lds, st);
+        if (IN != 0 || H) return (int)hipErrorInvalidValue;
+        return launch_nr<F, GEMV_ISUMS, 0, false>(1, 0, a, grid, block, lds, st);
     }
 }
 
@@ -510,10 +527,14 @@ template <int F> int launch_gemv_format(int mode, const GemvArgs &a, void *strea
     // With an f32 input stage every workgroup quantizes the whole input row,
     // so fewer, wider workgroups (4 waves) share that work.
     if (a.xin) waves = 4;
-    // half-group mode (Q2_0C, f32 stage, one row per lane): 4 rows per wave
-    const bool half = HasHalf<F>::value && a.xin && nr == 1 && mode != GEMV_ISUMS;
-    const int rows_per_block = (half ? 4 : 8) * nr * waves;
     const int ks = a.kslices > 1 ? a.kslices : 1;
+    // half-group mode (Q2_0C, f32 stage, one row per lane; 4 rows per wave)
+    // when its workgroups (twice the full-group count) still fit the 256 CUs
+    // one each: a CU holding two would be the launch's tail
+    const int half_wgs = (rows + 4 * waves - 1) / (4 * waves) * ks;
+    const bool half = HasHalf<F>::value && a.xin && nr == 1 && mode != GEMV_ISUMS &&
+                      half_wgs <= HALF_MAX_WORKGROUPS;
+    const int rows_per_block = (half ? 4 : 8) * nr * waves;
     // a K split is a plain GEMV of an f32 row without norm, residual or
     // partial-row inputs (each slice writes its own partial row)
     if (ks > 1 && (mode != GEMV_PLAIN || !a.xin || a.norm || a.residual || a.nsparts || a.nrparts))
@@ -526,9 +547,15 @@ template <int F> int launch_gemv_format(int mode, const GemvArgs &a, void *strea
     // groups per lane preloaded by the plain one-row-per-lane kernel
     const int pre = a.groups <= 32 ? (a.groups + 7) / 8 : 0;
     hipStream_t st = (hipStream_t)stream;
-    if (!a.xin) return launch_in<F, 0>(mode, nr, pre, a, grid, block, lds, st);
-    if (!a.norm) return launch_in<F, 1>(mode, nr, pre, a, grid, block, lds, st);
-    return launch_in<F, 2>(mode, nr, pre, a, grid, block, lds, st);
+    if (!a.xin) return launch_in<F, 0, false>(mode, nr, pre, a, grid, block, lds, st);
+    if constexpr (HasHalf<F>::value) {
+        if (half) {
+            if (!a.norm) return launch_in<F, 1, true>(mode, nr, pre, a, grid, block, lds, st);
+            return launch_in<F, 2, true>(mode, nr, pre, a, grid, block, lds, st);
+        }
+    }
+    if (!a.norm) return launch_in<F, 1, false>(mode, nr, pre, a, grid, block, lds, st);
+    return launch_in<F, 2, false>(mode, nr, pre, a, grid, block, lds, st);
 }
 
 } // namespace hyq
