@@ -339,6 +339,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     } else {
         load_group(min(gi, groups - 1));
     }
+    // the plain epilogue's residual and partial rows, loaded now (after the
+    // weights', so that nothing waits for them) rather than at the end
+    float res[GEMV_MAX_PARTS + 1][NR];
+    if (MODE == GEMV_PLAIN && (a.residual || a.nrparts)) {
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            res[0][i] = a.residual ? a.residual[lrowc[i]] : 0.f;
+#pragma unroll
+            for (int k = 0; k < GEMV_MAX_PARTS; ++k)
+                if (k < a.nrparts) res[k + 1][i] = a.rparts[(size_t)k * a.parts_stride + lrowc[i]];
+        }
+    }
     Q8View xq = a.x;
     if (IN == 0) {
         const int4 *src = reinterpret_cast<const int4 *>(a.x.q);
@@ -446,10 +458,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
             if (a.kslices > 1) {
                 a.seg[0].y[(size_t)blockIdx.y * a.rows_total + lrow[i]] = v;
             } else {
-                float r = a.residual ? a.residual[lrow[i]] : 0.f;
+                float r = res[0][i];
 #pragma unroll
                 for (int k = 0; k < GEMV_MAX_PARTS; ++k)
-                    if (k < a.nrparts) r += a.rparts[(size_t)k * a.parts_stride + lrow[i]];
+                    if (k < a.nrparts) r += res[k + 1][i];
                 a.seg[0].y[lrow[i]] = a.residual || a.nrparts ? r + v : v;
             }
         }
