@@ -69,6 +69,8 @@ SIGNATURES = {
     "hyq_rope_norm_append_d": (I, [P, P, P, P, P, P, P, P, SZ, SZ, SZ, ctypes.c_float, P, P]),
     "hyq_attention_scratch_floats": (SZ, [SZ, SZ]),
     "hyq_attention_d": (I, [P, P, P, P, P, SZ, SZ, SZ, SZ, P, P, P]),
+    "hyq_attention_rows_scratch_floats": (SZ, [SZ, SZ, SZ]),
+    "hyq_attention_rows_d": (I, [P, P, P, P, P, SZ, SZ, SZ, SZ, SZ, P, P]),
     "hyq_argmax_d": (I, [P, P, SZ, P, P]),
     "hyq_dense_create": (I, [P, P, SZ, ctypes.POINTER(P)]),
     "hyq_dense_destroy": (None, [P]),
@@ -78,6 +80,8 @@ SIGNATURES = {
     "hyq_dense_set_position": (I, [P, SZ]),
     "hyq_dense_get_position": (I, [P, ctypes.POINTER(SZ)]),
     "hyq_dense_forward": (I, [P, ctypes.c_int32, P, P]),
+    "hyq_dense_prefill": (I, [P, P, SZ, P, P]),
+    "hyq_dense_read_kv": (I, [P, I, SZ, P, P]),
     "hyq_dense_generate": (I, [P, ctypes.c_int32, SZ, I, P]),
 }
 
@@ -432,6 +436,25 @@ class DenseDecoder:
                                       _ptr(logits) if logits is not None else None,
                                       ctypes.byref(nxt)))
         return logits, nxt.value
+
+    def prefill(self, tokens, want_logits: bool = True):
+        """Model::prefill_into (src/model.rs:630-646): the prompt in chunks of
+        up to 256 tokens; returns (last logits or None, greedy next token)."""
+        toks = np.ascontiguousarray(tokens, np.int32)
+        logits = np.empty(self.cfg.vocab, np.float32) if want_logits else None
+        nxt = ctypes.c_int32()
+        check(lib().hyq_dense_prefill(self.handle, _ptr(toks) if toks.size else None, toks.size,
+                                      _ptr(logits) if logits is not None else None,
+                                      ctypes.byref(nxt)))
+        return logits, nxt.value
+
+    def read_kv(self, layer: int, positions: int):
+        """Cached keys and values [positions, kv_heads*head_dim] of one layer."""
+        kvw = self.cfg.kv_heads * self.cfg.head_dim
+        keys = np.empty((positions, kvw), np.float32)
+        values = np.empty((positions, kvw), np.float32)
+        check(lib().hyq_dense_read_kv(self.handle, layer, positions, _ptr(keys), _ptr(values)))
+        return keys, values
 
     def generate(self, token: int, steps: int, use_graph: bool = True) -> np.ndarray:
         out = np.empty(steps, np.int32)

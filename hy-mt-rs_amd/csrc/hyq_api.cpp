@@ -549,7 +549,7 @@ int hyq_matmul_d(hyq_ctx *ctx, const hyq_weight *w, const float *x_d, size_t bat
     float *rscale = (float *)((uint8_t *)ctx->xh.ptr() + xh_bytes);
     HYQ_LAUNCH(launch_to_f16(x_d, (int)batch, (int)w->cols, xh, rscale, ctx->stream), "to_f16");
     HYQ_LAUNCH(launch_gemm_f16(w->dtype, w->view, (int)w->cols, xh, rscale, (int)batch, y_d,
-                               ctx->stream),
+                               nullptr, ctx->stream),
                "gemm_f16");
     return HYQ_OK;
 }

@@ -7,10 +7,22 @@
 // gate/up SiLU GEMV -> Q8 -> down GEMV (+ residual); then output norm ->
 // Q8 -> lm_head GEMV -> argmax. Position and token stay in device memory, so
 // one step is captured once as a HIP graph and replayed per token.
+//
+// hyq_dense_prefill runs a prompt in chunks of up to PREFILL_CHUNK tokens
+// through the batch > 1 arm (src/model.rs:549-616, 630-646): per layer the
+// RMSNorm of every row fused with its f16 rounding, the Q, K and V
+// f16-MFMA GEMMs, RoPE + Q/K norm + KV append for all rows, causal attention
+// of every row over the cache, the attention-output GEMM with the residual
+// add in its epilogue, the FFN norm, the gate/up GEMM with silu(g)*u in its
+// epilogue and the down GEMM with the residual add; then the last row's
+// output norm, the lm_head GEMV and the argmax. A one-token chunk is the
+// batch-1 decode step, as in the reference.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <memory>
 #include <vector>
 
 #include "hyq_abi.hpp"
@@ -135,6 +147,31 @@ int hyq_attention_d(hyq_ctx *ctx, const float *q_d, const float *kcache_d,
     return HYQ_OK;
 }
 
+size_t hyq_attention_rows_scratch_floats(size_t context, size_t heads, size_t n)
+{
+    return n * (size_t)prefill_attention_splits((int)context) * heads * PART_STRIDE;
+}
+
+int hyq_attention_rows_d(hyq_ctx *ctx, const float *q_d, const float *kcache_d,
+                         const float *vcache_d, const int32_t *pos_d, size_t n, size_t context,
+                         size_t heads, size_t kv_heads, size_t head_dim, float *scratch_d,
+                         float *out_d)
+{
+    int rc = check_ctx(ctx, "attention_rows");
+    if (rc) return rc;
+    if (!q_d || !kcache_d || !vcache_d || !pos_d || !scratch_d || !out_d)
+        return fail(HYQ_EINVAL, "attention_rows: null argument");
+    if (head_dim != 128 || heads == 0 || kv_heads == 0 || heads % kv_heads ||
+        heads / kv_heads > (size_t)ATT_MAX_REP || context == 0 || context > 65536)
+        return fail(HYQ_EINVAL, "attention_rows: unsupported shape");
+    if (n == 0 || n > context) return fail(HYQ_EINVAL, "attention_rows: %zu query rows", n);
+    DeviceGuard g(ctx->device);
+    HYQ_LAUNCH(launch_attention_rows(q_d, kcache_d, vcache_d, pos_d, (int)n, (int)context,
+                                     (int)heads, (int)kv_heads, scratch_d, out_d, ctx->stream),
+               "attention_rows");
+    return HYQ_OK;
+}
+
 int hyq_argmax_d(hyq_ctx *ctx, const float *x_d, size_t n, float *scratch_d, int32_t *token_d)
 {
     int rc = check_ctx(ctx, "argmax");
@@ -185,6 +222,16 @@ struct hyq_dense {
 
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+
+    // chunked prefill activations (allocated on the first prefill):
+    // hid [n][H], q [n][QL], k/v [n][KV], att [n][QL], h [n][F] f32;
+    // xh [n][max(H, QL, F)] f16 with row scales rs [n]; attention partials;
+    // the chunk's token ids
+    std::unique_ptr<DeviceBuffer> pf_mem;
+    float *pf_hid = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr;
+    float *pf_att = nullptr, *pf_h = nullptr, *pf_rs = nullptr, *pf_part = nullptr;
+    _Float16 *pf_xh = nullptr;
+    int32_t *pf_tok = nullptr;
 
     ~hyq_dense()
     {
@@ -308,6 +355,100 @@ int enqueue_step(hyq_dense *m)
     }
     HYQ_LAUNCH(launch_argmax(m->logits, c.vocab, m->argmax_scratch,
                              (int *)(m->argmax_scratch + 64), m->token, m->state, m->history, st),
+               "argmax");
+    return HYQ_OK;
+}
+
+// PREFILL_CHUNK (src/model.rs:18): tokens per forward_into call.
+constexpr size_t PREFILL_CHUNK = 256;
+
+int prefill_buffers(hyq_dense *m)
+{
+    if (m->pf_mem) return HYQ_OK;
+    const hyq_dense_config &c = m->cfg;
+    const size_t N = PREFILL_CHUNK, H = (size_t)c.hidden, F = (size_t)c.ffn;
+    const size_t QL = (size_t)c.heads * c.head_dim, KV = (size_t)c.kv_heads * c.head_dim;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        size_t o = off;
+        off += align_up(bytes, 256);
+        return o;
+    };
+    const size_t o_hid = take(N * H * 4), o_q = take(N * QL * 4), o_k = take(N * KV * 4);
+    const size_t o_v = take(N * KV * 4), o_att = take(N * QL * 4), o_h = take(N * F * 4);
+    const size_t o_xh = take(N * std::max(H, std::max(QL, F)) * 2), o_rs = take(N * 4);
+    const size_t o_part = take(N * (size_t)c.heads *
+                               (size_t)prefill_attention_splits((int)m->context) * PART_STRIDE * 4);
+    const size_t o_tok = take(N * 4);
+    auto buf = std::make_unique<DeviceBuffer>();
+    int rc = buf->alloc(m->ctx->device, off);
+    if (rc) return rc;
+    uint8_t *b = (uint8_t *)buf->ptr;
+    m->pf_hid = (float *)(b + o_hid);
+    m->pf_q = (float *)(b + o_q);
+    m->pf_k = (float *)(b + o_k);
+    m->pf_v = (float *)(b + o_v);
+    m->pf_att = (float *)(b + o_att);
+    m->pf_h = (float *)(b + o_h);
+    m->pf_xh = (_Float16 *)(b + o_xh);
+    m->pf_rs = (float *)(b + o_rs);
+    m->pf_part = (float *)(b + o_part);
+    m->pf_tok = (int32_t *)(b + o_tok);
+    m->pf_mem = std::move(buf);
+    return HYQ_OK;
+}
+
+// One chunk of n >= 2 tokens at position m->state->pos (the chunk's ids are
+// in m->pf_tok); leaves the last row's logits in m->logits and the greedy
+// token in m->token.
+int enqueue_prefill_chunk(hyq_dense *m, int n)
+{
+    const hyq_dense_config &c = m->cfg;
+    hipStream_t st = m->ctx->stream;
+    const int H = c.hidden, F = c.ffn, QL = c.heads * c.head_dim;
+    const int *pos = &m->state->pos;
+    HYQ_LAUNCH(launch_embed_rows(m->embedding->dtype, m->embedding->view, H, m->pf_tok, n,
+                                 m->pf_hid, st),
+               "embed_rows");
+    for (int l = 0; l < c.layers; ++l) {
+        const hyq_dense::Layer &L = m->layers[l];
+        HYQ_LAUNCH(launch_norm_to_f16(m->pf_hid, n, H, L.attn_norm, c.rms_eps, m->pf_xh,
+                                      m->pf_rs, st),
+                   "norm_to_f16");
+        const hyq_weight *ws[3] = {L.q, L.k, L.v};
+        float *ys[3] = {m->pf_q, m->pf_k, m->pf_v};
+        for (int i = 0; i < 3; ++i)
+            HYQ_LAUNCH(launch_gemm_f16(ws[i]->dtype, ws[i]->view, H, m->pf_xh, m->pf_rs, n, ys[i],
+                                       nullptr, st),
+                       "gemm_qkv");
+        HYQ_LAUNCH(launch_rope_norm_kv_rows(m->pf_q, m->pf_k, m->pf_v, L.q_norm, L.k_norm,
+                                            m->freq, pos, n, c.heads, c.kv_heads, c.head_dim,
+                                            c.rms_eps, m->kcache(l), m->vcache(l), st),
+                   "rope_norm_kv_rows");
+        HYQ_LAUNCH(launch_attention_rows(m->pf_q, m->kcache(l), m->vcache(l), pos, n,
+                                         (int)m->context, c.heads, c.kv_heads, m->pf_part,
+                                         m->pf_att, st),
+                   "attention_rows");
+        HYQ_LAUNCH(launch_to_f16(m->pf_att, n, QL, m->pf_xh, m->pf_rs, st), "to_f16");
+        HYQ_LAUNCH(launch_gemm_f16(L.o->dtype, L.o->view, QL, m->pf_xh, m->pf_rs, n, m->pf_hid,
+                                   m->pf_hid, st),
+                   "gemm_attn_output");
+        HYQ_LAUNCH(launch_norm_to_f16(m->pf_hid, n, H, L.ffn_norm, c.rms_eps, m->pf_xh,
+                                      m->pf_rs, st),
+                   "norm_to_f16");
+        HYQ_LAUNCH(launch_gate_up_f16(L.gate->dtype, L.gate->view, L.up->view, H, m->pf_xh,
+                                      m->pf_rs, n, m->pf_h, st),
+                   "gemm_gate_up");
+        HYQ_LAUNCH(launch_to_f16(m->pf_h, n, F, m->pf_xh, m->pf_rs, st), "to_f16");
+        HYQ_LAUNCH(launch_gemm_f16(L.down->dtype, L.down->view, F, m->pf_xh, m->pf_rs, n,
+                                   m->pf_hid, m->pf_hid, st),
+                   "gemm_down");
+    }
+    GemvArgs a = staged(m->output, m->pf_hid + (size_t)(n - 1) * H, m->output_norm, c.rms_eps,
+                        m->logits, nullptr);
+    HYQ_LAUNCH(launch_gemv(m->output->dtype, GEMV_PLAIN, a, st), "gemv_lm_head");
+    HYQ_LAUNCH(launch_argmax(m->logits, c.vocab, m->argmax_scratch,
+                             (int *)(m->argmax_scratch + 64), m->token, nullptr, nullptr, st),
                "argmax");
     return HYQ_OK;
 }
@@ -548,6 +689,58 @@ int hyq_dense_forward(hyq_dense *m, int32_t token, float *logits, int32_t *next)
     HYQ_HIP(hipStreamSynchronize(m->ctx->stream), "hipStreamSynchronize");
     m->pos_host += 1;
     if (next) *next = nt;
+    return HYQ_OK;
+}
+
+int hyq_dense_prefill(hyq_dense *m, const int32_t *tokens, size_t n, float *logits,
+                      int32_t *next)
+{
+    if (!m) return fail(HYQ_EINVAL, "dense_prefill: null decoder");
+    int rc = ready(m);
+    if (rc) return rc;
+    if (n == 0 || !tokens) return fail(HYQ_EINVAL, "prompt must contain at least one token");
+    if (n > m->context - m->pos_host) return fail(HYQ_EINVAL, "prompt exceeds context limit");
+    for (size_t i = 0; i < n; ++i)
+        if (tokens[i] < 0 || tokens[i] >= m->cfg.vocab)
+            return fail(HYQ_EINVAL, "input token outside vocabulary");
+    DeviceGuard g(m->ctx->device);
+    hipStream_t st = m->ctx->stream;
+    if (n > 1 && (rc = prefill_buffers(m))) return rc;
+    for (size_t s = 0; s < n; s += PREFILL_CHUNK) {
+        const size_t cn = std::min(PREFILL_CHUNK, n - s);
+        if ((rc = write_state(m, tokens[s], 0, 0))) return rc;
+        if (cn == 1) {
+            if ((rc = enqueue_step(m))) return rc;
+        } else {
+            HYQ_HIP(hipMemcpyAsync(m->pf_tok, tokens + s, cn * 4, hipMemcpyHostToDevice, st),
+                    "hipMemcpy(tokens)");
+            if ((rc = enqueue_prefill_chunk(m, (int)cn))) return rc;
+        }
+        // the host-side state and token words are rewritten by the next chunk
+        HYQ_HIP(hipStreamSynchronize(st), "hipStreamSynchronize");
+        m->pos_host += cn;
+    }
+    if (logits)
+        HYQ_HIP(hipMemcpyAsync(logits, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost,
+                               st),
+                "hipMemcpy(logits)");
+    int32_t nt = 0;
+    HYQ_HIP(hipMemcpyAsync(&nt, m->token, 4, hipMemcpyDeviceToHost, st), "hipMemcpy(token)");
+    HYQ_HIP(hipStreamSynchronize(st), "hipStreamSynchronize");
+    if (next) *next = nt;
+    return HYQ_OK;
+}
+
+int hyq_dense_read_kv(hyq_dense *m, int layer, size_t positions, float *keys, float *values)
+{
+    if (!m || !keys || !values) return fail(HYQ_EINVAL, "dense_read_kv: null argument");
+    if (layer < 0 || layer >= m->cfg.layers) return fail(HYQ_EINVAL, "dense: layer %d", layer);
+    if (positions > m->context) return fail(HYQ_EINVAL, "context limit exceeded");
+    DeviceGuard g(m->ctx->device);
+    HYQ_HIP(hipStreamSynchronize(m->ctx->stream), "hipStreamSynchronize");
+    const size_t bytes = positions * m->kvw() * 4;
+    HYQ_HIP(hipMemcpy(keys, m->kcache(layer), bytes, hipMemcpyDeviceToHost), "hipMemcpy(k)");
+    HYQ_HIP(hipMemcpy(values, m->vcache(layer), bytes, hipMemcpyDeviceToHost), "hipMemcpy(v)");
     return HYQ_OK;
 }
 

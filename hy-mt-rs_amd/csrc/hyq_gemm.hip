@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 
 #include "hyq_tile.hpp"
+#include "hyq_wave.hpp"
 
 #pragma clang fp contract(off)
 
@@ -29,37 +30,63 @@ __device__ __forceinline__ int xcd_tile(int total)
     return (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
 }
 
-// One workgroup per row: xh[r][k] = f16(x[src][k] * 2^-e) and rscale[r] =
-// 2^e, where e = ceil(log2(max_k |x[src][k]|)) - 14 puts the row's largest
-// magnitude at or below 2^14, so no value overflows f16 or drops into its
-// subnormals; the power-of-two scale is exact and the GEMM epilogues multiply
-// it back. src = r, or ptok[order[r]] when order is given; rows r >= *count
-// (when count is given) are left alone. A row with a zero, infinite or NaN
-// maximum keeps scale 1 (and its infinities / NaNs propagate).
+// One workgroup per row: xh[r][k] = f16(v[k] * 2^-e) and rscale[r] = 2^e,
+// where v = x[src] (or, with `norm`, its RMSNorm v[k] = x[k] * s * norm[k],
+// s = 1 / sqrt(mean(x^2) + eps), the order of src/model.rs:832-870) and
+// e = ceil(log2(max_k |v[k]|)) - 14 puts the row's largest magnitude at or
+// below 2^14, so no value overflows f16 or drops into its subnormals; the
+// power-of-two scale is exact and the GEMM epilogues multiply it back.
+// src = r, or ptok[order[r]] when order is given; rows r >= *count (when
+// count is given) are left alone. A row with a zero, infinite or NaN maximum
+// keeps scale 1 (and its infinities / NaNs propagate).
 __global__ __launch_bounds__(256) void rows_to_f16_kernel(const float *__restrict__ x, int K,
                                                           const int *__restrict__ order,
                                                           const int *__restrict__ ptok,
                                                           const int *__restrict__ count,
+                                                          const float *__restrict__ norm,
+                                                          float eps,
                                                           _Float16 *__restrict__ xh,
                                                           float *__restrict__ rscale)
 {
-    __shared__ float wmax[4];
+    __shared__ float wred[4];
     const int r = blockIdx.x;
     if (count && r >= *count) return;
     const size_t src = order ? (size_t)ptok[order[r]] : (size_t)r;
     const float4 *x4 = reinterpret_cast<const float4 *>(x + src * K);
+    const float4 *n4p = reinterpret_cast<const float4 *>(norm);
     const int t = threadIdx.x, n4 = K / 4;
+    float s = 1.f;
+    if (norm) {
+        float ss = 0.f;
+        for (int i = t; i < n4; i += 256) {
+            const float4 v = x4[i];
+            ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+        }
+        ss = wave::sum64(ss);
+        if ((t & 63) == 0) wred[t >> 6] = ss;
+        __syncthreads();
+        ss = (wred[0] + wred[1]) + (wred[2] + wred[3]);
+        __syncthreads();
+        s = 1.0f / sqrtf(ss / (float)K + eps);
+    }
+    auto value = [&](int i) {
+        float4 v = x4[i];
+        if (norm) {
+            const float4 w = n4p[i];
+            v = make_float4(v.x * s * w.x, v.y * s * w.y, v.z * s * w.z, v.w * s * w.w);
+        }
+        return v;
+    };
     float m = 0.f;
     for (int i = t; i < n4; i += 256) {
-        const float4 v = x4[i];
+        const float4 v = value(i);
         m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         if (v.x != v.x || v.y != v.y || v.z != v.z || v.w != v.w) m = INFINITY;
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    if ((t & 63) == 0) wmax[t >> 6] = m;
+    m = wave::max64(m);
+    if ((t & 63) == 0) wred[t >> 6] = m;
     __syncthreads();
-    m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    m = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
     int e = 0;
     if (m > 0.f && m < INFINITY) {
         int ex;
@@ -71,7 +98,7 @@ __global__ __launch_bounds__(256) void rows_to_f16_kernel(const float *__restric
     if (t == 0) rscale[r] = ldexpf(1.0f, e);
     _Float16 *o = xh + (size_t)r * K;
     for (int i = t; i < n4; i += 256) {
-        const float4 v = x4[i];
+        const float4 v = value(i);
         const half2v a = __builtin_convertvector((float2v){v.x * inv, v.y * inv}, half2v);
         const half2v b = __builtin_convertvector((float2v){v.z * inv, v.w * inv}, half2v);
         *reinterpret_cast<half2v *>(o + 4 * i) = a;
@@ -79,12 +106,15 @@ __global__ __launch_bounds__(256) void rows_to_f16_kernel(const float *__restric
     }
 }
 
+// Y[n][m] = (X[n] . W[m]) * rscale[n], plus residual[n][m] when given (the
+// residual add of src/model.rs:595, 601 after the product is rounded; it
+// may alias y: each element is read and then written by one thread).
 template <int F>
 __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(WView w, int M, int K,
                                                           const _Float16 *__restrict__ xh,
                                                           const float *__restrict__ rscale, int N,
-                                                          float *__restrict__ y, int mtiles,
-                                                          int ntiles)
+                                                          float *y, const float *residual,
+                                                          int mtiles, int ntiles)
 {
     __shared__ __attribute__((aligned(16))) _Float16 lds[4 * TILE_HALVES];
     const int T = xcd_tile(mtiles * ntiles);
@@ -111,18 +141,26 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(WView w, int M, int K,
             const int n = n0 + acc_col(wn, j);
             if (n >= N) continue;
             float *yr = y + (size_t)n * M;
+            const float *rr = residual ? residual + (size_t)n * M : nullptr;
             const float sc = rscale[n];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int m = m0 + arow(i) + acc_row_in_block(4 * g);
                 if (m + 3 < M && (M & 3) == 0) {
-                    *reinterpret_cast<float4 *>(yr + m) =
-                        make_float4(acc[i][j][4 * g] * sc, acc[i][j][4 * g + 1] * sc,
-                                    acc[i][j][4 * g + 2] * sc, acc[i][j][4 * g + 3] * sc);
+                    float4 v = make_float4(acc[i][j][4 * g] * sc, acc[i][j][4 * g + 1] * sc,
+                                           acc[i][j][4 * g + 2] * sc, acc[i][j][4 * g + 3] * sc);
+                    if (rr) {
+                        const float4 a = *reinterpret_cast<const float4 *>(rr + m);
+                        v = make_float4(a.x + v.x, a.y + v.y, a.z + v.z, a.w + v.w);
+                    }
+                    *reinterpret_cast<float4 *>(yr + m) = v;
                 } else {
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        if (m + e < M) yr[m + e] = acc[i][j][4 * g + e] * sc;
+                        if (m + e < M) {
+                            const float v = acc[i][j][4 * g + e] * sc;
+                            yr[m + e] = rr ? rr[m + e] + v : v;
+                        }
                 }
             }
         }
@@ -287,6 +325,49 @@ __global__ __launch_bounds__(256, 2) void moe_gate_up_kernel(
     }
 }
 
+// Gate and up of a dense FFN at batch N (DenseFfn::forward, src/model.rs:
+// 679-683): the tile pairs gate rows m0..m0+63 with the same rows of up, as
+// moe_gate_up_kernel does, and writes H[n][m] = silu(g) * u in f32.
+template <int F>
+__global__ __launch_bounds__(256, 2) void gemm_gate_up_kernel(WView gate, WView up, int mid, int K,
+                                                              const _Float16 *__restrict__ xh,
+                                                              const float *__restrict__ rscale,
+                                                              int N, float *__restrict__ H,
+                                                              int mtiles, int ntiles)
+{
+    __shared__ __attribute__((aligned(16))) _Float16 lds[4 * TILE_HALVES];
+    const int T = xcd_tile(mtiles * ntiles);
+    if (T >= mtiles * ntiles) return;
+    const int m0 = (T / ntiles) * 64, n0 = (T % ntiles) * BN;
+    const int wave = threadIdx.x >> 6, wm = wave >> 1, wn = wave & 1;
+
+    f32x16 acc[2][2];
+    zero_acc(acc);
+    auto wsrc = [&](int lrow, WView &v, int &row) {
+        const int m = m0 + (lrow & 63);
+        v = lrow < 64 ? gate : up;
+        row = m < mid ? m : -1;
+    };
+    auto xrow = [&](int r) -> const _Float16 * {
+        return n0 + r < N ? xh + (size_t)(n0 + r) * K : nullptr;
+    };
+    auto arow = [&](int i) { return 64 * i + 32 * wm; };
+    k_loop<F>(wsrc, xrow, arow, K, wn, lds, acc);
+
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int n = n0 + acc_col(wn, j);
+        if (n >= N) continue;
+        float *hr = H + (size_t)n * mid;
+        const float sc = rscale[n];
+#pragma unroll
+        for (int e4 = 0; e4 < 16; ++e4) {
+            const int m = m0 + 32 * wm + acc_row_in_block(e4);
+            if (m < mid) hr[m] = silu_mul(acc[0][j][e4] * sc, acc[1][j][e4] * sc);
+        }
+    }
+}
+
 // Down of one expert chunk: outp[q][m] = down_e[m] . H[q] (H in f16 with its
 // row scale).
 template <int F>
@@ -360,14 +441,47 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(float *__restrict__ ou
 
 int launch_to_f16(const float *x, int rows, int K, _Float16 *xh, float *rscale, void *stream)
 {
+    return launch_norm_to_f16(x, rows, K, nullptr, 0.f, xh, rscale, stream);
+}
+
+int launch_norm_to_f16(const float *x, int rows, int K, const float *norm, float eps,
+                       _Float16 *xh, float *rscale, void *stream)
+{
     if (rows <= 0) return 0;
+    if (K % 4) return (int)hipErrorInvalidValue;
     hipLaunchKernelGGL(rows_to_f16_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream, x, K,
-                       nullptr, nullptr, nullptr, xh, rscale);
+                       nullptr, nullptr, nullptr, norm, eps, xh, rscale);
+    return (int)hipGetLastError();
+}
+
+int launch_gate_up_f16(int fmt, WView gate, WView up, int cols, const _Float16 *xh,
+                       const float *rscale, int batch, float *h, void *stream)
+{
+    if (cols % BK) return (int)hipErrorInvalidValue;
+    const int mid = gate.rows;
+    const int mtiles = (mid + 63) / 64, ntiles = (batch + BN - 1) / BN;
+    const int per = (mtiles * ntiles + 7) / 8;
+    dim3 grid(8 * per), block(256);
+    hipStream_t st = (hipStream_t)stream;
+#define HYQ_GU(F)                                                                              \
+    case F:                                                                                    \
+        hipLaunchKernelGGL(gemm_gate_up_kernel<F>, grid, block, 0, st, gate, up, mid, cols, xh, \
+                           rscale, batch, h, mtiles, ntiles);                                  \
+        break;
+    switch (fmt) {
+        HYQ_GU(Q4_K)
+        HYQ_GU(Q6_K)
+        HYQ_GU(Q8_0)
+        HYQ_GU(Q2_0C)
+        HYQ_GU(STQ1_0)
+    default: return (int)hipErrorInvalidValue;
+    }
+#undef HYQ_GU
     return (int)hipGetLastError();
 }
 
 int launch_gemm_f16(int fmt, WView w, int cols, const _Float16 *xh, const float *rscale,
-                    int batch, float *y, void *stream)
+                    int batch, float *y, const float *residual, void *stream)
 {
     if (cols % BK) return (int)hipErrorInvalidValue;
     const int M = w.rows;
@@ -378,7 +492,7 @@ int launch_gemm_f16(int fmt, WView w, int cols, const _Float16 *xh, const float 
 #define HYQ_GEMM(F)                                                                            \
     case F:                                                                                    \
         hipLaunchKernelGGL(gemm_f16_kernel<F>, grid, block, 0, st, w, M, cols, xh, rscale,      \
-                           batch, y, mtiles, ntiles);                                          \
+                           batch, y, residual, mtiles, ntiles);                                \
         break;
     switch (fmt) {
         HYQ_GEMM(Q4_K)
@@ -441,7 +555,7 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
     hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, ptok, pexp, npairs, tokens,
                        experts, eoff, order, rank, toff, tlist, tiles, ntiles);
     hipLaunchKernelGGL(rows_to_f16_kernel, dim3(npairs), dim3(256), 0, st, x, hidden, order,
-                       ptok, eoff + experts, xg, xscale);
+                       ptok, eoff + experts, nullptr, 0.f, xg, xscale);
     {
         const int mtiles = (mid + 63) / 64;
         const int per = (mtiles * L.max_tiles + 7) / 8;
@@ -462,7 +576,7 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
 #undef HYQ_MOE_GU
     }
     hipLaunchKernelGGL(rows_to_f16_kernel, dim3(npairs), dim3(256), 0, st, h32, mid, nullptr,
-                       nullptr, eoff + experts, H, hscale);
+                       nullptr, eoff + experts, nullptr, 0.f, H, hscale);
     {
         const int mtiles = (hidden + BM - 1) / BM;
         const int per = (mtiles * L.max_tiles + 7) / 8;

@@ -144,11 +144,18 @@ int launch_dequant_rows(int fmt, WView w, int row0, int nrows, int cols, float *
                         void *stream);
 int launch_decode_gguf(int fmt, const uint8_t *bytes, size_t nblocks, float *out, void *stream);
 // Batched products (hyq_gemm.hip): x [rows][K] f32 -> f16 with a power-of-two
-// scale per row (rscale), then the f16-MFMA GEMM
-// y[batch][w.rows] = rscale[batch] * (xh[batch][cols] W^T).
+// scale per row (rscale), optionally RMS-normalized first (norm [K], eps);
+// then the f16-MFMA GEMM
+// y[batch][w.rows] = rscale[batch] * (xh[batch][cols] W^T) (+ residual, which
+// may alias y), or the dense gate/up product h[batch][gate.rows] =
+// silu(gate . x) * (up . x).
 int launch_to_f16(const float *x, int rows, int K, _Float16 *xh, float *rscale, void *stream);
+int launch_norm_to_f16(const float *x, int rows, int K, const float *norm, float eps,
+                       _Float16 *xh, float *rscale, void *stream);
 int launch_gemm_f16(int fmt, WView w, int cols, const _Float16 *xh, const float *rscale,
-                    int batch, float *y, void *stream);
+                    int batch, float *y, const float *residual, void *stream);
+int launch_gate_up_f16(int fmt, WView gate, WView up, int cols, const _Float16 *xh,
+                       const float *rscale, int batch, float *h, void *stream);
 
 // Byte offsets of the MoE scratch regions (hyq_gemm.hip: moe_layout).
 struct MoeLayout {

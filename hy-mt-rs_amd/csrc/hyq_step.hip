@@ -24,14 +24,16 @@ namespace {
 __device__ __forceinline__ float wave_sum(float v) { return wave::sum64(v); }
 __device__ __forceinline__ float wave_max(float v) { return wave::max64(v); }
 
-// ---- embedding row (Weight::row_into with a device-resident token id) ----
+// ---- embedding rows (Weight::row_into with device-resident token ids) ----
+// Grid (cols / 256, tokens): row blockIdx.y of out takes token[blockIdx.y].
 template <int F>
 __global__ __launch_bounds__(256) void embed_kernel(WView w, int cols, const int *__restrict__ token,
                                                     float *__restrict__ out)
 {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= cols) return;
-    const size_t row = (size_t)*token;
+    const size_t row = (size_t)token[blockIdx.y];
+    out += (size_t)blockIdx.y * cols;
     const size_t blk = row * (size_t)w.nb + i / block_len(F);
     out[i] = dec::decode_plane_value<F>(w, blk, i % block_len(F));
 }
@@ -91,7 +93,9 @@ __global__ __launch_bounds__(256) void rms_norm_q8_kernel(const float *__restric
 // Workgroups [0, heads) rotate and normalise the query heads in place,
 // [heads, heads+kv) the key heads into kcache[pos], [heads+kv, heads+2kv)
 // copy the value heads into vcache[pos]. Lane j owns the NeoX pair
-// (j, j + dim/2) (docs/reference.md:79), so dim/2 lanes per head.
+// (j, j + dim/2) (docs/reference.md:79), so dim/2 lanes per head. Grid y
+// walks the tokens of a chunk: token y has rows q[y], k[y], v[y] and
+// position *pos_p + y (rope at start + token, src/model.rs:919-925).
 __global__ void rope_norm_kv_kernel(float *__restrict__ q, const float *__restrict__ k,
                                     const float *__restrict__ v, const float *__restrict__ qn,
                                     const float *__restrict__ kn,
@@ -102,8 +106,11 @@ __global__ void rope_norm_kv_kernel(float *__restrict__ q, const float *__restri
     const int b = blockIdx.x;
     const int j = threadIdx.x;
     const int half = dim / 2;
-    const int pos = *pos_p;
+    const int pos = *pos_p + (int)blockIdx.y;
     const size_t kvw = (size_t)kvh * dim;
+    q += (size_t)blockIdx.y * heads * dim;
+    k += (size_t)blockIdx.y * kvw;
+    v += (size_t)blockIdx.y * kvw;
     if (b >= heads + kvh) {
         const int h = b - heads - kvh;
         float *dst = vcache + (size_t)pos * kvw + (size_t)h * dim;
@@ -162,6 +169,10 @@ __global__ void rope_norm_kv_kernel(float *__restrict__ q, const float *__restri
 // The split's (max, exp-sum, V sum) per query head goes to `part`
 // ([heads][splits][PART_STRIDE]) for the merge (attn_merge_kernel).
 //
+// Grid z walks the query tokens of a prefill chunk whose keys and values are
+// already in the cache: token z reads query row q[z], sees positions
+// 0..=*pos_p + z (causal, src/model.rs:956-961) and writes partials block z.
+//
 // With `rope` set the workgroup first forms its query heads from the raw
 // projection (rope_with_cache + the dense order's per-head rms_norm,
 // src/model.rs:425-446, 874-917), and the split holding `pos` also forms the
@@ -202,9 +213,11 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(
     __shared__ __align__(16) float Vn[D];
     __shared__ __align__(16) float Es[ATT_MAX_REP][ATT_SUB];     // the slice's exp weights
     __shared__ __align__(16) float Red[2][ATT_MAX_REP][ATT_WAVES]; // per-wave max / exp-sum
-    const int split = blockIdx.x, kh = blockIdx.y;
+    const int split = blockIdx.x, kh = blockIdx.y, tq = blockIdx.z;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const size_t kvw = (size_t)kvh * D;
+    q += (size_t)tq * heads * D;
+    part += (size_t)tq * heads * splits * PART_STRIDE;
     const int p0 = split * chunk;
     const int rep = heads / kvh;
     // rope: wave w < rep forms query head w of the group (waves past `rep`
@@ -245,8 +258,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(
         kr[j] = reinterpret_cast<const float4 *>(kbase + (size_t)pp * kvw)[d4];
         vr[j] = reinterpret_cast<const float4 *>(vbase + (size_t)pp * kvw)[d4];
     }
-    const int pos = *pos_p;
-    const int visible = pos + 1;
+    const int pos = *pos_p + tq;
+    const int visible = min(pos + 1, context); // no cache row past the allocation
     const int nact = (visible + chunk - 1) / chunk;
     if (split >= nact) {
         // The idle split consumes its loads as well (a store that a valid
@@ -399,7 +412,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(
 // its weight, which reaches the accumulation by readlane. All loads (split
 // slots past `splits` clamped into bounds, slots past the visible splits
 // ignored) are issued together with the position's, so one memory round
-// trip is paid.
+// trip is paid. Grid z walks the query tokens of a prefill chunk (token z at
+// position *pos_p + z, partials block z, output row z).
 template <int MS>
 __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict__ part,
                                                          int splits, int chunk,
@@ -410,14 +424,16 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
     __shared__ float red[4][64];
     const int h = blockIdx.x, lane = threadIdx.x & 63, g = threadIdx.x >> 6;
     const int d = 64 * blockIdx.y + lane;
-    const float *ph = part + (size_t)h * splits * PART_STRIDE;
+    const int tq = blockIdx.z;
+    const float *ph = part + ((size_t)tq * gridDim.x + h) * splits * PART_STRIDE;
+    out += (size_t)tq * gridDim.x * ATT_D;
     const float2 ml =
         *reinterpret_cast<const float2 *>(ph + (size_t)min(lane, splits - 1) * PART_STRIDE);
     float a[MS / 4];
 #pragma unroll
     for (int k = 0; k < MS / 4; ++k)
         a[k] = ph[(size_t)min(g + 4 * k, splits - 1) * PART_STRIDE + 4 + d];
-    const int nact = (*pos_p + chunk) / chunk;
+    const int nact = min((*pos_p + tq + chunk) / chunk, splits);
     const bool live = lane < nact;
     const float M = wave::max64(live ? ml.x : -INFINITY);
     const float w = live ? expf(ml.x - M) : 0.f;
@@ -500,10 +516,17 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float *__restric
 
 int launch_embed_row(int fmt, WView w, int cols, const int *token, float *out, void *stream)
 {
-    dim3 grid((cols + 255) / 256), block(256);
+    return launch_embed_rows(fmt, w, cols, token, 1, out, stream);
+}
+
+int launch_embed_rows(int fmt, WView w, int cols, const int *tokens, int n, float *out,
+                      void *stream)
+{
+    if (n <= 0) return 0;
+    dim3 grid((cols + 255) / 256, n), block(256);
     hipStream_t st = (hipStream_t)stream;
 #define HYQ_EMB(F)                                                                             \
-    case F: hipLaunchKernelGGL(embed_kernel<F>, grid, block, 0, st, w, cols, token, out); break;
+    case F: hipLaunchKernelGGL(embed_kernel<F>, grid, block, 0, st, w, cols, tokens, out); break;
     switch (fmt) {
         HYQ_EMB(Q2_0C)
         HYQ_EMB(STQ1_0)
@@ -530,7 +553,17 @@ int launch_rope_norm_kv(float *q, const float *k, const float *v, const float *q
                         const float *kn, const float *freq, const int *pos, int heads, int kvh,
                         int dim, float eps, float *kcache, float *vcache, void *stream)
 {
-    hipLaunchKernelGGL(rope_norm_kv_kernel, dim3(heads + 2 * kvh), dim3(dim / 2), 0,
+    return launch_rope_norm_kv_rows(q, k, v, qn, kn, freq, pos, 1, heads, kvh, dim, eps, kcache,
+                                    vcache, stream);
+}
+
+int launch_rope_norm_kv_rows(float *q, const float *k, const float *v, const float *qn,
+                             const float *kn, const float *freq, const int *pos, int n,
+                             int heads, int kvh, int dim, float eps, float *kcache,
+                             float *vcache, void *stream)
+{
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(rope_norm_kv_kernel, dim3(heads + 2 * kvh, n), dim3(dim / 2), 0,
                        (hipStream_t)stream, q, k, v, qn, kn, freq, pos, heads, kvh, dim, eps,
                        kcache, vcache);
     return (int)hipGetLastError();
@@ -550,6 +583,19 @@ int attention_splits(int context)
     return (context + c - 1) / c;
 }
 
+int prefill_attention_chunk(int context)
+{
+    // n query tokens already fill the machine; splits of at least 128
+    // positions keep partials and merge work small
+    return std::max(128, attention_chunk(context));
+}
+
+int prefill_attention_splits(int context)
+{
+    const int c = prefill_attention_chunk(context);
+    return (context + c - 1) / c;
+}
+
 int launch_zero_u32(unsigned *p, int n, void *stream)
 {
     if (n <= 0) return 0;
@@ -560,17 +606,18 @@ int launch_zero_u32(unsigned *p, int n, void *stream)
 
 // The merge, instantiated for the smallest split bound that covers `splits`.
 static void launch_merge(const float *part, int splits, int chunk, int heads, const int *pos,
-                         float *out, hipStream_t st)
+                         float *out, hipStream_t st, int tokens = 1)
 {
+    const dim3 grid(heads, 2, tokens);
     if (splits <= 16)
-        hipLaunchKernelGGL(attn_merge_kernel<16>, dim3(heads, 2), dim3(256), 0, st, part,
-                           splits, chunk, pos, out);
+        hipLaunchKernelGGL(attn_merge_kernel<16>, grid, dim3(256), 0, st, part, splits, chunk,
+                           pos, out);
     else if (splits <= 32)
-        hipLaunchKernelGGL(attn_merge_kernel<32>, dim3(heads, 2), dim3(256), 0, st, part,
-                           splits, chunk, pos, out);
+        hipLaunchKernelGGL(attn_merge_kernel<32>, grid, dim3(256), 0, st, part, splits, chunk,
+                           pos, out);
     else
-        hipLaunchKernelGGL(attn_merge_kernel<ATT_MAX_SPLITS>, dim3(heads, 2), dim3(256), 0, st,
-                           part, splits, chunk, pos, out);
+        hipLaunchKernelGGL(attn_merge_kernel<ATT_MAX_SPLITS>, grid, dim3(256), 0, st, part,
+                           splits, chunk, pos, out);
 }
 
 int launch_attention(const float *q, const float *kcache, const float *vcache, const int *pos,
@@ -584,6 +631,22 @@ int launch_attention(const float *q, const float *kcache, const float *vcache, c
                        const_cast<float *>(vcache), pos, heads, kvh, scale, part, splits, chunk,
                        context);
     launch_merge(part, splits, chunk, heads, pos, out, st);
+    return (int)hipGetLastError();
+}
+
+int launch_attention_rows(const float *q, const float *kcache, const float *vcache,
+                          const int *pos, int n, int context, int heads, int kvh, float *part,
+                          float *out, void *stream)
+{
+    if (n <= 0) return 0;
+    const int splits = prefill_attention_splits(context), chunk = prefill_attention_chunk(context);
+    const float scale = 1.0f / sqrtf(128.0f);
+    hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL(attn_kernel, dim3(splits, kvh, n), dim3(ATT_THREADS), 0, st, false, q,
+                       nullptr, nullptr, nullptr, nullptr, nullptr, 0.f,
+                       const_cast<float *>(kcache), const_cast<float *>(vcache), pos, heads, kvh,
+                       scale, part, splits, chunk, context);
+    launch_merge(part, splits, chunk, heads, pos, out, st, n);
     return (int)hipGetLastError();
 }
 

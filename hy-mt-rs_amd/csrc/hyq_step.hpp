@@ -17,11 +17,19 @@ struct StepState {
 };
 
 int launch_embed_row(int fmt, WView w, int cols, const int *token, float *out, void *stream);
+// Rows out[i] = embedding row tokens[i] for i < n (tokens in device memory).
+int launch_embed_rows(int fmt, WView w, int cols, const int *tokens, int n, float *out,
+                      void *stream);
 int launch_rms_norm_q8(const float *x, const float *w, int n, float eps, float *y, int8_t *q,
                        float *s, int32_t *s16, int32_t *s32, int32_t *s256, void *stream);
 int launch_rope_norm_kv(float *q, const float *k, const float *v, const float *qn,
                         const float *kn, const float *freq, const int *pos, int heads, int kvh,
                         int dim, float eps, float *kcache, float *vcache, void *stream);
+// The same for n tokens of a chunk: rows q[i], k[i], v[i] at position *pos + i.
+int launch_rope_norm_kv_rows(float *q, const float *k, const float *v, const float *qn,
+                             const float *kn, const float *freq, const int *pos, int n,
+                             int heads, int kvh, int dim, float eps, float *kcache,
+                             float *vcache, void *stream);
 // Attention splits: `chunk` positions each (a multiple of ATT_SUB), at most
 // ATT_MAX_SPLITS; partials are [heads][splits][PART_STRIDE] floats holding
 // (max, exp-sum, -, -, exp-weighted V sum[128]).
@@ -33,11 +41,21 @@ constexpr int ATT_MAX_REP = 4; // query heads per KV head (one per wave)
 constexpr int PART_STRIDE = 132;
 int attention_chunk(int context);
 int attention_splits(int context);
+// Splits of the chunked-prefill attention (each of prefill_attention_chunk
+// positions); its partials are [n][heads][splits][PART_STRIDE].
+int prefill_attention_chunk(int context);
+int prefill_attention_splits(int context);
 int launch_zero_u32(unsigned *p, int n, void *stream);
 // Attention of one query token over cache rows 0..=*pos (q already rotated
 // and normalized), merged into out [heads*128].
 int launch_attention(const float *q, const float *kcache, const float *vcache, const int *pos,
                      int context, int heads, int kvh, float *part, float *out, void *stream);
+// Causal attention of the n query rows q [n][heads*128] of a chunk whose
+// keys and values are in the cache: row i at position *pos + i sees cache
+// rows 0..=*pos + i; merged into out [n][heads*128].
+int launch_attention_rows(const float *q, const float *kcache, const float *vcache,
+                          const int *pos, int n, int context, int heads, int kvh, float *part,
+                          float *out, void *stream);
 // Merge of the split partials into out [heads*128].
 int launch_attention_merge(const float *part, int context, int heads, const int *pos,
                            float *out, void *stream);

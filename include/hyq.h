@@ -209,6 +209,17 @@ int hyq_attention_d(hyq_ctx *ctx, const float *q_d, const float *kcache_d,
                     const float *vcache_d, const int32_t *pos_d, size_t context, size_t heads,
                     size_t kv_heads, size_t head_dim, float *scratch_d, float *out_d,
                     hyq_q8 *out_q8);
+/* attention (src/model.rs:949-1037) for n query rows of a chunk whose keys
+ * and values are already in the cache: row i (q_d [n][heads*128]) is the
+ * token at position *pos_d + i and sees cache rows 0..=*pos_d + i (causal,
+ * :956-961). out_d is [n][heads*128] f32; scratch_d holds
+ * hyq_attention_rows_scratch_floats(context, heads, n) floats. Rows past
+ * `context` are never read. */
+size_t hyq_attention_rows_scratch_floats(size_t context, size_t heads, size_t n);
+int hyq_attention_rows_d(hyq_ctx *ctx, const float *q_d, const float *kcache_d,
+                         const float *vcache_d, const int32_t *pos_d, size_t n, size_t context,
+                         size_t heads, size_t kv_heads, size_t head_dim, float *scratch_d,
+                         float *out_d);
 /* Greedy sampling (src/generation.rs:281-290): index of the first maximum.
  * scratch_d holds 128 floats. */
 int hyq_argmax_d(hyq_ctx *ctx, const float *x_d, size_t n, float *scratch_d, int32_t *token_d);
@@ -243,6 +254,18 @@ int hyq_dense_get_position(hyq_dense *m, size_t *position);
  * K/V at the current position, advances it, and returns the logits (if
  * non-null) and the greedy next token (if non-null). */
 int hyq_dense_forward(hyq_dense *m, int32_t token, float *logits, int32_t *next);
+/* Model::prefill_into (src/model.rs:630-646): the prompt in chunks of up to
+ * 256 tokens (PREFILL_CHUNK, :18), each through forward_into at batch n
+ * (:549-616, f16-MFMA products; a one-token chunk is the batch-1 step).
+ * Appends every token's K/V from the current position, advances it by n,
+ * and returns the last token's logits (if non-null) and greedy next token
+ * (if non-null). HYQ_EINVAL for an empty prompt, one that exceeds the
+ * context, or a token outside the vocabulary (checked before any work). */
+int hyq_dense_prefill(hyq_dense *m, const int32_t *tokens, size_t n, float *logits,
+                      int32_t *next);
+/* Reads cached keys/values [positions][kv_heads*head_dim] of one layer
+ * (the Session's KvCache, src/model.rs:650-669). */
+int hyq_dense_read_kv(hyq_dense *m, int layer, size_t positions, float *keys, float *values);
 /* Greedy decoding (Generator::generate at temperature 0 and repetition
  * penalty 1): feeds `token`, then each argmax, for `steps` steps; tokens[i]
  * is the argmax after step i. use_graph = 1 replays one captured HIP graph

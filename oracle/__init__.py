@@ -72,6 +72,8 @@ def _declare(L: ctypes.CDLL) -> None:
         "hyqo_attention": (None, [P, P, P, SZ, SZ, SZ, SZ, P]),
         "hyqo_decode_step": (ctypes.c_int, [P, P, P, SZ, SZ, ctypes.c_int, ctypes.c_int, P,
                                             ctypes.c_int]),
+        "hyqo_prefill_chunk": (ctypes.c_int, [P, P, P, SZ, SZ, P, SZ, ctypes.c_int, P,
+                                              ctypes.c_int]),
         "hyqo_argmax": (ctypes.c_int, [P, SZ]),
         "hyqo_max_threads": (ctypes.c_int, []),
     }
@@ -276,4 +278,22 @@ class DenseOracle:
                                     token, int(int8_path), _p(logits), threads)
         if rc != 0:
             raise ValueError("decode_step: bad position or token")
+        return logits
+
+    def prefill(self, kcache: np.ndarray, vcache: np.ndarray, pos: int, tokens,
+                int8_path: bool, threads: int = 0, chunk: int = 256) -> np.ndarray:
+        """Model::prefill_into (src/model.rs:630-646): chunks of `chunk` tokens
+        through forward_into at batch n; the last chunk's logits."""
+        assert kcache.flags["C_CONTIGUOUS"] and vcache.flags["C_CONTIGUOUS"]
+        toks = np.ascontiguousarray(tokens, np.int32)
+        if toks.size == 0 or pos + toks.size > kcache.shape[1]:
+            raise ValueError("prompt is empty or exceeds the context limit")
+        logits = np.empty(self.model["cfg"]["vocab"], np.float32)
+        for s in range(0, toks.size, chunk):
+            part = toks[s:s + chunk]
+            rc = lib().hyqo_prefill_chunk(ctypes.byref(self.m), _p(kcache), _p(vcache),
+                                          kcache.shape[1], pos + s, _p(part), part.size,
+                                          int(int8_path), _p(logits), threads)
+            if rc != 0:
+                raise ValueError("prefill_chunk: bad position or token")
         return logits

@@ -12,7 +12,10 @@
  *                  value of the integer formula rounded once to f32.
  * The glue follows the x86 arms of rms_norm_into (src/model.rs:785-830),
  * rms_norm (:832-870), rope_with_cache (:874-917), attention_into
- * (:949-1035) and add (:1043-1077).
+ * (:949-1035) and add (:1043-1077). hyqo_prefill_chunk is the batch > 1
+ * arm of forward_into (src/model.rs:549-616): f32 activations through the
+ * batched Weight::matmul (src/quant.rs:272-343), and the last row's logits
+ * through the batch-1 matmul of the chosen arm.
  */
 #include "hyq_oracle.h"
 #include "hyq_oracle_step.h"
@@ -198,6 +201,91 @@ int hyqo_decode_step(const hyqo_model *m, float *kcache, float *vcache, size_t c
     hyqo_rms_norm_rows(hidden, m->output_norm, H, H, m->eps);
     linear(m, m->dtype_embed, m->output ? m->output : m->embed, (size_t)m->vocab, H, hidden,
            logits, int8_path, threads);
+
+    free(hidden);
+    free(xn);
+    free(q);
+    free(k);
+    free(v);
+    free(att);
+    free(proj);
+    free(gate);
+    free(up);
+    return 0;
+}
+
+int hyqo_prefill_chunk(const hyqo_model *m, float *kcache, float *vcache, size_t ctx, size_t pos,
+                       const int *tokens, size_t n, int int8_path, float *logits, int threads)
+{
+    size_t H = (size_t)m->hidden, D = (size_t)m->head_dim;
+    size_t qlen = (size_t)m->heads * D, kvw = (size_t)m->kv_heads * D, F = (size_t)m->ffn;
+    if (n == 0 || pos + n > ctx) return -1;
+    for (size_t t = 0; t < n; ++t)
+        if (tokens[t] < 0 || tokens[t] >= m->vocab) return -1;
+    /* a one-token chunk takes the batch-1 arm (src/model.rs:557-558) */
+    if (n == 1) return hyqo_decode_step(m, kcache, vcache, ctx, pos, tokens[0], int8_path, logits,
+                                        threads);
+    float *hidden = (float *)malloc(sizeof(float) * n * H);
+    float *xn = (float *)malloc(sizeof(float) * n * H);
+    float *q = (float *)malloc(sizeof(float) * n * qlen);
+    float *k = (float *)malloc(sizeof(float) * n * kvw);
+    float *v = (float *)malloc(sizeof(float) * n * kvw);
+    float *att = (float *)malloc(sizeof(float) * n * qlen);
+    float *proj = (float *)malloc(sizeof(float) * n * H);
+    float *gate = (float *)malloc(sizeof(float) * n * F);
+    float *up = (float *)malloc(sizeof(float) * n * F);
+    float cos_s[512], sin_s[512];
+
+    /* embedding rows (src/model.rs:549-552) */
+    size_t erb = rb_of(m->dtype_embed, H);
+    for (size_t t = 0; t < n; ++t)
+        hyqo_decode(m->dtype_embed, m->embed + (size_t)tokens[t] * erb, erb, hidden + t * H, H);
+
+    for (int l = 0; l < m->layers; ++l) {
+        float *kc = kcache + (size_t)l * ctx * kvw;
+        float *vc = vcache + (size_t)l * ctx * kvw;
+        /* normalized = rms_norm(hidden) row by row; q/k/v = matmul(., batch) (:555-564) */
+        memcpy(xn, hidden, sizeof(float) * n * H);
+        hyqo_rms_norm_rows(xn, m->attn_norm[l], n * H, H, m->eps);
+        hyqo_matmul(m->dtype_linear, m->wq[l], qlen, H, xn, n, q, threads);
+        hyqo_matmul(m->dtype_linear, m->wk[l], kvw, H, xn, n, k, threads);
+        hyqo_matmul(m->dtype_linear, m->wv[l], kvw, H, xn, n, v, threads);
+        /* rope at start + token (src/model.rs:570-583, 919-947), then the dense
+         * order's per-head norms (:584-587) */
+        for (size_t t = 0; t < n; ++t) {
+            hyqo_rope_tables(D, m->rope_base, pos + t, cos_s, sin_s);
+            hyqo_rope(q + t * qlen, (size_t)m->heads, D, cos_s, sin_s);
+            hyqo_rope(k + t * kvw, (size_t)m->kv_heads, D, cos_s, sin_s);
+        }
+        hyqo_rms_norm_rows(q, m->q_norm[l], n * qlen, D, m->eps);
+        hyqo_rms_norm_rows(k, m->k_norm[l], n * kvw, D, m->eps);
+        /* cache.append (:588-593, 650-669), then causal attention: token t sees
+         * positions 0..=pos+t (src/model.rs:956-961) */
+        memcpy(kc + pos * kvw, k, sizeof(float) * n * kvw);
+        memcpy(vc + pos * kvw, v, sizeof(float) * n * kvw);
+        for (size_t t = 0; t < n; ++t)
+            hyqo_attention(q + t * qlen, kc, vc, (size_t)m->heads, (size_t)m->kv_heads, D,
+                           pos + t + 1, att + t * qlen);
+        hyqo_matmul(m->dtype_linear, m->wo[l], H, qlen, att, n, proj, threads);
+        for (size_t i = 0; i < n * H; ++i) hidden[i] += proj[i];
+        /* DenseFfn::forward at batch n (src/model.rs:672-685): two matmuls,
+         * silu(g) * u, down */
+        memcpy(xn, hidden, sizeof(float) * n * H);
+        hyqo_rms_norm_rows(xn, m->ffn_norm[l], n * H, H, m->eps);
+        hyqo_matmul(m->dtype_linear, m->wgate[l], F, H, xn, n, gate, threads);
+        hyqo_matmul(m->dtype_linear, m->wup[l], F, H, xn, n, up, threads);
+        for (size_t i = 0; i < n * F; ++i) {
+            float g = gate[i];
+            gate[i] = (g / (1.0f + expf(-g))) * up[i];
+        }
+        hyqo_matmul(m->dtype_linear, m->wdown[l], H, F, gate, n, proj, threads);
+        for (size_t i = 0; i < n * H; ++i) hidden[i] += proj[i];
+    }
+    /* the last row's output norm and a batch-1 matmul (src/model.rs:605-607) */
+    float *last = hidden + (n - 1) * H;
+    hyqo_rms_norm_rows(last, m->output_norm, H, H, m->eps);
+    linear(m, m->dtype_embed, m->output ? m->output : m->embed, (size_t)m->vocab, H, last, logits,
+           int8_path, threads);
 
     free(hidden);
     free(xn);

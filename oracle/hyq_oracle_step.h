@@ -34,6 +34,13 @@ void hyqo_attention(const float *q, const float *keys, const float *values, size
  * position `pos` and attends over 0..=pos. */
 int hyqo_decode_step(const hyqo_model *m, float *kcache, float *vcache, size_t ctx, size_t pos,
                      int token, int int8_path, float *logits, int threads);
+/* One chunk of Model::forward_into at batch n (src/model.rs:549-616): the
+ * tokens take positions pos..pos+n-1 (written to the caches); logits are the
+ * last row's, through the batch-1 matmul of the int8 or f32 arm. n == 1 is
+ * hyqo_decode_step. Returns -1 on an empty chunk, the context limit or a
+ * token outside the vocabulary. */
+int hyqo_prefill_chunk(const hyqo_model *m, float *kcache, float *vcache, size_t ctx, size_t pos,
+                       const int *tokens, size_t n, int int8_path, float *logits, int threads);
 int hyqo_argmax(const float *x, size_t n);
 /* OpenMP threads the matmul/attention loops use when threads <= 0. */
 int hyqo_max_threads(void);

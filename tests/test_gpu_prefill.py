@@ -1,0 +1,177 @@
+"""GPU parity of the chunked prefill (hyq_dense_prefill: Model::prefill_into
+and the batch > 1 arm of forward_into, src/model.rs:549-646) and of its
+batched causal attention against the oracle, through the C ABI.
+
+Tolerances (floating point, stated per test): the batched attention within a
+few f32 ulps of the oracle (rtol 1e-5, atol 1e-6, as the one-token
+attention). The prefill's products round activations and weights to f16
+(2^-11 relative each) where the oracle's batched products are f32, so the
+last row's logits and the appended K/V rows are held to 1e-2 relative in the
+2-norm. A one-token prompt takes the batch-1 step: bit-identical to
+hyq_dense_forward."""
+import numpy as np
+import pytest
+
+from synth import Q2_0C, Q6_K, STQ1_0, load_dense, make_dense_model, make_kv_cache, random_matrix
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(layers=2, hidden=512, heads=4, kv_heads=1, head_dim=128, ffn=1024, vocab=3000,
+             rope_base=11158840.0, rms_eps=1e-5)
+
+
+def _print(*a):
+    print(*a, flush=True)
+
+
+def _rel(a, b):
+    return float(np.linalg.norm(np.asarray(a, np.float64) - b) / np.linalg.norm(b))
+
+
+def _attention_rows(hyq, gpu_ctx, q, kc, vc, pos, n, heads, kvh):
+    L = hyq.lib()
+    ctxlen = kc.shape[0]
+    qd, kd, vd = gpu_ctx.array(q), gpu_ctx.array(kc), gpu_ctx.array(vc)
+    posd = gpu_ctx.array(np.array([pos], np.int32))
+    scratch = gpu_ctx.empty(L.hyq_attention_rows_scratch_floats(ctxlen, heads, n), np.float32)
+    out = gpu_ctx.empty(n * heads * 128, np.float32)
+    hyq.check(L.hyq_attention_rows_d(gpu_ctx.handle, qd.ptr, kd.ptr, vd.ptr, posd.ptr, n,
+                                     ctxlen, heads, kvh, 128, scratch.ptr, out.ptr))
+    return out.numpy().reshape(n, heads * 128)
+
+
+@pytest.mark.parametrize("pos,n", [(0, 1), (0, 37), (100, 64), (1000, 152), (5, 256)])
+def test_attention_rows_matches_oracle(gpu_ctx, hyq, oracle, pos, n):
+    heads, kvh, D, ctxlen = 16, 4, 128, 1152
+    _print("attention_rows", pos, n)
+    rng = np.random.default_rng(pos * 1000 + n)
+    q = rng.normal(0, 1, (n, heads * D)).astype(np.float32)
+    kc = rng.normal(0, 1, (ctxlen, kvh * D)).astype(np.float32)
+    vc = rng.normal(0, 1, (ctxlen, kvh * D)).astype(np.float32)
+    got = _attention_rows(hyq, gpu_ctx, q, kc, vc, pos, n, heads, kvh)
+    for i in range(n):
+        ref = np.empty(heads * D, np.float32)
+        oracle.lib().hyqo_attention(q[i].ctypes.data, kc.ctypes.data, vc.ctypes.data, heads,
+                                    kvh, D, pos + i + 1, ref.ctypes.data)
+        assert np.allclose(got[i], ref, rtol=1e-5, atol=1e-6), (i, np.abs(got[i] - ref).max())
+
+
+def test_attention_rows_do_not_see_future_values(gpu_ctx, hyq):
+    """src/model.rs:1104-1125 at head_dim 128: zero queries and keys, two
+    rows at positions 0 and 1 average the values they can see."""
+    heads, kvh, D = 2, 1, 128
+    vc = np.zeros((2, D), np.float32)
+    vc[0, :2] = [2.0, 4.0]
+    vc[1, :2] = [100.0, 200.0]
+    got = _attention_rows(hyq, gpu_ctx, np.zeros((2, heads * D), np.float32),
+                          np.zeros((2, D), np.float32), vc, 0, 2, heads, kvh)
+    o = got.reshape(2, heads, D)
+    assert np.array_equal(o[0, :, :2], [[2.0, 4.0], [2.0, 4.0]])
+    assert np.array_equal(o[1, :, :2], [[51.0, 102.0], [51.0, 102.0]])
+    assert not o[:, :, 2:].any()
+
+
+def _model(linear, seed):
+    c = SMALL
+    model = make_dense_model(c, linear=linear, seed=seed)
+    model["output"] = random_matrix(Q6_K, c["vocab"], c["hidden"], seed + 50)
+    return model
+
+
+def _decoder(hyq, gpu_ctx, model, context, past, seed):
+    c = model["cfg"]
+    dec = load_dense(hyq, gpu_ctx, model, context)
+    k, v = make_kv_cache(c, context, past, seed=seed)
+    for l in range(c["layers"]):
+        dec.load_kv(l, k[l, :past], v[l, :past])
+    dec.position = past
+    return dec, k, v
+
+
+@pytest.mark.parametrize("linear,n", [(Q2_0C, 2), (Q2_0C, 37), (Q2_0C, 300), (STQ1_0, 9),
+                                      (STQ1_0, 256)])
+def test_prefill_matches_oracle(gpu_ctx, hyq, oracle, linear, n):
+    """300 tokens run as chunks of 256 and 44 (PREFILL_CHUNK, src/model.rs:18)."""
+    c = SMALL
+    context, past = 320, 5
+    _print("prefill", linear, n)
+    model = _model(linear, seed=7)
+    dec, k, v = _decoder(hyq, gpu_ctx, model, context, past, seed=7)
+    tokens = np.random.default_rng(n).integers(0, c["vocab"], n).astype(np.int32)
+    logits, nxt = dec.prefill(tokens)
+    assert dec.position == past + n
+    ref = oracle.DenseOracle(model)
+    ref_logits = ref.prefill(k, v, past, tokens, int8_path=True)
+    rel = _rel(logits, ref_logits)
+    _print("  logits rel", rel)
+    assert rel <= 1e-2, rel
+    assert nxt == int(np.argmax(logits))
+    top = np.sort(ref_logits)[-2:]
+    if top[1] - top[0] > 2e-2 * np.abs(ref_logits).max():
+        assert nxt == int(np.argmax(ref_logits))
+    for l in range(c["layers"]):
+        kg, vg = dec.read_kv(l, past + n)
+        assert np.array_equal(kg[:past], k[l, :past]) and np.array_equal(vg[:past], v[l, :past])
+        rk, rv = _rel(kg[past:], k[l, past:past + n]), _rel(vg[past:], v[l, past:past + n])
+        _print("  layer", l, "kv rel", rk, rv)
+        assert rk <= 1e-2 and rv <= 1e-2, (l, rk, rv)
+    dec.close()
+
+
+def test_prefill_of_one_token_is_the_decode_step(gpu_ctx, hyq):
+    c = SMALL
+    model = _model(Q2_0C, seed=8)
+    a, _, _ = _decoder(hyq, gpu_ctx, model, 32, 11, seed=8)
+    b, _, _ = _decoder(hyq, gpu_ctx, model, 32, 11, seed=8)
+    la, ta = a.prefill([123])
+    lb, tb = b.forward(123)
+    assert ta == tb and np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    assert a.position == b.position == 12
+    for l in range(c["layers"]):
+        for x, y in zip(a.read_kv(l, 12), b.read_kv(l, 12)):
+            assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+    a.close()
+    b.close()
+
+
+def test_decode_continues_after_prefill(gpu_ctx, hyq, oracle):
+    """Batch-1 steps after a prefill attend to the prefilled rows: each
+    step's logits match the oracle's int8 step on the GPU's own cache (the
+    decode-step tolerance, 5e-3 relative)."""
+    c = SMALL
+    context, past, n = 64, 3, 40
+    model = _model(Q2_0C, seed=9)
+    dec, _, _ = _decoder(hyq, gpu_ctx, model, context, past, seed=9)
+    tokens = np.random.default_rng(1).integers(0, c["vocab"], n).astype(np.int32)
+    _, token = dec.prefill(tokens)
+    ref = oracle.DenseOracle(model)
+    kvw = c["kv_heads"] * c["head_dim"]
+    for i in range(3):
+        pos = past + n + i
+        k = np.zeros((c["layers"], context, kvw), np.float32)
+        v = np.zeros_like(k)
+        for l in range(c["layers"]):
+            k[l, :pos], v[l, :pos] = dec.read_kv(l, pos)
+        logits, nxt = dec.forward(token)
+        ref_logits = ref.step(k, v, pos, token, int8_path=True)
+        rel = _rel(logits, ref_logits)
+        assert rel <= 5e-3, (i, rel)
+        token = nxt
+    assert dec.position == past + n + 3
+    dec.close()
+
+
+def test_prefill_errors(gpu_ctx, hyq):
+    c = SMALL
+    model = _model(Q2_0C, seed=2)
+    dec, _, _ = _decoder(hyq, gpu_ctx, model, 16, 4, seed=2)
+    with pytest.raises(ValueError):
+        dec.prefill([])  # prompt must contain at least one token
+    with pytest.raises(ValueError):
+        dec.prefill(np.arange(13))  # prompt exceeds context limit
+    with pytest.raises(ValueError):
+        dec.prefill([1, c["vocab"]])  # input token outside vocabulary
+    assert dec.position == 4
+    _, t = dec.prefill(np.arange(12))  # exactly fills the context
+    assert dec.position == 16
+    dec.close()
