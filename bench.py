@@ -28,6 +28,8 @@ Also reported, from live HIP-event timings on the context stream:
                   the 1.8B Q2_0C/STQ1_0 set; Q6_K lm_head), Q8 input, weights
                   rotated over >= 512 MiB;
   prefill, moe    the batched f16-MFMA GEMM (TFLOP/s) and the MoE expert layer;
+  prefill_1p8b    the same model's chunked prefill of a 1024-token prompt
+                  (hyq_dense_prefill), wall-clock tok/s;
   cpu_baseline    the reference's x86 decode step (f32 activations, scalar
                   Q2_0C row dot, AVX2 dot; oracle/hyq_oracle_step.c), timed on
                   this host's cores on a bounded sample of the same workload.
@@ -128,6 +130,28 @@ def prefill_rate(hyq, ctx, ev, dtype, rows, cols, batch, seed=3):
     flop = 2.0 * rows * cols * batch
     W.release()
     return ms * 1e3, flop / (ms * 1e-3) / 1e12
+
+
+def prefill_e2e(dec, cfg, tokens: int, runs: int = 3) -> dict:
+    """Model::prefill_into of a `tokens`-token prompt from position 0 (chunks of
+    256 through the batch > 1 forward pass, last row's logits and argmax):
+    best wall-clock time of `runs` after one untimed run. linear_TFLOPs counts
+    2 * tokens * (Q/K/V/o/gate/up/down weights) multiply-adds per second."""
+    ids = np.random.default_rng(11).integers(0, cfg["vocab"], tokens).astype(np.int32)
+    best = None
+    for r in range(runs + 1):
+        dec.position = 0
+        t0 = time.perf_counter()
+        dec.prefill(ids, want_logits=False)
+        dt = time.perf_counter() - t0
+        if r and (best is None or dt < best):
+            best = dt
+    H, F, D = cfg["hidden"], cfg["ffn"], cfg["head_dim"]
+    QL, KV = cfg["heads"] * D, cfg["kv_heads"] * D
+    per_layer = H * (QL + 2 * KV) + QL * H + 2 * H * F + F * H
+    flop = 2.0 * tokens * cfg["layers"] * per_layer
+    return dict(tokens=tokens, ms=round(best * 1e3, 3), tok_s=round(tokens / best, 1),
+                linear_TFLOPs=round(flop / best / 1e12, 1))
 
 
 def moe_rate(hyq, ctx, ev, tokens=64, experts=64, used=8, hidden=2048, mid=1536, seed=5):
@@ -438,6 +462,12 @@ def main() -> int:
                                  frac=round(tf / MFMA_F16_PEAK_TFLOPS, 4))
             log(f"{name}: {us:.1f} us {tf:.0f} TFLOP/s")
 
+    pf = None
+    if not args.no_prefill:
+        pf = prefill_e2e(dec, cfg, PREFILLED)
+        log(f"1.8B prefill of a {PREFILLED}-token prompt: {pf['ms']:.2f} ms, "
+            f"{pf['tok_s']:.0f} tok/s, {pf['linear_TFLOPs']:.0f} TFLOP/s in the linears")
+
     moe = None
     if not args.no_prefill:
         moe = moe_rate(hyq, ctx, ev)
@@ -467,6 +497,7 @@ def main() -> int:
         "decode_kernels": table,
         "gemv": gemv,
         "prefill": prefill,
+        "prefill_1p8b": pf,
         "moe": moe,
         "reference_published": {"value": 86.86, "unit": "tok/s",
                                 "note": "Apple M2 Pro 8 threads, real weights, ~14-18 "
