@@ -634,19 +634,11 @@ int launch_attention(const float *q, const float *kcache, const float *vcache, c
     return (int)hipGetLastError();
 }
 
-int launch_attention_rows(const float *q, const float *kcache, const float *vcache,
-                          const int *pos, int n, int context, int heads, int kvh, float *part,
-                          float *out, void *stream)
+int launch_attention_merge_rows(const float *part, int splits, int chunk, int heads,
+                                const int *pos, int n, float *out, void *stream)
 {
     if (n <= 0) return 0;
-    const int splits = prefill_attention_splits(context), chunk = prefill_attention_chunk(context);
-    const float scale = 1.0f / sqrtf(128.0f);
-    hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(attn_kernel, dim3(splits, kvh, n), dim3(ATT_THREADS), 0, st, false, q,
-                       nullptr, nullptr, nullptr, nullptr, nullptr, 0.f,
-                       const_cast<float *>(kcache), const_cast<float *>(vcache), pos, heads, kvh,
-                       scale, part, splits, chunk, context);
-    launch_merge(part, splits, chunk, heads, pos, out, st, n);
+    launch_merge(part, splits, chunk, heads, pos, out, (hipStream_t)stream, n);
     return (int)hipGetLastError();
 }
 

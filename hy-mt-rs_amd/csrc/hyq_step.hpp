@@ -52,10 +52,15 @@ int launch_attention(const float *q, const float *kcache, const float *vcache, c
                      int context, int heads, int kvh, float *part, float *out, void *stream);
 // Causal attention of the n query rows q [n][heads*128] of a chunk whose
 // keys and values are in the cache: row i at position *pos + i sees cache
-// rows 0..=*pos + i; merged into out [n][heads*128].
+// rows 0..=*pos + i; merged into out [n][heads*128] (hyq_attn_rows.hip: f16
+// matrix-core products of split f16 operand pairs).
 int launch_attention_rows(const float *q, const float *kcache, const float *vcache,
                           const int *pos, int n, int context, int heads, int kvh, float *part,
                           float *out, void *stream);
+// Merge of n query rows' split partials ([n][heads][splits][PART_STRIDE],
+// `chunk` positions per split) into out [n][heads*128].
+int launch_attention_merge_rows(const float *part, int splits, int chunk, int heads,
+                                const int *pos, int n, float *out, void *stream);
 // Merge of the split partials into out [heads*128].
 int launch_attention_merge(const float *part, int context, int heads, const int *pos,
                            float *out, void *stream);

@@ -2,10 +2,11 @@
 and the batch > 1 arm of forward_into, src/model.rs:549-646) and of its
 batched causal attention against the oracle, through the C ABI.
 
-Tolerances (floating point, stated per test): the batched attention within a
-few f32 ulps of the oracle (rtol 1e-5, atol 1e-6, as the one-token
-attention). The prefill's products round activations and weights to f16
-(2^-11 relative each) where the oracle's batched products are f32, so the
+Tolerances (floating point, stated per test): the batched attention within
+rtol 1e-5, atol 1e-6 of the oracle, as the one-token attention (its matrix
+products carry f16 operand pairs hi + lo, within 2^-21 of f32). The
+prefill's products round activations and weights to f16 (2^-11 relative
+each) where the oracle's batched products are f32, so the
 last row's logits and the appended K/V rows are held to 1e-2 relative in the
 2-norm. A one-token prompt takes the batch-1 step: bit-identical to
 hyq_dense_forward."""
@@ -40,10 +41,14 @@ def _attention_rows(hyq, gpu_ctx, q, kc, vc, pos, n, heads, kvh):
     return out.numpy().reshape(n, heads * 128)
 
 
-@pytest.mark.parametrize("pos,n", [(0, 1), (0, 37), (100, 64), (1000, 152), (5, 256)])
-def test_attention_rows_matches_oracle(gpu_ctx, hyq, oracle, pos, n):
-    heads, kvh, D, ctxlen = 16, 4, 128, 1152
-    _print("attention_rows", pos, n)
+@pytest.mark.parametrize("pos,n,heads,kvh", [(0, 1, 16, 4), (0, 37, 16, 4), (100, 64, 16, 4),
+                                             (1000, 152, 16, 4), (5, 256, 16, 4),
+                                             (70, 200, 4, 4), (33, 99, 8, 4), (300, 45, 12, 4),
+                                             (0, 300, 16, 4)])
+def test_attention_rows_matches_oracle(gpu_ctx, hyq, oracle, pos, n, heads, kvh):
+    """Query heads per KV head 4, 1, 2 and 3; chunks from 1 to 300 rows."""
+    D, ctxlen = 128, 1152
+    _print("attention_rows", pos, n, heads, kvh)
     rng = np.random.default_rng(pos * 1000 + n)
     q = rng.normal(0, 1, (n, heads * D)).astype(np.float32)
     kc = rng.normal(0, 1, (ctxlen, kvh * D)).astype(np.float32)
