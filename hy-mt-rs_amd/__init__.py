@@ -82,6 +82,7 @@ SIGNATURES = {
     "hyq_dense_forward": (I, [P, ctypes.c_int32, P, P]),
     "hyq_dense_prefill": (I, [P, P, SZ, P, P]),
     "hyq_dense_read_kv": (I, [P, I, SZ, P, P]),
+    "hyq_dense_set_prefill_rows": (I, [P, SZ]),
     "hyq_dense_generate": (I, [P, ctypes.c_int32, SZ, I, P]),
 }
 
@@ -438,8 +439,9 @@ class DenseDecoder:
         return logits, nxt.value
 
     def prefill(self, tokens, want_logits: bool = True):
-        """Model::prefill_into (src/model.rs:630-646): the prompt in chunks of
-        up to 256 tokens; returns (last logits or None, greedy next token)."""
+        """Model::prefill_into (src/model.rs:630-646): the prompt through the
+        batch > 1 forward pass; returns (last logits or None, greedy next
+        token)."""
         toks = np.ascontiguousarray(tokens, np.int32)
         logits = np.empty(self.cfg.vocab, np.float32) if want_logits else None
         nxt = ctypes.c_int32()
@@ -447,6 +449,10 @@ class DenseDecoder:
                                       _ptr(logits) if logits is not None else None,
                                       ctypes.byref(nxt)))
         return logits, nxt.value
+
+    def set_prefill_rows(self, rows: int) -> None:
+        """Tokens per device pass of prefill (results do not depend on it)."""
+        check(lib().hyq_dense_set_prefill_rows(self.handle, rows))
 
     def read_kv(self, layer: int, positions: int):
         """Cached keys and values [positions, kv_heads*head_dim] of one layer."""

@@ -8,15 +8,19 @@
 // Q8 -> lm_head GEMV -> argmax. Position and token stay in device memory, so
 // one step is captured once as a HIP graph and replayed per token.
 //
-// hyq_dense_prefill runs a prompt in chunks of up to PREFILL_CHUNK tokens
-// through the batch > 1 arm (src/model.rs:549-616, 630-646): per layer the
-// RMSNorm of every row fused with its f16 rounding, the Q, K and V
-// f16-MFMA GEMMs, RoPE + Q/K norm + KV append for all rows, causal attention
-// of every row over the cache, the attention-output GEMM with the residual
-// add in its epilogue, the FFN norm, the gate/up GEMM with silu(g)*u in its
-// epilogue and the down GEMM with the residual add; then the last row's
-// output norm, the lm_head GEMV and the argmax. A one-token chunk is the
-// batch-1 decode step, as in the reference.
+// hyq_dense_prefill runs a prompt through the batch > 1 arm
+// (src/model.rs:549-616, 630-646): per layer the RMSNorm of every row fused
+// with its f16 rounding, one f16-MFMA GEMM for Q, K and V, RoPE + Q/K norm +
+// KV append for all rows, causal attention of every row over the cache, the
+// attention-output GEMM with the residual add in its epilogue, the FFN norm,
+// the gate/up GEMM with silu(g)*u in its epilogue and the down GEMM with the
+// residual add; then the last row's output norm, the lm_head GEMV and the
+// argmax. Every row's result is independent of the other rows of its pass,
+// so the device takes up to `prefill_rows` tokens per pass (default 1024)
+// instead of the reference's 256-token chunks with identical results; the
+// one case where the chunking shows is kept: a prompt of 256k + 1 tokens
+// ends with a one-token chunk, which the reference runs through the batch-1
+// arm, and so does this decoder (the decode step).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -228,6 +232,7 @@ struct hyq_dense {
     // xh [n][max(H, QL, F)] f16 with row scales rs [n]; attention partials;
     // the chunk's token ids
     std::unique_ptr<DeviceBuffer> pf_mem;
+    size_t pf_rows = 1024, pf_cap = 0; // rows per pass; rows the buffers hold
     float *pf_hid = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr;
     float *pf_att = nullptr, *pf_h = nullptr, *pf_rs = nullptr, *pf_part = nullptr;
     _Float16 *pf_xh = nullptr;
@@ -364,9 +369,12 @@ constexpr size_t PREFILL_CHUNK = 256;
 
 int prefill_buffers(hyq_dense *m)
 {
-    if (m->pf_mem) return HYQ_OK;
+    const size_t N = std::min(m->pf_rows, m->context);
+    if (m->pf_mem && m->pf_cap == N) return HYQ_OK;
+    m->pf_mem.reset();
+    m->pf_cap = 0;
     const hyq_dense_config &c = m->cfg;
-    const size_t N = PREFILL_CHUNK, H = (size_t)c.hidden, F = (size_t)c.ffn;
+    const size_t H = (size_t)c.hidden, F = (size_t)c.ffn;
     const size_t QL = (size_t)c.heads * c.head_dim, KV = (size_t)c.kv_heads * c.head_dim;
     size_t off = 0;
     auto take = [&](size_t bytes) {
@@ -395,6 +403,7 @@ int prefill_buffers(hyq_dense *m)
     m->pf_part = (float *)(b + o_part);
     m->pf_tok = (int32_t *)(b + o_tok);
     m->pf_mem = std::move(buf);
+    m->pf_cap = N;
     return HYQ_OK;
 }
 
@@ -415,12 +424,19 @@ int enqueue_prefill_chunk(hyq_dense *m, int n)
         HYQ_LAUNCH(launch_norm_to_f16(m->pf_hid, n, H, L.attn_norm, c.rms_eps, m->pf_xh,
                                       m->pf_rs, st),
                    "norm_to_f16");
-        const hyq_weight *ws[3] = {L.q, L.k, L.v};
-        float *ys[3] = {m->pf_q, m->pf_k, m->pf_v};
-        for (int i = 0; i < 3; ++i)
-            HYQ_LAUNCH(launch_gemm_f16(ws[i]->dtype, ws[i]->view, H, m->pf_xh, m->pf_rs, n, ys[i],
-                                       nullptr, st),
+        {
+            GemmSegs gs{};
+            const hyq_weight *ws[3] = {L.q, L.k, L.v};
+            float *ys[3] = {m->pf_q, m->pf_k, m->pf_v};
+            for (int i = 0; i < 3; ++i) {
+                gs.s[i].w = ws[i]->view;
+                gs.s[i].y = ys[i];
+                gs.s[i].rows = (int)ws[i]->rows;
+            }
+            gs.nseg = 3;
+            HYQ_LAUNCH(launch_gemm_f16_segs(L.q->dtype, gs, H, m->pf_xh, m->pf_rs, n, st),
                        "gemm_qkv");
+        }
         HYQ_LAUNCH(launch_rope_norm_kv_rows(m->pf_q, m->pf_k, m->pf_v, L.q_norm, L.k_norm,
                                             m->freq, pos, n, c.heads, c.kv_heads, c.head_dim,
                                             c.rms_eps, m->kcache(l), m->vcache(l), st),
@@ -705,20 +721,24 @@ int hyq_dense_prefill(hyq_dense *m, const int32_t *tokens, size_t n, float *logi
             return fail(HYQ_EINVAL, "input token outside vocabulary");
     DeviceGuard g(m->ctx->device);
     hipStream_t st = m->ctx->stream;
-    if (n > 1 && (rc = prefill_buffers(m))) return rc;
-    for (size_t s = 0; s < n; s += PREFILL_CHUNK) {
-        const size_t cn = std::min(PREFILL_CHUNK, n - s);
+    // the reference's chunks of PREFILL_CHUNK tokens take the batch-1 arm
+    // only when one token is left over
+    const size_t batched = n % PREFILL_CHUNK == 1 ? n - 1 : n;
+    if (batched && (rc = prefill_buffers(m))) return rc;
+    for (size_t s = 0; s < n;) {
+        const size_t cn = s < batched ? std::min(m->pf_cap, batched - s) : 1;
         if ((rc = write_state(m, tokens[s], 0, 0))) return rc;
-        if (cn == 1) {
-            if ((rc = enqueue_step(m))) return rc;
-        } else {
+        if (s < batched) {
             HYQ_HIP(hipMemcpyAsync(m->pf_tok, tokens + s, cn * 4, hipMemcpyHostToDevice, st),
                     "hipMemcpy(tokens)");
             if ((rc = enqueue_prefill_chunk(m, (int)cn))) return rc;
+        } else if ((rc = enqueue_step(m))) {
+            return rc;
         }
-        // the host-side state and token words are rewritten by the next chunk
+        // the host-side state and token words are rewritten by the next pass
         HYQ_HIP(hipStreamSynchronize(st), "hipStreamSynchronize");
         m->pos_host += cn;
+        s += cn;
     }
     if (logits)
         HYQ_HIP(hipMemcpyAsync(logits, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost,
@@ -728,6 +748,14 @@ int hyq_dense_prefill(hyq_dense *m, const int32_t *tokens, size_t n, float *logi
     HYQ_HIP(hipMemcpyAsync(&nt, m->token, 4, hipMemcpyDeviceToHost, st), "hipMemcpy(token)");
     HYQ_HIP(hipStreamSynchronize(st), "hipStreamSynchronize");
     if (next) *next = nt;
+    return HYQ_OK;
+}
+
+int hyq_dense_set_prefill_rows(hyq_dense *m, size_t rows)
+{
+    if (!m) return fail(HYQ_EINVAL, "dense_set_prefill_rows: null decoder");
+    if (rows == 0 || rows > 65536) return fail(HYQ_EINVAL, "dense: prefill rows %zu", rows);
+    m->pf_rows = rows;
     return HYQ_OK;
 }
 

@@ -108,24 +108,30 @@ __global__ __launch_bounds__(256) void rows_to_f16_kernel(const float *__restric
 
 // Y[n][m] = (X[n] . W[m]) * rscale[n], plus residual[n][m] when given (the
 // residual add of src/model.rs:595, 601 after the product is rounded; it
-// may alias y: each element is read and then written by one thread).
+// may alias y: each element is read and then written by one thread). The
+// row space is up to three weights sharing the activation rows (Q, K and V
+// in one launch); a tile's BM rows lie in one of them (its row count is a
+// multiple of BM, or it is the last).
 template <int F>
-__global__ __launch_bounds__(256, 2) void gemm_f16_kernel(WView w, int M, int K,
+__global__ __launch_bounds__(256, 2) void gemm_f16_kernel(GemmSegs g, int K,
                                                           const _Float16 *__restrict__ xh,
                                                           const float *__restrict__ rscale, int N,
-                                                          float *y, const float *residual,
                                                           int mtiles, int ntiles)
 {
     __shared__ __attribute__((aligned(16))) _Float16 lds[4 * TILE_HALVES];
     const int T = xcd_tile(mtiles * ntiles);
     if (T >= mtiles * ntiles) return;
-    const int m0 = (T / ntiles) * BM, n0 = (T % ntiles) * BN;
+    int mt = T / ntiles, sg = 0;
+    while (sg + 1 < g.nseg && mt >= g.s[sg].tiles) mt -= g.s[sg++].tiles;
+    const GemmSeg &S = g.s[sg];
+    const int M = S.rows;
+    const int m0 = mt * BM, n0 = (T % ntiles) * BN;
     const int wave = threadIdx.x >> 6, wm = wave >> 1, wn = wave & 1;
 
     f32x16 acc[2][2];
     zero_acc(acc);
     auto wsrc = [&](int lrow, WView &v, int &row) {
-        v = w;
+        v = S.w;
         row = m0 + lrow < M ? m0 + lrow : -1;
     };
     auto xrow = [&](int r) -> const _Float16 * {
@@ -134,6 +140,8 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(WView w, int M, int K,
     auto arow = [&](int i) { return wm * 64 + 32 * i; };
     k_loop<F>(wsrc, xrow, arow, K, wn, lds, acc);
 
+    float *y = S.y;
+    const float *residual = S.residual;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -144,11 +152,11 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(WView w, int M, int K,
             const float *rr = residual ? residual + (size_t)n * M : nullptr;
             const float sc = rscale[n];
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int m = m0 + arow(i) + acc_row_in_block(4 * g);
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int m = m0 + arow(i) + acc_row_in_block(4 * g4);
                 if (m + 3 < M && (M & 3) == 0) {
-                    float4 v = make_float4(acc[i][j][4 * g] * sc, acc[i][j][4 * g + 1] * sc,
-                                           acc[i][j][4 * g + 2] * sc, acc[i][j][4 * g + 3] * sc);
+                    float4 v = make_float4(acc[i][j][4 * g4] * sc, acc[i][j][4 * g4 + 1] * sc,
+                                           acc[i][j][4 * g4 + 2] * sc, acc[i][j][4 * g4 + 3] * sc);
                     if (rr) {
                         const float4 a = *reinterpret_cast<const float4 *>(rr + m);
                         v = make_float4(a.x + v.x, a.y + v.y, a.z + v.z, a.w + v.w);
@@ -158,7 +166,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(WView w, int M, int K,
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
                         if (m + e < M) {
-                            const float v = acc[i][j][4 * g + e] * sc;
+                            const float v = acc[i][j][4 * g4 + e] * sc;
                             yr[m + e] = rr ? rr[m + e] + v : v;
                         }
                 }
@@ -483,16 +491,33 @@ int launch_gate_up_f16(int fmt, WView gate, WView up, int cols, const _Float16 *
 int launch_gemm_f16(int fmt, WView w, int cols, const _Float16 *xh, const float *rscale,
                     int batch, float *y, const float *residual, void *stream)
 {
-    if (cols % BK) return (int)hipErrorInvalidValue;
-    const int M = w.rows;
-    const int mtiles = (M + BM - 1) / BM, ntiles = (batch + BN - 1) / BN;
+    GemmSegs g{};
+    g.nseg = 1;
+    g.s[0].w = w;
+    g.s[0].y = y;
+    g.s[0].residual = residual;
+    g.s[0].rows = w.rows;
+    return launch_gemm_f16_segs(fmt, g, cols, xh, rscale, batch, stream);
+}
+
+int launch_gemm_f16_segs(int fmt, GemmSegs g, int cols, const _Float16 *xh, const float *rscale,
+                         int batch, void *stream)
+{
+    if (cols % BK || g.nseg < 1 || g.nseg > 3) return (int)hipErrorInvalidValue;
+    int mtiles = 0;
+    for (int i = 0; i < g.nseg; ++i) {
+        if (i + 1 < g.nseg && g.s[i].rows % BM) return (int)hipErrorInvalidValue;
+        g.s[i].tiles = (g.s[i].rows + BM - 1) / BM;
+        mtiles += g.s[i].tiles;
+    }
+    const int ntiles = (batch + BN - 1) / BN;
     const int per = (mtiles * ntiles + 7) / 8;
     dim3 grid(8 * per), block(256);
     hipStream_t st = (hipStream_t)stream;
 #define HYQ_GEMM(F)                                                                            \
     case F:                                                                                    \
-        hipLaunchKernelGGL(gemm_f16_kernel<F>, grid, block, 0, st, w, M, cols, xh, rscale,      \
-                           batch, y, residual, mtiles, ntiles);                                \
+        hipLaunchKernelGGL(gemm_f16_kernel<F>, grid, block, 0, st, g, cols, xh, rscale, batch,  \
+                           mtiles, ntiles);                                                    \
         break;
     switch (fmt) {
         HYQ_GEMM(Q4_K)

@@ -154,6 +154,22 @@ int launch_norm_to_f16(const float *x, int rows, int K, const float *norm, float
                        _Float16 *xh, float *rscale, void *stream);
 int launch_gemm_f16(int fmt, WView w, int cols, const _Float16 *xh, const float *rscale,
                     int batch, float *y, const float *residual, void *stream);
+// Up to three weights of one format sharing the activation rows (fused
+// Q/K/V): segment i writes y_i [batch][rows_i] (+ residual_i); every segment
+// but the last has a multiple of 128 rows. `tiles` is set by the launcher.
+struct GemmSeg {
+    WView w;
+    float *y;
+    const float *residual;
+    int rows;
+    int tiles;
+};
+struct GemmSegs {
+    GemmSeg s[3];
+    int nseg;
+};
+int launch_gemm_f16_segs(int fmt, GemmSegs g, int cols, const _Float16 *xh, const float *rscale,
+                         int batch, void *stream);
 int launch_gate_up_f16(int fmt, WView gate, WView up, int cols, const _Float16 *xh,
                        const float *rscale, int batch, float *h, void *stream);
 

@@ -254,15 +254,23 @@ int hyq_dense_get_position(hyq_dense *m, size_t *position);
  * K/V at the current position, advances it, and returns the logits (if
  * non-null) and the greedy next token (if non-null). */
 int hyq_dense_forward(hyq_dense *m, int32_t token, float *logits, int32_t *next);
-/* Model::prefill_into (src/model.rs:630-646): the prompt in chunks of up to
- * 256 tokens (PREFILL_CHUNK, :18), each through forward_into at batch n
- * (:549-616, f16-MFMA products; a one-token chunk is the batch-1 step).
+/* Model::prefill_into (src/model.rs:630-646): the prompt through
+ * forward_into at batch n (:549-616, f16-MFMA products), on the device in
+ * passes of hyq_dense_set_prefill_rows tokens; as in the reference's
+ * 256-token chunking (PREFILL_CHUNK, :18), a prompt of 256k + 1 tokens ends
+ * with its last token through the batch-1 step.
  * Appends every token's K/V from the current position, advances it by n,
  * and returns the last token's logits (if non-null) and greedy next token
  * (if non-null). HYQ_EINVAL for an empty prompt, one that exceeds the
  * context, or a token outside the vocabulary (checked before any work). */
 int hyq_dense_prefill(hyq_dense *m, const int32_t *tokens, size_t n, float *logits,
                       int32_t *next);
+/* Tokens per device pass of hyq_dense_prefill (default 1024; 1..65536). The
+ * results do not depend on it; it sets the activation memory: per row about
+ * 4*hidden + 8*(heads + kv_heads)*head_dim + 6*ffn bytes, plus 528 bytes per
+ * query head and attention split. No counterpart in the reference, whose
+ * chunk is fixed. */
+int hyq_dense_set_prefill_rows(hyq_dense *m, size_t rows);
 /* Reads cached keys/values [positions][kv_heads*head_dim] of one layer
  * (the Session's KvCache, src/model.rs:650-669). */
 int hyq_dense_read_kv(hyq_dense *m, int layer, size_t positions, float *keys, float *values);

@@ -94,9 +94,10 @@ def _decoder(hyq, gpu_ctx, model, context, past, seed):
 
 
 @pytest.mark.parametrize("linear,n", [(Q2_0C, 2), (Q2_0C, 37), (Q2_0C, 300), (STQ1_0, 9),
-                                      (STQ1_0, 256)])
+                                      (STQ1_0, 256), (Q2_0C, 257)])
 def test_prefill_matches_oracle(gpu_ctx, hyq, oracle, linear, n):
-    """300 tokens run as chunks of 256 and 44 (PREFILL_CHUNK, src/model.rs:18)."""
+    """The oracle runs 300 tokens as chunks of 256 and 44 (PREFILL_CHUNK,
+    src/model.rs:18), 257 as 256 and a batch-1 step."""
     c = SMALL
     context, past = 320, 5
     _print("prefill", linear, n)
@@ -121,6 +122,41 @@ def test_prefill_matches_oracle(gpu_ctx, hyq, oracle, linear, n):
         _print("  layer", l, "kv rel", rk, rv)
         assert rk <= 1e-2 and rv <= 1e-2, (l, rk, rv)
     dec.close()
+
+
+def test_prefill_results_do_not_depend_on_the_pass_size(gpu_ctx, hyq):
+    c = SMALL
+    model = _model(Q2_0C, seed=6)
+    tokens = np.random.default_rng(6).integers(0, c["vocab"], 300).astype(np.int32)
+    runs = []
+    for rows in (1024, 64, 7, 1):
+        dec, _, _ = _decoder(hyq, gpu_ctx, model, 320, 4, seed=6)
+        dec.set_prefill_rows(rows)
+        logits, nxt = dec.prefill(tokens)
+        kv = [dec.read_kv(l, 304) for l in range(c["layers"])]
+        runs.append((logits, nxt, kv))
+        dec.close()
+    for logits, nxt, kv in runs[1:]:
+        assert nxt == runs[0][1]
+        assert np.array_equal(logits.view(np.uint32), runs[0][0].view(np.uint32))
+        for (k, v), (k0, v0) in zip(kv, runs[0][2]):
+            assert np.array_equal(k.view(np.uint32), k0.view(np.uint32))
+            assert np.array_equal(v.view(np.uint32), v0.view(np.uint32))
+
+
+def test_prompt_of_256k_plus_1_ends_with_the_decode_step(gpu_ctx, hyq):
+    """src/model.rs:642-644: the last of 257 tokens is a one-token chunk."""
+    c = SMALL
+    model = _model(Q2_0C, seed=5)
+    tokens = np.random.default_rng(5).integers(0, c["vocab"], 257).astype(np.int32)
+    a, _, _ = _decoder(hyq, gpu_ctx, model, 300, 2, seed=5)
+    b, _, _ = _decoder(hyq, gpu_ctx, model, 300, 2, seed=5)
+    la, ta = a.prefill(tokens)
+    b.prefill(tokens[:256], want_logits=False)
+    lb, tb = b.forward(int(tokens[256]))
+    assert ta == tb and np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    a.close()
+    b.close()
 
 
 def test_prefill_of_one_token_is_the_decode_step(gpu_ctx, hyq):
