@@ -84,7 +84,38 @@ SIGNATURES = {
     "hyq_dense_read_kv": (I, [P, I, SZ, P, P]),
     "hyq_dense_set_prefill_rows": (I, [P, SZ]),
     "hyq_dense_generate": (I, [P, ctypes.c_int32, SZ, I, P]),
+    "hyq_gguf_open": (I, [ctypes.c_char_p, I, ctypes.POINTER(P)]),
+    "hyq_gguf_open_bytes": (I, [P, SZ, I, ctypes.POINTER(P)]),
+    "hyq_gguf_close": (None, [P]),
+    "hyq_gguf_profile": (I, [P]),
+    "hyq_gguf_byte_len": (SZ, [P]),
+    "hyq_gguf_bytes": (P, [P]),
+    "hyq_gguf_tensor_count": (SZ, [P]),
+    "hyq_gguf_tensor_at": (I, [P, SZ, P]),
+    "hyq_gguf_find_tensor": (I, [P, ctypes.c_char_p, P]),
+    "hyq_gguf_meta_u64": (I, [P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64)]),
+    "hyq_gguf_meta_f64": (I, [P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)]),
+    "hyq_gguf_meta_bool": (I, [P, ctypes.c_char_p, ctypes.POINTER(I)]),
+    "hyq_gguf_meta_str": (I, [P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p),
+                              ctypes.POINTER(SZ)]),
+    "hyq_gguf_meta_array": (I, [P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32),
+                                ctypes.POINTER(ctypes.c_uint64)]),
+    "hyq_gguf_upload": (I, [P, P, ctypes.c_char_p, ctypes.POINTER(P)]),
+    "hyq_gguf_read_f32": (I, [P, P, ctypes.c_char_p, P, SZ]),
+    "hyq_sha256": (I, [P, SZ, P]),
+    "hyq_dense_from_gguf": (I, [P, P, SZ, ctypes.POINTER(P)]),
 }
+
+PROFILE_AUTO, PROFILE_STANDARD, PROFILE_TENCENT_Q2_0C, PROFILE_TENCENT_STQ1 = 0, 1, 2, 3
+PROFILES = {"auto": PROFILE_AUTO, "standard": PROFILE_STANDARD,
+            "tencent-q2-0c": PROFILE_TENCENT_Q2_0C, "tencent-stq1": PROFILE_TENCENT_STQ1}
+
+
+class GgufTensor(ctypes.Structure):
+    """hyq_gguf_tensor: TensorInfo (src/gguf.rs:28-38)."""
+    _fields_ = [("name", ctypes.c_char_p), ("dims", ctypes.c_uint64 * 4), ("rank", I),
+                ("type_id", ctypes.c_uint32), ("dtype", I), ("offset", ctypes.c_uint64),
+                ("byte_len", ctypes.c_uint64)]
 
 
 class DenseConfig(ctypes.Structure):
@@ -450,6 +481,27 @@ class DenseDecoder:
                                       ctypes.byref(nxt)))
         return logits, nxt.value
 
+    @classmethod
+    def from_gguf(cls, ctx: "Context", gguf: "Gguf", context: int) -> "DenseDecoder":
+        """Model::from_gguf (src/model.rs:136-262, dense arm) + a session of
+        `context` positions; the decoder owns the uploaded weights."""
+        h = P()
+        check(lib().hyq_dense_from_gguf(ctx.handle, gguf.handle, context, ctypes.byref(h)))
+        self = cls.__new__(cls)
+        self.ctx = ctx
+        c = gguf
+        self.cfg = DenseConfig(
+            c.u64(f"{c.architecture}.block_count"), c.u64(f"{c.architecture}.embedding_length"),
+            c.u64(f"{c.architecture}.attention.head_count"),
+            c.u64(f"{c.architecture}.attention.head_count_kv"),
+            c.u64(f"{c.architecture}.attention.key_length"),
+            c.u64(f"{c.architecture}.feed_forward_length"), c.array_len("tokenizer.ggml.tokens"),
+            c.f64(f"{c.architecture}.rope.freq_base"),
+            c.f64(f"{c.architecture}.attention.layer_norm_rms_epsilon"))
+        self.handle = h.value
+        self._keep = [gguf]
+        return self
+
     def set_prefill_rows(self, rows: int) -> None:
         """Tokens per device pass of prefill (results do not depend on it)."""
         check(lib().hyq_dense_set_prefill_rows(self.handle, rows))
@@ -466,3 +518,108 @@ class DenseDecoder:
         out = np.empty(steps, np.int32)
         check(lib().hyq_dense_generate(self.handle, token, steps, int(use_graph), _ptr(out)))
         return out
+
+
+class Gguf:
+    """A GGUF v3 file (Gguf::open, src/gguf.rs:50-210): validated like the
+    reference, tensors by name, metadata accessors, uploads to the device.
+    ``profile``: "auto", "standard", "tencent-q2-0c" or "tencent-stq1"."""
+
+    def __init__(self, path=None, profile: str = "auto", data: bytes | None = None):
+        if (path is None) == (data is None):
+            raise ValueError("give a path or the file's bytes")
+        h = P()
+        pid = PROFILES[profile]
+        if path is not None:
+            check(lib().hyq_gguf_open(os.fsencode(path), pid, ctypes.byref(h)))
+            self._buf = None
+        else:
+            self._buf = np.frombuffer(bytes(data), np.uint8)  # borrowed by the handle
+            check(lib().hyq_gguf_open_bytes(self._buf.ctypes.data if self._buf.size else None,
+                                            self._buf.size, pid, ctypes.byref(h)))
+        self.handle = h.value
+
+    def close(self) -> None:
+        if self.handle:
+            lib().hyq_gguf_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def profile(self) -> str:
+        pid = lib().hyq_gguf_profile(self.handle)
+        return {v: k for k, v in PROFILES.items()}[pid]
+
+    @property
+    def architecture(self) -> str:
+        return self.string("general.architecture")
+
+    def tensors(self) -> dict:
+        """name -> dict(dims, type_id, dtype, offset, byte_len), in name order."""
+        out = {}
+        t = GgufTensor()
+        for i in range(lib().hyq_gguf_tensor_count(self.handle)):
+            check(lib().hyq_gguf_tensor_at(self.handle, i, ctypes.byref(t)))
+            out[t.name.decode()] = dict(dims=list(t.dims[:t.rank]), type_id=t.type_id,
+                                        dtype=t.dtype, offset=t.offset, byte_len=t.byte_len)
+        return out
+
+    def tensor_bytes(self, name: str) -> np.ndarray:
+        t = GgufTensor()
+        check(lib().hyq_gguf_find_tensor(self.handle, name.encode(), ctypes.byref(t)))
+        base = lib().hyq_gguf_bytes(self.handle)
+        return np.ctypeslib.as_array((ctypes.c_uint8 * t.byte_len).from_address(
+            base + t.offset)).copy()
+
+    def u64(self, key: str) -> int:
+        v = ctypes.c_uint64()
+        check(lib().hyq_gguf_meta_u64(self.handle, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def f64(self, key: str) -> float:
+        v = ctypes.c_double()
+        check(lib().hyq_gguf_meta_f64(self.handle, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def boolean(self, key: str) -> bool:
+        v = I()
+        check(lib().hyq_gguf_meta_bool(self.handle, key.encode(), ctypes.byref(v)))
+        return bool(v.value)
+
+    def string(self, key: str) -> str:
+        p, n = ctypes.c_char_p(), SZ()
+        check(lib().hyq_gguf_meta_str(self.handle, key.encode(), ctypes.byref(p),
+                                      ctypes.byref(n)))
+        return ctypes.string_at(p, n.value).decode()
+
+    def array_len(self, key: str) -> int:
+        et, n = ctypes.c_uint32(), ctypes.c_uint64()
+        check(lib().hyq_gguf_meta_array(self.handle, key.encode(), ctypes.byref(et),
+                                        ctypes.byref(n)))
+        return n.value
+
+    def upload(self, ctx: "Context", name: str) -> "Weight":
+        """Gguf::tensor as a device weight (rank 2 or 3)."""
+        h = P()
+        check(lib().hyq_gguf_upload(ctx.handle, self.handle, name.encode(), ctypes.byref(h)))
+        return Weight(ctx, h.value)
+
+    def read_f32(self, ctx: "Context", name: str) -> np.ndarray:
+        """Weight::to_vec of a tensor (norm vectors)."""
+        n = int(np.prod(self.tensors()[name]["dims"]))
+        out = np.empty(n, np.float32)
+        check(lib().hyq_gguf_read_f32(ctx.handle, self.handle, name.encode(), _ptr(out), n))
+        return out
+
+
+def sha256(data: bytes) -> str:
+    """SHA-256 hex digest computed by the library (the AUTO profile's check)."""
+    buf = np.frombuffer(bytes(data), np.uint8)
+    out = np.empty(32, np.uint8)
+    check(lib().hyq_sha256(buf.ctypes.data if buf.size else None, buf.size, _ptr(out)))
+    return out.tobytes().hex()

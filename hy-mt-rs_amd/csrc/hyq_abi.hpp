@@ -116,6 +116,9 @@ struct Q8Ref {
 };
 
 int q8_alloc(int device, size_t n, hyq_q8 **out);
+// Hands a weight to a dense decoder, which releases it when destroyed (the
+// weights a GGUF loader uploads for it).
+void dense_adopt(hyq_dense *m, hyq_weight *w);
 
 } // namespace hyq
 

@@ -226,6 +226,7 @@ struct hyq_dense {
 
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    std::vector<hyq_weight *> owned; // weights this decoder releases
 
     // chunked prefill activations (allocated on the first prefill):
     // hid [n][H], q [n][QL], k/v [n][KV], att [n][QL], h [n][F] f32;
@@ -242,6 +243,7 @@ struct hyq_dense {
     {
         if (exec) (void)hipGraphExecDestroy(exec);
         if (graph) (void)hipGraphDestroy(graph);
+        for (hyq_weight *w : owned) hyq_weight_release(w);
     }
     size_t kvw() const { return (size_t)cfg.kv_heads * cfg.head_dim; }
     float *kcache(int l) { return (float *)kv.ptr + (size_t)l * 2 * context * kvw(); }
@@ -254,6 +256,8 @@ struct hyq_dense {
         graph = nullptr;
     }
 };
+
+void hyq::dense_adopt(hyq_dense *m, hyq_weight *w) { m->owned.push_back(w); }
 
 namespace {
 

@@ -281,6 +281,66 @@ int hyq_dense_read_kv(hyq_dense *m, int layer, size_t positions, float *keys, fl
 int hyq_dense_generate(hyq_dense *m, int32_t token, size_t steps, int use_graph,
                        int32_t *tokens);
 
+/* ---- GGUF v3 files (Gguf::open / parse, src/gguf.rs:50-210) ---- */
+/* Profiles (src/gguf.rs:17-26): type ids 40 and 42 are Q2_0C / STQ1_0 only
+ * under their Tencent profiles; AUTO resolves a file carrying them by its
+ * SHA-256 (the two known exports, :14-15) and fails otherwise. */
+enum {
+    HYQ_PROFILE_AUTO = 0,
+    HYQ_PROFILE_STANDARD = 1,
+    HYQ_PROFILE_TENCENT_Q2_0C = 2,
+    HYQ_PROFILE_TENCENT_STQ1 = 3
+};
+typedef struct hyq_gguf hyq_gguf;
+/* TensorInfo (src/gguf.rs:28-38); name is valid while the file is open. */
+typedef struct {
+    const char *name;
+    uint64_t dims[4]; /* GGUF order: the contiguous input dimension first */
+    int rank;
+    uint32_t type_id; /* as stored */
+    int dtype;        /* hyq_dtype after profile resolution */
+    uint64_t offset;  /* absolute byte offset in the file */
+    uint64_t byte_len;
+} hyq_gguf_tensor;
+/* Gguf::open: maps the file read-only and validates it like the reference
+ * (every count, string, array and tensor extent bounds-checked; errors
+ * HYQ_EINVAL, or HYQ_EDTYPE for a type id with no format under the profile).
+ * The file must stay unchanged while open. */
+int hyq_gguf_open(const char *path, int profile, hyq_gguf **out);
+/* The same over caller memory, borrowed until hyq_gguf_close. */
+int hyq_gguf_open_bytes(const uint8_t *bytes, size_t len, int profile, hyq_gguf **out);
+void hyq_gguf_close(hyq_gguf *g);
+/* The resolved profile (never HYQ_PROFILE_AUTO). */
+int hyq_gguf_profile(const hyq_gguf *g);
+size_t hyq_gguf_byte_len(const hyq_gguf *g);
+const uint8_t *hyq_gguf_bytes(const hyq_gguf *g);
+/* Tensors in name order (the reference's BTreeMap). */
+size_t hyq_gguf_tensor_count(const hyq_gguf *g);
+int hyq_gguf_tensor_at(const hyq_gguf *g, size_t index, hyq_gguf_tensor *out);
+int hyq_gguf_find_tensor(const hyq_gguf *g, const char *name, hyq_gguf_tensor *out);
+/* Metadata accessors (Gguf::usize / float / boolean / string, :220-258):
+ * u64 takes non-negative integers, f64 any number; arrays give their
+ * element type and length. HYQ_EINVAL when missing or of another type. */
+int hyq_gguf_meta_u64(const hyq_gguf *g, const char *key, uint64_t *out);
+int hyq_gguf_meta_f64(const hyq_gguf *g, const char *key, double *out);
+int hyq_gguf_meta_bool(const hyq_gguf *g, const char *key, int *out);
+int hyq_gguf_meta_str(const hyq_gguf *g, const char *key, const char **out, size_t *len);
+int hyq_gguf_meta_array(const hyq_gguf *g, const char *key, uint32_t *elem_type,
+                        uint64_t *count);
+/* Gguf::tensor + upload: a rank-2 matrix or rank-3 expert stack as a
+ * device weight (hyq_weight_upload of the tensor's bytes). */
+int hyq_gguf_upload(hyq_ctx *ctx, const hyq_gguf *g, const char *name, hyq_weight **out);
+/* Weight::to_vec of any tensor (norm vectors): n f32 values. */
+int hyq_gguf_read_f32(hyq_ctx *ctx, const hyq_gguf *g, const char *name, float *out, size_t n);
+/* SHA-256 (FIPS 180-4), the digest the AUTO profile checks. */
+int hyq_sha256(const uint8_t *bytes, size_t len, uint8_t digest[32]);
+/* Model::from_gguf, dense arm (src/model.rs:136-262) + Model::new_session's
+ * context check (:264-270): reads the hunyuan-dense configuration, checks
+ * every tensor's shape, uploads the weights (owned by the decoder) and the
+ * norm vectors. vocab = the length of tokenizer.ggml.tokens. hy_v3 (MoE)
+ * files return HYQ_EDTYPE. */
+int hyq_dense_from_gguf(hyq_ctx *ctx, const hyq_gguf *g, size_t context, hyq_dense **out);
+
 #ifdef __cplusplus
 }
 #endif
