@@ -239,7 +239,13 @@ __device__ __forceinline__ void stage_loop(const GemvArgs &a, const float *xin, 
 
 // Q8 input rows (no input stage) of up to Q8_REG int4 per thread are read
 // into registers before the weights' loads are issued, then copied to LDS.
+// With several rows per lane (the large launches) so are the row's scales
+// and the integer sums the format's dot reads (up to Q8_META words per
+// thread), which the dots then read from LDS instead of global memory; the
+// small launches read them from global memory, where their latency hides
+// behind the weights'.
 constexpr int Q8_REG = 8;
+constexpr int Q8_META = 8;
 // (a clang vector type: an array of HIP's int4 struct is not promoted to
 // registers here)
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -323,6 +329,32 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     i32x4 qv[Q8_REG];
     const bool stage_reg = IN != 0 && groups <= 8 * STAGE_PASSES && (a.nsparts == 0 || groups <= 8);
     const bool q8_reg = IN == 0 && groups * 16 <= Q8_REG * (int)blockDim.x;
+    // The words staged for the dots: the scales, then each sum array the
+    // format reads, numbered [s | sum256 | sum16 | sum32] over the arrays
+    // present; word i's source and LDS index are chosen by selects, so its
+    // load is unconditional.
+    constexpr bool N256 = G::QSUMS & Q8_SUM256, N16 = G::QSUMS & Q8_SUM16,
+                   N32 = G::QSUMS & Q8_SUM32;
+    const int m1 = groups, m2 = m1 + (N256 ? groups : 0), m3 = m2 + (N16 ? 16 * groups : 0);
+    const int mwords = m3 + (N32 ? 8 * groups : 0);
+    constexpr bool STAGE_META = IN == 0 && NR >= 2;
+    const bool meta_reg = STAGE_META && mwords <= Q8_META * (int)blockDim.x;
+    auto meta_src = [&](int i) -> const int * {
+        const int *p = reinterpret_cast<const int *>(a.x.s) + i;
+        if (N256) p = i >= m1 ? a.x.sum256 + (i - m1) : p;
+        if (N16) p = i >= m2 ? a.x.sum16 + (i - m2) : p;
+        if (N32) p = i >= m3 ? a.x.sum32 + (i - m3) : p;
+        return p;
+    };
+    // LDS index (in words from the scales) of word i
+    auto meta_dst = [&](int i) -> int {
+        int d = i;
+        if (N256) d = i >= m1 ? groups + (i - m1) : d;
+        if (N16) d = i >= m2 ? 2 * groups + (i - m2) : d;
+        if (N32) d = i >= m3 ? 18 * groups + (i - m3) : d;
+        return d;
+    };
+    int mv[Q8_META];
     if (IN != 0 && stage_reg) stage_load<IN>(a, xin, a.norm, sr);
     if (IN == 0 && q8_reg) {
         // clamped into bounds; the copy to LDS keeps the in-range ones
@@ -330,6 +362,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
 #pragma unroll
         for (int j = 0; j < Q8_REG; ++j)
             qv[j] = src[min((int)threadIdx.x + j * (int)blockDim.x, groups * 16 - 1)];
+    }
+    if (IN == 0 && meta_reg) {
+#pragma unroll
+        for (int j = 0; j < Q8_META; ++j)
+            mv[j] = *meta_src(min((int)threadIdx.x + j * (int)blockDim.x, mwords - 1));
     }
     static_assert(P == 0 || (NR == 1 && MODE == GEMV_PLAIN), "preload: plain, one row per lane");
     Dt dp[P > 0 ? P : 1];
@@ -352,6 +389,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
         }
     }
     Q8View xq = a.x;
+    // scales, then 256/16/32-value sums after the slots (contiguous, in the
+    // order meta_word numbers them)
+    float *sc = reinterpret_cast<float *>(lds + groups * SLOT_INTS);
+    int *s256 = reinterpret_cast<int *>(sc + groups);
+    int *s16 = s256 + groups;
+    int *s32 = s16 + groups * 16;
+    if (IN != 0 || STAGE_META) {
+        xq.s = sc;
+        xq.sum256 = s256;
+        xq.sum16 = s16;
+        xq.sum32 = s32;
+    }
     if (IN == 0) {
         const int4 *src = reinterpret_cast<const int4 *>(a.x.q);
         int4 *dst = reinterpret_cast<int4 *>(lds);
@@ -366,18 +415,21 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
             for (int i = threadIdx.x; i < groups * 16; i += blockDim.x)
                 dst[(i >> 4) * (SLOT_INTS / 4) + (i & 15)] = src[i];
         }
+        int *meta = reinterpret_cast<int *>(sc);
+        if (!STAGE_META) {
+        } else if (meta_reg) {
+#pragma unroll
+            for (int j = 0; j < Q8_META; ++j) {
+                const int i = threadIdx.x + j * (int)blockDim.x;
+                if (i < mwords) meta[meta_dst(i)] = mv[j];
+            }
+        } else {
+            for (int i = threadIdx.x; i < mwords; i += blockDim.x) meta[meta_dst(i)] = *meta_src(i);
+        }
     } else {
-        float *sc = reinterpret_cast<float *>(lds + groups * SLOT_INTS);
-        int *s256 = reinterpret_cast<int *>(sc + groups);
-        int *s16 = s256 + groups;
-        int *s32 = s16 + groups * 16;
         float *gss = reinterpret_cast<float *>(s32 + groups * 8);
         if (stage_reg) stage_regs<IN>(a, sr, lds, sc, s256, s16, s32, gss);
         else stage_loop<IN>(a, xin, a.norm, lds, sc, s256, s16, s32, gss);
-        xq.s = sc;
-        xq.sum256 = s256;
-        xq.sum16 = s16;
-        xq.sum32 = s32;
     }
     __syncthreads();
 
@@ -554,8 +606,8 @@ template <int F> int launch_gemv_format(int mode, const GemvArgs &a, void *strea
     if (a.nsparts > GEMV_MAX_PARTS || a.nrparts > GEMV_MAX_PARTS) return (int)hipErrorInvalidValue;
     dim3 grid((rows + rows_per_block - 1) / rows_per_block, ks), block(64 * waves);
     // slots, then (input stage) scales, 256/16/32-value sums and group sums of squares
-    const size_t lds = (size_t)a.groups * SLOT_INTS * 4 +
-                       (a.xin ? (size_t)a.groups * (4 + 4 + 64 + 32 + 4) : 0);
+    const size_t lds = (size_t)a.groups * SLOT_INTS * 4 + (size_t)a.groups * (4 + 4 + 64 + 32) +
+                       (a.xin ? (size_t)a.groups * 4 : 0);
     // groups per lane preloaded by the plain one-row-per-lane kernel
     const int pre = a.groups <= 32 ? (a.groups + 7) / 8 : 0;
     hipStream_t st = (hipStream_t)stream;

@@ -61,8 +61,12 @@ __device__ __forceinline__ void hold(uint16_t &v)
 // isum_half = sum (2c-3) q = 2 sum c q - 3 sum q   (src/quant.rs:1891-1951)
 // contribution = f32(isum) * (d * s_g)             (src/quant.rs:1896,1922)
 // ---------------------------------------------------------------------------
+// The Q8 integer sums a format's dot reads (QSUMS: a mask of these).
+constexpr int Q8_SUM256 = 1, Q8_SUM16 = 2, Q8_SUM32 = 4;
+
 struct GroupQ2C {
     static constexpr int ISUMS = 1;
+    static constexpr int QSUMS = Q8_SUM256 | Q8_SUM32; // full / half-group dots
     struct Data {
         uint4 w[4];
         uint16_t d;
@@ -184,6 +188,7 @@ struct GroupQ2C {
 // ---------------------------------------------------------------------------
 struct GroupSTQ {
     static constexpr int ISUMS = 1;
+    static constexpr int QSUMS = Q8_SUM256;
     struct Data {
         uint4 nib[2];
         uint2 sgn;
@@ -267,6 +272,7 @@ struct GroupSTQ {
 // ---------------------------------------------------------------------------
 struct GroupQ4K {
     static constexpr int ISUMS = 2;
+    static constexpr int QSUMS = Q8_SUM32;
     struct Data {
         uint4 qs[8];
         uint4 meta;
@@ -342,6 +348,7 @@ struct GroupQ4K {
 // ---------------------------------------------------------------------------
 struct GroupQ6K {
     static constexpr int ISUMS = 16;
+    static constexpr int QSUMS = Q8_SUM16;
     struct Data {
         uint4 q[12];
         uint4 sc;
@@ -422,6 +429,7 @@ struct GroupQ6K {
 // ---------------------------------------------------------------------------
 struct GroupQ80 {
     static constexpr int ISUMS = 8;
+    static constexpr int QSUMS = 0;
     struct Data {
         uint4 q[16];
         uint4 d;
