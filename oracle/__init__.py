@@ -239,7 +239,7 @@ class _Model(ctypes.Structure):
                 ("kv_heads", ctypes.c_int), ("head_dim", ctypes.c_int), ("ffn", ctypes.c_int),
                 ("vocab", ctypes.c_int), ("rope_base", ctypes.c_float),
                 ("eps", ctypes.c_float), ("dtype_linear", ctypes.c_int),
-                ("dtype_embed", ctypes.c_int), ("embed", P), ("output", P), ("output_norm", P),
+                ("dtype_embed", ctypes.c_int), ("dtype_down", ctypes.c_int), ("embed", P), ("output", P), ("output_norm", P),
                 ("wq", P), ("wk", P), ("wv", P), ("wo", P), ("wgate", P), ("wup", P),
                 ("wdown", P), ("attn_norm", P), ("ffn_norm", P), ("q_norm", P),
                 ("k_norm", P)]
@@ -262,7 +262,8 @@ class DenseOracle:
 
         self.m = _Model(c["layers"], c["hidden"], c["heads"], c["kv_heads"], c["head_dim"],
                         c["ffn"], c["vocab"], c["rope_base"], c["rms_eps"], model["linear"],
-                        model["embed_dtype"], _p(model["embed"]),
+                        model["embed_dtype"], model.get("down_dtype", model["linear"]),
+                        _p(model["embed"]),
                         _p(model["output"]) if "output" in model else None,
                         _p(model["output_norm"]),
                         ptrs("q"), ptrs("k"), ptrs("v"), ptrs("o"), ptrs("gate"), ptrs("up"),

@@ -195,7 +195,7 @@ int hyqo_decode_step(const hyqo_model *m, float *kcache, float *vcache, size_t c
         } else {
             hyqo_gate_up_silu(m->dtype_linear, m->wgate[l], m->wup[l], F, H, xn, gate, threads);
         }
-        linear(m, m->dtype_linear, m->wdown[l], H, F, gate, proj, int8_path, threads);
+        linear(m, m->dtype_down, m->wdown[l], H, F, gate, proj, int8_path, threads);
         for (size_t i = 0; i < H; ++i) hidden[i] += proj[i];
     }
     hyqo_rms_norm_rows(hidden, m->output_norm, H, H, m->eps);
@@ -278,7 +278,7 @@ int hyqo_prefill_chunk(const hyqo_model *m, float *kcache, float *vcache, size_t
             float g = gate[i];
             gate[i] = (g / (1.0f + expf(-g))) * up[i];
         }
-        hyqo_matmul(m->dtype_linear, m->wdown[l], H, F, gate, n, proj, threads);
+        hyqo_matmul(m->dtype_down, m->wdown[l], H, F, gate, n, proj, threads);
         for (size_t i = 0; i < n * H; ++i) hidden[i] += proj[i];
     }
     /* the last row's output norm and a batch-1 matmul (src/model.rs:605-607) */

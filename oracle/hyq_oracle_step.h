@@ -15,6 +15,7 @@ typedef struct {
     int layers, hidden, heads, kv_heads, head_dim, ffn, vocab;
     float rope_base, eps;
     int dtype_linear, dtype_embed;
+    int dtype_down; /* ffn_down's format (Q6_K in the Q4_K_M mix) */
     const uint8_t *embed;
     const uint8_t *output; /* NULL: tied to embed */
     const float *output_norm;

@@ -94,9 +94,12 @@ DENSE_1P8B = dict(layers=32, hidden=2048, heads=16, kv_heads=4, head_dim=128, ff
                   vocab=120818, rope_base=11158840.0, rms_eps=1e-5)
 
 
-def make_dense_model(cfg: dict, linear: int = Q2_0C, embed: int = Q6_K, seed: int = 0) -> dict:
+def make_dense_model(cfg: dict, linear: int = Q2_0C, embed: int = Q6_K, seed: int = 0,
+                     down: int | None = None) -> dict:
     """Packed GGUF bytes for every matrix plus f32 norms ~ N(1, 0.02).
-    The output matrix is tied to the embedding (src/model.rs:194-202)."""
+    The output matrix is tied to the embedding (src/model.rs:194-202).
+    `down` gives ffn_down its own format (Q6_K in the Q4_K_M mix)."""
+    down = linear if down is None else down
     rng = np.random.default_rng(seed)
     H, F, D = cfg["hidden"], cfg["ffn"], cfg["head_dim"]
     QL, KV = cfg["heads"] * D, cfg["kv_heads"] * D
@@ -107,12 +110,12 @@ def make_dense_model(cfg: dict, linear: int = Q2_0C, embed: int = Q6_K, seed: in
             q=random_matrix(linear, QL, H, s + 1), k=random_matrix(linear, KV, H, s + 2),
             v=random_matrix(linear, KV, H, s + 3), o=random_matrix(linear, H, QL, s + 4),
             gate=random_matrix(linear, F, H, s + 5), up=random_matrix(linear, F, H, s + 6),
-            down=random_matrix(linear, H, F, s + 7),
+            down=random_matrix(down, H, F, s + 7),
             attn_norm=rng.normal(1, 0.02, H).astype(np.float32),
             ffn_norm=rng.normal(1, 0.02, H).astype(np.float32),
             q_norm=rng.normal(1, 0.02, D).astype(np.float32),
             k_norm=rng.normal(1, 0.02, D).astype(np.float32)))
-    return dict(cfg=dict(cfg), linear=linear, embed_dtype=embed, layers=layers,
+    return dict(cfg=dict(cfg), linear=linear, down_dtype=down, embed_dtype=embed, layers=layers,
                 embed=random_matrix(embed, cfg["vocab"], H, seed * 1000 + 999),
                 output_norm=rng.normal(1, 0.02, H).astype(np.float32))
 
@@ -148,7 +151,7 @@ def load_dense(hyq, ctx, model: dict, context: int):
         W = dict(q=ctx.upload(lin, L["q"], (H, QL)), k=ctx.upload(lin, L["k"], (H, KV)),
                  v=ctx.upload(lin, L["v"], (H, KV)), o=ctx.upload(lin, L["o"], (QL, H)),
                  gate=ctx.upload(lin, L["gate"], (H, F)), up=ctx.upload(lin, L["up"], (H, F)),
-                 down=ctx.upload(lin, L["down"], (F, H)))
+                 down=ctx.upload(model.get("down_dtype", lin), L["down"], (F, H)))
         dec.set_layer(l, W["q"], W["k"], W["v"], W["o"], W["gate"], W["up"], W["down"],
                       L["attn_norm"], L["ffn_norm"], L["q_norm"], L["k_norm"])
     E = ctx.upload(model["embed_dtype"], model["embed"], (H, c["vocab"]))

@@ -13,7 +13,8 @@ hyq_dense_forward."""
 import numpy as np
 import pytest
 
-from synth import Q2_0C, Q6_K, STQ1_0, load_dense, make_dense_model, make_kv_cache, random_matrix
+from synth import (Q2_0C, Q4_K, Q6_K, Q8_0, STQ1_0, load_dense, make_dense_model, make_kv_cache,
+                   random_matrix)
 
 pytestmark = pytest.mark.gpu
 
@@ -215,4 +216,39 @@ def test_prefill_errors(gpu_ctx, hyq):
     assert dec.position == 4
     _, t = dec.prefill(np.arange(12))  # exactly fills the context
     assert dec.position == 16
+    dec.close()
+
+
+MIXED = dict(SMALL, ffn=6144)  # 24 groups: the down projection runs as three K slices
+
+
+@pytest.mark.parametrize("linear,down", [(Q4_K, Q6_K), (Q8_0, Q8_0), (Q6_K, Q6_K)])
+def test_mixed_formats_prefill_and_decode(gpu_ctx, hyq, oracle, linear, down):
+    """The Q4_K_M mix (Q4_K linears, Q6_K down) and single-format Q8_0 / Q6_K
+    models: prefill within 1e-2 and the following decode steps within 5e-3
+    (on the GPU's own cache) of the oracle."""
+    c = MIXED
+    _print("mixed", linear, down)
+    model = make_dense_model(c, linear=linear, down=down, seed=31)
+    model["output"] = random_matrix(Q6_K, c["vocab"], c["hidden"], 81)
+    context, past, n = 48, 6, 30
+    dec, k, v = _decoder(hyq, gpu_ctx, model, context, past, seed=31)
+    tokens = np.random.default_rng(31).integers(0, c["vocab"], n).astype(np.int32)
+    logits, token = dec.prefill(tokens)
+    ref = oracle.DenseOracle(model)
+    rel = _rel(logits, ref.prefill(k, v, past, tokens, int8_path=True))
+    _print("  prefill rel", rel)
+    assert rel <= 1e-2, rel
+    kvw = c["kv_heads"] * c["head_dim"]
+    for i in range(2):
+        pos = past + n + i
+        kc = np.zeros((c["layers"], context, kvw), np.float32)
+        vc = np.zeros_like(kc)
+        for l in range(c["layers"]):
+            kc[l, :pos], vc[l, :pos] = dec.read_kv(l, pos)
+        step_logits, nxt = dec.forward(token)
+        rel = _rel(step_logits, ref.step(kc, vc, pos, token, int8_path=True))
+        _print("  step", i, "rel", rel)
+        assert rel <= 5e-3, (i, rel)
+        token = nxt
     dec.close()
