@@ -131,7 +131,7 @@ struct hyq_q8 {
 struct hyq_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
-    hyq::Scratch x, y, bytes, xh, moe;
+    hyq::Scratch x, y, bytes, xh, moe, kpart; // kpart: K-slice partials of batched products
     hyq_q8 *q8 = nullptr; // grown on demand for host-pointer calls
 };
 

@@ -236,6 +236,8 @@ struct hyq_dense {
     size_t pf_rows = 1024, pf_cap = 0; // rows per pass; rows the buffers hold
     float *pf_hid = nullptr, *pf_q = nullptr, *pf_k = nullptr, *pf_v = nullptr;
     float *pf_att = nullptr, *pf_h = nullptr, *pf_rs = nullptr, *pf_part = nullptr;
+    float *pf_kpart = nullptr; // K-slice partials of the output and down GEMMs
+    size_t pf_kpart_floats = 0;
     _Float16 *pf_xh = nullptr;
     int32_t *pf_tok = nullptr;
 
@@ -392,6 +394,14 @@ int prefill_buffers(hyq_dense *m)
     const size_t o_part = take(N * (size_t)c.heads *
                                (size_t)prefill_attention_splits((int)m->context) * PART_STRIDE * 4);
     const size_t o_tok = take(N * 4);
+    // the split attention-output and down GEMMs' partials (every layer's
+    // formats: they may differ)
+    size_t kp = 0;
+    for (const hyq_dense::Layer &L : m->layers) {
+        kp = std::max(kp, gemm_split_floats(L.o->dtype, (int)H, (int)N, (int)QL));
+        kp = std::max(kp, gemm_split_floats(L.down->dtype, (int)H, (int)N, (int)F));
+    }
+    const size_t o_kpart = take(kp * 4);
     auto buf = std::make_unique<DeviceBuffer>();
     int rc = buf->alloc(m->ctx->device, off);
     if (rc) return rc;
@@ -406,6 +416,8 @@ int prefill_buffers(hyq_dense *m)
     m->pf_rs = (float *)(b + o_rs);
     m->pf_part = (float *)(b + o_part);
     m->pf_tok = (int32_t *)(b + o_tok);
+    m->pf_kpart = (float *)(b + o_kpart);
+    m->pf_kpart_floats = kp;
     m->pf_mem = std::move(buf);
     m->pf_cap = N;
     return HYQ_OK;
@@ -451,7 +463,7 @@ int enqueue_prefill_chunk(hyq_dense *m, int n)
                    "attention_rows");
         HYQ_LAUNCH(launch_to_f16(m->pf_att, n, QL, m->pf_xh, m->pf_rs, st), "to_f16");
         HYQ_LAUNCH(launch_gemm_f16(L.o->dtype, L.o->view, QL, m->pf_xh, m->pf_rs, n, m->pf_hid,
-                                   m->pf_hid, st),
+                                   m->pf_hid, st, m->pf_kpart, m->pf_kpart_floats),
                    "gemm_attn_output");
         HYQ_LAUNCH(launch_norm_to_f16(m->pf_hid, n, H, L.ffn_norm, c.rms_eps, m->pf_xh,
                                       m->pf_rs, st),
@@ -461,7 +473,7 @@ int enqueue_prefill_chunk(hyq_dense *m, int n)
                    "gemm_gate_up");
         HYQ_LAUNCH(launch_to_f16(m->pf_h, n, F, m->pf_xh, m->pf_rs, st), "to_f16");
         HYQ_LAUNCH(launch_gemm_f16(L.down->dtype, L.down->view, F, m->pf_xh, m->pf_rs, n,
-                                   m->pf_hid, m->pf_hid, st),
+                                   m->pf_hid, m->pf_hid, st, m->pf_kpart, m->pf_kpart_floats),
                    "gemm_down");
     }
     GemvArgs a = staged(m->output, m->pf_hid + (size_t)(n - 1) * H, m->output_norm, c.rms_eps,

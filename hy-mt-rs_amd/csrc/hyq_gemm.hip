@@ -13,6 +13,8 @@
 // the tiles sharing one weight row block land on the same XCD and its L2.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "hyq_tile.hpp"
 #include "hyq_wave.hpp"
 
@@ -111,12 +113,15 @@ __global__ __launch_bounds__(256) void rows_to_f16_kernel(const float *__restric
 // may alias y: each element is read and then written by one thread). The
 // row space is up to three weights sharing the activation rows (Q, K and V
 // in one launch); a tile's BM rows lie in one of them (its row count is a
-// multiple of BM, or it is the last).
+// multiple of BM, or it is the last). With kslices > 1 (one weight) grid.y
+// splits K: slice z writes its scaled partial product to
+// part[z][n][m] and gemm_reduce_kernel adds the slices in order.
 template <int F>
 __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(GemmSegs g, int K,
                                                           const _Float16 *__restrict__ xh,
                                                           const float *__restrict__ rscale, int N,
-                                                          int mtiles, int ntiles)
+                                                          int mtiles, int ntiles, int kslices,
+                                                          float *__restrict__ part)
 {
     __shared__ __attribute__((aligned(16))) _Float16 lds[4 * TILE_HALVES];
     const int T = xcd_tile(mtiles * ntiles);
@@ -138,10 +143,11 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(GemmSegs g, int K,
         return n0 + r < N ? xh + (size_t)(n0 + r) * K : nullptr;
     };
     auto arow = [&](int i) { return wm * 64 + 32 * i; };
-    k_loop<F>(wsrc, xrow, arow, K, wn, lds, acc);
+    const int kslice = K / kslices;
+    k_loop<F>(wsrc, xrow, arow, kslice, wn, lds, acc, blockIdx.y * kslice);
 
-    float *y = S.y;
-    const float *residual = S.residual;
+    float *y = kslices > 1 ? part + (size_t)blockIdx.y * N * M : S.y;
+    const float *residual = kslices > 1 ? nullptr : S.residual;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -172,6 +178,27 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(GemmSegs g, int K,
                 }
             }
         }
+}
+
+// y = residual + (((part[0] + part[1]) + part[2]) + ...) over `count`
+// floats (float4 lanes; count a multiple of 4): the K slices of a split GEMM
+// added in slice order, then the residual, as the unsplit epilogue adds it.
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(const float4 *__restrict__ part,
+                                                          int kslices, size_t count4,
+                                                          const float4 *residual, float4 *y)
+{
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= count4) return;
+    float4 v = part[i];
+    for (int z = 1; z < kslices; ++z) {
+        const float4 p = part[(size_t)z * count4 + i];
+        v = make_float4(v.x + p.x, v.y + p.y, v.z + p.z, v.w + p.w);
+    }
+    if (residual) {
+        const float4 r = residual[i];
+        v = make_float4(r.x + v.x, r.y + v.y, r.z + v.z, r.w + v.w);
+    }
+    y[i] = v;
 }
 
 // ---------------------------------------------------------------------------
@@ -488,8 +515,32 @@ int launch_gate_up_f16(int fmt, WView gate, WView up, int cols, const _Float16 *
     return (int)hipGetLastError();
 }
 
+// K slices for a one-weight GEMM of few row tiles, whose tiles would leave
+// CUs idle: up to 4 slices for at most 32 row tiles, 2 for at most 64 - the
+// largest count that cuts K into whole numbers of the format's blocks (and
+// 64-column steps) of at least 1024 columns. It depends on the weight's
+// shape only, so a token row's result does not depend on how many rows
+// share the launch.
+int gemm_kslices(int fmt, int M, int K)
+{
+    const int unit = std::max(BK, block_len(fmt));
+    const int mtiles = (M + BM - 1) / BM;
+    const int kmax = mtiles <= 32 ? 4 : mtiles <= 64 ? 2 : 1;
+    if (K % unit || M % 4) return 1;
+    for (int k = kmax; k > 1; --k)
+        if ((K / unit) % k == 0 && K / k >= 1024) return k;
+    return 1;
+}
+
+size_t gemm_split_floats(int fmt, int M, int N, int K)
+{
+    const int k = gemm_kslices(fmt, M, K);
+    return k > 1 ? (size_t)k * N * M : 0;
+}
+
 int launch_gemm_f16(int fmt, WView w, int cols, const _Float16 *xh, const float *rscale,
-                    int batch, float *y, const float *residual, void *stream)
+                    int batch, float *y, const float *residual, void *stream, float *part,
+                    size_t part_floats)
 {
     GemmSegs g{};
     g.nseg = 1;
@@ -497,13 +548,26 @@ int launch_gemm_f16(int fmt, WView w, int cols, const _Float16 *xh, const float 
     g.s[0].y = y;
     g.s[0].residual = residual;
     g.s[0].rows = w.rows;
+    const int ks = gemm_kslices(fmt, w.rows, cols);
+    if (ks > 1 && part && part_floats >= (size_t)ks * batch * w.rows) {
+        int rc = launch_gemm_f16_segs(fmt, g, cols, xh, rscale, batch, stream, ks, part);
+        if (rc) return rc;
+        const size_t count4 = (size_t)batch * w.rows / 4;
+        hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((count4 + 255) / 256)), dim3(256),
+                           0, (hipStream_t)stream, reinterpret_cast<const float4 *>(part), ks,
+                           count4, reinterpret_cast<const float4 *>(residual),
+                           reinterpret_cast<float4 *>(y));
+        return (int)hipGetLastError();
+    }
     return launch_gemm_f16_segs(fmt, g, cols, xh, rscale, batch, stream);
 }
 
 int launch_gemm_f16_segs(int fmt, GemmSegs g, int cols, const _Float16 *xh, const float *rscale,
-                         int batch, void *stream)
+                         int batch, void *stream, int kslices, float *part)
 {
     if (cols % BK || g.nseg < 1 || g.nseg > 3) return (int)hipErrorInvalidValue;
+    if (kslices < 1 || (kslices > 1 && (g.nseg != 1 || !part || cols % kslices)))
+        return (int)hipErrorInvalidValue;
     int mtiles = 0;
     for (int i = 0; i < g.nseg; ++i) {
         if (i + 1 < g.nseg && g.s[i].rows % BM) return (int)hipErrorInvalidValue;
@@ -512,12 +576,12 @@ int launch_gemm_f16_segs(int fmt, GemmSegs g, int cols, const _Float16 *xh, cons
     }
     const int ntiles = (batch + BN - 1) / BN;
     const int per = (mtiles * ntiles + 7) / 8;
-    dim3 grid(8 * per), block(256);
+    dim3 grid(8 * per, kslices), block(256);
     hipStream_t st = (hipStream_t)stream;
 #define HYQ_GEMM(F)                                                                            \
     case F:                                                                                    \
         hipLaunchKernelGGL(gemm_f16_kernel<F>, grid, block, 0, st, g, cols, xh, rscale, batch,  \
-                           mtiles, ntiles);                                                    \
+                           mtiles, ntiles, kslices, part);                                     \
         break;
     switch (fmt) {
         HYQ_GEMM(Q4_K)

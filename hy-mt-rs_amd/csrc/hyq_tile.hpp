@@ -404,11 +404,13 @@ __device__ __forceinline__ void zero_acc(f32x16 (&acc)[2][2])
 // xrow(r) gives the f16 activation row of token r of the tile (nullptr =
 // zeros); arow(i) the first LDS weight row of the wave's block i. lds holds
 // 2 * 2 * TILE_HALVES halves: buffer b at lds + b * 2 * TILE_HALVES, weights
-// then activations.
+// then activations. The loop covers columns [kbase, kbase + K) (a K slice
+// when kbase > 0; both multiples of the format's block).
 // ---------------------------------------------------------------------------
 template <int F, class WSrc, class XRow, class ARow>
 __device__ __forceinline__ void k_loop(const WSrc &wsrc, const XRow &xrow, const ARow &arow,
-                                       int K, int wn, _Float16 *lds, f32x16 (&acc)[2][2])
+                                       int K, int wn, _Float16 *lds, f32x16 (&acc)[2][2],
+                                       int kbase = 0)
 {
     using D = Deq<F>;
     const int t = threadIdx.x;
@@ -426,12 +428,12 @@ __device__ __forceinline__ void k_loop(const WSrc &wsrc, const XRow &xrow, const
     typename D::Raw raw;
     XRaw xr;
     auto fetch = [&](int k0) {
-        if (row >= 0) D::load(raw, rp, k0, h);
-        load_x(xr, xp, k0);
+        if (row >= 0) D::load(raw, rp, kbase + k0, h);
+        load_x(xr, xp, kbase + k0);
     };
     auto put = [&](int k0, int b) {
         _Float16 *Ws = lds + b * 2 * TILE_HALVES;
-        if (row >= 0) D::convert(raw, (k0 >> 6) & 3, h, Ws + lrow * LDK);
+        if (row >= 0) D::convert(raw, ((kbase + k0) >> 6) & 3, h, Ws + lrow * LDK);
         else zero_half(Ws + lrow * LDK, h);
         store_x(Ws + TILE_HALVES, xr);
     };
