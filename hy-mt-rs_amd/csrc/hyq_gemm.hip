@@ -344,7 +344,8 @@ __global__ __launch_bounds__(256, 2) void moe_gate_up_kernel(
         return r < cnt ? xg + (size_t)(nb + r) * K : nullptr;
     };
     auto arow = [&](int i) { return 64 * i + 32 * wm; };
-    k_loop<F>(wsrc, xrow, arow, K, wn, lds, acc);
+    if (cnt <= 32) k_loop<F, 1>(wsrc, xrow, arow, K, wn, lds, acc);
+    else k_loop<F, 2>(wsrc, xrow, arow, K, wn, lds, acc);
 
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -432,7 +433,8 @@ __global__ __launch_bounds__(256, 2) void moe_down_kernel(
         return r < cnt ? H + (size_t)(nb + r) * K : nullptr;
     };
     auto arow = [&](int i) { return wm * 64 + 32 * i; };
-    k_loop<F>(wsrc, xrow, arow, K, wn, lds, acc);
+    if (cnt <= 32) k_loop<F, 1>(wsrc, xrow, arow, K, wn, lds, acc);
+    else k_loop<F, 2>(wsrc, xrow, arow, K, wn, lds, acc);
 
 #pragma unroll
     for (int i = 0; i < 2; ++i)

@@ -354,8 +354,9 @@ __device__ __forceinline__ void store_x(_Float16 *Xs, const XRaw &x)
 }
 
 // One 64-deep step: acc[i][j] accumulates LDS weight rows arow(i) + lane%32
-// against tokens wn*64 + 32*j + lane%32.
-template <class ARow>
+// against tokens wn*64 + 32*j + lane%32, for the wave's first J token
+// blocks (the others hold no token of the tile).
+template <int J, class ARow>
 __device__ __forceinline__ void mma_step(const _Float16 *Ws, const _Float16 *Xs, const ARow &arow,
                                          int wn, f32x16 (&acc)[2][2])
 {
@@ -367,12 +368,14 @@ __device__ __forceinline__ void mma_step(const _Float16 *Ws, const _Float16 *Xs,
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             a[i] = *reinterpret_cast<const half8 *>(Ws + (arow(i) + r) * LDK + kk + kq);
-            b[i] = *reinterpret_cast<const half8 *>(Xs + (wn * 64 + 32 * i + r) * LDK + kk + kq);
+            if (i < J)
+                b[i] = *reinterpret_cast<const half8 *>(Xs + (wn * 64 + 32 * i + r) * LDK + kk +
+                                                        kq);
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < J; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
     }
 }
@@ -405,9 +408,12 @@ __device__ __forceinline__ void zero_acc(f32x16 (&acc)[2][2])
 // zeros); arow(i) the first LDS weight row of the wave's block i. lds holds
 // 2 * 2 * TILE_HALVES halves: buffer b at lds + b * 2 * TILE_HALVES, weights
 // then activations. The loop covers columns [kbase, kbase + K) (a K slice
-// when kbase > 0; both multiples of the format's block).
+// when kbase > 0; both multiples of the format's block). JM = 1 is the
+// variant for tiles of at most 32 tokens (MoE experts): only the first token
+// block holds tokens, so the waves with wn = 1 skip their MFMAs and the
+// others run one token block.
 // ---------------------------------------------------------------------------
-template <int F, class WSrc, class XRow, class ARow>
+template <int F, int JM = 2, class WSrc, class XRow, class ARow>
 __device__ __forceinline__ void k_loop(const WSrc &wsrc, const XRow &xrow, const ARow &arow,
                                        int K, int wn, _Float16 *lds, f32x16 (&acc)[2][2],
                                        int kbase = 0)
@@ -438,6 +444,7 @@ __device__ __forceinline__ void k_loop(const WSrc &wsrc, const XRow &xrow, const
         store_x(Ws + TILE_HALVES, xr);
     };
     const int steps = K / BK;
+    const bool mma = JM == 2 || __builtin_amdgcn_readfirstlane(wn) == 0;
     fetch(0);
     put(0, 0);
     if (steps > 1) fetch(BK);
@@ -445,7 +452,7 @@ __device__ __forceinline__ void k_loop(const WSrc &wsrc, const XRow &xrow, const
     for (int s = 0; s < steps; ++s) {
         const int cur = s & 1;
         const _Float16 *Ws = lds + cur * 2 * TILE_HALVES;
-        mma_step(Ws, Ws + TILE_HALVES, arow, wn, acc);
+        if (mma) mma_step<JM>(Ws, Ws + TILE_HALVES, arow, wn, acc);
         if (s + 1 < steps) {
             put((s + 1) * BK, cur ^ 1);
             if (s + 2 < steps) fetch((s + 2) * BK);
