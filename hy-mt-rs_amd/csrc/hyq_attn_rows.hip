@@ -22,6 +22,7 @@
 // close to f32 accuracy. Values must lie within the f16 range (|x| < 65504).
 #include <hip/hip_runtime.h>
 
+#include "hyq_f16rows.hpp"
 #include "hyq_step.hpp"
 #include "hyq_wave.hpp"
 
@@ -266,16 +267,108 @@ __global__ __launch_bounds__(256, 2) void attn_rows_kernel(
                             acc[j][4 * g + 3]);
 }
 
+// Merge of one token row's split partials over all heads (grid: the n
+// tokens, 256 threads), reading only the splits the token sees (splits
+// 0 .. (pos + chunk) / chunk - 1): per head M = max_s m_s, w_s =
+// exp(m_s - M), row = (sum_s w_s acc_s) / (sum_s w_s l_s), sums in split
+// order. It writes the f32 row to out (if given) and/or the row as f16 with
+// its power-of-two scale (xh, rscale: the attention-output GEMM's operand,
+// rows_to_f16_kernel's rounding). Dynamic LDS: the row (heads * 128 floats)
+// and the per-(head, split) weights (heads * splits floats, twice).
+__global__ __launch_bounds__(256) void merge_rows_kernel(const float *__restrict__ part,
+                                                         int splits, int chunk, int heads,
+                                                         const int *__restrict__ pos_p,
+                                                         float *__restrict__ out,
+                                                         _Float16 *__restrict__ xh,
+                                                         float *__restrict__ rscale)
+{
+    extern __shared__ float ms[];
+    const int tq = blockIdx.x, t = threadIdx.x;
+    const int W = heads * ATT_D;
+    float *row = ms;                 // [heads * 128]
+    float *wt = ms + W;              // [heads][splits]: exp(m_s - M)
+    float *den = wt + heads * splits; // [heads]
+    const int nact = min((*pos_p + tq + chunk) / chunk, splits);
+    const float *pt = part + (size_t)tq * heads * splits * PART_STRIDE;
+    for (int h = t; h < heads; h += 256) {
+        const float *ph = pt + (size_t)h * splits * PART_STRIDE;
+        float M = -INFINITY;
+        for (int sp = 0; sp < nact; ++sp) M = fmaxf(M, ph[(size_t)sp * PART_STRIDE]);
+        float d = 0.f;
+        for (int sp = 0; sp < nact; ++sp) {
+            const float w = expf(ph[(size_t)sp * PART_STRIDE] - M);
+            wt[h * splits + sp] = w;
+            d += w * ph[(size_t)sp * PART_STRIDE + 1];
+        }
+        den[h] = d;
+    }
+    __syncthreads();
+    float mx = 0.f;
+    for (int i = t; i < W; i += 256) {
+        const int h = i / ATT_D, dd = i % ATT_D;
+        const float *ph = pt + (size_t)h * splits * PART_STRIDE + 4 + dd;
+        float num = 0.f;
+#pragma unroll 4
+        for (int sp = 0; sp < nact; ++sp) num += wt[h * splits + sp] * ph[(size_t)sp * PART_STRIDE];
+        const float v = num / den[h];
+        row[i] = v;
+        if (out) out[(size_t)tq * W + i] = v;
+        mx = fmaxf(mx, fabsf(v));
+        if (v != v) mx = INFINITY;
+    }
+    if (!xh) return;
+    __shared__ float red[4];
+    mx = wave::max64(mx);
+    if ((t & 63) == 0) red[t >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const int e = f16_row_exponent(mx);
+    const float inv = ldexpf(1.0f, -e);
+    if (t == 0) rscale[tq] = ldexpf(1.0f, e);
+    for (int i = t; i < W; i += 256) xh[(size_t)tq * W + i] = (_Float16)(row[i] * inv);
+}
+
 } // namespace
+
+size_t merge_rows_lds(int heads, int splits)
+{
+    return ((size_t)heads * ATT_D + (size_t)heads * splits + heads) * 4;
+}
+
+int launch_attention_rows_f16(const float *q, const float *kcache, const float *vcache,
+                              const int *pos, int n, int context, int heads, int kvh,
+                              float *part, float *out, _Float16 *xh, float *rscale,
+                              void *stream)
+{
+    if (n <= 0) return 0;
+    const int rep = heads / kvh;
+    if (rep < 1 || rep > ATT_MAX_REP) return (int)hipErrorInvalidValue;
+    const int splits = prefill_attention_splits(context), span = prefill_attention_chunk(context);
+    const size_t lds = merge_rows_lds(heads, splits);
+    if (lds > 64 * 1024) return (int)hipErrorInvalidValue;
+    const int tpw = FA_ROWS / rep;
+    const float scale = 1.0f / sqrtf(128.0f);
+    hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL(attn_rows_kernel, dim3(splits, (n + tpw - 1) / tpw, kvh), dim3(256), 0, st,
+                       q, kcache, vcache, pos, n, heads, kvh, scale, part, splits, span, context);
+    hipLaunchKernelGGL(merge_rows_kernel, dim3(n), dim3(256), lds, st, part, splits, span, heads,
+                       pos, out, xh, rscale);
+    return (int)hipGetLastError();
+}
 
 int launch_attention_rows(const float *q, const float *kcache, const float *vcache,
                           const int *pos, int n, int context, int heads, int kvh, float *part,
                           float *out, void *stream)
 {
     if (n <= 0) return 0;
+    const int splits = prefill_attention_splits(context);
+    if (merge_rows_lds(heads, splits) <= 64 * 1024)
+        return launch_attention_rows_f16(q, kcache, vcache, pos, n, context, heads, kvh, part,
+                                         out, nullptr, nullptr, stream);
+    // rows too wide for the one-workgroup-per-token merge: per-head merge
     const int rep = heads / kvh;
     if (rep < 1 || rep > ATT_MAX_REP) return (int)hipErrorInvalidValue;
-    const int splits = prefill_attention_splits(context), span = prefill_attention_chunk(context);
+    const int span = prefill_attention_chunk(context);
     const int tpw = FA_ROWS / rep;
     const float scale = 1.0f / sqrtf(128.0f);
     hipStream_t st = (hipStream_t)stream;

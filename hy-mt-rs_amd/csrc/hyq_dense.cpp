@@ -457,11 +457,19 @@ int enqueue_prefill_chunk(hyq_dense *m, int n)
                                             m->freq, pos, n, c.heads, c.kv_heads, c.head_dim,
                                             c.rms_eps, m->kcache(l), m->vcache(l), st),
                    "rope_norm_kv_rows");
-        HYQ_LAUNCH(launch_attention_rows(m->pf_q, m->kcache(l), m->vcache(l), pos, n,
-                                         (int)m->context, c.heads, c.kv_heads, m->pf_part,
-                                         m->pf_att, st),
-                   "attention_rows");
-        HYQ_LAUNCH(launch_to_f16(m->pf_att, n, QL, m->pf_xh, m->pf_rs, st), "to_f16");
+        if (merge_rows_lds(c.heads, prefill_attention_splits((int)m->context)) <= 64 * 1024) {
+            // attention with its rows merged straight into the GEMM's f16 operand
+            HYQ_LAUNCH(launch_attention_rows_f16(m->pf_q, m->kcache(l), m->vcache(l), pos, n,
+                                                 (int)m->context, c.heads, c.kv_heads,
+                                                 m->pf_part, nullptr, m->pf_xh, m->pf_rs, st),
+                       "attention_rows");
+        } else {
+            HYQ_LAUNCH(launch_attention_rows(m->pf_q, m->kcache(l), m->vcache(l), pos, n,
+                                             (int)m->context, c.heads, c.kv_heads, m->pf_part,
+                                             m->pf_att, st),
+                       "attention_rows");
+            HYQ_LAUNCH(launch_to_f16(m->pf_att, n, QL, m->pf_xh, m->pf_rs, st), "to_f16");
+        }
         HYQ_LAUNCH(launch_gemm_f16(L.o->dtype, L.o->view, QL, m->pf_xh, m->pf_rs, n, m->pf_hid,
                                    m->pf_hid, st, m->pf_kpart, m->pf_kpart_floats),
                    "gemm_attn_output");

@@ -15,6 +15,7 @@
 
 #include <algorithm>
 
+#include "hyq_f16rows.hpp"
 #include "hyq_tile.hpp"
 #include "hyq_wave.hpp"
 
@@ -89,13 +90,7 @@ __global__ __launch_bounds__(256) void rows_to_f16_kernel(const float *__restric
     if ((t & 63) == 0) wred[t >> 6] = m;
     __syncthreads();
     m = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
-    int e = 0;
-    if (m > 0.f && m < INFINITY) {
-        int ex;
-        const float fr = frexpf(m, &ex); // m = fr * 2^ex, fr in [0.5, 1)
-        e = (fr == 0.5f ? ex - 1 : ex) - 14;
-        e = max(-110, min(114, e)); // both 2^e and 2^-e stay normal floats
-    }
+    const int e = f16_row_exponent(m);
     const float inv = ldexpf(1.0f, -e);
     if (t == 0) rscale[r] = ldexpf(1.0f, e);
     _Float16 *o = xh + (size_t)r * K;

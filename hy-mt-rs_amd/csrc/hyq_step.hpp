@@ -57,6 +57,15 @@ int launch_attention(const float *q, const float *kcache, const float *vcache, c
 int launch_attention_rows(const float *q, const float *kcache, const float *vcache,
                           const int *pos, int n, int context, int heads, int kvh, float *part,
                           float *out, void *stream);
+// The same with the rows merged one workgroup per token, written as f32
+// (out, if given) and/or as the attention-output GEMM's f16 operand rows
+// with their power-of-two scales (xh, rscale, if given); hipErrorInvalidValue
+// when a row's merge needs more than 64 KiB of LDS (merge_rows_lds).
+int launch_attention_rows_f16(const float *q, const float *kcache, const float *vcache,
+                              const int *pos, int n, int context, int heads, int kvh,
+                              float *part, float *out, _Float16 *xh, float *rscale,
+                              void *stream);
+size_t merge_rows_lds(int heads, int splits);
 // Merge of n query rows' split partials ([n][heads][splits][PART_STRIDE],
 // `chunk` positions per split) into out [n][heads*128].
 int launch_attention_merge_rows(const float *part, int splits, int chunk, int heads,
