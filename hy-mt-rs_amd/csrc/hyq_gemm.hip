@@ -202,7 +202,8 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float4 *__restri
 //              ascending; inside an expert, pairs in input order - the order
 //              in which Moe::forward pushes assignments, src/model.rs:694-697)
 //   eoff[e]    first position of expert e (eoff[E] = valid pairs)
-//   tiles[i]   (expert, chunk) of every BN-token chunk of a non-empty expert
+//   tiles[i]   (expert, chunk) of every chunk of a non-empty expert: BN tokens
+//              for the LDS-tiled kernels, 16 for the Q4_K register kernels
 //   toff/tlist for each token, its positions q in ascending expert order
 //              (the order the scatter-add visits them, src/model.rs:700-722)
 // Pairs whose token or expert is out of range are dropped.
@@ -263,7 +264,7 @@ __global__ __launch_bounds__(256) void moe_plan_kernel(const int *__restrict__ p
                                                        const int *__restrict__ pexp, int P, int T,
                                                        int E, int *eoff, int *order, int *rank,
                                                        int *toff, int *tlist, int *tiles,
-                                                       int *ntiles)
+                                                       int *ntiles, int chunk)
 {
     __shared__ int cnt[PLAN_MAX];
     __shared__ int lkey[256];
@@ -280,8 +281,8 @@ __global__ __launch_bounds__(256) void moe_plan_kernel(const int *__restrict__ p
         const int e = ekey(p);
         if (e >= 0) order[eoff[e] + rank[p]] = p;
     }
-    // BN-token chunks of every expert
-    for (int e = t; e < E; e += 256) cnt[e] = (cnt[e] + BN - 1) / BN;
+    // chunk-token chunks of every expert
+    for (int e = t; e < E; e += 256) cnt[e] = (cnt[e] + chunk - 1) / chunk;
     __syncthreads();
     block_exclusive_scan(cnt, E, rank, lsum); // rank[0..E] reused as chunk offsets
     for (int e = t; e < E; e += 256)
@@ -601,13 +602,15 @@ MoeLayout moe_layout(int tokens, int npairs, int experts, int hidden, int mid)
         off += (bytes + 255) / 256 * 256;
         return o;
     };
+    const int few = moe_q4k_chunk();
     L.max_tiles = npairs / BN + (experts < npairs ? experts : npairs) + 1;
+    L.max_tiles_few = npairs / few + (experts < npairs ? experts : npairs) + 1;
     L.eoff = take(4 * ((size_t)experts + 1));
     L.order = take(4 * (size_t)npairs);
     L.rank = take(4 * ((size_t)npairs + experts + tokens + 1));
     L.toff = take(4 * ((size_t)tokens + 1));
     L.tlist = take(4 * (size_t)npairs);
-    L.tiles = take(8 * (size_t)L.max_tiles);
+    L.tiles = take(8 * (size_t)L.max_tiles_few);
     L.ntiles = take(4);
     L.xg = take(2 * (size_t)npairs * hidden);
     L.xscale = take(4 * (size_t)npairs);
@@ -615,6 +618,15 @@ MoeLayout moe_layout(int tokens, int npairs, int experts, int hidden, int mid)
     L.h = take(2 * (size_t)npairs * mid);
     L.hscale = take(4 * (size_t)npairs);
     L.outp = take(4 * (size_t)npairs * hidden);
+    const size_t cols = (size_t)L.max_tiles_few * few; // chunk columns of the Q4_K kernels
+    L.tmax = take(4 * (size_t)tokens);
+    L.hmax = take(4 * (size_t)npairs);
+    L.xc = take(2 * cols * hidden);
+    L.xmc = take(2 * (size_t)L.max_tiles_few * hidden);
+    L.xsc = take(4 * cols);
+    L.hc = take(2 * cols * mid);
+    L.hmc = take(2 * (size_t)L.max_tiles_few * mid);
+    L.hsc = take(4 * cols);
     L.bytes = off;
     return L;
 }
@@ -638,8 +650,25 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
     float *h32 = (float *)(scratch + L.h32), *outp = (float *)(scratch + L.outp);
     if (npairs == 0) return 0;
 
+    // Register-operand Q4_K kernels while the pairs average at most one
+    // 16-token chunk per expert (weight-bound); the LDS-tiled GEMM otherwise.
+    const bool few = fmt_gu == Q4_K && fmt_down == Q4_K && hidden % 256 == 0 &&
+                     mid % 256 == 0 && npairs <= moe_q4k_chunk() * experts;
     hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, ptok, pexp, npairs, tokens,
-                       experts, eoff, order, rank, toff, tlist, tiles, ntiles);
+                       experts, eoff, order, rank, toff, tlist, tiles, ntiles,
+                       few ? moe_q4k_chunk() : BN);
+    if (few) {
+        int rc = launch_moe_q4k(gate, up, down, hidden, mid, x, tokens, ptok, eoff, order, tiles,
+                                ntiles, L.max_tiles_few, (float *)(scratch + L.tmax),
+                                (_Float16 *)(scratch + L.xc), (_Float16 *)(scratch + L.xmc),
+                                (float *)(scratch + L.xsc), h32, (uint32_t *)(scratch + L.hmax),
+                                (_Float16 *)(scratch + L.hc), (_Float16 *)(scratch + L.hmc),
+                                (float *)(scratch + L.hsc), outp, stream);
+        if (rc) return rc;
+        hipLaunchKernelGGL(moe_combine_kernel, dim3((hidden + 255) / 256, tokens), dim3(256), 0,
+                           st, out, hidden, toff, tlist, order, pw, outp);
+        return (int)hipGetLastError();
+    }
     hipLaunchKernelGGL(rows_to_f16_kernel, dim3(npairs), dim3(256), 0, st, x, hidden, order,
                        ptok, eoff + experts, nullptr, 0.f, xg, xscale);
     {

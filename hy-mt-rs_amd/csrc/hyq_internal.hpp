@@ -180,8 +180,9 @@ int launch_gate_up_f16(int fmt, WView gate, WView up, int cols, const _Float16 *
 
 // Byte offsets of the MoE scratch regions (hyq_gemm.hip: moe_layout).
 struct MoeLayout {
-    size_t eoff, order, rank, toff, tlist, tiles, ntiles, xg, xscale, h32, h, hscale, outp, bytes;
-    int max_tiles;
+    size_t eoff, order, rank, toff, tlist, tiles, ntiles, xg, xscale, h32, h, hscale, outp;
+    size_t tmax, xc, xmc, xsc, hmax, hc, hmc, hsc, bytes;
+    int max_tiles, max_tiles_few;
 };
 MoeLayout moe_layout(int tokens, int npairs, int experts, int hidden, int mid);
 int moe_plan_max();
@@ -190,6 +191,16 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
                const float *x, int tokens, const int *ptok, const int *pexp, const float *pw,
                int npairs, int experts, uint8_t *scratch, const MoeLayout &L, float *out,
                void *stream);
+// The Q4_K register-operand expert kernels (hyq_moe_q4k.hip) after a plan
+// of moe_q4k_chunk()-token chunks; xc/xmc/xsc and hc/hmc/hsc hold the
+// per-chunk activation operands of gate/up and of down, tmax / hmax the
+// largest magnitudes of the token rows and of the SiLU product rows.
+int launch_moe_q4k(WView gate, WView up, WView down, int hidden, int mid, const float *x,
+                   int tokens, const int *ptok, const int *eoff, const int *order,
+                   const int *tiles, const int *ntiles, int max_tiles, float *tmax,
+                   _Float16 *xc, _Float16 *xmc, float *xsc, float *h32, uint32_t *hmax,
+                   _Float16 *hc, _Float16 *hmc, float *hsc, float *outp, void *stream);
+int moe_q4k_chunk();
 int isums_per_group(int fmt);
 
 } // namespace hyq

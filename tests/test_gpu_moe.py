@@ -125,6 +125,37 @@ def test_moe_uneven_groups_and_empty_experts(gpu_ctx, hyq, oracle):
     assert np.all(got[150:159] == 0.0)  # tokens 150..158 are routed nowhere
 
 
+def test_moe_q4k_few_token_chunks(gpu_ctx, hyq, oracle):
+    """Pairs averaging at most 16 per expert take the Q4_K register kernels:
+    one expert with 40 tokens (16-token chunks 16 + 16 + 8), empty experts, a
+    token routed nowhere, and token rows scaled by 1e6 and 1e-6 (the f16 row
+    scale of the activation operand and of the SiLU product)."""
+    hidden, mid, experts, tokens = 512, 768, 12, 44
+    gate = random_matrix(Q4_K, experts * mid, hidden, seed=41)
+    up = random_matrix(Q4_K, experts * mid, hidden, seed=42)
+    down = random_matrix(Q4_K, experts * hidden, mid, seed=43)
+    x = np.random.default_rng(44).normal(0, 1, (tokens, hidden)).astype(np.float32)
+    x[5] *= 1e6
+    x[9] *= 1e-6
+    x = x.ravel()
+    seed_out = np.random.default_rng(45).normal(0, 1, (tokens, hidden)).astype(np.float32)
+    seed_out[9] = 0.0  # so row 9's check sees its 1e-6-scaled expert sum
+    pt = list(range(40)) + [40, 41, 42, 5, 9, 0]
+    pe = [3] * 40 + [7, 7, 11, 0, 0, 11]
+    pw = np.random.default_rng(46).uniform(0.1, 1.0, len(pt)).astype(np.float32)
+    perm = np.random.default_rng(47).permutation(len(pt))
+    pt, pe, pw = np.array(pt, np.int32)[perm], np.array(pe, np.int32)[perm], pw[perm]
+    G = gpu_ctx.upload(Q4_K, gate, (hidden, mid, experts))
+    U = gpu_ctx.upload(Q4_K, up, (hidden, mid, experts))
+    D = gpu_ctx.upload(Q4_K, down, (mid, hidden, experts))
+    got = hyq.moe_experts(G, U, D, x, tokens, pt, pe, pw, seed_out).reshape(tokens, hidden)
+    ref, mag = chain_f64(oracle, Q4_K, Q4_K, gate, up, down, hidden, mid, x, pt, pe, pw,
+                         seed_out, range(tokens))
+    for t in range(tokens):
+        check_moe(got[t:t + 1], ref[t][None], mag[t][None], f"few-token row {t}")
+    assert np.array_equal(got[43], seed_out[43])  # token 43 is routed nowhere
+
+
 def test_moe_30b_a3b_shape_sampled_tokens(gpu_ctx, hyq, oracle):
     """64 tokens, top-8 of 64 experts (softmax routing), hidden 2048, mid 1536,
     Q4_K experts; every token's output is produced, 6 seeded tokens are
