@@ -444,6 +444,12 @@ def main() -> int:
             "C2_STQ1_0_gate_up_12288x2048": (STQ1_0, 12288, 2048),
             "C2_STQ1_0_down_2048x6144": (STQ1_0, 2048, 6144),
             "C2_Q6_K_lm_head_120818x2048": (Q6_K, 120818, 2048),
+            # the same kernels at 7B shapes (hidden 4096, FFN 14336)
+            "7B_Q4_K_qkv_6144x4096": (Q4_K, 6144, 4096),
+            "7B_Q4_K_gate_14336x4096": (Q4_K, 14336, 4096),
+            "7B_Q6_K_down_4096x14336": (Q6_K, 4096, 14336),
+            "7B_Q2_0C_gate_up_28672x4096": (Q2_0C, 28672, 4096),
+            "7B_STQ1_0_gate_up_28672x4096": (STQ1_0, 28672, 4096),
         }.items():
             us, gbs = gemv_rate(hyq, ctx, ev, dt_, rows, cols)
             gemv[name] = dict(us=round(us, 3), GBs=round(gbs, 1),

@@ -210,28 +210,32 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float4 *__restri
 // ---------------------------------------------------------------------------
 constexpr int PLAN_MAX = 4096; // experts and tokens per call
 
-// Exclusive scan of cnt[0..n) in LDS into off[0..n] (global), 256 threads.
+// Exclusive scan of cnt[0..n) in LDS into off[0..n] (global), 256 threads:
+// each thread sums a contiguous range, the range sums are scanned within each
+// wave by shuffles and across the four waves through lsum[0..3].
 __device__ void block_exclusive_scan(const int *cnt, int n, int *off, int *lsum)
 {
-    const int t = threadIdx.x;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int per = (n + 255) / 256;
     const int lo = t * per, hi = min(n, lo + per);
     int s = 0;
     for (int i = lo; i < hi; ++i) s += cnt[i];
-    lsum[t] = s;
-    __syncthreads();
-    for (int d = 1; d < 256; d <<= 1) {
-        const int v = t >= d ? lsum[t - d] : 0;
-        __syncthreads();
-        lsum[t] += v;
-        __syncthreads();
+    int v = s; // inclusive scan over the wave
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int u = __shfl_up(v, d);
+        if (lane >= d) v += u;
     }
-    int run = lsum[t] - s;
+    if (lane == 63) lsum[w] = v;
+    __syncthreads();
+    int wb = 0;
+    for (int j = 0; j < w; ++j) wb += lsum[j];
+    int run = wb + v - s;
     for (int i = lo; i < hi; ++i) {
         off[i] = run;
         run += cnt[i];
     }
-    if (t == 255) off[n] = lsum[255];
+    if (t == 255) off[n] = wb + v;
     __syncthreads();
 }
 
@@ -250,8 +254,15 @@ __device__ void stable_rank(const KeyFn &key, int n, int *cnt, int nkeys, int *r
         lkey[t] = k;
         __syncthreads();
         if (k >= 0) {
+            // keys of the earlier threads, four per LDS read, four reads in flight
+            const int4 *l4 = reinterpret_cast<const int4 *>(lkey);
             int r = 0;
-            for (int j = 0; j < t; ++j) r += lkey[j] == k;
+#pragma unroll 4
+            for (int j = 0; j < (t >> 2); ++j) {
+                const int4 v = l4[j];
+                r += (v.x == k) + (v.y == k) + (v.z == k) + (v.w == k);
+            }
+            for (int j = t & ~3; j < t; ++j) r += lkey[j] == k;
             rank[i] = cnt[k] + r;
         }
         __syncthreads();
@@ -267,7 +278,7 @@ __global__ __launch_bounds__(256) void moe_plan_kernel(const int *__restrict__ p
                                                        int *ntiles, int chunk)
 {
     __shared__ int cnt[PLAN_MAX];
-    __shared__ int lkey[256];
+    __shared__ __attribute__((aligned(16))) int lkey[256];
     __shared__ int lsum[256];
     const int t = threadIdx.x;
     auto ekey = [&](int p) {
@@ -298,6 +309,119 @@ __global__ __launch_bounds__(256) void moe_plan_kernel(const int *__restrict__ p
     stable_rank(tkey, nv, cnt, T, rank, lkey);
     block_exclusive_scan(cnt, T, toff, lsum);
     for (int q = t; q < nv; q += 256) tlist[toff[tkey(q)] + rank[q]] = q;
+}
+
+// The plan for up to PLAN_SMALL pairs (and at most PLAN_SMALL tokens and
+// experts) with every intermediate in LDS: the same outputs as
+// moe_plan_kernel, without its global round trips between the steps.
+constexpr int PLAN_SMALL = 2048;
+
+__device__ void lds_exclusive_scan(const int *cnt, int n, int *off, int *lsum)
+{
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int per = (n + 255) / 256;
+    const int lo = t * per, hi = min(n, lo + per);
+    int s = 0;
+    for (int i = lo; i < hi; ++i) s += cnt[i];
+    int v = s;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int u = __shfl_up(v, d);
+        if (lane >= d) v += u;
+    }
+    if (lane == 63) lsum[w] = v;
+    __syncthreads();
+    int wb = 0;
+    for (int j = 0; j < w; ++j) wb += lsum[j];
+    int run = wb + v - s;
+    for (int i = lo; i < hi; ++i) {
+        off[i] = run;
+        run += cnt[i];
+    }
+    if (t == 255) off[n] = wb + v;
+    __syncthreads();
+}
+
+// rank[i] = number of j < i with key[j] == key[i] (key < 0 skipped), cnt[k]
+// = count of key k; all arrays in LDS, key 16-byte aligned and padded with
+// -1 to a multiple of 4.
+__device__ void lds_stable_rank(const int *key, int n, int *cnt, int nkeys, int *rank)
+{
+    const int t = threadIdx.x;
+    for (int k = t; k < nkeys; k += 256) cnt[k] = 0;
+    __syncthreads();
+    for (int base = 0; base < n; base += 256) {
+        const int i = base + t;
+        const int k = i < n ? key[i] : -1;
+        if (k >= 0) {
+            const int4 *l4 = reinterpret_cast<const int4 *>(key + base);
+            int r = 0;
+#pragma unroll 4
+            for (int j = 0; j < (t >> 2); ++j) {
+                const int4 v = l4[j];
+                r += (v.x == k) + (v.y == k) + (v.z == k) + (v.w == k);
+            }
+            for (int j = t & ~3; j < t; ++j) r += key[base + j] == k;
+            rank[i] = cnt[k] + r;
+        }
+        __syncthreads();
+        if (k >= 0) atomicAdd(&cnt[k], 1);
+        __syncthreads();
+    }
+}
+
+__global__ __launch_bounds__(256) void moe_plan_small_kernel(
+    const int *__restrict__ ptok, const int *__restrict__ pexp, int P, int T, int E, int *eoff,
+    int *order, int *toff, int *tlist, int *tiles, int *ntiles, int chunk)
+{
+    __shared__ int cnt[PLAN_SMALL];
+    __shared__ int off[PLAN_SMALL + 1];
+    __shared__ __attribute__((aligned(16))) int key[PLAN_SMALL + 4];
+    __shared__ int tok[PLAN_SMALL];
+    __shared__ int ord[PLAN_SMALL];
+    __shared__ int rank[PLAN_SMALL + 1];
+    __shared__ int lsum[4];
+    const int t = threadIdx.x;
+    const int P4 = (P + 3) & ~3;
+    for (int p = t; p < P4; p += 256) {
+        int e = -1, tk = -1;
+        if (p < P) {
+            tk = ptok[p];
+            e = pexp[p];
+            if (!(tk >= 0 && tk < T && e >= 0 && e < E)) e = -1;
+        }
+        key[p] = e;
+        tok[p] = tk;
+    }
+    __syncthreads();
+    // group pairs by expert (stable)
+    lds_stable_rank(key, P, cnt, E, rank);
+    lds_exclusive_scan(cnt, E, off, lsum);
+    for (int e = t; e <= E; e += 256) eoff[e] = off[e];
+    for (int p = t; p < P; p += 256)
+        if (key[p] >= 0) ord[off[key[p]] + rank[p]] = p;
+    __syncthreads();
+    const int nv = off[E];
+    for (int q = t; q < nv; q += 256) order[q] = ord[q];
+    // chunk-token chunks of every expert
+    for (int e = t; e < E; e += 256) cnt[e] = (off[e + 1] - off[e] + chunk - 1) / chunk;
+    __syncthreads();
+    lds_exclusive_scan(cnt, E, rank, lsum); // rank[0..E]: chunk offsets
+    for (int e = t; e < E; e += 256)
+        for (int c = 0; c < cnt[e]; ++c) {
+            tiles[2 * (rank[e] + c)] = e;
+            tiles[2 * (rank[e] + c) + 1] = c;
+        }
+    if (t == 0) *ntiles = rank[E];
+    __syncthreads();
+    // for each token, its positions in ascending expert order
+    const int nv4 = (nv + 3) & ~3;
+    for (int q = t; q < nv4; q += 256) key[q] = q < nv ? tok[ord[q]] : -1;
+    __syncthreads();
+    lds_stable_rank(key, nv, cnt, T, rank);
+    lds_exclusive_scan(cnt, T, off, lsum);
+    for (int k = t; k <= T; k += 256) toff[k] = off[k];
+    for (int q = t; q < nv; q += 256) tlist[off[key[q]] + rank[q]] = q;
 }
 
 __device__ __forceinline__ float silu_mul(float g, float u)
@@ -654,9 +778,14 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
     // 16-token chunk per expert (weight-bound); the LDS-tiled GEMM otherwise.
     const bool few = fmt_gu == Q4_K && fmt_down == Q4_K && hidden % 256 == 0 &&
                      mid % 256 == 0 && npairs <= moe_q4k_chunk() * experts;
-    hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, ptok, pexp, npairs, tokens,
-                       experts, eoff, order, rank, toff, tlist, tiles, ntiles,
-                       few ? moe_q4k_chunk() : BN);
+    if (npairs <= PLAN_SMALL && tokens <= PLAN_SMALL && experts <= PLAN_SMALL)
+        hipLaunchKernelGGL(moe_plan_small_kernel, dim3(1), dim3(256), 0, st, ptok, pexp, npairs,
+                           tokens, experts, eoff, order, toff, tlist, tiles, ntiles,
+                           few ? moe_q4k_chunk() : BN);
+    else
+        hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, ptok, pexp, npairs, tokens,
+                           experts, eoff, order, rank, toff, tlist, tiles, ntiles,
+                           few ? moe_q4k_chunk() : BN);
     if (few) {
         int rc = launch_moe_q4k(gate, up, down, hidden, mid, x, tokens, ptok, eoff, order, tiles,
                                 ntiles, L.max_tiles_few, (float *)(scratch + L.tmax),
