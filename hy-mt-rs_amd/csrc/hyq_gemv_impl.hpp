@@ -34,6 +34,12 @@ __device__ __forceinline__ float silu_mul(float g, float u)
 }
 
 __device__ __forceinline__ float reduce8(float v) { return wave::sum8(v); }
+// sum over each 32-lane half of the wave
+__device__ __forceinline__ float sum32(float v)
+{
+    v = wave::sum16(v);
+    return v + __shfl_xor(v, 16);
+}
 
 // The f32 input stage, as Q8::quantize_into (src/quant.rs:904-922) and
 // q8_quantize_group do, writing the Q8 row to the LDS slots and the group
@@ -259,13 +265,16 @@ constexpr int HALF_MAX_WORKGROUPS = 256;
 template <int F, int NR, int MODE, int IN>
 constexpr bool HALF_GEMV = HasHalf<F>::value && IN != 0 && NR == 1 && MODE != GEMV_ISUMS;
 
-template <int F, int NR, int MODE, int IN, int P, bool H>
+template <int F, int NR, int MODE, int IN, int P, bool H, int SL = 0>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
 {
     static_assert(!H || HALF_GEMV<F, NR, MODE, IN>, "half-group mode: see HALF_GEMV");
+    static_assert(SL == 0 || (SL == 32 && !H && NR == 1 && MODE == GEMV_PLAIN && P == 0),
+                  "wide rows: 32 lanes per row, plain, one row per lane");
     using G = typename GroupOf<F>::T;
     using Dt = typename GemvData<G, H>::T;
-    constexpr int SUBL = H ? 16 : 8; // lanes per row
+    constexpr int SUBL = SL ? SL : H ? 16 : 8; // lanes per row
+    constexpr int GSTEP = H ? 8 : SUBL;        // groups a row-set takes per step
     extern __shared__ int lds[];
 
     const int groups = a.groups;
@@ -372,7 +381,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     Dt dp[P > 0 ? P : 1];
     if (P > 0) {
 #pragma unroll
-        for (int u = 0; u < P; ++u) load(dp[u], a.seg[0].w, lrowc[0], min(gi + 8 * u, groups - 1));
+        for (int u = 0; u < P; ++u) load(dp[u], a.seg[0].w, lrowc[0], min(gi + GSTEP * u, groups - 1));
     } else {
         load_group(min(gi, groups - 1));
     }
@@ -468,18 +477,55 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
             return acc + G::template dot<false>(D, act, xq, g, nullptr);
         }
     };
-    if (P > 0) {
+    if constexpr (P > 0) {
 #pragma unroll
         for (int u = 0; u < P; ++u) {
-            const int g = gi + 8 * u;
+            const int g = gi + GSTEP * u;
             // (uniform over each pair of half lanes, so the DPP partner is live)
             if (g >= groups || !valid[0]) continue;
             int act[NACT];
             stage_act(g, act);
             acc[0] = accum(acc[0], dp[u], act, g);
         }
+    } else if constexpr (NR == 1 && MODE != GEMV_SILU) {
+        // The lane's next group is in flight while the current one is used:
+        // two register sets, the loop unrolled by two; the load past the
+        // lane's last group re-reads group groups - 1 (in bounds, unused).
+        Dt e[NR];
+        Dt e2[MODE == GEMV_SILU ? NR : 1];
+        auto load_into = [&](Dt *dd, Dt *dd2, int g) {
+#pragma unroll
+            for (int i = 0; i < NR; ++i) {
+                const WView &w = MODE == GEMV_MULTI ? a.seg[seg[i]].w : a.seg[0].w;
+                load(dd[i], w, lrowc[i], g);
+                if (MODE == GEMV_SILU) load(dd2[i], a.seg[1].w, lrowc[i], g);
+            }
+        };
+        auto step = [&](const Dt *dc, const Dt *dc2, int g) {
+            int act[NACT];
+            stage_act(g, act);
+#pragma unroll
+            for (int i = 0; i < NR; ++i) {
+                if (!valid[i]) continue;
+                if constexpr (MODE == GEMV_ISUMS && !H) {
+                    int32_t *out = a.isums + ((size_t)lrow[i] * groups + g) * G::ISUMS;
+                    acc[i] += G::template dot<true>(dc[i], act, xq, g, out);
+                } else {
+                    acc[i] = accum(acc[i], dc[i], act, g);
+                    if (MODE == GEMV_SILU) acc2[i] = accum(acc2[i], dc2[i], act, g);
+                }
+            }
+        };
+        int g = gi;
+        for (; g + GSTEP < groups; g += 2 * GSTEP) {
+            load_into(e, e2, g + GSTEP);
+            step(d, d2, g);
+            load_into(d, d2, min(g + 2 * GSTEP, groups - 1));
+            step(e, e2, g + GSTEP);
+        }
+        if (g < groups) step(d, d2, g);
     } else {
-        for (int g = gi; g < groups; g += 8) {
+        for (int g = gi; g < groups; g += GSTEP) {
             int act[NACT];
             stage_act(g, act);
             if (g != gi) load_group(g);
@@ -499,7 +545,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
 
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
-        const float v = H ? wave::sum16(acc[i]) : reduce8(acc[i]);
+        const float v = H ? wave::sum16(acc[i]) : SUBL == 32 ? sum32(acc[i]) : reduce8(acc[i]);
         const float v2 = MODE == GEMV_SILU ? (H ? wave::sum16(acc2[i]) : reduce8(acc2[i])) : 0.f;
         if (sub != 0 || !valid[i] || MODE == GEMV_ISUMS) continue;
         if (MODE == GEMV_SILU) {
@@ -585,20 +631,31 @@ template <int F> int launch_gemv_format(int mode, const GemvArgs &a, void *strea
         const bool heavy = F == Q6_K || F == Q8_0 || F == Q4_K || mode == GEMV_SILU;
         if (rows >= 8 * 4 * 4 * 1024 && !heavy) nr = 4;
         else if (rows >= 8 * 2 * 4 * 1024) nr = 2;
-        if (rows >= 8 * nr * 4 * 512) waves = 4;
+        // one row per lane with Q8 input: single-wave workgroups measured
+        // fastest (7B shapes, 6144-28672 rows); otherwise the largest tiles
+        // that keep ~2 workgroups per CU
+        if (nr == 1 && !a.xin) waves = 1;
+        else if (rows >= 8 * nr * 4 * 512) waves = 4;
         else if (rows >= 8 * nr * 2 * 512) waves = 2;
     }
     // With an f32 input stage every workgroup quantizes the whole input row,
     // so fewer, wider workgroups (4 waves) share that work.
     if (a.xin) waves = 4;
     const int ks = a.kslices > 1 ? a.kslices : 1;
+    // wide rows (32 lanes per row, two rows per wave): a plain GEMV of at
+    // least 32 groups per row whose 8-lane row-sets would leave most SIMDs
+    // without a wave; chosen from the shape alone, for the Q8 and the f32
+    // input alike, so that both launches sum in the same order
+    const bool wide = mode == GEMV_PLAIN && nr == 1 && ks == 1 && a.norm == nullptr &&
+                      a.groups >= 32 && rows < 8 * 2048;
     // half-group mode (Q2_0C, f32 stage, one row per lane; 4 rows per wave)
     // when its workgroups (twice the full-group count) still fit the 256 CUs
     // one each: a CU holding two would be the launch's tail
     const int half_wgs = (rows + 4 * waves - 1) / (4 * waves) * ks;
-    const bool half = HasHalf<F>::value && a.xin && nr == 1 && mode != GEMV_ISUMS &&
+    const bool half = HasHalf<F>::value && a.xin && nr == 1 && mode != GEMV_ISUMS && !wide &&
                       half_wgs <= HALF_MAX_WORKGROUPS;
-    const int rows_per_block = (half ? 4 : 8) * nr * waves;
+    if (wide) waves = 4;
+    const int rows_per_block = (wide ? 2 : half ? 4 : 8) * nr * waves;
     // a K split is a plain GEMV of an f32 row without norm, residual or
     // partial-row inputs (each slice writes its own partial row)
     if (ks > 1 && (mode != GEMV_PLAIN || !a.xin || a.norm || a.residual || a.nsparts || a.nrparts))
@@ -611,6 +668,13 @@ template <int F> int launch_gemv_format(int mode, const GemvArgs &a, void *strea
     // groups per lane preloaded by the plain one-row-per-lane kernel
     const int pre = a.groups <= 32 ? (a.groups + 7) / 8 : 0;
     hipStream_t st = (hipStream_t)stream;
+    if (wide) {
+        if (!a.xin)
+            hipLaunchKernelGGL((gemv_kernel<F, 1, GEMV_PLAIN, 0, 0, false, 32>), grid, block, lds, st, a);
+        else
+            hipLaunchKernelGGL((gemv_kernel<F, 1, GEMV_PLAIN, 1, 0, false, 32>), grid, block, lds, st, a);
+        return (int)hipGetLastError();
+    }
     if (!a.xin) return launch_in<F, 0, false>(mode, nr, pre, a, grid, block, lds, st);
     if constexpr (HasHalf<F>::value) {
         if (half) {

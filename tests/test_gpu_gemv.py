@@ -134,6 +134,30 @@ def test_gemv_k6144_down_shape(gpu_ctx, oracle, dtype):
     check_decode_path(y, y_ref, mag, NAMES[dtype])
 
 
+@pytest.mark.parametrize("dtype", QUANT, ids=lambda d: NAMES[d])
+def test_gemv_wide_rows(gpu_ctx, hyq, oracle, dtype):
+    """Rows of at least 32 groups with few rows (a 7B down-projection shape,
+    shortened) take the kernel with 32 lanes per row: 36 groups (some lanes
+    hold two, some one), a ragged last workgroup; both the f32-input launch
+    (matmul, which for Q2_0C takes the half-group kernel at this row count)
+    and the Q8-input launch."""
+    rows, cols = 1001, 36 * 256
+    _print("wide", NAMES[dtype])
+    w = random_matrix(dtype, rows, cols, seed=31 + dtype)
+    x = np.random.default_rng(11 + dtype).normal(0, 1, cols).astype(np.float32)
+    W = gpu_ctx.upload(dtype, w, (cols, rows))
+    y = W.matmul(x, 1)
+    q, s = oracle.q8_quantize(x)
+    y_ref, mag = oracle.gemv_q8_f64(dtype, w, rows, cols, q, s)
+    check_decode_path(y, y_ref, mag, NAMES[dtype])
+    q8 = gpu_ctx.q8(cols)
+    xd = gpu_ctx.array(x)
+    q8.quantize_into(xd.ptr)
+    yd = gpu_ctx.empty(rows, np.float32)
+    hyq.check(hyq.lib().hyq_gemv_q8_d(gpu_ctx.handle, W.handle, q8.handle, None, yd.ptr))
+    check_decode_path(yd.numpy(), y_ref, mag, NAMES[dtype] + " q8 input")
+
+
 @pytest.mark.parametrize("rows", [1, 7, 8, 9, 63, 65, 513])
 def test_gemv_ragged_rows(gpu_ctx, oracle, rows):
     cols = 512
