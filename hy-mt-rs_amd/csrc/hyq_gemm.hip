@@ -581,7 +581,8 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(float *__restrict__ ou
                                                           const int *__restrict__ tlist,
                                                           const int *__restrict__ order,
                                                           const float *__restrict__ pw,
-                                                          const float *__restrict__ outp)
+                                                          const float *__restrict__ outp,
+                                                          const float *__restrict__ outp2)
 {
     const int t = blockIdx.y;
     const int col = blockIdx.x * 256 + threadIdx.x;
@@ -589,7 +590,9 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(float *__restrict__ ou
     float acc = out[(size_t)t * hidden + col];
     for (int i = toff[t]; i < toff[t + 1]; ++i) {
         const int q = tlist[i];
-        acc = acc + pw[order[q]] * outp[(size_t)q * hidden + col];
+        float v = outp[(size_t)q * hidden + col];
+        if (outp2) v = v + outp2[(size_t)q * hidden + col]; // the second K slice
+        acc = acc + pw[order[q]] * v;
     }
     out[(size_t)t * hidden + col] = acc;
 }
@@ -751,6 +754,9 @@ MoeLayout moe_layout(int tokens, int npairs, int experts, int hidden, int mid)
     L.hc = take(2 * cols * mid);
     L.hmc = take(2 * (size_t)L.max_tiles_few * mid);
     L.hsc = take(4 * cols);
+    L.gpart = take(4 * 2 * (size_t)npairs * mid);
+    L.upart = take(4 * 2 * (size_t)npairs * mid);
+    L.outp2 = take(4 * (size_t)npairs * hidden);
     L.bytes = off;
     return L;
 }
@@ -776,8 +782,8 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
 
     // Register-operand Q4_K kernels while the pairs average at most one
     // 16-token chunk per expert (weight-bound); the LDS-tiled GEMM otherwise.
-    const bool few = fmt_gu == Q4_K && fmt_down == Q4_K && hidden % 256 == 0 &&
-                     mid % 256 == 0 && npairs <= moe_q4k_chunk() * experts;
+    const bool few = fmt_gu == Q4_K && fmt_down == Q4_K && moe_q4k_fits(hidden, mid) &&
+                     npairs <= moe_q4k_chunk() * experts;
     if (npairs <= PLAN_SMALL && tokens <= PLAN_SMALL && experts <= PLAN_SMALL)
         hipLaunchKernelGGL(moe_plan_small_kernel, dim3(1), dim3(256), 0, st, ptok, pexp, npairs,
                            tokens, experts, eoff, order, toff, tlist, tiles, ntiles,
@@ -787,15 +793,19 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
                            experts, eoff, order, rank, toff, tlist, tiles, ntiles,
                            few ? moe_q4k_chunk() : BN);
     if (few) {
-        int rc = launch_moe_q4k(gate, up, down, hidden, mid, x, tokens, ptok, eoff, order, tiles,
-                                ntiles, L.max_tiles_few, (float *)(scratch + L.tmax),
-                                (_Float16 *)(scratch + L.xc), (_Float16 *)(scratch + L.xmc),
-                                (float *)(scratch + L.xsc), h32, (uint32_t *)(scratch + L.hmax),
-                                (_Float16 *)(scratch + L.hc), (_Float16 *)(scratch + L.hmc),
-                                (float *)(scratch + L.hsc), outp, stream);
+        float *outp2 = (float *)(scratch + L.outp2);
+        int rc = launch_moe_q4k(gate, up, down, hidden, mid, x, tokens, ptok, eoff, eoff + experts,
+                                order, tiles, ntiles, L.max_tiles_few, npairs,
+                                (float *)(scratch + L.tmax), (_Float16 *)(scratch + L.xc),
+                                (_Float16 *)(scratch + L.xmc), (float *)(scratch + L.xsc),
+                                (float *)(scratch + L.gpart), (float *)(scratch + L.upart), h32,
+                                (float *)(scratch + L.hmax), (_Float16 *)(scratch + L.hc),
+                                (_Float16 *)(scratch + L.hmc), (float *)(scratch + L.hsc), outp,
+                                outp2, stream);
         if (rc) return rc;
         hipLaunchKernelGGL(moe_combine_kernel, dim3((hidden + 255) / 256, tokens), dim3(256), 0,
-                           st, out, hidden, toff, tlist, order, pw, outp);
+                           st, out, hidden, toff, tlist, order, pw, outp,
+                           moe_q4k_down_slices(mid) > 1 ? outp2 : nullptr);
         return (int)hipGetLastError();
     }
     hipLaunchKernelGGL(rows_to_f16_kernel, dim3(npairs), dim3(256), 0, st, x, hidden, order,
@@ -841,7 +851,7 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
 #undef HYQ_MOE_DN
     }
     hipLaunchKernelGGL(moe_combine_kernel, dim3((hidden + 255) / 256, tokens), dim3(256), 0, st,
-                       out, hidden, toff, tlist, order, pw, outp);
+                       out, hidden, toff, tlist, order, pw, outp, (const float *)nullptr);
     return (int)hipGetLastError();
 }
 

@@ -55,6 +55,17 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int CHUNK = 16; // tokens per expert chunk (one MFMA column block)
+constexpr int MOE_Q4K_MAX_K = 4096;  // largest K (hidden or mid)
+constexpr int MOE_Q4K_MAX_KL = 2048; // largest K slice of one workgroup: 34 KL bytes of LDS
+
+// K slices of the gate/up product: two when its superblocks split evenly
+// (the tiles then number twice the workgroups, which evens out the last
+// round of workgroups on the CUs), else one. The down product (fewer,
+// shorter rows) measured faster unsplit.
+__host__ __device__ inline int moe_kslices(int K) { return (K / 256) % 2 == 0 ? 2 : 1; }
+
+// s_waitcnt lgkmcnt(0), leaving the other counters alone.
+#define HYQ_LGKM0() __builtin_amdgcn_s_waitcnt(0xc07f)
 
 __device__ __forceinline__ float half_bits(uint32_t b)
 {
@@ -148,97 +159,96 @@ __device__ __forceinline__ void superblock(const WRaw &w, const XRaw &x, int g, 
     }
 }
 
-// One superblock of a chunk's activation operand in LDS: 8 MFMA steps x 64
-// lanes x 16 bytes, and 64 lanes x 8 bytes of half-sums.
-struct XLds {
-    uint4 v[8 * 64];
-    uint2 m[64];
-};
-
 // R row tiles (rows[r] = the tile's first weight row, 16 rows each, of
-// matrices w[r]) against one chunk's activation operand (xc, xmc at the
-// chunk) over K: acc[r]. Called by all 256 threads of the workgroup (it holds
-// barriers); the four waves share the activation operand, which the
-// workgroup stages through LDS one superblock ahead (xs[2]), while each wave
-// streams its weights one superblock ahead in two register sets. Loads
-// return in issue order, so each iteration issues the activation loads of
-// superblock b+1 before the weight prefetch of b+1: the compute of b waits
-// for neither, and the LDS store at the end of b waits only for the former.
-// sched_barrier keeps the compiler from moving loads across those points.
-// Every load is unconditional (the last prefetch re-reads superblock nbk-1,
-// an L2 hit).
+// matrices w[r]) against one chunk's activation operand over K: acc[r].
+// Called by all 256 threads of the workgroup. The chunk's whole activation
+// operand (xc: 16 K halves in MFMA lane order, xmc: K half-sums) is copied
+// into LDS once (xl), and each wave then streams its weights through four
+// register sets, three superblocks ahead of the compute: the loop holds no
+// barrier and no other global load, so the compiler's in-order load count
+// waits for exactly the set being used. The first three weight superblocks
+// are issued after the activation loads and before their LDS stores, so
+// their latency overlaps the copy. Past the last superblock the weight loads
+// read an L2-hot dummy (the activation operand), so every step issues the
+// same loads without a branch.
 template <int R>
-__device__ __forceinline__ void tile_rows(const WView *w, const int *rows, int K,
-                                          const _Float16 *xc, const _Float16 *xmc, XLds *xs,
+__device__ __forceinline__ void tile_rows(const WView *w, const int *rows, int kb0, int nbk,
+                                          const _Float16 *xc, const _Float16 *xmc, uint4 *xl,
                                           f4 *acc)
 {
     uint32_t magic;
     asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, rr = lane & 15;
-    const int nbk = K / 256;
+    const int K = 256 * nbk; // the slice: superblocks kb0 .. kb0 + nbk - 1
     const uint8_t *qp[R], *mp[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const size_t blk = (size_t)(rows[r] + rr) * w[r].nb;
+        const size_t blk = (size_t)(rows[r] + rr) * w[r].nb + kb0;
         qp[r] = w[r].p0 + blk * 128 + 16 * g;
         mp[r] = w[r].p1 + blk * 16;
         acc[r] = f4{0.f, 0.f, 0.f, 0.f};
     }
-    const uint4 *xv = reinterpret_cast<const uint4 *>(xc);
-    const uint2 *xm = reinterpret_cast<const uint2 *>(xmc);
-    WRaw wa[R], wb[R];
-    uint4 s0, s1;
-    uint2 sm = make_uint2(0, 0);
-    auto stage = [&](int b) { // global -> registers: this thread's share of superblock b
-        s0 = xv[512 * b + tid];
-        s1 = xv[512 * b + 256 + tid];
-        if (tid < 64) sm = xm[64 * b + tid];
-    };
-    auto store = [&](int b) { // registers -> LDS buffer b & 1
-        XLds &d = xs[b & 1];
-        d.v[tid] = s0;
-        d.v[256 + tid] = s1;
-        if (tid < 64) d.m[tid] = sm;
-    };
-    auto loadw = [&](WRaw *wr, int b) {
+    const uint8_t *dummy = reinterpret_cast<const uint8_t *>(xc); // >= 144 bytes, L2-hot
+    WRaw w0[R], w1[R], w2[R], w3[R];
+    auto loadw = [&](WRaw *wr, int j) {
+        const bool in = j < nbk;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            wr[r].q0 = *reinterpret_cast<const uint4 *>(qp[r] + b * 128);
-            wr[r].q1 = *reinterpret_cast<const uint4 *>(qp[r] + b * 128 + 64);
-            wr[r].meta = *reinterpret_cast<const uint4 *>(mp[r] + b * 16);
+            const uint8_t *q = in ? qp[r] + j * 128 : dummy;
+            const uint8_t *m = in ? mp[r] + j * 16 : dummy;
+            wr[r].q0 = *reinterpret_cast<const uint4 *>(q);
+            wr[r].q1 = *reinterpret_cast<const uint4 *>(q + 64);
+            wr[r].meta = *reinterpret_cast<const uint4 *>(m);
         }
     };
+    // the slice's activation operand: 2K uint4 of steps and K/4 uint2 of
+    // half-sums (K <= MOE_Q4K_MAX_KL: at most 16 and 2 per thread)
+    const uint4 *xs = reinterpret_cast<const uint4 *>(xc) + 512 * kb0;
+    const uint2 *ms = reinterpret_cast<const uint2 *>(xmc) + 64 * kb0;
+    uint2 *xlm = reinterpret_cast<uint2 *>(xl + 2 * K);
+    uint4 tv[MOE_Q4K_MAX_KL / 128];
+    uint2 tm[MOE_Q4K_MAX_KL / 1024];
+    // (loads clamped into bounds and issued unconditionally)
+#pragma unroll
+    for (int j = 0; j < MOE_Q4K_MAX_KL / 128; ++j) tv[j] = xs[min(tid + 256 * j, 2 * K - 1)];
+#pragma unroll
+    for (int j = 0; j < MOE_Q4K_MAX_KL / 1024; ++j) tm[j] = ms[min(tid + 256 * j, K / 4 - 1)];
+    loadw(w0, 0);
+    loadw(w1, 1);
+    loadw(w2, 2);
+    // (stores unconditional too, so that no load sinks into a branch: the
+    // clamped duplicates rewrite the last element with its own value)
+#pragma unroll
+    for (int j = 0; j < MOE_Q4K_MAX_KL / 128; ++j) xl[min(tid + 256 * j, 2 * K - 1)] = tv[j];
+#pragma unroll
+    for (int j = 0; j < MOE_Q4K_MAX_KL / 1024; ++j) xlm[min(tid + 256 * j, K / 4 - 1)] = tm[j];
+    HYQ_LGKM0();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
     auto compute = [&](const WRaw *wr, int b) {
-        const XLds &d = xs[b & 1];
         XRaw xr;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) xr.v[t] = d.v[64 * t + lane];
-        xr.m = d.m[lane];
+        for (int t = 0; t < 8; ++t) xr.v[t] = xl[512 * b + 64 * t + lane];
+        xr.m = xlm[64 * b + lane];
 #pragma unroll
         for (int r = 0; r < R; ++r) superblock(wr[r], xr, g, magic, acc[r]);
     };
-    // one iteration: stage b+1, prefetch weights of b+1 into wn, compute b
-    // from wc, publish b+1
-    auto iter = [&](WRaw *wc, WRaw *wn, int b) {
-        const int nx = min(b + 1, nbk - 1);
-        stage(nx);
-        loadw(wn, nx);
+    auto step = [&](WRaw *wc, WRaw *wn, int b) {
+        loadw(wn, b + 3);
         __builtin_amdgcn_sched_barrier(0);
         compute(wc, b);
         __builtin_amdgcn_sched_barrier(0);
-        store(b + 1);
-        __syncthreads();
     };
-    stage(0);
-    loadw(wa, 0);
-    store(0);
-    __syncthreads();
     int b = 0;
-    for (; b + 2 <= nbk; b += 2) {
-        iter(wa, wb, b);
-        iter(wb, wa, b + 1);
+    for (; b + 4 <= nbk; b += 4) {
+        step(w0, w3, b);
+        step(w1, w0, b + 1);
+        step(w2, w1, b + 2);
+        step(w3, w2, b + 3);
     }
-    if (b < nbk) iter(wa, wb, b);
+    if (b < nbk) step(w0, w3, b);
+    if (b + 1 < nbk) step(w1, w0, b + 1);
+    if (b + 2 < nbk) step(w2, w1, b + 2);
 }
 
 // Workgroup order. Workgroups are dispatched round-robin over the 8 XCDs
@@ -260,76 +270,107 @@ __device__ __forceinline__ bool chunk_tile(int mgroups, int max_tiles, const int
 inline int chunk_grid(int mgroups, int max_tiles) { return 8 * mgroups * ((max_tiles + 7) / 8); }
 
 //
-// Gate and up of one 16-token chunk of an expert: wave w of the workgroup
-// takes mid rows m0 = 64 mg + 16 w of gate and of up; H[q][m] = silu(g) * u
-// for the chunk's pair positions q, in f32, and hmax[q] = the largest |H[q]|
-// as float bits (atomic max; NaN bits order above infinity).
-__global__ __launch_bounds__(256) void moe_q4k_gate_up_kernel(
+// Gate and up of one 16-token chunk of an expert over one K slice: wave w of
+// the workgroup takes mid rows m0 = 64 mg + 16 w of gate and of up; the
+// slice's sums, scaled back by the token column's scale, go to
+// gpart / upart[slice][q][m] for the chunk's pair positions q.
+__global__ __launch_bounds__(256, 2) void moe_q4k_gate_up_kernel(
     WView gate, WView up, int mid, int K, const int *__restrict__ eoff,
     const int *__restrict__ tiles, const int *__restrict__ ntiles,
     const _Float16 *__restrict__ xc, const _Float16 *__restrict__ xmc,
-    const float *__restrict__ xsc, float *__restrict__ H, uint32_t *__restrict__ hmax,
-    int mgroups, int max_tiles)
+    const float *__restrict__ xsc, float *__restrict__ gpart, float *__restrict__ upart,
+    size_t part_stride, int mgroups, int max_tiles)
 {
-    int ti, mg;
-    if (!chunk_tile(mgroups, max_tiles, ntiles, ti, mg)) return;
+    const int ks = moe_kslices(K);
+    int ti, mgk;
+    if (!chunk_tile(mgroups * ks, max_tiles, ntiles, ti, mgk)) return;
+    const int mg = mgk / ks, kh = mgk % ks, nbk = K / 256 / ks;
     const int e = tiles[2 * ti], c = tiles[2 * ti + 1];
     const int nb = eoff[e] + c * CHUNK, cnt = min(CHUNK, eoff[e + 1] - nb);
     const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
     const int m0 = 64 * mg + 16 * (threadIdx.x >> 6);
-    __shared__ XLds xs[2];
+    extern __shared__ uint4 xl[];
     const WView w[2] = {gate, up};
     const int rows[2] = {e * mid + m0, e * mid + m0};
     f4 acc[2];
-    tile_rows<2>(w, rows, K, xc + (size_t)ti * CHUNK * K, xmc + (size_t)ti * K, xs, acc);
+    tile_rows<2>(w, rows, kh * nbk, nbk, xc + (size_t)ti * CHUNK * K, xmc + (size_t)ti * K, xl,
+                 acc);
     // lane (g, rr): tokens 4g+i of mid row m0 + rr
-    const int rr = col;
-    float *hbase = H + (size_t)nb * mid + m0 + rr;
+    const size_t base = kh * part_stride + (size_t)nb * mid + m0 + col;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int tok = 4 * g + i;
-        uint32_t mb = 0;
-        if (tok < cnt) {
-            const float s = xsc[ti * CHUNK + tok];
-            const float h = silu_mul(acc[0][i] * s, acc[1][i] * s);
-            hbase[(size_t)tok * mid] = h;
-            mb = __float_as_uint(fabsf(h));
-        }
-        // the 16 lanes of a lane group hold the wave's 16 rows of this token
-        mb = max(mb, (uint32_t)__shfl_xor((int)mb, 1));
-        mb = max(mb, (uint32_t)__shfl_xor((int)mb, 2));
-        mb = max(mb, (uint32_t)__shfl_xor((int)mb, 4));
-        mb = max(mb, (uint32_t)__shfl_xor((int)mb, 8));
-        if (rr == 0 && tok < cnt) atomicMax(hmax + nb + tok, mb);
+        if (tok >= cnt) continue;
+        const float s = xsc[ti * CHUNK + tok];
+        gpart[base + (size_t)tok * mid] = acc[0][i] * s;
+        upart[base + (size_t)tok * mid] = acc[1][i] * s;
     }
 }
 
-// Down of one 16-token chunk: wave w takes hidden rows m0 = 128 mg + 32 w ..
-// m0 + 31 (two row tiles); outp[q][m] = down_e[m] . H[q].
-__global__ __launch_bounds__(256) void moe_q4k_down_kernel(
+// h[q][m] = silu(g) * u with g, u the sums of the K slices' partial rows (in
+// slice order), and hmax[q] = the row's largest |h| (infinity when it holds
+// a NaN); one workgroup per valid pair position q.
+__global__ __launch_bounds__(256) void silu_rows_kernel(const float *__restrict__ gpart,
+                                                        const float *__restrict__ upart,
+                                                        int ks, size_t part_stride, int mid,
+                                                        const int *__restrict__ valid,
+                                                        float *__restrict__ h,
+                                                        float *__restrict__ hmax)
+{
+    __shared__ float wred[4];
+    const int q = blockIdx.x;
+    if (q >= *valid) return;
+    const int t = threadIdx.x;
+    const size_t row = (size_t)q * mid;
+    float m = 0.f;
+    for (int i = t; i < mid; i += 256) {
+        float gv = gpart[row + i], uv = upart[row + i];
+        if (ks > 1) {
+            gv = gv + gpart[part_stride + row + i];
+            uv = uv + upart[part_stride + row + i];
+        }
+        const float v = silu_mul(gv, uv);
+        h[row + i] = v;
+        m = fmaxf(m, fabsf(v));
+        if (v != v) m = INFINITY;
+    }
+    m = wave::max64(m);
+    if ((t & 63) == 0) wred[t >> 6] = m;
+    __syncthreads();
+    if (t == 0) hmax[q] = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
+}
+
+// Down of one 16-token chunk over one K slice: wave w takes hidden rows
+// m0 = 128 mg + 32 w .. m0 + 31 (two row tiles); the slice's sums
+// down_e[m] . H[q], scaled back, go to outp (slice 0) or outp2 (slice 1).
+__global__ __launch_bounds__(256, 2) void moe_q4k_down_kernel(
     WView down, int hidden, int K, const int *__restrict__ eoff, const int *__restrict__ tiles,
     const int *__restrict__ ntiles, const _Float16 *__restrict__ hc,
     const _Float16 *__restrict__ hmc, const float *__restrict__ hsc, float *__restrict__ outp,
-    int mgroups, int max_tiles)
+    float *__restrict__ outp2, int mgroups, int max_tiles)
 {
-    int ti, mg;
-    if (!chunk_tile(mgroups, max_tiles, ntiles, ti, mg)) return;
+    const int ks = 1;
+    int ti, mgk;
+    if (!chunk_tile(mgroups * ks, max_tiles, ntiles, ti, mgk)) return;
+    const int mg = mgk / ks, kh = mgk % ks, nbk = K / 256 / ks;
     const int m0 = 128 * mg + 32 * (threadIdx.x >> 6); // hidden % 128 == 0: all rows exist
     const int e = tiles[2 * ti], c = tiles[2 * ti + 1];
     const int nb = eoff[e] + c * CHUNK, cnt = min(CHUNK, eoff[e + 1] - nb);
     const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
-    __shared__ XLds xs[2];
+    extern __shared__ uint4 xl[];
     const WView w[2] = {down, down};
     const int rows[2] = {e * hidden + m0, e * hidden + m0 + 16};
     f4 acc[2];
-    tile_rows<2>(w, rows, K, hc + (size_t)ti * CHUNK * K, hmc + (size_t)ti * K, xs, acc);
+    tile_rows<2>(w, rows, kh * nbk, nbk, hc + (size_t)ti * CHUNK * K, hmc + (size_t)ti * K, xl,
+                 acc);
+    float *dst = kh ? outp2 : outp;
     // lane (g, rr): tokens 4g+i of hidden rows m0 + 16r + rr
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int tok = 4 * g + i;
         if (tok >= cnt) continue;
         const float s = hsc[ti * CHUNK + tok];
-        float *orow = outp + (size_t)(nb + tok) * hidden + m0 + col;
+        float *orow = dst + (size_t)(nb + tok) * hidden + m0 + col;
 #pragma unroll
         for (int r = 0; r < 2; ++r) orow[16 * r] = acc[r][i] * s;
     }
@@ -362,13 +403,11 @@ __global__ __launch_bounds__(256) void row_max_kernel(const float *__restrict__ 
 // (a zero, infinite or NaN maximum keeps scale 1); xsc[ti][col] = 2^e. xmc
 // holds per lane f16(X / 16) of the four 16-element half-sums its lane group
 // covers (f32 sums in a fixed order). Columns >= cnt are zero with scale 1.
-// Workgroups (ti, 0) also clear hzero[q] of the chunk's positions (when
-// given), ahead of the atomic maxima of the gate/up epilogue.
 __global__ __launch_bounds__(64) void chunk_q4k_kernel(
     const float *__restrict__ x, int K, const float *__restrict__ rmax,
     const int *__restrict__ tiles, const int *__restrict__ ntiles, const int *__restrict__ eoff,
     const int *__restrict__ order, const int *__restrict__ ptok, _Float16 *__restrict__ xc,
-    _Float16 *__restrict__ xmc, float *__restrict__ xsc, uint32_t *__restrict__ hzero)
+    _Float16 *__restrict__ xmc, float *__restrict__ xsc)
 {
     const int ti = blockIdx.x, b = blockIdx.y;
     if (ti >= *ntiles) return;
@@ -379,10 +418,7 @@ __global__ __launch_bounds__(64) void chunk_q4k_kernel(
     const int src = live ? (order ? ptok[order[nb + col]] : nb + col) : 0;
     const int ex = live ? f16_row_exponent(rmax[src]) : 0;
     const float inv = ldexpf(1.0f, -ex);
-    if (b == 0 && g == 0) {
-        xsc[ti * CHUNK + col] = ldexpf(1.0f, ex);
-        if (hzero && live) hzero[nb + col] = 0u;
-    }
+    if (b == 0 && g == 0) xsc[ti * CHUNK + col] = ldexpf(1.0f, ex);
     auto pk = [](float p, float q) {
         const h2 v = {(_Float16)p, (_Float16)q};
         return __builtin_bit_cast(uint32_t, v);
@@ -412,33 +448,45 @@ __global__ __launch_bounds__(64) void chunk_q4k_kernel(
 } // namespace
 
 int launch_moe_q4k(WView gate, WView up, WView down, int hidden, int mid, const float *x,
-                   int tokens, const int *ptok, const int *eoff, const int *order,
-                   const int *tiles, const int *ntiles, int max_tiles, float *tmax,
-                   _Float16 *xc, _Float16 *xmc, float *xsc, float *h32, uint32_t *hmax,
-                   _Float16 *hc, _Float16 *hmc, float *hsc, float *outp, void *stream)
+                   int tokens, const int *ptok, const int *eoff, const int *valid,
+                   const int *order, const int *tiles, const int *ntiles, int max_tiles,
+                   int npairs, float *tmax, _Float16 *xc, _Float16 *xmc, float *xsc,
+                   float *gpart, float *upart, float *h32, float *hmax, _Float16 *hc,
+                   _Float16 *hmc, float *hsc, float *outp, float *outp2, void *stream)
 {
-    if (hidden % 256 || mid % 256) return (int)hipErrorInvalidValue;
+    if (!moe_q4k_fits(hidden, mid)) return (int)hipErrorInvalidValue;
     hipStream_t st = (hipStream_t)stream;
+    const size_t gstride = (size_t)npairs * mid;
     hipLaunchKernelGGL(row_max_kernel, dim3(tokens), dim3(256), 0, st, x, hidden, tmax);
     hipLaunchKernelGGL(chunk_q4k_kernel, dim3(max_tiles, hidden / 256), dim3(64), 0, st, x, hidden,
-                       tmax, tiles, ntiles, eoff, order, ptok, xc, xmc, xsc, hmax);
+                       tmax, tiles, ntiles, eoff, order, ptok, xc, xmc, xsc);
     {
-        const int mgroups = mid / 64;
-        hipLaunchKernelGGL(moe_q4k_gate_up_kernel, dim3(chunk_grid(mgroups, max_tiles)), dim3(256), 0, st, gate,
-                           up, mid, hidden, eoff, tiles, ntiles, xc, xmc, xsc, h32, hmax, mgroups,
-                           max_tiles);
+        const int mgroups = mid / 64, ks = moe_kslices(hidden);
+        hipLaunchKernelGGL(moe_q4k_gate_up_kernel, dim3(chunk_grid(mgroups * ks, max_tiles)),
+                           dim3(256), (size_t)34 * (hidden / ks), st, gate, up, mid, hidden, eoff,
+                           tiles, ntiles, xc, xmc, xsc, gpart, upart, gstride, mgroups, max_tiles);
     }
+    hipLaunchKernelGGL(silu_rows_kernel, dim3(npairs), dim3(256), 0, st, gpart, upart,
+                       moe_kslices(hidden), gstride, mid, valid, h32, hmax);
     hipLaunchKernelGGL(chunk_q4k_kernel, dim3(max_tiles, mid / 256), dim3(64), 0, st, h32, mid,
-                       reinterpret_cast<const float *>(hmax), tiles, ntiles, eoff, nullptr,
-                       nullptr, hc, hmc, hsc, nullptr);
+                       hmax, tiles, ntiles, eoff, nullptr, nullptr, hc, hmc, hsc);
     {
         const int mgroups = hidden / 128;
-        hipLaunchKernelGGL(moe_q4k_down_kernel, dim3(chunk_grid(mgroups, max_tiles)), dim3(256), 0, st, down,
-                           hidden, mid, eoff, tiles, ntiles, hc, hmc, hsc, outp, mgroups,
-                           max_tiles);
+        hipLaunchKernelGGL(moe_q4k_down_kernel, dim3(chunk_grid(mgroups, max_tiles)),
+                           dim3(256), (size_t)34 * mid, st, down, hidden, mid, eoff, tiles,
+                           ntiles, hc, hmc, hsc, outp, outp2, mgroups, max_tiles);
     }
     return (int)hipGetLastError();
 }
+
+bool moe_q4k_fits(int hidden, int mid)
+{
+    return hidden % 256 == 0 && mid % 256 == 0 && hidden <= MOE_Q4K_MAX_K &&
+           mid <= MOE_Q4K_MAX_K && hidden / moe_kslices(hidden) <= MOE_Q4K_MAX_KL &&
+           mid <= MOE_Q4K_MAX_KL && hidden % 128 == 0;
+}
+
+int moe_q4k_down_slices(int) { return 1; }
 
 int moe_q4k_chunk() { return CHUNK; }
 
