@@ -110,23 +110,23 @@ __global__ __launch_bounds__(256) void rows_to_f16_kernel(const float *__restric
 // in one launch); a tile's BM rows lie in one of them (its row count is a
 // multiple of BM, or it is the last). With kslices > 1 (one weight) grid.y
 // splits K: slice z writes its scaled partial product to
-// part[z][n][m] and gemm_reduce_kernel adds the slices in order.
-template <int F>
-__global__ __launch_bounds__(256, 2) void gemm_f16_kernel(GemmSegs g, int K,
-                                                          const _Float16 *__restrict__ xh,
-                                                          const float *__restrict__ rscale, int N,
-                                                          int mtiles, int ntiles, int kslices,
-                                                          float *__restrict__ part)
+// part[z][n][m] and gemm_reduce_kernel adds the slices in order. NW waves
+// per workgroup: tiles of BM rows by 32 NW tokens, the same arithmetic per
+// element for NW = 4 and 8.
+template <int F, int NW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void gemm_f16_kernel(
+    GemmSegs g, int K, const _Float16 *__restrict__ xh, const float *__restrict__ rscale, int N,
+    int mtiles, int ntiles, int kslices, float *__restrict__ part)
 {
-    __shared__ __attribute__((aligned(16))) _Float16 lds[4 * TILE_HALVES];
+    __shared__ __attribute__((aligned(16))) _Float16 lds[lds_halves<NW>()];
     const int T = xcd_tile(mtiles * ntiles);
     if (T >= mtiles * ntiles) return;
     int mt = T / ntiles, sg = 0;
     while (sg + 1 < g.nseg && mt >= g.s[sg].tiles) mt -= g.s[sg++].tiles;
     const GemmSeg &S = g.s[sg];
     const int M = S.rows;
-    const int m0 = mt * BM, n0 = (T % ntiles) * BN;
-    const int wave = threadIdx.x >> 6, wm = wave >> 1, wn = wave & 1;
+    const int m0 = mt * BM, n0 = (T % ntiles) * (32 * NW);
+    const int wave = threadIdx.x >> 6, wm = wave / (NW / 2), wn = wave % (NW / 2);
 
     f32x16 acc[2][2];
     zero_acc(acc);
@@ -139,7 +139,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(GemmSegs g, int K,
     };
     auto arow = [&](int i) { return wm * 64 + 32 * i; };
     const int kslice = K / kslices;
-    k_loop<F>(wsrc, xrow, arow, kslice, wn, lds, acc, blockIdx.y * kslice);
+    k_loop<F, 2, NW>(wsrc, xrow, arow, kslice, wn, lds, acc, blockIdx.y * kslice);
 
     float *y = kslices > 1 ? part + (size_t)blockIdx.y * N * M : S.y;
     const float *residual = kslices > 1 ? nullptr : S.residual;
@@ -483,19 +483,18 @@ __global__ __launch_bounds__(256, 2) void moe_gate_up_kernel(
 
 // Gate and up of a dense FFN at batch N (DenseFfn::forward, src/model.rs:
 // 679-683): the tile pairs gate rows m0..m0+63 with the same rows of up, as
-// moe_gate_up_kernel does, and writes H[n][m] = silu(g) * u in f32.
-template <int F>
-__global__ __launch_bounds__(256, 2) void gemm_gate_up_kernel(WView gate, WView up, int mid, int K,
-                                                              const _Float16 *__restrict__ xh,
-                                                              const float *__restrict__ rscale,
-                                                              int N, float *__restrict__ H,
-                                                              int mtiles, int ntiles)
+// moe_gate_up_kernel does, and writes H[n][m] = silu(g) * u in f32 (NW waves,
+// 32 NW tokens per tile, as gemm_f16_kernel).
+template <int F, int NW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void gemm_gate_up_kernel(
+    WView gate, WView up, int mid, int K, const _Float16 *__restrict__ xh,
+    const float *__restrict__ rscale, int N, float *__restrict__ H, int mtiles, int ntiles)
 {
-    __shared__ __attribute__((aligned(16))) _Float16 lds[4 * TILE_HALVES];
+    __shared__ __attribute__((aligned(16))) _Float16 lds[lds_halves<NW>()];
     const int T = xcd_tile(mtiles * ntiles);
     if (T >= mtiles * ntiles) return;
-    const int m0 = (T / ntiles) * 64, n0 = (T % ntiles) * BN;
-    const int wave = threadIdx.x >> 6, wm = wave >> 1, wn = wave & 1;
+    const int m0 = (T / ntiles) * 64, n0 = (T % ntiles) * (32 * NW);
+    const int wave = threadIdx.x >> 6, wm = wave / (NW / 2), wn = wave % (NW / 2);
 
     f32x16 acc[2][2];
     zero_acc(acc);
@@ -508,7 +507,7 @@ __global__ __launch_bounds__(256, 2) void gemm_gate_up_kernel(WView gate, WView 
         return n0 + r < N ? xh + (size_t)(n0 + r) * K : nullptr;
     };
     auto arow = [&](int i) { return 64 * i + 32 * wm; };
-    k_loop<F>(wsrc, xrow, arow, K, wn, lds, acc);
+    k_loop<F, 2, NW>(wsrc, xrow, arow, K, wn, lds, acc);
 
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -614,19 +613,37 @@ int launch_norm_to_f16(const float *x, int rows, int K, const float *norm, float
     return (int)hipGetLastError();
 }
 
+// Waves per dense GEMM workgroup: 8 (256-token tiles, each dequantized
+// weight slice feeding twice the MFMAs) when the batch exceeds one 128-token
+// tile and the 8-wave grid (`tiles` row tiles x K slices, times the 256-token
+// tiles) still gives at least 3/4 of the 256 CUs a workgroup; else 4 (two
+// workgroups per CU). Measured: Q4_K [14336 x 4096] x 512 tokens 120 -> 100
+// us, while grids of 64-96 workgroups ran 6-13 % slower with 8 waves. Both
+// forms give every element the same result, so the choice is free.
+int gemm_waves(int batch, int tiles)
+{
+    return batch > BN && (size_t)tiles * ((batch + 255) / 256) >= 192 ? 8 : 4;
+}
+
 int launch_gate_up_f16(int fmt, WView gate, WView up, int cols, const _Float16 *xh,
                        const float *rscale, int batch, float *h, void *stream)
 {
     if (cols % BK) return (int)hipErrorInvalidValue;
     const int mid = gate.rows;
-    const int mtiles = (mid + 63) / 64, ntiles = (batch + BN - 1) / BN;
+    const int mtiles = (mid + 63) / 64;
+    const int nw = gemm_waves(batch, mtiles), bn = 32 * nw;
+    const int ntiles = (batch + bn - 1) / bn;
     const int per = (mtiles * ntiles + 7) / 8;
-    dim3 grid(8 * per), block(256);
+    dim3 grid(8 * per), block(64 * nw);
     hipStream_t st = (hipStream_t)stream;
 #define HYQ_GU(F)                                                                              \
     case F:                                                                                    \
-        hipLaunchKernelGGL(gemm_gate_up_kernel<F>, grid, block, 0, st, gate, up, mid, cols, xh, \
-                           rscale, batch, h, mtiles, ntiles);                                  \
+        if (nw == 8)                                                                           \
+            hipLaunchKernelGGL((gemm_gate_up_kernel<F, 8>), grid, block, 0, st, gate, up, mid,  \
+                               cols, xh, rscale, batch, h, mtiles, ntiles);                    \
+        else                                                                                   \
+            hipLaunchKernelGGL((gemm_gate_up_kernel<F, 4>), grid, block, 0, st, gate, up, mid,  \
+                               cols, xh, rscale, batch, h, mtiles, ntiles);                    \
         break;
     switch (fmt) {
         HYQ_GU(Q4_K)
@@ -699,14 +716,19 @@ int launch_gemm_f16_segs(int fmt, GemmSegs g, int cols, const _Float16 *xh, cons
         g.s[i].tiles = (g.s[i].rows + BM - 1) / BM;
         mtiles += g.s[i].tiles;
     }
-    const int ntiles = (batch + BN - 1) / BN;
+    const int nw = gemm_waves(batch, mtiles * kslices), bn = 32 * nw;
+    const int ntiles = (batch + bn - 1) / bn;
     const int per = (mtiles * ntiles + 7) / 8;
-    dim3 grid(8 * per, kslices), block(256);
+    dim3 grid(8 * per, kslices), block(64 * nw);
     hipStream_t st = (hipStream_t)stream;
 #define HYQ_GEMM(F)                                                                            \
     case F:                                                                                    \
-        hipLaunchKernelGGL(gemm_f16_kernel<F>, grid, block, 0, st, g, cols, xh, rscale, batch,  \
-                           mtiles, ntiles, kslices, part);                                     \
+        if (nw == 8)                                                                           \
+            hipLaunchKernelGGL((gemm_f16_kernel<F, 8>), grid, block, 0, st, g, cols, xh, rscale, \
+                               batch, mtiles, ntiles, kslices, part);                          \
+        else                                                                                   \
+            hipLaunchKernelGGL((gemm_f16_kernel<F, 4>), grid, block, 0, st, g, cols, xh, rscale, \
+                               batch, mtiles, ntiles, kslices, part);                          \
         break;
     switch (fmt) {
         HYQ_GEMM(Q4_K)

@@ -15,6 +15,11 @@
 // Two LDS buffers let one barrier per step separate writers from readers.
 // LDS rows are padded to 72 halves (144 bytes), so the 16-byte fragment
 // reads of 8 consecutive rows fall on 8 distinct 4-bank windows.
+// The wide form (NW = 8 waves, 512 threads) takes 256 tokens: waves 0-3
+// dequantize the weight slice as above, all eight fetch the activations and
+// each multiplies its own 64 x 64 sub-tile, so a dequantized weight feeds
+// twice the MFMAs. Every output element sees the same operands in the same
+// k order in both forms, so their results are bit-identical.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -345,13 +350,19 @@ __device__ __forceinline__ void load_x(XRaw &x, const _Float16 *const (&xp)[4], 
         x.v[i] = xp[i] ? *reinterpret_cast<const uint4 *>(xp[i] + k0) : make_uint4(0, 0, 0, 0);
 }
 
-__device__ __forceinline__ void store_x(_Float16 *Xs, const XRaw &x)
+// NW waves: load i of thread t covers token row t / 8 + 8 NW i.
+template <int NW = 4> __device__ __forceinline__ void store_x(_Float16 *Xs, const XRaw &x)
 {
     const int t = threadIdx.x;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<uint4 *>(Xs + ((t >> 3) + 32 * i) * LDK + 8 * (t & 7)) = x.v[i];
+        *reinterpret_cast<uint4 *>(Xs + ((t >> 3) + 8 * NW * i) * LDK + 8 * (t & 7)) = x.v[i];
 }
+
+// LDS halves of one operand buffer (weights, then activations) and of the
+// two buffers a k_loop of NW waves uses.
+template <int NW> constexpr int buf_halves() { return TILE_HALVES + 32 * NW * LDK; }
+template <int NW> constexpr int lds_halves() { return 2 * buf_halves<NW>(); }
 
 // One 64-deep step: acc[i][j] accumulates LDS weight rows arow(i) + lane%32
 // against tokens wn*64 + 32*j + lane%32, for the wave's first J token
@@ -406,21 +417,25 @@ __device__ __forceinline__ void zero_acc(f32x16 (&acc)[2][2])
 // weight view and row that LDS row lrow dequantizes (row < 0: zeros);
 // xrow(r) gives the f16 activation row of token r of the tile (nullptr =
 // zeros); arow(i) the first LDS weight row of the wave's block i. lds holds
-// 2 * 2 * TILE_HALVES halves: buffer b at lds + b * 2 * TILE_HALVES, weights
+// lds_halves<NW>() halves: buffer b at lds + b * buf_halves<NW>(), weights
 // then activations. The loop covers columns [kbase, kbase + K) (a K slice
 // when kbase > 0; both multiples of the format's block). JM = 1 is the
 // variant for tiles of at most 32 tokens (MoE experts): only the first token
 // block holds tokens, so the waves with wn = 1 skip their MFMAs and the
 // others run one token block.
 // ---------------------------------------------------------------------------
-template <int F, int JM = 2, class WSrc, class XRow, class ARow>
+template <int F, int JM = 2, int NW = 4, class WSrc, class XRow, class ARow>
 __device__ __forceinline__ void k_loop(const WSrc &wsrc, const XRow &xrow, const ARow &arow,
                                        int K, int wn, _Float16 *lds, f32x16 (&acc)[2][2],
                                        int kbase = 0)
 {
+    static_assert(NW == 4 || NW == 8, "4 or 8 waves");
     using D = Deq<F>;
+    constexpr int BUF = buf_halves<NW>();
     const int t = threadIdx.x;
-    const int lrow = t >> 1, h = t & 1;
+    // the first 256 threads dequantize the weight slice (a wave-uniform test)
+    const bool wthr = NW == 4 || t < 256;
+    const int lrow = (t & 255) >> 1, h = t & 1;
     WView wv{};
     int row = -1;
     wsrc(lrow, wv, row);
@@ -428,20 +443,22 @@ __device__ __forceinline__ void k_loop(const WSrc &wsrc, const XRow &xrow, const
     const _Float16 *xp[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const _Float16 *p = xrow((t >> 3) + 32 * i);
+        const _Float16 *p = xrow((t >> 3) + 8 * NW * i);
         xp[i] = p ? p + 8 * (t & 7) : nullptr;
     }
     typename D::Raw raw;
     XRaw xr;
     auto fetch = [&](int k0) {
-        if (row >= 0) D::load(raw, rp, kbase + k0, h);
+        if (wthr && row >= 0) D::load(raw, rp, kbase + k0, h);
         load_x(xr, xp, kbase + k0);
     };
     auto put = [&](int k0, int b) {
-        _Float16 *Ws = lds + b * 2 * TILE_HALVES;
-        if (row >= 0) D::convert(raw, ((kbase + k0) >> 6) & 3, h, Ws + lrow * LDK);
-        else zero_half(Ws + lrow * LDK, h);
-        store_x(Ws + TILE_HALVES, xr);
+        _Float16 *Ws = lds + b * BUF;
+        if (wthr) {
+            if (row >= 0) D::convert(raw, ((kbase + k0) >> 6) & 3, h, Ws + lrow * LDK);
+            else zero_half(Ws + lrow * LDK, h);
+        }
+        store_x<NW>(Ws + TILE_HALVES, xr);
     };
     const int steps = K / BK;
     const bool mma = JM == 2 || __builtin_amdgcn_readfirstlane(wn) == 0;
@@ -451,7 +468,7 @@ __device__ __forceinline__ void k_loop(const WSrc &wsrc, const XRow &xrow, const
     __syncthreads();
     for (int s = 0; s < steps; ++s) {
         const int cur = s & 1;
-        const _Float16 *Ws = lds + cur * 2 * TILE_HALVES;
+        const _Float16 *Ws = lds + cur * BUF;
         if (mma) mma_step<JM>(Ws, Ws + TILE_HALVES, arow, wn, acc);
         if (s + 1 < steps) {
             put((s + 1) * BK, cur ^ 1);

@@ -76,6 +76,24 @@ def test_batched_rows_are_independent_of_batch(gpu_ctx):
         assert np.array_equal(part, full[lo:hi])
 
 
+def test_batched_rows_match_across_workgroup_forms(gpu_ctx):
+    """96 row tiles at 300 tokens take the 8-wave, 256-token workgroups (a
+    grid of 192); 2 and 50 tokens take the 4-wave, 128-token ones. Every
+    element sees the same operands in the same order, so the rows agree bit
+    for bit (a 256-token tile boundary and its partial tile included)."""
+    rows, cols = 96 * 128, 256
+    for dtype, seed in ((Q4_K, 11), (Q2_0C, 12)):
+        ccols = 512 if dtype == Q2_0C else cols
+        w = random_matrix(dtype, rows, ccols, seed=seed)
+        x = np.random.default_rng(seed).normal(0, 1, 300 * ccols).astype(np.float32)
+        W = gpu_ctx.upload(dtype, w, (ccols, rows))
+        full = W.matmul(x, 300).reshape(300, rows)
+        for lo, hi in ((0, 2), (255, 257), (250, 300)):
+            part = W.matmul(x[lo * ccols:hi * ccols], hi - lo).reshape(hi - lo, rows)
+            assert np.array_equal(part, full[lo:hi]), (NAMES[dtype], lo, hi)
+        W.release()
+
+
 def test_batched_shape_errors(gpu_ctx):
     w = random_matrix(Q8_0, 8, 96, seed=0)  # 96 columns: not a multiple of 64
     W = gpu_ctx.upload(Q8_0, w, (96, 8))
