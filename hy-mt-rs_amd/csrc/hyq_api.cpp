@@ -547,11 +547,12 @@ int hyq_matmul_d(hyq_ctx *ctx, const hyq_weight *w, const float *x_d, size_t bat
     if (rc) return rc;
     _Float16 *xh = (_Float16 *)ctx->xh.ptr();
     float *rscale = (float *)((uint8_t *)ctx->xh.ptr() + xh_bytes);
-    const size_t part = gemm_split_floats(w->dtype, (int)w->rows, (int)batch, (int)w->cols);
+    const int ks = matmul_kslices(w->dtype, (int)w->rows, (int)w->cols, (int)batch);
+    const size_t part = ks > 1 ? (size_t)ks * batch * w->rows : 0;
     if (part && (rc = ctx->kpart.reserve(ctx->device, part * 4))) return rc;
     HYQ_LAUNCH(launch_to_f16(x_d, (int)batch, (int)w->cols, xh, rscale, ctx->stream), "to_f16");
     HYQ_LAUNCH(launch_gemm_f16(w->dtype, w->view, (int)w->cols, xh, rscale, (int)batch, y_d,
-                               nullptr, ctx->stream, (float *)ctx->kpart.ptr(), part),
+                               nullptr, ctx->stream, (float *)ctx->kpart.ptr(), part, ks),
                "gemm_f16");
     return HYQ_OK;
 }

@@ -680,9 +680,30 @@ size_t gemm_split_floats(int fmt, int M, int N, int K)
     return k > 1 ? (size_t)k * N * M : 0;
 }
 
+// K slices of Weight::matmul's batched product (hyq_matmul_d). Above one
+// token tile (BN rows) it is gemm_kslices, a rule on the weight's shape only.
+// A batch of at most BN token rows is one token tile, so the grid is the row
+// tiles times the slices: the largest count up to 8 that keeps that grid
+// within the 256 CUs and cuts K into whole blocks (and 64-column steps) of at
+// least 256 columns, never fewer than gemm_kslices gives. A [2048 x 2048]
+// weight at 64 tokens (the MoE shared projection) runs as 8 slices on 128
+// workgroups instead of 2 slices on 32. Token rows of batches on the same
+// side of BN get identical results.
+int matmul_kslices(int fmt, int M, int K, int batch)
+{
+    const int base = gemm_kslices(fmt, M, K);
+    if (batch > BN || K % BK || M % 4) return base;
+    const int unit = std::max(BK, block_len(fmt));
+    if (K % unit) return base;
+    const int mtiles = (M + BM - 1) / BM;
+    for (int k = 8; k > base; --k)
+        if (mtiles * k <= 256 && (K / unit) % k == 0 && K / k >= 256) return k;
+    return base;
+}
+
 int launch_gemm_f16(int fmt, WView w, int cols, const _Float16 *xh, const float *rscale,
                     int batch, float *y, const float *residual, void *stream, float *part,
-                    size_t part_floats)
+                    size_t part_floats, int kslices)
 {
     GemmSegs g{};
     g.nseg = 1;
@@ -690,7 +711,7 @@ int launch_gemm_f16(int fmt, WView w, int cols, const _Float16 *xh, const float 
     g.s[0].y = y;
     g.s[0].residual = residual;
     g.s[0].rows = w.rows;
-    const int ks = gemm_kslices(fmt, w.rows, cols);
+    const int ks = kslices > 0 ? kslices : gemm_kslices(fmt, w.rows, cols);
     if (ks > 1 && part && part_floats >= (size_t)ks * batch * w.rows) {
         int rc = launch_gemm_f16_segs(fmt, g, cols, xh, rscale, batch, stream, ks, part);
         if (rc) return rc;

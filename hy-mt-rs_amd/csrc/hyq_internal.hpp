@@ -152,13 +152,15 @@ int launch_decode_gguf(int fmt, const uint8_t *bytes, size_t nblocks, float *out
 int launch_to_f16(const float *x, int rows, int K, _Float16 *xh, float *rscale, void *stream);
 int launch_norm_to_f16(const float *x, int rows, int K, const float *norm, float eps,
                        _Float16 *xh, float *rscale, void *stream);
-// With `part` (part_floats >= gemm_split_floats(...)) a GEMM of few row
-// tiles runs as gemm_kslices K slices into part, added in slice order.
+// With `part` (part_floats >= kslices * batch * w.rows) a GEMM of few row
+// tiles runs as K slices into part, added in slice order: `kslices` of them,
+// or gemm_kslices when kslices is 0.
 int launch_gemm_f16(int fmt, WView w, int cols, const _Float16 *xh, const float *rscale,
                     int batch, float *y, const float *residual, void *stream,
-                    float *part = nullptr, size_t part_floats = 0);
+                    float *part = nullptr, size_t part_floats = 0, int kslices = 0);
 int gemm_kslices(int fmt, int M, int K);
 size_t gemm_split_floats(int fmt, int M, int N, int K);
+int matmul_kslices(int fmt, int M, int K, int batch);
 // Up to three weights of one format sharing the activation rows (fused
 // Q/K/V): segment i writes y_i [batch][rows_i] (+ residual_i); every segment
 // but the last has a multiple of 128 rows. `tiles` is set by the launcher.

@@ -65,15 +65,42 @@ def test_prefill_7b_full_size_sampled_rows(gpu_ctx, oracle, dtype, rows, cols):
 
 def test_batched_rows_are_independent_of_batch(gpu_ctx):
     """Each token's output row does not depend on the other tokens of the
-    batch (a 128-token tile boundary and a partial tile included)."""
+    batch, for batches on the same side of one 128-token tile: above it the
+    K split is a rule on the weight's shape (here none); at or below it the
+    row tiles alone leave CUs idle and K is split in two (a 128-token tile
+    boundary and partial tiles included on both sides)."""
     rows, cols = 256, 512
     w = random_matrix(Q4_K, rows, cols, seed=3)
     x = np.random.default_rng(3).normal(0, 1, 300 * cols).astype(np.float32)
     W = gpu_ctx.upload(Q4_K, w, (cols, rows))
     full = W.matmul(x, 300).reshape(300, rows)
-    for lo, hi in ((0, 2), (127, 129), (250, 300)):
+    for lo, hi in ((0, 129), (100, 300), (127, 257)):
         part = W.matmul(x[lo * cols:hi * cols], hi - lo).reshape(hi - lo, rows)
-        assert np.array_equal(part, full[lo:hi])
+        assert np.array_equal(part, full[lo:hi]), (lo, hi)
+    few = W.matmul(x[:128 * cols], 128).reshape(128, rows)
+    for lo, hi in ((0, 2), (60, 128), (126, 128)):
+        part = W.matmul(x[lo * cols:hi * cols], hi - lo).reshape(hi - lo, rows)
+        assert np.array_equal(part, few[lo:hi]), (lo, hi)
+    # both splits agree with each other to the f16 path's tolerance
+    assert np.allclose(few, full[:128], rtol=0, atol=2e-3 * np.abs(full[:128]).max())
+
+
+@pytest.mark.parametrize("dtype,rows,cols,batch", [(Q8_0, 2048, 2048, 64), (Q4_K, 2048, 2048, 16),
+                                                   (Q2_0C, 1024, 4096, 5), (STQ1_0, 512, 2048, 128)],
+                         ids=["q80_shared_64", "q4k_16", "q2c_5", "stq_128"])
+def test_matmul_few_tokens_split_k(gpu_ctx, oracle, dtype, rows, cols, batch):
+    """Batches of at most 128 tokens on weights of few row tiles run with K cut
+    into up to 8 slices (the MoE shared projection [2048x2048] Q8_0 at 64
+    tokens: 8 slices of 256 columns); parity with the oracle as every batched
+    product."""
+    _print("gemm few tokens", NAMES[dtype], rows, cols, batch)
+    w = random_matrix(dtype, rows, cols, seed=rows + batch)
+    x = np.random.default_rng(batch).normal(0, 1, batch * cols).astype(np.float32)
+    W = gpu_ctx.upload(dtype, w, (cols, rows))
+    y = W.matmul(x, batch).reshape(batch, rows)
+    y_ref, mag = oracle.matmul_f64(dtype, w, rows, cols, x, batch)
+    check_prefill_path(y, y_ref, mag, f"{NAMES[dtype]} batch {batch}")
+    W.release()
 
 
 def test_batched_rows_match_across_workgroup_forms(gpu_ctx):
