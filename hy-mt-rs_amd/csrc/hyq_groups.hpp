@@ -210,27 +210,37 @@ struct GroupSTQ {
         D.sgn = reinterpret_cast<const uint2 *>(w.p1)[blk];
         D.d = reinterpret_cast<const uint16_t *>(w.p2)[blk];
     }
+    // 0xFF in each byte whose bit 7 is set, else 0x00: v_perm_b32 selectors
+    // 8, 9, 10, 11 replicate bit 7 of bytes 1, 3, 5, 7 of {first, second};
+    // with second = v << 8 those are v's bytes 0, 2 and first's 1, 3.
+    __device__ __forceinline__ static uint32_t byte_mask(uint32_t v)
+    {
+        return __builtin_amdgcn_perm(v, v << 8, 0x0B090A08u);
+    }
+    // Codebook bytes of four groups: nibbles nb (one per byte, 0..15) and a
+    // per-byte sign mask ms. STQ_CODEBOOK (src/quant.rs:1081-1084) holds 2-bit
+    // digit codes (0..2, digit = code - 1); each of its sign-1 entries is the
+    // sign-0 entry of the same nibble with every code c replaced by 2 - c
+    // (the digits negated), i.e. the byte 0xAA - e, so only the 16 sign-0
+    // entries are looked up (packed 4 per dword, little endian; v_perm_b32
+    // selects bytes 0-3 from its second operand and 4-7 from its first) and
+    // the sign picks e or 0xAA - e per byte (no borrows: every code is <= 2).
+    __device__ __forceinline__ static uint32_t codes(uint32_t nb, uint32_t ms)
+    {
+        constexpr uint32_t CB0 = 0x092989a9u, CB1 = 0x062686a6u, CB2 = 0x121a929au,
+                           CB3 = 0x424a626au;
+        const uint32_t sel = nb & 0x07070707u;
+        const uint32_t r0 = __builtin_amdgcn_perm(CB1, CB0, sel);
+        const uint32_t r1 = __builtin_amdgcn_perm(CB3, CB2, sel);
+        const uint32_t m3 = byte_mask(nb << 4); // nibble bit 3
+        const uint32_t e = (r1 & m3) | (r0 & ~m3);
+        const uint32_t en = 0xAAAAAAAAu - e;
+        return (en & ms) | (e & ~ms);
+    }
     // 5-bit index bytes (sign<<4 | nibble) -> codebook bytes, four at a time.
     __device__ __forceinline__ static uint32_t lut(uint32_t idx)
     {
-        // STQ_CODEBOOK (src/quant.rs:1081-1084) packed 4 entries per dword,
-        // little endian; v_perm_b32 selects bytes 0-3 from its second operand
-        // and 4-7 from its first.
-        constexpr uint32_t CB0 = 0x092989a9u, CB1 = 0x062686a6u, CB2 = 0x121a929au,
-                           CB3 = 0x424a626au, CB4 = 0xa1812101u, CB5 = 0xa4842404u,
-                           CB6 = 0x98901810u, CB7 = 0x68604840u;
-        uint32_t sel = idx & 0x07070707u;
-        uint32_t r0 = __builtin_amdgcn_perm(CB1, CB0, sel);
-        uint32_t r1 = __builtin_amdgcn_perm(CB3, CB2, sel);
-        uint32_t r2 = __builtin_amdgcn_perm(CB5, CB4, sel);
-        uint32_t r3 = __builtin_amdgcn_perm(CB7, CB6, sel);
-        uint32_t b3 = (idx >> 3) & 0x01010101u;
-        uint32_t m3 = (b3 << 8) - b3;
-        uint32_t b4 = (idx >> 4) & 0x01010101u;
-        uint32_t m4 = (b4 << 8) - b4;
-        uint32_t lo = (r1 & m3) | (r0 & ~m3);
-        uint32_t hi = (r3 & m3) | (r2 & ~m3);
-        return (hi & m4) | (lo & ~m4);
+        return codes(idx & 0x0F0F0F0Fu, byte_mask(idx << 3));
     }
     template <bool EMIT>
     __device__ __forceinline__ static float dot(const Data &Din, const int *act,
@@ -249,9 +259,8 @@ struct GroupSTQ {
                 const uint32_t dw = nib[2 * c + (qi >> 1)];
                 const uint32_t nb = (qi & 1) ? (dw >> 4) & 0x0F0F0F0Fu : dw & 0x0F0F0F0Fu;
                 const int q = (c & 1) * 4 + qi; // quad index inside the sign dword
-                const uint32_t S = sg[c >> 1];
-                const uint32_t sb = (q <= 4 ? (S << (4 - q)) : (S >> (q - 4))) & 0x10101010u;
-                const uint32_t e = lut(nb | sb);
+                // sign bit q of each byte of S moved to bit 7
+                const uint32_t e = codes(nb, byte_mask(sg[c >> 1] << (7 - q)));
 #pragma unroll
                 for (int p = 0; p < 4; ++p)
                     raw = sdot4((e >> (2 * p)) & 0x03030303u, act[16 * c + 4 * p + qi], raw);
