@@ -11,6 +11,7 @@ without a GPU, raises.
 from __future__ import annotations
 
 import ctypes
+import weakref
 import os
 
 import numpy as np
@@ -83,6 +84,7 @@ SIGNATURES = {
     "hyq_dense_prefill": (I, [P, P, SZ, P, P]),
     "hyq_dense_read_kv": (I, [P, I, SZ, P, P]),
     "hyq_dense_set_prefill_rows": (I, [P, SZ]),
+    "hyq_dense_set_trace": (I, [P, P, SZ]),
     "hyq_dense_generate": (I, [P, ctypes.c_int32, SZ, I, P]),
     "hyq_gguf_open": (I, [ctypes.c_char_p, I, ctypes.POINTER(P)]),
     "hyq_gguf_open_bytes": (I, [P, SZ, I, ctypes.POINTER(P)]),
@@ -175,6 +177,8 @@ class Context:
         check(lib().hyq_ctx_create(device, ctypes.byref(h)))
         self.handle = h.value
         self.device = device
+        # objects that use the context's stream (decoders): closed first
+        self._dependents = weakref.WeakSet()
 
     @property
     def stream(self) -> int:
@@ -185,6 +189,8 @@ class Context:
 
     def close(self) -> None:
         if self.handle:
+            for d in list(self._dependents):
+                d.close()
             lib().hyq_ctx_destroy(self.handle)
             self.handle = None
 
@@ -416,11 +422,13 @@ class DenseDecoder:
         check(lib().hyq_dense_create(ctx.handle, ctypes.byref(cfg), context, ctypes.byref(h)))
         self.handle = h.value
         self._keep = []
+        ctx._dependents.add(self)
 
     def close(self) -> None:
-        if self.handle:
+        # a decoder uses its context's stream: it goes first (Context.close)
+        if self.handle and self.ctx.handle:
             lib().hyq_dense_destroy(self.handle)
-            self.handle = None
+        self.handle = None
 
     def __del__(self):
         try:
@@ -500,11 +508,30 @@ class DenseDecoder:
             c.f64(f"{c.architecture}.attention.layer_norm_rms_epsilon"))
         self.handle = h.value
         self._keep = [gguf]
+        ctx._dependents.add(self)
         return self
 
     def set_prefill_rows(self, rows: int) -> None:
         """Tokens per device pass of prefill (results do not depend on it)."""
         check(lib().hyq_dense_set_prefill_rows(self.handle, rows))
+
+    def set_trace(self, rows: int | None) -> None:
+        """Record the hidden row after the embedding and after every layer
+        (eager forward: one token; prefill: a pass of up to ``rows`` tokens);
+        ``None`` stops recording. ``trace()`` reads the last record."""
+        self._trace = None
+        if rows is None:
+            check(lib().hyq_dense_set_trace(self.handle, None, 0))
+            return
+        n = (self.cfg.layers + 1) * rows * self.cfg.hidden
+        self._trace = self.ctx.empty(n, np.float32)
+        check(lib().hyq_dense_set_trace(self.handle, self._trace.ptr, n))
+
+    def trace(self, rows: int = 1) -> np.ndarray:
+        """[layers + 1, rows, hidden] hidden rows of the last traced pass."""
+        h = self.cfg.hidden
+        t = self._trace.numpy()[:(self.cfg.layers + 1) * rows * h]
+        return t.reshape(self.cfg.layers + 1, rows, h)
 
     def read_kv(self, layer: int, positions: int):
         """Cached keys and values [positions, kv_heads*head_dim] of one layer."""

@@ -88,6 +88,8 @@ int quantize_into(hyq_ctx *ctx, const float *x_d, const Q8Ref &q8)
     return HYQ_OK;
 }
 
+bool is_raw(int d) { return d == HYQ_F32 || d == HYQ_F16; }
+
 bool dtype_known(int d)
 {
     return d == HYQ_F32 || d == HYQ_F16 || d == HYQ_Q8_0 || d == HYQ_Q4_K || d == HYQ_Q6_K ||
@@ -202,6 +204,11 @@ int check_qkv(const hyq_weight *q, const hyq_weight *k, const hyq_weight *v)
         return fail(HYQ_EINVAL, "query, key and value must be matrices that share an input width");
     if (q->device != k->device || q->device != v->device)
         return fail(HYQ_EINVAL, "gemv_qkv: weights live on different devices");
+    if (is_raw(q->dtype) || is_raw(k->dtype) || is_raw(v->dtype)) {
+        if (!(is_raw(q->dtype) && is_raw(k->dtype) && is_raw(v->dtype)))
+            return fail(HYQ_EDTYPE, "gemv_qkv: F32/F16 mixed with quantized weights");
+        return HYQ_OK;
+    }
     rc = check_int8_path(q, "gemv_qkv");
     if (!rc) rc = check_int8_path(k, "gemv_qkv");
     if (!rc) rc = check_int8_path(v, "gemv_qkv");
@@ -218,6 +225,7 @@ int check_gate_up(const hyq_weight *gate, const hyq_weight *up)
     if (gate->dtype != up->dtype)
         return fail(HYQ_EDTYPE, "gate_up_silu: gate and up formats differ (%d vs %d)",
                     gate->dtype, up->dtype);
+    if (is_raw(gate->dtype)) return HYQ_OK;
     return check_int8_path(gate, "gate_up_silu");
 }
 
@@ -467,6 +475,7 @@ int hyq_gemv_qkv_q8_d(hyq_ctx *ctx, const hyq_weight *q, const hyq_weight *k,
 {
     int rc = check_ctx_weight(ctx, q, "gemv_qkv");
     if (!rc) rc = check_qkv(q, k, v);
+    if (!rc) rc = check_int8_path(q, "gemv_qkv");
     if (!rc) rc = check_q8(x, q->cols, "gemv_qkv");
     if (rc) return rc;
     if (!yq_d || !yk_d || !yv_d) return fail(HYQ_EINVAL, "gemv_qkv: null output");
@@ -479,6 +488,7 @@ int hyq_gate_up_silu_q8_d(hyq_ctx *ctx, const hyq_weight *gate, const hyq_weight
 {
     int rc = check_ctx_weight(ctx, gate, "gate_up_silu");
     if (!rc) rc = check_gate_up(gate, up);
+    if (!rc) rc = check_int8_path(gate, "gate_up_silu");
     if (!rc) rc = check_q8(x, gate->cols, "gate_up_silu");
     if (rc) return rc;
     if (!y_d) return fail(HYQ_EINVAL, "gate_up_silu: null output");
@@ -516,6 +526,22 @@ int hyq_matmul_d(hyq_ctx *ctx, const hyq_weight *w, const float *x_d, size_t bat
     if (batch == 0) return fail(HYQ_EINVAL, "%s: invalid activation shape", "matmul");
     if (!x_d || !y_d) return fail(HYQ_EINVAL, "matmul: null buffer");
     DeviceGuard g(ctx->device);
+    // Q8_0 of a width the int8 GEMV (256-value groups) or the GEMM (64-column
+    // slices) does not tile: the decoded-row path, as F32/F16
+    const bool q80_odd = w->dtype == HYQ_Q8_0 && w->cols % (batch == 1 ? 256 : 64) != 0;
+    if (is_raw(w->dtype) || q80_odd) {
+        // decode rows to f32 + dot (src/quant.rs:225-267; batched :312-343)
+        if (batch > 65535 * 64) return fail(HYQ_EINVAL, "matmul: batch %zu too large", batch);
+        if (batch == 1)
+            HYQ_LAUNCH(launch_f32_gemv(w->dtype, w->view, nullptr, (int)w->cols, x_d, y_d,
+                                       ctx->stream),
+                       "f32_gemv");
+        else
+            HYQ_LAUNCH(launch_f32_gemm(w->dtype, w->view, (int)w->cols, x_d, (int)batch, y_d,
+                                       ctx->stream),
+                       "f32_gemm");
+        return HYQ_OK;
+    }
     if (batch == 1) {
         rc = check_int8_path(w, "matmul");
         if (rc) return rc;
@@ -663,15 +689,26 @@ int hyq_gemv_qkv(hyq_ctx *ctx, const hyq_weight *q, const hyq_weight *k, const h
     const size_t cols = q->cols, nq = q->rows, nk = k->rows, nv = v->rows;
     rc = ctx->x.reserve(ctx->device, cols * 4);
     if (!rc) rc = ctx->y.reserve(ctx->device, (nq + nk + nv) * 4);
-    Q8Ref q8;
-    if (!rc) rc = ctx_q8(ctx, cols, &q8);
     if (rc) return rc;
     float *yd = (float *)ctx->y.ptr();
+    const float *xd = (const float *)ctx->x.ptr();
     HYQ_HIP(hipMemcpyAsync(ctx->x.ptr(), x, cols * 4, hipMemcpyHostToDevice, ctx->stream),
             "hipMemcpy");
-    rc = quantize_into(ctx, (const float *)ctx->x.ptr(), q8);
-    if (!rc) rc = gemv_qkv(ctx, q, k, v, q8, yd, yd + nq, yd + nq + nk);
-    if (rc) return rc;
+    if (is_raw(q->dtype)) {
+        // three matmuls (src/quant.rs:716-720)
+        const hyq_weight *ws[3] = {q, k, v};
+        float *ys[3] = {yd, yd + nq, yd + nq + nk};
+        for (int i = 0; i < 3; ++i)
+            HYQ_LAUNCH(launch_f32_gemv(ws[i]->dtype, ws[i]->view, nullptr, (int)cols, xd, ys[i],
+                                       ctx->stream),
+                       "f32_gemv");
+    } else {
+        Q8Ref q8;
+        rc = ctx_q8(ctx, cols, &q8);
+        if (!rc) rc = quantize_into(ctx, xd, q8);
+        if (!rc) rc = gemv_qkv(ctx, q, k, v, q8, yd, yd + nq, yd + nq + nk);
+        if (rc) return rc;
+    }
     HYQ_HIP(hipMemcpyAsync(yq, yd, nq * 4, hipMemcpyDeviceToHost, ctx->stream), "hipMemcpy");
     HYQ_HIP(hipMemcpyAsync(yk, yd + nq, nk * 4, hipMemcpyDeviceToHost, ctx->stream), "hipMemcpy");
     HYQ_HIP(hipMemcpyAsync(yv, yd + nq + nk, nv * 4, hipMemcpyDeviceToHost, ctx->stream),
@@ -691,14 +728,22 @@ int hyq_gate_up_silu(hyq_ctx *ctx, const hyq_weight *gate, const hyq_weight *up,
     const size_t cols = gate->cols, rows = gate->rows;
     rc = ctx->x.reserve(ctx->device, cols * 4);
     if (!rc) rc = ctx->y.reserve(ctx->device, rows * 4);
-    Q8Ref q8;
-    if (!rc) rc = ctx_q8(ctx, cols, &q8);
     if (rc) return rc;
     HYQ_HIP(hipMemcpyAsync(ctx->x.ptr(), x, cols * 4, hipMemcpyHostToDevice, ctx->stream),
             "hipMemcpy");
-    rc = quantize_into(ctx, (const float *)ctx->x.ptr(), q8);
-    if (!rc) rc = gate_up(ctx, gate, up, q8, (float *)ctx->y.ptr());
-    if (rc) return rc;
+    if (is_raw(gate->dtype)) {
+        // two matmuls and silu(g) * u (src/quant.rs:831-838)
+        HYQ_LAUNCH(launch_f32_gemv(gate->dtype, gate->view, &up->view, (int)cols,
+                                   (const float *)ctx->x.ptr(), (float *)ctx->y.ptr(),
+                                   ctx->stream),
+                   "f32_gate_up");
+    } else {
+        Q8Ref q8;
+        rc = ctx_q8(ctx, cols, &q8);
+        if (!rc) rc = quantize_into(ctx, (const float *)ctx->x.ptr(), q8);
+        if (!rc) rc = gate_up(ctx, gate, up, q8, (float *)ctx->y.ptr());
+        if (rc) return rc;
+    }
     HYQ_HIP(hipMemcpyAsync(y, ctx->y.ptr(), rows * 4, hipMemcpyDeviceToHost, ctx->stream),
             "hipMemcpy");
     HYQ_HIP(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");

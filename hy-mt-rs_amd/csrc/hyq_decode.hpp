@@ -22,7 +22,7 @@ __device__ __forceinline__ float h2f_bytes(const uint8_t *p)
     return (float)h;
 }
 
-// STQ_CODEBOOK (src/quant.rs:1081-1084), ggml-derived (MIT).
+// STQ_CODEBOOK (src/quant.rs:1081-1084), ggml-derived (MIT; notice in THIRD_PARTY_NOTICES.md).
 static __constant__ uint8_t kStqCodebook[32] = {
     0xa9, 0x89, 0x29, 0x09, 0xa6, 0x86, 0x26, 0x06, 0x9a, 0x92, 0x1a, 0x12, 0x6a, 0x62, 0x4a, 0x42,
     0x01, 0x21, 0x81, 0xa1, 0x04, 0x24, 0x84, 0xa4, 0x10, 0x18, 0x90, 0x98, 0x40, 0x48, 0x60, 0x68,

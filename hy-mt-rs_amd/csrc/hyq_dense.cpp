@@ -199,6 +199,10 @@ struct hyq_dense {
     hyq_dense_config cfg{};
     size_t context = 0;
     size_t pos_host = 0;
+    // set when a forward produced non-finite logits (the reference poisons
+    // the session, src/model.rs:348-351, :371, :540-545); cleared by a new
+    // position
+    bool poisoned = false;
     struct Layer {
         const hyq_weight *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
         const hyq_weight *gate = nullptr, *up = nullptr, *down = nullptr;
@@ -223,6 +227,11 @@ struct hyq_dense {
     StepState *state = nullptr;
     size_t history_cap = 0;
     std::unique_ptr<DeviceBuffer> history_mem;
+
+    // hidden rows after the embedding and after every layer, written by the
+    // eager forward and prefill when set (hyq_dense_set_trace)
+    float *trace = nullptr;
+    size_t trace_floats = 0;
 
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
@@ -294,7 +303,7 @@ GemvArgs staged(const hyq_weight *w, const float *xin, const float *norm, float 
     return a;
 }
 
-int enqueue_step(hyq_dense *m)
+int enqueue_step(hyq_dense *m, bool trace = false)
 {
     const hyq_dense_config &c = m->cfg;
     hipStream_t st = m->ctx->stream;
@@ -303,6 +312,9 @@ int enqueue_step(hyq_dense *m)
                "embed_row");
     const int *pos = &m->state->pos;
     const int ks = m->down_ks;
+    trace = trace && m->trace;
+    if (trace)
+        HYQ_LAUNCH(launch_sum_parts(m->hidden, nullptr, 0, 0, c.hidden, m->trace, st), "trace");
     for (int l = 0; l < c.layers; ++l) {
         const hyq_dense::Layer &L = m->layers[l];
         // the previous layer's down projection left `ks` partial rows
@@ -356,6 +368,10 @@ int enqueue_step(hyq_dense *m)
                                    staged(L.down, m->gb, nullptr, 0.f, m->hidden, m->hidden), st),
                        "gemv_down");
         }
+        if (trace)
+            HYQ_LAUNCH(launch_sum_parts(m->hidden, m->parts, ks > 1 ? ks : 0, c.hidden, c.hidden,
+                                        m->trace + (size_t)(l + 1) * c.hidden, st),
+                       "trace");
     }
     {
         GemvArgs a = staged(m->output, m->hidden, m->output_norm, c.rms_eps, m->logits, nullptr);
@@ -435,6 +451,11 @@ int enqueue_prefill_chunk(hyq_dense *m, int n)
     HYQ_LAUNCH(launch_embed_rows(m->embedding->dtype, m->embedding->view, H, m->pf_tok, n,
                                  m->pf_hid, st),
                "embed_rows");
+    const size_t rows = (size_t)n * H;
+    const bool trace = m->trace && (size_t)(c.layers + 1) * rows <= m->trace_floats;
+    if (trace)
+        HYQ_HIP(hipMemcpyAsync(m->trace, m->pf_hid, rows * 4, hipMemcpyDeviceToDevice, st),
+                "trace");
     for (int l = 0; l < c.layers; ++l) {
         const hyq_dense::Layer &L = m->layers[l];
         HYQ_LAUNCH(launch_norm_to_f16(m->pf_hid, n, H, L.attn_norm, c.rms_eps, m->pf_xh,
@@ -483,18 +504,23 @@ int enqueue_prefill_chunk(hyq_dense *m, int n)
         HYQ_LAUNCH(launch_gemm_f16(L.down->dtype, L.down->view, F, m->pf_xh, m->pf_rs, n,
                                    m->pf_hid, m->pf_hid, st, m->pf_kpart, m->pf_kpart_floats),
                    "gemm_down");
+        if (trace)
+            HYQ_HIP(hipMemcpyAsync(m->trace + (size_t)(l + 1) * rows, m->pf_hid, rows * 4,
+                                   hipMemcpyDeviceToDevice, st),
+                    "trace");
     }
     GemvArgs a = staged(m->output, m->pf_hid + (size_t)(n - 1) * H, m->output_norm, c.rms_eps,
                         m->logits, nullptr);
     HYQ_LAUNCH(launch_gemv(m->output->dtype, GEMV_PLAIN, a, st), "gemv_lm_head");
     HYQ_LAUNCH(launch_argmax(m->logits, c.vocab, m->argmax_scratch,
-                             (int *)(m->argmax_scratch + 64), m->token, nullptr, nullptr, st),
+                             (int *)(m->argmax_scratch + 64), m->token, m->state, nullptr, st),
                "argmax");
     return HYQ_OK;
 }
 
 int ready(hyq_dense *m)
 {
+    if (m->poisoned) return fail(HYQ_EINVAL, "session was invalidated by a failed forward");
     for (size_t l = 0; l < m->layers.size(); ++l)
         if (!m->layers[l].q) return fail(HYQ_EINVAL, "dense: layer %zu has no weights", l);
     if (!m->embedding || !m->output) return fail(HYQ_EINVAL, "dense: output weights not set");
@@ -509,6 +535,20 @@ int write_state(hyq_dense *m, int32_t token, int step, int cap)
     HYQ_HIP(hipMemcpyAsync(m->token, &token, sizeof token, hipMemcpyHostToDevice,
                            m->ctx->stream),
             "hipMemcpy(token)");
+    return HYQ_OK;
+}
+
+// After the stream has drained: the argmax's non-finite flag of the steps
+// since the last write_state. forward_into rejects non-finite logits
+// (src/model.rs:540-543, :609-612) and the failed forward poisons the session.
+int check_finite(hyq_dense *m)
+{
+    StepState s{};
+    HYQ_HIP(hipMemcpy(&s, m->state, sizeof s, hipMemcpyDeviceToHost), "hipMemcpy(state)");
+    if (s.nonfinite) {
+        m->poisoned = true;
+        return fail(HYQ_EINVAL, "model produced non-finite logits; check model format and weights");
+    }
     return HYQ_OK;
 }
 
@@ -699,6 +739,7 @@ int hyq_dense_set_position(hyq_dense *m, size_t position)
     if (!m) return fail(HYQ_EINVAL, "dense_set_position: null decoder");
     if (position > m->context) return fail(HYQ_EINVAL, "context limit exceeded");
     m->pos_host = position;
+    m->poisoned = false;
     return HYQ_OK;
 }
 
@@ -718,7 +759,7 @@ int hyq_dense_forward(hyq_dense *m, int32_t token, float *logits, int32_t *next)
     if (m->pos_host + 1 > m->context) return fail(HYQ_EINVAL, "context limit exceeded");
     DeviceGuard g(m->ctx->device);
     if ((rc = write_state(m, token, 0, 0))) return rc;
-    if ((rc = enqueue_step(m))) return rc;
+    if ((rc = enqueue_step(m, true))) return rc;
     if (logits)
         HYQ_HIP(hipMemcpyAsync(logits, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost,
                                m->ctx->stream),
@@ -727,6 +768,7 @@ int hyq_dense_forward(hyq_dense *m, int32_t token, float *logits, int32_t *next)
     HYQ_HIP(hipMemcpyAsync(&nt, m->token, 4, hipMemcpyDeviceToHost, m->ctx->stream),
             "hipMemcpy(token)");
     HYQ_HIP(hipStreamSynchronize(m->ctx->stream), "hipStreamSynchronize");
+    if ((rc = check_finite(m))) return rc;
     m->pos_host += 1;
     if (next) *next = nt;
     return HYQ_OK;
@@ -756,11 +798,12 @@ int hyq_dense_prefill(hyq_dense *m, const int32_t *tokens, size_t n, float *logi
             HYQ_HIP(hipMemcpyAsync(m->pf_tok, tokens + s, cn * 4, hipMemcpyHostToDevice, st),
                     "hipMemcpy(tokens)");
             if ((rc = enqueue_prefill_chunk(m, (int)cn))) return rc;
-        } else if ((rc = enqueue_step(m))) {
+        } else if ((rc = enqueue_step(m, true))) {
             return rc;
         }
         // the host-side state and token words are rewritten by the next pass
         HYQ_HIP(hipStreamSynchronize(st), "hipStreamSynchronize");
+        if ((rc = check_finite(m))) return rc;
         m->pos_host += cn;
         s += cn;
     }
@@ -772,6 +815,17 @@ int hyq_dense_prefill(hyq_dense *m, const int32_t *tokens, size_t n, float *logi
     HYQ_HIP(hipMemcpyAsync(&nt, m->token, 4, hipMemcpyDeviceToHost, st), "hipMemcpy(token)");
     HYQ_HIP(hipStreamSynchronize(st), "hipStreamSynchronize");
     if (next) *next = nt;
+    return HYQ_OK;
+}
+
+int hyq_dense_set_trace(hyq_dense *m, float *trace_d, size_t floats)
+{
+    if (!m) return fail(HYQ_EINVAL, "dense_set_trace: null decoder");
+    const size_t need = (size_t)(m->cfg.layers + 1) * (size_t)m->cfg.hidden;
+    if (trace_d && floats < need)
+        return fail(HYQ_EINVAL, "dense_set_trace: %zu floats < %zu", floats, need);
+    m->trace = trace_d;
+    m->trace_floats = trace_d ? floats : 0;
     return HYQ_OK;
 }
 
@@ -843,6 +897,7 @@ int hyq_dense_generate(hyq_dense *m, int32_t token, size_t steps, int use_graph,
     HYQ_HIP(hipMemcpyAsync(tokens, m->history, steps * 4, hipMemcpyDeviceToHost, st),
             "hipMemcpy(tokens)");
     HYQ_HIP(hipStreamSynchronize(st), "hipStreamSynchronize");
+    if ((rc = check_finite(m))) return rc;
     m->pos_host += steps;
     return HYQ_OK;
 }

@@ -211,5 +211,11 @@ bool moe_q4k_fits(int hidden, int mid);
 int moe_q4k_down_slices(int mid);
 int moe_q4k_chunk();
 int isums_per_group(int fmt);
+// F32/F16 weights (hyq_f32mm.hip): y[rows] = W x in f32, or silu(W x) *
+// (U x) when `up` is given (batch 1); y[batch][rows] = X W^T (batch >= 1).
+int launch_f32_gemv(int fmt, WView w, const WView *up, int cols, const float *x, float *y,
+                    void *stream);
+int launch_f32_gemm(int fmt, WView w, int cols, const float *x, int batch, float *y,
+                    void *stream);
 
 } // namespace hyq

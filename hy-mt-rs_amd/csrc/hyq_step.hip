@@ -447,16 +447,40 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float *__restrict
     if (g == 0) out[h * ATT_D + d] = ((red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane])) / den;
 }
 
+// out = ((x + p[0]) + p[1]) + ... over np partial rows (p[k] = parts + k *
+// stride): the hidden row as the next stage forms it.
+__global__ void sum_parts_kernel(const float *__restrict__ x, const float *__restrict__ parts,
+                                 int np, int stride, int n, float *__restrict__ out)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float v = x[i];
+    for (int k = 0; k < np; ++k) v += parts[(size_t)k * stride + i];
+    out[i] = v;
+}
+
 __global__ void zero_u32_kernel(unsigned *p, int n)
 {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = 0u;
 }
 
-// ---- greedy argmax: first maximum wins ----
-// Pass 1: each workgroup reduces a slice to (value, index); pass 2: one
-// workgroup reduces the partials and stores the token (and optionally
-// advances the step state).
+// ---- greedy argmax (src/generation.rs:281-290) ----
+// The reference keeps (best, value) = (0, x[0]) and takes index i only when
+// x[i] > value: the first maximum wins, a NaN is never taken, and a NaN at
+// index 0 keeps token 0 (no later value compares greater than it). In
+// parallel: every non-NaN value is a candidate, candidates reduce by larger
+// value then smaller index, and a NaN x[0] forces token 0. Whenever x[0] is
+// not NaN it is itself a candidate, so the result is a valid index; it is
+// still clamped into [0, n) before it is stored, because the decode loop
+// embeds it as the next token. Pass 1: each workgroup reduces a slice to
+// (value, index), with bit 31 of the index set when the slice holds a
+// non-finite value (forward_into rejects non-finite logits,
+// src/model.rs:540-543); pass 2: one workgroup reduces the partials, stores
+// the token and (in the decode loop) advances the step state and records the
+// non-finite flag there.
+constexpr int ARGMAX_NONFINITE = (int)0x80000000;
+
 __device__ __forceinline__ void better(float &v, int &i, float ov, int oi)
 {
     if (ov > v || (ov == v && oi < i)) {
@@ -471,26 +495,39 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float *__rest
 {
     __shared__ float sv[4];
     __shared__ int si[4];
+    __shared__ int sf[4];
     const int t = threadIdx.x;
     float v = -INFINITY;
     int idx = 0x7fffffff;
-    for (int i = blockIdx.x * 256 + t; i < n; i += gridDim.x * 256) better(v, idx, x[i], i);
+    bool nonfinite = false;
+    for (int i = blockIdx.x * 256 + t; i < n; i += gridDim.x * 256) {
+        const float xi = x[i];
+        nonfinite |= !isfinite(xi);
+        if (!isnan(xi)) better(v, idx, xi, i);
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1)
         better(v, idx, __shfl_xor(v, off, 64), __shfl_xor(idx, off, 64));
+    const bool any_nf = __any(nonfinite);
     if ((t & 63) == 0) {
         sv[t >> 6] = v;
         si[t >> 6] = idx;
+        sf[t >> 6] = any_nf;
     }
     __syncthreads();
     if (t == 0) {
-        for (int w = 1; w < 4; ++w) better(v, idx, sv[w], si[w]);
+        int f = sf[0];
+        for (int w = 1; w < 4; ++w) {
+            better(v, idx, sv[w], si[w]);
+            f |= sf[w];
+        }
         pv[blockIdx.x] = v;
-        pi[blockIdx.x] = idx;
+        pi[blockIdx.x] = idx | (f ? ARGMAX_NONFINITE : 0);
     }
 }
 
-__global__ __launch_bounds__(64) void argmax_final_kernel(const float *__restrict__ pv,
+__global__ __launch_bounds__(64) void argmax_final_kernel(const float *__restrict__ x, int n,
+                                                          const float *__restrict__ pv,
                                                           const int *__restrict__ pi, int np,
                                                           int *__restrict__ token,
                                                           StepState *st, int *history)
@@ -498,16 +535,25 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float *__restric
     const int t = threadIdx.x;
     float v = -INFINITY;
     int idx = 0x7fffffff;
-    for (int i = t; i < np; i += 64) better(v, idx, pv[i], pi[i]);
+    bool nonfinite = false;
+    for (int i = t; i < np; i += 64) {
+        const int pii = pi[i];
+        nonfinite |= (pii & ARGMAX_NONFINITE) != 0;
+        better(v, idx, pv[i], pii & ~ARGMAX_NONFINITE);
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1)
         better(v, idx, __shfl_xor(v, off, 64), __shfl_xor(idx, off, 64));
+    const bool any_nf = __any(nonfinite);
     if (t == 0) {
+        if (isnan(x[0])) idx = 0;
+        idx = min(max(idx, 0), n - 1);
         *token = idx;
         if (st) {
             if (history && st->step < st->history_cap) history[st->step] = idx;
             st->step += 1;
             st->pos += 1;
+            if (any_nf) st->nonfinite = 1;
         }
     }
 }
@@ -596,6 +642,15 @@ int prefill_attention_splits(int context)
     return (context + c - 1) / c;
 }
 
+int launch_sum_parts(const float *x, const float *parts, int np, int stride, int n, float *out,
+                     void *stream)
+{
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(sum_parts_kernel, dim3((n + 255) / 256), dim3(256), 0,
+                       (hipStream_t)stream, x, parts, np, stride, n, out);
+    return (int)hipGetLastError();
+}
+
 int launch_zero_u32(unsigned *p, int n, void *stream)
 {
     if (n <= 0) return 0;
@@ -671,7 +726,7 @@ int launch_argmax(const float *x, int n, float *pv, int *pi, int *token, StepSta
     const int np = argmax_partials(n);
     hipStream_t s = (hipStream_t)stream;
     hipLaunchKernelGGL(argmax_partial_kernel, dim3(np), dim3(256), 0, s, x, n, pv, pi);
-    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(64), 0, s, pv, pi, np, token, st,
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(64), 0, s, x, n, pv, pi, np, token, st,
                        history);
     return (int)hipGetLastError();
 }

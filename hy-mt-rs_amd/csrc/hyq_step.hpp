@@ -7,13 +7,14 @@
 
 namespace hyq {
 
-// Device-resident step state: the position of the token being decoded and the
-// number of tokens generated so far (index into the history buffer).
+// Device-resident step state: the position of the token being decoded, the
+// number of tokens generated so far (index into the history buffer), and a
+// flag the argmax sets when a step's logits held a non-finite value.
 struct StepState {
     int pos;
     int step;
     int history_cap;
-    int pad;
+    int nonfinite;
 };
 
 int launch_embed_row(int fmt, WView w, int cols, const int *token, float *out, void *stream);
@@ -46,6 +47,9 @@ int attention_splits(int context);
 int prefill_attention_chunk(int context);
 int prefill_attention_splits(int context);
 int launch_zero_u32(unsigned *p, int n, void *stream);
+// out[i] = ((x[i] + parts[i]) + parts[stride + i]) + ... over np partial rows.
+int launch_sum_parts(const float *x, const float *parts, int np, int stride, int n, float *out,
+                     void *stream);
 // Attention of one query token over cache rows 0..=*pos (q already rotated
 // and normalized), merged into out [heads*128].
 int launch_attention(const float *q, const float *kcache, const float *vcache, const int *pos,

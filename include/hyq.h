@@ -64,6 +64,8 @@ int hyq_block_bytes(int dtype);
 
 /* ---- context: the device and stream a rayon pool stood for ---- */
 int hyq_ctx_create(int device, hyq_ctx **out);
+/* Decoders created on a context (hyq_dense_*) use its stream: destroy them
+ * first. Weights and Q8 buffers may outlive it. */
 void hyq_ctx_destroy(hyq_ctx *ctx);
 /* The context's hipStream_t, for callers that enqueue their own work. */
 void *hyq_ctx_stream(hyq_ctx *ctx);
@@ -271,6 +273,14 @@ int hyq_dense_prefill(hyq_dense *m, const int32_t *tokens, size_t n, float *logi
  * query head and attention split. No counterpart in the reference, whose
  * chunk is fixed. */
 int hyq_dense_set_prefill_rows(hyq_dense *m, size_t rows);
+/* Parity tracing (no counterpart in the reference: it exposes the hidden row
+ * that Model::forward_into carries between layers, src/model.rs:394-513).
+ * With trace_d set (device memory of `floats` floats, at least
+ * (layers + 1) * hidden), hyq_dense_forward writes the hidden row after the
+ * embedding and after each layer as [layers + 1][hidden]; a hyq_dense_prefill
+ * pass of n rows writes [layers + 1][n][hidden] when it fits in `floats`.
+ * Graph replays (hyq_dense_generate) never write it. NULL switches it off. */
+int hyq_dense_set_trace(hyq_dense *m, float *trace_d, size_t floats);
 /* Reads cached keys/values [positions][kv_heads*head_dim] of one layer
  * (the Session's KvCache, src/model.rs:650-669). */
 int hyq_dense_read_kv(hyq_dense *m, int layer, size_t positions, float *keys, float *values);

@@ -74,6 +74,11 @@ def _declare(L: ctypes.CDLL) -> None:
                                             ctypes.c_int]),
         "hyqo_prefill_chunk": (ctypes.c_int, [P, P, P, SZ, SZ, P, SZ, ctypes.c_int, P,
                                               ctypes.c_int]),
+        "hyqo_layer_step": (ctypes.c_int, [P, ctypes.c_int, P, P, P, SZ, SZ, ctypes.c_int,
+                                           ctypes.c_int]),
+        "hyqo_prefill_layer": (ctypes.c_int, [P, ctypes.c_int, P, P, P, SZ, SZ, SZ,
+                                              ctypes.c_int]),
+        "hyqo_output_logits": (None, [P, P, ctypes.c_int, P, ctypes.c_int]),
         "hyqo_argmax": (ctypes.c_int, [P, SZ]),
         "hyqo_max_threads": (ctypes.c_int, []),
     }
@@ -279,6 +284,37 @@ class DenseOracle:
                                     token, int(int8_path), _p(logits), threads)
         if rc != 0:
             raise ValueError("decode_step: bad position or token")
+        return logits
+
+    def layer(self, l: int, hidden: np.ndarray, kc: np.ndarray, vc: np.ndarray, pos: int,
+              int8_path: bool, threads: int = 0) -> np.ndarray:
+        """One layer of the batch-1 step on a copy of `hidden` [H], with that
+        layer's caches kc/vc [ctx, kv_heads*head_dim] (row `pos` written)."""
+        h = np.ascontiguousarray(hidden, np.float32).copy()
+        assert kc.flags["C_CONTIGUOUS"] and vc.flags["C_CONTIGUOUS"]
+        rc = lib().hyqo_layer_step(ctypes.byref(self.m), l, _p(h), _p(kc), _p(vc),
+                                   kc.shape[0], pos, int(int8_path), threads)
+        if rc != 0:
+            raise ValueError("layer_step: bad layer or position")
+        return h
+
+    def prefill_layer(self, l: int, hidden: np.ndarray, kc: np.ndarray, vc: np.ndarray,
+                      pos: int, threads: int = 0) -> np.ndarray:
+        """One layer of the batch-n arm on a copy of `hidden` [n, H]."""
+        h = np.ascontiguousarray(hidden, np.float32).copy()
+        n = h.size // self.model["cfg"]["hidden"]
+        rc = lib().hyqo_prefill_layer(ctypes.byref(self.m), l, _p(h), _p(kc), _p(vc),
+                                      kc.shape[0], pos, n, threads)
+        if rc != 0:
+            raise ValueError("prefill_layer: bad layer, rows or position")
+        return h
+
+    def output(self, hidden: np.ndarray, int8_path: bool, threads: int = 0) -> np.ndarray:
+        """Output norm + output matmul of one hidden row."""
+        h = np.ascontiguousarray(hidden, np.float32).copy()
+        logits = np.empty(self.model["cfg"]["vocab"], np.float32)
+        lib().hyqo_output_logits(ctypes.byref(self.m), _p(h), int(int8_path), _p(logits),
+                                 threads)
         return logits
 
     def prefill(self, kcache: np.ndarray, vcache: np.ndarray, pos: int, tokens,

@@ -88,8 +88,8 @@ static float half_at(const uint8_t *p)
     return hyqo_f16_to_f32((uint16_t)(p[0] | (p[1] << 8)));
 }
 
-/* STQ_CODEBOOK (src/quant.rs:1081-1084), ggml-derived (MIT, see
- * THIRD_PARTY_NOTICES.md of the reference). Index = sign<<4 | nibble; entry
+/* STQ_CODEBOOK (src/quant.rs:1081-1084), ggml-derived (MIT; the notice is in
+ * THIRD_PARTY_NOTICES.md at the top of this repository). Index = sign<<4 | nibble; entry
  * holds four 2-bit codes, digit = code - 1. */
 static const uint8_t STQ_CODEBOOK[32] = {
     0xa9, 0x89, 0x29, 0x09, 0xa6, 0x86, 0x26, 0x06, 0x9a, 0x92, 0x1a, 0x12, 0x6a, 0x62, 0x4a, 0x42,

@@ -144,13 +144,12 @@ static void linear(const hyqo_model *m, int dtype, const uint8_t *w, size_t rows
     (void)m;
 }
 
-int hyqo_decode_step(const hyqo_model *m, float *kcache, float *vcache, size_t ctx, size_t pos,
-                     int token, int int8_path, float *logits, int threads)
+int hyqo_layer_step(const hyqo_model *m, int l, float *hidden, float *kc, float *vc, size_t ctx,
+                    size_t pos, int int8_path, int threads)
 {
     size_t H = (size_t)m->hidden, D = (size_t)m->head_dim;
     size_t qlen = (size_t)m->heads * D, kvw = (size_t)m->kv_heads * D, F = (size_t)m->ffn;
-    if (pos >= ctx || token < 0 || token >= m->vocab) return -1;
-    float *hidden = (float *)malloc(sizeof(float) * H);
+    if (l < 0 || l >= m->layers || pos >= ctx) return -1;
     float *xn = (float *)malloc(sizeof(float) * H);
     float *q = (float *)malloc(sizeof(float) * qlen);
     float *k = (float *)malloc(sizeof(float) * kvw);
@@ -160,49 +159,129 @@ int hyqo_decode_step(const hyqo_model *m, float *kcache, float *vcache, size_t c
     float *gate = (float *)malloc(sizeof(float) * F);
     float *up = (float *)malloc(sizeof(float) * F);
     float cos_s[512], sin_s[512];
-
-    /* embedding.row_into (src/model.rs:376) */
-    size_t erb = rb_of(m->dtype_embed, H);
-    hyqo_decode(m->dtype_embed, m->embed + (size_t)token * erb, erb, hidden, H);
+    /* the step's RoPE tables at `pos` (src/model.rs:378-392) */
     hyqo_rope_tables(D, m->rope_base, pos, cos_s, sin_s);
 
-    for (int l = 0; l < m->layers; ++l) {
-        float *kc = kcache + (size_t)l * ctx * kvw;
-        float *vc = vcache + (size_t)l * ctx * kvw;
-        hyqo_rms_norm_into(hidden, m->attn_norm[l], H, m->eps, xn);
-        linear(m, m->dtype_linear, m->wq[l], qlen, H, xn, q, int8_path, threads);
-        linear(m, m->dtype_linear, m->wk[l], kvw, H, xn, k, int8_path, threads);
-        linear(m, m->dtype_linear, m->wv[l], kvw, H, xn, v, int8_path, threads);
-        /* dense order: RoPE, then per-head Q/K RMSNorm (src/model.rs:425-446) */
-        hyqo_rope(q, (size_t)m->heads, D, cos_s, sin_s);
-        hyqo_rope(k, (size_t)m->kv_heads, D, cos_s, sin_s);
-        hyqo_rms_norm_rows(q, m->q_norm[l], qlen, D, m->eps);
-        hyqo_rms_norm_rows(k, m->k_norm[l], kvw, D, m->eps);
-        memcpy(kc + pos * kvw, k, sizeof(float) * kvw);
-        memcpy(vc + pos * kvw, v, sizeof(float) * kvw);
-        hyqo_attention(q, kc, vc, (size_t)m->heads, (size_t)m->kv_heads, D, pos + 1, att);
-        linear(m, m->dtype_linear, m->wo[l], H, qlen, att, proj, int8_path, threads);
-        for (size_t i = 0; i < H; ++i) hidden[i] += proj[i];
-        hyqo_rms_norm_into(hidden, m->ffn_norm[l], H, m->eps, xn);
-        if (int8_path) {
-            gemv_int8(m->dtype_linear, m->wgate[l], F, H, xn, gate);
-            gemv_int8(m->dtype_linear, m->wup[l], F, H, xn, up);
-            for (size_t i = 0; i < F; ++i) {
-                float g = gate[i];
-                float silu = g / (1.0f + expf(-g));
-                gate[i] = silu * up[i];
-            }
-        } else {
-            hyqo_gate_up_silu(m->dtype_linear, m->wgate[l], m->wup[l], F, H, xn, gate, threads);
+    hyqo_rms_norm_into(hidden, m->attn_norm[l], H, m->eps, xn);
+    linear(m, m->dtype_linear, m->wq[l], qlen, H, xn, q, int8_path, threads);
+    linear(m, m->dtype_linear, m->wk[l], kvw, H, xn, k, int8_path, threads);
+    linear(m, m->dtype_linear, m->wv[l], kvw, H, xn, v, int8_path, threads);
+    /* dense order: RoPE, then per-head Q/K RMSNorm (src/model.rs:425-446) */
+    hyqo_rope(q, (size_t)m->heads, D, cos_s, sin_s);
+    hyqo_rope(k, (size_t)m->kv_heads, D, cos_s, sin_s);
+    hyqo_rms_norm_rows(q, m->q_norm[l], qlen, D, m->eps);
+    hyqo_rms_norm_rows(k, m->k_norm[l], kvw, D, m->eps);
+    memcpy(kc + pos * kvw, k, sizeof(float) * kvw);
+    memcpy(vc + pos * kvw, v, sizeof(float) * kvw);
+    hyqo_attention(q, kc, vc, (size_t)m->heads, (size_t)m->kv_heads, D, pos + 1, att);
+    linear(m, m->dtype_linear, m->wo[l], H, qlen, att, proj, int8_path, threads);
+    for (size_t i = 0; i < H; ++i) hidden[i] += proj[i];
+    hyqo_rms_norm_into(hidden, m->ffn_norm[l], H, m->eps, xn);
+    if (int8_path) {
+        gemv_int8(m->dtype_linear, m->wgate[l], F, H, xn, gate);
+        gemv_int8(m->dtype_linear, m->wup[l], F, H, xn, up);
+        for (size_t i = 0; i < F; ++i) {
+            float g = gate[i];
+            float silu = g / (1.0f + expf(-g));
+            gate[i] = silu * up[i];
         }
-        linear(m, m->dtype_down, m->wdown[l], H, F, gate, proj, int8_path, threads);
-        for (size_t i = 0; i < H; ++i) hidden[i] += proj[i];
+    } else {
+        hyqo_gate_up_silu(m->dtype_linear, m->wgate[l], m->wup[l], F, H, xn, gate, threads);
     }
+    linear(m, m->dtype_down, m->wdown[l], H, F, gate, proj, int8_path, threads);
+    for (size_t i = 0; i < H; ++i) hidden[i] += proj[i];
+
+    free(xn);
+    free(q);
+    free(k);
+    free(v);
+    free(att);
+    free(proj);
+    free(gate);
+    free(up);
+    return 0;
+}
+
+void hyqo_output_logits(const hyqo_model *m, float *hidden, int int8_path, float *logits,
+                        int threads)
+{
+    size_t H = (size_t)m->hidden;
+    /* rms_norm(hidden, output_norm), then the output matmul (src/model.rs:515-538) */
     hyqo_rms_norm_rows(hidden, m->output_norm, H, H, m->eps);
     linear(m, m->dtype_embed, m->output ? m->output : m->embed, (size_t)m->vocab, H, hidden,
            logits, int8_path, threads);
+}
 
+int hyqo_decode_step(const hyqo_model *m, float *kcache, float *vcache, size_t ctx, size_t pos,
+                     int token, int int8_path, float *logits, int threads)
+{
+    size_t H = (size_t)m->hidden, kvw = (size_t)m->kv_heads * m->head_dim;
+    if (pos >= ctx || token < 0 || token >= m->vocab) return -1;
+    float *hidden = (float *)malloc(sizeof(float) * H);
+    /* embedding.row_into (src/model.rs:376) */
+    size_t erb = rb_of(m->dtype_embed, H);
+    hyqo_decode(m->dtype_embed, m->embed + (size_t)token * erb, erb, hidden, H);
+    for (int l = 0; l < m->layers; ++l)
+        hyqo_layer_step(m, l, hidden, kcache + (size_t)l * ctx * kvw,
+                        vcache + (size_t)l * ctx * kvw, ctx, pos, int8_path, threads);
+    hyqo_output_logits(m, hidden, int8_path, logits, threads);
     free(hidden);
+    return 0;
+}
+
+int hyqo_prefill_layer(const hyqo_model *m, int l, float *hidden, float *kc, float *vc,
+                       size_t ctx, size_t pos, size_t n, int threads)
+{
+    size_t H = (size_t)m->hidden, D = (size_t)m->head_dim;
+    size_t qlen = (size_t)m->heads * D, kvw = (size_t)m->kv_heads * D, F = (size_t)m->ffn;
+    if (l < 0 || l >= m->layers || n == 0 || pos + n > ctx) return -1;
+    float *xn = (float *)malloc(sizeof(float) * n * H);
+    float *q = (float *)malloc(sizeof(float) * n * qlen);
+    float *k = (float *)malloc(sizeof(float) * n * kvw);
+    float *v = (float *)malloc(sizeof(float) * n * kvw);
+    float *att = (float *)malloc(sizeof(float) * n * qlen);
+    float *proj = (float *)malloc(sizeof(float) * n * H);
+    float *gate = (float *)malloc(sizeof(float) * n * F);
+    float *up = (float *)malloc(sizeof(float) * n * F);
+    float cos_s[512], sin_s[512];
+
+    /* normalized = rms_norm(hidden) row by row; q/k/v = matmul(., batch) (:555-564) */
+    memcpy(xn, hidden, sizeof(float) * n * H);
+    hyqo_rms_norm_rows(xn, m->attn_norm[l], n * H, H, m->eps);
+    hyqo_matmul(m->dtype_linear, m->wq[l], qlen, H, xn, n, q, threads);
+    hyqo_matmul(m->dtype_linear, m->wk[l], kvw, H, xn, n, k, threads);
+    hyqo_matmul(m->dtype_linear, m->wv[l], kvw, H, xn, n, v, threads);
+    /* rope at start + token (src/model.rs:570-583, 919-947), then the dense
+     * order's per-head norms (:584-587) */
+    for (size_t t = 0; t < n; ++t) {
+        hyqo_rope_tables(D, m->rope_base, pos + t, cos_s, sin_s);
+        hyqo_rope(q + t * qlen, (size_t)m->heads, D, cos_s, sin_s);
+        hyqo_rope(k + t * kvw, (size_t)m->kv_heads, D, cos_s, sin_s);
+    }
+    hyqo_rms_norm_rows(q, m->q_norm[l], n * qlen, D, m->eps);
+    hyqo_rms_norm_rows(k, m->k_norm[l], n * kvw, D, m->eps);
+    /* cache.append (:588-593, 650-669), then causal attention: token t sees
+     * positions 0..=pos+t (src/model.rs:956-961) */
+    memcpy(kc + pos * kvw, k, sizeof(float) * n * kvw);
+    memcpy(vc + pos * kvw, v, sizeof(float) * n * kvw);
+    for (size_t t = 0; t < n; ++t)
+        hyqo_attention(q + t * qlen, kc, vc, (size_t)m->heads, (size_t)m->kv_heads, D,
+                       pos + t + 1, att + t * qlen);
+    hyqo_matmul(m->dtype_linear, m->wo[l], H, qlen, att, n, proj, threads);
+    for (size_t i = 0; i < n * H; ++i) hidden[i] += proj[i];
+    /* DenseFfn::forward at batch n (src/model.rs:672-685): two matmuls,
+     * silu(g) * u, down */
+    memcpy(xn, hidden, sizeof(float) * n * H);
+    hyqo_rms_norm_rows(xn, m->ffn_norm[l], n * H, H, m->eps);
+    hyqo_matmul(m->dtype_linear, m->wgate[l], F, H, xn, n, gate, threads);
+    hyqo_matmul(m->dtype_linear, m->wup[l], F, H, xn, n, up, threads);
+    for (size_t i = 0; i < n * F; ++i) {
+        float g = gate[i];
+        gate[i] = (g / (1.0f + expf(-g))) * up[i];
+    }
+    hyqo_matmul(m->dtype_down, m->wdown[l], H, F, gate, n, proj, threads);
+    for (size_t i = 0; i < n * H; ++i) hidden[i] += proj[i];
+
     free(xn);
     free(q);
     free(k);
@@ -217,8 +296,7 @@ int hyqo_decode_step(const hyqo_model *m, float *kcache, float *vcache, size_t c
 int hyqo_prefill_chunk(const hyqo_model *m, float *kcache, float *vcache, size_t ctx, size_t pos,
                        const int *tokens, size_t n, int int8_path, float *logits, int threads)
 {
-    size_t H = (size_t)m->hidden, D = (size_t)m->head_dim;
-    size_t qlen = (size_t)m->heads * D, kvw = (size_t)m->kv_heads * D, F = (size_t)m->ffn;
+    size_t H = (size_t)m->hidden, kvw = (size_t)m->kv_heads * m->head_dim;
     if (n == 0 || pos + n > ctx) return -1;
     for (size_t t = 0; t < n; ++t)
         if (tokens[t] < 0 || tokens[t] >= m->vocab) return -1;
@@ -226,76 +304,16 @@ int hyqo_prefill_chunk(const hyqo_model *m, float *kcache, float *vcache, size_t
     if (n == 1) return hyqo_decode_step(m, kcache, vcache, ctx, pos, tokens[0], int8_path, logits,
                                         threads);
     float *hidden = (float *)malloc(sizeof(float) * n * H);
-    float *xn = (float *)malloc(sizeof(float) * n * H);
-    float *q = (float *)malloc(sizeof(float) * n * qlen);
-    float *k = (float *)malloc(sizeof(float) * n * kvw);
-    float *v = (float *)malloc(sizeof(float) * n * kvw);
-    float *att = (float *)malloc(sizeof(float) * n * qlen);
-    float *proj = (float *)malloc(sizeof(float) * n * H);
-    float *gate = (float *)malloc(sizeof(float) * n * F);
-    float *up = (float *)malloc(sizeof(float) * n * F);
-    float cos_s[512], sin_s[512];
-
     /* embedding rows (src/model.rs:549-552) */
     size_t erb = rb_of(m->dtype_embed, H);
     for (size_t t = 0; t < n; ++t)
         hyqo_decode(m->dtype_embed, m->embed + (size_t)tokens[t] * erb, erb, hidden + t * H, H);
-
-    for (int l = 0; l < m->layers; ++l) {
-        float *kc = kcache + (size_t)l * ctx * kvw;
-        float *vc = vcache + (size_t)l * ctx * kvw;
-        /* normalized = rms_norm(hidden) row by row; q/k/v = matmul(., batch) (:555-564) */
-        memcpy(xn, hidden, sizeof(float) * n * H);
-        hyqo_rms_norm_rows(xn, m->attn_norm[l], n * H, H, m->eps);
-        hyqo_matmul(m->dtype_linear, m->wq[l], qlen, H, xn, n, q, threads);
-        hyqo_matmul(m->dtype_linear, m->wk[l], kvw, H, xn, n, k, threads);
-        hyqo_matmul(m->dtype_linear, m->wv[l], kvw, H, xn, n, v, threads);
-        /* rope at start + token (src/model.rs:570-583, 919-947), then the dense
-         * order's per-head norms (:584-587) */
-        for (size_t t = 0; t < n; ++t) {
-            hyqo_rope_tables(D, m->rope_base, pos + t, cos_s, sin_s);
-            hyqo_rope(q + t * qlen, (size_t)m->heads, D, cos_s, sin_s);
-            hyqo_rope(k + t * kvw, (size_t)m->kv_heads, D, cos_s, sin_s);
-        }
-        hyqo_rms_norm_rows(q, m->q_norm[l], n * qlen, D, m->eps);
-        hyqo_rms_norm_rows(k, m->k_norm[l], n * kvw, D, m->eps);
-        /* cache.append (:588-593, 650-669), then causal attention: token t sees
-         * positions 0..=pos+t (src/model.rs:956-961) */
-        memcpy(kc + pos * kvw, k, sizeof(float) * n * kvw);
-        memcpy(vc + pos * kvw, v, sizeof(float) * n * kvw);
-        for (size_t t = 0; t < n; ++t)
-            hyqo_attention(q + t * qlen, kc, vc, (size_t)m->heads, (size_t)m->kv_heads, D,
-                           pos + t + 1, att + t * qlen);
-        hyqo_matmul(m->dtype_linear, m->wo[l], H, qlen, att, n, proj, threads);
-        for (size_t i = 0; i < n * H; ++i) hidden[i] += proj[i];
-        /* DenseFfn::forward at batch n (src/model.rs:672-685): two matmuls,
-         * silu(g) * u, down */
-        memcpy(xn, hidden, sizeof(float) * n * H);
-        hyqo_rms_norm_rows(xn, m->ffn_norm[l], n * H, H, m->eps);
-        hyqo_matmul(m->dtype_linear, m->wgate[l], F, H, xn, n, gate, threads);
-        hyqo_matmul(m->dtype_linear, m->wup[l], F, H, xn, n, up, threads);
-        for (size_t i = 0; i < n * F; ++i) {
-            float g = gate[i];
-            gate[i] = (g / (1.0f + expf(-g))) * up[i];
-        }
-        hyqo_matmul(m->dtype_down, m->wdown[l], H, F, gate, n, proj, threads);
-        for (size_t i = 0; i < n * H; ++i) hidden[i] += proj[i];
-    }
+    for (int l = 0; l < m->layers; ++l)
+        hyqo_prefill_layer(m, l, hidden, kcache + (size_t)l * ctx * kvw,
+                           vcache + (size_t)l * ctx * kvw, ctx, pos, n, threads);
     /* the last row's output norm and a batch-1 matmul (src/model.rs:605-607) */
-    float *last = hidden + (n - 1) * H;
-    hyqo_rms_norm_rows(last, m->output_norm, H, H, m->eps);
-    linear(m, m->dtype_embed, m->output ? m->output : m->embed, (size_t)m->vocab, H, last, logits,
-           int8_path, threads);
-
+    hyqo_output_logits(m, hidden + (n - 1) * H, int8_path, logits, threads);
     free(hidden);
-    free(xn);
-    free(q);
-    free(k);
-    free(v);
-    free(att);
-    free(proj);
-    free(gate);
-    free(up);
     return 0;
 }
 

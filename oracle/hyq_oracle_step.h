@@ -42,6 +42,16 @@ int hyqo_decode_step(const hyqo_model *m, float *kcache, float *vcache, size_t c
  * token outside the vocabulary. */
 int hyqo_prefill_chunk(const hyqo_model *m, float *kcache, float *vcache, size_t ctx, size_t pos,
                        const int *tokens, size_t n, int int8_path, float *logits, int threads);
+/* The pieces of those two: one layer of the batch-1 step on `hidden` [H]
+ * (in place) with that layer's caches kc/vc [ctx][kv_heads*head_dim]; one
+ * layer of the batch-n arm on hidden [n][H]; the output norm (in place) and
+ * the output matmul of one row. */
+int hyqo_layer_step(const hyqo_model *m, int l, float *hidden, float *kc, float *vc, size_t ctx,
+                    size_t pos, int int8_path, int threads);
+int hyqo_prefill_layer(const hyqo_model *m, int l, float *hidden, float *kc, float *vc,
+                       size_t ctx, size_t pos, size_t n, int threads);
+void hyqo_output_logits(const hyqo_model *m, float *hidden, int int8_path, float *logits,
+                        int threads);
 int hyqo_argmax(const float *x, size_t n);
 /* OpenMP threads the matmul/attention loops use when threads <= 0. */
 int hyqo_max_threads(void);

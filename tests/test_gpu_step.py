@@ -128,12 +128,27 @@ def test_causal_attention_closed_form(gpu_ctx, hyq):
 
 
 def test_argmax_first_maximum_wins(gpu_ctx, hyq, oracle):
+    """Greedy sampling (src/generation.rs:281-290): the first maximum wins, a
+    NaN is never taken and a NaN at index 0 keeps token 0; the oracle
+    restates that loop."""
     L = hyq.lib()
     rng = np.random.default_rng(0)
     cases = [rng.normal(0, 1, 120818).astype(np.float32), np.zeros(1000, np.float32),
-             np.full(7, -np.inf, np.float32)]
+             np.full(7, -np.inf, np.float32), np.full(5000, np.nan, np.float32)]
     x = rng.normal(0, 1, 50000).astype(np.float32)
     x[[123, 4567, 40000]] = 9.0
+    cases.append(x)
+    x = rng.normal(0, 1, 70000).astype(np.float32)
+    x[0] = np.nan
+    x[60000] = 50.0  # a larger value after a NaN at index 0 is not taken
+    cases.append(x)
+    x = rng.normal(0, 1, 70000).astype(np.float32)
+    x[[5, 33333, 69999]] = np.nan
+    x[44444] = np.inf  # +inf is a value like any other
+    cases.append(x)
+    x = np.full(9000, -np.inf, np.float32)
+    x[[100, 8000]] = np.nan
+    x[4000] = -1.0
     cases.append(x)
     for x in cases:
         xd = gpu_ctx.array(x)
@@ -142,9 +157,7 @@ def test_argmax_first_maximum_wins(gpu_ctx, hyq, oracle):
         hyq.check(L.hyq_argmax_d(gpu_ctx.handle, xd.ptr, x.size, scratch.ptr, tok.ptr))
         got = int(tok.numpy()[0])
         exp = oracle.lib().hyqo_argmax(x.ctypes.data, x.size)
-        if np.isneginf(x).all():
-            exp = 0
-        assert got == exp
+        assert got == exp, (got, exp)
 
 
 def test_embed_row(gpu_ctx, hyq, oracle):
@@ -257,3 +270,25 @@ def test_dense_errors(gpu_ctx, hyq):
     bad = hyq.DenseConfig(2, 500, 4, 1, 128, 1024, 3000, 1e4, 1e-5)
     with pytest.raises(ValueError):
         hyq.DenseDecoder(gpu_ctx, bad, 8)
+
+
+def test_non_finite_logits_poison_the_session(gpu_ctx, hyq):
+    """forward_into rejects non-finite logits and the failed forward poisons
+    the session (src/model.rs:348-351, :371, :540-545): an output row whose
+    block scale is +inf makes the logits non-finite; the forward fails, so do
+    later ones, until a new position starts a new session. The decode loop
+    never embeds an out-of-range token meanwhile (the argmax clamps)."""
+    c = SMALL
+    model = _untied(make_dense_model(c, linear=Q2_0C, seed=12), seed=120)
+    out = model["output"].reshape(c["vocab"], -1).copy()
+    out[77, 208:210] = np.array([np.inf], np.float16).view(np.uint8)  # Q6_K d of row 77
+    model["output"] = out.reshape(-1)
+    dec = load_dense(hyq, gpu_ctx, model, 32)
+    for call in (lambda: dec.forward(3), lambda: dec.generate(3, 4),
+                 lambda: dec.prefill([1, 2, 3])):
+        dec.position = 2
+        with pytest.raises(ValueError, match="non-finite"):
+            call()
+        with pytest.raises(ValueError, match="invalidated"):
+            dec.forward(3)
+    dec.close()

@@ -21,6 +21,10 @@ def _f(x):
     return ctypes.c_float(x)
 
 
+def _p(a):
+    return a.ctypes.data
+
+
 def test_rotary_pairs_halves_not_neighbors(oracle):
     """src/model.rs:1096-1102: dim 4, frequencies (pi/2, 1), position 1."""
     freqs = np.array([math.pi / 2, 1.0], np.float32)
@@ -103,3 +107,194 @@ def test_prefill_errors(oracle):
         ref.prefill(k, v, 4, [1, 2, 3, 4, 5], int8_path=False)  # exceeds the context
     with pytest.raises(ValueError):
         ref.prefill(k, v, 0, [1, c["vocab"]], int8_path=False)
+
+
+# ---- pins of the step glue by what the mathematics fixes ----
+
+def test_rms_norm_constant_row_closed_form(oracle):
+    """rms_norm_into (src/model.rs:785-830): a constant row c has mean square
+    c^2, so every output is c * (1/sqrt(c^2 + eps)) * w_i; a wrong divisor
+    (n - 1, or the sum instead of the mean) or a missing eps changes it."""
+    L = oracle.lib()
+    n = 2048
+    w = np.random.default_rng(1).normal(1, 0.02, n).astype(np.float32)
+    for c, eps in ((0.75, 1e-5), (3.0, 1e-5), (1e-3, 1e-5), (0.5, 0.0)):
+        x = np.full(n, c, np.float32)
+        out = np.empty(n, np.float32)
+        L.hyqo_rms_norm_into(_p(x), _p(w), n, _f(eps), _p(out))
+        scale = np.float32(1.0) / np.sqrt(np.float32(c) * np.float32(c) + np.float32(eps))
+        exp = (np.float32(c) * scale) * w
+        assert np.allclose(out, exp, rtol=2e-7, atol=0), (c, eps)
+        # the rows form equals the single-row form row by row
+        rows = np.tile(x, 3)
+        L.hyqo_rms_norm_rows(_p(rows), _p(w), rows.size, n, _f(eps))
+        assert np.array_equal(rows.reshape(3, n), np.tile(out, (3, 1)))
+
+
+def test_rms_norm_power_of_two_invariance(oracle):
+    """With eps = 0, scaling the row by 2^k scales the mean square by 4^k and
+    its root by 2^k, all exactly, so the output is unchanged bit for bit."""
+    L = oracle.lib()
+    rng = np.random.default_rng(2)
+    n = 6144
+    x = rng.normal(0, 1, n).astype(np.float32)
+    w = rng.normal(1, 0.02, n).astype(np.float32)
+    base = np.empty(n, np.float32)
+    L.hyqo_rms_norm_into(_p(x), _p(w), n, _f(0.0), _p(base))
+    for k in (-20, -3, 5, 30):
+        xs = (x * np.float32(2.0 ** k)).astype(np.float32)
+        out = np.empty(n, np.float32)
+        L.hyqo_rms_norm_into(_p(xs), _p(w), n, _f(0.0), _p(out))
+        assert np.array_equal(out.view(np.uint32), base.view(np.uint32)), k
+    # and against float64 within f32 rounding
+    ref = x.astype(np.float64) / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-5) * w
+    out = np.empty(n, np.float32)
+    L.hyqo_rms_norm_into(_p(x), _p(w), n, _f(1e-5), _p(out))
+    assert np.allclose(out, ref, rtol=1e-5, atol=1e-6)
+
+
+def test_attention_grouped_query_closed_form(oracle):
+    """attention_into (src/model.rs:949-1035) with 8 query heads on 2 KV heads
+    of dim 128 and keys along one axis: query head h is sqrt(128) * a_h * e0,
+    key p of KV head g is b_{g,p} * e0, so with the 1/sqrt(128) scale the
+    score is exactly a_h * b_{g,p} and the softmax weights are known in
+    closed form. Each KV head has its own keys and values, so a wrong scale
+    or a wrong head map (h % kv_heads instead of h / repeats) fails."""
+    L = oracle.lib()
+    heads, kvh, D, visible = 8, 2, 128, 5
+    rng = np.random.default_rng(3)
+    a = np.array([1.0, 0.5, -1.0, 2.0, 0.25, 1.5, -0.5, 1.0])
+    b = rng.normal(0, 1, (kvh, visible))
+    vals = rng.normal(0, 1, (kvh, visible, D))
+    q = np.zeros((heads, D), np.float32)
+    q[:, 0] = np.sqrt(128.0) * a
+    keys = np.zeros((visible, kvh, D), np.float32)
+    keys[:, :, 0] = b.T
+    values = np.ascontiguousarray(vals.transpose(1, 0, 2), dtype=np.float32)
+    out = np.empty(heads * D, np.float32)
+    L.hyqo_attention(_p(q), _p(keys), _p(values), heads, kvh, D, visible, _p(out))
+    out = out.reshape(heads, D)
+    for h in range(heads):
+        g = h // (heads // kvh)
+        s = a[h] * b[g].astype(np.float32).astype(np.float64)
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        exp = p @ values[:, g].astype(np.float64)
+        assert np.allclose(out[h], exp, rtol=1e-5, atol=1e-6), h
+
+
+def _rotate(oracle, x, heads, pos, base=11158840.0):
+    c = np.empty(64, np.float32)
+    s = np.empty(64, np.float32)
+    oracle.lib().hyqo_rope_tables(128, _f(base), pos, _p(c), _p(s))
+    y = np.ascontiguousarray(x, np.float32).copy()
+    oracle.lib().hyqo_rope(_p(y), heads, 128, _p(c), _p(s))
+    return y
+
+
+def test_rope_preserves_pair_norms_and_is_relative(oracle):
+    """rope_with_cache (src/model.rs:874-917) rotates each pair (j, j + 64) by
+    pos * base^(-2j/128): every pair keeps its length at any position, and the
+    product of a rotated query and key depends only on the position
+    difference; position 0 is the identity."""
+    rng = np.random.default_rng(4)
+    q = rng.normal(0, 1, 128).astype(np.float32)
+    k = rng.normal(0, 1, 128).astype(np.float32)
+    pair = lambda v: v[:64].astype(np.float64) ** 2 + v[64:].astype(np.float64) ** 2
+    for pos in (1, 7, 1023, 1151, 40000):
+        r = _rotate(oracle, q, 1, pos)
+        assert np.allclose(pair(r), pair(q), rtol=1e-5, atol=1e-6), pos
+        assert not np.array_equal(r, q)
+    dots = []
+    for p in (3, 10, 500, 1100):
+        for d in (0, 5, 37):
+            rq = _rotate(oracle, q, 1, p + d).astype(np.float64)
+            rk = _rotate(oracle, k, 1, p).astype(np.float64)
+            dots.append((d, float(rq @ rk)))
+    for d in (0, 5, 37):
+        vals = [v for dd, v in dots if dd == d]
+        assert max(vals) - min(vals) <= 2e-3 * max(1.0, abs(vals[0])), (d, vals)
+    # positions of one row apply per head: two heads rotate alike
+    two = _rotate(oracle, np.concatenate([q, k]), 2, 9)
+    assert np.array_equal(two[:128], _rotate(oracle, q, 1, 9))
+    assert np.array_equal(two[128:], _rotate(oracle, k, 1, 9))
+
+
+def _sigmoid(x):
+    x = np.float32(x)
+    if x >= 0:
+        return np.float32(1.0) / (np.float32(1.0) + np.exp(-x))
+    e = np.exp(x)
+    return e / (np.float32(1.0) + e)
+
+
+def test_route_closed_forms(oracle):
+    """route (src/model.rs:728-767): without normalisation every weight is
+    sigmoid(logit) * scale (the bias only selects); with it the weights sum to
+    scale unless the selected sigmoids sum below f16's smallest normal
+    (6.1035e-5), which then divides instead; equal scores keep index order."""
+    logits = np.array([0.0, 2.0, -2.0, 1.0, -30.0, 3.0], np.float32)
+    bias = np.array([0.0, 0.0, 10.0, 0.0, 0.0, -5.0], np.float32)
+    r = oracle.route(logits, bias, 3, False, 2.5)
+    assert [e for e, _ in r] == [2, 1, 3]
+    for e, w in r:  # (numpy's and glibc's f32 exp may differ by an ulp)
+        assert np.isclose(np.float32(w), _sigmoid(logits[e]) * np.float32(2.5), rtol=3e-7,
+                          atol=0), e
+    assert oracle.route(np.zeros(4, np.float32), np.zeros(4, np.float32), 2, False,
+                        1.0) == [(0, 0.5), (1, 0.5)]  # sigmoid(0) = 1/2 exactly; ties by index
+    r = oracle.route(logits, bias, 2, True, 2.826)
+    assert abs(sum(w for _, w in r) - 2.826) < 1e-6
+    # a softmax route would weight expert 2 by exp(-2)/(exp(-2)+exp(2)), not this
+    s2, s1 = _sigmoid(-2.0), _sigmoid(2.0)
+    assert abs(r[0][1] - s2 / (s2 + s1) * 2.826) < 1e-6
+    # tiny sigmoids: the denominator is floored at f16::MIN_POSITIVE
+    tiny = np.array([-20.0, -21.0, -22.0], np.float32)
+    r = oracle.route(tiny, np.zeros(3, np.float32), 2, True, 1.0)
+    floor = np.float32(6.1035156e-05)
+    for e, w in r:
+        assert np.isclose(np.float32(w), _sigmoid(tiny[e]) / floor, rtol=3e-7, atol=0), e
+    assert abs(sum(w for _, w in r) - 1.0) > 0.5  # not renormalised to the scale
+
+
+def test_argmax_ties_and_nan(oracle):
+    """Greedy sampling (src/generation.rs:281-290): the first maximum wins;
+    comparisons with NaN are false, so a NaN is never taken and a NaN at
+    index 0 keeps token 0."""
+    L = oracle.lib()
+    cases = [([1.0, 3.0, 3.0, 2.0], 1), ([np.nan, 5.0, 6.0], 0), ([1.0, np.nan, 0.5], 0),
+             ([0.0, np.nan, 2.0, np.nan, 2.0], 2), ([-np.inf] * 4, 0), ([-np.inf, -5.0], 1),
+             ([2.0, np.inf, np.inf], 1), ([7.0], 0)]
+    for vals, exp in cases:
+        x = np.array(vals, np.float32)
+        assert L.hyqo_argmax(_p(x), x.size) == exp, vals
+
+
+@pytest.mark.parametrize("int8", [False, True])
+def test_layer_pieces_compose_to_the_step(oracle, int8):
+    """The per-layer oracle functions the GPU's traced layers are checked
+    against compose to the whole step and the whole chunk bit for bit."""
+    c = SMALL
+    model = make_dense_model(c, linear=Q2_0C, seed=6)
+    model["output"] = random_matrix(Q6_K, c["vocab"], c["hidden"], 66)
+    ref = oracle.DenseOracle(model)
+    k1, v1 = make_kv_cache(c, 24, 9, seed=6)
+    k2, v2 = k1.copy(), v1.copy()
+    logits = ref.step(k1, v1, 9, 21, int8_path=int8)
+    rb = model["embed"].size // c["vocab"]
+    h = oracle.decode(model["embed_dtype"], model["embed"][21 * rb:22 * rb])
+    for l in range(c["layers"]):
+        h = ref.layer(l, h, k2[l], v2[l], 9, int8_path=int8)
+    assert np.array_equal(ref.output(h, int8_path=int8).view(np.uint32), logits.view(np.uint32))
+    assert np.array_equal(k1, k2) and np.array_equal(v1, v2)
+    # batch n
+    toks = np.array([5, 17, 2999, 0, 44], np.int32)
+    k1, v1 = make_kv_cache(c, 24, 9, seed=6)
+    k2, v2 = k1.copy(), v1.copy()
+    logits = ref.prefill(k1, v1, 9, toks, int8_path=int8)
+    h = np.stack([oracle.decode(model["embed_dtype"], model["embed"][t * rb:(t + 1) * rb])
+                  for t in toks])
+    for l in range(c["layers"]):
+        h = ref.prefill_layer(l, h, k2[l], v2[l], 9).reshape(toks.size, -1)
+    assert np.array_equal(ref.output(h[-1], int8_path=int8).view(np.uint32),
+                          logits.view(np.uint32))
+    assert np.array_equal(k1, k2) and np.array_equal(v1, v2)
