@@ -11,6 +11,7 @@
 #include <memory>
 #include <mutex>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "hyq_abi.hpp"
@@ -238,6 +239,146 @@ int check_ctx_weight(hyq_ctx *ctx, const hyq_weight *w, const char *who)
     return HYQ_OK;
 }
 
+// ---- Weight::matmul on device buffers, with its temporaries either from the
+// context (grown by hipMalloc on demand) or from the fixed per-device array
+// of hyq_matmul_noalloc_d ----
+
+// `scratch`: the no-allocation entry point's temporaries, one copy per GPU
+// (a module global, resident while the library is loaded). Host code never
+// passes this name to a kernel: it uses the per-device address that
+// hipGetSymbolAddress returned (g_scratch), resolved once per device by
+// hyq_ctx_create with that device current.
+static __device__ __align__(256) uint8_t scratch[HYQ_NOALLOC_SCRATCH_BYTES];
+std::mutex g_scratch_mu;
+std::unordered_map<int, void *> g_scratch;
+
+int resolve_scratch(int device)
+{
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch.count(device)) return HYQ_OK;
+    void *ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    g_scratch[device] = ptr;
+    return HYQ_OK;
+}
+
+struct FixedScratch {
+    uint8_t *base;
+    size_t bytes;
+};
+
+// Carves [offset, offset + bytes) out of the fixed array, or fails when the
+// request exceeds it.
+int take_fixed(const FixedScratch &fs, size_t &off, size_t bytes, void **out, const char *what)
+{
+    const size_t o = align_up(off, 256);
+    if (o + bytes > fs.bytes)
+        return fail(HYQ_EINVAL,
+                    "matmul_noalloc: %s needs %zu bytes of scratch beyond the %zu-byte maximum",
+                    what, o + bytes - fs.bytes, fs.bytes);
+    *out = fs.base + o;
+    off = o + bytes;
+    return HYQ_OK;
+}
+
+// Q8 buffers of length n laid out like q8_alloc's, inside the fixed array.
+int fixed_q8(const FixedScratch &fs, size_t &off, size_t n, Q8Ref *out)
+{
+    const size_t ng = (n + 255) / 256, n16 = (n + 15) / 16, n32 = (n + 31) / 32;
+    void *q = nullptr, *sc = nullptr, *s16 = nullptr, *s32 = nullptr, *s256 = nullptr;
+    int rc = take_fixed(fs, off, n, &q, "Q8 values");
+    if (!rc) rc = take_fixed(fs, off, ng * 4, &sc, "Q8 scales");
+    if (!rc) rc = take_fixed(fs, off, n16 * 4, &s16, "Q8 sums");
+    if (!rc) rc = take_fixed(fs, off, n32 * 4, &s32, "Q8 sums");
+    if (!rc) rc = take_fixed(fs, off, ng * 4, &s256, "Q8 sums");
+    if (rc) return rc;
+    out->q = (int8_t *)q;
+    out->s = (float *)sc;
+    out->sum16 = (int32_t *)s16;
+    out->sum32 = (int32_t *)s32;
+    out->sum256 = (int32_t *)s256;
+    out->n = n;
+    return HYQ_OK;
+}
+
+int matmul_dev(hyq_ctx *ctx, const hyq_weight *w, const float *x_d, size_t batch, float *y_d,
+               const FixedScratch *fs)
+{
+    int rc = check_ctx_weight(ctx, w, "matmul");
+    if (!rc) rc = check_matrix(w, "matmul");
+    if (rc) return rc;
+    if (batch == 0) return fail(HYQ_EINVAL, "%s: invalid activation shape", "matmul");
+    if (!x_d || !y_d) return fail(HYQ_EINVAL, "matmul: null buffer");
+    DeviceGuard g(ctx->device);
+    // Q8_0 of a width the int8 GEMV (256-value groups) or the GEMM (64-column
+    // slices) does not tile: the decoded-row path, as F32/F16
+    const bool q80_odd = w->dtype == HYQ_Q8_0 && w->cols % (batch == 1 ? 256 : 64) != 0;
+    if (is_raw(w->dtype) || q80_odd) {
+        // decode rows to f32 + dot (src/quant.rs:225-267; batched :312-343)
+        if (batch > 65535 * 64) return fail(HYQ_EINVAL, "matmul: batch %zu too large", batch);
+        if (batch == 1)
+            HYQ_LAUNCH(launch_f32_gemv(w->dtype, w->view, nullptr, (int)w->cols, x_d, y_d,
+                                       ctx->stream),
+                       "f32_gemv");
+        else
+            HYQ_LAUNCH(launch_f32_gemm(w->dtype, w->view, (int)w->cols, x_d, (int)batch, y_d,
+                                       ctx->stream),
+                       "f32_gemm");
+        return HYQ_OK;
+    }
+    if (batch == 1) {
+        rc = check_int8_path(w, "matmul");
+        if (rc) return rc;
+        if (can_stage(x_d, w->cols)) {
+            GemvArgs a{};
+            a.nseg = 1;
+            a.seg[0].w = w->view;
+            a.seg[0].y = y_d;
+            a.rows_total = (int)w->rows;
+            a.groups = (int)(w->cols / 256);
+            a.xin = x_d;
+            HYQ_LAUNCH(launch_gemv(w->dtype, GEMV_PLAIN, a, ctx->stream), "gemv");
+            return HYQ_OK;
+        }
+        Q8Ref q8;
+        size_t off = 0;
+        rc = fs ? fixed_q8(*fs, off, w->cols, &q8) : ctx_q8(ctx, w->cols, &q8);
+        if (!rc) rc = quantize_into(ctx, x_d, q8);
+        if (!rc) rc = gemv_plain(ctx, w, q8, nullptr, y_d);
+        return rc;
+    }
+    if (!is_quant(w->dtype)) return fail(HYQ_EDTYPE, "matmul: dtype %d has no batched path", w->dtype);
+    // the GEMM walks K in 64-column slices and loads x as float4
+    if (w->cols % 64) return fail(HYQ_EINVAL, "matmul: cols %zu is not a multiple of 64", w->cols);
+    if ((uintptr_t)x_d % 16 || (uintptr_t)y_d % 16)
+        return fail(HYQ_EINVAL, "matmul: device buffers must be 16-byte aligned");
+    if (batch > 65535) return fail(HYQ_EINVAL, "matmul: batch %zu exceeds 65535", batch);
+    const size_t xh_bytes = align_up(batch * w->cols * 2, 256);
+    const int ks = matmul_kslices(w->dtype, (int)w->rows, (int)w->cols, (int)batch);
+    const size_t part = ks > 1 ? (size_t)ks * batch * w->rows : 0;
+    void *xh_mem = nullptr, *part_mem = nullptr;
+    if (fs) {
+        size_t off = 0;
+        rc = take_fixed(*fs, off, xh_bytes + batch * 4, &xh_mem, "f16 activation rows");
+        if (!rc && part) rc = take_fixed(*fs, off, part * 4, &part_mem, "K-slice partials");
+        if (rc) return rc;
+    } else {
+        rc = ctx->xh.reserve(ctx->device, xh_bytes + batch * 4);
+        if (!rc && part) rc = ctx->kpart.reserve(ctx->device, part * 4);
+        if (rc) return rc;
+        xh_mem = ctx->xh.ptr();
+        part_mem = ctx->kpart.ptr();
+    }
+    _Float16 *xh = (_Float16 *)xh_mem;
+    float *rscale = (float *)((uint8_t *)xh_mem + xh_bytes);
+    HYQ_LAUNCH(launch_to_f16(x_d, (int)batch, (int)w->cols, xh, rscale, ctx->stream), "to_f16");
+    HYQ_LAUNCH(launch_gemm_f16(w->dtype, w->view, (int)w->cols, xh, rscale, (int)batch, y_d,
+                               nullptr, ctx->stream, (float *)part_mem, part, ks),
+               "gemm_f16");
+    return HYQ_OK;
+}
+
 } // namespace
 
 // ---------------------------------------------------------------------------
@@ -260,6 +401,9 @@ int hyq_ctx_create(int device, hyq_ctx **out)
     if (!g.ok) return fail(HYQ_EDEVICE, "hipSetDevice(%d) failed", device);
     auto ctx = std::make_unique<hyq_ctx>();
     ctx->device = device;
+    // the no-allocation entry point's per-device scratch address
+    int rc = resolve_scratch(device);
+    if (rc) return rc;
     HYQ_HIP(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking), "hipStreamCreate");
     *out = ctx.release();
     return HYQ_OK;
@@ -520,67 +664,24 @@ int hyq_gemv_isums_d(hyq_ctx *ctx, const hyq_weight *w, const hyq_q8 *x, int32_t
 
 int hyq_matmul_d(hyq_ctx *ctx, const hyq_weight *w, const float *x_d, size_t batch, float *y_d)
 {
-    int rc = check_ctx_weight(ctx, w, "matmul");
-    if (!rc) rc = check_matrix(w, "matmul");
-    if (rc) return rc;
-    if (batch == 0) return fail(HYQ_EINVAL, "%s: invalid activation shape", "matmul");
-    if (!x_d || !y_d) return fail(HYQ_EINVAL, "matmul: null buffer");
-    DeviceGuard g(ctx->device);
-    // Q8_0 of a width the int8 GEMV (256-value groups) or the GEMM (64-column
-    // slices) does not tile: the decoded-row path, as F32/F16
-    const bool q80_odd = w->dtype == HYQ_Q8_0 && w->cols % (batch == 1 ? 256 : 64) != 0;
-    if (is_raw(w->dtype) || q80_odd) {
-        // decode rows to f32 + dot (src/quant.rs:225-267; batched :312-343)
-        if (batch > 65535 * 64) return fail(HYQ_EINVAL, "matmul: batch %zu too large", batch);
-        if (batch == 1)
-            HYQ_LAUNCH(launch_f32_gemv(w->dtype, w->view, nullptr, (int)w->cols, x_d, y_d,
-                                       ctx->stream),
-                       "f32_gemv");
-        else
-            HYQ_LAUNCH(launch_f32_gemm(w->dtype, w->view, (int)w->cols, x_d, (int)batch, y_d,
-                                       ctx->stream),
-                       "f32_gemm");
-        return HYQ_OK;
+    return matmul_dev(ctx, w, x_d, batch, y_d, nullptr);
+}
+
+int hyq_matmul_noalloc_d(hyq_ctx *ctx, const hyq_weight *w, const float *x_d, size_t batch,
+                         float *y_d)
+{
+    if (!ctx) return fail(HYQ_EINVAL, "matmul_noalloc: null context");
+    FixedScratch fs{};
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        auto it = g_scratch.find(ctx->device);
+        if (it == g_scratch.end() || !it->second)
+            return fail(HYQ_EDEVICE, "matmul_noalloc: no scratch address for device %d",
+                        ctx->device);
+        fs.base = (uint8_t *)it->second;
     }
-    if (batch == 1) {
-        rc = check_int8_path(w, "matmul");
-        if (rc) return rc;
-        if (can_stage(x_d, w->cols)) {
-            GemvArgs a{};
-            a.nseg = 1;
-            a.seg[0].w = w->view;
-            a.seg[0].y = y_d;
-            a.rows_total = (int)w->rows;
-            a.groups = (int)(w->cols / 256);
-            a.xin = x_d;
-            HYQ_LAUNCH(launch_gemv(w->dtype, GEMV_PLAIN, a, ctx->stream), "gemv");
-            return HYQ_OK;
-        }
-        Q8Ref q8;
-        rc = ctx_q8(ctx, w->cols, &q8);
-        if (!rc) rc = quantize_into(ctx, x_d, q8);
-        if (!rc) rc = gemv_plain(ctx, w, q8, nullptr, y_d);
-        return rc;
-    }
-    if (!is_quant(w->dtype)) return fail(HYQ_EDTYPE, "matmul: dtype %d has no batched path", w->dtype);
-    // the GEMM walks K in 64-column slices and loads x as float4
-    if (w->cols % 64) return fail(HYQ_EINVAL, "matmul: cols %zu is not a multiple of 64", w->cols);
-    if ((uintptr_t)x_d % 16 || (uintptr_t)y_d % 16)
-        return fail(HYQ_EINVAL, "matmul: device buffers must be 16-byte aligned");
-    if (batch > 65535) return fail(HYQ_EINVAL, "matmul: batch %zu exceeds 65535", batch);
-    const size_t xh_bytes = align_up(batch * w->cols * 2, 256);
-    rc = ctx->xh.reserve(ctx->device, xh_bytes + batch * 4);
-    if (rc) return rc;
-    _Float16 *xh = (_Float16 *)ctx->xh.ptr();
-    float *rscale = (float *)((uint8_t *)ctx->xh.ptr() + xh_bytes);
-    const int ks = matmul_kslices(w->dtype, (int)w->rows, (int)w->cols, (int)batch);
-    const size_t part = ks > 1 ? (size_t)ks * batch * w->rows : 0;
-    if (part && (rc = ctx->kpart.reserve(ctx->device, part * 4))) return rc;
-    HYQ_LAUNCH(launch_to_f16(x_d, (int)batch, (int)w->cols, xh, rscale, ctx->stream), "to_f16");
-    HYQ_LAUNCH(launch_gemm_f16(w->dtype, w->view, (int)w->cols, xh, rscale, (int)batch, y_d,
-                               nullptr, ctx->stream, (float *)ctx->kpart.ptr(), part, ks),
-               "gemm_f16");
-    return HYQ_OK;
+    fs.bytes = HYQ_NOALLOC_SCRATCH_BYTES;
+    return matmul_dev(ctx, w, x_d, batch, y_d, &fs);
 }
 
 int hyq_dequant_rows_d(hyq_ctx *ctx, const hyq_weight *w, size_t row0, size_t nrows,

@@ -147,6 +147,24 @@ int hyq_gemv_isums_d(hyq_ctx *ctx, const hyq_weight *w, const hyq_q8 *x, int32_t
  * batch >= 2 is the f16-MFMA GEMM (src/quant.rs:272-344). */
 int hyq_matmul_d(hyq_ctx *ctx, const hyq_weight *w, const float *x_d, size_t batch,
                  float *y_d);
+/* Weight::matmul on device buffers for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). No counterpart in the reference. Same arguments, results
+ * and launches as hyq_matmul_d (bit for bit), but every temporary - the Q8
+ * row of an unstaged batch-1 input, the f16 activation rows and their
+ * scales, the K-slice partial sums of a batched product - lives in one
+ * fixed per-device array of HYQ_NOALLOC_SCRATCH_BYTES, resident from the
+ * first hyq_ctx_create on that device until the process ends; the call makes
+ * no hipMalloc/hipFree or other allocating call. A product whose temporaries
+ * exceed the array (batch * cols * 2 bytes of f16 rows plus, for batches of at
+ * most 128, up to 8 * batch * rows * 4 bytes of partials) returns HYQ_EINVAL
+ * before any work. Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (several contexts or streams at once) race; serialize
+ * them. The array keeps the last call's contents; nothing in it needs to
+ * start at zero. */
+#define HYQ_NOALLOC_SCRATCH_BYTES (32u * 1024u * 1024u)
+int hyq_matmul_noalloc_d(hyq_ctx *ctx, const hyq_weight *w, const float *x_d, size_t batch,
+                         float *y_d);
 /* ---- MoE expert products: the expert loop of Moe::forward (src/model.rs:699-725).
  * gate and up are rank-3 weights {hidden, mid, E}, down is {mid, hidden, E}
  * (the expert stacks Weight::expert slices, src/quant.rs:144-154). The
