@@ -86,6 +86,11 @@ SIGNATURES = {
     "hyq_dense_read_kv": (I, [P, I, SZ, P, P]),
     "hyq_dense_set_prefill_rows": (I, [P, SZ]),
     "hyq_dense_set_trace": (I, [P, P, SZ]),
+    "hyq_dense_set_architecture": (I, [P, I]),
+    "hyq_dense_set_moe": (I, [P, I, P, P, P, P, P, P, P, P, P]),
+    "hyq_moe_route_d": (I, [P, P, P, SZ, SZ, SZ, I, ctypes.c_float, P, P, P]),
+    "hyq_moe_forward_scratch_bytes": (SZ, [P, SZ, SZ]),
+    "hyq_moe_forward_d": (I, [P, P, P, P, P, P, P, P, P, P, P, SZ, P, SZ, P]),
     "hyq_dense_generate": (I, [P, ctypes.c_int32, SZ, I, P]),
     "hyq_gguf_open": (I, [ctypes.c_char_p, I, ctypes.POINTER(P)]),
     "hyq_gguf_open_bytes": (I, [P, SZ, I, ctypes.POINTER(P)]),
@@ -411,6 +416,62 @@ def isums_per_row(dtype: int, cols: int) -> int:
     return lib().hyq_isums_per_row(dtype, cols)
 
 
+ARCH_DENSE, ARCH_HYV3 = 0, 1
+
+
+class MoeConfig(ctypes.Structure):
+    """hyq_moe_config: the expert_* metadata of a HyV3 model."""
+    _fields_ = [("experts", I), ("used", I), ("mid", I), ("shared_mid", I), ("normalize", I),
+                ("scale", ctypes.c_float)]
+
+
+class MoeFfn:
+    """Moe::forward (src/model.rs:687-726) on the device: an F32 router, its
+    selection bias, expert stacks (rank-3 ``Weight``s) and a shared expert."""
+
+    def __init__(self, ctx: "Context", cfg: MoeConfig, router, bias, gate, up, down, sgate,
+                 sup, sdown):
+        self.ctx, self.cfg = ctx, cfg
+        self.weights = (router, gate, up, down, sgate, sup, sdown)
+        self.bias = ctx.array(np.ascontiguousarray(bias, np.float32))
+        self.hidden = router.cols
+
+    def forward_d(self, x_d: int, tokens: int, out_d: int) -> None:
+        """hyq_moe_forward_d on device buffers x [tokens][hidden] -> out."""
+        need = lib().hyq_moe_forward_scratch_bytes(ctypes.byref(self.cfg), self.hidden, tokens)
+        if need == 0:
+            raise ValueError("moe_forward: unsupported token count")
+        scratch = self.ctx.empty(need, np.uint8)
+        r, g, u, d, sg, su, sd = self.weights
+        check(lib().hyq_moe_forward_d(self.ctx.handle, ctypes.byref(self.cfg), r.handle,
+                                      self.bias.ptr, g.handle, u.handle, d.handle, sg.handle,
+                                      su.handle, sd.handle, x_d, tokens, scratch.ptr, need,
+                                      out_d))
+        self.ctx.sync()
+
+    def forward(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, self.hidden)
+        xd = self.ctx.array(x)
+        od = self.ctx.empty(x.size, np.float32)
+        self.forward_d(xd.ptr, x.shape[0], od.ptr)
+        return od.numpy().reshape(x.shape)
+
+
+def moe_route(ctx: "Context", logits: np.ndarray, bias: np.ndarray, used: int, normalize: bool,
+              scale: float):
+    """route (src/model.rs:728-767) of logits [tokens][experts] on the
+    device: (token, expert, weight) arrays, token-major, ascending experts."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    tokens, experts = logits.shape
+    ld, bd = ctx.array(logits), ctx.array(np.ascontiguousarray(bias, np.float32))
+    pt = ctx.empty(tokens * used, np.int32)
+    pe = ctx.empty(tokens * used, np.int32)
+    pw = ctx.empty(tokens * used, np.float32)
+    check(lib().hyq_moe_route_d(ctx.handle, ld.ptr, bd.ptr, tokens, experts, used,
+                                int(normalize), scale, pt.ptr, pe.ptr, pw.ptr))
+    return pt.numpy(), pe.numpy(), pw.numpy()
+
+
 class DenseDecoder:
     """Batch-1 decode of the dense graph on the device (Model::forward_into,
     src/model.rs:374-546, plus greedy sampling). Weights are borrowed
@@ -441,10 +502,23 @@ class DenseDecoder:
                   q_norm, k_norm) -> None:
         norms = [np.ascontiguousarray(a, np.float32) for a in (attn_norm, ffn_norm, q_norm,
                                                                k_norm)]
+        h = lambda w: w.handle if w is not None else None
         check(lib().hyq_dense_set_layer(self.handle, layer, q.handle, k.handle, v.handle,
-                                        o.handle, gate.handle, up.handle, down.handle,
+                                        o.handle, h(gate), h(up), h(down),
                                         *[_ptr(a) for a in norms]))
         self._keep.extend([q, k, v, o, gate, up, down])
+
+    def set_architecture(self, arch: int) -> None:
+        check(lib().hyq_dense_set_architecture(self.handle, arch))
+
+    def set_moe(self, layer: int, ffn: MoeFfn) -> None:
+        """The layer's FFN becomes ``ffn`` (Ffn::Moe)."""
+        r, g, u, d, sg, su, sd = ffn.weights
+        bias = ffn.bias.numpy()
+        check(lib().hyq_dense_set_moe(self.handle, layer, ctypes.byref(ffn.cfg), r.handle,
+                                      _ptr(bias), g.handle, u.handle, d.handle, sg.handle,
+                                      su.handle, sd.handle))
+        self._keep.append(ffn)
 
     def set_output(self, embedding, output, output_norm) -> None:
         on = np.ascontiguousarray(output_norm, np.float32)

@@ -30,6 +30,7 @@
 #include <vector>
 
 #include "hyq_abi.hpp"
+#include "hyq_moe_ffn.hpp"
 #include "hyq_step.hpp"
 
 using namespace hyq;
@@ -205,10 +206,22 @@ struct hyq_dense {
     bool poisoned = false;
     struct Layer {
         const hyq_weight *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
+        // the dense FFN, or none when the layer's FFN is an MoE (moe set)
         const hyq_weight *gate = nullptr, *up = nullptr, *down = nullptr;
         float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+        std::unique_ptr<MoeFfn> moe;
+        std::unique_ptr<DeviceBuffer> moe_bias; // the MoE's selection bias
     };
     std::vector<Layer> layers;
+    int arch = HYQ_ARCH_DENSE;
+    // the MoE shape every MoE layer shares (expert_* metadata is model-wide)
+    hyq_moe_config moe_cfg{};
+    bool has_moe = false;
+    // batch-1 MoE temporaries: the normalized row, its Q8, the FFN's buffers
+    std::unique_ptr<DeviceBuffer> moe_mem;
+    float *moe_xn = nullptr;
+    Q8Ref moe_q8;
+    MoeRowBuf moe_row{};
     const hyq_weight *embedding = nullptr, *output = nullptr;
     float *output_norm = nullptr;
 
@@ -247,6 +260,8 @@ struct hyq_dense {
     float *pf_att = nullptr, *pf_h = nullptr, *pf_rs = nullptr, *pf_part = nullptr;
     float *pf_kpart = nullptr; // K-slice partials of the output and down GEMMs
     size_t pf_kpart_floats = 0;
+    float *pf_xn = nullptr;    // MoE layers: the normalized rows [n][H] f32
+    MoeRowsBuf pf_moe{};
     _Float16 *pf_xh = nullptr;
     int32_t *pf_tok = nullptr;
 
@@ -312,13 +327,15 @@ int enqueue_step(hyq_dense *m, bool trace = false)
                "embed_row");
     const int *pos = &m->state->pos;
     const int ks = m->down_ks;
+    const bool norm_first = m->arch == HYQ_ARCH_HYV3;
     trace = trace && m->trace;
     if (trace)
         HYQ_LAUNCH(launch_sum_parts(m->hidden, nullptr, 0, 0, c.hidden, m->trace, st), "trace");
+    // partial rows the previous layer's down projection left (a dense layer
+    // with a K-split down; an MoE layer writes the whole hidden row)
+    int np = 0;
     for (int l = 0; l < c.layers; ++l) {
         const hyq_dense::Layer &L = m->layers[l];
-        // the previous layer's down projection left `ks` partial rows
-        const int np = l > 0 && ks > 1 ? ks : 0;
         {
             GemvArgs a = staged(L.q, m->hidden, L.attn_norm, c.rms_eps, m->qb, nullptr);
             a.sparts = m->parts;
@@ -340,7 +357,7 @@ int enqueue_step(hyq_dense *m, bool trace = false)
         HYQ_LAUNCH(launch_attention_rope(m->qb, m->kb, m->vb, L.q_norm, L.k_norm, m->freq,
                                          c.rms_eps, m->kcache(l), m->vcache(l), pos,
                                          (int)m->context, c.heads, c.kv_heads, m->att_scratch,
-                                         st),
+                                         st, norm_first),
                    "attention");
         HYQ_LAUNCH(launch_attention_merge(m->att_scratch, (int)m->context, c.heads, pos,
                                           m->att_out, st),
@@ -351,6 +368,19 @@ int enqueue_step(hyq_dense *m, bool trace = false)
             a.nrparts = np;
             a.parts_stride = c.hidden;
             HYQ_LAUNCH(launch_gemv(L.o->dtype, GEMV_PLAIN, a, st), "gemv_attn_output");
+        }
+        if (L.moe) {
+            // Ffn::Moe (src/model.rs:507-510): the normalized row and its Q8,
+            // then Moe::forward and the residual add (:512)
+            const Q8Ref &q = m->moe_q8;
+            HYQ_LAUNCH(launch_rms_norm_q8(m->hidden, L.ffn_norm, c.hidden, c.rms_eps, m->moe_xn,
+                                          q.q, q.s, q.sum16, q.sum32, q.sum256, st),
+                       "rms_norm_q8");
+            int rc = moe_ffn_row(st, *L.moe, m->moe_xn, q, m->moe_row, m->hidden, m->hidden,
+                                 trace ? m->trace + (size_t)(l + 1) * c.hidden : nullptr);
+            if (rc) return rc;
+            np = 0;
+            continue;
         }
         {
             GemvArgs a = staged(L.gate, m->hidden, L.ffn_norm, c.rms_eps, m->gb, nullptr);
@@ -368,15 +398,16 @@ int enqueue_step(hyq_dense *m, bool trace = false)
                                    staged(L.down, m->gb, nullptr, 0.f, m->hidden, m->hidden), st),
                        "gemv_down");
         }
+        np = ks > 1 ? ks : 0;
         if (trace)
-            HYQ_LAUNCH(launch_sum_parts(m->hidden, m->parts, ks > 1 ? ks : 0, c.hidden, c.hidden,
+            HYQ_LAUNCH(launch_sum_parts(m->hidden, m->parts, np, c.hidden, c.hidden,
                                         m->trace + (size_t)(l + 1) * c.hidden, st),
                        "trace");
     }
     {
         GemvArgs a = staged(m->output, m->hidden, m->output_norm, c.rms_eps, m->logits, nullptr);
         a.sparts = m->parts;
-        a.nsparts = c.layers > 0 && ks > 1 ? ks : 0;
+        a.nsparts = np;
         a.parts_stride = c.hidden;
         HYQ_LAUNCH(launch_gemv(m->output->dtype, GEMV_PLAIN, a, st), "gemv_lm_head");
     }
@@ -389,9 +420,19 @@ int enqueue_step(hyq_dense *m, bool trace = false)
 // PREFILL_CHUNK (src/model.rs:18): tokens per forward_into call.
 constexpr size_t PREFILL_CHUNK = 256;
 
+// Rows per prefill pass: the set size, at most the context, and for a model
+// with MoE layers at most what the grouped expert kernels take per call.
+size_t pass_rows(const hyq_dense *m)
+{
+    size_t N = std::min(m->pf_rows, m->context);
+    for (const hyq_dense::Layer &L : m->layers)
+        if (L.moe) N = std::min(N, (size_t)moe_rows_max(*L.moe));
+    return N;
+}
+
 int prefill_buffers(hyq_dense *m)
 {
-    const size_t N = std::min(m->pf_rows, m->context);
+    const size_t N = pass_rows(m);
     if (m->pf_mem && m->pf_cap == N) return HYQ_OK;
     m->pf_mem.reset();
     m->pf_cap = 0;
@@ -412,12 +453,19 @@ int prefill_buffers(hyq_dense *m)
     const size_t o_tok = take(N * 4);
     // the split attention-output and down GEMMs' partials (every layer's
     // formats: they may differ)
-    size_t kp = 0;
+    size_t kp = 0, moe_bytes = 0;
+    const MoeFfn *moe = nullptr;
     for (const hyq_dense::Layer &L : m->layers) {
         kp = std::max(kp, gemm_split_floats(L.o->dtype, (int)H, (int)N, (int)QL));
-        kp = std::max(kp, gemm_split_floats(L.down->dtype, (int)H, (int)N, (int)F));
+        if (L.down) kp = std::max(kp, gemm_split_floats(L.down->dtype, (int)H, (int)N, (int)F));
+        if (L.moe && moe_rows_bytes(*L.moe, (int)N) > moe_bytes) {
+            moe = L.moe.get();
+            moe_bytes = moe_rows_bytes(*moe, (int)N);
+        }
     }
     const size_t o_kpart = take(kp * 4);
+    const size_t o_xn = moe ? take(N * H * 4) : 0;
+    const size_t o_moe = moe ? take(moe_bytes) : 0;
     auto buf = std::make_unique<DeviceBuffer>();
     int rc = buf->alloc(m->ctx->device, off);
     if (rc) return rc;
@@ -434,6 +482,10 @@ int prefill_buffers(hyq_dense *m)
     m->pf_tok = (int32_t *)(b + o_tok);
     m->pf_kpart = (float *)(b + o_kpart);
     m->pf_kpart_floats = kp;
+    if (moe) {
+        m->pf_xn = (float *)(b + o_xn);
+        m->pf_moe = moe_rows_carve(*moe, (int)N, b + o_moe);
+    }
     m->pf_mem = std::move(buf);
     m->pf_cap = N;
     return HYQ_OK;
@@ -476,7 +528,8 @@ int enqueue_prefill_chunk(hyq_dense *m, int n)
         }
         HYQ_LAUNCH(launch_rope_norm_kv_rows(m->pf_q, m->pf_k, m->pf_v, L.q_norm, L.k_norm,
                                             m->freq, pos, n, c.heads, c.kv_heads, c.head_dim,
-                                            c.rms_eps, m->kcache(l), m->vcache(l), st),
+                                            c.rms_eps, m->kcache(l), m->vcache(l), st,
+                                            m->arch == HYQ_ARCH_HYV3),
                    "rope_norm_kv_rows");
         if (merge_rows_lds(c.heads, prefill_attention_splits((int)m->context)) <= 64 * 1024) {
             // attention with its rows merged straight into the GEMM's f16 operand
@@ -494,6 +547,13 @@ int enqueue_prefill_chunk(hyq_dense *m, int n)
         HYQ_LAUNCH(launch_gemm_f16(L.o->dtype, L.o->view, QL, m->pf_xh, m->pf_rs, n, m->pf_hid,
                                    m->pf_hid, st, m->pf_kpart, m->pf_kpart_floats),
                    "gemm_attn_output");
+        if (L.moe) {
+            // Moe::forward at batch n (src/model.rs:598-601) and the add (:602)
+            HYQ_LAUNCH(launch_rms_rows(m->pf_hid, L.ffn_norm, n, H, c.rms_eps, m->pf_xn, st),
+                       "rms_rows");
+            int rc = moe_ffn_rows(st, *L.moe, m->pf_xn, n, m->pf_moe, m->pf_hid, m->pf_hid);
+            if (rc) return rc;
+        } else {
         HYQ_LAUNCH(launch_norm_to_f16(m->pf_hid, n, H, L.ffn_norm, c.rms_eps, m->pf_xh,
                                       m->pf_rs, st),
                    "norm_to_f16");
@@ -504,6 +564,7 @@ int enqueue_prefill_chunk(hyq_dense *m, int n)
         HYQ_LAUNCH(launch_gemm_f16(L.down->dtype, L.down->view, F, m->pf_xh, m->pf_rs, n,
                                    m->pf_hid, m->pf_hid, st, m->pf_kpart, m->pf_kpart_floats),
                    "gemm_down");
+        }
         if (trace)
             HYQ_HIP(hipMemcpyAsync(m->trace + (size_t)(l + 1) * rows, m->pf_hid, rows * 4,
                                    hipMemcpyDeviceToDevice, st),
@@ -521,8 +582,11 @@ int enqueue_prefill_chunk(hyq_dense *m, int n)
 int ready(hyq_dense *m)
 {
     if (m->poisoned) return fail(HYQ_EINVAL, "session was invalidated by a failed forward");
-    for (size_t l = 0; l < m->layers.size(); ++l)
-        if (!m->layers[l].q) return fail(HYQ_EINVAL, "dense: layer %zu has no weights", l);
+    for (size_t l = 0; l < m->layers.size(); ++l) {
+        const hyq_dense::Layer &L = m->layers[l];
+        if (!L.q) return fail(HYQ_EINVAL, "dense: layer %zu has no weights", l);
+        if (!L.gate && !L.moe) return fail(HYQ_EINVAL, "dense: layer %zu has no FFN", l);
+    }
     if (!m->embedding || !m->output) return fail(HYQ_EINVAL, "dense: output weights not set");
     return HYQ_OK;
 }
@@ -672,13 +736,18 @@ int hyq_dense_set_layer(hyq_dense *m, int layer, const hyq_weight *q, const hyq_
     if (!rc) rc = check_weight(m, k, H, KV, "attn_k");
     if (!rc) rc = check_weight(m, v, H, KV, "attn_v");
     if (!rc) rc = check_weight(m, o, QL, H, "attn_output");
-    if (!rc) rc = check_weight(m, gate, H, F, "ffn_gate");
-    if (!rc) rc = check_weight(m, up, H, F, "ffn_up");
-    if (!rc) rc = check_weight(m, down, F, H, "ffn_down");
+    // no dense FFN: the layer's FFN is an MoE (hyq_dense_set_moe)
+    const bool dense_ffn = gate || up || down;
+    if (dense_ffn) {
+        if (!rc) rc = check_weight(m, gate, H, F, "ffn_gate");
+        if (!rc) rc = check_weight(m, up, H, F, "ffn_up");
+        if (!rc) rc = check_weight(m, down, F, H, "ffn_down");
+    }
     if (rc) return rc;
     if (!(q->dtype == k->dtype && k->dtype == v->dtype))
         return fail(HYQ_EDTYPE, "dense: q/k/v formats differ");
-    if (gate->dtype != up->dtype) return fail(HYQ_EDTYPE, "dense: gate/up formats differ");
+    if (dense_ffn && gate->dtype != up->dtype)
+        return fail(HYQ_EDTYPE, "dense: gate/up formats differ");
     if (!attn_norm || !ffn_norm || !q_norm || !k_norm)
         return fail(HYQ_EINVAL, "dense: null norm vector");
     for (const float *vec : {attn_norm, ffn_norm})
@@ -693,10 +762,101 @@ int hyq_dense_set_layer(hyq_dense *m, int layer, const hyq_weight *q, const hyq_
     L.gate = gate;
     L.up = up;
     L.down = down;
+    if (dense_ffn) {
+        L.moe.reset();
+        L.moe_bias.reset();
+    }
+    m->pf_mem.reset(); // the prefill buffers depend on the layers' FFNs
+    m->pf_cap = 0;
     HYQ_HIP(hipMemcpy(L.attn_norm, attn_norm, H * 4, hipMemcpyHostToDevice), "hipMemcpy");
     HYQ_HIP(hipMemcpy(L.ffn_norm, ffn_norm, H * 4, hipMemcpyHostToDevice), "hipMemcpy");
     HYQ_HIP(hipMemcpy(L.q_norm, q_norm, D * 4, hipMemcpyHostToDevice), "hipMemcpy");
     HYQ_HIP(hipMemcpy(L.k_norm, k_norm, D * 4, hipMemcpyHostToDevice), "hipMemcpy");
+    m->drop_graph();
+    return HYQ_OK;
+}
+
+int hyq_dense_set_architecture(hyq_dense *m, int arch)
+{
+    if (!m) return fail(HYQ_EINVAL, "dense_set_architecture: null decoder");
+    if (arch != HYQ_ARCH_DENSE && arch != HYQ_ARCH_HYV3)
+        return fail(HYQ_EINVAL, "unsupported model architecture %d", arch);
+    m->arch = arch;
+    m->drop_graph();
+    return HYQ_OK;
+}
+
+int hyq_dense_set_moe(hyq_dense *m, int layer, const hyq_moe_config *mc,
+                      const hyq_weight *router, const float *bias, const hyq_weight *gate,
+                      const hyq_weight *up, const hyq_weight *down, const hyq_weight *shared_gate,
+                      const hyq_weight *shared_up, const hyq_weight *shared_down)
+{
+    if (!m || !mc) return fail(HYQ_EINVAL, "dense_set_moe: null argument");
+    const hyq_dense_config &c = m->cfg;
+    if (layer < 0 || layer >= c.layers) return fail(HYQ_EINVAL, "dense: layer %d", layer);
+    if (m->has_moe && (mc->experts != m->moe_cfg.experts || mc->used != m->moe_cfg.used ||
+                       mc->mid != m->moe_cfg.mid || mc->shared_mid != m->moe_cfg.shared_mid))
+        return fail(HYQ_EINVAL, "dense: MoE layers must share one expert shape");
+    if (!bias) return fail(HYQ_EINVAL, "dense: null selection bias");
+    for (int e = 0; e < mc->experts; ++e)
+        if (!std::isfinite(bias[e])) return fail(HYQ_EINVAL, "non-finite normalization/router tensor");
+    DeviceGuard g(m->ctx->device);
+    auto bias_d = std::make_unique<DeviceBuffer>();
+    int rc = mc->experts > 0 ? bias_d->alloc(m->ctx->device, (size_t)mc->experts * 4)
+                             : fail(HYQ_EINVAL, "invalid expert dimensions");
+    if (rc) return rc;
+    auto f = std::make_unique<MoeFfn>();
+    f->router = router;
+    f->bias_d = (const float *)bias_d->ptr;
+    f->gate = gate;
+    f->up = up;
+    f->down = down;
+    f->sgate = shared_gate;
+    f->sup = shared_up;
+    f->sdown = shared_down;
+    f->hidden = c.hidden;
+    f->experts = mc->experts;
+    f->used = mc->used;
+    f->mid = mc->mid;
+    f->smid = mc->shared_mid;
+    f->normalize = mc->normalize;
+    f->scale = mc->scale;
+    if ((rc = moe_ffn_check(*f, m->ctx->device))) return rc;
+    HYQ_HIP(hipMemcpy(bias_d->ptr, bias, (size_t)mc->experts * 4, hipMemcpyHostToDevice),
+            "hipMemcpy(bias)");
+    if (!m->moe_mem) {
+        // the batch-1 temporaries: normalized row, its Q8, the FFN's buffers
+        const size_t H = c.hidden, ng = H / 256;
+        size_t off = 0;
+        auto take = [&](size_t bytes) {
+            const size_t o = off;
+            off += align_up(bytes, 256);
+            return o;
+        };
+        const size_t o_xn = take(H * 4), o_q = take(H), o_s = take(ng * 4);
+        const size_t o_16 = take(H / 4), o_32 = take(H / 8), o_256 = take(ng * 4);
+        const size_t o_row = take(moe_row_bytes(*f));
+        auto mem = std::make_unique<DeviceBuffer>();
+        if ((rc = mem->alloc(m->ctx->device, off))) return rc;
+        uint8_t *b = (uint8_t *)mem->ptr;
+        m->moe_xn = (float *)(b + o_xn);
+        m->moe_q8.q = (int8_t *)(b + o_q);
+        m->moe_q8.s = (float *)(b + o_s);
+        m->moe_q8.sum16 = (int32_t *)(b + o_16);
+        m->moe_q8.sum32 = (int32_t *)(b + o_32);
+        m->moe_q8.sum256 = (int32_t *)(b + o_256);
+        m->moe_q8.n = H;
+        m->moe_row = moe_row_carve(*f, b + o_row);
+        m->moe_mem = std::move(mem);
+    }
+    hyq_dense::Layer &L = m->layers[layer];
+    L.gate = L.up = L.down = nullptr;
+    L.moe = std::move(f);
+    L.moe_bias = std::move(bias_d);
+    m->moe_cfg = *mc;
+    m->has_moe = true;
+    m->pf_mem.reset();
+    m->pf_cap = 0;
     m->drop_graph();
     return HYQ_OK;
 }

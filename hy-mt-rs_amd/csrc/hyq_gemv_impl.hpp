@@ -287,9 +287,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     const int nwaves = blockDim.x >> 6;
     const int row0 = ((blockIdx.x * nwaves + wave) * (64 / SUBL) + rset) * NR;
     // K slice of this workgroup row (kslices > 1: plain mode, f32 input
-    // without norm or partial rows): groups [gbase, gbase + groups)
-    const int gbase = blockIdx.y * groups;
-    const float *xin = a.xin + (size_t)gbase * 256;
+    // without norm or partial rows): groups [gbase, gbase + groups); or the
+    // expert slot of this workgroup row (slot form: whole rows)
+    const int gbase = a.nslots ? 0 : blockIdx.y * groups;
+    const float *xin =
+        a.xin + (a.nslots ? (size_t)blockIdx.y * a.slot_xin_stride : (size_t)gbase * 256);
+    // the slot's expert, first of all loads: the weight addresses need it
+    int slot_e = 0;
+    if (a.slot_expert && a.nslots)
+        slot_e = min(max(a.slot_expert[blockIdx.y], 0), a.slot_experts - 1);
 
     // Resolve each row of this lane to (segment, local row).
     int seg[NR], lrow[NR];
@@ -311,6 +317,21 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     int lrowc[NR];
 #pragma unroll
     for (int i = 0; i < NR; ++i) lrowc[i] = valid[i] ? lrow[i] : 0;
+    // the weight rows the loads read (an expert's rows in a stack)
+    int wrow[NR];
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        wrow[i] = lrowc[i];
+        if (a.slot_expert) {
+            if (a.nslots) {
+                wrow[i] = slot_e * a.rows_total + lrowc[i];
+            } else {
+                const int slot = lrowc[i] / a.slot_rows;
+                const int e = min(max(a.slot_expert[slot], 0), a.slot_experts - 1);
+                wrow[i] = e * a.slot_rows + (lrowc[i] - slot * a.slot_rows);
+            }
+        }
+    }
 
     auto load = [&](Dt &D, const WView &w, int row, int g) {
         if constexpr (H) G::load_half(D, w, row, gbase + g, hh);
@@ -322,8 +343,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
 #pragma unroll
         for (int i = 0; i < NR; ++i) {
             const WView &w = MODE == GEMV_MULTI ? a.seg[seg[i]].w : a.seg[0].w;
-            load(d[i], w, lrowc[i], g);
-            if (MODE == GEMV_SILU) load(d2[i], a.seg[1].w, lrowc[i], g);
+            load(d[i], w, wrow[i], g);
+            if (MODE == GEMV_SILU) load(d2[i], a.seg[1].w, wrow[i], g);
         }
     };
     // The activation row's loads are issued first, then the weights' (which
@@ -381,7 +402,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     Dt dp[P > 0 ? P : 1];
     if (P > 0) {
 #pragma unroll
-        for (int u = 0; u < P; ++u) load(dp[u], a.seg[0].w, lrowc[0], min(gi + GSTEP * u, groups - 1));
+        for (int u = 0; u < P; ++u) load(dp[u], a.seg[0].w, wrow[0], min(gi + GSTEP * u, groups - 1));
     } else {
         load_group(min(gi, groups - 1));
     }
@@ -497,8 +518,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
 #pragma unroll
             for (int i = 0; i < NR; ++i) {
                 const WView &w = MODE == GEMV_MULTI ? a.seg[seg[i]].w : a.seg[0].w;
-                load(dd[i], w, lrowc[i], g);
-                if (MODE == GEMV_SILU) load(dd2[i], a.seg[1].w, lrowc[i], g);
+                load(dd[i], w, wrow[i], g);
+                if (MODE == GEMV_SILU) load(dd2[i], a.seg[1].w, wrow[i], g);
             }
         };
         auto step = [&](const Dt *dc, const Dt *dc2, int g) {
@@ -553,7 +574,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
         } else if (MODE == GEMV_MULTI) {
             a.seg[seg[i]].y[lrow[i]] = v;
         } else {
-            if (a.kslices > 1) {
+            if (a.kslices > 1 || a.nslots) {
                 a.seg[0].y[(size_t)blockIdx.y * a.rows_total + lrow[i]] = v;
             } else {
                 float r = res[0][i];
@@ -641,7 +662,7 @@ template <int F> int launch_gemv_format(int mode, const GemvArgs &a, void *strea
     // With an f32 input stage every workgroup quantizes the whole input row,
     // so fewer, wider workgroups (4 waves) share that work.
     if (a.xin) waves = 4;
-    const int ks = a.kslices > 1 ? a.kslices : 1;
+    const int ks = a.nslots > 0 ? a.nslots : a.kslices > 1 ? a.kslices : 1;
     // wide rows (32 lanes per row, two rows per wave): a plain GEMV of at
     // least 32 groups per row whose 8-lane row-sets would leave most SIMDs
     // without a wave; chosen from the shape alone, for the Q8 and the f32
@@ -658,8 +679,12 @@ template <int F> int launch_gemv_format(int mode, const GemvArgs &a, void *strea
     const int rows_per_block = (wide ? 2 : half ? 4 : 8) * nr * waves;
     // a K split is a plain GEMV of an f32 row without norm, residual or
     // partial-row inputs (each slice writes its own partial row)
-    if (ks > 1 && (mode != GEMV_PLAIN || !a.xin || a.norm || a.residual || a.nsparts || a.nrparts))
+    if ((ks > 1 || a.nslots) &&
+        (mode != GEMV_PLAIN || !a.xin || a.norm || a.residual || a.nsparts || a.nrparts))
         return (int)hipErrorInvalidValue;
+    if (a.slot_expert && (a.slot_experts <= 0 || (!a.nslots && a.slot_rows <= 0)))
+        return (int)hipErrorInvalidValue;
+    if (a.nslots && (a.kslices > 1 || !a.slot_expert)) return (int)hipErrorInvalidValue;
     if (a.nsparts > GEMV_MAX_PARTS || a.nrparts > GEMV_MAX_PARTS) return (int)hipErrorInvalidValue;
     dim3 grid((rows + rows_per_block - 1) / rows_per_block, ks), block(64 * waves);
     // slots, then (input stage) scales, 256/16/32-value sums and group sums of squares

@@ -712,7 +712,7 @@ int hyq_gguf_read_f32(hyq_ctx *ctx, const hyq_gguf *g, const char *name, float *
 } // extern "C"
 
 // ---------------------------------------------------------------------------
-// Model::from_gguf, dense arm (src/model.rs:136-262)
+// Model::from_gguf (src/model.rs:136-262): the hunyuan-dense and hy_v3 arms
 // ---------------------------------------------------------------------------
 namespace {
 
@@ -769,9 +769,8 @@ extern "C" int hyq_dense_from_gguf(hyq_ctx *ctx, const hyq_gguf *g, size_t conte
     if (!arch || !arch->is_str)
         return fail(HYQ_EINVAL, "missing or invalid string metadata general.architecture");
     const std::string prefix = arch->s;
-    if (prefix == "hy_v3")
-        return fail(HYQ_EDTYPE, "hy_v3 (MoE) models are not run by the dense decoder");
-    if (prefix != "hunyuan-dense")
+    const bool hyv3 = prefix == "hy_v3";
+    if (prefix != "hunyuan-dense" && !hyv3)
         return fail(HYQ_EINVAL, "unsupported model architecture %s", prefix.c_str());
     auto integer = [&](const char *suffix, uint64_t *v) {
         return hyq_gguf_meta_u64(g, (prefix + "." + suffix).c_str(), v);
@@ -838,6 +837,7 @@ extern "C" int hyq_dense_from_gguf(hyq_ctx *ctx, const hyq_gguf *g, size_t conte
     hyq_dense *m = nullptr;
     if ((rc = hyq_dense_create(ctx, &cfg, context, &m))) return rc;
     std::unique_ptr<hyq_dense, void (*)(hyq_dense *)> guard(m, hyq_dense_destroy);
+    if (hyv3 && (rc = hyq_dense_set_architecture(m, HYQ_ARCH_HYV3))) return rc;
     Owned own;
     const uint64_t H = hidden, QL = heads * head_dim, KV = kv_heads * head_dim;
     hyq_weight *emb, *outw;
@@ -845,13 +845,14 @@ extern "C" int hyq_dense_from_gguf(hyq_ctx *ctx, const hyq_gguf *g, size_t conte
     if (g->find("output.weight")) {
         if ((rc = matrix(ctx, g, "output.weight", {H, vocab}, own, &outw))) return rc;
     } else {
+        if (hyv3) return fail(HYQ_EINVAL, "HYV3 requires separate output weights");
         outw = emb; // tied (src/model.rs:194-202)
     }
     std::vector<float> onorm;
     if ((rc = norm(ctx, g, "output_norm.weight", H, onorm))) return rc;
     for (uint64_t i = 0; i < layers; ++i) {
         const std::string p = "blk." + std::to_string(i) + ".";
-        hyq_weight *q, *k, *v, *o, *gate, *up, *down;
+        hyq_weight *q, *k, *v, *o, *gate = nullptr, *up = nullptr, *down = nullptr;
         std::vector<float> an, fn, qn, kn;
         if ((rc = norm(ctx, g, p + "attn_norm.weight", H, an)) ||
             (rc = norm(ctx, g, p + "ffn_norm.weight", H, fn)) ||
@@ -860,13 +861,51 @@ extern "C" int hyq_dense_from_gguf(hyq_ctx *ctx, const hyq_gguf *g, size_t conte
             (rc = matrix(ctx, g, p + "attn_v.weight", {H, KV}, own, &v)) ||
             (rc = matrix(ctx, g, p + "attn_output.weight", {QL, H}, own, &o)) ||
             (rc = norm(ctx, g, p + "attn_q_norm.weight", head_dim, qn)) ||
-            (rc = norm(ctx, g, p + "attn_k_norm.weight", head_dim, kn)) ||
-            (rc = matrix(ctx, g, p + "ffn_gate.weight", {H, ffn}, own, &gate)) ||
-            (rc = matrix(ctx, g, p + "ffn_up.weight", {H, ffn}, own, &up)) ||
-            (rc = matrix(ctx, g, p + "ffn_down.weight", {ffn, H}, own, &down)))
+            (rc = norm(ctx, g, p + "attn_k_norm.weight", head_dim, kn)))
+            return rc;
+        // HyV3: every layer after the first has an MoE FFN (src/model.rs:206-235)
+        const bool moe = hyv3 && i > 0;
+        if (!moe && ((rc = matrix(ctx, g, p + "ffn_gate.weight", {H, ffn}, own, &gate)) ||
+                     (rc = matrix(ctx, g, p + "ffn_up.weight", {H, ffn}, own, &up)) ||
+                     (rc = matrix(ctx, g, p + "ffn_down.weight", {ffn, H}, own, &down))))
             return rc;
         if ((rc = hyq_dense_set_layer(m, (int)i, q, k, v, o, gate, up, down, an.data(), fn.data(),
                                       qn.data(), kn.data())))
+            return rc;
+        if (!moe) continue;
+        uint64_t experts, used, mid, shared, gating;
+        float scale;
+        int norm_w;
+        if ((rc = integer("expert_count", &experts)) ||
+            (rc = integer("expert_used_count", &used)) ||
+            (rc = integer("expert_feed_forward_length", &mid)) ||
+            (rc = integer("expert_shared_feed_forward_length", &shared)))
+            return rc;
+        if (!(experts > 0 && used > 0 && used <= experts && mid > 0 && shared > 0) ||
+            experts > 65536 || mid > 0x7fffffff || shared > 0x7fffffff)
+            return fail(HYQ_EINVAL, "invalid expert dimensions");
+        if ((rc = integer("expert_gating_func", &gating))) return rc;
+        if (gating != 2) return fail(HYQ_EINVAL, "HYV3 requires a sigmoid router");
+        hyq_weight *router, *eg, *eu, *ed, *sg, *su, *sd;
+        std::vector<float> bias;
+        if ((rc = matrix(ctx, g, p + "ffn_gate_inp.weight", {H, experts}, own, &router)))
+            return rc;
+        if (router->dtype != HYQ_F32) return fail(HYQ_EINVAL, "HYV3 router must use F32");
+        if ((rc = norm(ctx, g, p + "exp_probs_b", experts, bias)) ||
+            (rc = real("expert_weights_scale", &scale)))
+            return rc;
+        if (!(scale > 0.f)) return fail(HYQ_EINVAL, "invalid expert weight scale");
+        if ((rc = matrix(ctx, g, p + "ffn_gate_exps.weight", {H, mid, experts}, own, &eg)) ||
+            (rc = matrix(ctx, g, p + "ffn_up_exps.weight", {H, mid, experts}, own, &eu)) ||
+            (rc = matrix(ctx, g, p + "ffn_down_exps.weight", {mid, H, experts}, own, &ed)) ||
+            (rc = matrix(ctx, g, p + "ffn_gate_shexp.weight", {H, shared}, own, &sg)) ||
+            (rc = matrix(ctx, g, p + "ffn_up_shexp.weight", {H, shared}, own, &su)) ||
+            (rc = matrix(ctx, g, p + "ffn_down_shexp.weight", {shared, H}, own, &sd)) ||
+            (rc = hyq_gguf_meta_bool(g, (prefix + ".expert_weights_norm").c_str(), &norm_w)))
+            return rc;
+        hyq_moe_config mc{(int)experts, (int)used, (int)mid, (int)shared, norm_w, scale};
+        if ((rc = hyq_dense_set_moe(m, (int)i, &mc, router, bias.data(), eg, eu, ed, sg, su,
+                                    sd)))
             return rc;
     }
     if ((rc = hyq_dense_set_output(m, emb, outw, onorm.data()))) return rc;

@@ -131,6 +131,20 @@ struct GemvArgs {
     const float *rparts;
     int nrparts;
     int parts_stride;
+    // Expert slots (an MoE layer at batch 1): seg[0] (and seg[1]) are stacks
+    // of slot_experts experts, and slot_expert[s] (device memory, clamped
+    // into range) names the expert of slot s. Row form (nslots == 0): launch
+    // row r belongs to slot r / slot_rows and reads row
+    // slot_expert[r / slot_rows] * slot_rows + r % slot_rows of the stack;
+    // it writes output row r. Slot form (nslots > 0; plain, f32 input stage
+    // without norm): workgroup row s is slot s, quantizes its input at
+    // xin + s * slot_xin_stride, reads row slot_expert[s] * rows_total + r
+    // and writes seg[0].y + s * rows_total.
+    const int *slot_expert;
+    int slot_experts;
+    int slot_rows;
+    int nslots;
+    int slot_xin_stride;
 };
 constexpr int GEMV_MAX_PARTS = 4;
 
@@ -216,6 +230,21 @@ int isums_per_group(int fmt);
 int launch_f32_gemv(int fmt, WView w, const WView *up, int cols, const float *x, float *y,
                     void *stream);
 int launch_f32_gemm(int fmt, WView w, int cols, const float *x, int batch, float *y,
+                    void *stream);
+// route (hyq_route.hip): per token the `used` experts in ascending index
+// with their weights, as slot lists [tokens][used] (slot_expert,
+// slot_weight) and, when pair_token is given, the token of each pair.
+int route_max_experts();
+int launch_route(const float *logits, const float *bias, int tokens, int experts, int used,
+                 bool normalize, float scale, int *slot_expert, float *slot_weight,
+                 int *pair_token, void *stream);
+// out[t] = residual[t] + (shared[t] + w_0 ex[t][0] + ...) in that order
+// (without residual: the sum); trace gets a copy when set.
+int launch_ffn_combine(const float *residual, const float *shared, const float *ex,
+                       const float *w, int used, int H, int tokens, float *out, float *trace,
+                       void *stream);
+// rms_norm_into of `rows` rows of width H into y (f32).
+int launch_rms_rows(const float *x, const float *w, int rows, int H, float eps, float *y,
                     void *stream);
 
 } // namespace hyq

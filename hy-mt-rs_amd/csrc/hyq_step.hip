@@ -90,6 +90,9 @@ __global__ __launch_bounds__(256) void rms_norm_q8_kernel(const float *__restric
 }
 
 // ---- RoPE + per-head Q/K RMSNorm + KV append ----
+// The per-head rms_norm follows RoPE in the dense graph and precedes it in
+// hy_v3 (norm_first, src/model.rs:425-446); RoPE keeps each pair's length,
+// so both orders normalise by the same mean square up to rounding.
 // Workgroups [0, heads) rotate and normalise the query heads in place,
 // [heads, heads+kv) the key heads into kcache[pos], [heads+kv, heads+2kv)
 // copy the value heads into vcache[pos]. Lane j owns the NeoX pair
@@ -100,7 +103,7 @@ __global__ void rope_norm_kv_kernel(float *__restrict__ q, const float *__restri
                                     const float *__restrict__ v, const float *__restrict__ qn,
                                     const float *__restrict__ kn,
                                     const float *__restrict__ freq, const int *__restrict__ pos_p,
-                                    int heads, int kvh, int dim, float eps,
+                                    int heads, int kvh, int dim, float eps, int norm_first,
                                     float *__restrict__ kcache, float *__restrict__ vcache)
 {
     const int b = blockIdx.x;
@@ -124,19 +127,30 @@ __global__ void rope_norm_kv_kernel(float *__restrict__ q, const float *__restri
     const float a = src[j], c2 = src[j + half];
     const float ang = (float)pos * freq[j];
     const float cs = cosf(ang), sn = sinf(ang);
-    const float r0 = a * cs - c2 * sn;
-    const float r1 = a * sn + c2 * cs;
+    const float *nw = is_q ? qn : kn;
     // rms_norm over the head (src/model.rs:832-870): scale = 1/sqrt(mean + eps)
     __shared__ float part[4];
-    float ss = wave_sum(r0 * r0 + r1 * r1);
-    if ((j & 63) == 0) part[j >> 6] = ss;
-    __syncthreads();
-    ss = 0.f;
-    for (int i = 0; i < (half + 63) / 64; ++i) ss += part[i];
-    const float scale = 1.0f / sqrtf(ss / (float)dim + eps);
-    const float *nw = is_q ? qn : kn;
-    const float o0 = r0 * scale * nw[j];
-    const float o1 = r1 * scale * nw[j + half];
+    auto head_scale = [&](float u0, float u1) {
+        float ss = wave_sum(u0 * u0 + u1 * u1);
+        if ((j & 63) == 0) part[j >> 6] = ss;
+        __syncthreads();
+        ss = 0.f;
+        for (int i = 0; i < (half + 63) / 64; ++i) ss += part[i];
+        return 1.0f / sqrtf(ss / (float)dim + eps);
+    };
+    float o0, o1;
+    if (norm_first) {
+        const float scale = head_scale(a, c2);
+        const float n0 = a * scale * nw[j], n1 = c2 * scale * nw[j + half];
+        o0 = n0 * cs - n1 * sn;
+        o1 = n0 * sn + n1 * cs;
+    } else {
+        const float r0 = a * cs - c2 * sn;
+        const float r1 = a * sn + c2 * cs;
+        const float scale = head_scale(r0, r1);
+        o0 = r0 * scale * nw[j];
+        o1 = r1 * scale * nw[j + half];
+    }
     if (is_q) {
         q[(size_t)h * dim + j] = o0;
         q[(size_t)h * dim + j + half] = o1;
@@ -179,11 +193,21 @@ __global__ void rope_norm_kv_kernel(float *__restrict__ q, const float *__restri
 // new key (RoPE + norm) and value, appends them to the caches
 // (KvCache::append, src/model.rs:650-669) and uses them from LDS.
 
-// RoPE (NeoX halves j, j+64) of one 128-wide head followed by its rms_norm;
-// lane j of a full wave owns the pair.
+// RoPE (NeoX halves j, j+64) of one 128-wide head and its rms_norm, in the
+// dense order (RoPE first) or the hy_v3 one (norm first); lane j of a full
+// wave owns the pair.
 __device__ __forceinline__ void rope_norm_pair(float a, float c2, float cs, float sn, float n0,
-                                               float n1, float eps, float &o0, float &o1)
+                                               float n1, float eps, bool norm_first, float &o0,
+                                               float &o1)
 {
+    if (norm_first) {
+        const float ss = wave_sum(a * a + c2 * c2);
+        const float scale = 1.0f / sqrtf(ss / (float)ATT_D + eps);
+        const float u0 = a * scale * n0, u1 = c2 * scale * n1;
+        o0 = u0 * cs - u1 * sn;
+        o1 = u0 * sn + u1 * cs;
+        return;
+    }
     const float r0 = a * cs - c2 * sn;
     const float r1 = a * sn + c2 * cs;
     const float ss = wave_sum(r0 * r0 + r1 * r1);
@@ -196,7 +220,7 @@ constexpr int ATT_WAVES = 8;
 constexpr int ATT_THREADS = 64 * ATT_WAVES;
 
 __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(
-    bool rope, const float *__restrict__ q, const float *__restrict__ knew,
+    bool rope, bool norm_first, const float *__restrict__ q, const float *__restrict__ knew,
     const float *__restrict__ vnew, const float *__restrict__ qn, const float *__restrict__ kn,
     const float *__restrict__ freq, float eps, float *__restrict__ kcache,
     float *__restrict__ vcache, const int *__restrict__ pos_p, int heads, int kvh, float scale,
@@ -289,13 +313,13 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(
             const float cs = cosf(ang), sn = sinf(ang);
             if (has_q) {
                 float o0, o1;
-                rope_norm_pair(qa, qb, cs, sn, qn0, qn1, eps, o0, o1);
+                rope_norm_pair(qa, qb, cs, sn, qn0, qn1, eps, norm_first, o0, o1);
                 Qs[wave][lane] = o0;
                 Qs[wave][lane + D / 2] = o1;
             }
             if (pnew >= 0 && wave == 0) {
                 float o0, o1;
-                rope_norm_pair(ka, kb, cs, sn, kn0, kn1, eps, o0, o1);
+                rope_norm_pair(ka, kb, cs, sn, kn0, kn1, eps, norm_first, o0, o1);
                 Kn[lane] = o0;
                 Kn[lane + D / 2] = o1;
                 float *kdst = kcache + (size_t)pos * kvw + (size_t)kh * D;
@@ -597,21 +621,22 @@ int launch_rms_norm_q8(const float *x, const float *w, int n, float eps, float *
 
 int launch_rope_norm_kv(float *q, const float *k, const float *v, const float *qn,
                         const float *kn, const float *freq, const int *pos, int heads, int kvh,
-                        int dim, float eps, float *kcache, float *vcache, void *stream)
+                        int dim, float eps, float *kcache, float *vcache, void *stream,
+                        bool norm_first)
 {
     return launch_rope_norm_kv_rows(q, k, v, qn, kn, freq, pos, 1, heads, kvh, dim, eps, kcache,
-                                    vcache, stream);
+                                    vcache, stream, norm_first);
 }
 
 int launch_rope_norm_kv_rows(float *q, const float *k, const float *v, const float *qn,
                              const float *kn, const float *freq, const int *pos, int n,
                              int heads, int kvh, int dim, float eps, float *kcache,
-                             float *vcache, void *stream)
+                             float *vcache, void *stream, bool norm_first)
 {
     if (n <= 0) return 0;
     hipLaunchKernelGGL(rope_norm_kv_kernel, dim3(heads + 2 * kvh, n), dim3(dim / 2), 0,
                        (hipStream_t)stream, q, k, v, qn, kn, freq, pos, heads, kvh, dim, eps,
-                       kcache, vcache);
+                       (int)norm_first, kcache, vcache);
     return (int)hipGetLastError();
 }
 
@@ -681,7 +706,7 @@ int launch_attention(const float *q, const float *kcache, const float *vcache, c
     const int splits = attention_splits(context), chunk = attention_chunk(context);
     const float scale = 1.0f / sqrtf(128.0f);
     hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(attn_kernel, dim3(splits, kvh), dim3(ATT_THREADS), 0, st, false, q, nullptr,
+    hipLaunchKernelGGL(attn_kernel, dim3(splits, kvh), dim3(ATT_THREADS), 0, st, false, false, q, nullptr,
                        nullptr, nullptr, nullptr, nullptr, 0.f, const_cast<float *>(kcache),
                        const_cast<float *>(vcache), pos, heads, kvh, scale, part, splits, chunk,
                        context);
@@ -708,11 +733,11 @@ int launch_attention_merge(const float *part, int context, int heads, const int 
 int launch_attention_rope(const float *q, const float *k, const float *v, const float *qn,
                           const float *kn, const float *freq, float eps, float *kcache,
                           float *vcache, const int *pos, int context, int heads, int kvh,
-                          float *part, void *stream)
+                          float *part, void *stream, bool norm_first)
 {
     const int splits = attention_splits(context), chunk = attention_chunk(context);
     const float scale = 1.0f / sqrtf(128.0f);
-    hipLaunchKernelGGL(attn_kernel, dim3(splits, kvh), dim3(ATT_THREADS), 0, (hipStream_t)stream, true, q,
+    hipLaunchKernelGGL(attn_kernel, dim3(splits, kvh), dim3(ATT_THREADS), 0, (hipStream_t)stream, true, norm_first, q,
                        k, v, qn, kn, freq, eps, kcache, vcache, pos, heads, kvh, scale, part,
                        splits, chunk, context);
     return (int)hipGetLastError();

@@ -23,14 +23,17 @@ int launch_embed_rows(int fmt, WView w, int cols, const int *tokens, int n, floa
                       void *stream);
 int launch_rms_norm_q8(const float *x, const float *w, int n, float eps, float *y, int8_t *q,
                        float *s, int32_t *s16, int32_t *s32, int32_t *s256, void *stream);
+// norm_first: the hy_v3 order (per-head rms_norm, then RoPE); otherwise the
+// dense one (src/model.rs:425-446).
 int launch_rope_norm_kv(float *q, const float *k, const float *v, const float *qn,
                         const float *kn, const float *freq, const int *pos, int heads, int kvh,
-                        int dim, float eps, float *kcache, float *vcache, void *stream);
+                        int dim, float eps, float *kcache, float *vcache, void *stream,
+                        bool norm_first = false);
 // The same for n tokens of a chunk: rows q[i], k[i], v[i] at position *pos + i.
 int launch_rope_norm_kv_rows(float *q, const float *k, const float *v, const float *qn,
                              const float *kn, const float *freq, const int *pos, int n,
                              int heads, int kvh, int dim, float eps, float *kcache,
-                             float *vcache, void *stream);
+                             float *vcache, void *stream, bool norm_first = false);
 // Attention splits: `chunk` positions each (a multiple of ATT_SUB), at most
 // ATT_MAX_SPLITS; partials are [heads][splits][PART_STRIDE] floats holding
 // (max, exp-sum, -, -, exp-weighted V sum[128]).
@@ -82,7 +85,7 @@ int launch_attention_merge(const float *part, int context, int heads, const int 
 int launch_attention_rope(const float *q, const float *k, const float *v, const float *qn,
                           const float *kn, const float *freq, float eps, float *kcache,
                           float *vcache, const int *pos, int context, int heads, int kvh,
-                          float *part, void *stream);
+                          float *part, void *stream, bool norm_first = false);
 int argmax_partials(int n);
 int launch_argmax(const float *x, int n, float *pv, int *pi, int *token, StepState *st,
                   int *history, void *stream);

@@ -192,6 +192,44 @@ int hyq_moe_experts(hyq_ctx *ctx, const hyq_weight *gate, const hyq_weight *up,
                     const int32_t *pair_token, const int32_t *pair_expert,
                     const float *pair_weight, size_t npairs, float *out);
 
+/* ---- the whole MoE FFN of a HyV3 layer: Moe::forward (src/model.rs:687-726)
+ * ---- */
+typedef struct {
+    int experts;    /* expert_count */
+    int used;       /* expert_used_count */
+    int mid;        /* expert_feed_forward_length */
+    int shared_mid; /* expert_shared_feed_forward_length */
+    int normalize;  /* expert_weights_norm */
+    float scale;    /* expert_weights_scale */
+} hyq_moe_config;
+/* route (src/model.rs:728-767) for `tokens` rows of router logits
+ * [tokens][experts]: stable sigmoid, the `used` largest sigmoid + bias
+ * (IEEE total order, ties to the lower index), weights sigmoid / sum * scale
+ * with the sum of the chosen sigmoids floored at f16's smallest normal when
+ * normalize is set (else sum = 1). Writes tokens * used pairs, token-major
+ * and in ascending expert order within a token: the lists hyq_moe_experts_d
+ * takes. pair_token_d may be null. At most 1024 experts. */
+int hyq_moe_route_d(hyq_ctx *ctx, const float *logits_d, const float *bias_d, size_t tokens,
+                    size_t experts, size_t used, int normalize, float scale,
+                    int32_t *pair_token_d, int32_t *pair_expert_d, float *pair_weight_d);
+/* Moe::forward of x_d [tokens][hidden] (rows already normalised) into out_d
+ * [tokens][hidden]: router [hidden, experts] F32 (its logits by the F32
+ * matmul), route with bias_d [experts] (device), the shared expert
+ * (shared_gate/up [hidden, shared_mid], shared_down [shared_mid, hidden])
+ * seeding the output, then each chosen expert (gate/up [hidden, mid, E],
+ * down [mid, hidden, E]) adding weight * its FFN in ascending expert order.
+ * One token runs the int8 GEMVs of the batch-1 path (src/model.rs:507-510);
+ * more run the f16-MFMA products. Widths must be whole 256-value groups.
+ * scratch_d: 256-byte aligned, hyq_moe_forward_scratch_bytes bytes (0 when
+ * the call is not supported: too many tokens per call). */
+size_t hyq_moe_forward_scratch_bytes(const hyq_moe_config *mc, size_t hidden, size_t tokens);
+int hyq_moe_forward_d(hyq_ctx *ctx, const hyq_moe_config *mc, const hyq_weight *router,
+                      const float *bias_d, const hyq_weight *gate, const hyq_weight *up,
+                      const hyq_weight *down, const hyq_weight *shared_gate,
+                      const hyq_weight *shared_up, const hyq_weight *shared_down,
+                      const float *x_d, size_t tokens, void *scratch_d, size_t scratch_bytes,
+                      float *out_d);
+
 /* decode of rows [row0, row0+nrows) to f32 on the device (Weight::row_into /
  * to_vec, src/quant.rs:99-142). */
 int hyq_dequant_rows_d(hyq_ctx *ctx, const hyq_weight *w, size_t row0, size_t nrows,
@@ -257,11 +295,27 @@ int hyq_dense_create(hyq_ctx *ctx, const hyq_dense_config *cfg, size_t context,
                      hyq_dense **out);
 void hyq_dense_destroy(hyq_dense *m);
 /* Layer weights (borrowed: they must outlive the decoder) and f32 norm vectors
- * (copied), as Model::from_gguf binds them (src/model.rs:204-258). */
+ * (copied), as Model::from_gguf binds them (src/model.rs:204-258). gate, up
+ * and down may all be null for a layer whose FFN is an MoE
+ * (hyq_dense_set_moe). */
 int hyq_dense_set_layer(hyq_dense *m, int layer, const hyq_weight *q, const hyq_weight *k,
                         const hyq_weight *v, const hyq_weight *o, const hyq_weight *gate,
                         const hyq_weight *up, const hyq_weight *down, const float *attn_norm,
                         const float *ffn_norm, const float *q_norm, const float *k_norm);
+/* Model::from_gguf's architecture (src/model.rs:137-142): hunyuan-dense
+ * normalises q and k per head after RoPE, hy_v3 before it (:425-446). */
+enum { HYQ_ARCH_DENSE = 0, HYQ_ARCH_HYV3 = 1 };
+int hyq_dense_set_architecture(hyq_dense *m, int arch);
+/* Ffn::Moe of one layer (src/model.rs:82-92, :206-235): the layer's FFN
+ * becomes Moe::forward (see hyq_moe_forward_d for the weights' shapes) with
+ * the selection bias `bias` [experts] (host, copied); hyq_dense_set_layer's
+ * gate/up/down are then null for that layer. Every MoE layer of a decoder
+ * shares one hyq_moe_config shape (the expert_* metadata is model-wide).
+ * Weights are borrowed. */
+int hyq_dense_set_moe(hyq_dense *m, int layer, const hyq_moe_config *mc,
+                      const hyq_weight *router, const float *bias, const hyq_weight *gate,
+                      const hyq_weight *up, const hyq_weight *down, const hyq_weight *shared_gate,
+                      const hyq_weight *shared_up, const hyq_weight *shared_down);
 /* token_embd / output (tied when the same weight, src/model.rs:194-202). */
 int hyq_dense_set_output(hyq_dense *m, const hyq_weight *embedding, const hyq_weight *output,
                          const float *output_norm);
@@ -362,11 +416,14 @@ int hyq_gguf_upload(hyq_ctx *ctx, const hyq_gguf *g, const char *name, hyq_weigh
 int hyq_gguf_read_f32(hyq_ctx *ctx, const hyq_gguf *g, const char *name, float *out, size_t n);
 /* SHA-256 (FIPS 180-4), the digest the AUTO profile checks. */
 int hyq_sha256(const uint8_t *bytes, size_t len, uint8_t digest[32]);
-/* Model::from_gguf, dense arm (src/model.rs:136-262) + Model::new_session's
- * context check (:264-270): reads the hunyuan-dense configuration, checks
+/* Model::from_gguf (src/model.rs:136-262) + Model::new_session's context
+ * check (:264-270): reads the hunyuan-dense or hy_v3 configuration, checks
  * every tensor's shape, uploads the weights (owned by the decoder) and the
- * norm vectors. vocab = the length of tokenizer.ggml.tokens. hy_v3 (MoE)
- * files return HYQ_EDTYPE. */
+ * norm vectors. vocab = the length of tokenizer.ggml.tokens. A hy_v3 file
+ * gets the hy_v3 Q/K-norm order and, for every layer after the first, its
+ * MoE FFN (expert_* metadata, sigmoid gating required, F32 router
+ * ffn_gate_inp, bias exp_probs_b, ffn_{gate,up,down}_exps expert stacks,
+ * ffn_{gate,up,down}_shexp shared expert) and needs a separate output. */
 int hyq_dense_from_gguf(hyq_ctx *ctx, const hyq_gguf *g, size_t context, hyq_dense **out);
 
 #ifdef __cplusplus

@@ -80,6 +80,7 @@ def _declare(L: ctypes.CDLL) -> None:
                                               ctypes.c_int]),
         "hyqo_output_logits": (None, [P, P, ctypes.c_int, P, ctypes.c_int]),
         "hyqo_argmax": (ctypes.c_int, [P, SZ]),
+        "hyqo_moe_forward": (None, [P, SZ, P, SZ, P, ctypes.c_int, ctypes.c_int]),
         "hyqo_max_threads": (ctypes.c_int, []),
     }
     for name, (res, args) in sig.items():
@@ -247,7 +248,34 @@ class _Model(ctypes.Structure):
                 ("dtype_embed", ctypes.c_int), ("dtype_down", ctypes.c_int), ("embed", P), ("output", P), ("output_norm", P),
                 ("wq", P), ("wk", P), ("wv", P), ("wo", P), ("wgate", P), ("wup", P),
                 ("wdown", P), ("attn_norm", P), ("ffn_norm", P), ("q_norm", P),
-                ("k_norm", P)]
+                ("k_norm", P), ("arch", ctypes.c_int), ("moe", P)]
+
+
+class _Moe(ctypes.Structure):
+    _fields_ = [("experts", ctypes.c_int), ("used", ctypes.c_int), ("mid", ctypes.c_int),
+                ("shared_mid", ctypes.c_int), ("normalize", ctypes.c_int),
+                ("scale", ctypes.c_float), ("dtype_gate", ctypes.c_int),
+                ("dtype_down", ctypes.c_int), ("dtype_shared", ctypes.c_int),
+                ("dtype_shared_down", ctypes.c_int), ("router", P), ("bias", P), ("gate", P),
+                ("up", P), ("down", P), ("sgate", P), ("sup", P), ("sdown", P)]
+
+
+def moe_struct(e: dict) -> _Moe:
+    """The oracle's hyqo_moe for a synthetic MoE FFN (tests/synth.py)."""
+    return _Moe(e["experts"], e["used"], e["mid"], e["shared_mid"], int(e["normalize"]),
+                e["scale"], e["dtype_gate"], e["dtype_down"], e["dtype_shared"],
+                e["dtype_shared_down"], _p(e["router"]), _p(e["bias"]), _p(e["gate"]),
+                _p(e["up"]), _p(e["down"]), _p(e["sgate"]), _p(e["sup"]), _p(e["sdown"]))
+
+
+def moe_forward(e: dict, hidden: int, x: np.ndarray, n: int, int8_path: bool,
+                threads: int = 0) -> np.ndarray:
+    """Moe::forward (src/model.rs:687-726) of n rows."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(n * hidden, np.float32)
+    st = moe_struct(e)
+    lib().hyqo_moe_forward(ctypes.byref(st), hidden, _p(x), n, _p(out), int(int8_path), threads)
+    return out.reshape(n, hidden)
 
 
 class DenseOracle:
@@ -261,9 +289,14 @@ class DenseOracle:
         self._arrays = []
 
         def ptrs(key):
-            arr = (P * len(L))(*[_p(layer[key]) for layer in L])
+            arr = (P * len(L))(*[_p(layer[key]) if key in layer else None for layer in L])
             self._arrays.append(arr)
             return ctypes.cast(arr, P)
+
+        self._moe = [moe_struct(layer["moe"]) if "moe" in layer else None for layer in L]
+        moe_arr = (P * len(L))(*[ctypes.addressof(m) if m is not None else None
+                                 for m in self._moe])
+        self._arrays.append(moe_arr)
 
         self.m = _Model(c["layers"], c["hidden"], c["heads"], c["kv_heads"], c["head_dim"],
                         c["ffn"], c["vocab"], c["rope_base"], c["rms_eps"], model["linear"],
@@ -273,7 +306,7 @@ class DenseOracle:
                         _p(model["output_norm"]),
                         ptrs("q"), ptrs("k"), ptrs("v"), ptrs("o"), ptrs("gate"), ptrs("up"),
                         ptrs("down"), ptrs("attn_norm"), ptrs("ffn_norm"), ptrs("q_norm"),
-                        ptrs("k_norm"))
+                        ptrs("k_norm"), model.get("arch", 0), ctypes.cast(moe_arr, P))
 
     def step(self, kcache: np.ndarray, vcache: np.ndarray, pos: int, token: int,
              int8_path: bool, threads: int = 0) -> np.ndarray:

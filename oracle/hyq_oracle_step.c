@@ -144,6 +144,91 @@ static void linear(const hyqo_model *m, int dtype, const uint8_t *w, size_t rows
     (void)m;
 }
 
+/* DenseFfn::forward at batch 1 on the int8 path (src/model.rs:487-501):
+ * silu(gate x) * (up x) from Q8 inputs, then down of the product's Q8. */
+static void ffn_int8(int dtype_gu, int dtype_down, const uint8_t *gate, const uint8_t *up,
+                     const uint8_t *down, size_t hidden, size_t mid, const float *x, float *out)
+{
+    float *g = (float *)malloc(sizeof(float) * mid);
+    float *u = (float *)malloc(sizeof(float) * mid);
+    gemv_int8(dtype_gu, gate, mid, hidden, x, g);
+    gemv_int8(dtype_gu, up, mid, hidden, x, u);
+    for (size_t i = 0; i < mid; ++i) {
+        float v = g[i];
+        g[i] = (v / (1.0f + expf(-v))) * u[i];
+    }
+    gemv_int8(dtype_down, down, hidden, mid, g, out);
+    free(g);
+    free(u);
+}
+
+/* DenseFfn::forward (src/model.rs:672-685) on f32 activations: batch 1
+ * through matmul_gate_up_silu, batch n through two matmuls and silu(g) * u. */
+static void ffn_f32(int dtype_gu, int dtype_down, const uint8_t *gate, const uint8_t *up,
+                    const uint8_t *down, size_t hidden, size_t mid, const float *x, size_t n,
+                    float *out, int threads)
+{
+    float *g = (float *)malloc(sizeof(float) * n * mid);
+    if (n == 1) {
+        hyqo_gate_up_silu(dtype_gu, gate, up, mid, hidden, x, g, threads);
+    } else {
+        float *u = (float *)malloc(sizeof(float) * n * mid);
+        hyqo_matmul(dtype_gu, gate, mid, hidden, x, n, g, threads);
+        hyqo_matmul(dtype_gu, up, mid, hidden, x, n, u, threads);
+        for (size_t i = 0; i < n * mid; ++i) g[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
+        free(u);
+    }
+    hyqo_matmul(dtype_down, down, hidden, mid, g, n, out, threads);
+    free(g);
+}
+
+void hyqo_moe_forward(const hyqo_moe *e, size_t hidden, const float *x, size_t n, float *out,
+                      int int8_path, int threads)
+{
+    size_t E = (size_t)e->experts, U = (size_t)e->used, mid = (size_t)e->mid;
+    /* router.matmul (F32, src/model.rs:691) and route per token (:692-698);
+     * assignments in token order per expert */
+    float *logits = (float *)malloc(sizeof(float) * n * E);
+    hyqo_matmul(0 /* F32 */, (const uint8_t *)e->router, E, hidden, x, n, logits, threads);
+    int32_t *pt = (int32_t *)malloc(sizeof(int32_t) * n * U);
+    int32_t *pe = (int32_t *)malloc(sizeof(int32_t) * n * U);
+    float *pw = (float *)malloc(sizeof(float) * n * U);
+    for (size_t t = 0; t < n; ++t) {
+        hyqo_route(logits + t * E, e->bias, E, U, e->normalize, e->scale, pe + t * U, pw + t * U);
+        for (size_t k = 0; k < U; ++k) pt[t * U + k] = (int32_t)t;
+    }
+    /* output = shared.forward(input, batch) (:699) */
+    if (int8_path && n == 1)
+        ffn_int8(e->dtype_shared, e->dtype_shared_down, e->sgate, e->sup, e->sdown, hidden,
+                 (size_t)e->shared_mid, x, out);
+    else
+        ffn_f32(e->dtype_shared, e->dtype_shared_down, e->sgate, e->sup, e->sdown, hidden,
+                (size_t)e->shared_mid, x, n, out, threads);
+    /* experts in ascending order, out[t] += w * ffn (:700-722) */
+    if (int8_path && n == 1) {
+        size_t gb = mid * (size_t)hyqo_block_bytes(e->dtype_gate) * hidden /
+                    (size_t)hyqo_block_len(e->dtype_gate);
+        size_t db = hidden * (size_t)hyqo_block_bytes(e->dtype_down) * mid /
+                    (size_t)hyqo_block_len(e->dtype_down);
+        float *res = (float *)malloc(sizeof(float) * hidden);
+        for (size_t ex = 0; ex < E; ++ex)
+            for (size_t k = 0; k < U; ++k) {
+                if ((size_t)pe[k] != ex) continue;
+                ffn_int8(e->dtype_gate, e->dtype_down, e->gate + ex * gb, e->up + ex * gb,
+                         e->down + ex * db, hidden, mid, x, res);
+                for (size_t i = 0; i < hidden; ++i) out[i] += pw[k] * res[i];
+            }
+        free(res);
+    } else {
+        hyqo_moe_experts(e->dtype_gate, e->dtype_down, e->gate, e->up, e->down, E, hidden, mid,
+                         x, n, pt, pe, pw, n * U, out, threads);
+    }
+    free(logits);
+    free(pt);
+    free(pe);
+    free(pw);
+}
+
 int hyqo_layer_step(const hyqo_model *m, int l, float *hidden, float *kc, float *vc, size_t ctx,
                     size_t pos, int int8_path, int threads)
 {
@@ -166,18 +251,28 @@ int hyqo_layer_step(const hyqo_model *m, int l, float *hidden, float *kc, float 
     linear(m, m->dtype_linear, m->wq[l], qlen, H, xn, q, int8_path, threads);
     linear(m, m->dtype_linear, m->wk[l], kvw, H, xn, k, int8_path, threads);
     linear(m, m->dtype_linear, m->wv[l], kvw, H, xn, v, int8_path, threads);
-    /* dense order: RoPE, then per-head Q/K RMSNorm (src/model.rs:425-446) */
+    /* per-head Q/K RMSNorm before RoPE (hy_v3) or after it (dense)
+     * (src/model.rs:425-446) */
+    if (m->arch == 1) {
+        hyqo_rms_norm_rows(q, m->q_norm[l], qlen, D, m->eps);
+        hyqo_rms_norm_rows(k, m->k_norm[l], kvw, D, m->eps);
+    }
     hyqo_rope(q, (size_t)m->heads, D, cos_s, sin_s);
     hyqo_rope(k, (size_t)m->kv_heads, D, cos_s, sin_s);
-    hyqo_rms_norm_rows(q, m->q_norm[l], qlen, D, m->eps);
-    hyqo_rms_norm_rows(k, m->k_norm[l], kvw, D, m->eps);
+    if (m->arch != 1) {
+        hyqo_rms_norm_rows(q, m->q_norm[l], qlen, D, m->eps);
+        hyqo_rms_norm_rows(k, m->k_norm[l], kvw, D, m->eps);
+    }
     memcpy(kc + pos * kvw, k, sizeof(float) * kvw);
     memcpy(vc + pos * kvw, v, sizeof(float) * kvw);
     hyqo_attention(q, kc, vc, (size_t)m->heads, (size_t)m->kv_heads, D, pos + 1, att);
     linear(m, m->dtype_linear, m->wo[l], H, qlen, att, proj, int8_path, threads);
     for (size_t i = 0; i < H; ++i) hidden[i] += proj[i];
     hyqo_rms_norm_into(hidden, m->ffn_norm[l], H, m->eps, xn);
-    if (int8_path) {
+    if (m->moe && m->moe[l]) {
+        /* Ffn::Moe (src/model.rs:507-510) */
+        hyqo_moe_forward(m->moe[l], H, xn, 1, proj, int8_path, threads);
+    } else if (int8_path) {
         gemv_int8(m->dtype_linear, m->wgate[l], F, H, xn, gate);
         gemv_int8(m->dtype_linear, m->wup[l], F, H, xn, up);
         for (size_t i = 0; i < F; ++i) {
@@ -188,7 +283,8 @@ int hyqo_layer_step(const hyqo_model *m, int l, float *hidden, float *kc, float 
     } else {
         hyqo_gate_up_silu(m->dtype_linear, m->wgate[l], m->wup[l], F, H, xn, gate, threads);
     }
-    linear(m, m->dtype_down, m->wdown[l], H, F, gate, proj, int8_path, threads);
+    if (!(m->moe && m->moe[l]))
+        linear(m, m->dtype_down, m->wdown[l], H, F, gate, proj, int8_path, threads);
     for (size_t i = 0; i < H; ++i) hidden[i] += proj[i];
 
     free(xn);
@@ -253,13 +349,19 @@ int hyqo_prefill_layer(const hyqo_model *m, int l, float *hidden, float *kc, flo
     hyqo_matmul(m->dtype_linear, m->wv[l], kvw, H, xn, n, v, threads);
     /* rope at start + token (src/model.rs:570-583, 919-947), then the dense
      * order's per-head norms (:584-587) */
+    if (m->arch == 1) {
+        hyqo_rms_norm_rows(q, m->q_norm[l], n * qlen, D, m->eps);
+        hyqo_rms_norm_rows(k, m->k_norm[l], n * kvw, D, m->eps);
+    }
     for (size_t t = 0; t < n; ++t) {
         hyqo_rope_tables(D, m->rope_base, pos + t, cos_s, sin_s);
         hyqo_rope(q + t * qlen, (size_t)m->heads, D, cos_s, sin_s);
         hyqo_rope(k + t * kvw, (size_t)m->kv_heads, D, cos_s, sin_s);
     }
-    hyqo_rms_norm_rows(q, m->q_norm[l], n * qlen, D, m->eps);
-    hyqo_rms_norm_rows(k, m->k_norm[l], n * kvw, D, m->eps);
+    if (m->arch != 1) {
+        hyqo_rms_norm_rows(q, m->q_norm[l], n * qlen, D, m->eps);
+        hyqo_rms_norm_rows(k, m->k_norm[l], n * kvw, D, m->eps);
+    }
     /* cache.append (:588-593, 650-669), then causal attention: token t sees
      * positions 0..=pos+t (src/model.rs:956-961) */
     memcpy(kc + pos * kvw, k, sizeof(float) * n * kvw);
@@ -273,13 +375,18 @@ int hyqo_prefill_layer(const hyqo_model *m, int l, float *hidden, float *kc, flo
      * silu(g) * u, down */
     memcpy(xn, hidden, sizeof(float) * n * H);
     hyqo_rms_norm_rows(xn, m->ffn_norm[l], n * H, H, m->eps);
-    hyqo_matmul(m->dtype_linear, m->wgate[l], F, H, xn, n, gate, threads);
-    hyqo_matmul(m->dtype_linear, m->wup[l], F, H, xn, n, up, threads);
-    for (size_t i = 0; i < n * F; ++i) {
-        float g = gate[i];
-        gate[i] = (g / (1.0f + expf(-g))) * up[i];
+    if (m->moe && m->moe[l]) {
+        /* Moe::forward at batch n (src/model.rs:598-601) */
+        hyqo_moe_forward(m->moe[l], H, xn, n, proj, 0, threads);
+    } else {
+        hyqo_matmul(m->dtype_linear, m->wgate[l], F, H, xn, n, gate, threads);
+        hyqo_matmul(m->dtype_linear, m->wup[l], F, H, xn, n, up, threads);
+        for (size_t i = 0; i < n * F; ++i) {
+            float g = gate[i];
+            gate[i] = (g / (1.0f + expf(-g))) * up[i];
+        }
+        hyqo_matmul(m->dtype_down, m->wdown[l], H, F, gate, n, proj, threads);
     }
-    hyqo_matmul(m->dtype_down, m->wdown[l], H, F, gate, n, proj, threads);
     for (size_t i = 0; i < n * H; ++i) hidden[i] += proj[i];
 
     free(xn);

@@ -9,8 +9,26 @@
 extern "C" {
 #endif
 
-/* Weights of a dense Hunyuan model (src/model.rs:49-76), packed GGUF bytes.
- * The embedding doubles as the output matrix (tied, src/model.rs:194-202). */
+/* The MoE FFN of a HyV3 layer (src/model.rs:82-92, :206-235): an F32 router
+ * [experts][hidden] with its selection bias, expert stacks gate/up
+ * [experts][mid][hidden] and down [experts][hidden][mid] (GGUF bytes, expert
+ * after expert) and the shared expert's gate/up [shared_mid][hidden] and
+ * down [hidden][shared_mid]. */
+typedef struct {
+    int experts, used, mid, shared_mid, normalize;
+    float scale;
+    int dtype_gate, dtype_down, dtype_shared, dtype_shared_down;
+    const float *router;
+    const float *bias;
+    const uint8_t *gate, *up, *down;
+    const uint8_t *sgate, *sup, *sdown;
+} hyqo_moe;
+
+/* Weights of a Hunyuan model (src/model.rs:49-76), packed GGUF bytes. The
+ * embedding doubles as the output matrix when output is NULL (tied, dense
+ * only, src/model.rs:194-202). arch 0 is hunyuan-dense, 1 is hy_v3 (Q/K
+ * norms before RoPE, src/model.rs:425-446); moe[l] is layer l's MoE FFN or
+ * NULL for a dense FFN (moe itself may be NULL). */
 typedef struct {
     int layers, hidden, heads, kv_heads, head_dim, ffn, vocab;
     float rope_base, eps;
@@ -22,7 +40,17 @@ typedef struct {
     const uint8_t *const *wq, *const *wk, *const *wv, *const *wo;
     const uint8_t *const *wgate, *const *wup, *const *wdown;
     const float *const *attn_norm, *const *ffn_norm, *const *q_norm, *const *k_norm;
+    int arch;
+    const hyqo_moe *const *moe;
 } hyqo_model;
+
+/* Moe::forward (src/model.rs:687-726) for n rows x [n][hidden]: router
+ * matmul, route, shared expert, then the experts in ascending order,
+ * out[t] += w * ffn_e(x_t); out [n][hidden] is written. With int8_path and
+ * n == 1 every quantized product takes the int8 path; otherwise the f32
+ * products of the reference's x86 arm. */
+void hyqo_moe_forward(const hyqo_moe *e, size_t hidden, const float *x, size_t n, float *out,
+                      int int8_path, int threads);
 
 void hyqo_rms_norm_into(const float *x, const float *w, size_t n, float eps, float *out);
 void hyqo_rms_norm_rows(float *x, const float *w, size_t total, size_t wlen, float eps);

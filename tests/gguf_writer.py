@@ -97,3 +97,71 @@ def dense_model_file(model: dict, linear_id: int, embed_id: int = 14, file_type:
                     (p + "ffn_up.weight", [H, F], linear_id, L["up"].tobytes()),
                     (p + "ffn_down.weight", [F, H], linear_id, L["down"].tobytes())]
     return build(meta, tensors)
+
+
+def hyv3_model_file(model: dict, linear_id: int = 12, embed_id: int = 14, expert_id: int = 12,
+                    shared_id: int = 8, context_length: int = 4096,
+                    gating: int = 2, drop: str | None = None,
+                    router_f16: bool = False) -> bytes:
+    """A hy_v3 GGUF of a synthetic model (tests/synth.py:make_hyv3_model):
+    layer 0 with a dense FFN, later layers with an F32 router, the
+    exp_probs_b bias, expert stacks and a shared expert; `drop` leaves out
+    one tensor by name; router_f16 stores the routers as F16 (type 1)."""
+    c = model["cfg"]
+    a = "hy_v3"
+    moe = next(L["moe"] for L in model["layers"] if "moe" in L)
+    meta = [("general.architecture", STR, a),
+            (f"{a}.block_count", U32, c["layers"]), (f"{a}.embedding_length", U32, c["hidden"]),
+            (f"{a}.attention.head_count", U32, c["heads"]),
+            (f"{a}.attention.head_count_kv", U32, c["kv_heads"]),
+            (f"{a}.attention.key_length", U32, c["head_dim"]),
+            (f"{a}.attention.value_length", U32, c["head_dim"]),
+            (f"{a}.context_length", U32, context_length),
+            (f"{a}.rope.freq_base", F32, c["rope_base"]),
+            (f"{a}.attention.layer_norm_rms_epsilon", F32, c["rms_eps"]),
+            (f"{a}.feed_forward_length", U32, c["ffn"]),
+            (f"{a}.expert_count", U32, moe["experts"]),
+            (f"{a}.expert_used_count", U32, moe["used"]),
+            (f"{a}.expert_feed_forward_length", U32, moe["mid"]),
+            (f"{a}.expert_shared_feed_forward_length", U32, moe["shared_mid"]),
+            (f"{a}.expert_gating_func", U32, gating),
+            (f"{a}.expert_weights_scale", F32, moe["scale"]),
+            (f"{a}.expert_weights_norm", BOOL, bool(moe["normalize"])),
+            ("tokenizer.ggml.model", STR, "gpt2"),
+            ("tokenizer.ggml.tokens", ARR, (STR, [f"t{i}" for i in range(c["vocab"])]))]
+    H, F, D = c["hidden"], c["ffn"], c["head_dim"]
+    QL, KV = c["heads"] * D, c["kv_heads"] * D
+    f32 = lambda v: np.ascontiguousarray(v, np.float32).tobytes()
+    tensors = [("token_embd.weight", [H, c["vocab"]], embed_id, model["embed"].tobytes()),
+               ("output_norm.weight", [H], 0, f32(model["output_norm"])),
+               ("output.weight", [H, c["vocab"]], embed_id, model["output"].tobytes())]
+    for i, L in enumerate(model["layers"]):
+        p = f"blk.{i}."
+        tensors += [(p + "attn_norm.weight", [H], 0, f32(L["attn_norm"])),
+                    (p + "ffn_norm.weight", [H], 0, f32(L["ffn_norm"])),
+                    (p + "attn_q.weight", [H, QL], linear_id, L["q"].tobytes()),
+                    (p + "attn_k.weight", [H, KV], linear_id, L["k"].tobytes()),
+                    (p + "attn_v.weight", [H, KV], linear_id, L["v"].tobytes()),
+                    (p + "attn_output.weight", [QL, H], linear_id, L["o"].tobytes()),
+                    (p + "attn_q_norm.weight", [D], 0, f32(L["q_norm"])),
+                    (p + "attn_k_norm.weight", [D], 0, f32(L["k_norm"]))]
+        if "moe" not in L:
+            tensors += [(p + "ffn_gate.weight", [H, F], linear_id, L["gate"].tobytes()),
+                        (p + "ffn_up.weight", [H, F], linear_id, L["up"].tobytes()),
+                        (p + "ffn_down.weight", [F, H], linear_id, L["down"].tobytes())]
+            continue
+        e = L["moe"]
+        E, M, S = e["experts"], e["mid"], e["shared_mid"]
+        router = (("ffn_gate_inp.weight", [H, E], 1, e["router"].astype(np.float16).tobytes())
+                  if router_f16 else ("ffn_gate_inp.weight", [H, E], 0, f32(e["router"])))
+        tensors += [(p + router[0], router[1], router[2], router[3]),
+                    (p + "exp_probs_b", [E], 0, f32(e["bias"])),
+                    (p + "ffn_gate_exps.weight", [H, M, E], expert_id, e["gate"].tobytes()),
+                    (p + "ffn_up_exps.weight", [H, M, E], expert_id, e["up"].tobytes()),
+                    (p + "ffn_down_exps.weight", [M, H, E], expert_id, e["down"].tobytes()),
+                    (p + "ffn_gate_shexp.weight", [H, S], shared_id, e["sgate"].tobytes()),
+                    (p + "ffn_up_shexp.weight", [H, S], shared_id, e["sup"].tobytes()),
+                    (p + "ffn_down_shexp.weight", [S, H], shared_id, e["sdown"].tobytes())]
+    if drop is not None:
+        tensors = [t for t in tensors if t[0] != drop]
+    return build(meta, tensors)

@@ -120,6 +120,39 @@ def make_dense_model(cfg: dict, linear: int = Q2_0C, embed: int = Q6_K, seed: in
                 output_norm=rng.normal(1, 0.02, H).astype(np.float32))
 
 
+def make_hyv3_model(cfg: dict, moe: dict, linear: int = Q4_K, expert: int = Q4_K,
+                    shared: int = Q8_0, embed: int = Q6_K, seed: int = 0) -> dict:
+    """A synthetic hy_v3 model (src/model.rs:136-262): layer 0 keeps a dense
+    FFN of width cfg["ffn"], every later layer an MoE FFN of `moe`'s shape
+    (experts, used, mid, shared_mid, normalize, scale) with an F32 router
+    ~ N(0, 1/sqrt(hidden)) (router logits ~ N(0, 1)), a selection bias
+    ~ N(0, 0.1), Q4_K expert stacks and a Q8_0 shared expert; a separate
+    output matrix (HyV3 requires one, src/model.rs:194-201)."""
+    model = make_dense_model(cfg, linear=linear, embed=embed, seed=seed)
+    model["arch"] = 1
+    H, V = cfg["hidden"], cfg["vocab"]
+    E, mid, smid = moe["experts"], moe["mid"], moe["shared_mid"]
+    model["output"] = random_matrix(embed, V, H, seed * 1000 + 998)
+    rng = np.random.default_rng(seed + 777)
+    for l in range(1, cfg["layers"]):
+        L = model["layers"][l]
+        for k in ("gate", "up", "down"):
+            del L[k]
+        s = seed * 1000 + l * 10 + 500
+        L["moe"] = dict(
+            moe, dtype_gate=expert, dtype_down=expert, dtype_shared=shared,
+            dtype_shared_down=shared,
+            router=(rng.normal(0, 1, (E, H)) / np.sqrt(H)).astype(np.float32),
+            bias=rng.normal(0, 0.1, E).astype(np.float32),
+            gate=random_matrix(expert, E * mid, H, s + 1),
+            up=random_matrix(expert, E * mid, H, s + 2),
+            down=random_matrix(expert, E * H, mid, s + 3),
+            sgate=random_matrix(shared, smid, H, s + 4),
+            sup=random_matrix(shared, smid, H, s + 5),
+            sdown=random_matrix(shared, H, smid, s + 6))
+    return model
+
+
 def make_kv_cache(cfg: dict, context: int, prefilled: int, seed: int = 0):
     """f32 K/V caches [layers][context][kv_heads*head_dim], N(0,1) up to prefilled."""
     rng = np.random.default_rng(seed + 12345)
@@ -158,5 +191,47 @@ def load_dense(hyq, ctx, model: dict, context: int):
     O = E
     if "output" in model:
         O = ctx.upload(model["embed_dtype"], model["output"], (H, c["vocab"]))
+    dec.set_output(E, O, model["output_norm"])
+    return dec
+
+
+def upload_moe(hyq, ctx, moe: dict, hidden: int):
+    """A synthetic MoE FFN (make_hyv3_model's layer["moe"]) as a hyq.MoeFfn."""
+    E, mid, smid = moe["experts"], moe["mid"], moe["shared_mid"]
+    cfg = hyq.MoeConfig(E, moe["used"], mid, smid, int(moe["normalize"]), moe["scale"])
+    router = ctx.upload(F32, moe["router"].view(np.uint8).reshape(-1), (hidden, E))
+    g = ctx.upload(moe["dtype_gate"], moe["gate"], (hidden, mid, E))
+    u = ctx.upload(moe["dtype_gate"], moe["up"], (hidden, mid, E))
+    d = ctx.upload(moe["dtype_down"], moe["down"], (mid, hidden, E))
+    sg = ctx.upload(moe["dtype_shared"], moe["sgate"], (hidden, smid))
+    su = ctx.upload(moe["dtype_shared"], moe["sup"], (hidden, smid))
+    sd = ctx.upload(moe["dtype_shared_down"], moe["sdown"], (smid, hidden))
+    return hyq.MoeFfn(ctx, cfg, router, moe["bias"], g, u, d, sg, su, sd)
+
+
+def load_hyv3(hyq, ctx, model: dict, context: int):
+    """Upload a synthetic hy_v3 model (make_hyv3_model) into a decoder."""
+    c = model["cfg"]
+    cfg = hyq.DenseConfig(c["layers"], c["hidden"], c["heads"], c["kv_heads"], c["head_dim"],
+                          c["ffn"], c["vocab"], c["rope_base"], c["rms_eps"])
+    dec = hyq.DenseDecoder(ctx, cfg, context)
+    dec.set_architecture(hyq.ARCH_HYV3)
+    H, F, D = c["hidden"], c["ffn"], c["head_dim"]
+    QL, KV = c["heads"] * D, c["kv_heads"] * D
+    lin = model["linear"]
+    for l, L in enumerate(model["layers"]):
+        W = dict(q=ctx.upload(lin, L["q"], (H, QL)), k=ctx.upload(lin, L["k"], (H, KV)),
+                 v=ctx.upload(lin, L["v"], (H, KV)), o=ctx.upload(lin, L["o"], (QL, H)))
+        if "moe" in L:
+            W.update(gate=None, up=None, down=None)
+        else:
+            W.update(gate=ctx.upload(lin, L["gate"], (H, F)), up=ctx.upload(lin, L["up"], (H, F)),
+                     down=ctx.upload(model.get("down_dtype", lin), L["down"], (F, H)))
+        dec.set_layer(l, W["q"], W["k"], W["v"], W["o"], W["gate"], W["up"], W["down"],
+                      L["attn_norm"], L["ffn_norm"], L["q_norm"], L["k_norm"])
+        if "moe" in L:
+            dec.set_moe(l, upload_moe(hyq, ctx, L["moe"], H))
+    E = ctx.upload(model["embed_dtype"], model["embed"], (H, c["vocab"]))
+    O = ctx.upload(model["embed_dtype"], model["output"], (H, c["vocab"]))
     dec.set_output(E, O, model["output_norm"])
     return dec

@@ -82,6 +82,58 @@ def test_dense_from_gguf_errors(gpu_ctx, hyq, tmp_path):
                                                             b"blk.1.ffn_dowX.weight")
     with pytest.raises(ValueError, match="missing tensor blk.1.ffn_down.weight"):
         hyq.DenseDecoder.from_gguf(gpu_ctx, hyq.Gguf(data=bad, profile="tencent-q2-0c"), 8)
-    moe = build([("general.architecture", STR, "hy_v3"), ("hy_v3.block_count", U32, 1)], [])
-    with pytest.raises(ValueError, match="hy_v3"):
-        hyq.DenseDecoder.from_gguf(gpu_ctx, hyq.Gguf(data=moe), 8)
+    other = build([("general.architecture", STR, "llama"), ("llama.block_count", U32, 1)], [])
+    with pytest.raises(ValueError, match="unsupported model architecture llama"):
+        hyq.DenseDecoder.from_gguf(gpu_ctx, hyq.Gguf(data=other), 8)
+
+
+HYV3_SMALL = dict(layers=3, hidden=512, heads=4, kv_heads=1, head_dim=128, ffn=1024, vocab=3000,
+                  rope_base=11158840.0, rms_eps=1e-5)
+MOE_SMALL = dict(experts=16, used=4, mid=512, shared_mid=768, normalize=True, scale=2.5)
+
+
+def test_hyv3_decoder_from_gguf_equals_manual_load(gpu_ctx, hyq, tmp_path):
+    """Model::from_gguf's hy_v3 arm (src/model.rs:136-262): a dense first
+    layer, MoE layers after it, a separate output; prefill and decoding
+    bit-identical to the decoder assembled by hand from the same model."""
+    from gguf_writer import hyv3_model_file
+    from synth import Q8_0, load_hyv3, make_hyv3_model
+    model = make_hyv3_model(HYV3_SMALL, MOE_SMALL, linear=Q4_K, expert=Q4_K, shared=Q8_0,
+                            seed=23)
+    path = tmp_path / "hyv3.gguf"
+    path.write_bytes(hyv3_model_file(model))
+    g = hyq.Gguf(str(path))
+    context = 64
+    a = hyq.DenseDecoder.from_gguf(gpu_ctx, g, context)
+    b = load_hyv3(hyq, gpu_ctx, model, context)
+    tokens = np.random.default_rng(4).integers(0, HYV3_SMALL["vocab"], 20).astype(np.int32)
+    la, ta = a.prefill(tokens)
+    lb, tb = b.prefill(tokens)
+    assert ta == tb and np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    sa, sb = a.generate(ta, 6), b.generate(tb, 6)
+    assert np.array_equal(sa, sb)
+    _print("hy_v3 from_gguf tokens", sa)
+    a.close()
+    b.close()
+    g.close()
+
+
+@pytest.mark.parametrize("case,match", [
+    ("gating", "sigmoid router"), ("no_output", "separate output"),
+    ("no_bias", "missing tensor blk.1.exp_probs_b"), ("f16_router", "router must use F32")])
+def test_hyv3_from_gguf_errors(gpu_ctx, hyq, case, match):
+    """The hy_v3 arm's ensure! rules (src/model.rs:199-226)."""
+    from gguf_writer import hyv3_model_file
+    from synth import Q8_0, make_hyv3_model
+    model = make_hyv3_model(dict(HYV3_SMALL, layers=2), MOE_SMALL, linear=Q4_K, expert=Q4_K,
+                            shared=Q8_0, seed=24)
+    if case == "gating":
+        data = hyv3_model_file(model, gating=1)
+    elif case == "no_output":
+        data = hyv3_model_file(model, drop="output.weight")
+    elif case == "no_bias":
+        data = hyv3_model_file(model, drop="blk.1.exp_probs_b")
+    else:
+        data = hyv3_model_file(model, router_f16=True)
+    with pytest.raises(ValueError, match=match):
+        hyq.DenseDecoder.from_gguf(gpu_ctx, hyq.Gguf(data=data), 16)

@@ -1,0 +1,190 @@
+"""GPU parity of the HyV3 (MoE) arm against the oracle: route
+(src/model.rs:728-767), Moe::forward (:687-726) as one device entry point at
+batch 1 and batch n, and the decoder with MoE layers (forward_into's MoE call
+site, :507-510 and :598-601) with the hy_v3 Q/K-norm order (:425-446).
+
+Bars: expert selections equal; route weights within 2 f32 ulps (the GPU's
+expf and glibc's differ by an ulp); a batch-1 MoE FFN within 1e-4 relative
+unless one of its Q8 inputs hit a rounding midpoint (a flip moves one int8
+code, ~6e-4 of a product; at most one such case per test); an f16-MFMA batch
+within 2e-3; decoder layers teacher-forced as in test_gpu_c3.py."""
+import numpy as np
+import pytest
+
+from synth import Q4_K, Q8_0, make_hyv3_model, make_kv_cache, load_hyv3, upload_moe
+
+pytestmark = pytest.mark.gpu
+
+
+def _print(*a):
+    print(*a, flush=True)
+
+
+def _rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+@pytest.mark.parametrize("experts,used,normalize", [(64, 8, True), (64, 8, False),
+                                                    (160, 6, True), (7, 7, True),
+                                                    (1024, 16, True)])
+def test_route_matches_oracle(gpu_ctx, hyq, oracle, experts, used, normalize):
+    tokens = 37
+    rng = np.random.default_rng(experts + used)
+    logits = rng.normal(0, 1, (tokens, experts)).astype(np.float32)
+    bias = rng.normal(0, 0.1, experts).astype(np.float32)
+    # ties: equal keys must fall back to the lower index
+    logits[3, :] = 0.5
+    bias_t = bias.copy()
+    logits[4, :4] = [1.0, 1.0, -30.0, -31.0]  # tiny sigmoids, the floored sum
+    pt, pe, pw = hyq.moe_route(gpu_ctx, logits, bias, used, normalize, 2.826)
+    for t in range(tokens):
+        ref = sorted(oracle.route(logits[t], bias_t, used, normalize, 2.826))
+        sl = slice(t * used, (t + 1) * used)
+        assert list(pt[sl]) == [t] * used
+        assert list(pe[sl]) == [e for e, _ in ref], t
+        w = np.array([v for _, v in ref], np.float32)
+        assert np.allclose(pw[sl], w, rtol=3e-7, atol=0), (t, pw[sl], w)
+    # all-equal logits and bias: the lowest indices, in order
+    flat = np.zeros((1, experts), np.float32)
+    _, pe, _ = hyq.moe_route(gpu_ctx, flat, np.zeros(experts, np.float32), used, normalize, 1.0)
+    assert list(pe) == list(range(used))
+
+
+MOE_C5 = dict(experts=64, used=8, mid=1536, shared_mid=1536, normalize=True, scale=2.5)
+HYV3 = dict(layers=3, hidden=2048, heads=16, kv_heads=4, head_dim=128, ffn=6144, vocab=8192,
+            rope_base=11158840.0, rms_eps=1e-5)
+
+
+def _moe_model(moe, seed):
+    return make_hyv3_model(dict(HYV3, layers=2), moe, linear=Q4_K, expert=Q4_K, shared=Q8_0,
+                           seed=seed)
+
+
+def test_moe_forward_one_token(gpu_ctx, hyq, oracle):
+    """Moe::forward of single rows (the decode step's int8 GEMVs) at the
+    30B-A3B-style shape: 64 Q4_K experts of width 1536, top 8, a Q8_0
+    shared expert."""
+    model = _moe_model(MOE_C5, seed=2)
+    e = model["layers"][1]["moe"]
+    H = HYV3["hidden"]
+    ffn = upload_moe(hyq, gpu_ctx, e, H)
+    errs = []
+    for s in range(4):
+        x = np.random.default_rng(s).normal(0, 1, (1, H)).astype(np.float32)
+        got = ffn.forward(x)
+        ref = oracle.moe_forward(e, H, x, 1, int8_path=True)
+        errs.append(_rel(got, ref))
+    _print("moe batch-1 rel", ["%.1e" % v for v in errs])
+    assert max(errs) <= 2e-3, errs
+    assert sum(v > 1e-4 for v in errs) <= 1, errs
+
+
+@pytest.mark.parametrize("n", [5, 64])
+def test_moe_forward_batch(gpu_ctx, hyq, oracle, n):
+    """n rows: F32 router GEMM, route, the shared expert and the grouped
+    expert kernels (f16 MFMA) against the oracle's f32 products."""
+    moe = dict(MOE_C5, experts=32, mid=512, shared_mid=1024)
+    model = _moe_model(moe, seed=3)
+    e = model["layers"][1]["moe"]
+    H = HYV3["hidden"]
+    ffn = upload_moe(hyq, gpu_ctx, e, H)
+    x = np.random.default_rng(n).normal(0, 1, (n, H)).astype(np.float32)
+    got = ffn.forward(x)
+    ref = oracle.moe_forward(e, H, x, n, int8_path=False)
+    rel = _rel(got, ref)
+    _print(f"moe batch {n} rel {rel:.2e}")
+    assert rel <= 2e-3
+
+
+def _teacher_forced(ref, dec, cfg, pos, logits, label):
+    tr = dec.trace(1)[:, 0]
+    errs = []
+    for l in range(cfg["layers"]):
+        kc, vc = dec.read_kv(l, pos + 1)
+        kref = np.zeros((pos + 1, kc.shape[1]), np.float32)
+        vref = kref.copy()
+        kref[:pos] = kc[:pos]
+        vref[:pos] = vc[:pos]
+        out = ref.layer(l, tr[l], kref, vref, pos, int8_path=True)
+        errs.append(max(_rel(tr[l + 1], out), _rel(kc[pos], kref[pos]),
+                        _rel(vc[pos], vref[pos])))
+    errs.append(_rel(logits, ref.output(tr[-1], int8_path=True)))
+    _print(label, "per-layer rel (last: logits)", ["%.1e" % e for e in errs])
+    assert max(errs) <= 2e-3, (label, errs)
+    assert sum(e > 1e-4 for e in errs) <= max(1, len(errs) // 4), (label, errs)
+
+
+def test_hyv3_decoder_matches_oracle(gpu_ctx, hyq, oracle):
+    """Three layers (a dense one, then two MoE layers of 64 experts) at the
+    30B-A3B-style shapes, cache pre-filled to 700 of 768 positions; four
+    tokens checked layer by layer and free-running; the graph replay of the
+    same steps gives the same tokens."""
+    cfg = HYV3
+    context, prefilled = 768, 700
+    model = make_hyv3_model(cfg, MOE_C5, linear=Q4_K, expert=Q4_K, shared=Q8_0, seed=4)
+    dec = load_hyv3(hyq, gpu_ctx, model, context)
+    k, v = make_kv_cache(cfg, context, prefilled, seed=4)
+    for l in range(cfg["layers"]):
+        dec.load_kv(l, k[l, :prefilled], v[l, :prefilled])
+    dec.position = prefilled
+    k0, v0 = k.copy(), v.copy()
+    ref = oracle.DenseOracle(model)
+    dec.set_trace(1)
+    token, toks = 11, []
+    for i in range(4):
+        pos = prefilled + i
+        logits, nxt = dec.forward(token)
+        _teacher_forced(ref, dec, cfg, pos, logits, f"hyv3 step {i}")
+        ref_logits = ref.step(k, v, pos, token, int8_path=True)
+        rel = _rel(logits, ref_logits)
+        _print(f"hyv3 step {i}: free-running logits rel {rel:.2e}")
+        assert rel <= 5e-3, (i, rel)
+        top = np.sort(ref_logits)[-2:]
+        if top[1] - top[0] > 1e-3 * np.abs(ref_logits).max():
+            assert nxt == int(np.argmax(ref_logits))
+        toks.append(nxt)
+        token = nxt
+    dec.set_trace(None)
+    for l in range(cfg["layers"]):
+        dec.load_kv(l, k0[l, :prefilled], v0[l, :prefilled])
+    dec.position = prefilled
+    assert list(dec.generate(11, 4, use_graph=True)) == toks
+    dec.close()
+
+
+def test_hyv3_prefill_matches_oracle(gpu_ctx, hyq, oracle):
+    """hyq_dense_prefill of 120 tokens through a HyV3 model (32 experts of
+    width 512, top 8): every layer's rows against the oracle's batch-n layer
+    on the GPU's inputs (f16-MFMA bar), the logits at the decode bar."""
+    cfg = dict(HYV3, vocab=4096)
+    moe = dict(MOE_C5, experts=32, mid=512, shared_mid=1024)
+    context, prefilled, n = 512, 40, 120
+    model = make_hyv3_model(cfg, moe, linear=Q4_K, expert=Q4_K, shared=Q8_0, seed=5)
+    dec = load_hyv3(hyq, gpu_ctx, model, context)
+    k, v = make_kv_cache(cfg, context, prefilled, seed=5)
+    for l in range(cfg["layers"]):
+        dec.load_kv(l, k[l, :prefilled], v[l, :prefilled])
+    dec.position = prefilled
+    ref = oracle.DenseOracle(model)
+    dec.set_trace(n)
+    toks = np.random.default_rng(n).integers(0, cfg["vocab"], n).astype(np.int32)
+    logits, _ = dec.prefill(toks)
+    tr = dec.trace(n)
+    errs = []
+    for l in range(cfg["layers"]):
+        kc, vc = dec.read_kv(l, prefilled + n)
+        kref = np.zeros((prefilled + n, kc.shape[1]), np.float32)
+        vref = kref.copy()
+        kref[:prefilled] = kc[:prefilled]
+        vref[:prefilled] = vc[:prefilled]
+        out = ref.prefill_layer(l, tr[l], kref, vref, prefilled).reshape(n, -1)
+        errs.append(_rel(tr[l + 1], out))
+        assert _rel(kc[prefilled:], kref[prefilled:]) <= 2e-3, (l, "K rows")
+    lerr = _rel(logits, ref.output(tr[-1, -1], int8_path=True))
+    _print("hyv3 prefill per-layer rel", ["%.1e" % e for e in errs], "logits %.1e" % lerr)
+    assert max(errs) <= 2e-3, errs
+    assert lerr <= 2e-3, lerr
+    dec.set_trace(None)
+    dec.close()

@@ -298,3 +298,114 @@ def test_layer_pieces_compose_to_the_step(oracle, int8):
     assert np.array_equal(ref.output(h[-1], int8_path=int8).view(np.uint32),
                           logits.view(np.uint32))
     assert np.array_equal(k1, k2) and np.array_equal(v1, v2)
+
+
+# ---- the MoE FFN and the hy_v3 order ----
+
+HYV3_SMALL = dict(layers=2, hidden=512, heads=4, kv_heads=1, head_dim=128, ffn=1024, vocab=3000,
+                  rope_base=11158840.0, rms_eps=1e-5)
+MOE_SMALL = dict(experts=8, used=2, mid=256, shared_mid=512, normalize=True, scale=2.5)
+
+
+def _hyv3(seed=0, **kw):
+    from synth import Q4_K, Q8_0, make_hyv3_model
+    moe = dict(MOE_SMALL, **kw)
+    return make_hyv3_model(HYV3_SMALL, moe, linear=Q4_K, expert=Q4_K, shared=Q8_0, seed=seed)
+
+
+def _ffn64(oracle, dg, dd, g, u, d, hidden, mid, x):
+    """f64 DenseFfn::forward of rows x over golden-pinned decoded weights."""
+    G = oracle.decode(dg, g).reshape(mid, hidden).astype(np.float64)
+    U = oracle.decode(dg, u).reshape(mid, hidden).astype(np.float64)
+    D = oracle.decode(dd, d).reshape(hidden, mid).astype(np.float64)
+    a, b = x @ G.T, x @ U.T
+    return ((a / (1.0 + np.exp(-a))) * b) @ D.T
+
+
+def _moe64(oracle, e, hidden, x):
+    """Moe::forward (src/model.rs:687-726) in f64 from pinned pieces: the F32
+    router product, route (pinned above), the shared expert and each chosen
+    expert's FFN, added in ascending expert order."""
+    x64 = x.astype(np.float64)
+    logits = (x64 @ e["router"].astype(np.float64).T).astype(np.float32)
+    out = _ffn64(oracle, e["dtype_shared"], e["dtype_shared_down"], e["sgate"], e["sup"],
+                 e["sdown"], hidden, e["shared_mid"], x64)
+    E, mid = e["experts"], e["mid"]
+    gb, db = e["gate"].size // E, e["down"].size // E
+    for t in range(x.shape[0]):
+        for ex, w in sorted(oracle.route(logits[t], e["bias"], e["used"], e["normalize"],
+                                         e["scale"])):
+            out[t] += w * _ffn64(oracle, e["dtype_gate"], e["dtype_down"],
+                                 e["gate"][ex * gb:(ex + 1) * gb], e["up"][ex * gb:(ex + 1) * gb],
+                                 e["down"][ex * db:(ex + 1) * db], hidden, mid, x64[t:t + 1])[0]
+    return out
+
+
+@pytest.mark.parametrize("n", [1, 6])
+def test_moe_forward_matches_f64_chain(oracle, n):
+    model = _hyv3(seed=3)
+    e = model["layers"][1]["moe"]
+    H = HYV3_SMALL["hidden"]
+    x = np.random.default_rng(n).normal(0, 1, (n, H)).astype(np.float32)
+    ref = _moe64(oracle, e, H, x)
+    got = oracle.moe_forward(e, H, x, n, int8_path=False)
+    assert _rel(got, ref) <= 2e-6, _rel(got, ref)
+    if n == 1:
+        # the int8 arm: every product from Q8 activations (~1/127 of a value)
+        q = oracle.moe_forward(e, H, x, 1, int8_path=True)
+        assert 1e-5 < _rel(q, ref) <= 3e-2, _rel(q, ref)
+
+
+def test_moe_forward_single_expert_identity(oracle):
+    """One expert, used 1, normalised: the weight is sigmoid/sigmoid * scale =
+    scale exactly, so with scale 1 the output is shared(x) + expert(x) - the
+    same f32 operations as two dense FFNs (in both arms)."""
+    model = _hyv3(seed=4, experts=1, used=1, scale=1.0)
+    e = model["layers"][1]["moe"]
+    H = HYV3_SMALL["hidden"]
+    x = np.random.default_rng(9).normal(0, 1, (1, H)).astype(np.float32)
+    from synth import Q4_K, Q8_0
+    for int8 in (False, True):
+        got = oracle.moe_forward(e, H, x, 1, int8_path=int8)
+        sh = oracle.moe_forward(dict(e, scale=1e-30), H, x, 1, int8_path=int8)  # ~shared only
+        ex = got - sh
+        ref = _ffn64(oracle, Q4_K, Q4_K, e["gate"], e["up"], e["down"], H, e["mid"],
+                     x.astype(np.float64))
+        assert _rel(ex, ref) <= (3e-2 if int8 else 1e-5), int8
+        shref = _ffn64(oracle, Q8_0, Q8_0, e["sgate"], e["sup"], e["sdown"], H,
+                       e["shared_mid"], x.astype(np.float64))
+        assert _rel(sh, shref) <= (3e-2 if int8 else 1e-5), int8
+
+
+@pytest.mark.parametrize("arch", [0, 1])
+def test_qk_norm_order_by_architecture(oracle, arch):
+    """hy_v3 normalises q and k per head before RoPE, hunyuan-dense after it
+    (src/model.rs:425-446): the K row the layer appends equals an f64
+    restatement of the chosen order, and not of the other one."""
+    model = _hyv3(seed=5)
+    model["arch"] = arch
+    c = HYV3_SMALL
+    ref = oracle.DenseOracle(model)
+    H, D, pos = c["hidden"], 128, 7
+    kc = np.zeros((16, D), np.float32)
+    vc = np.zeros((16, D), np.float32)
+    h = np.random.default_rng(1).normal(0, 1, H).astype(np.float32)
+    ref.layer(0, h, kc, vc, pos, int8_path=False)
+    L = model["layers"][0]
+    xn = h.astype(np.float64) / np.sqrt(np.mean(h.astype(np.float64) ** 2) + 1e-5)
+    xn = xn * L["attn_norm"]
+    k = oracle.decode(model["linear"], L["k"]).reshape(D, H).astype(np.float64) @ xn
+    freq = np.float32(c["rope_base"]) ** (-2.0 * np.arange(64, dtype=np.float64) / 128)
+    ang = pos * freq.astype(np.float32).astype(np.float64)
+    cs, sn = np.cos(ang), np.sin(ang)
+
+    def rope(v):
+        return np.concatenate([v[:64] * cs - v[64:] * sn, v[:64] * sn + v[64:] * cs])
+
+    def norm(v):
+        return v / np.sqrt(np.mean(v ** 2) + 1e-5) * L["k_norm"]
+
+    exp = rope(norm(k)) if arch == 1 else norm(rope(k))
+    other = norm(rope(k)) if arch == 1 else rope(norm(k))
+    assert _rel(kc[pos], exp) <= 1e-5
+    assert _rel(kc[pos], other) > 1e-3
