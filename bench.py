@@ -15,24 +15,31 @@ Also reported, from live HIP-event timings on the context stream:
                   attention output and, as three K slices, for the down
                   projection), launched alone through the C ABI as the very
                   instantiation the step launches, on the attention-output
-                  shape [2048 x 2048], weights rotated over 512 MiB and inputs
+                  shape [2048 x 2048], weights rotated over 1 GiB and inputs
                   over 64 rows so that both come from HBM:
                   algorithmic bytes per launch / average launch time; `traffic`
                   is the counter-measured HBM bytes per launch of the same
                   kernel (profiles/*_traffic.json);
   step_hbm        the bytes a token streams (weights + KV cache) / time per token;
   device_copy_GBs (in roofline) a 1 GiB device-to-device copy's read + write
-                  bytes / time, the practical HBM ceiling beside the peak;
+                  bytes / time;
+  read_ceiling_GBs (in roofline) a read-only stream of a 2 GiB buffer: the
+                  practical ceiling of the HBM-bound (read-dominated) kernels;
   decode_kernels  the step's other kernels timed the same way;
   gemv            GB/s of every matrix of the GEMV workloads (Q4_K [6144x2048];
-                  the 1.8B Q2_0C/STQ1_0 set; Q6_K lm_head), Q8 input, weights
-                  rotated over >= 512 MiB;
+                  the 1.8B Q2_0C/STQ1_0 set; Q6_K lm_head; the 7B shapes), Q8
+                  input, weights rotated over >= 1 GiB of distinct copies:
+                  back-to-back launches, and (graph_GBs) one HIP graph that
+                  launches every copy once;
   prefill, moe    the batched f16-MFMA GEMM (TFLOP/s) and the MoE expert layer;
   prefill_1p8b    the same model's chunked prefill of a 1024-token prompt
                   (hyq_dense_prefill), wall-clock tok/s;
   cpu_baseline    the reference's x86 decode step (f32 activations, scalar
                   Q2_0C row dot, AVX2 dot; oracle/hyq_oracle_step.c), timed on
-                  this host's cores on a bounded sample of the same workload.
+                  this host's cores (median of 5 tokens after 2 warm-ups);
+  cpu_baselines   the same restatement on every other workload (C1/C2 GEMVs,
+                  a 256-row sample of each C4 GEMM, the C5 MoE layer), with the
+                  host's CPU model and core count.
 """
 from __future__ import annotations
 
@@ -66,6 +73,23 @@ class Events:
         self.hip = ctypes.CDLL("libamdhip64.so.7")
         self.stream = ctypes.c_void_p(stream)
 
+    def graph_ms(self, fn, n: int, replays: int = 10) -> float:
+        """Captures fn(0) .. fn(n-1) (launches on the stream) into one HIP
+        graph and returns the average ms per replay of it (after one untimed
+        replay): back-to-back launches with no host work between them."""
+        h = self.hip
+        graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
+        assert h.hipStreamSynchronize(self.stream) == 0
+        assert h.hipStreamBeginCapture(self.stream, 1) == 0  # thread-local mode
+        for i in range(n):
+            fn(i)
+        assert h.hipStreamEndCapture(self.stream, ctypes.byref(graph)) == 0
+        assert h.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+        ms = self.time_ms(lambda i: h.hipGraphLaunch(exe, self.stream), replays)
+        h.hipGraphExecDestroy(exe)
+        h.hipGraphDestroy(graph)
+        return ms
+
     def _ev(self):
         e = ctypes.c_void_p()
         assert self.hip.hipEventCreate(ctypes.byref(e)) == 0
@@ -87,11 +111,16 @@ class Events:
         return ms.value / iters
 
 
-def gemv_rate(hyq, ctx, ev, dtype, rows, cols, seed=1, min_bytes=512 << 20):
-    """Standalone int8 GEMV: (us per launch, algorithmic GB/s), HBM-resident."""
+ROTATE_BYTES = 1 << 30  # distinct weight copies per measurement: 4x the 256 MB MALL
+
+
+def gemv_rate(hyq, ctx, ev, dtype, rows, cols, seed=1, min_bytes=ROTATE_BYTES):
+    """Standalone int8 GEMV with Q8 input over >= 1 GiB of distinct weight
+    copies: (us per launch, algorithmic GB/s) from back-to-back launches, and
+    the aggregate GB/s of one HIP graph that launches every copy once."""
     from synth import random_matrix
     base = random_matrix(dtype, rows, cols, seed=seed)
-    copies = int(min(1024, max(2, np.ceil(min_bytes / base.size))))
+    copies = int(min(2048, max(2, np.ceil(min_bytes / base.size))))
     Ws = [ctx.upload(dtype, base, (cols, rows)) for _ in range(copies)]
     x = np.random.default_rng(seed).normal(0, 1, cols).astype(np.float32)
     q8 = ctx.q8(cols)
@@ -103,11 +132,28 @@ def gemv_rate(hyq, ctx, ev, dtype, rows, cols, seed=1, min_bytes=512 << 20):
     def launch(i):
         L.hyq_gemv_q8_d(ctx.handle, Ws[i % copies].handle, q8.handle, None, y.ptr)
 
-    ms = ev.time_ms(launch, max(64, 4 * copies))
+    ms = ev.time_ms(launch, max(64, 2 * copies))
+    gms = ev.graph_ms(launch, copies)
     alg = base.size + cols + 4 * (cols // 256) + 4 * rows
     for W in Ws:
         W.release()
-    return ms * 1e3, alg / (ms * 1e-3) / 1e9
+    return ms * 1e3, alg / (ms * 1e-3) / 1e9, alg * copies / (gms * 1e-3) / 1e9, copies
+
+
+def read_ceiling(hyq, ctx, ev, nbytes=2 << 30):
+    """The read-only HBM rate: one 2 GiB buffer (8x the MALL) read once per
+    launch by the streaming kernel, best over workgroup counts."""
+    L = hyq.lib()
+    buf = ctx.empty(nbytes, np.uint8)
+    sink = ctx.empty(1 << 16, np.float32)
+    best = None
+    for wgs in (1024, 2048, 4096, 8192):
+        ms = ev.time_ms(lambda i: L.hyq_hbm_read_d(ctx.handle, buf.ptr, nbytes, wgs, sink.ptr), 10)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        if best is None or gbs > best["GBs"]:
+            best = dict(bytes=nbytes, workgroups=wgs, ms=round(ms, 4), GBs=round(gbs, 1))
+    buf.free()
+    return best
 
 
 MFMA_F16_PEAK_TFLOPS = 2500.0
@@ -214,7 +260,7 @@ def _upload_rotation(ctx, dtype, blobs, dims, min_bytes):
 def step_kernel_table(hyq, ctx, ev, model, kv, pos):
     """Per-launch time (HIP events on the context stream) of the decode step's
     kernels launched in isolation through the C ABI, each with its operands
-    rotated over more memory than the 256 MB Infinity Cache holds (512 MiB of
+    rotated over more memory than the 256 MB Infinity Cache holds (1 GiB of
     weights, 64 inputs), so that they
     come from HBM as they do in the step (a token streams ~0.8 GB).
 
@@ -229,7 +275,7 @@ def step_kernel_table(hyq, ctx, ev, model, kv, pos):
     rng = np.random.default_rng(1)
     table = {}
 
-    def staged_gemv(name, key, rows, cols, per_step, note, min_bytes=512 << 20, same=True):
+    def staged_gemv(name, key, rows, cols, per_step, note, min_bytes=ROTATE_BYTES, same=True):
         blobs = [model["layers"][l][key] for l in range(c["layers"])]
         Ws = _upload_rotation(ctx, lin, blobs, (cols, rows), min_bytes)
         xs = [ctx.array(rng.normal(0, 1, cols).astype(np.float32)) for _ in range(64)]
@@ -322,7 +368,7 @@ def roofline_loop(hyq, ctx, ev, model, iters):
     QL = c["heads"] * c["head_dim"]
     rng = np.random.default_rng(1)
     blobs = [model["layers"][l]["o"] for l in range(c["layers"])]
-    Ws = _upload_rotation(ctx, model["linear"], blobs, (QL, H), 512 << 20)
+    Ws = _upload_rotation(ctx, model["linear"], blobs, (QL, H), ROTATE_BYTES)
     xs = [ctx.array(rng.normal(0, 1, QL).astype(np.float32)) for _ in range(64)]
     y = ctx.empty(H, np.float32)
     n = len(Ws)
@@ -335,24 +381,123 @@ def roofline_loop(hyq, ctx, ev, model, iters):
     return ms * 1e3
 
 
-def cpu_baseline(model, kv, steps: int):
+def host_cpu() -> dict:
+    """The host's CPU model and the cores this process may use."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return dict(model=model, nproc=len(os.sched_getaffinity(0)))
+
+
+def _median_s(fn, runs: int = 5, warm: int = 2) -> float:
+    """Median wall time of `runs` calls after `warm` untimed ones (the
+    reference's probe warms twice, src/quant.rs:2741-2747)."""
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(runs):
+        t = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t)
+    return float(np.median(ts))
+
+
+def cpu_baselines(model, kv) -> dict:
+    """The reference's x86 path restated in C (oracle/, OpenMP over this
+    host's cores; each figure the median of 5 runs after 2 warm-ups) on the
+    workloads of the GPU figures: the C3 decode step, the C1/C2 GEMVs (f32
+    activations: scalar Q2_0C row dot, decoded-row + AVX2 dot for the other
+    formats), a bounded sample of each C4 GEMM (64-row tile decode + the
+    restatement's AVX2 FMA tile GEMM, and beside it the decoded rows through
+    OpenBLAS's sgemm, numpy's BLAS) and the C5 MoE layer."""
     import oracle as O
+    from synth import Q2_0C, Q4_K, Q6_K, Q8_0, STQ1_0, random_matrix
+    threads = O.lib().hyqo_max_threads()
+    rng = np.random.default_rng(7)
+    out = dict(host=host_cpu(), threads=threads, runs="median of 5 after 2 warm-ups")
+    # C3: one decode token of the 1.8B 2Bit model per run (x86 arm)
     o = O.DenseOracle(model)
     k, v = kv
-    threads = O.lib().hyqo_max_threads()
-    pos = PREFILLED
-    o.step(k, v, pos, 5, int8_path=False)  # warm
-    t = time.perf_counter()
-    tok = 5
-    for i in range(steps):
-        logits = o.step(k, v, pos + 1 + i, tok, int8_path=False)
-        tok = int(np.argmax(logits))
-    dt = time.perf_counter() - t
-    return dict(value=round(steps / dt, 3), unit="tok/s", cores=threads, kind="port",
-                sample=f"{steps} greedy decode tokens at positions {pos + 1}.."
-                       f"{pos + steps} (after 1 warm-up token) of the same synthetic 1.8B "
-                       f"2Bit model and KV cache, x86 path of Model::forward_into "
-                       f"(f32 activations) restated in C, {threads} OpenMP threads")
+    pos = [PREFILLED]
+
+    def step():
+        o.step(k, v, pos[0], 5, int8_path=False)
+        pos[0] = PREFILLED + (pos[0] - PREFILLED + 1) % 8
+    t = _median_s(step)
+    out["C3_decode"] = dict(tok_s=round(1.0 / t, 3), ms=round(t * 1e3, 2),
+                            sample="1 token at positions 1024..1031 per run")
+    # C1 / C2 GEMVs at batch 1
+    gemv = {}
+    for name, (dt_, rows, cols) in {
+        "C1_Q4_K_6144x2048": (Q4_K, 6144, 2048),
+        "C2_Q2_0C_qkv_3072x2048": (Q2_0C, 3072, 2048),
+        "C2_Q2_0C_attn_out_2048x2048": (Q2_0C, 2048, 2048),
+        "C2_Q2_0C_gate_up_12288x2048": (Q2_0C, 12288, 2048),
+        "C2_Q2_0C_down_2048x6144": (Q2_0C, 2048, 6144),
+        "C2_STQ1_0_qkv_3072x2048": (STQ1_0, 3072, 2048),
+        "C2_STQ1_0_attn_out_2048x2048": (STQ1_0, 2048, 2048),
+        "C2_STQ1_0_gate_up_12288x2048": (STQ1_0, 12288, 2048),
+        "C2_STQ1_0_down_2048x6144": (STQ1_0, 2048, 6144),
+        "C2_Q6_K_lm_head_120818x2048": (Q6_K, 120818, 2048),
+    }.items():
+        w = random_matrix(dt_, rows, cols, seed=1)
+        x = rng.normal(0, 1, cols).astype(np.float32)
+        t = _median_s(lambda: O.matmul(dt_, w, rows, cols, x, 1))
+        alg = w.size + 4 * cols + 4 * rows
+        gemv[name] = dict(us=round(t * 1e6, 1), GBs=round(alg / t / 1e9, 2))
+    out["gemv"] = gemv
+    # C4: the first 256 rows of each weight at 512 tokens
+    pre = {}
+    for name, (dt_, rows, cols) in {
+        "C4_Q4_K_gate_up_14336x4096x512": (Q4_K, 14336, 4096),
+        "C4_Q6_K_down_4096x14336x512": (Q6_K, 4096, 14336),
+        "C4_Q4_K_qkv_6144x4096x512": (Q4_K, 6144, 4096),
+    }.items():
+        n = 256
+        w = random_matrix(dt_, n, cols, seed=3)
+        x = rng.normal(0, 1, 512 * cols).astype(np.float32)
+        t = _median_s(lambda: O.matmul(dt_, w, n, cols, x, 512), runs=5, warm=1)
+        # the same work with a BLAS GEMM (the reference's candle GEMM is a
+        # tuned one): decode the rows, then OpenBLAS sgemm through numpy
+        xm = x.reshape(512, cols)
+        tb = _median_s(lambda: xm @ O.decode(dt_, w).reshape(n, cols).T, runs=5, warm=1)
+        pre[name] = dict(GFLOPs=round(2.0 * n * cols * 512 / t / 1e9, 1),
+                         GFLOPs_openblas=round(2.0 * n * cols * 512 / tb / 1e9, 1),
+                         sample=f"rows 0..255 of {rows} at 512 tokens ({t * 1e3:.0f} ms; "
+                                f"decode + OpenBLAS sgemm {tb * 1e3:.0f} ms)")
+    out["prefill"] = pre
+    # C5: the MoE layer (shared Q8_0 projection + 64 tokens x top-8 Q4_K experts)
+    E, U, Hd, M, T = 64, 8, 2048, 1536, 64
+    G = random_matrix(Q4_K, E * M, Hd, 5)
+    Uw = random_matrix(Q4_K, E * M, Hd, 6)
+    D = random_matrix(Q4_K, E * Hd, M, 7)
+    S = random_matrix(Q8_0, Hd, Hd, 8)
+    x = rng.normal(0, 1, T * Hd).astype(np.float32)
+    pt = np.repeat(np.arange(T), U).astype(np.int32)
+    pe = np.concatenate([np.sort(rng.choice(E, U, replace=False)) for _ in range(T)]).astype(
+        np.int32)
+    pw = np.full(T * U, 1.0 / U, np.float32)
+
+    def moe():
+        seed = O.matmul(Q8_0, S, Hd, Hd, x, T).reshape(-1)
+        O.moe_experts(Q4_K, Q4_K, G, Uw, D, E, Hd, M, x, pt, pe, pw, seed)
+    t = _median_s(moe, runs=5, warm=1)
+    out["moe"] = dict(us=round(t * 1e6, 1),
+                      sample="64 tokens, top-8 of 64 Q4_K experts (width 1536) + Q8_0 shared "
+                             "[2048x2048]")
+    out["headline"] = dict(
+        value=out["C3_decode"]["tok_s"], unit="tok/s", cores=threads, kind="port",
+        sample=f"one greedy decode token per run at positions 1024..1031, median of 5 after 2 "
+               f"warm-ups, of the same synthetic 1.8B 2Bit model and KV cache: the x86 path of "
+               f"Model::forward_into (f32 activations) restated in C, {threads} OpenMP threads "
+               f"on {out['host']['nproc']} cores of {out['host']['model']}")
+    return out
 
 
 def main() -> int:
@@ -364,7 +509,6 @@ def main() -> int:
     ap.add_argument("--no-gemv", action="store_true", help="skip the standalone GEMV table")
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the batched (prefill) GEMM table")
-    ap.add_argument("--cpu-steps", type=int, default=3)
     ap.add_argument("--roofline-only", action="store_true",
                     help="run only the roofline kernel loop and a 256 MiB copy (for hardware "
                          "counter runs), print its time and exit")
@@ -423,6 +567,9 @@ def main() -> int:
                     traffic=traffic, algorithmic_bytes=dk["bytes"], avg_us=dk["us"])
     copy = copy_rate(hyq, ctx, ev)
     roofline["device_copy_GBs"] = copy["GBs"]
+    ceiling = read_ceiling(hyq, ctx, ev)
+    roofline["read_ceiling_GBs"] = ceiling["GBs"]
+    log(f"HBM: device copy {copy['GBs']:.0f} GB/s, read-only stream {ceiling['GBs']:.0f} GB/s")
     # the whole step against the same peak: bytes a token streams from HBM
     kvw = cfg["kv_heads"] * cfg["head_dim"]
     mid = PREFILLED + args.warmup + args.steps // 2
@@ -451,10 +598,11 @@ def main() -> int:
             "7B_Q2_0C_gate_up_28672x4096": (Q2_0C, 28672, 4096),
             "7B_STQ1_0_gate_up_28672x4096": (STQ1_0, 28672, 4096),
         }.items():
-            us, gbs = gemv_rate(hyq, ctx, ev, dt_, rows, cols)
+            us, gbs, agg, copies = gemv_rate(hyq, ctx, ev, dt_, rows, cols)
             gemv[name] = dict(us=round(us, 3), GBs=round(gbs, 1),
-                              frac=round(gbs / HBM_PEAK_GBS, 4))
-            log(f"{name}: {us:.2f} us {gbs:.0f} GB/s")
+                              frac=round(gbs / HBM_PEAK_GBS, 4), graph_GBs=round(agg, 1),
+                              graph_frac=round(agg / HBM_PEAK_GBS, 4), copies=copies)
+            log(f"{name}: {us:.2f} us {gbs:.0f} GB/s; graph of {copies} copies {agg:.0f} GB/s")
 
     prefill = {}
     if not args.no_prefill:
@@ -480,10 +628,12 @@ def main() -> int:
         log(f"C5 MoE layer (64 tokens, top-8 of 64 Q4_K experts + Q8_0 shared): "
             f"{moe['us']:.1f} us {moe['GBs']:.0f} GB/s")
 
-    cpu = None
+    cpu, cpus = None, None
     if not args.no_cpu:
-        log("cpu baseline")
-        cpu = cpu_baseline(model, kv, args.cpu_steps)
+        log("cpu baselines")
+        cpus = cpu_baselines(model, kv)
+        cpu = cpus.pop("headline")
+        log(f"cpu: {cpu['value']} tok/s on {cpu['cores']} threads")
 
     out = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1,
@@ -499,6 +649,7 @@ def main() -> int:
                    "graph": use_graph},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "cpu_baselines": cpus,
         "step_hbm": step,
         "decode_kernels": table,
         "gemv": gemv,

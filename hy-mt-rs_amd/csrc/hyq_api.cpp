@@ -684,6 +684,17 @@ int hyq_matmul_noalloc_d(hyq_ctx *ctx, const hyq_weight *w, const float *x_d, si
     return matmul_dev(ctx, w, x_d, batch, y_d, &fs);
 }
 
+int hyq_hbm_read_d(hyq_ctx *ctx, const void *buf_d, size_t bytes, int workgroups,
+                   float *sink_d)
+{
+    if (!ctx || !buf_d || !sink_d) return fail(HYQ_EINVAL, "hbm_read: null argument");
+    if ((uintptr_t)buf_d % 16 || bytes < 16 || workgroups <= 0 || workgroups > (1 << 20))
+        return fail(HYQ_EINVAL, "hbm_read: bad buffer or workgroup count");
+    DeviceGuard g(ctx->device);
+    HYQ_LAUNCH(launch_hbm_read(buf_d, bytes, workgroups, sink_d, ctx->stream), "hbm_read");
+    return HYQ_OK;
+}
+
 int hyq_dequant_rows_d(hyq_ctx *ctx, const hyq_weight *w, size_t row0, size_t nrows,
                        float *out_d)
 {

@@ -265,10 +265,15 @@ constexpr int HALF_MAX_WORKGROUPS = 256;
 template <int F, int NR, int MODE, int IN>
 constexpr bool HALF_GEMV = HasHalf<F>::value && IN != 0 && NR == 1 && MODE != GEMV_ISUMS;
 
-template <int F, int NR, int MODE, int IN, int P, bool H, int SL = 0>
+// SLOT: the expert-slot forms of an MoE layer (GemvArgs::slot_expert), a
+// separate instantiation so that the other kernels carry none of it.
+template <int F, int NR, int MODE, int IN, int P, bool H, int SL = 0, bool SLOT = false>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
 {
     static_assert(!H || HALF_GEMV<F, NR, MODE, IN>, "half-group mode: see HALF_GEMV");
+    static_assert(!SLOT || (NR == 1 && !H && SL == 0 && P == 0 &&
+                            (MODE == GEMV_SILU || MODE == GEMV_PLAIN)),
+                  "expert slots: one row per lane, gate/up or plain");
     static_assert(SL == 0 || (SL == 32 && !H && NR == 1 && MODE == GEMV_PLAIN && P == 0),
                   "wide rows: 32 lanes per row, plain, one row per lane");
     using G = typename GroupOf<F>::T;
@@ -289,13 +294,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     // K slice of this workgroup row (kslices > 1: plain mode, f32 input
     // without norm or partial rows): groups [gbase, gbase + groups); or the
     // expert slot of this workgroup row (slot form: whole rows)
-    const int gbase = a.nslots ? 0 : blockIdx.y * groups;
+    const int gbase = SLOT ? 0 : blockIdx.y * groups;
     const float *xin =
-        a.xin + (a.nslots ? (size_t)blockIdx.y * a.slot_xin_stride : (size_t)gbase * 256);
+        a.xin + (SLOT ? (size_t)blockIdx.y * a.slot_xin_stride : (size_t)gbase * 256);
     // the slot's expert, first of all loads: the weight addresses need it
     int slot_e = 0;
-    if (a.slot_expert && a.nslots)
-        slot_e = min(max(a.slot_expert[blockIdx.y], 0), a.slot_experts - 1);
+    if (SLOT && a.nslots) slot_e = min(max(a.slot_expert[blockIdx.y], 0), a.slot_experts - 1);
 
     // Resolve each row of this lane to (segment, local row).
     int seg[NR], lrow[NR];
@@ -322,7 +326,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
         wrow[i] = lrowc[i];
-        if (a.slot_expert) {
+        if constexpr (SLOT) {
             if (a.nslots) {
                 wrow[i] = slot_e * a.rows_total + lrowc[i];
             } else {
@@ -574,7 +578,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
         } else if (MODE == GEMV_MULTI) {
             a.seg[seg[i]].y[lrow[i]] = v;
         } else {
-            if (a.kslices > 1 || a.nslots) {
+            if (a.kslices > 1 || (SLOT && a.nslots)) {
                 a.seg[0].y[(size_t)blockIdx.y * a.rows_total + lrow[i]] = v;
             } else {
                 float r = res[0][i];
@@ -686,6 +690,25 @@ template <int F> int launch_gemv_format(int mode, const GemvArgs &a, void *strea
         return (int)hipErrorInvalidValue;
     if (a.nslots && (a.kslices > 1 || !a.slot_expert)) return (int)hipErrorInvalidValue;
     if (a.nsparts > GEMV_MAX_PARTS || a.nrparts > GEMV_MAX_PARTS) return (int)hipErrorInvalidValue;
+    if (a.slot_expert) {
+        // expert slots: one row per lane; gate/up from Q8 input (row form)
+        // or a plain product of f32 rows quantized in the launch (slot form)
+        const int wv = a.xin ? 4 : (rows >= 8 * 4 * 512 ? 4 : rows >= 8 * 2 * 512 ? 2 : 1);
+        const dim3 sgrid((rows + 8 * wv - 1) / (8 * wv), ks), sblock(64 * wv);
+        const size_t slds = (size_t)a.groups * SLOT_INTS * 4 +
+                            (size_t)a.groups * (4 + 4 + 64 + 32) +
+                            (a.xin ? (size_t)a.groups * 4 : 0);
+        hipStream_t sst = (hipStream_t)stream;
+        if (mode == GEMV_SILU && !a.xin && !a.nslots)
+            hipLaunchKernelGGL((gemv_kernel<F, 1, GEMV_SILU, 0, 0, false, 0, true>), sgrid,
+                               sblock, slds, sst, a);
+        else if (mode == GEMV_PLAIN && a.xin && !a.norm && a.nslots)
+            hipLaunchKernelGGL((gemv_kernel<F, 1, GEMV_PLAIN, 1, 0, false, 0, true>), sgrid,
+                               sblock, slds, sst, a);
+        else
+            return (int)hipErrorInvalidValue;
+        return (int)hipGetLastError();
+    }
     dim3 grid((rows + rows_per_block - 1) / rows_per_block, ks), block(64 * waves);
     // slots, then (input stage) scales, 256/16/32-value sums and group sums of squares
     const size_t lds = (size_t)a.groups * SLOT_INTS * 4 + (size_t)a.groups * (4 + 4 + 64 + 32) +

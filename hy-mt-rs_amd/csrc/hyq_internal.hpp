@@ -243,6 +243,9 @@ int launch_route(const float *logits, const float *bias, int tokens, int experts
 int launch_ffn_combine(const float *residual, const float *shared, const float *ex,
                        const float *w, int used, int H, int tokens, float *out, float *trace,
                        void *stream);
+// A read-only stream of `bytes` (16-byte aligned) by `workgroups` workgroups,
+// one float per workgroup into sink.
+int launch_hbm_read(const void *buf, size_t bytes, int workgroups, float *sink, void *stream);
 // rms_norm_into of `rows` rows of width H into y (f32).
 int launch_rms_rows(const float *x, const float *w, int rows, int H, float eps, float *y,
                     void *stream);

@@ -230,6 +230,13 @@ int hyq_moe_forward_d(hyq_ctx *ctx, const hyq_moe_config *mc, const hyq_weight *
                       const float *x_d, size_t tokens, void *scratch_d, size_t scratch_bytes,
                       float *out_d);
 
+/* Measurement aid (no counterpart in the reference): reads `bytes` of
+ * device memory at buf_d (16-byte aligned) once with `workgroups`
+ * workgroups of 256 threads and writes one float per workgroup to sink_d -
+ * the read-only HBM rate the HBM-bound products are compared with. */
+int hyq_hbm_read_d(hyq_ctx *ctx, const void *buf_d, size_t bytes, int workgroups,
+                   float *sink_d);
+
 /* decode of rows [row0, row0+nrows) to f32 on the device (Weight::row_into /
  * to_vec, src/quant.rs:99-142). */
 int hyq_dequant_rows_d(hyq_ctx *ctx, const hyq_weight *w, size_t row0, size_t nrows,
