@@ -52,7 +52,8 @@ inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 // does not walk page tables for every few kilobytes.
 struct PoolChunk;
 void *pool_alloc(int device, size_t bytes, PoolChunk **chunk);
-void pool_release(PoolChunk *chunk);
+// Returns [ptr, ptr + bytes) that pool_alloc(.., bytes, &chunk) gave.
+void pool_release(PoolChunk *chunk, void *ptr, size_t bytes);
 
 struct DeviceBuffer {
     void *ptr = nullptr;
@@ -65,7 +66,7 @@ struct DeviceBuffer {
     ~DeviceBuffer()
     {
         if (chunk) {
-            pool_release(chunk);
+            pool_release(chunk, ptr, bytes);
         } else if (ptr) {
             DeviceGuard g(device);
             (void)hipFree(ptr);
@@ -143,4 +144,16 @@ struct hyq_weight {
     size_t cols = 0, rows = 0;
     int device = 0;
     hyq::WView view{};
+    // an upper bound of |value| over the tensor (all experts), from its
+    // scales at upload; the f16-MFMA products need it inside f16's range
+    float max_abs = 0.f;
 };
+
+namespace hyq {
+// Bound of |decoded value| over n blocks of GGUF bytes (host memory).
+float weight_max_abs(int dtype, const uint8_t *bytes, size_t nblocks);
+// HYQ_EINVAL unless the tensor's values fit the f16 operands of the batched
+// products: none above f16's largest finite value, and not all of them
+// below its smallest normal (an all-zero tensor is fine).
+int check_f16_range(const hyq_weight *w, const char *who);
+} // namespace hyq

@@ -7,6 +7,8 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <mutex>
@@ -38,6 +40,78 @@ int hip_fail(hipError_t e, const char *what)
 {
     return fail(e == hipErrorOutOfMemory ? HYQ_ENOMEM : HYQ_EDEVICE, "%s: %s", what,
                 hipGetErrorString(e));
+}
+
+namespace {
+float f16_bits(const uint8_t *p)
+{
+    _Float16 h;
+    std::memcpy(&h, p, 2);
+    return (float)h;
+}
+} // namespace
+
+float weight_max_abs(int dtype, const uint8_t *b, size_t nblocks)
+{
+    const size_t bb = (size_t)block_bytes(dtype);
+    float m = 0.f;
+    auto upd = [&](float v) {
+        v = std::fabs(v);
+        if (!(v <= m)) m = v; // NaN propagates
+    };
+    for (size_t i = 0; i < nblocks; ++i) {
+        const uint8_t *x = b + i * bb;
+        switch (dtype) {
+        case F32: {
+            float v;
+            std::memcpy(&v, x, 4);
+            upd(v);
+            break;
+        }
+        case F16: upd(f16_bits(x)); break;
+        case Q8_0: upd(f16_bits(x) * 128.f); break;   // d * q, |q| <= 128
+        case Q2_0C: upd(f16_bits(x) * 3.f); break;    // (2c - 3) d
+        case STQ1_0: upd(f16_bits(x + 40)); break;    // digit * d, |digit| <= 1
+        case Q4_K: {                                   // d s q - dmin m, q <= 15, s, m <= 63
+            int smax = 0, mmax = 0;
+            for (int j = 0; j < 8; ++j) {
+                const uint8_t *sc = x + 4;
+                const int s6 = j < 4 ? sc[j] & 63 : (sc[j + 4] & 15) | ((sc[j - 4] >> 6) << 4);
+                const int m6 = j < 4 ? sc[j + 4] & 63 : (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
+                smax = s6 > smax ? s6 : smax;
+                mmax = m6 > mmax ? m6 : mmax;
+            }
+            upd(std::fabs(f16_bits(x)) * (float)(15 * smax) + std::fabs(f16_bits(x + 2)) * (float)mmax);
+            break;
+        }
+        case Q6_K: { // (d sc) (q - 32), |q - 32| <= 32
+            int smax = 0;
+            for (int j = 0; j < 16; ++j) {
+                const int v = std::abs((int)(int8_t)x[192 + j]);
+                smax = v > smax ? v : smax;
+            }
+            upd(f16_bits(x + 208) * (float)(32 * smax));
+            break;
+        }
+        default: break;
+        }
+    }
+    return m;
+}
+
+int check_f16_range(const hyq_weight *w, const char *who)
+{
+    const float m = w->max_abs;
+    if (!(m <= 65504.f))
+        return fail(HYQ_EINVAL,
+                    "%s: weight values up to %g leave the f16 range of the batched products",
+                    who, (double)m);
+    if (m > 0.f && m < 6.103515625e-05f)
+        return fail(HYQ_EINVAL,
+                    "%s: all weight values are below %g, f16's smallest normal: the batched "
+                    "products would lose them",
+                    who, 6.103515625e-05);
+    return HYQ_OK;
 }
 
 int q8_alloc(int device, size_t n, hyq_q8 **out)
@@ -349,6 +423,7 @@ int matmul_dev(hyq_ctx *ctx, const hyq_weight *w, const float *x_d, size_t batch
         return rc;
     }
     if (!is_quant(w->dtype)) return fail(HYQ_EDTYPE, "matmul: dtype %d has no batched path", w->dtype);
+    if ((rc = check_f16_range(w, "matmul"))) return rc;
     // the GEMM walks K in 64-column slices and loads x as float4
     if (w->cols % 64) return fail(HYQ_EINVAL, "matmul: cols %zu is not a multiple of 64", w->cols);
     if ((uintptr_t)x_d % 16 || (uintptr_t)y_d % 16)
@@ -537,6 +612,7 @@ int hyq_weight_upload(hyq_ctx *ctx, int dtype, const uint8_t *gguf_bytes, size_t
     w->view.p2 = base + sz[0] + sz[1];
     w->view.rows = (int)(rows * experts);
     w->view.nb = (int)nb;
+    w->max_abs = weight_max_abs(dtype, gguf_bytes, nblocks);
     *out = w.release();
     return HYQ_OK;
 }

@@ -945,11 +945,20 @@ int hyq_dense_prefill(hyq_dense *m, const int32_t *tokens, size_t n, float *logi
     for (size_t i = 0; i < n; ++i)
         if (tokens[i] < 0 || tokens[i] >= m->cfg.vocab)
             return fail(HYQ_EINVAL, "input token outside vocabulary");
-    DeviceGuard g(m->ctx->device);
-    hipStream_t st = m->ctx->stream;
     // the reference's chunks of PREFILL_CHUNK tokens take the batch-1 arm
     // only when one token is left over
     const size_t batched = n % PREFILL_CHUNK == 1 ? n - 1 : n;
+    if (batched) // the batched products' f16 operands
+        for (const hyq_dense::Layer &L : m->layers) {
+            for (const hyq_weight *w : {L.q, L.k, L.v, L.o, L.gate, L.up, L.down})
+                if (w && (rc = check_f16_range(w, "prefill"))) return rc;
+            if (L.moe)
+                for (const hyq_weight *w : {L.moe->gate, L.moe->up, L.moe->down, L.moe->sgate,
+                                            L.moe->sup, L.moe->sdown})
+                    if ((rc = check_f16_range(w, "prefill"))) return rc;
+        }
+    DeviceGuard g(m->ctx->device);
+    hipStream_t st = m->ctx->stream;
     if (batched && (rc = prefill_buffers(m))) return rc;
     for (size_t s = 0; s < n;) {
         const size_t cn = s < batched ? std::min(m->pf_cap, batched - s) : 1;

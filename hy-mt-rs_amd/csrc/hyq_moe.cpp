@@ -25,6 +25,8 @@ int check_experts(hyq_ctx *ctx, const hyq_weight *gate, const hyq_weight *up,
         if (w->rank != 3) return fail(HYQ_EINVAL, "moe: expert weights must have rank 3");
         if (w->device != ctx->device) return fail(HYQ_EINVAL, "moe: weight on another device");
         if (!is_quant(w->dtype)) return fail(HYQ_EDTYPE, "moe: dtype %d has no batched path", w->dtype);
+        int rc = check_f16_range(w, "moe");
+        if (rc) return rc;
     }
     const size_t hidden = gate->dims[0], mid = gate->dims[1], E = gate->dims[2];
     if (up->dims[0] != hidden || up->dims[1] != mid || up->dims[2] != E)

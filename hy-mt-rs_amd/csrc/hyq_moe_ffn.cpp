@@ -334,6 +334,9 @@ int hyq_moe_forward_d(hyq_ctx *ctx, const hyq_moe_config *mc, const hyq_weight *
     if (tokens > (size_t)moe_rows_max(f))
         return fail(HYQ_EINVAL, "moe_forward: %zu tokens exceed %d per call", tokens,
                     moe_rows_max(f));
+    if (tokens > 1)
+        for (const hyq_weight *w : {gate, up, down, shared_gate, shared_up, shared_down})
+            if ((rc = check_f16_range(w, "moe_forward"))) return rc;
     if (!x_d || !out_d || !scratch_d) return fail(HYQ_EINVAL, "moe_forward: null buffer");
     if ((uintptr_t)x_d % 16 || (uintptr_t)scratch_d % 256)
         return fail(HYQ_EINVAL, "moe_forward: x must be 16-byte and scratch 256-byte aligned");

@@ -1,22 +1,25 @@
 // Per-device pool of large allocations for weight storage.
 //
-// Tensors are bump-allocated (256-byte aligned) from chunks of at least
-// 1 GiB, each a single 2 MiB-aligned hipMalloc, so that a model's weights
-// sit in a few large mappings. A chunk is freed when the last tensor placed
-// in it is released; space inside a live chunk is not reused.
+// Tensors are placed (256-byte aligned) in chunks of at least 1 GiB, each a
+// single 2 MiB-aligned hipMalloc, so that a model's weights sit in a few
+// large mappings. Inside a chunk, released tensors' space is reused
+// first-fit (hyq_ranges.hpp); a chunk is freed when its last tensor is
+// released. When a 1 GiB chunk cannot be had, a chunk of the tensor's own
+// size is tried before failing.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
 #include <vector>
 
 #include "hyq_abi.hpp"
+#include "hyq_ranges.hpp"
 
 namespace hyq {
 
 struct PoolChunk {
     int device;
     uint8_t *base;
-    size_t size, used;
+    Ranges ranges;
     int refs;
 };
 
@@ -31,27 +34,35 @@ void *pool_alloc(int device, size_t bytes, PoolChunk **chunk)
 {
     const size_t need = align_up(bytes ? bytes : 1, 256);
     std::lock_guard<std::mutex> lk(g_mu);
-    for (PoolChunk *c : g_chunks)
-        if (c->device == device && c->size - c->used >= need) {
-            void *p = c->base + c->used;
-            c->used += need;
+    for (PoolChunk *c : g_chunks) {
+        size_t off;
+        if (c->device == device && c->ranges.take(need, &off)) {
             c->refs += 1;
             *chunk = c;
-            return p;
+            return c->base + off;
         }
-    const size_t size = align_up(need > CHUNK_MIN ? need : CHUNK_MIN, PAGE);
+    }
     DeviceGuard g(device);
     void *base = nullptr;
-    if (hipMalloc(&base, size) != hipSuccess) return nullptr;
-    auto *c = new PoolChunk{device, (uint8_t *)base, size, need, 1};
+    size_t size = align_up(need > CHUNK_MIN ? need : CHUNK_MIN, PAGE);
+    if (hipMalloc(&base, size) != hipSuccess) {
+        (void)hipGetLastError(); // clear the failed allocation's error
+        size = align_up(need, PAGE);
+        if (hipMalloc(&base, size) != hipSuccess) return nullptr;
+    }
+    auto *c = new PoolChunk{device, (uint8_t *)base, Ranges{}, 1};
+    c->ranges.size = size;
+    size_t off;
+    c->ranges.take(need, &off); // off == 0
     g_chunks.push_back(c);
     *chunk = c;
     return base;
 }
 
-void pool_release(PoolChunk *c)
+void pool_release(PoolChunk *c, void *ptr, size_t bytes)
 {
     std::lock_guard<std::mutex> lk(g_mu);
+    c->ranges.give((size_t)((uint8_t *)ptr - c->base), align_up(bytes ? bytes : 1, 256));
     if (--c->refs > 0) return;
     for (size_t i = 0; i < g_chunks.size(); ++i)
         if (g_chunks[i] == c) {

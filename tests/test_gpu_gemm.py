@@ -142,3 +142,23 @@ def test_activation_rows_scale_exactly(gpu_ctx):
     assert np.array_equal(scaled, (base * np.exp2(k)[:, None]).astype(np.float32))
     zero = W.matmul(np.zeros(2 * cols, np.float32), 2)
     assert np.array_equal(zero, np.zeros(2 * rows, np.float32))
+
+
+def test_f16_range_of_batched_weights(gpu_ctx):
+    """The batched products round weights to f16: a tensor whose values could
+    exceed f16's largest finite value, or whose values all lie below its
+    smallest normal, is refused there (HYQ_EINVAL) while batch 1 (the int8
+    GEMV, f32 arithmetic) still takes it."""
+    from synth import set_block_scale
+    rows, cols = 64, 512
+    x = np.random.default_rng(4).normal(0, 1, 2 * cols).astype(np.float32)
+    for d, ok in ((60000.0, False), (6e-8, False), (0.02, True)):
+        w = set_block_scale(Q4_K, random_matrix(Q4_K, rows, cols, seed=5), d, dmin=d)
+        W = gpu_ctx.upload(Q4_K, w, (cols, rows))
+        assert np.all(np.isfinite(W.matmul(x[:cols], 1)))
+        if ok:
+            assert np.all(np.isfinite(W.matmul(x, 2)))
+        else:
+            with pytest.raises(ValueError, match="f16"):
+                W.matmul(x, 2)
+        W.release()
