@@ -57,7 +57,7 @@ sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 HBM_PEAK_GBS = 8000.0
-ROOFLINE_PROFILE = "attn_out_gemv_q2c_2048x2048"
+ROOFLINE_PROFILE = "decode_attention_1p8b_ctx1153"
 METRIC = "decode tok/s 1.8B Q2_0C; quant GEMV HBM GB/s as % of ~8 TB/s peak"
 PREFILLED = 1024
 
@@ -294,36 +294,50 @@ def step_kernel_table(hyq, ctx, ev, model, kv, pos):
         for W in Ws:
             W.release()
 
-    staged_gemv("attn_output", "o", H, QL, 4 * c["layers"],
-                "hyq_matmul_d batch 1: Q2_0C [2048 x 2048], f32 input quantized in the launch; "
-                "the step launches this kernel for the attention output (+ residual) and, as "
-                "three K slices of 2048, for the down projection (per_step counts both, in "
-                "units of this launch's work)")
+    staged_gemv("attn_output", "o", H, QL, c["layers"],
+                "hyq_matmul_d batch 1: Q2_0C [2048 x 2048], f32 input quantized in the launch: "
+                "the instantiation the step launches for the attention output (+ residual)")
     staged_gemv("down", "down", H, F, c["layers"],
                 "hyq_matmul_d batch 1: Q2_0C [2048 x 6144] as one launch (the step splits it "
                 "into three K slices of the attention-output kernel instead)", same=False)
 
-    # attention (+ split merge) over the prefilled cache at the bench's positions
+    # the step's attention launch (RoPE, q/k norms, KV append, split partials)
+    # and its merge, over the prefilled cache at the bench's positions, K/V
+    # rotated over 64 layer caches (~150 MB)
     ctxlen = kv[0].shape[1]
     ks = [ctx.array(np.ascontiguousarray(kv[0][l % c["layers"]])) for l in range(64)]
     vs = [ctx.array(np.ascontiguousarray(kv[1][l % c["layers"]])) for l in range(64)]
     qd = ctx.array(rng.normal(0, 1, QL).astype(np.float32))
+    kd = ctx.array(rng.normal(0, 1, KVW).astype(np.float32))
+    vd = ctx.array(rng.normal(0, 1, KVW).astype(np.float32))
+    L0 = model["layers"][0]
+    qn, kn = ctx.array(L0["q_norm"]), ctx.array(L0["k_norm"])
+    freq = ctx.array(np.array([np.float32(c["rope_base"]) ** np.float32(-2.0 * j / D)
+                               for j in range(D // 2)], np.float32))
     posd = ctx.array(np.array([pos], np.int32))
     scratch = ctx.empty(L.hyq_attention_scratch_floats(ctxlen, c["heads"]), np.float32)
     out = ctx.empty(QL, np.float32)
 
-    def att(i):
-        L.hyq_attention_d(ctx.handle, qd.ptr, ks[i % 64].ptr, vs[i % 64].ptr, posd.ptr, ctxlen,
-                          c["heads"], c["kv_heads"], D, scratch.ptr, out.ptr, None)
+    def att(i, o):
+        L.hyq_attention_rope_d(ctx.handle, qd.ptr, kd.ptr, vd.ptr, qn.ptr, kn.ptr, freq.ptr,
+                               posd.ptr, ctxlen, c["heads"], c["kv_heads"], D,
+                               ctypes.c_float(c["rms_eps"]), 0, ks[i % 64].ptr, vs[i % 64].ptr,
+                               scratch.ptr, o)
 
-    ms = ev.time_ms(att, 256)
-    alg = 2 * (pos + 1) * KVW * 4 + QL * 4 + QL * 4
+    ms = ev.time_ms(lambda i: att(i, None), 256)
+    alg = attention_bytes(c, pos, ctxlen)
     table["attention"] = dict(us=round(ms * 1e3, 3), bytes=int(alg), per_step=c["layers"],
                               GBs=round(alg / (ms * 1e-3) / 1e9, 1),
-                              us_per_step=round(ms * 1e3 * c["layers"], 2), same_kernel=False,
-                              launch="hyq_attention_d: split attention + merge (the step's "
-                                     "attention kernel also applies RoPE, the q/k norms and the "
-                                     "KV append)")
+                              us_per_step=round(ms * 1e3 * c["layers"], 2), same_kernel=True,
+                              launch="hyq_attention_rope_d without its merge: the step's "
+                                     "attention kernel (RoPE + q/k norms of the raw "
+                                     "projections, KV append, split softmax partials of 16 "
+                                     "heads over the cache)")
+    ms2 = ev.time_ms(lambda i: att(i, out.ptr), 256)
+    table["attention_and_merge"] = dict(
+        us=round(ms2 * 1e3, 3), per_step=c["layers"], us_per_step=round(ms2 * 1e3 * c["layers"], 2),
+        same_kernel=False, launch="hyq_attention_rope_d: the step's attention kernel and its "
+                                  "split merge (two launches)")
     del ks, vs
 
     # lm_head: the tied Q6_K matrix (203 MB), two copies alternating
@@ -347,6 +361,20 @@ def step_kernel_table(hyq, ctx, ev, model, kv, pos):
     return table
 
 
+def attention_bytes(c, pos, ctxlen) -> int:
+    """Algorithmic bytes of the step's attention launch at position `pos`:
+    the cached K/V rows 0..pos-1 of every KV head read once, the raw q/k/v
+    rows read, the new K/V row written, and the split partials written."""
+    from_cache = 2 * pos * c["kv_heads"] * c["head_dim"] * 4
+    qkv = (c["heads"] + 2 * c["kv_heads"]) * c["head_dim"] * 4
+    append = 2 * c["kv_heads"] * c["head_dim"] * 4
+    per = -(-ctxlen // 64)
+    chunk = -(-per // 32) * 32
+    nact = -(-(pos + 1) // chunk)
+    partials = nact * c["heads"] * 132 * 4
+    return from_cache + qkv + append + partials
+
+
 def copy_rate(hyq, ctx, ev, nbytes=1 << 30):
     """Device-to-device copy bandwidth on the context stream (read + write
     bytes / time), the practical HBM ceiling beside the 8 TB/s peak."""
@@ -358,22 +386,32 @@ def copy_rate(hyq, ctx, ev, nbytes=1 << 30):
     return dict(bytes=2 * nbytes, ms=round(ms, 4), GBs=round(2 * nbytes / (ms * 1e-3) / 1e9, 1))
 
 
-def roofline_loop(hyq, ctx, ev, model, iters):
-    """The roofline kernel alone (for counter runs): the attention-output GEMV
-    as step_kernel_table times it, then one 256 MiB device copy whose HBM
-    traffic is known (the scale of the FETCH_SIZE / WRITE_SIZE counters)."""
+def roofline_loop(hyq, ctx, ev, model, kv, pos, iters):
+    """The roofline kernel alone (for counter runs): the step's attention
+    launch as step_kernel_table times it, then one 256 MiB device copy whose
+    HBM traffic is known (the scale of the FETCH_SIZE / WRITE_SIZE counters)."""
+    table = {}
     c = model["cfg"]
     L = hyq.lib()
-    H = c["hidden"]
-    QL = c["heads"] * c["head_dim"]
+    D = c["head_dim"]
+    QL, KVW = c["heads"] * D, c["kv_heads"] * D
     rng = np.random.default_rng(1)
-    blobs = [model["layers"][l]["o"] for l in range(c["layers"])]
-    Ws = _upload_rotation(ctx, model["linear"], blobs, (QL, H), ROTATE_BYTES)
-    xs = [ctx.array(rng.normal(0, 1, QL).astype(np.float32)) for _ in range(64)]
-    y = ctx.empty(H, np.float32)
-    n = len(Ws)
-    ms = ev.time_ms(lambda i: L.hyq_matmul_d(ctx.handle, Ws[i % n].handle, xs[i % 64].ptr, 1,
-                                             y.ptr), iters)
+    ctxlen = kv[0].shape[1]
+    ks = [ctx.array(np.ascontiguousarray(kv[0][l % c["layers"]])) for l in range(64)]
+    vs = [ctx.array(np.ascontiguousarray(kv[1][l % c["layers"]])) for l in range(64)]
+    qd = ctx.array(rng.normal(0, 1, QL).astype(np.float32))
+    kd = ctx.array(rng.normal(0, 1, KVW).astype(np.float32))
+    vd = ctx.array(rng.normal(0, 1, KVW).astype(np.float32))
+    L0 = model["layers"][0]
+    qn, kn = ctx.array(L0["q_norm"]), ctx.array(L0["k_norm"])
+    freq = ctx.array(np.array([np.float32(c["rope_base"]) ** np.float32(-2.0 * j / D)
+                               for j in range(D // 2)], np.float32))
+    posd = ctx.array(np.array([pos], np.int32))
+    scratch = ctx.empty(L.hyq_attention_scratch_floats(ctxlen, c["heads"]), np.float32)
+    ms = ev.time_ms(lambda i: L.hyq_attention_rope_d(
+        ctx.handle, qd.ptr, kd.ptr, vd.ptr, qn.ptr, kn.ptr, freq.ptr, posd.ptr, ctxlen,
+        c["heads"], c["kv_heads"], D, ctypes.c_float(c["rms_eps"]), 0, ks[i % 64].ptr,
+        vs[i % 64].ptr, scratch.ptr, None), iters)
     nb = 256 << 20
     a, b = ctx.empty(nb, np.uint8), ctx.empty(nb, np.uint8)
     hyq.check(L.hyq_memcpy_d2d(ctx.handle, b.ptr, a.ptr, nb))
@@ -534,8 +572,9 @@ def main() -> int:
     ctx = hyq.Context(0)
     ev = Events(ctx.stream)
     if args.roofline_only:
-        us = roofline_loop(hyq, ctx, ev, model, max(args.steps, 64))
-        print(json.dumps({"kernel": "attn_output", "avg_us": round(us, 3)}), flush=True)
+        us = roofline_loop(hyq, ctx, ev, model, kv, PREFILLED + args.warmup,
+                           max(args.steps, 64))
+        print(json.dumps({"kernel": "attention", "avg_us": round(us, 3)}), flush=True)
         ctx.close()
         return 0
     dec = load_dense(hyq, ctx, model, context)

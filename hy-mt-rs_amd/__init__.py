@@ -72,6 +72,8 @@ SIGNATURES = {
     "hyq_rope_norm_append_d": (I, [P, P, P, P, P, P, P, P, SZ, SZ, SZ, ctypes.c_float, P, P]),
     "hyq_attention_scratch_floats": (SZ, [SZ, SZ]),
     "hyq_attention_d": (I, [P, P, P, P, P, SZ, SZ, SZ, SZ, P, P, P]),
+    "hyq_attention_rope_d": (I, [P, P, P, P, P, P, P, P, SZ, SZ, SZ, SZ, ctypes.c_float, I, P, P,
+                                 P, P]),
     "hyq_attention_rows_scratch_floats": (SZ, [SZ, SZ, SZ]),
     "hyq_attention_rows_d": (I, [P, P, P, P, P, SZ, SZ, SZ, SZ, SZ, P, P]),
     "hyq_argmax_d": (I, [P, P, SZ, P, P]),

@@ -152,6 +152,32 @@ int hyq_attention_d(hyq_ctx *ctx, const float *q_d, const float *kcache_d,
     return HYQ_OK;
 }
 
+int hyq_attention_rope_d(hyq_ctx *ctx, const float *q_d, const float *k_d, const float *v_d,
+                         const float *q_norm_d, const float *k_norm_d, const float *freq_d,
+                         const int32_t *pos_d, size_t context, size_t heads, size_t kv_heads,
+                         size_t head_dim, float eps, int norm_first, float *kcache_d,
+                         float *vcache_d, float *scratch_d, float *out_d)
+{
+    int rc = check_ctx(ctx, "attention_rope");
+    if (rc) return rc;
+    if (!q_d || !k_d || !v_d || !q_norm_d || !k_norm_d || !freq_d || !pos_d || !kcache_d ||
+        !vcache_d || !scratch_d)
+        return fail(HYQ_EINVAL, "attention_rope: null argument");
+    if (head_dim != 128 || heads == 0 || kv_heads == 0 || heads % kv_heads ||
+        heads / kv_heads > (size_t)ATT_MAX_REP || context == 0 || context > 65536)
+        return fail(HYQ_EINVAL, "attention_rope: unsupported shape");
+    DeviceGuard g(ctx->device);
+    HYQ_LAUNCH(launch_attention_rope(q_d, k_d, v_d, q_norm_d, k_norm_d, freq_d, eps, kcache_d,
+                                     vcache_d, pos_d, (int)context, (int)heads, (int)kv_heads,
+                                     scratch_d, ctx->stream, norm_first != 0),
+               "attention_rope");
+    if (out_d)
+        HYQ_LAUNCH(launch_attention_merge(scratch_d, (int)context, (int)heads, pos_d, out_d,
+                                          ctx->stream),
+                   "attention_merge");
+    return HYQ_OK;
+}
+
 size_t hyq_attention_rows_scratch_floats(size_t context, size_t heads, size_t n)
 {
     return n * (size_t)prefill_attention_splits((int)context) * heads * PART_STRIDE;

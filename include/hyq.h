@@ -274,6 +274,20 @@ int hyq_attention_d(hyq_ctx *ctx, const float *q_d, const float *kcache_d,
                     const float *vcache_d, const int32_t *pos_d, size_t context, size_t heads,
                     size_t kv_heads, size_t head_dim, float *scratch_d, float *out_d,
                     hyq_q8 *out_q8);
+/* The decode step's attention as the decoder launches it: for the token at
+ * position *pos_d, RoPE and the per-head Q/K rms_norm of the raw projections
+ * q_d [heads*128] and k_d [kv_heads*128] (dense order, or the hy_v3 one when
+ * norm_first is set, src/model.rs:425-446), the append of the new key and
+ * v_d to row *pos_d of the caches (KvCache::append, :650-669), then
+ * attention_into over rows 0..=*pos_d (:949-1035) into out_d [heads*128].
+ * q_d is not modified; scratch_d holds hyq_attention_scratch_floats floats.
+ * With out_d null only the split partials are formed (the first of the
+ * step's two launches: its attention kernel without the merge). */
+int hyq_attention_rope_d(hyq_ctx *ctx, const float *q_d, const float *k_d, const float *v_d,
+                         const float *q_norm_d, const float *k_norm_d, const float *freq_d,
+                         const int32_t *pos_d, size_t context, size_t heads, size_t kv_heads,
+                         size_t head_dim, float eps, int norm_first, float *kcache_d,
+                         float *vcache_d, float *scratch_d, float *out_d);
 /* attention (src/model.rs:949-1037) for n query rows of a chunk whose keys
  * and values are already in the cache: row i (q_d [n][heads*128]) is the
  * token at position *pos_d + i and sees cache rows 0..=*pos_d + i (causal,

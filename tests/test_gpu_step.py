@@ -292,3 +292,57 @@ def test_non_finite_logits_poison_the_session(gpu_ctx, hyq):
         with pytest.raises(ValueError, match="invalidated"):
             dec.forward(3)
     dec.close()
+
+
+@pytest.mark.parametrize("pos,norm_first", [(0, False), (1087, False), (1151, False),
+                                            (1087, True)])
+def test_attention_rope_fused(gpu_ctx, hyq, oracle, pos, norm_first):
+    """hyq_attention_rope_d (the decode step's attention launch): RoPE and the
+    per-head q/k norms in the dense or the hy_v3 order, the K/V append and
+    attention over rows 0..=pos, against the oracle's functions."""
+    heads, kvh, D, ctxlen = 16, 4, 128, 1152
+    base, eps = 11158840.0, 1e-5
+    rng = np.random.default_rng(pos + 7)
+    q = rng.normal(0, 1, heads * D).astype(np.float32)
+    k = rng.normal(0, 1, kvh * D).astype(np.float32)
+    v = rng.normal(0, 1, kvh * D).astype(np.float32)
+    qn = rng.normal(1, 0.02, D).astype(np.float32)
+    kn = rng.normal(1, 0.02, D).astype(np.float32)
+    kc = rng.normal(0, 1, (ctxlen, kvh * D)).astype(np.float32)
+    vc = rng.normal(0, 1, (ctxlen, kvh * D)).astype(np.float32)
+    freq = np.array([np.float32(base) ** np.float32(-2.0 * j / D) for j in range(64)],
+                    np.float32)
+    d = {n: gpu_ctx.array(a) for n, a in dict(q=q, k=k, v=v, qn=qn, kn=kn, freq=freq, kc=kc,
+                                               vc=vc, pos=np.array([pos], np.int32)).items()}
+    L = hyq.lib()
+    scratch = gpu_ctx.empty(L.hyq_attention_scratch_floats(ctxlen, heads), np.float32)
+    out = gpu_ctx.empty(heads * D, np.float32)
+    hyq.check(L.hyq_attention_rope_d(gpu_ctx.handle, d["q"].ptr, d["k"].ptr, d["v"].ptr,
+                                     d["qn"].ptr, d["kn"].ptr, d["freq"].ptr, d["pos"].ptr,
+                                     ctxlen, heads, kvh, D, _f(eps), int(norm_first),
+                                     d["kc"].ptr, d["vc"].ptr, scratch.ptr, out.ptr))
+    c = np.empty(64, np.float32)
+    s = np.empty(64, np.float32)
+    O = oracle.lib()
+    O.hyqo_rope_tables(128, _f(base), pos, c.ctypes.data, s.ctypes.data)
+
+    def rot(x, n, w):
+        x = x.copy()
+        if norm_first:
+            O.hyqo_rms_norm_rows(x.ctypes.data, w.ctypes.data, x.size, 128, _f(eps))
+        O.hyqo_rope(x.ctypes.data, n, 128, c.ctypes.data, s.ctypes.data)
+        if not norm_first:
+            O.hyqo_rms_norm_rows(x.ctypes.data, w.ctypes.data, x.size, 128, _f(eps))
+        return x
+    q_ref, k_ref = rot(q, heads, qn), rot(k, kvh, kn)
+    kc_ref, vc_ref = kc.copy(), vc.copy()
+    kc_ref[pos], vc_ref[pos] = k_ref, v
+    ref = np.empty(heads * D, np.float32)
+    O.hyqo_attention(q_ref.ctypes.data, kc_ref.ctypes.data, vc_ref.ctypes.data, heads, kvh, D,
+                     pos + 1, ref.ctypes.data)
+    kg, vg = d["kc"].numpy(), d["vc"].numpy()
+    assert np.allclose(kg[pos], k_ref, rtol=2e-5, atol=2e-6)
+    assert np.array_equal(vg[pos], v)
+    assert np.array_equal(np.delete(kg, pos, 0), np.delete(kc, pos, 0))
+    assert np.allclose(out.numpy(), ref, rtol=2e-5, atol=2e-6), np.abs(out.numpy() - ref).max()
+    assert np.array_equal(d["q"].numpy(), q)  # the raw query is not modified
