@@ -114,7 +114,7 @@ class Events:
 ROTATE_BYTES = 1 << 30  # distinct weight copies per measurement: 4x the 256 MB MALL
 
 
-def gemv_rate(hyq, ctx, ev, dtype, rows, cols, seed=1, min_bytes=ROTATE_BYTES):
+def gemv_rate(hyq, ctx, ev, dtype, rows, cols, seed=1, min_bytes=ROTATE_BYTES, graph=True):
     """Standalone int8 GEMV with Q8 input over >= 1 GiB of distinct weight
     copies: (us per launch, algorithmic GB/s) from back-to-back launches, and
     the aggregate GB/s of one HIP graph that launches every copy once."""
@@ -133,11 +133,12 @@ def gemv_rate(hyq, ctx, ev, dtype, rows, cols, seed=1, min_bytes=ROTATE_BYTES):
         L.hyq_gemv_q8_d(ctx.handle, Ws[i % copies].handle, q8.handle, None, y.ptr)
 
     ms = ev.time_ms(launch, max(64, 2 * copies))
-    gms = ev.graph_ms(launch, copies)
+    gms = ev.graph_ms(launch, copies) if graph else None
     alg = base.size + cols + 4 * (cols // 256) + 4 * rows
     for W in Ws:
         W.release()
-    return ms * 1e3, alg / (ms * 1e-3) / 1e9, alg * copies / (gms * 1e-3) / 1e9, copies
+    agg = alg * copies / (gms * 1e-3) / 1e9 if gms else None
+    return ms * 1e3, alg / (ms * 1e-3) / 1e9, agg, copies, alg
 
 
 def read_ceiling(hyq, ctx, ev, nbytes=2 << 30):
@@ -153,6 +154,29 @@ def read_ceiling(hyq, ctx, ev, nbytes=2 << 30):
         if best is None or gbs > best["GBs"]:
             best = dict(bytes=nbytes, workgroups=wgs, ms=round(ms, 4), GBs=round(gbs, 1))
     buf.free()
+    return best
+
+
+def sized_read_ceiling(hyq, ctx, ev, nbytes, pool=2 << 30) -> dict:
+    """The read-only rate of one launch that reads `nbytes`: the streaming
+    kernel over windows of that size rotated through a 2 GiB buffer (no
+    window is read again before the other 2 GiB have been), back-to-back
+    launches, best over workgroup counts - what any kernel moving that many
+    bytes per launch can reach, launch and ramp included."""
+    L = hyq.lib()
+    n = -(-nbytes // 256) * 256
+    windows = max(2, pool // n)
+    buf = ctx.empty(windows * n, np.uint8)
+    sink = ctx.empty(1 << 16, np.float32)
+    best = None
+    for wgs in (256, 512, 1024, 2048, 4096, 8192):
+        ms = ev.time_ms(lambda i: L.hyq_hbm_read_d(ctx.handle, buf.ptr + (i % windows) * n, n,
+                                                   wgs, sink.ptr), max(64, windows))
+        gbs = n / (ms * 1e-3) / 1e9
+        if best is None or gbs > best["GBs"]:
+            best = dict(us=round(ms * 1e3, 3), workgroups=wgs, GBs=round(gbs, 1))
+    buf.free()
+    sink.free()
     return best
 
 
@@ -552,7 +576,8 @@ def main() -> int:
                          "counter runs), print its time and exit")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the step's kernels one by one instead of replaying a HIP "
-                         "graph (for profilers that cannot follow graph capture)")
+                         "graph, and skip the GEMVs' graph aggregates (for profilers that "
+                         "cannot follow graph capture)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -637,11 +662,17 @@ def main() -> int:
             "7B_Q2_0C_gate_up_28672x4096": (Q2_0C, 28672, 4096),
             "7B_STQ1_0_gate_up_28672x4096": (STQ1_0, 28672, 4096),
         }.items():
-            us, gbs, agg, copies = gemv_rate(hyq, ctx, ev, dt_, rows, cols)
+            us, gbs, agg, copies, alg = gemv_rate(hyq, ctx, ev, dt_, rows, cols, graph=use_graph)
+            ceil = sized_read_ceiling(hyq, ctx, ev, alg)
             gemv[name] = dict(us=round(us, 3), GBs=round(gbs, 1),
-                              frac=round(gbs / HBM_PEAK_GBS, 4), graph_GBs=round(agg, 1),
-                              graph_frac=round(agg / HBM_PEAK_GBS, 4), copies=copies)
-            log(f"{name}: {us:.2f} us {gbs:.0f} GB/s; graph of {copies} copies {agg:.0f} GB/s")
+                              frac=round(gbs / HBM_PEAK_GBS, 4), copies=copies,
+                              graph_GBs=round(agg, 1) if agg else None,
+                              graph_frac=round(agg / HBM_PEAK_GBS, 4) if agg else None,
+                              read_ceiling_same_bytes=ceil,
+                              of_read_ceiling=round(gbs / ceil["GBs"], 4))
+            log(f"{name}: {us:.2f} us {gbs:.0f} GB/s; graph of {copies} copies "
+                f"{agg or 0:.0f} GB/s; a read-only launch of the same bytes {ceil['us']:.2f} us "
+                f"{ceil['GBs']:.0f} GB/s")
 
     prefill = {}
     if not args.no_prefill:

@@ -295,54 +295,72 @@ def test_non_finite_logits_poison_the_session(gpu_ctx, hyq):
 
 
 @pytest.mark.parametrize("pos,norm_first", [(0, False), (1087, False), (1151, False),
-                                            (1087, True)])
+                                            (1087, True), (40, True)])
 def test_attention_rope_fused(gpu_ctx, hyq, oracle, pos, norm_first):
-    """hyq_attention_rope_d (the decode step's attention launch): RoPE and the
-    per-head q/k norms in the dense or the hy_v3 order, the K/V append and
-    attention over rows 0..=pos, against the oracle's functions."""
+    """hyq_attention_rope_d (the decode step's attention launches): RoPE and
+    the per-head q/k norms in the dense or the hy_v3 order, the K/V append
+    and attention over rows 0..=pos, against the oracle's functions; then
+    again at a smaller position with other rows in the same buffers, and
+    once with the split partials only (no merge: the output row is left as
+    it was), against hyq_attention_d over the appended cache."""
     heads, kvh, D, ctxlen = 16, 4, 128, 1152
     base, eps = 11158840.0, 1e-5
     rng = np.random.default_rng(pos + 7)
-    q = rng.normal(0, 1, heads * D).astype(np.float32)
-    k = rng.normal(0, 1, kvh * D).astype(np.float32)
-    v = rng.normal(0, 1, kvh * D).astype(np.float32)
     qn = rng.normal(1, 0.02, D).astype(np.float32)
     kn = rng.normal(1, 0.02, D).astype(np.float32)
     kc = rng.normal(0, 1, (ctxlen, kvh * D)).astype(np.float32)
     vc = rng.normal(0, 1, (ctxlen, kvh * D)).astype(np.float32)
     freq = np.array([np.float32(base) ** np.float32(-2.0 * j / D) for j in range(64)],
                     np.float32)
-    d = {n: gpu_ctx.array(a) for n, a in dict(q=q, k=k, v=v, qn=qn, kn=kn, freq=freq, kc=kc,
-                                               vc=vc, pos=np.array([pos], np.int32)).items()}
+    d = {n: gpu_ctx.array(a) for n, a in dict(qn=qn, kn=kn, freq=freq, kc=kc, vc=vc).items()}
     L = hyq.lib()
+    O = oracle.lib()
     scratch = gpu_ctx.empty(L.hyq_attention_scratch_floats(ctxlen, heads), np.float32)
     out = gpu_ctx.empty(heads * D, np.float32)
-    hyq.check(L.hyq_attention_rope_d(gpu_ctx.handle, d["q"].ptr, d["k"].ptr, d["v"].ptr,
-                                     d["qn"].ptr, d["kn"].ptr, d["freq"].ptr, d["pos"].ptr,
-                                     ctxlen, heads, kvh, D, _f(eps), int(norm_first),
-                                     d["kc"].ptr, d["vc"].ptr, scratch.ptr, out.ptr))
-    c = np.empty(64, np.float32)
-    s = np.empty(64, np.float32)
-    O = oracle.lib()
-    O.hyqo_rope_tables(128, _f(base), pos, c.ctypes.data, s.ctypes.data)
-
-    def rot(x, n, w):
-        x = x.copy()
-        if norm_first:
-            O.hyqo_rms_norm_rows(x.ctypes.data, w.ctypes.data, x.size, 128, _f(eps))
-        O.hyqo_rope(x.ctypes.data, n, 128, c.ctypes.data, s.ctypes.data)
-        if not norm_first:
-            O.hyqo_rms_norm_rows(x.ctypes.data, w.ctypes.data, x.size, 128, _f(eps))
-        return x
-    q_ref, k_ref = rot(q, heads, qn), rot(k, kvh, kn)
     kc_ref, vc_ref = kc.copy(), vc.copy()
-    kc_ref[pos], vc_ref[pos] = k_ref, v
-    ref = np.empty(heads * D, np.float32)
-    O.hyqo_attention(q_ref.ctypes.data, kc_ref.ctypes.data, vc_ref.ctypes.data, heads, kvh, D,
-                     pos + 1, ref.ctypes.data)
-    kg, vg = d["kc"].numpy(), d["vc"].numpy()
-    assert np.allclose(kg[pos], k_ref, rtol=2e-5, atol=2e-6)
-    assert np.array_equal(vg[pos], v)
-    assert np.array_equal(np.delete(kg, pos, 0), np.delete(kc, pos, 0))
-    assert np.allclose(out.numpy(), ref, rtol=2e-5, atol=2e-6), np.abs(out.numpy() - ref).max()
-    assert np.array_equal(d["q"].numpy(), q)  # the raw query is not modified
+    for p in (pos, max(pos - 700, 0) // 2):
+        q = rng.normal(0, 1, heads * D).astype(np.float32)
+        k = rng.normal(0, 1, kvh * D).astype(np.float32)
+        v = rng.normal(0, 1, kvh * D).astype(np.float32)
+        qd, kd, vd = gpu_ctx.array(q), gpu_ctx.array(k), gpu_ctx.array(v)
+        posd = gpu_ctx.array(np.array([p], np.int32))
+        hyq.check(L.hyq_attention_rope_d(gpu_ctx.handle, qd.ptr, kd.ptr, vd.ptr, d["qn"].ptr,
+                                         d["kn"].ptr, d["freq"].ptr, posd.ptr, ctxlen, heads,
+                                         kvh, D, _f(eps), int(norm_first), d["kc"].ptr,
+                                         d["vc"].ptr, scratch.ptr, out.ptr))
+        c = np.empty(64, np.float32)
+        s = np.empty(64, np.float32)
+        O.hyqo_rope_tables(128, _f(base), p, c.ctypes.data, s.ctypes.data)
+
+        def rot(x, n, w):
+            x = x.copy()
+            if norm_first:
+                O.hyqo_rms_norm_rows(x.ctypes.data, w.ctypes.data, x.size, 128, _f(eps))
+            O.hyqo_rope(x.ctypes.data, n, 128, c.ctypes.data, s.ctypes.data)
+            if not norm_first:
+                O.hyqo_rms_norm_rows(x.ctypes.data, w.ctypes.data, x.size, 128, _f(eps))
+            return x
+        q_ref, k_ref = rot(q, heads, qn), rot(k, kvh, kn)
+        kc_ref[p], vc_ref[p] = k_ref, v
+        ref = np.empty(heads * D, np.float32)
+        O.hyqo_attention(q_ref.ctypes.data, kc_ref.ctypes.data, vc_ref.ctypes.data, heads, kvh,
+                         D, p + 1, ref.ctypes.data)
+        kg, vg = d["kc"].numpy(), d["vc"].numpy()
+        assert np.allclose(kg[p], k_ref, rtol=2e-5, atol=2e-6)
+        assert np.array_equal(vg[p], v)
+        assert np.allclose(kg, kc_ref, rtol=2e-5, atol=2e-6)
+        assert np.array_equal(vg, vc_ref)
+        got = out.numpy()
+        assert np.allclose(got, ref, rtol=2e-5, atol=2e-6), (p, np.abs(got - ref).max())
+        assert np.array_equal(qd.numpy(), q)  # the raw query is not modified
+    # partials only (out untouched), then hyq_attention_d over the same cache
+    hyq.check(L.hyq_attention_rope_d(gpu_ctx.handle, qd.ptr, kd.ptr, vd.ptr, d["qn"].ptr,
+                                     d["kn"].ptr, d["freq"].ptr, posd.ptr, ctxlen, heads, kvh,
+                                     D, _f(eps), int(norm_first), d["kc"].ptr, d["vc"].ptr,
+                                     scratch.ptr, None))
+    assert np.array_equal(out.numpy(), got)
+    out2 = gpu_ctx.empty(heads * D, np.float32)
+    hyq.check(L.hyq_attention_d(gpu_ctx.handle, gpu_ctx.array(q_ref).ptr, d["kc"].ptr,
+                                d["vc"].ptr, posd.ptr, ctxlen, heads, kvh, D, scratch.ptr,
+                                out2.ptr, None))
+    assert np.allclose(out2.numpy(), got, rtol=2e-5, atol=2e-6)
