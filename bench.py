@@ -181,6 +181,18 @@ def sized_read_ceiling(hyq, ctx, ev, nbytes, pool=2 << 30) -> dict:
 
 
 MFMA_F16_PEAK_TFLOPS = 2500.0
+HIP_ATTR_CLOCK_KHZ, HIP_ATTR_CUS = 5, 63  # hipDeviceAttributeClockRate, ...MultiprocessorCount
+
+
+def mfma_peak_from_clock(ev, device: int = 0) -> dict:
+    """The dense f16 MFMA peak recomputed from the device's CU count and peak
+    clock: 4 SIMDs per CU, each a 32x32x16 f16 MFMA (32,768 flop) per 32
+    cycles, i.e. 4,096 flop per clock per CU."""
+    cl, cu = ctypes.c_int(), ctypes.c_int()
+    ev.hip.hipDeviceGetAttribute(ctypes.byref(cl), HIP_ATTR_CLOCK_KHZ, device)
+    ev.hip.hipDeviceGetAttribute(ctypes.byref(cu), HIP_ATTR_CUS, device)
+    tf = cu.value * 4096 * cl.value * 1e3 / 1e12
+    return dict(cus=cu.value, clock_mhz=round(cl.value / 1e3, 1), TFLOPs=round(tf, 1))
 
 
 def prefill_rate(hyq, ctx, ev, dtype, rows, cols, batch, seed=3):
@@ -676,14 +688,17 @@ def main() -> int:
 
     prefill = {}
     if not args.no_prefill:
+        prefill["mfma_peak_from_clock"] = mfma_peak_from_clock(ev)
         for name, (dt_, rows, cols) in {
             "C4_Q4_K_gate_up_14336x4096x512": (Q4_K, 14336, 4096),
             "C4_Q6_K_down_4096x14336x512": (Q6_K, 4096, 14336),
             "C4_Q4_K_qkv_6144x4096x512": (Q4_K, 6144, 4096),
         }.items():
             us, tf = prefill_rate(hyq, ctx, ev, dt_, rows, cols, 512)
+            clk = prefill["mfma_peak_from_clock"]["TFLOPs"]
             prefill[name] = dict(us=round(us, 2), TFLOPs=round(tf, 1),
-                                 frac=round(tf / MFMA_F16_PEAK_TFLOPS, 4))
+                                 frac=round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                                 frac_of_clock_peak=round(tf / clk, 4) if clk else None)
             log(f"{name}: {us:.1f} us {tf:.0f} TFLOP/s")
 
     pf = None

@@ -274,7 +274,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     static_assert(!SLOT || (NR == 1 && !H && SL == 0 && P == 0 &&
                             (MODE == GEMV_SILU || MODE == GEMV_PLAIN)),
                   "expert slots: one row per lane, gate/up or plain");
-    static_assert(SL == 0 || (SL == 32 && !H && NR == 1 && MODE == GEMV_PLAIN && P == 0),
+    static_assert(SL == 0 || (SL == 32 && !H && NR == 1 && MODE == GEMV_PLAIN && (P == 0 || P == 2)),
                   "wide rows: 32 lanes per row, plain, one row per lane");
     using G = typename GroupOf<F>::T;
     using Dt = typename GemvData<G, H>::T;
@@ -717,10 +717,18 @@ template <int F> int launch_gemv_format(int mode, const GemvArgs &a, void *strea
     const int pre = a.groups <= 32 ? (a.groups + 7) / 8 : 0;
     hipStream_t st = (hipStream_t)stream;
     if (wide) {
-        if (!a.xin)
+        // rows of at most 64 groups: both of a lane's groups preloaded
+        // before the input stage (the same sums in the same order)
+        if (a.groups <= 64) {
+            if (!a.xin)
+                hipLaunchKernelGGL((gemv_kernel<F, 1, GEMV_PLAIN, 0, 2, false, 32>), grid, block, lds, st, a);
+            else
+                hipLaunchKernelGGL((gemv_kernel<F, 1, GEMV_PLAIN, 1, 2, false, 32>), grid, block, lds, st, a);
+        } else if (!a.xin) {
             hipLaunchKernelGGL((gemv_kernel<F, 1, GEMV_PLAIN, 0, 0, false, 32>), grid, block, lds, st, a);
-        else
+        } else {
             hipLaunchKernelGGL((gemv_kernel<F, 1, GEMV_PLAIN, 1, 0, false, 32>), grid, block, lds, st, a);
+        }
         return (int)hipGetLastError();
     }
     if (!a.xin) return launch_in<F, 0, false>(mode, nr, pre, a, grid, block, lds, st);
