@@ -574,6 +574,15 @@ def cpu_baselines(model, kv) -> dict:
     return out
 
 
+# single-kernel loops for counter runs: (kind, format, rows, cols)
+ONLY = {
+    "c4_q4k_gate_up_14336x4096x512": ("gemm", "Q4_K", 14336, 4096),
+    "c4_q6k_down_4096x14336x512": ("gemm", "Q6_K", 4096, 14336),
+    "gemv_stq1_0_gate_up_28672x4096": ("gemv", "STQ1_0", 28672, 4096),
+    "gemv_q4k_gate_14336x4096": ("gemv", "Q4_K", 14336, 4096),
+}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -586,6 +595,9 @@ def main() -> int:
     ap.add_argument("--roofline-only", action="store_true",
                     help="run only the roofline kernel loop and a 256 MiB copy (for hardware "
                          "counter runs), print its time and exit")
+    ap.add_argument("--only", choices=sorted(ONLY),
+                    help="run only this kernel's measurement loop (for hardware counter "
+                         "runs), print its time and exit")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the step's kernels one by one instead of replaying a HIP "
                          "graph, and skip the GEMVs' graph aggregates (for profilers that "
@@ -600,6 +612,21 @@ def main() -> int:
         make_dense_model, make_kv_cache
 
     hyq = ge.package()
+    if args.only:
+        ctx = hyq.Context(0)
+        ev = Events(ctx.stream)
+        kind, dt_name, rows, cols = ONLY[args.only]
+        dt_ = dict(Q4_K=Q4_K, Q6_K=Q6_K, STQ1_0=STQ1_0, Q2_0C=Q2_0C)[dt_name]
+        if kind == "gemm":
+            us, tf = prefill_rate(hyq, ctx, ev, dt_, rows, cols, 512)
+            print(json.dumps({"kernel": args.only, "avg_us": round(us, 3),
+                              "TFLOPs": round(tf, 1)}), flush=True)
+        else:
+            us, gbs, _, copies, _ = gemv_rate(hyq, ctx, ev, dt_, rows, cols, graph=False)
+            print(json.dumps({"kernel": args.only, "avg_us": round(us, 3), "GBs": round(gbs, 1),
+                              "copies": copies}), flush=True)
+        ctx.close()
+        return 0
     cfg = DENSE_1P8B
     context = PREFILLED + args.warmup + args.steps + 1
     log("building the synthetic 1.8B 2Bit model")
