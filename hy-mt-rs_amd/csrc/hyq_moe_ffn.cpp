@@ -307,7 +307,10 @@ int hyq_moe_route_d(hyq_ctx *ctx, const float *logits_d, const float *bias_d, si
 
 size_t hyq_moe_forward_scratch_bytes(const hyq_moe_config *mc, size_t hidden, size_t tokens)
 {
-    if (!mc || tokens == 0 || hidden == 0 || mc->experts <= 0 || mc->used <= 0) return 0;
+    if (!mc || tokens == 0 || hidden == 0 || hidden > (1u << 20) || mc->experts <= 0 ||
+        mc->used <= 0 || mc->mid <= 0 || mc->shared_mid <= 0 || mc->experts > (1 << 20) ||
+        mc->mid > (1 << 20) || mc->shared_mid > (1 << 20))
+        return 0;
     MoeFfn f;
     f.hidden = (int)hidden;
     f.experts = mc->experts;
