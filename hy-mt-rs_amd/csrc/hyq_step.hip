@@ -294,8 +294,10 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_kernel(
         return;
     }
     const int n = min(chunk, visible - p0);
-    // the new position's row of this head is formed here, not read
-    const int pnew = rope && split == nact - 1 ? pos - p0 : -1;
+    // the new position's row of this head is formed here, not read (and
+    // appended only inside the allocation: a position the caller let reach
+    // `context` attends to the cache without writing past it)
+    const int pnew = rope && split == nact - 1 && pos < context ? pos - p0 : -1;
 #define HYQ_ATT_LOAD(SB)                                                                       \
     _Pragma("unroll") for (int j = 0; j < 2; ++j)                                             \
     {                                                                                          \

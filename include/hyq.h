@@ -260,7 +260,9 @@ int hyq_rms_norm_q8_d(hyq_ctx *ctx, const float *x_d, const float *w_d, size_t n
  * src/model.rs:874-917), then the dense order's per-head rms_norm of q and k
  * (src/model.rs:425-446), then KvCache::append (src/model.rs:650-669) of k and
  * v into row *pos_d of kcache/vcache ([context][kv_heads*head_dim] f32).
- * q is updated in place. freq_d[j] = rope_base^(-2j/head_dim). head_dim 128. */
+ * q is updated in place. freq_d[j] = rope_base^(-2j/head_dim). head_dim 128.
+ * *pos_d is read on the device, so the library cannot check it: the caches
+ * must hold row *pos_d. */
 int hyq_rope_norm_append_d(hyq_ctx *ctx, float *q_d, const float *k_d, const float *v_d,
                            const float *q_norm_d, const float *k_norm_d, const float *freq_d,
                            const int32_t *pos_d, size_t heads, size_t kv_heads, size_t head_dim,
@@ -281,6 +283,8 @@ int hyq_attention_d(hyq_ctx *ctx, const float *q_d, const float *kcache_d,
  * v_d to row *pos_d of the caches (KvCache::append, :650-669), then
  * attention_into over rows 0..=*pos_d (:949-1035) into out_d [heads*128].
  * q_d is not modified; scratch_d holds hyq_attention_scratch_floats floats.
+ * *pos_d must lie in [0, context): the launch appends nothing outside the
+ * caches' `context` rows, whatever the device value.
  * With out_d null only the split partials are formed (the first of the
  * step's two launches: its attention kernel without the merge). */
 int hyq_attention_rope_d(hyq_ctx *ctx, const float *q_d, const float *k_d, const float *v_d,

@@ -364,3 +364,29 @@ def test_attention_rope_fused(gpu_ctx, hyq, oracle, pos, norm_first):
                                 d["vc"].ptr, posd.ptr, ctxlen, heads, kvh, D, scratch.ptr,
                                 out2.ptr, None))
     assert np.allclose(out2.numpy(), got, rtol=2e-5, atol=2e-6)
+
+
+def test_attention_rope_position_at_context_appends_nothing(gpu_ctx, hyq):
+    """A device position equal to `context` (which the library cannot check
+    on the host) must not be appended past the caches' `context` rows. The
+    caches here hold one spare row beyond `context`, so even a wrong append
+    stays inside the allocation; the spare row must come back unchanged."""
+    heads, kvh, D, ctxlen = 16, 4, 128, 96
+    rng = np.random.default_rng(5)
+    kc = rng.normal(0, 1, (ctxlen + 1, kvh * D)).astype(np.float32)
+    vc = rng.normal(0, 1, (ctxlen + 1, kvh * D)).astype(np.float32)
+    arrs = dict(q=rng.normal(0, 1, heads * D), k=rng.normal(0, 1, kvh * D),
+                v=rng.normal(0, 1, kvh * D), qn=np.ones(D), kn=np.ones(D),
+                freq=np.ones(D // 2), kc=kc, vc=vc)
+    d = {n: gpu_ctx.array(np.asarray(a, np.float32)) for n, a in arrs.items()}
+    posd = gpu_ctx.array(np.array([ctxlen], np.int32))
+    L = hyq.lib()
+    scratch = gpu_ctx.empty(L.hyq_attention_scratch_floats(ctxlen, heads), np.float32)
+    out = gpu_ctx.empty(heads * D, np.float32)
+    hyq.check(L.hyq_attention_rope_d(gpu_ctx.handle, d["q"].ptr, d["k"].ptr, d["v"].ptr,
+                                     d["qn"].ptr, d["kn"].ptr, d["freq"].ptr, posd.ptr, ctxlen,
+                                     heads, kvh, D, _f(1e-5), 0, d["kc"].ptr, d["vc"].ptr,
+                                     scratch.ptr, out.ptr))
+    assert np.array_equal(d["kc"].numpy(), kc)
+    assert np.array_equal(d["vc"].numpy(), vc)
+    assert np.isfinite(out.numpy()).all()
