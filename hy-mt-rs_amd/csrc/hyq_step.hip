@@ -25,14 +25,17 @@ __device__ __forceinline__ float wave_sum(float v) { return wave::sum64(v); }
 __device__ __forceinline__ float wave_max(float v) { return wave::max64(v); }
 
 // ---- embedding rows (Weight::row_into with device-resident token ids) ----
-// Grid (cols / 256, tokens): row blockIdx.y of out takes token[blockIdx.y].
+// Grid (cols / 256, tokens): row blockIdx.y of out takes token[blockIdx.y]
+// (clamped into [0, rows): the reference rejects an id past the table, which
+// a device-side id cannot report, so it never reads outside the table).
 template <int F>
 __global__ __launch_bounds__(256) void embed_kernel(WView w, int cols, const int *__restrict__ token,
                                                     float *__restrict__ out)
 {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= cols) return;
-    const size_t row = (size_t)token[blockIdx.y];
+    // a device-resident id the host cannot check: clamped into the table
+    const size_t row = (size_t)min(max(token[blockIdx.y], 0), w.rows - 1);
     out += (size_t)blockIdx.y * cols;
     const size_t blk = row * (size_t)w.nb + i / block_len(F);
     out[i] = dec::decode_plane_value<F>(w, blk, i % block_len(F));

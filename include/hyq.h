@@ -249,7 +249,9 @@ int hyq_decode_d(hyq_ctx *ctx, int dtype, const uint8_t *bytes_d, size_t byte_le
  * Positions and token ids are read from device memory so that a caller can
  * capture a whole step in a HIP graph and replay it. */
 
-/* Weight::row_into (src/quant.rs:123-142) with the row index in device memory. */
+/* Weight::row_into (src/quant.rs:123-142) with the row index in device memory.
+ * The library cannot check a device-resident index: one outside [0, rows)
+ * is clamped into it (the reference's bounds error has no device form). */
 int hyq_embed_row_d(hyq_ctx *ctx, const hyq_weight *w, const int32_t *token_d, float *out_d);
 /* rms_norm_into (src/model.rs:785-830) fused with Q8::quantize_into: the
  * normalized row y = x * (1/sqrt(mean(x^2)+eps)) * w goes to `out` as Q8 and,

@@ -166,10 +166,11 @@ def test_embed_row(gpu_ctx, hyq, oracle):
     W = gpu_ctx.upload(Q6_K, w, (cols, rows))
     out = gpu_ctx.empty(cols, np.float32)
     rb = w.size // rows
-    for tok in (0, 151, rows - 1):
+    # (rows: an id one past the table, which the device clamps to the last row)
+    for tok, src in ((0, 0), (151, 151), (rows - 1, rows - 1), (rows, rows - 1)):
         td = gpu_ctx.array(np.array([tok], np.int32))
         hyq.check(hyq.lib().hyq_embed_row_d(gpu_ctx.handle, W.handle, td.ptr, out.ptr))
-        ref = oracle.decode(Q6_K, w[tok * rb:(tok + 1) * rb])
+        ref = oracle.decode(Q6_K, w[src * rb:(src + 1) * rb])
         assert np.array_equal(out.numpy().view(np.uint32), ref.view(np.uint32))
 
 
