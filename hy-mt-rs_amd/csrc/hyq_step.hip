@@ -118,6 +118,7 @@ __global__ void rope_norm_kv_kernel(float *__restrict__ q, const float *__restri
     k += (size_t)blockIdx.y * kvw;
     v += (size_t)blockIdx.y * kvw;
     if (b >= heads + kvh) {
+        if (pos < 0) return; // (a negative device position appends nothing)
         const int h = b - heads - kvh;
         float *dst = vcache + (size_t)pos * kvw + (size_t)h * dim;
         dst[j] = v[h * dim + j];
@@ -157,7 +158,7 @@ __global__ void rope_norm_kv_kernel(float *__restrict__ q, const float *__restri
     if (is_q) {
         q[(size_t)h * dim + j] = o0;
         q[(size_t)h * dim + j + half] = o1;
-    } else {
+    } else if (pos >= 0) {
         float *dst = kcache + (size_t)pos * kvw + (size_t)h * dim;
         dst[j] = o0;
         dst[j + half] = o1;

@@ -264,7 +264,7 @@ int hyq_rms_norm_q8_d(hyq_ctx *ctx, const float *x_d, const float *w_d, size_t n
  * v into row *pos_d of kcache/vcache ([context][kv_heads*head_dim] f32).
  * q is updated in place. freq_d[j] = rope_base^(-2j/head_dim). head_dim 128.
  * *pos_d is read on the device, so the library cannot check it: the caches
- * must hold row *pos_d. */
+ * must hold row *pos_d (a negative position appends nothing). */
 int hyq_rope_norm_append_d(hyq_ctx *ctx, float *q_d, const float *k_d, const float *v_d,
                            const float *q_norm_d, const float *k_norm_d, const float *freq_d,
                            const int32_t *pos_d, size_t heads, size_t kv_heads, size_t head_dim,
