@@ -188,3 +188,57 @@ def test_hyv3_prefill_matches_oracle(gpu_ctx, hyq, oracle):
     assert lerr <= 2e-3, lerr
     dec.set_trace(None)
     dec.close()
+
+
+def test_moe_entry_point_errors(gpu_ctx, hyq):
+    """The argument checks of hyq_moe_route_d / hyq_moe_forward_d (the
+    reference's ensure! arms of Model::from_gguf's MoE binding,
+    src/model.rs:206-235, and route's preconditions): each returns an error
+    before any launch, and a valid call afterwards still runs."""
+    import ctypes
+    L = hyq.lib()
+    moe = dict(MOE_C5, experts=8, used=2, mid=256, shared_mid=256)
+    model = _moe_model(moe, seed=9)
+    e = model["layers"][1]["moe"]
+    H = HYV3["hidden"]
+    ffn = upload_moe(hyq, gpu_ctx, e, H)
+    r, g, u, d, sg, su, sd = ffn.weights
+    x = gpu_ctx.array(np.random.default_rng(1).normal(0, 1, (3, H)).astype(np.float32))
+    out = gpu_ctx.empty(3 * H, np.float32)
+    need = L.hyq_moe_forward_scratch_bytes(ctypes.byref(ffn.cfg), H, 3)
+    assert need > 0
+    scratch = gpu_ctx.empty(need, np.uint8)
+
+    def fwd(cfg=None, router=r, gate=g, down=d, tokens=3, nbytes=need, xptr=None):
+        return L.hyq_moe_forward_d(gpu_ctx.handle, ctypes.byref(cfg or ffn.cfg), router.handle,
+                                   ffn.bias.ptr, gate.handle, u.handle, down.handle, sg.handle,
+                                   su.handle, sd.handle, x.ptr if xptr is None else xptr, tokens,
+                                   scratch.ptr, nbytes, out.ptr)
+    EINVAL = hyq.EINVAL
+    assert fwd(router=g) == EINVAL                               # not [hidden, experts]
+    assert fwd(gate=d) == EINVAL                                 # gate shaped like down
+    assert fwd(down=g) == EINVAL
+    assert fwd(nbytes=need - 1) == EINVAL                        # scratch too small
+    assert fwd(xptr=x.ptr + 4) == EINVAL                         # misaligned rows
+    bad = hyq.MoeConfig(8, 9, 256, 256, 1, 2.5)                  # used > experts
+    assert fwd(cfg=bad) == EINVAL
+    bad = hyq.MoeConfig(8, 2, 256, 256, 1, 0.0)                  # non-positive scale
+    assert fwd(cfg=bad) == EINVAL
+    assert L.hyq_moe_forward_scratch_bytes(ctypes.byref(hyq.MoeConfig(8, 2, -1, 256, 1, 1.0)),
+                                           H, 3) == 0
+    # route: used > experts, too many experts, null buffers
+    lg = gpu_ctx.array(np.zeros((2, 8), np.float32))
+    bias = gpu_ctx.array(np.zeros(8, np.float32))
+    pe = gpu_ctx.empty(2 * 2, np.int32)
+    pw = gpu_ctx.empty(2 * 2, np.float32)
+    f = ctypes.c_float(1.0)
+    assert L.hyq_moe_route_d(gpu_ctx.handle, lg.ptr, bias.ptr, 2, 8, 9, 1, f, None, pe.ptr,
+                             pw.ptr) == EINVAL
+    assert L.hyq_moe_route_d(gpu_ctx.handle, lg.ptr, bias.ptr, 2, 2048, 2, 1, f, None, pe.ptr,
+                             pw.ptr) == EINVAL
+    assert L.hyq_moe_route_d(gpu_ctx.handle, lg.ptr, bias.ptr, 2, 8, 2, 1, f, None, None,
+                             pw.ptr) == EINVAL
+    # a valid call still runs and matches the Python wrapper's
+    hyq.check(fwd())
+    gpu_ctx.sync()
+    assert np.array_equal(out.numpy().reshape(3, H), ffn.forward(x.numpy().reshape(3, H)))
