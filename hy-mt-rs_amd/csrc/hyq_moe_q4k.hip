@@ -171,31 +171,44 @@ __device__ __forceinline__ void superblock(const WRaw &w, const XRaw &x, int g, 
 // their latency overlaps the copy. Past the last superblock the weight loads
 // read an L2-hot dummy (the activation operand), so every step issues the
 // same loads without a branch.
-template <int R>
+//
+// With RG > 1 the wave streams RG row groups one after another against the
+// same activation operand (group g at rows rows[r] + g gstride, into
+// acc[g R + r]): one stream of RG nbk superblocks, its prefetch running
+// across the group boundaries, so a workgroup's startup (the activation
+// copy, the first loads) is paid once per RG groups. nbk must then be a
+// multiple of 4 (the register ring restarts at each group).
+template <int R, int RG = 1>
 __device__ __forceinline__ void tile_rows(const WView *w, const int *rows, int kb0, int nbk,
                                           const _Float16 *xc, const _Float16 *xmc, uint4 *xl,
-                                          f4 *acc)
+                                          f4 *acc, int gstride = 0)
 {
     uint32_t magic;
     asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, rr = lane & 15;
     const int K = 256 * nbk; // the slice: superblocks kb0 .. kb0 + nbk - 1
     const uint8_t *qp[R], *mp[R];
+    size_t gq[R], gm[R]; // bytes from one row group to the next
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const size_t blk = (size_t)(rows[r] + rr) * w[r].nb + kb0;
         qp[r] = w[r].p0 + blk * 128 + 16 * g;
         mp[r] = w[r].p1 + blk * 16;
-        acc[r] = f4{0.f, 0.f, 0.f, 0.f};
+        gq[r] = (size_t)gstride * w[r].nb * 128;
+        gm[r] = (size_t)gstride * w[r].nb * 16;
     }
+#pragma unroll
+    for (int i = 0; i < RG * R; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
     const uint8_t *dummy = reinterpret_cast<const uint8_t *>(xc); // >= 144 bytes, L2-hot
     WRaw w0[R], w1[R], w2[R], w3[R];
+    // superblock j of the stream (group j / nbk, superblock j % nbk)
     auto loadw = [&](WRaw *wr, int j) {
-        const bool in = j < nbk;
+        const int gj = RG == 1 ? 0 : j / nbk, sj = RG == 1 ? j : j - gj * nbk;
+        const bool in = gj < RG && sj < nbk;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const uint8_t *q = in ? qp[r] + j * 128 : dummy;
-            const uint8_t *m = in ? mp[r] + j * 16 : dummy;
+            const uint8_t *q = in ? qp[r] + gj * gq[r] + sj * 128 : dummy;
+            const uint8_t *m = in ? mp[r] + gj * gm[r] + sj * 16 : dummy;
             wr[r].q0 = *reinterpret_cast<const uint4 *>(q);
             wr[r].q1 = *reinterpret_cast<const uint4 *>(q + 64);
             wr[r].meta = *reinterpret_cast<const uint4 *>(m);
@@ -225,30 +238,38 @@ __device__ __forceinline__ void tile_rows(const WView *w, const int *rows, int k
     HYQ_LGKM0();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    auto compute = [&](const WRaw *wr, int b) {
+    auto compute = [&](const WRaw *wr, int b, f4 *ac) {
         XRaw xr;
 #pragma unroll
         for (int t = 0; t < 8; ++t) xr.v[t] = xl[512 * b + 64 * t + lane];
         xr.m = xlm[64 * b + lane];
 #pragma unroll
-        for (int r = 0; r < R; ++r) superblock(wr[r], xr, g, magic, acc[r]);
+        for (int r = 0; r < R; ++r) superblock(wr[r], xr, g, magic, ac[r]);
     };
-    auto step = [&](WRaw *wc, WRaw *wn, int b) {
-        loadw(wn, b + 3);
+    // superblock b of group gg from wc, prefetching stream position
+    // gg nbk + b + 3 into wn
+    auto step = [&](WRaw *wc, WRaw *wn, int gg, int b, f4 *ac) {
+        loadw(wn, gg * nbk + b + 3);
         __builtin_amdgcn_sched_barrier(0);
-        compute(wc, b);
+        compute(wc, b, ac);
         __builtin_amdgcn_sched_barrier(0);
     };
-    int b = 0;
-    for (; b + 4 <= nbk; b += 4) {
-        step(w0, w3, b);
-        step(w1, w0, b + 1);
-        step(w2, w1, b + 2);
-        step(w3, w2, b + 3);
+#pragma unroll
+    for (int gg = 0; gg < RG; ++gg) {
+        f4 *ac = acc + gg * R;
+        int b = 0;
+        for (; b + 4 <= nbk; b += 4) {
+            step(w0, w3, gg, b, ac);
+            step(w1, w0, gg, b + 1, ac);
+            step(w2, w1, gg, b + 2, ac);
+            step(w3, w2, gg, b + 3, ac);
+        }
+        if (RG == 1) {
+            if (b < nbk) step(w0, w3, gg, b, ac);
+            if (b + 1 < nbk) step(w1, w0, gg, b + 1, ac);
+            if (b + 2 < nbk) step(w2, w1, gg, b + 2, ac);
+        }
     }
-    if (b < nbk) step(w0, w3, b);
-    if (b + 1 < nbk) step(w1, w0, b + 1);
-    if (b + 2 < nbk) step(w2, w1, b + 2);
 }
 
 // Workgroup order. Workgroups are dispatched round-robin over the 8 XCDs
@@ -274,6 +295,7 @@ inline int chunk_grid(int mgroups, int max_tiles) { return 8 * mgroups * ((max_t
 // the workgroup takes mid rows m0 = 64 mg + 16 w of gate and of up; the
 // slice's sums, scaled back by the token column's scale, go to
 // gpart / upart[slice][q][m] for the chunk's pair positions q.
+template <int RG>
 __global__ __launch_bounds__(256, 2) void moe_q4k_gate_up_kernel(
     WView gate, WView up, int mid, int K, const int *__restrict__ eoff,
     const int *__restrict__ tiles, const int *__restrict__ ntiles,
@@ -283,8 +305,8 @@ __global__ __launch_bounds__(256, 2) void moe_q4k_gate_up_kernel(
 {
     const int ks = moe_kslices(K);
     int ti, mgk;
-    if (!chunk_tile(mgroups * ks, max_tiles, ntiles, ti, mgk)) return;
-    const int mg = mgk / ks, kh = mgk % ks, nbk = K / 256 / ks;
+    if (!chunk_tile(mgroups / RG * ks, max_tiles, ntiles, ti, mgk)) return;
+    const int mg = mgk / ks * RG, kh = mgk % ks, nbk = K / 256 / ks;
     const int e = tiles[2 * ti], c = tiles[2 * ti + 1];
     const int nb = eoff[e] + c * CHUNK, cnt = min(CHUNK, eoff[e + 1] - nb);
     const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
@@ -292,18 +314,21 @@ __global__ __launch_bounds__(256, 2) void moe_q4k_gate_up_kernel(
     extern __shared__ uint4 xl[];
     const WView w[2] = {gate, up};
     const int rows[2] = {e * mid + m0, e * mid + m0};
-    f4 acc[2];
-    tile_rows<2>(w, rows, kh * nbk, nbk, xc + (size_t)ti * CHUNK * K, xmc + (size_t)ti * K, xl,
-                 acc);
-    // lane (g, rr): tokens 4g+i of mid row m0 + rr
-    const size_t base = kh * part_stride + (size_t)nb * mid + m0 + col;
+    f4 acc[2 * RG];
+    tile_rows<2, RG>(w, rows, kh * nbk, nbk, xc + (size_t)ti * CHUNK * K, xmc + (size_t)ti * K,
+                     xl, acc, 64);
+    // lane (g, rr): tokens 4g+i of mid row m0 + 64 gg + rr
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int tok = 4 * g + i;
-        if (tok >= cnt) continue;
-        const float s = xsc[ti * CHUNK + tok];
-        gpart[base + (size_t)tok * mid] = acc[0][i] * s;
-        upart[base + (size_t)tok * mid] = acc[1][i] * s;
+    for (int gg = 0; gg < RG; ++gg) {
+        const size_t base = kh * part_stride + (size_t)nb * mid + m0 + 64 * gg + col;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int tok = 4 * g + i;
+            if (tok >= cnt) continue;
+            const float s = xsc[ti * CHUNK + tok];
+            gpart[base + (size_t)tok * mid] = acc[2 * gg][i] * s;
+            upart[base + (size_t)tok * mid] = acc[2 * gg + 1][i] * s;
+        }
     }
 }
 
@@ -461,10 +486,19 @@ int launch_moe_q4k(WView gate, WView up, WView down, int hidden, int mid, const 
     hipLaunchKernelGGL(chunk_q4k_kernel, dim3(max_tiles, hidden / 256), dim3(64), 0, st, x, hidden,
                        tmax, tiles, ntiles, eoff, order, ptok, xc, xmc, xsc);
     {
-        const int mgroups = mid / 64, ks = moe_kslices(hidden);
-        hipLaunchKernelGGL(moe_q4k_gate_up_kernel, dim3(chunk_grid(mgroups * ks, max_tiles)),
-                           dim3(256), (size_t)34 * (hidden / ks), st, gate, up, mid, hidden, eoff,
-                           tiles, ntiles, xc, xmc, xsc, gpart, upart, gstride, mgroups, max_tiles);
+        // row groups per workgroup: 6 or else 4 (mid is a multiple of 256, so
+        // the 64-row groups number a multiple of 4) when the slice's
+        // superblocks fill the register ring evenly
+        const int mgroups = mid / 64, ks = moe_kslices(hidden), nbk = hidden / 256 / ks;
+        const size_t lds = (size_t)34 * (hidden / ks);
+        auto launch = [&](auto kern, int rg) {
+            hipLaunchKernelGGL(kern, dim3(chunk_grid(mgroups / rg * ks, max_tiles)), dim3(256),
+                               lds, st, gate, up, mid, hidden, eoff, tiles, ntiles, xc, xmc, xsc,
+                               gpart, upart, gstride, mgroups, max_tiles);
+        };
+        if (nbk % 4 != 0) launch(moe_q4k_gate_up_kernel<1>, 1);
+        else if (mgroups % 6 == 0) launch(moe_q4k_gate_up_kernel<6>, 6);
+        else launch(moe_q4k_gate_up_kernel<4>, 4);
     }
     hipLaunchKernelGGL(silu_rows_kernel, dim3(npairs), dim3(256), 0, st, gpart, upart,
                        moe_kslices(hidden), gstride, mid, valid, h32, hmax);

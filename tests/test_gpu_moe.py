@@ -180,6 +180,29 @@ def test_moe_30b_a3b_shape_sampled_tokens(gpu_ctx, hyq, oracle):
               "30B-A3B")
 
 
+@pytest.mark.parametrize("hidden,mid", [(2048, 1024), (4096, 512), (2048, 768)])
+def test_moe_row_group_streams(gpu_ctx, hyq, oracle, hidden, mid):
+    """Gate/up workgroups that stream several 64-row groups (4 when mid / 64
+    is not a multiple of 6, else 6) against one activation copy, at slices of
+    4 and 8 superblocks: every token checked against the f64 chain."""
+    experts, tokens, used = 8, 24, 3
+    _print(f"moe row groups hidden {hidden} mid {mid}")
+    gate = random_matrix(Q4_K, experts * mid, hidden, seed=51)
+    up = random_matrix(Q4_K, experts * mid, hidden, seed=52)
+    down = random_matrix(Q4_K, experts * hidden, mid, seed=53)
+    x = np.random.default_rng(54).normal(0, 1, tokens * hidden).astype(np.float32)
+    seed_out = np.random.default_rng(55).normal(0, 1, (tokens, hidden)).astype(np.float32)
+    pt, pe, pw = routed_pairs(tokens, experts, used, seed=56)
+    G = gpu_ctx.upload(Q4_K, gate, (hidden, mid, experts))
+    U = gpu_ctx.upload(Q4_K, up, (hidden, mid, experts))
+    D = gpu_ctx.upload(Q4_K, down, (mid, hidden, experts))
+    got = hyq.moe_experts(G, U, D, x, tokens, pt, pe, pw, seed_out).reshape(tokens, hidden)
+    ref, mag = chain_f64(oracle, Q4_K, Q4_K, gate, up, down, hidden, mid, x, pt, pe, pw,
+                         seed_out, range(tokens))
+    check_moe(got, np.stack([ref[t] for t in range(tokens)]),
+              np.stack([mag[t] for t in range(tokens)]), f"row groups {hidden}x{mid}")
+
+
 def test_moe_device_entry_point_and_rerun(gpu_ctx, hyq):
     """hyq_moe_experts_d on device buffers equals the host entry point, twice
     in a row on the same scratch (the second with fewer pairs)."""
