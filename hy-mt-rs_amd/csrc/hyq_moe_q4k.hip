@@ -57,6 +57,7 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 constexpr int CHUNK = 16; // tokens per expert chunk (one MFMA column block)
 constexpr int MOE_Q4K_MAX_K = 4096;  // largest K (hidden or mid)
 constexpr int MOE_Q4K_MAX_KL = 2048; // largest K slice of one workgroup: 34 KL bytes of LDS
+constexpr int DOWN_RG = 2;           // down: groups of 128 rows per workgroup
 
 // K slices of the gate/up product: two when its superblocks split evenly
 // (the tiles then number twice the workgroups, which evens out the last
@@ -177,8 +178,9 @@ __device__ __forceinline__ void superblock(const WRaw &w, const XRaw &x, int g, 
 // acc[g R + r]): one stream of RG nbk superblocks, its prefetch running
 // across the group boundaries, so a workgroup's startup (the activation
 // copy, the first loads) is paid once per RG groups. nbk must then be a
-// multiple of 4 (the register ring restarts at each group).
-template <int R, int RG = 1>
+// multiple of 4, or with PAIRS be 2 mod 4 with RG even (the stream then
+// holds whole rounds of the four-set ring per group or per pair of groups).
+template <int R, int RG = 1, bool PAIRS = false>
 __device__ __forceinline__ void tile_rows(const WView *w, const int *rows, int kb0, int nbk,
                                           const _Float16 *xc, const _Float16 *xmc, uint4 *xl,
                                           f4 *acc, int gstride = 0)
@@ -254,20 +256,50 @@ __device__ __forceinline__ void tile_rows(const WView *w, const int *rows, int k
         compute(wc, b, ac);
         __builtin_amdgcn_sched_barrier(0);
     };
+    // stream position p computes from set p % 4 and prefetches into set
+    // (p + 3) % 4
+    if constexpr (!PAIRS) {
 #pragma unroll
-    for (int gg = 0; gg < RG; ++gg) {
-        f4 *ac = acc + gg * R;
-        int b = 0;
-        for (; b + 4 <= nbk; b += 4) {
+        for (int gg = 0; gg < RG; ++gg) {
+            f4 *ac = acc + gg * R;
+            int b = 0;
+            for (; b + 4 <= nbk; b += 4) {
+                step(w0, w3, gg, b, ac);
+                step(w1, w0, gg, b + 1, ac);
+                step(w2, w1, gg, b + 2, ac);
+                step(w3, w2, gg, b + 3, ac);
+            }
+            if (RG == 1) {
+                if (b < nbk) step(w0, w3, gg, b, ac);
+                if (b + 1 < nbk) step(w1, w0, gg, b + 1, ac);
+                if (b + 2 < nbk) step(w2, w1, gg, b + 2, ac);
+            }
+        }
+    } else {
+        // PAIRS (nbk % 4 == 2, RG even): a pair of groups is 2 nbk
+        // positions, a multiple of 4; the second group of the pair starts at
+        // set 2
+        static_assert(RG % 2 == 0, "row groups stream in pairs");
+#pragma unroll
+        for (int gg = 0; gg < RG; gg += 2) {
+            f4 *ac = acc + gg * R, *ac2 = ac + R;
+            int b = 0;
+            for (; b + 4 <= nbk; b += 4) {
+                step(w0, w3, gg, b, ac);
+                step(w1, w0, gg, b + 1, ac);
+                step(w2, w1, gg, b + 2, ac);
+                step(w3, w2, gg, b + 3, ac);
+            }
             step(w0, w3, gg, b, ac);
             step(w1, w0, gg, b + 1, ac);
-            step(w2, w1, gg, b + 2, ac);
-            step(w3, w2, gg, b + 3, ac);
-        }
-        if (RG == 1) {
-            if (b < nbk) step(w0, w3, gg, b, ac);
-            if (b + 1 < nbk) step(w1, w0, gg, b + 1, ac);
-            if (b + 2 < nbk) step(w2, w1, gg, b + 2, ac);
+            step(w2, w1, gg + 1, 0, ac2);
+            step(w3, w2, gg + 1, 1, ac2);
+            for (b = 2; b + 4 <= nbk; b += 4) {
+                step(w0, w3, gg + 1, b, ac2);
+                step(w1, w0, gg + 1, b + 1, ac2);
+                step(w2, w1, gg + 1, b + 2, ac2);
+                step(w3, w2, gg + 1, b + 3, ac2);
+            }
         }
     }
 }
@@ -295,7 +327,7 @@ inline int chunk_grid(int mgroups, int max_tiles) { return 8 * mgroups * ((max_t
 // the workgroup takes mid rows m0 = 64 mg + 16 w of gate and of up; the
 // slice's sums, scaled back by the token column's scale, go to
 // gpart / upart[slice][q][m] for the chunk's pair positions q.
-template <int RG>
+template <int RG, bool PAIRS = false>
 __global__ __launch_bounds__(256, 2) void moe_q4k_gate_up_kernel(
     WView gate, WView up, int mid, int K, const int *__restrict__ eoff,
     const int *__restrict__ tiles, const int *__restrict__ ntiles,
@@ -315,8 +347,8 @@ __global__ __launch_bounds__(256, 2) void moe_q4k_gate_up_kernel(
     const WView w[2] = {gate, up};
     const int rows[2] = {e * mid + m0, e * mid + m0};
     f4 acc[2 * RG];
-    tile_rows<2, RG>(w, rows, kh * nbk, nbk, xc + (size_t)ti * CHUNK * K, xmc + (size_t)ti * K,
-                     xl, acc, 64);
+    tile_rows<2, RG, PAIRS>(w, rows, kh * nbk, nbk, xc + (size_t)ti * CHUNK * K,
+                            xmc + (size_t)ti * K, xl, acc, 64);
     // lane (g, rr): tokens 4g+i of mid row m0 + 64 gg + rr
 #pragma unroll
     for (int gg = 0; gg < RG; ++gg) {
@@ -366,8 +398,10 @@ __global__ __launch_bounds__(256) void silu_rows_kernel(const float *__restrict_
 }
 
 // Down of one 16-token chunk over one K slice: wave w takes hidden rows
-// m0 = 128 mg + 32 w .. m0 + 31 (two row tiles); the slice's sums
+// m0 = 128 mg + 32 w .. m0 + 31 (two row tiles) and, with RG > 1, the same
+// rows of the next RG - 1 groups of 128 rows; the slice's sums
 // down_e[m] . H[q], scaled back, go to outp (slice 0) or outp2 (slice 1).
+template <int RG, bool PAIRS = false>
 __global__ __launch_bounds__(256, 2) void moe_q4k_down_kernel(
     WView down, int hidden, int K, const int *__restrict__ eoff, const int *__restrict__ tiles,
     const int *__restrict__ ntiles, const _Float16 *__restrict__ hc,
@@ -376,8 +410,8 @@ __global__ __launch_bounds__(256, 2) void moe_q4k_down_kernel(
 {
     const int ks = 1;
     int ti, mgk;
-    if (!chunk_tile(mgroups * ks, max_tiles, ntiles, ti, mgk)) return;
-    const int mg = mgk / ks, kh = mgk % ks, nbk = K / 256 / ks;
+    if (!chunk_tile(mgroups / RG * ks, max_tiles, ntiles, ti, mgk)) return;
+    const int mg = mgk / ks * RG, kh = mgk % ks, nbk = K / 256 / ks;
     const int m0 = 128 * mg + 32 * (threadIdx.x >> 6); // hidden % 128 == 0: all rows exist
     const int e = tiles[2 * ti], c = tiles[2 * ti + 1];
     const int nb = eoff[e] + c * CHUNK, cnt = min(CHUNK, eoff[e + 1] - nb);
@@ -385,11 +419,11 @@ __global__ __launch_bounds__(256, 2) void moe_q4k_down_kernel(
     extern __shared__ uint4 xl[];
     const WView w[2] = {down, down};
     const int rows[2] = {e * hidden + m0, e * hidden + m0 + 16};
-    f4 acc[2];
-    tile_rows<2>(w, rows, kh * nbk, nbk, hc + (size_t)ti * CHUNK * K, hmc + (size_t)ti * K, xl,
-                 acc);
+    f4 acc[2 * RG];
+    tile_rows<2, RG, PAIRS>(w, rows, kh * nbk, nbk, hc + (size_t)ti * CHUNK * K,
+                            hmc + (size_t)ti * K, xl, acc, 128);
     float *dst = kh ? outp2 : outp;
-    // lane (g, rr): tokens 4g+i of hidden rows m0 + 16r + rr
+    // lane (g, rr): tokens 4g+i of hidden rows m0 + 128 gg + 16r + rr
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int tok = 4 * g + i;
@@ -397,7 +431,9 @@ __global__ __launch_bounds__(256, 2) void moe_q4k_down_kernel(
         const float s = hsc[ti * CHUNK + tok];
         float *orow = dst + (size_t)(nb + tok) * hidden + m0 + col;
 #pragma unroll
-        for (int r = 0; r < 2; ++r) orow[16 * r] = acc[r][i] * s;
+        for (int gg = 0; gg < RG; ++gg)
+#pragma unroll
+            for (int r = 0; r < 2; ++r) orow[128 * gg + 16 * r] = acc[2 * gg + r][i] * s;
     }
 }
 
@@ -486,9 +522,9 @@ int launch_moe_q4k(WView gate, WView up, WView down, int hidden, int mid, const 
     hipLaunchKernelGGL(chunk_q4k_kernel, dim3(max_tiles, hidden / 256), dim3(64), 0, st, x, hidden,
                        tmax, tiles, ntiles, eoff, order, ptok, xc, xmc, xsc);
     {
-        // row groups per workgroup: 6 or else 4 (mid is a multiple of 256, so
+        // row groups per workgroup: 6 or 4 (mid is a multiple of 256, so
         // the 64-row groups number a multiple of 4) when the slice's
-        // superblocks fill the register ring evenly
+        // superblocks fill the register ring (see tile_rows)
         const int mgroups = mid / 64, ks = moe_kslices(hidden), nbk = hidden / 256 / ks;
         const size_t lds = (size_t)34 * (hidden / ks);
         auto launch = [&](auto kern, int rg) {
@@ -496,19 +532,32 @@ int launch_moe_q4k(WView gate, WView up, WView down, int hidden, int mid, const 
                                lds, st, gate, up, mid, hidden, eoff, tiles, ntiles, xc, xmc, xsc,
                                gpart, upart, gstride, mgroups, max_tiles);
         };
-        if (nbk % 4 != 0) launch(moe_q4k_gate_up_kernel<1>, 1);
-        else if (mgroups % 6 == 0) launch(moe_q4k_gate_up_kernel<6>, 6);
-        else launch(moe_q4k_gate_up_kernel<4>, 4);
+        if (nbk % 2 != 0) launch(moe_q4k_gate_up_kernel<1>, 1);
+        else if (nbk % 4 == 2) // (6 groups in pairs spill to scratch)
+            launch(moe_q4k_gate_up_kernel<4, true>, 4);
+        else
+            mgroups % 6 == 0 ? launch(moe_q4k_gate_up_kernel<6>, 6)
+                             : launch(moe_q4k_gate_up_kernel<4>, 4);
     }
     hipLaunchKernelGGL(silu_rows_kernel, dim3(npairs), dim3(256), 0, st, gpart, upart,
                        moe_kslices(hidden), gstride, mid, valid, h32, hmax);
     hipLaunchKernelGGL(chunk_q4k_kernel, dim3(max_tiles, mid / 256), dim3(64), 0, st, h32, mid,
                        hmax, tiles, ntiles, eoff, nullptr, nullptr, hc, hmc, hsc);
     {
-        const int mgroups = hidden / 128;
-        hipLaunchKernelGGL(moe_q4k_down_kernel, dim3(chunk_grid(mgroups, max_tiles)),
-                           dim3(256), (size_t)34 * mid, st, down, hidden, mid, eoff, tiles,
-                           ntiles, hc, hmc, hsc, outp, outp2, mgroups, max_tiles);
+        // groups of 128 rows per workgroup: DOWN_RG when they divide and the
+        // superblocks fill the register ring (see tile_rows)
+        const int mgroups = hidden / 128, nbk = mid / 256;
+        auto launch = [&](auto kern, int rg) {
+            hipLaunchKernelGGL(kern, dim3(chunk_grid(mgroups / rg, max_tiles)), dim3(256),
+                               (size_t)34 * mid, st, down, hidden, mid, eoff, tiles, ntiles, hc,
+                               hmc, hsc, outp, outp2, mgroups, max_tiles);
+        };
+        if (nbk % 4 == 0 && mgroups % DOWN_RG == 0)
+            launch(moe_q4k_down_kernel<DOWN_RG>, DOWN_RG);
+        else if (nbk % 4 == 2 && mgroups % DOWN_RG == 0)
+            launch(moe_q4k_down_kernel<DOWN_RG, true>, DOWN_RG);
+        else
+            launch(moe_q4k_down_kernel<1>, 1);
     }
     return (int)hipGetLastError();
 }

@@ -180,11 +180,13 @@ def test_moe_30b_a3b_shape_sampled_tokens(gpu_ctx, hyq, oracle):
               "30B-A3B")
 
 
-@pytest.mark.parametrize("hidden,mid", [(2048, 1024), (4096, 512), (2048, 768)])
+@pytest.mark.parametrize("hidden,mid", [(2048, 1024), (4096, 512), (2048, 768), (1024, 1536)])
 def test_moe_row_group_streams(gpu_ctx, hyq, oracle, hidden, mid):
-    """Gate/up workgroups that stream several 64-row groups (4 when mid / 64
-    is not a multiple of 6, else 6) against one activation copy, at slices of
-    4 and 8 superblocks: every token checked against the f64 chain."""
+    """Workgroups that stream several row groups against one activation copy
+    (gate/up: 4 or 6 groups of 64 rows; down: groups of 128 rows), with K
+    slices of 2, 4, 6 and 8 superblocks (the register ring in whole rounds
+    per group or per pair of groups) and of 3 (one group): every token
+    checked against the f64 chain."""
     experts, tokens, used = 8, 24, 3
     _print(f"moe row groups hidden {hidden} mid {mid}")
     gate = random_matrix(Q4_K, experts * mid, hidden, seed=51)
