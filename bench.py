@@ -580,6 +580,7 @@ ONLY = {
     "c4_q6k_down_4096x14336x512": ("gemm", "Q6_K", 4096, 14336),
     "gemv_stq1_0_gate_up_28672x4096": ("gemv", "STQ1_0", 28672, 4096),
     "gemv_q4k_gate_14336x4096": ("gemv", "Q4_K", 14336, 4096),
+    "c5_moe_layer_64tok_top8of64": ("moe", None, 0, 0),
 }
 
 
@@ -616,8 +617,12 @@ def main() -> int:
         ctx = hyq.Context(0)
         ev = Events(ctx.stream)
         kind, dt_name, rows, cols = ONLY[args.only]
-        dt_ = dict(Q4_K=Q4_K, Q6_K=Q6_K, STQ1_0=STQ1_0, Q2_0C=Q2_0C)[dt_name]
-        if kind == "gemm":
+        dt_ = dict(Q4_K=Q4_K, Q6_K=Q6_K, STQ1_0=STQ1_0, Q2_0C=Q2_0C).get(dt_name)
+        if kind == "moe":
+            m = moe_rate(hyq, ctx, ev)
+            print(json.dumps({"kernel": args.only, "avg_us": m["us"], "GBs": m["GBs"]}),
+                  flush=True)
+        elif kind == "gemm":
             us, tf = prefill_rate(hyq, ctx, ev, dt_, rows, cols, 512)
             print(json.dumps({"kernel": args.only, "avg_us": round(us, 3),
                               "TFLOPs": round(tf, 1)}), flush=True)

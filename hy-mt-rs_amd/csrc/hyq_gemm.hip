@@ -424,6 +424,145 @@ __global__ __launch_bounds__(256) void moe_plan_small_kernel(
     for (int q = t; q < nv; q += 256) tlist[off[key[q]] + rank[q]] = q;
 }
 
+// The plan for up to PLAN_FAST pairs, tokens and experts, with at most
+// PLAN_FAST_TAB (batch, key) cells per grouping, on 1024 threads: the same
+// outputs as moe_plan_small_kernel. A grouping's stable rank comes from wave
+// ballots instead of pairwise compares: batch b (64 consecutive elements,
+// one wave) walks its distinct keys (one ballot per key), which gives each
+// lane its rank among the batch's equal keys and each key its batch count;
+// a per-key prefix over the batches and a scan over the keys then place
+// element i at off[key] + (its key's count in earlier batches) + (its rank
+// in its batch).
+constexpr int PLAN_FAST = 1024;
+constexpr int PLAN_FAST_TAB = 4096;
+
+// Exclusive scan of v[0..n) in place (n <= 1024 * 4), v[n] = the total; all
+// 1024 threads.
+__device__ void lds_scan_1024(int *v, int n, int *lsum)
+{
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int per = (n + 1023) / 1024, lo = min(n, t * per), hi = min(n, lo + per);
+    int s = 0;
+    for (int i = lo; i < hi; ++i) s += v[i];
+    int x = s;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int u = __shfl_up(x, d);
+        if (lane >= d) x += u;
+    }
+    if (lane == 63) lsum[w] = x;
+    __syncthreads();
+    int run = x - s;
+    for (int j = 0; j < w; ++j) run += lsum[j];
+    for (int i = lo; i < hi; ++i) {
+        const int c = v[i];
+        v[i] = run;
+        run += c;
+    }
+    if (t == 1023) v[n] = run;
+    __syncthreads();
+}
+
+// Stable grouping of key[0..n) (key < 0: not grouped) into nkeys groups:
+// off[0..nkeys] = the exclusive scan of the group sizes, and element i goes
+// to off[key[i]] + tab[(i / 64) nkeys + key[i]] + rk[i]. Needs
+// ceil(n / 64) nkeys <= PLAN_FAST_TAB; all 1024 threads.
+__device__ void lds_group_1024(const int *key, int n, int nkeys, int *tab, int *rk, int *off,
+                               int *lsum)
+{
+    const int t = threadIdx.x, lane = t & 63, nb = (n + 63) / 64;
+    for (int i = t; i < nb * nkeys; i += 1024) tab[i] = 0;
+    __syncthreads();
+    for (int b = t >> 6; b < nb; b += 16) { // wave-uniform
+        const int i = 64 * b + lane;
+        const int k = i < n ? key[i] : -1;
+        int r = 0, c = 0;
+        unsigned long long rem = __ballot(k >= 0);
+        while (rem) { // one round per distinct key, all in registers
+            const int kl = __builtin_amdgcn_readlane(k, __builtin_ctzll(rem));
+            const unsigned long long m = __ballot(k == kl);
+            if (k == kl) {
+                r = __builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32),
+                                              __builtin_amdgcn_mbcnt_lo((unsigned)m, 0));
+                c = __popcll(m);
+            }
+            rem &= ~m;
+        }
+        if (k >= 0) {
+            rk[i] = r;
+            if (r == 0) tab[b * nkeys + k] = c;
+        }
+    }
+    __syncthreads();
+    for (int k = t; k < nkeys; k += 1024) {
+        int s = 0;
+        for (int b = 0; b < nb; ++b) {
+            const int c = tab[b * nkeys + k];
+            tab[b * nkeys + k] = s;
+            s += c;
+        }
+        off[k] = s;
+    }
+    __syncthreads();
+    lds_scan_1024(off, nkeys, lsum);
+}
+
+__host__ __device__ inline bool plan_fast_fits(int P, int T, int E)
+{
+    const long nb = (P + 63) / 64;
+    return P <= PLAN_FAST && T <= PLAN_FAST && E <= PLAN_FAST && nb * E <= PLAN_FAST_TAB &&
+           nb * T <= PLAN_FAST_TAB;
+}
+
+__global__ __launch_bounds__(1024) void moe_plan_fast_kernel(
+    const int *__restrict__ ptok, const int *__restrict__ pexp, int P, int T, int E, int *eoff,
+    int *order, int *toff, int *tlist, int *tiles, int *ntiles, int chunk)
+{
+    __shared__ int key[PLAN_FAST];
+    __shared__ int tok[PLAN_FAST];
+    __shared__ int rk[PLAN_FAST];
+    __shared__ int ord[PLAN_FAST];
+    __shared__ int tab[PLAN_FAST_TAB];
+    __shared__ int off[PLAN_FAST + 1];
+    __shared__ int lsum[16];
+    const int t = threadIdx.x;
+    for (int p = t; p < P; p += 1024) {
+        const int tk = ptok[p], e = pexp[p];
+        key[p] = tk >= 0 && tk < T && e >= 0 && e < E ? e : -1;
+        tok[p] = tk;
+    }
+    __syncthreads();
+    // group pairs by expert (stable)
+    lds_group_1024(key, P, E, tab, rk, off, lsum);
+    for (int e = t; e <= E; e += 1024) eoff[e] = off[e];
+    for (int p = t; p < P; p += 1024) {
+        const int e = key[p];
+        if (e >= 0) ord[off[e] + tab[(p >> 6) * E + e] + rk[p]] = p;
+    }
+    __syncthreads();
+    const int nv = off[E];
+    for (int q = t; q < nv; q += 1024) order[q] = ord[q];
+    // chunk-token chunks of every expert (counts in tab, scanned)
+    for (int e = t; e < E; e += 1024) tab[e] = (off[e + 1] - off[e] + chunk - 1) / chunk;
+    __syncthreads();
+    lds_scan_1024(tab, E, lsum);
+    for (int e = t; e < E; e += 1024)
+        for (int c = 0; c < tab[e + 1] - tab[e]; ++c) {
+            tiles[2 * (tab[e] + c)] = e;
+            tiles[2 * (tab[e] + c) + 1] = c;
+        }
+    if (t == 0) *ntiles = tab[E];
+    // for each token, its positions in ascending expert order
+    for (int q = t; q < nv; q += 1024) key[q] = tok[ord[q]];
+    __syncthreads();
+    lds_group_1024(key, nv, T, tab, rk, off, lsum);
+    for (int k = t; k <= T; k += 1024) toff[k] = off[k];
+    for (int q = t; q < nv; q += 1024) {
+        const int k = key[q];
+        tlist[off[k] + tab[(q >> 6) * T + k] + rk[q]] = q;
+    }
+}
+
 __device__ __forceinline__ float silu_mul(float g, float u)
 {
     // (g / (1 + exp(-g))) * u, DenseFfn::forward (src/model.rs:680-682)
@@ -827,7 +966,11 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
     // 16-token chunk per expert (weight-bound); the LDS-tiled GEMM otherwise.
     const bool few = fmt_gu == Q4_K && fmt_down == Q4_K && moe_q4k_fits(hidden, mid) &&
                      npairs <= moe_q4k_chunk() * experts;
-    if (npairs <= PLAN_SMALL && tokens <= PLAN_SMALL && experts <= PLAN_SMALL)
+    if (plan_fast_fits(npairs, tokens, experts))
+        hipLaunchKernelGGL(moe_plan_fast_kernel, dim3(1), dim3(1024), 0, st, ptok, pexp, npairs,
+                           tokens, experts, eoff, order, toff, tlist, tiles, ntiles,
+                           few ? moe_q4k_chunk() : BN);
+    else if (npairs <= PLAN_SMALL && tokens <= PLAN_SMALL && experts <= PLAN_SMALL)
         hipLaunchKernelGGL(moe_plan_small_kernel, dim3(1), dim3(256), 0, st, ptok, pexp, npairs,
                            tokens, experts, eoff, order, toff, tlist, tiles, ntiles,
                            few ? moe_q4k_chunk() : BN);
