@@ -426,11 +426,12 @@ __global__ __launch_bounds__(256) void moe_plan_small_kernel(
 
 // The plan for up to PLAN_FAST pairs, tokens and experts, with at most
 // PLAN_FAST_TAB (batch, key) cells per grouping, on 1024 threads: the same
-// outputs as moe_plan_small_kernel. A grouping's stable rank comes from wave
-// ballots instead of pairwise compares: batch b (64 consecutive elements,
-// one wave) walks its distinct keys (one ballot per key), which gives each
-// lane its rank among the batch's equal keys and each key its batch count;
-// a per-key prefix over the batches and a scan over the keys then place
+// outputs as moe_plan_small_kernel. A grouping's stable rank comes from
+// bit masks instead of pairwise compares: in batch b (64 consecutive
+// elements, one wave) every lane sets its bit in the mask of (b, its key)
+// with one LDS atomic OR, so the bits below its own give its rank among the
+// batch's equal keys and the mask's population the key's batch count; a
+// per-key prefix over the batches and a scan over the keys then place
 // element i at off[key] + (its key's count in earlier batches) + (its rank
 // in its batch).
 constexpr int PLAN_FAST = 1024;
@@ -467,41 +468,33 @@ __device__ void lds_scan_1024(int *v, int n, int *lsum)
 // off[0..nkeys] = the exclusive scan of the group sizes, and element i goes
 // to off[key[i]] + tab[(i / 64) nkeys + key[i]] + rk[i]. Needs
 // ceil(n / 64) nkeys <= PLAN_FAST_TAB; all 1024 threads.
-__device__ void lds_group_1024(const int *key, int n, int nkeys, int *tab, int *rk, int *off,
-                               int *lsum)
+__device__ void lds_group_1024(const int *key, int n, int nkeys, unsigned long long *tab,
+                               int *rk, int *off, int *lsum)
 {
     const int t = threadIdx.x, lane = t & 63, nb = (n + 63) / 64;
     for (int i = t; i < nb * nkeys; i += 1024) tab[i] = 0;
     __syncthreads();
-    for (int b = t >> 6; b < nb; b += 16) { // wave-uniform
+    const unsigned long long below = (1ull << lane) - 1;
+    for (int b = t >> 6; b < nb; b += 16) {
         const int i = 64 * b + lane;
         const int k = i < n ? key[i] : -1;
-        int r = 0, c = 0;
-        unsigned long long rem = __ballot(k >= 0);
-        while (rem) { // one round per distinct key, all in registers
-            const int kl = __builtin_amdgcn_readlane(k, __builtin_ctzll(rem));
-            const unsigned long long m = __ballot(k == kl);
-            if (k == kl) {
-                r = __builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32),
-                                              __builtin_amdgcn_mbcnt_lo((unsigned)m, 0));
-                c = __popcll(m);
-            }
-            rem &= ~m;
-        }
         if (k >= 0) {
-            rk[i] = r;
-            if (r == 0) tab[b * nkeys + k] = c;
+            unsigned long long *m = tab + b * nkeys + k;
+            atomicOr(m, 1ull << lane);
+            // one wave's LDS operations complete in order, and the batch is
+            // this wave's alone: the read sees the bit of every lane of it
+            rk[i] = __popcll(*m & below);
         }
     }
     __syncthreads();
     for (int k = t; k < nkeys; k += 1024) {
-        int s = 0;
+        unsigned long long s = 0;
         for (int b = 0; b < nb; ++b) {
-            const int c = tab[b * nkeys + k];
+            const unsigned long long c = __popcll(tab[b * nkeys + k]);
             tab[b * nkeys + k] = s;
             s += c;
         }
-        off[k] = s;
+        off[k] = (int)s;
     }
     __syncthreads();
     lds_scan_1024(off, nkeys, lsum);
@@ -514,18 +507,36 @@ __host__ __device__ inline bool plan_fast_fits(int P, int T, int E)
            nb * T <= PLAN_FAST_TAB;
 }
 
+// Workgroup 0 makes the plan. With x given, workgroups 1, 2, ... also
+// write rmax[r] = the largest |x[r][k]| of token row r of x [T, K]
+// (infinity when the row holds a NaN), one wave per row.
 __global__ __launch_bounds__(1024) void moe_plan_fast_kernel(
     const int *__restrict__ ptok, const int *__restrict__ pexp, int P, int T, int E, int *eoff,
-    int *order, int *toff, int *tlist, int *tiles, int *ntiles, int chunk)
+    int *order, int *toff, int *tlist, int *tiles, int *ntiles, int chunk,
+    const float *__restrict__ x, int K, float *__restrict__ rmax)
 {
+    const int t = threadIdx.x;
+    if (blockIdx.x > 0) {
+        const int r = 16 * (blockIdx.x - 1) + (t >> 6);
+        if (r >= T) return;
+        const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)r * K);
+        float m = 0.f;
+        for (int i = t & 63; i < K / 4; i += 64) {
+            const float4 v = x4[i];
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+            if (v.x != v.x || v.y != v.y || v.z != v.z || v.w != v.w) m = INFINITY;
+        }
+        m = wave::max64(m);
+        if ((t & 63) == 0) rmax[r] = m;
+        return;
+    }
     __shared__ int key[PLAN_FAST];
     __shared__ int tok[PLAN_FAST];
-    __shared__ int rk[PLAN_FAST];
+    __shared__ int rk[PLAN_FAST + 1];
     __shared__ int ord[PLAN_FAST];
-    __shared__ int tab[PLAN_FAST_TAB];
+    __shared__ unsigned long long tab[PLAN_FAST_TAB];
     __shared__ int off[PLAN_FAST + 1];
     __shared__ int lsum[16];
-    const int t = threadIdx.x;
     for (int p = t; p < P; p += 1024) {
         const int tk = ptok[p], e = pexp[p];
         key[p] = tk >= 0 && tk < T && e >= 0 && e < E ? e : -1;
@@ -537,21 +548,21 @@ __global__ __launch_bounds__(1024) void moe_plan_fast_kernel(
     for (int e = t; e <= E; e += 1024) eoff[e] = off[e];
     for (int p = t; p < P; p += 1024) {
         const int e = key[p];
-        if (e >= 0) ord[off[e] + tab[(p >> 6) * E + e] + rk[p]] = p;
+        if (e >= 0) ord[off[e] + (int)tab[(p >> 6) * E + e] + rk[p]] = p;
     }
     __syncthreads();
     const int nv = off[E];
     for (int q = t; q < nv; q += 1024) order[q] = ord[q];
-    // chunk-token chunks of every expert (counts in tab, scanned)
-    for (int e = t; e < E; e += 1024) tab[e] = (off[e + 1] - off[e] + chunk - 1) / chunk;
+    // chunk-token chunks of every expert (counts in rk, scanned)
+    for (int e = t; e < E; e += 1024) rk[e] = (off[e + 1] - off[e] + chunk - 1) / chunk;
     __syncthreads();
-    lds_scan_1024(tab, E, lsum);
+    lds_scan_1024(rk, E, lsum);
     for (int e = t; e < E; e += 1024)
-        for (int c = 0; c < tab[e + 1] - tab[e]; ++c) {
-            tiles[2 * (tab[e] + c)] = e;
-            tiles[2 * (tab[e] + c) + 1] = c;
+        for (int c = 0; c < rk[e + 1] - rk[e]; ++c) {
+            tiles[2 * (rk[e] + c)] = e;
+            tiles[2 * (rk[e] + c) + 1] = c;
         }
-    if (t == 0) *ntiles = tab[E];
+    if (t == 0) *ntiles = rk[E];
     // for each token, its positions in ascending expert order
     for (int q = t; q < nv; q += 1024) key[q] = tok[ord[q]];
     __syncthreads();
@@ -559,7 +570,7 @@ __global__ __launch_bounds__(1024) void moe_plan_fast_kernel(
     for (int k = t; k <= T; k += 1024) toff[k] = off[k];
     for (int q = t; q < nv; q += 1024) {
         const int k = key[q];
-        tlist[off[k] + tab[(q >> 6) * T + k] + rk[q]] = q;
+        tlist[off[k] + (int)tab[(q >> 6) * T + k] + rk[q]] = q;
     }
 }
 
@@ -966,10 +977,14 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
     // 16-token chunk per expert (weight-bound); the LDS-tiled GEMM otherwise.
     const bool few = fmt_gu == Q4_K && fmt_down == Q4_K && moe_q4k_fits(hidden, mid) &&
                      npairs <= moe_q4k_chunk() * experts;
-    if (plan_fast_fits(npairs, tokens, experts))
-        hipLaunchKernelGGL(moe_plan_fast_kernel, dim3(1), dim3(1024), 0, st, ptok, pexp, npairs,
-                           tokens, experts, eoff, order, toff, tlist, tiles, ntiles,
-                           few ? moe_q4k_chunk() : BN);
+    // (the few-token kernels take the token rows' largest magnitudes from the
+    // plan's launch)
+    const bool fast = plan_fast_fits(npairs, tokens, experts);
+    if (fast)
+        hipLaunchKernelGGL(moe_plan_fast_kernel, dim3(few ? 1 + (tokens + 15) / 16 : 1),
+                           dim3(1024), 0, st, ptok, pexp, npairs, tokens, experts, eoff, order,
+                           toff, tlist, tiles, ntiles, few ? moe_q4k_chunk() : BN,
+                           few ? x : nullptr, hidden, (float *)(scratch + L.tmax));
     else if (npairs <= PLAN_SMALL && tokens <= PLAN_SMALL && experts <= PLAN_SMALL)
         hipLaunchKernelGGL(moe_plan_small_kernel, dim3(1), dim3(256), 0, st, ptok, pexp, npairs,
                            tokens, experts, eoff, order, toff, tlist, tiles, ntiles,
@@ -981,7 +996,7 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
     if (few) {
         float *outp2 = (float *)(scratch + L.outp2);
         int rc = launch_moe_q4k(gate, up, down, hidden, mid, x, tokens, ptok, eoff, eoff + experts,
-                                order, tiles, ntiles, L.max_tiles_few, npairs,
+                                order, tiles, ntiles, L.max_tiles_few, npairs, fast,
                                 (float *)(scratch + L.tmax), (_Float16 *)(scratch + L.xc),
                                 (_Float16 *)(scratch + L.xmc), (float *)(scratch + L.xsc),
                                 (float *)(scratch + L.gpart), (float *)(scratch + L.upart), h32,

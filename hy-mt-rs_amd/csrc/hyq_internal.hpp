@@ -210,15 +210,17 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
 // The Q4_K register-operand expert kernels (hyq_moe_q4k.hip) after a plan
 // of moe_q4k_chunk()-token chunks; xc/xmc/xsc and hc/hmc/hsc hold the
 // per-chunk activation operands of gate/up and of down, tmax / hmax the
-// largest magnitudes of the token rows and of the SiLU product rows, gpart /
-// upart the gate and up partial rows of the K slices [2][npairs][mid], outp2
-// the down product's second K slice.
+// largest magnitudes of the token rows (computed here unless have_tmax:
+// the plan's launch wrote them) and of the SiLU product rows, gpart / upart
+// the gate and up partial rows of the K slices [2][npairs][mid], outp2 the
+// down product's second K slice.
 int launch_moe_q4k(WView gate, WView up, WView down, int hidden, int mid, const float *x,
                    int tokens, const int *ptok, const int *eoff, const int *valid,
                    const int *order, const int *tiles, const int *ntiles, int max_tiles,
-                   int npairs, float *tmax, _Float16 *xc, _Float16 *xmc, float *xsc,
-                   float *gpart, float *upart, float *h32, float *hmax, _Float16 *hc,
-                   _Float16 *hmc, float *hsc, float *outp, float *outp2, void *stream);
+                   int npairs, bool have_tmax, float *tmax, _Float16 *xc, _Float16 *xmc,
+                   float *xsc, float *gpart, float *upart, float *h32, float *hmax,
+                   _Float16 *hc, _Float16 *hmc, float *hsc, float *outp, float *outp2,
+                   void *stream);
 // whether the register-operand kernels take these expert shapes
 bool moe_q4k_fits(int hidden, int mid);
 // K slices of the down product (1 or 2): outp2 is read when 2

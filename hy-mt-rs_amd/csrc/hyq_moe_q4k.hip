@@ -57,7 +57,6 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 constexpr int CHUNK = 16; // tokens per expert chunk (one MFMA column block)
 constexpr int MOE_Q4K_MAX_K = 4096;  // largest K (hidden or mid)
 constexpr int MOE_Q4K_MAX_KL = 2048; // largest K slice of one workgroup: 34 KL bytes of LDS
-constexpr int DOWN_RG = 2;           // down: groups of 128 rows per workgroup
 
 // K slices of the gate/up product: two when its superblocks split evenly
 // (the tiles then number twice the workgroups, which evens out the last
@@ -160,208 +159,204 @@ __device__ __forceinline__ void superblock(const WRaw &w, const XRaw &x, int g, 
     }
 }
 
-// R row tiles (rows[r] = the tile's first weight row, 16 rows each, of
-// matrices w[r]) against one chunk's activation operand over K: acc[r].
-// Called by all 256 threads of the workgroup. The chunk's whole activation
-// operand (xc: 16 K halves in MFMA lane order, xmc: K half-sums) is copied
-// into LDS once (xl), and each wave then streams its weights through four
-// register sets, three superblocks ahead of the compute: the loop holds no
-// barrier and no other global load, so the compiler's in-order load count
-// waits for exactly the set being used. The first three weight superblocks
-// are issued after the activation loads and before their LDS stores, so
-// their latency overlaps the copy. Past the last superblock the weight loads
-// read an L2-hot dummy (the activation operand), so every step issues the
-// same loads without a branch.
+// Work units. A unit is one 16-token chunk ti of an expert, one K slice kh
+// and one group mg of 64 weight rows (wave w of the workgroup takes rows
+// 16 w .. 16 w + 15 of the group, of each matrix it streams):
+// u = (ti ks + kh) mgroups + mg, so the units that share one activation
+// operand (ti, kh) are consecutive. The grid is a fixed count of
+// workgroups, a multiple of 8 sized to be resident at once, and the unit
+// count U = *ntiles ks mgroups is known only on the device. Workgroup b
+// runs on XCD b % 8 (round-robin dispatch): XCD x takes the units
+// [x U / 8, (x + 1) U / 8) and its j-th of W workgroups the j-th of W even
+// shares of them. Every workgroup thus gets the same number of units to
+// within one (no last round of a few workgroups on an idle chip), and a
+// chunk's units stay on one or two XCDs, whose L2 holds its operand.
+__device__ __forceinline__ void unit_range(int U, int &u0, int &u1)
+{
+    const int per = (int)gridDim.x / 8, x = (int)(blockIdx.x % 8), j = (int)(blockIdx.x / 8);
+    const int ux0 = (int)((long)U * x / 8), n = (int)((long)U * (x + 1) / 8) - ux0;
+    u0 = ux0 + (int)((long)n * j / per);
+    u1 = ux0 + (int)((long)n * (j + 1) / per);
+}
+
+// The workgroup's units [u0, u1) against R matrices (all 256 threads). Per
+// run of units that share an activation operand, the chunk's operand slice
+// (xc: 16 K halves in MFMA lane order, xmc: K half-sums) is copied into LDS
+// once (xl), and each wave then streams its weights through NS register
+// sets, NS - 1 superblocks ahead of the compute, across the run's row
+// groups: stream position p is superblock p % nbk of the run's group
+// p / nbk. The loop holds no barrier and no other global load, so the
+// compiler's in-order load count waits for exactly the set being used. The
+// first NS - 1 weight loads are issued after the activation loads and
+// before their LDS stores, so their latency overlaps the copy; past the
+// run's last superblock the weight loads read an L2-hot dummy (the
+// activation operand), so every step issues the same loads.
 //
-// With RG > 1 the wave streams RG row groups one after another against the
-// same activation operand (group g at rows rows[r] + g gstride, into
-// acc[g R + r]): one stream of RG nbk superblocks, its prefetch running
-// across the group boundaries, so a workgroup's startup (the activation
-// copy, the first loads) is paid once per RG groups. nbk must then be a
-// multiple of 4, or with PAIRS be 2 mod 4 with RG even (the stream then
-// holds whole rounds of the four-set ring per group or per pair of groups).
-template <int R, int RG = 1, bool PAIRS = false>
-__device__ __forceinline__ void tile_rows(const WView *w, const int *rows, int kb0, int nbk,
-                                          const _Float16 *xc, const _Float16 *xmc, uint4 *xl,
-                                          f4 *acc, int gstride = 0)
+// run(ti, kh, mg, qp, mp, gq, gm) sets, for the run's first group mg, the
+// lane's row pointers of each matrix at the slice start (qs and header
+// planes) and the byte steps from one group to the next, and loads what
+// flush needs; flush(gj, acc) takes the sums of the run's group gj when its
+// last superblock is done (acc then restarts from zero).
+template <int R, int NS, class Run, class Flush>
+__device__ __forceinline__ void stream_units(int u0, int u1, int mgroups, int ks, int nbk,
+                                             const _Float16 *xc, const _Float16 *xmc, uint4 *xl,
+                                             Run run, Flush flush)
 {
     uint32_t magic;
     asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
-    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, rr = lane & 15;
-    const int K = 256 * nbk; // the slice: superblocks kb0 .. kb0 + nbk - 1
-    const uint8_t *qp[R], *mp[R];
-    size_t gq[R], gm[R]; // bytes from one row group to the next
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const size_t blk = (size_t)(rows[r] + rr) * w[r].nb + kb0;
-        qp[r] = w[r].p0 + blk * 128 + 16 * g;
-        mp[r] = w[r].p1 + blk * 16;
-        gq[r] = (size_t)gstride * w[r].nb * 128;
-        gm[r] = (size_t)gstride * w[r].nb * 16;
-    }
-#pragma unroll
-    for (int i = 0; i < RG * R; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
-    const uint8_t *dummy = reinterpret_cast<const uint8_t *>(xc); // >= 144 bytes, L2-hot
-    WRaw w0[R], w1[R], w2[R], w3[R];
-    // superblock j of the stream (group j / nbk, superblock j % nbk)
-    auto loadw = [&](WRaw *wr, int j) {
-        const int gj = RG == 1 ? 0 : j / nbk, sj = RG == 1 ? j : j - gj * nbk;
-        const bool in = gj < RG && sj < nbk;
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const uint8_t *q = in ? qp[r] + gj * gq[r] + sj * 128 : dummy;
-            const uint8_t *m = in ? mp[r] + gj * gm[r] + sj * 16 : dummy;
-            wr[r].q0 = *reinterpret_cast<const uint4 *>(q);
-            wr[r].q1 = *reinterpret_cast<const uint4 *>(q + 64);
-            wr[r].meta = *reinterpret_cast<const uint4 *>(m);
-        }
-    };
-    // the slice's activation operand: 2K uint4 of steps and K/4 uint2 of
-    // half-sums (K <= MOE_Q4K_MAX_KL: at most 16 and 2 per thread)
-    const uint4 *xs = reinterpret_cast<const uint4 *>(xc) + 512 * kb0;
-    const uint2 *ms = reinterpret_cast<const uint2 *>(xmc) + 64 * kb0;
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4;
+    const int K = 256 * nbk, KF = K * ks; // the slice and the whole row
     uint2 *xlm = reinterpret_cast<uint2 *>(xl + 2 * K);
-    uint4 tv[MOE_Q4K_MAX_KL / 128];
-    uint2 tm[MOE_Q4K_MAX_KL / 1024];
-    // (loads clamped into bounds and issued unconditionally)
+    for (int u = u0; u < u1;) {
+        const int blk = u / mgroups, nr = min(u1, (blk + 1) * mgroups) - u;
+        const int ti = blk / ks, kh = blk - ti * ks;
+        const uint8_t *qp[R], *mp[R];
+        size_t gq[R], gm[R];
+        run(ti, kh, u - blk * mgroups, qp, mp, gq, gm);
+        const _Float16 *xct = xc + (size_t)ti * CHUNK * KF;
+        const uint8_t *dummy = reinterpret_cast<const uint8_t *>(xct); // >= 144 bytes, L2-hot
+        WRaw ring[NS][R];
+        int lg = 0, ls = 0; // the next stream position to load: group, superblock
+        auto loadw = [&](WRaw *wr) {
+            const bool in = lg < nr;
 #pragma unroll
-    for (int j = 0; j < MOE_Q4K_MAX_KL / 128; ++j) tv[j] = xs[min(tid + 256 * j, 2 * K - 1)];
+            for (int r = 0; r < R; ++r) {
+                const uint8_t *q = in ? qp[r] + lg * gq[r] + ls * 128 : dummy;
+                const uint8_t *m = in ? mp[r] + lg * gm[r] + ls * 16 : dummy;
+                wr[r].q0 = *reinterpret_cast<const uint4 *>(q);
+                wr[r].q1 = *reinterpret_cast<const uint4 *>(q + 64);
+                wr[r].meta = *reinterpret_cast<const uint4 *>(m);
+            }
+            if (++ls == nbk) {
+                ls = 0;
+                ++lg;
+            }
+        };
+        // the slice's operand: 2K uint4 of steps and K/4 uint2 of half-sums
+        // (K <= MOE_Q4K_MAX_KL: at most 16 and 2 per thread; loads clamped
+        // into bounds and issued unconditionally)
+        // (the thread index made opaque per run, so that the copy's 2 x 16
+        // clamped addresses are not hoisted out of the loop and held in
+        // registers through the stream)
+        int t = tid;
+        asm volatile("" : "+v"(t));
+        const uint4 *xs = reinterpret_cast<const uint4 *>(xct) + 512 * kh * nbk;
+        const uint2 *ms = reinterpret_cast<const uint2 *>(xmc + (size_t)ti * KF) + 64 * kh * nbk;
+        // (staged in clang vectors: HIP's uint4 struct copies stay in scratch)
+        typedef unsigned u4v __attribute__((ext_vector_type(4)));
+        typedef unsigned u2v __attribute__((ext_vector_type(2)));
+        const u4v *xs4 = reinterpret_cast<const u4v *>(xs);
+        const u2v *ms2 = reinterpret_cast<const u2v *>(ms);
+        u4v tv[MOE_Q4K_MAX_KL / 128];
+        u2v tm[MOE_Q4K_MAX_KL / 1024];
 #pragma unroll
-    for (int j = 0; j < MOE_Q4K_MAX_KL / 1024; ++j) tm[j] = ms[min(tid + 256 * j, K / 4 - 1)];
-    loadw(w0, 0);
-    loadw(w1, 1);
-    loadw(w2, 2);
-    // (stores unconditional too, so that no load sinks into a branch: the
-    // clamped duplicates rewrite the last element with its own value)
+        for (int j = 0; j < MOE_Q4K_MAX_KL / 128; ++j) tv[j] = xs4[min(t + 256 * j, 2 * K - 1)];
 #pragma unroll
-    for (int j = 0; j < MOE_Q4K_MAX_KL / 128; ++j) xl[min(tid + 256 * j, 2 * K - 1)] = tv[j];
+        for (int j = 0; j < MOE_Q4K_MAX_KL / 1024; ++j) tm[j] = ms2[min(t + 256 * j, K / 4 - 1)];
 #pragma unroll
-    for (int j = 0; j < MOE_Q4K_MAX_KL / 1024; ++j) xlm[min(tid + 256 * j, K / 4 - 1)] = tm[j];
-    HYQ_LGKM0();
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-    auto compute = [&](const WRaw *wr, int b, f4 *ac) {
-        XRaw xr;
+        for (int k = 0; k < NS - 1; ++k) loadw(ring[k]);
+        // every wave is done reading the previous run's operand (its LDS
+        // reads have returned: lgkmcnt 0) before any wave overwrites it
+        HYQ_LGKM0();
+        asm volatile("s_barrier" ::: "memory");
+        // (stores unconditional too, so that no load sinks into a branch:
+        // the clamped duplicates rewrite the last element with its own value)
 #pragma unroll
-        for (int t = 0; t < 8; ++t) xr.v[t] = xl[512 * b + 64 * t + lane];
-        xr.m = xlm[64 * b + lane];
+        for (int j = 0; j < MOE_Q4K_MAX_KL / 128; ++j)
+            reinterpret_cast<u4v *>(xl)[min(t + 256 * j, 2 * K - 1)] = tv[j];
 #pragma unroll
-        for (int r = 0; r < R; ++r) superblock(wr[r], xr, g, magic, ac[r]);
-    };
-    // superblock b of group gg from wc, prefetching stream position
-    // gg nbk + b + 3 into wn
-    auto step = [&](WRaw *wc, WRaw *wn, int gg, int b, f4 *ac) {
-        loadw(wn, gg * nbk + b + 3);
+        for (int j = 0; j < MOE_Q4K_MAX_KL / 1024; ++j)
+            reinterpret_cast<u2v *>(xlm)[min(t + 256 * j, K / 4 - 1)] = tm[j];
+        HYQ_LGKM0();
+        asm volatile("s_barrier" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
-        compute(wc, b, ac);
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    // stream position p computes from set p % 4 and prefetches into set
-    // (p + 3) % 4
-    if constexpr (!PAIRS) {
+        f4 acc[R];
 #pragma unroll
-        for (int gg = 0; gg < RG; ++gg) {
-            f4 *ac = acc + gg * R;
-            int b = 0;
-            for (; b + 4 <= nbk; b += 4) {
-                step(w0, w3, gg, b, ac);
-                step(w1, w0, gg, b + 1, ac);
-                step(w2, w1, gg, b + 2, ac);
-                step(w3, w2, gg, b + 3, ac);
-            }
-            if (RG == 1) {
-                if (b < nbk) step(w0, w3, gg, b, ac);
-                if (b + 1 < nbk) step(w1, w0, gg, b + 1, ac);
-                if (b + 2 < nbk) step(w2, w1, gg, b + 2, ac);
-            }
-        }
-    } else {
-        // PAIRS (nbk % 4 == 2, RG even): a pair of groups is 2 nbk
-        // positions, a multiple of 4; the second group of the pair starts at
-        // set 2
-        static_assert(RG % 2 == 0, "row groups stream in pairs");
+        for (int r = 0; r < R; ++r) acc[r] = f4{0.f, 0.f, 0.f, 0.f};
+        int cg = 0, cs = 0; // the stream position being computed
+        auto step = [&](WRaw *wc, WRaw *wn) {
+            loadw(wn);
+            __builtin_amdgcn_sched_barrier(0);
+            XRaw xr;
 #pragma unroll
-        for (int gg = 0; gg < RG; gg += 2) {
-            f4 *ac = acc + gg * R, *ac2 = ac + R;
-            int b = 0;
-            for (; b + 4 <= nbk; b += 4) {
-                step(w0, w3, gg, b, ac);
-                step(w1, w0, gg, b + 1, ac);
-                step(w2, w1, gg, b + 2, ac);
-                step(w3, w2, gg, b + 3, ac);
+            for (int t = 0; t < 8; ++t) xr.v[t] = xl[512 * cs + 64 * t + lane];
+            xr.m = xlm[64 * cs + lane];
+#pragma unroll
+            for (int r = 0; r < R; ++r) superblock(wc[r], xr, g, magic, acc[r]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (++cs == nbk) {
+                flush(cg, acc);
+#pragma unroll
+                for (int r = 0; r < R; ++r) acc[r] = f4{0.f, 0.f, 0.f, 0.f};
+                cs = 0;
+                ++cg;
             }
-            step(w0, w3, gg, b, ac);
-            step(w1, w0, gg, b + 1, ac);
-            step(w2, w1, gg + 1, 0, ac2);
-            step(w3, w2, gg + 1, 1, ac2);
-            for (b = 2; b + 4 <= nbk; b += 4) {
-                step(w0, w3, gg + 1, b, ac2);
-                step(w1, w0, gg + 1, b + 1, ac2);
-                step(w2, w1, gg + 1, b + 2, ac2);
-                step(w3, w2, gg + 1, b + 3, ac2);
-            }
+        };
+        const int np = nr * nbk;
+        int p = 0;
+        for (; p + NS <= np; p += NS) {
+#pragma unroll
+            for (int k = 0; k < NS; ++k) step(ring[k], ring[(k + NS - 1) % NS]);
         }
+#pragma unroll
+        for (int k = 0; k < NS - 1; ++k)
+            if (p + k < np) step(ring[k], ring[(k + NS - 1) % NS]);
+        u += nr;
     }
 }
 
-// Workgroup order. Workgroups are dispatched round-robin over the 8 XCDs
-// (workgroup b runs on XCD b % 8), and every workgroup of a chunk reads the
-// chunk's whole activation operand, so a chunk's workgroups share one XCD
-// and its L2: chunk ti runs on XCD ti % 8, as workgroups b = 8 k + ti % 8
-// with k = mgroups (ti / 8) + mg. The chunk count is known only on the
-// device: the grid covers the largest count, and on every XCD the
-// workgroups past it come last and exit.
-__device__ __forceinline__ bool chunk_tile(int mgroups, int max_tiles, const int *ntiles, int &ti,
-                                           int &mg)
-{
-    const int xcd = (int)(blockIdx.x % 8), k = (int)(blockIdx.x / 8);
-    ti = xcd + 8 * (k / mgroups);
-    mg = k % mgroups;
-    return ti < max_tiles && ti < *ntiles;
-}
+inline int unit_grid(int cus) { return 8 * ((2 * cus + 7) / 8); } // two workgroups per CU
 
-inline int chunk_grid(int mgroups, int max_tiles) { return 8 * mgroups * ((max_tiles + 7) / 8); }
-
-//
-// Gate and up of one 16-token chunk of an expert over one K slice: wave w of
-// the workgroup takes mid rows m0 = 64 mg + 16 w of gate and of up; the
-// slice's sums, scaled back by the token column's scale, go to
-// gpart / upart[slice][q][m] for the chunk's pair positions q.
-template <int RG, bool PAIRS = false>
+// Gate and up of the units: wave w takes mid rows 64 mg + 16 w .. + 15 of
+// gate and of up for one chunk and K slice; the slice's sums, scaled back by
+// the token column's scale, go to gpart / upart[slice][q][m] for the chunk's
+// pair positions q.
 __global__ __launch_bounds__(256, 2) void moe_q4k_gate_up_kernel(
     WView gate, WView up, int mid, int K, const int *__restrict__ eoff,
     const int *__restrict__ tiles, const int *__restrict__ ntiles,
     const _Float16 *__restrict__ xc, const _Float16 *__restrict__ xmc,
     const float *__restrict__ xsc, float *__restrict__ gpart, float *__restrict__ upart,
-    size_t part_stride, int mgroups, int max_tiles)
+    size_t part_stride, int mgroups)
 {
-    const int ks = moe_kslices(K);
-    int ti, mgk;
-    if (!chunk_tile(mgroups / RG * ks, max_tiles, ntiles, ti, mgk)) return;
-    const int mg = mgk / ks * RG, kh = mgk % ks, nbk = K / 256 / ks;
-    const int e = tiles[2 * ti], c = tiles[2 * ti + 1];
-    const int nb = eoff[e] + c * CHUNK, cnt = min(CHUNK, eoff[e + 1] - nb);
-    const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
-    const int m0 = 64 * mg + 16 * (threadIdx.x >> 6);
+    const int ks = moe_kslices(K), nbk = K / 256 / ks;
+    int u0, u1;
+    unit_range(*ntiles * ks * mgroups, u0, u1);
+    const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15, w16 = 16 * (threadIdx.x >> 6);
     extern __shared__ uint4 xl[];
-    const WView w[2] = {gate, up};
-    const int rows[2] = {e * mid + m0, e * mid + m0};
-    f4 acc[2 * RG];
-    tile_rows<2, RG, PAIRS>(w, rows, kh * nbk, nbk, xc + (size_t)ti * CHUNK * K,
-                            xmc + (size_t)ti * K, xl, acc, 64);
-    // lane (g, rr): tokens 4g+i of mid row m0 + 64 gg + rr
+    int nb = 0, cnt = 0, kh = 0, mg0 = 0;
+    float s[4];
+    auto run = [&](int ti, int kh_, int mg, const uint8_t **qp, const uint8_t **mp, size_t *gq,
+                   size_t *gm) {
+        const int e = tiles[2 * ti], c = tiles[2 * ti + 1];
+        nb = eoff[e] + c * CHUNK;
+        cnt = min(CHUNK, eoff[e + 1] - nb);
+        kh = kh_;
+        mg0 = mg;
+        const int row = e * mid + 64 * mg + w16 + col;
 #pragma unroll
-    for (int gg = 0; gg < RG; ++gg) {
-        const size_t base = kh * part_stride + (size_t)nb * mid + m0 + 64 * gg + col;
+        for (int r = 0; r < 2; ++r) {
+            const WView &W = r ? up : gate;
+            const size_t blk = (size_t)row * W.nb + kh * nbk;
+            qp[r] = W.p0 + blk * 128 + 16 * g;
+            mp[r] = W.p1 + blk * 16;
+            gq[r] = (size_t)64 * W.nb * 128;
+            gm[r] = (size_t)64 * W.nb * 16;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[i] = xsc[ti * CHUNK + 4 * g + i];
+    };
+    // lane (g, col): tokens 4g+i of mid row 64 (mg0 + gj) + 16 w + col
+    auto flush = [&](int gj, const f4 *acc) {
+        const size_t base = kh * part_stride + (size_t)nb * mid + 64 * (mg0 + gj) + w16 + col;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int tok = 4 * g + i;
             if (tok >= cnt) continue;
-            const float s = xsc[ti * CHUNK + tok];
-            gpart[base + (size_t)tok * mid] = acc[2 * gg][i] * s;
-            upart[base + (size_t)tok * mid] = acc[2 * gg + 1][i] * s;
+            gpart[base + (size_t)tok * mid] = acc[0][i] * s[i];
+            upart[base + (size_t)tok * mid] = acc[1][i] * s[i];
         }
-    }
+    };
+    stream_units<2, 4>(u0, u1, mgroups, ks, nbk, xc, xmc, xl, run, flush);
 }
 
 // h[q][m] = silu(g) * u with g, u the sums of the K slices' partial rows (in
@@ -397,44 +392,47 @@ __global__ __launch_bounds__(256) void silu_rows_kernel(const float *__restrict_
     if (t == 0) hmax[q] = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
 }
 
-// Down of one 16-token chunk over one K slice: wave w takes hidden rows
-// m0 = 128 mg + 32 w .. m0 + 31 (two row tiles) and, with RG > 1, the same
-// rows of the next RG - 1 groups of 128 rows; the slice's sums
-// down_e[m] . H[q], scaled back, go to outp (slice 0) or outp2 (slice 1).
-template <int RG, bool PAIRS = false>
+// Down of the units (one K slice): wave w takes hidden rows 64 mg + 16 w ..
+// + 15 for one chunk; the sums down_e[m] . H[q], scaled back, go to outp.
+// One matrix per wave, so eight register sets (seven superblocks ahead)
+// keep as many bytes in flight as gate/up's four sets of two matrices.
 __global__ __launch_bounds__(256, 2) void moe_q4k_down_kernel(
     WView down, int hidden, int K, const int *__restrict__ eoff, const int *__restrict__ tiles,
     const int *__restrict__ ntiles, const _Float16 *__restrict__ hc,
     const _Float16 *__restrict__ hmc, const float *__restrict__ hsc, float *__restrict__ outp,
-    float *__restrict__ outp2, int mgroups, int max_tiles)
+    int mgroups)
 {
-    const int ks = 1;
-    int ti, mgk;
-    if (!chunk_tile(mgroups / RG * ks, max_tiles, ntiles, ti, mgk)) return;
-    const int mg = mgk / ks * RG, kh = mgk % ks, nbk = K / 256 / ks;
-    const int m0 = 128 * mg + 32 * (threadIdx.x >> 6); // hidden % 128 == 0: all rows exist
-    const int e = tiles[2 * ti], c = tiles[2 * ti + 1];
-    const int nb = eoff[e] + c * CHUNK, cnt = min(CHUNK, eoff[e + 1] - nb);
-    const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
+    const int nbk = K / 256;
+    int u0, u1;
+    unit_range(*ntiles * mgroups, u0, u1);
+    const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15, w16 = 16 * (threadIdx.x >> 6);
     extern __shared__ uint4 xl[];
-    const WView w[2] = {down, down};
-    const int rows[2] = {e * hidden + m0, e * hidden + m0 + 16};
-    f4 acc[2 * RG];
-    tile_rows<2, RG, PAIRS>(w, rows, kh * nbk, nbk, hc + (size_t)ti * CHUNK * K,
-                            hmc + (size_t)ti * K, xl, acc, 128);
-    float *dst = kh ? outp2 : outp;
-    // lane (g, rr): tokens 4g+i of hidden rows m0 + 128 gg + 16r + rr
+    int nb = 0, cnt = 0, mg0 = 0;
+    float s[4];
+    auto run = [&](int ti, int, int mg, const uint8_t **qp, const uint8_t **mp, size_t *gq,
+                   size_t *gm) {
+        const int e = tiles[2 * ti], c = tiles[2 * ti + 1];
+        nb = eoff[e] + c * CHUNK;
+        cnt = min(CHUNK, eoff[e + 1] - nb);
+        mg0 = mg;
+        const size_t blk = (size_t)(e * hidden + 64 * mg + w16 + col) * down.nb;
+        qp[0] = down.p0 + blk * 128 + 16 * g;
+        mp[0] = down.p1 + blk * 16;
+        gq[0] = (size_t)64 * down.nb * 128;
+        gm[0] = (size_t)64 * down.nb * 16;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int tok = 4 * g + i;
-        if (tok >= cnt) continue;
-        const float s = hsc[ti * CHUNK + tok];
-        float *orow = dst + (size_t)(nb + tok) * hidden + m0 + col;
+        for (int i = 0; i < 4; ++i) s[i] = hsc[ti * CHUNK + 4 * g + i];
+    };
+    // lane (g, col): tokens 4g+i of hidden row 64 (mg0 + gj) + 16 w + col
+    auto flush = [&](int gj, const f4 *acc) {
 #pragma unroll
-        for (int gg = 0; gg < RG; ++gg)
-#pragma unroll
-            for (int r = 0; r < 2; ++r) orow[128 * gg + 16 * r] = acc[2 * gg + r][i] * s;
-    }
+        for (int i = 0; i < 4; ++i) {
+            const int tok = 4 * g + i;
+            if (tok >= cnt) continue;
+            outp[(size_t)(nb + tok) * hidden + 64 * (mg0 + gj) + w16 + col] = acc[0][i] * s[i];
+        }
+    };
+    stream_units<1, 8>(u0, u1, mgroups, 1, nbk, hc, hmc, xl, run, flush);
 }
 
 // rmax[r] = the largest |x[r][k]| of row r of x [rows, K] (infinity when the
@@ -511,54 +509,31 @@ __global__ __launch_bounds__(64) void chunk_q4k_kernel(
 int launch_moe_q4k(WView gate, WView up, WView down, int hidden, int mid, const float *x,
                    int tokens, const int *ptok, const int *eoff, const int *valid,
                    const int *order, const int *tiles, const int *ntiles, int max_tiles,
-                   int npairs, float *tmax, _Float16 *xc, _Float16 *xmc, float *xsc,
-                   float *gpart, float *upart, float *h32, float *hmax, _Float16 *hc,
-                   _Float16 *hmc, float *hsc, float *outp, float *outp2, void *stream)
+                   int npairs, bool have_tmax, float *tmax, _Float16 *xc, _Float16 *xmc,
+                   float *xsc, float *gpart, float *upart, float *h32, float *hmax,
+                   _Float16 *hc, _Float16 *hmc, float *hsc, float *outp, float *outp2,
+                   void *stream)
 {
     if (!moe_q4k_fits(hidden, mid)) return (int)hipErrorInvalidValue;
     hipStream_t st = (hipStream_t)stream;
     const size_t gstride = (size_t)npairs * mid;
-    hipLaunchKernelGGL(row_max_kernel, dim3(tokens), dim3(256), 0, st, x, hidden, tmax);
+    if (!have_tmax)
+        hipLaunchKernelGGL(row_max_kernel, dim3(tokens), dim3(256), 0, st, x, hidden, tmax);
     hipLaunchKernelGGL(chunk_q4k_kernel, dim3(max_tiles, hidden / 256), dim3(64), 0, st, x, hidden,
                        tmax, tiles, ntiles, eoff, order, ptok, xc, xmc, xsc);
-    {
-        // row groups per workgroup: 6 or 4 (mid is a multiple of 256, so
-        // the 64-row groups number a multiple of 4) when the slice's
-        // superblocks fill the register ring (see tile_rows)
-        const int mgroups = mid / 64, ks = moe_kslices(hidden), nbk = hidden / 256 / ks;
-        const size_t lds = (size_t)34 * (hidden / ks);
-        auto launch = [&](auto kern, int rg) {
-            hipLaunchKernelGGL(kern, dim3(chunk_grid(mgroups / rg * ks, max_tiles)), dim3(256),
-                               lds, st, gate, up, mid, hidden, eoff, tiles, ntiles, xc, xmc, xsc,
-                               gpart, upart, gstride, mgroups, max_tiles);
-        };
-        if (nbk % 2 != 0) launch(moe_q4k_gate_up_kernel<1>, 1);
-        else if (nbk % 4 == 2) // (6 groups in pairs spill to scratch)
-            launch(moe_q4k_gate_up_kernel<4, true>, 4);
-        else
-            mgroups % 6 == 0 ? launch(moe_q4k_gate_up_kernel<6>, 6)
-                             : launch(moe_q4k_gate_up_kernel<4>, 4);
-    }
+    int dev = 0, cus = 0;
+    hipGetDevice(&dev);
+    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    const dim3 grid(unit_grid(cus));
+    hipLaunchKernelGGL(moe_q4k_gate_up_kernel, grid, dim3(256),
+                       (size_t)34 * (hidden / moe_kslices(hidden)), st, gate, up, mid, hidden,
+                       eoff, tiles, ntiles, xc, xmc, xsc, gpart, upart, gstride, mid / 64);
     hipLaunchKernelGGL(silu_rows_kernel, dim3(npairs), dim3(256), 0, st, gpart, upart,
                        moe_kslices(hidden), gstride, mid, valid, h32, hmax);
     hipLaunchKernelGGL(chunk_q4k_kernel, dim3(max_tiles, mid / 256), dim3(64), 0, st, h32, mid,
                        hmax, tiles, ntiles, eoff, nullptr, nullptr, hc, hmc, hsc);
-    {
-        // groups of 128 rows per workgroup: DOWN_RG when they divide and the
-        // superblocks fill the register ring (see tile_rows)
-        const int mgroups = hidden / 128, nbk = mid / 256;
-        auto launch = [&](auto kern, int rg) {
-            hipLaunchKernelGGL(kern, dim3(chunk_grid(mgroups / rg, max_tiles)), dim3(256),
-                               (size_t)34 * mid, st, down, hidden, mid, eoff, tiles, ntiles, hc,
-                               hmc, hsc, outp, outp2, mgroups, max_tiles);
-        };
-        if (nbk % 4 == 0 && mgroups % DOWN_RG == 0)
-            launch(moe_q4k_down_kernel<DOWN_RG>, DOWN_RG);
-        else if (nbk % 4 == 2 && mgroups % DOWN_RG == 0)
-            launch(moe_q4k_down_kernel<DOWN_RG, true>, DOWN_RG);
-        else
-            launch(moe_q4k_down_kernel<1>, 1);
-    }
+    hipLaunchKernelGGL(moe_q4k_down_kernel, grid, dim3(256), (size_t)34 * mid, st, down, hidden,
+                       mid, eoff, tiles, ntiles, hc, hmc, hsc, outp, hidden / 64);
     return (int)hipGetLastError();
 }
 
