@@ -16,6 +16,7 @@
 #include <algorithm>
 
 #include "hyq_f16rows.hpp"
+#include "hyq_moe_operand.hpp"
 #include "hyq_tile.hpp"
 #include "hyq_wave.hpp"
 
@@ -507,27 +508,24 @@ __host__ __device__ inline bool plan_fast_fits(int P, int T, int E)
            nb * T <= PLAN_FAST_TAB;
 }
 
-// Workgroup 0 makes the plan. With x given, workgroups 1, 2, ... also
-// write rmax[r] = the largest |x[r][k]| of token row r of x [T, K]
-// (infinity when the row holds a NaN), one wave per row.
+// Workgroup 0 makes the plan. With x given (the Q4_K register-operand
+// kernels), workgroups 1, 2, ... also form the row operand of each token row
+// of x [T, K] (wave_row_operand: xop, xhs, xsc), one wave per row, and the
+// plan also writes, per chunk column (ti, col), the pair position it takes
+// (cpos: the chunk's last pair for columns past its pairs) and that pair's
+// token (ctok).
 __global__ __launch_bounds__(1024) void moe_plan_fast_kernel(
     const int *__restrict__ ptok, const int *__restrict__ pexp, int P, int T, int E, int *eoff,
     int *order, int *toff, int *tlist, int *tiles, int *ntiles, int chunk,
-    const float *__restrict__ x, int K, float *__restrict__ rmax)
+    const float *__restrict__ x, int K, uint4 *__restrict__ xop, uint2 *__restrict__ xhs,
+    float *__restrict__ xsc, int *__restrict__ cpos, int *__restrict__ ctok)
 {
     const int t = threadIdx.x;
     if (blockIdx.x > 0) {
         const int r = 16 * (blockIdx.x - 1) + (t >> 6);
         if (r >= T) return;
-        const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)r * K);
-        float m = 0.f;
-        for (int i = t & 63; i < K / 4; i += 64) {
-            const float4 v = x4[i];
-            m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-            if (v.x != v.x || v.y != v.y || v.z != v.z || v.w != v.w) m = INFINITY;
-        }
-        m = wave::max64(m);
-        if ((t & 63) == 0) rmax[r] = m;
+        wave_row_operand(x + (size_t)r * K, K, xop + (size_t)r * (K / 8),
+                         xhs + (size_t)r * (K / 64), xsc + r);
         return;
     }
     __shared__ int key[PLAN_FAST];
@@ -561,6 +559,14 @@ __global__ __launch_bounds__(1024) void moe_plan_fast_kernel(
         for (int c = 0; c < rk[e + 1] - rk[e]; ++c) {
             tiles[2 * (rk[e] + c)] = e;
             tiles[2 * (rk[e] + c) + 1] = c;
+            if (cpos) {
+                const int nb = off[e] + c * chunk, last = min(chunk, off[e + 1] - nb) - 1;
+                for (int col = 0; col < chunk; ++col) {
+                    const int q = nb + min(col, last);
+                    cpos[(rk[e] + c) * chunk + col] = q;
+                    ctok[(rk[e] + c) * chunk + col] = tok[ord[q]];
+                }
+            }
         }
     if (t == 0) *ntiles = rk[E];
     // for each token, its positions in ascending expert order
@@ -939,14 +945,14 @@ MoeLayout moe_layout(int tokens, int npairs, int experts, int hidden, int mid)
     L.hscale = take(4 * (size_t)npairs);
     L.outp = take(4 * (size_t)npairs * hidden);
     const size_t cols = (size_t)L.max_tiles_few * few; // chunk columns of the Q4_K kernels
-    L.tmax = take(4 * (size_t)tokens);
-    L.hmax = take(4 * (size_t)npairs);
-    L.xc = take(2 * cols * hidden);
-    L.xmc = take(2 * (size_t)L.max_tiles_few * hidden);
-    L.xsc = take(4 * cols);
-    L.hc = take(2 * cols * mid);
-    L.hmc = take(2 * (size_t)L.max_tiles_few * mid);
-    L.hsc = take(4 * cols);
+    L.xop = take(2 * (size_t)tokens * hidden);
+    L.xhs = take((size_t)tokens * hidden / 8);
+    L.xsc = take(4 * (size_t)tokens);
+    L.hop = take(2 * (size_t)npairs * mid);
+    L.hhs = take((size_t)npairs * mid / 8);
+    L.hsc = take(4 * (size_t)npairs);
+    L.cpos = take(4 * cols);
+    L.ctok = take(4 * cols);
     L.gpart = take(4 * 2 * (size_t)npairs * mid);
     L.upart = take(4 * 2 * (size_t)npairs * mid);
     L.outp2 = take(4 * (size_t)npairs * hidden);
@@ -980,11 +986,16 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
     // (the few-token kernels take the token rows' largest magnitudes from the
     // plan's launch)
     const bool fast = plan_fast_fits(npairs, tokens, experts);
+    uint4 *xop = (uint4 *)(scratch + L.xop);
+    uint2 *xhs = (uint2 *)(scratch + L.xhs);
+    float *xsc = (float *)(scratch + L.xsc);
+    int *cpos = (int *)(scratch + L.cpos), *ctok = (int *)(scratch + L.ctok);
     if (fast)
         hipLaunchKernelGGL(moe_plan_fast_kernel, dim3(few ? 1 + (tokens + 15) / 16 : 1),
                            dim3(1024), 0, st, ptok, pexp, npairs, tokens, experts, eoff, order,
                            toff, tlist, tiles, ntiles, few ? moe_q4k_chunk() : BN,
-                           few ? x : nullptr, hidden, (float *)(scratch + L.tmax));
+                           few ? x : nullptr, hidden, xop, xhs, xsc, few ? cpos : nullptr,
+                           ctok);
     else if (npairs <= PLAN_SMALL && tokens <= PLAN_SMALL && experts <= PLAN_SMALL)
         hipLaunchKernelGGL(moe_plan_small_kernel, dim3(1), dim3(256), 0, st, ptok, pexp, npairs,
                            tokens, experts, eoff, order, toff, tlist, tiles, ntiles,
@@ -996,12 +1007,10 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
     if (few) {
         float *outp2 = (float *)(scratch + L.outp2);
         int rc = launch_moe_q4k(gate, up, down, hidden, mid, x, tokens, ptok, eoff, eoff + experts,
-                                order, tiles, ntiles, L.max_tiles_few, npairs, fast,
-                                (float *)(scratch + L.tmax), (_Float16 *)(scratch + L.xc),
-                                (_Float16 *)(scratch + L.xmc), (float *)(scratch + L.xsc),
-                                (float *)(scratch + L.gpart), (float *)(scratch + L.upart), h32,
-                                (float *)(scratch + L.hmax), (_Float16 *)(scratch + L.hc),
-                                (_Float16 *)(scratch + L.hmc), (float *)(scratch + L.hsc), outp,
+                                order, tiles, ntiles, L.max_tiles_few, npairs, fast, xop, xhs,
+                                xsc, cpos, ctok, (float *)(scratch + L.gpart),
+                                (float *)(scratch + L.upart), (uint4 *)(scratch + L.hop),
+                                (uint2 *)(scratch + L.hhs), (float *)(scratch + L.hsc), outp,
                                 outp2, stream);
         if (rc) return rc;
         hipLaunchKernelGGL(moe_combine_kernel, dim3((hidden + 255) / 256, tokens), dim3(256), 0,

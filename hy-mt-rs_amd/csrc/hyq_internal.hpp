@@ -197,7 +197,7 @@ int launch_gate_up_f16(int fmt, WView gate, WView up, int cols, const _Float16 *
 // Byte offsets of the MoE scratch regions (hyq_gemm.hip: moe_layout).
 struct MoeLayout {
     size_t eoff, order, rank, toff, tlist, tiles, ntiles, xg, xscale, h32, h, hscale, outp;
-    size_t tmax, xc, xmc, xsc, hmax, hc, hmc, hsc, gpart, upart, outp2, bytes;
+    size_t xop, xhs, xsc, hop, hhs, hsc, cpos, ctok, gpart, upart, outp2, bytes;
     int max_tiles, max_tiles_few;
 };
 MoeLayout moe_layout(int tokens, int npairs, int experts, int hidden, int mid);
@@ -208,19 +208,18 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
                int npairs, int experts, uint8_t *scratch, const MoeLayout &L, float *out,
                void *stream);
 // The Q4_K register-operand expert kernels (hyq_moe_q4k.hip) after a plan
-// of moe_q4k_chunk()-token chunks; xc/xmc/xsc and hc/hmc/hsc hold the
-// per-chunk activation operands of gate/up and of down, tmax / hmax the
-// largest magnitudes of the token rows (computed here unless have_tmax:
-// the plan's launch wrote them) and of the SiLU product rows, gpart / upart
-// the gate and up partial rows of the K slices [2][npairs][mid], outp2 the
-// down product's second K slice.
+// of moe_q4k_chunk()-token chunks. xop/xhs/xsc hold the row operands of the
+// token rows of x and hop/hhs/hsc those of the pairs' SiLU rows
+// (hyq_moe_operand.hpp), cpos / ctok each chunk column's pair position and
+// token (the column's rows), gpart / upart the gate and up partial rows of
+// the K slices [2][npairs][mid], outp2 the down product's second K slice.
+// have_ops: the plan's launch already wrote xop/xhs/xsc and cpos/ctok.
 int launch_moe_q4k(WView gate, WView up, WView down, int hidden, int mid, const float *x,
                    int tokens, const int *ptok, const int *eoff, const int *valid,
                    const int *order, const int *tiles, const int *ntiles, int max_tiles,
-                   int npairs, bool have_tmax, float *tmax, _Float16 *xc, _Float16 *xmc,
-                   float *xsc, float *gpart, float *upart, float *h32, float *hmax,
-                   _Float16 *hc, _Float16 *hmc, float *hsc, float *outp, float *outp2,
-                   void *stream);
+                   int npairs, bool have_ops, uint4 *xop, uint2 *xhs, float *xsc, int *cpos,
+                   int *ctok, float *gpart, float *upart, uint4 *hop, uint2 *hhs, float *hsc,
+                   float *outp, float *outp2, void *stream);
 // whether the register-operand kernels take these expert shapes
 bool moe_q4k_fits(int hidden, int mid);
 // K slices of the down product (1 or 2): outp2 is read when 2

@@ -28,19 +28,22 @@
 // 0x64006400 = (1024 + 16 q'(b0), ...) takes (sc'/16, -64 sc'); w >> 8 gives
 // b1 and b3 the same way.
 //
-// Activation operand (chunk_q4k_kernel). Per 16-token chunk, superblock b and
-// step t, 64 lanes x 16 bytes in lane order (lane = 16 g + column), so one
-// load instruction reads 1 KiB of consecutive bytes. Lane (g, col)'s 8 halves
-// for step t are x(a), x(a+2), x(a+1), x(a+3), x(a+32), x(a+34), x(a+33),
-// x(a+35) of token col with a = 256 b + 64 c + o, c = g/2 (+ 2 for t >= 4),
-// o = 16 (g & 1) + 4 (t & 3): the A and B lanes of an MFMA pair the same k.
-// The activations are the MFMA's A operand, the weights its B operand: output
-// lane l holds tokens 4 (l / 16) + i, i = 0..3, of weight row l % 16, the row
-// whose d and dmin the lane loaded.
+// Activation operand. Per 16-token chunk, superblock b and step t, 64
+// lanes x 16 bytes in lane order (lane = 16 g + column) in LDS. Lane (g,
+// col)'s 8 halves for step t are x(a), x(a+2), x(a+1), x(a+3), x(a+32),
+// x(a+34), x(a+33), x(a+35) of token col with a = 256 b + 64 c + o, c = g/2
+// (+ 2 for t >= 4), o = 16 (g & 1) + 4 (t & 3): the A and B lanes of an MFMA
+// pair the same k. Each column's pieces come from its row's operand
+// (hyq_moe_operand.hpp: a token row of x, formed in the plan's launch, or a
+// pair's SiLU row, formed by silu_rows_kernel), gathered while the operand
+// is copied into LDS. The activations are the MFMA's A operand, the weights
+// its B operand: output lane l holds tokens 4 (l / 16) + i, i = 0..3, of
+// weight row l % 16, the row whose d and dmin the lane loaded.
 #include <hip/hip_runtime.h>
 
 #include "hyq_f16rows.hpp"
 #include "hyq_internal.hpp"
+#include "hyq_moe_operand.hpp"
 #include "hyq_wave.hpp"
 
 #pragma clang fp contract(off)
@@ -181,40 +184,41 @@ __device__ __forceinline__ void unit_range(int U, int &u0, int &u1)
 
 // The workgroup's units [u0, u1) against R matrices (all 256 threads). Per
 // run of units that share an activation operand, the chunk's operand slice
-// (xc: 16 K halves in MFMA lane order, xmc: K half-sums) is copied into LDS
-// once (xl), and each wave then streams its weights through NS register
+// (16 K halves in MFMA lane order and the K / 4 half-sums, gathered from the
+// columns' row operands) is copied into LDS once (xl), and each wave then streams its weights through NS register
 // sets, NS - 1 superblocks ahead of the compute, across the run's row
 // groups: stream position p is superblock p % nbk of the run's group
 // p / nbk. The loop holds no barrier and no other global load, so the
 // compiler's in-order load count waits for exactly the set being used. The
 // first NS - 1 weight loads are issued after the activation loads and
 // before their LDS stores, so their latency overlaps the copy; past the
-// run's last superblock the weight loads read an L2-hot dummy (the
-// activation operand), so every step issues the same loads.
+// run's last superblock the weight loads read an L2-hot dummy (the thread's
+// column row operand), so every step issues the same loads.
 //
-// run(ti, kh, mg, qp, mp, gq, gm) sets, for the run's first group mg, the
-// lane's row pointers of each matrix at the slice start (qs and header
-// planes) and the byte steps from one group to the next, and loads what
-// flush needs; flush(gj, acc) takes the sums of the run's group gj when its
-// last superblock is done (acc then restarts from zero).
+// run(ti, kh, mg, qp, mp, gq, gm, xrow, mrow) sets, for the run's first
+// group mg, the lane's row pointers of each matrix at the slice start (qs
+// and header planes) and the byte steps from one group to the next, the row
+// operand (op and hs, hyq_moe_operand.hpp) of chunk column threadIdx.x % 16,
+// and loads what flush needs; flush(gj, acc) takes the sums of the run's
+// group gj when its last superblock is done (acc then restarts from zero).
 template <int R, int NS, class Run, class Flush>
 __device__ __forceinline__ void stream_units(int u0, int u1, int mgroups, int ks, int nbk,
-                                             const _Float16 *xc, const _Float16 *xmc, uint4 *xl,
-                                             Run run, Flush flush)
+                                             uint4 *xl, Run run, Flush flush)
 {
     uint32_t magic;
     asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4;
-    const int K = 256 * nbk, KF = K * ks; // the slice and the whole row
+    const int K = 256 * nbk; // the slice
     uint2 *xlm = reinterpret_cast<uint2 *>(xl + 2 * K);
     for (int u = u0; u < u1;) {
         const int blk = u / mgroups, nr = min(u1, (blk + 1) * mgroups) - u;
         const int ti = blk / ks, kh = blk - ti * ks;
         const uint8_t *qp[R], *mp[R];
         size_t gq[R], gm[R];
-        run(ti, kh, u - blk * mgroups, qp, mp, gq, gm);
-        const _Float16 *xct = xc + (size_t)ti * CHUNK * KF;
-        const uint8_t *dummy = reinterpret_cast<const uint8_t *>(xct); // >= 144 bytes, L2-hot
+        const uint4 *xrow;
+        const uint2 *mrow;
+        run(ti, kh, u - blk * mgroups, qp, mp, gq, gm, xrow, mrow);
+        const uint8_t *dummy = reinterpret_cast<const uint8_t *>(xrow); // >= 512 bytes, L2-hot
         WRaw ring[NS][R];
         int lg = 0, ls = 0; // the next stream position to load: group, superblock
         auto loadw = [&](WRaw *wr) {
@@ -233,26 +237,37 @@ __device__ __forceinline__ void stream_units(int u0, int u1, int mgroups, int ks
             }
         };
         // the slice's operand: 2K uint4 of steps and K/4 uint2 of half-sums
-        // (K <= MOE_Q4K_MAX_KL: at most 16 and 2 per thread; loads clamped
-        // into bounds and issued unconditionally)
+        // (K <= MOE_Q4K_MAX_KL: at most 16 and 2 per thread), element i of
+        // either in LDS lane order (column i % 16, the thread's own),
+        // gathered from the column's row operand; indices past the end are
+        // clamped to the last element of the thread's column, so every load
+        // and store is issued unconditionally and a duplicate rewrites its
+        // element with its own value
         // (the thread index made opaque per run, so that the copy's 2 x 16
-        // clamped addresses are not hoisted out of the loop and held in
+        // clamped indices are not hoisted out of the loop and held in
         // registers through the stream)
         int t = tid;
         asm volatile("" : "+v"(t));
-        const uint4 *xs = reinterpret_cast<const uint4 *>(xct) + 512 * kh * nbk;
-        const uint2 *ms = reinterpret_cast<const uint2 *>(xmc + (size_t)ti * KF) + 64 * kh * nbk;
+        const int last4 = 2 * K - 16 + (t & 15), last2 = K / 4 - 16 + (t & 15);
         // (staged in clang vectors: HIP's uint4 struct copies stay in scratch)
         typedef unsigned u4v __attribute__((ext_vector_type(4)));
         typedef unsigned u2v __attribute__((ext_vector_type(2)));
-        const u4v *xs4 = reinterpret_cast<const u4v *>(xs);
-        const u2v *ms2 = reinterpret_cast<const u2v *>(ms);
+        const u4v *xs4 = reinterpret_cast<const u4v *>(xrow) + MOE_OP_U4_PER_SB * kh * nbk;
+        const u2v *ms2 = reinterpret_cast<const u2v *>(mrow) + MOE_OP_U2_PER_SB * kh * nbk;
         u4v tv[MOE_Q4K_MAX_KL / 128];
         u2v tm[MOE_Q4K_MAX_KL / 1024];
 #pragma unroll
-        for (int j = 0; j < MOE_Q4K_MAX_KL / 128; ++j) tv[j] = xs4[min(t + 256 * j, 2 * K - 1)];
+        for (int j = 0; j < MOE_Q4K_MAX_KL / 128; ++j) {
+            // LDS element i = 512 superblock + 64 step + 16 g + col
+            const int i = min(t + 256 * j, last4);
+            tv[j] = xs4[MOE_OP_U4_PER_SB * (i >> 9) + 4 * ((i >> 6) & 7) + ((i >> 4) & 3)];
+        }
 #pragma unroll
-        for (int j = 0; j < MOE_Q4K_MAX_KL / 1024; ++j) tm[j] = ms2[min(t + 256 * j, K / 4 - 1)];
+        for (int j = 0; j < MOE_Q4K_MAX_KL / 1024; ++j) {
+            // LDS element i = 64 superblock + 16 g + col
+            const int i = min(t + 256 * j, last2);
+            tm[j] = ms2[MOE_OP_U2_PER_SB * (i >> 6) + ((i >> 4) & 3)];
+        }
 #pragma unroll
         for (int k = 0; k < NS - 1; ++k) loadw(ring[k]);
         // every wave is done reading the previous run's operand (its LDS
@@ -263,10 +278,10 @@ __device__ __forceinline__ void stream_units(int u0, int u1, int mgroups, int ks
         // the clamped duplicates rewrite the last element with its own value)
 #pragma unroll
         for (int j = 0; j < MOE_Q4K_MAX_KL / 128; ++j)
-            reinterpret_cast<u4v *>(xl)[min(t + 256 * j, 2 * K - 1)] = tv[j];
+            reinterpret_cast<u4v *>(xl)[min(t + 256 * j, last4)] = tv[j];
 #pragma unroll
         for (int j = 0; j < MOE_Q4K_MAX_KL / 1024; ++j)
-            reinterpret_cast<u2v *>(xlm)[min(t + 256 * j, K / 4 - 1)] = tm[j];
+            reinterpret_cast<u2v *>(xlm)[min(t + 256 * j, last2)] = tm[j];
         HYQ_LGKM0();
         asm volatile("s_barrier" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
@@ -308,13 +323,14 @@ __device__ __forceinline__ void stream_units(int u0, int u1, int mgroups, int ks
 inline int unit_grid(int cus) { return 8 * ((2 * cus + 7) / 8); } // two workgroups per CU
 
 // Gate and up of the units: wave w takes mid rows 64 mg + 16 w .. + 15 of
-// gate and of up for one chunk and K slice; the slice's sums, scaled back by
-// the token column's scale, go to gpart / upart[slice][q][m] for the chunk's
-// pair positions q.
+// gate and of up for one chunk and K slice; chunk column col reads the row
+// operand of token ctok[ti][col] (xop, xhs); the slice's sums, scaled back
+// by the token's scale xsc, go to gpart / upart[slice][q][m] for the
+// chunk's pair positions q.
 __global__ __launch_bounds__(256, 2) void moe_q4k_gate_up_kernel(
     WView gate, WView up, int mid, int K, const int *__restrict__ eoff,
     const int *__restrict__ tiles, const int *__restrict__ ntiles,
-    const _Float16 *__restrict__ xc, const _Float16 *__restrict__ xmc,
+    const int *__restrict__ ctok, const uint4 *__restrict__ xop, const uint2 *__restrict__ xhs,
     const float *__restrict__ xsc, float *__restrict__ gpart, float *__restrict__ upart,
     size_t part_stride, int mgroups)
 {
@@ -326,8 +342,11 @@ __global__ __launch_bounds__(256, 2) void moe_q4k_gate_up_kernel(
     int nb = 0, cnt = 0, kh = 0, mg0 = 0;
     float s[4];
     auto run = [&](int ti, int kh_, int mg, const uint8_t **qp, const uint8_t **mp, size_t *gq,
-                   size_t *gm) {
+                   size_t *gm, const uint4 *&xrow, const uint2 *&mrow) {
         const int e = tiles[2 * ti], c = tiles[2 * ti + 1];
+        const int tok = ctok[ti * CHUNK + col];
+        xrow = xop + (size_t)tok * (K / 8);
+        mrow = xhs + (size_t)tok * (K / 64);
         nb = eoff[e] + c * CHUNK;
         cnt = min(CHUNK, eoff[e + 1] - nb);
         kh = kh_;
@@ -343,7 +362,7 @@ __global__ __launch_bounds__(256, 2) void moe_q4k_gate_up_kernel(
             gm[r] = (size_t)64 * W.nb * 16;
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) s[i] = xsc[ti * CHUNK + 4 * g + i];
+        for (int i = 0; i < 4; ++i) s[i] = xsc[ctok[ti * CHUNK + 4 * g + i]];
     };
     // lane (g, col): tokens 4g+i of mid row 64 (mg0 + gj) + 16 w + col
     auto flush = [&](int gj, const f4 *acc) {
@@ -356,19 +375,22 @@ __global__ __launch_bounds__(256, 2) void moe_q4k_gate_up_kernel(
             upart[base + (size_t)tok * mid] = acc[1][i] * s[i];
         }
     };
-    stream_units<2, 4>(u0, u1, mgroups, ks, nbk, xc, xmc, xl, run, flush);
+    stream_units<2, 4>(u0, u1, mgroups, ks, nbk, xl, run, flush);
 }
 
-// h[q][m] = silu(g) * u with g, u the sums of the K slices' partial rows (in
-// slice order), and hmax[q] = the row's largest |h| (infinity when it holds
-// a NaN); one workgroup per valid pair position q.
+// The SiLU rows of the pairs: h[m] = silu(g) * u with g, u the sums of the
+// K slices' partial rows (in slice order), formed as pair q's row operand
+// (hop, hhs, hsc: hyq_moe_operand.hpp, scaled by the row's largest |h|,
+// infinity when it holds a NaN); one workgroup per valid pair position q.
 __global__ __launch_bounds__(256) void silu_rows_kernel(const float *__restrict__ gpart,
                                                         const float *__restrict__ upart,
                                                         int ks, size_t part_stride, int mid,
                                                         const int *__restrict__ valid,
-                                                        float *__restrict__ h,
-                                                        float *__restrict__ hmax)
+                                                        uint4 *__restrict__ hop,
+                                                        uint2 *__restrict__ hhs,
+                                                        float *__restrict__ hsc)
 {
+    __shared__ __align__(16) float hl[MOE_Q4K_MAX_K];
     __shared__ float wred[4];
     const int q = blockIdx.x;
     if (q >= *valid) return;
@@ -382,14 +404,21 @@ __global__ __launch_bounds__(256) void silu_rows_kernel(const float *__restrict_
             uv = uv + upart[part_stride + row + i];
         }
         const float v = silu_mul(gv, uv);
-        h[row + i] = v;
+        hl[i] = v;
         m = fmaxf(m, fabsf(v));
         if (v != v) m = INFINITY;
     }
     m = wave::max64(m);
     if ((t & 63) == 0) wred[t >> 6] = m;
     __syncthreads();
-    if (t == 0) hmax[q] = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
+    const int e = f16_row_exponent(fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3])));
+    const float inv = ldexpf(1.0f, -e);
+    if (t == 0) hsc[q] = ldexpf(1.0f, e);
+    auto val = [&](int i) { return hl[i]; };
+    uint4 *op = hop + (size_t)q * (mid / 8);
+    uint32_t *hs = reinterpret_cast<uint32_t *>(hhs + (size_t)q * (mid / 64));
+    for (int it = t; it < 8 * (mid / 256); it += 256)
+        row_operand_item(val, inv, it >> 3, (it >> 1) & 3, it & 1, op, hs);
 }
 
 // Down of the units (one K slice): wave w takes hidden rows 64 mg + 16 w ..
@@ -398,8 +427,8 @@ __global__ __launch_bounds__(256) void silu_rows_kernel(const float *__restrict_
 // keep as many bytes in flight as gate/up's four sets of two matrices.
 __global__ __launch_bounds__(256, 2) void moe_q4k_down_kernel(
     WView down, int hidden, int K, const int *__restrict__ eoff, const int *__restrict__ tiles,
-    const int *__restrict__ ntiles, const _Float16 *__restrict__ hc,
-    const _Float16 *__restrict__ hmc, const float *__restrict__ hsc, float *__restrict__ outp,
+    const int *__restrict__ ntiles, const int *__restrict__ cpos, const uint4 *__restrict__ hop,
+    const uint2 *__restrict__ hhs, const float *__restrict__ hsc, float *__restrict__ outp,
     int mgroups)
 {
     const int nbk = K / 256;
@@ -410,8 +439,11 @@ __global__ __launch_bounds__(256, 2) void moe_q4k_down_kernel(
     int nb = 0, cnt = 0, mg0 = 0;
     float s[4];
     auto run = [&](int ti, int, int mg, const uint8_t **qp, const uint8_t **mp, size_t *gq,
-                   size_t *gm) {
+                   size_t *gm, const uint4 *&xrow, const uint2 *&mrow) {
         const int e = tiles[2 * ti], c = tiles[2 * ti + 1];
+        const int q = cpos[ti * CHUNK + col];
+        xrow = hop + (size_t)q * (K / 8);
+        mrow = hhs + (size_t)q * (K / 64);
         nb = eoff[e] + c * CHUNK;
         cnt = min(CHUNK, eoff[e + 1] - nb);
         mg0 = mg;
@@ -421,7 +453,7 @@ __global__ __launch_bounds__(256, 2) void moe_q4k_down_kernel(
         gq[0] = (size_t)64 * down.nb * 128;
         gm[0] = (size_t)64 * down.nb * 16;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) s[i] = hsc[ti * CHUNK + 4 * g + i];
+        for (int i = 0; i < 4; ++i) s[i] = hsc[cpos[ti * CHUNK + 4 * g + i]];
     };
     // lane (g, col): tokens 4g+i of hidden row 64 (mg0 + gj) + 16 w + col
     auto flush = [&](int gj, const f4 *acc) {
@@ -432,76 +464,39 @@ __global__ __launch_bounds__(256, 2) void moe_q4k_down_kernel(
             outp[(size_t)(nb + tok) * hidden + 64 * (mg0 + gj) + w16 + col] = acc[0][i] * s[i];
         }
     };
-    stream_units<1, 8>(u0, u1, mgroups, 1, nbk, hc, hmc, xl, run, flush);
+    stream_units<1, 8>(u0, u1, mgroups, 1, nbk, xl, run, flush);
 }
 
-// rmax[r] = the largest |x[r][k]| of row r of x [rows, K] (infinity when the
-// row holds a NaN), one workgroup per row.
-__global__ __launch_bounds__(256) void row_max_kernel(const float *__restrict__ x, int K,
-                                                      float *__restrict__ rmax)
+// The row operands of the token rows of x [T, K] (wave_row_operand), one
+// wave per row, when the plan's launch did not form them.
+__global__ __launch_bounds__(256) void row_operand_kernel(const float *__restrict__ x, int T,
+                                                          int K, uint4 *__restrict__ xop,
+                                                          uint2 *__restrict__ xhs,
+                                                          float *__restrict__ xsc)
 {
-    __shared__ float wred[4];
-    const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)blockIdx.x * K);
-    const int t = threadIdx.x;
-    float m = 0.f;
-    for (int i = t; i < K / 4; i += 256) {
-        const float4 v = x4[i];
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-        if (v.x != v.x || v.y != v.y || v.z != v.z || v.w != v.w) m = INFINITY;
-    }
-    m = wave::max64(m);
-    if ((t & 63) == 0) wred[t >> 6] = m;
-    __syncthreads();
-    if (t == 0) rmax[blockIdx.x] = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
+    const int r = 4 * blockIdx.x + (threadIdx.x >> 6);
+    if (r >= T) return;
+    wave_row_operand(x + (size_t)r * K, K, xop + (size_t)r * (K / 8), xhs + (size_t)r * (K / 64),
+                     xsc + r);
 }
 
-// Workgroup (ti, b), 64 lanes, ti < *ntiles: superblock b of the activation
-// operand of chunk ti (layout at the top of this file). Column col < cnt is
-// row src = ptok[order[q]] of x (order given) or row q (order null), q the
-// chunk's pair position, scaled by 2^-e with e = f16_row_exponent(rmax[src])
-// (a zero, infinite or NaN maximum keeps scale 1); xsc[ti][col] = 2^e. xmc
-// holds per lane f16(X / 16) of the four 16-element half-sums its lane group
-// covers (f32 sums in a fixed order). Columns >= cnt are zero with scale 1.
-__global__ __launch_bounds__(64) void chunk_q4k_kernel(
-    const float *__restrict__ x, int K, const float *__restrict__ rmax,
-    const int *__restrict__ tiles, const int *__restrict__ ntiles, const int *__restrict__ eoff,
-    const int *__restrict__ order, const int *__restrict__ ptok, _Float16 *__restrict__ xc,
-    _Float16 *__restrict__ xmc, float *__restrict__ xsc)
+// Per chunk column (ti, col), ti < *ntiles: the pair position the column
+// takes (the chunk's last pair for columns past its pairs) and its token.
+__global__ __launch_bounds__(256) void chunk_cols_kernel(const int *__restrict__ tiles,
+                                                         const int *__restrict__ ntiles,
+                                                         const int *__restrict__ eoff,
+                                                         const int *__restrict__ order,
+                                                         const int *__restrict__ ptok,
+                                                         int max_tiles, int *__restrict__ cpos,
+                                                         int *__restrict__ ctok)
 {
-    const int ti = blockIdx.x, b = blockIdx.y;
-    if (ti >= *ntiles) return;
+    const int idx = blockIdx.x * 256 + threadIdx.x, ti = idx / CHUNK, col = idx % CHUNK;
+    if (ti >= max_tiles || ti >= *ntiles) return;
     const int e = tiles[2 * ti], c = tiles[2 * ti + 1];
-    const int nb = eoff[e] + c * CHUNK, cnt = min(CHUNK, eoff[e + 1] - nb);
-    const int lane = threadIdx.x, col = lane & 15, g = lane >> 4;
-    const bool live = col < cnt;
-    const int src = live ? (order ? ptok[order[nb + col]] : nb + col) : 0;
-    const int ex = live ? f16_row_exponent(rmax[src]) : 0;
-    const float inv = ldexpf(1.0f, -ex);
-    if (b == 0 && g == 0) xsc[ti * CHUNK + col] = ldexpf(1.0f, ex);
-    auto pk = [](float p, float q) {
-        const h2 v = {(_Float16)p, (_Float16)q};
-        return __builtin_bit_cast(uint32_t, v);
-    };
-    const float4 *r4 = reinterpret_cast<const float4 *>(x + (size_t)src * K);
-    uint4 *dst = reinterpret_cast<uint4 *>(xc + (size_t)ti * CHUNK * K) + 8 * b * 64 + lane;
-    float ps[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int tt = 0; tt < 8; ++tt) {
-        uint4 o = make_uint4(0, 0, 0, 0);
-        if (live) {
-            const int a = 256 * b + 64 * ((tt < 4 ? 0 : 2) + (g >> 1)) + 16 * (g & 1) + 4 * (tt & 3);
-            const float4 lo = r4[a / 4], hi = r4[a / 4 + 8];
-            const float l0 = lo.x * inv, l1 = lo.y * inv, l2 = lo.z * inv, l3 = lo.w * inv;
-            const float h0 = hi.x * inv, h1 = hi.y * inv, h2v = hi.z * inv, h3 = hi.w * inv;
-            o = make_uint4(pk(l0, l2), pk(l1, l3), pk(h0, h2v), pk(h1, h3));
-            const int p = tt < 4 ? 0 : 2;
-            ps[p] += (l0 + l1) + (l2 + l3);
-            ps[p + 1] += (h0 + h1) + (h2v + h3);
-        }
-        dst[tt * 64] = o;
-    }
-    reinterpret_cast<uint2 *>(xmc + (size_t)ti * K)[64 * b + lane] =
-        make_uint2(pk(ps[0] * 0.0625f, ps[1] * 0.0625f), pk(ps[2] * 0.0625f, ps[3] * 0.0625f));
+    const int nb = eoff[e] + c * CHUNK, last = min(CHUNK, eoff[e + 1] - nb) - 1;
+    const int q = nb + min(col, last);
+    cpos[idx] = q;
+    ctok[idx] = ptok[order[q]];
 }
 
 } // namespace
@@ -509,31 +504,30 @@ __global__ __launch_bounds__(64) void chunk_q4k_kernel(
 int launch_moe_q4k(WView gate, WView up, WView down, int hidden, int mid, const float *x,
                    int tokens, const int *ptok, const int *eoff, const int *valid,
                    const int *order, const int *tiles, const int *ntiles, int max_tiles,
-                   int npairs, bool have_tmax, float *tmax, _Float16 *xc, _Float16 *xmc,
-                   float *xsc, float *gpart, float *upart, float *h32, float *hmax,
-                   _Float16 *hc, _Float16 *hmc, float *hsc, float *outp, float *outp2,
-                   void *stream)
+                   int npairs, bool have_ops, uint4 *xop, uint2 *xhs, float *xsc, int *cpos,
+                   int *ctok, float *gpart, float *upart, uint4 *hop, uint2 *hhs, float *hsc,
+                   float *outp, float *outp2, void *stream)
 {
     if (!moe_q4k_fits(hidden, mid)) return (int)hipErrorInvalidValue;
     hipStream_t st = (hipStream_t)stream;
     const size_t gstride = (size_t)npairs * mid;
-    if (!have_tmax)
-        hipLaunchKernelGGL(row_max_kernel, dim3(tokens), dim3(256), 0, st, x, hidden, tmax);
-    hipLaunchKernelGGL(chunk_q4k_kernel, dim3(max_tiles, hidden / 256), dim3(64), 0, st, x, hidden,
-                       tmax, tiles, ntiles, eoff, order, ptok, xc, xmc, xsc);
+    if (!have_ops) {
+        hipLaunchKernelGGL(row_operand_kernel, dim3((tokens + 3) / 4), dim3(256), 0, st, x, tokens,
+                           hidden, xop, xhs, xsc);
+        hipLaunchKernelGGL(chunk_cols_kernel, dim3((max_tiles * CHUNK + 255) / 256), dim3(256), 0,
+                           st, tiles, ntiles, eoff, order, ptok, max_tiles, cpos, ctok);
+    }
     int dev = 0, cus = 0;
     hipGetDevice(&dev);
     hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     const dim3 grid(unit_grid(cus));
     hipLaunchKernelGGL(moe_q4k_gate_up_kernel, grid, dim3(256),
                        (size_t)34 * (hidden / moe_kslices(hidden)), st, gate, up, mid, hidden,
-                       eoff, tiles, ntiles, xc, xmc, xsc, gpart, upart, gstride, mid / 64);
+                       eoff, tiles, ntiles, ctok, xop, xhs, xsc, gpart, upart, gstride, mid / 64);
     hipLaunchKernelGGL(silu_rows_kernel, dim3(npairs), dim3(256), 0, st, gpart, upart,
-                       moe_kslices(hidden), gstride, mid, valid, h32, hmax);
-    hipLaunchKernelGGL(chunk_q4k_kernel, dim3(max_tiles, mid / 256), dim3(64), 0, st, h32, mid,
-                       hmax, tiles, ntiles, eoff, nullptr, nullptr, hc, hmc, hsc);
+                       moe_kslices(hidden), gstride, mid, valid, hop, hhs, hsc);
     hipLaunchKernelGGL(moe_q4k_down_kernel, grid, dim3(256), (size_t)34 * mid, st, down, hidden,
-                       mid, eoff, tiles, ntiles, hc, hmc, hsc, outp, hidden / 64);
+                       mid, eoff, tiles, ntiles, cpos, hop, hhs, hsc, outp, hidden / 64);
     return (int)hipGetLastError();
 }
 

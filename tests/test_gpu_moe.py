@@ -156,6 +156,32 @@ def test_moe_q4k_few_token_chunks(gpu_ctx, hyq, oracle):
     assert np.array_equal(got[43], seed_out[43])  # token 43 is routed nowhere
 
 
+def test_moe_q4k_few_token_chunks_large_plan(gpu_ctx, hyq, oracle):
+    """The Q4_K register kernels after a plan of more than 1024 pairs (the
+    plan kernels that do not form the token operands in their launch, so
+    separate launches do): 1600 pairs over 160 experts, 10 per expert on
+    average, hidden = mid = 256 (one superblock per row); 12 seeded tokens
+    checked against the f64 chain."""
+    hidden, mid, experts, tokens, used = 256, 256, 160, 200, 8
+    _print("moe few-token chunks, 1600 pairs")
+    gate = random_matrix(Q4_K, experts * mid, hidden, seed=61)
+    up = random_matrix(Q4_K, experts * mid, hidden, seed=62)
+    down = random_matrix(Q4_K, experts * hidden, mid, seed=63)
+    x = np.random.default_rng(64).normal(0, 1, tokens * hidden).astype(np.float32)
+    seed_out = np.random.default_rng(65).normal(0, 1, (tokens, hidden)).astype(np.float32)
+    pt, pe, pw = routed_pairs(tokens, experts, used, seed=66)
+    G = gpu_ctx.upload(Q4_K, gate, (hidden, mid, experts))
+    U = gpu_ctx.upload(Q4_K, up, (hidden, mid, experts))
+    D = gpu_ctx.upload(Q4_K, down, (mid, hidden, experts))
+    got = hyq.moe_experts(G, U, D, x, tokens, pt, pe, pw, seed_out).reshape(tokens, hidden)
+    assert np.all(np.isfinite(got))
+    pick = sorted(np.random.default_rng(67).choice(tokens, 12, replace=False).tolist())
+    ref, mag = chain_f64(oracle, Q4_K, Q4_K, gate, up, down, hidden, mid, x, pt, pe, pw,
+                         seed_out, pick)
+    check_moe(got[pick], np.stack([ref[t] for t in pick]), np.stack([mag[t] for t in pick]),
+              "few-token chunks, 1600 pairs")
+
+
 def test_moe_30b_a3b_shape_sampled_tokens(gpu_ctx, hyq, oracle):
     """64 tokens, top-8 of 64 experts (softmax routing), hidden 2048, mid 1536,
     Q4_K experts; every token's output is produced, 6 seeded tokens are
