@@ -581,6 +581,11 @@ int hyq_weight_upload(hyq_ctx *ctx, int dtype, const uint8_t *gguf_bytes, size_t
 
     size_t sz[3];
     for (int p = 0; p < 3; ++p) sz[p] = align_up(nblocks * (size_t)plane_bytes(dtype, p), 256);
+    // A Q4_K expert stack also keeps its headers in 16-row tiles (plane 2,
+    // which Q4_K does not otherwise use): the few-token expert kernels read
+    // the headers of 16 rows of one superblock as 256 contiguous bytes.
+    const bool q4k_tiles = dtype == Q4_K && rank == 3 && rows % 16 == 0;
+    if (q4k_tiles) sz[2] = align_up(nblocks * 16, 256);
     auto storage = std::make_shared<DeviceBuffer>();
     storage->device = ctx->device;
     storage->bytes = sz[0] + sz[1] + sz[2];
@@ -595,6 +600,10 @@ int hyq_weight_upload(hyq_ctx *ctx, int dtype, const uint8_t *gguf_bytes, size_t
     HYQ_LAUNCH(launch_repack(dtype, stage, nblocks, (int)nb, base, base + sz[0],
                              base + sz[0] + sz[1], ctx->stream),
                "repack");
+    if (q4k_tiles)
+        HYQ_LAUNCH(launch_tile_headers(base + sz[0], (size_t)(rows * experts), (int)nb,
+                                       base + sz[0] + sz[1], ctx->stream),
+                   "tile_headers");
     HYQ_HIP(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(upload)");
 
     auto w = std::make_unique<hyq_weight>();
@@ -609,7 +618,7 @@ int hyq_weight_upload(hyq_ctx *ctx, int dtype, const uint8_t *gguf_bytes, size_t
     w->device = ctx->device;
     w->view.p0 = base;
     w->view.p1 = base + sz[0];
-    w->view.p2 = base + sz[0] + sz[1];
+    w->view.p2 = dtype == Q4_K && !q4k_tiles ? nullptr : base + sz[0] + sz[1];
     w->view.rows = (int)(rows * experts);
     w->view.nb = (int)nb;
     w->max_abs = weight_max_abs(dtype, gguf_bytes, nblocks);
@@ -627,7 +636,9 @@ int hyq_weight_expert(const hyq_weight *w, size_t e, hyq_weight **view)
     const size_t rows = w->dims[1], nb = (size_t)w->view.nb;
     v->view.p0 = w->view.p0 + e * rows * nb * plane_bytes(w->dtype, 0);
     v->view.p1 = w->view.p1 + e * rows * nb * plane_bytes(w->dtype, 1);
-    v->view.p2 = w->view.p2 + e * rows * nb * plane_bytes(w->dtype, 2);
+    // (a Q4_K stack's header tiles: 16 bytes per block, whole tiles per expert)
+    const size_t p2b = w->dtype == Q4_K ? (w->view.p2 ? 16 : 0) : plane_bytes(w->dtype, 2);
+    v->view.p2 = w->view.p2 ? w->view.p2 + e * rows * nb * p2b : nullptr;
     v->view.rows = (int)rows;
     *view = v.release();
     return HYQ_OK;

@@ -982,7 +982,7 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
     // Register-operand Q4_K kernels while the pairs average at most one
     // 16-token chunk per expert (weight-bound); the LDS-tiled GEMM otherwise.
     const bool few = fmt_gu == Q4_K && fmt_down == Q4_K && moe_q4k_fits(hidden, mid) &&
-                     npairs <= moe_q4k_chunk() * experts;
+                     gate.p2 && up.p2 && down.p2 && npairs <= moe_q4k_chunk() * experts;
     // (the few-token kernels take the token rows' largest magnitudes from the
     // plan's launch)
     const bool fast = plan_fast_fits(npairs, tokens, experts);

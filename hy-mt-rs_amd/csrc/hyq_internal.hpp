@@ -149,6 +149,9 @@ struct GemvArgs {
 constexpr int GEMV_MAX_PARTS = 4;
 
 // Kernel launchers (defined in the .hip files). All return hipError_t as int.
+// The Q4_K header plane hdr [rows][nb][16 B] (rows a multiple of 16) copied
+// into 16-row tiles [rows / 16][nb][16][16 B] (tiles: rows * nb * 16 bytes).
+int launch_tile_headers(const uint8_t *hdr, size_t rows, int nb, uint8_t *tiles, void *stream);
 int launch_repack(int fmt, const uint8_t *gguf, size_t nblocks, int nb_per_row, uint8_t *p0,
                   uint8_t *p1, uint8_t *p2, void *stream);
 int launch_quantize_q8(const float *x, int n, int8_t *q, float *s, int32_t *sum16,

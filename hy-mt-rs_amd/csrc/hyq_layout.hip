@@ -102,7 +102,32 @@ __global__ void dequant_rows_kernel(WView w, int row0, int nrows, int cols,
     out[idx] = decode_plane_value<F>(w, blk, i % block_len(F));
 }
 
+// Q4_K headers in 16-row tiles: the 16-byte header of (row r, block b) of a
+// weight of `rows` rows (a multiple of 16) and nb blocks per row goes from
+// hdr[r nb + b] to tiles[((r / 16) nb + b) 16 + r % 16], so the headers of
+// one block of 16 consecutive rows are 256 contiguous bytes.
+__global__ void tile_headers_kernel(const uint4 *__restrict__ hdr, size_t rows, int nb,
+                                    uint4 *__restrict__ tiles)
+{
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * (size_t)nb) return;
+    const size_t t = i / (16 * (size_t)nb), rem = i % (16 * (size_t)nb);
+    const int b = (int)(rem / 16), rr = (int)(rem % 16);
+    tiles[i] = hdr[(t * 16 + rr) * nb + b];
+}
+
 } // namespace
+
+int launch_tile_headers(const uint8_t *hdr, size_t rows, int nb, uint8_t *tiles, void *stream)
+{
+    const size_t n = rows * (size_t)nb;
+    if (n == 0) return 0;
+    if (rows % 16) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(tile_headers_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, reinterpret_cast<const uint4 *>(hdr), rows, nb,
+                       reinterpret_cast<uint4 *>(tiles));
+    return (int)hipGetLastError();
+}
 
 int launch_repack(int fmt, const uint8_t *gguf, size_t nblocks, int, uint8_t *p0, uint8_t *p1,
                   uint8_t *p2, void *stream)

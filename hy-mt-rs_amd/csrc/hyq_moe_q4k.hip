@@ -226,7 +226,7 @@ __device__ __forceinline__ void stream_units(int u0, int u1, int mgroups, int ks
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const uint8_t *q = in ? qp[r] + lg * gq[r] + ls * 128 : dummy;
-                const uint8_t *m = in ? mp[r] + lg * gm[r] + ls * 16 : dummy;
+                const uint8_t *m = in ? mp[r] + lg * gm[r] + ls * 256 : dummy;
                 wr[r].q0 = *reinterpret_cast<const uint4 *>(q);
                 wr[r].q1 = *reinterpret_cast<const uint4 *>(q + 64);
                 wr[r].meta = *reinterpret_cast<const uint4 *>(m);
@@ -357,9 +357,9 @@ __global__ __launch_bounds__(256, 2) void moe_q4k_gate_up_kernel(
             const WView &W = r ? up : gate;
             const size_t blk = (size_t)row * W.nb + kh * nbk;
             qp[r] = W.p0 + blk * 128 + 16 * g;
-            mp[r] = W.p1 + blk * 16;
+            mp[r] = W.p2 + (((size_t)(row >> 4) * W.nb + kh * nbk) * 16 + col) * 16;
             gq[r] = (size_t)64 * W.nb * 128;
-            gm[r] = (size_t)64 * W.nb * 16;
+            gm[r] = (size_t)4 * W.nb * 256;
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) s[i] = xsc[ctok[ti * CHUNK + 4 * g + i]];
@@ -447,11 +447,12 @@ __global__ __launch_bounds__(256, 2) void moe_q4k_down_kernel(
         nb = eoff[e] + c * CHUNK;
         cnt = min(CHUNK, eoff[e + 1] - nb);
         mg0 = mg;
-        const size_t blk = (size_t)(e * hidden + 64 * mg + w16 + col) * down.nb;
+        const int row = e * hidden + 64 * mg + w16 + col;
+        const size_t blk = (size_t)row * down.nb;
         qp[0] = down.p0 + blk * 128 + 16 * g;
-        mp[0] = down.p1 + blk * 16;
+        mp[0] = down.p2 + ((size_t)(row >> 4) * down.nb * 16 + col) * 16;
         gq[0] = (size_t)64 * down.nb * 128;
-        gm[0] = (size_t)64 * down.nb * 16;
+        gm[0] = (size_t)4 * down.nb * 256;
 #pragma unroll
         for (int i = 0; i < 4; ++i) s[i] = hsc[cpos[ti * CHUNK + 4 * g + i]];
     };
