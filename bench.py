@@ -32,6 +32,9 @@ Also reported, from live HIP-event timings on the context stream:
                   back-to-back launches, and (graph_GBs) one HIP graph that
                   launches every copy once;
   prefill, moe    the batched f16-MFMA GEMM (TFLOP/s) and the MoE expert layer;
+                  mfma_ceiling (in prefill) the sustained rate of back-to-back
+                  independent f16 MFMAs on every CU: the practical ceiling of
+                  the GEMMs (of_mfma_ceiling);
   prefill_1p8b    the same model's chunked prefill of a 1024-token prompt
                   (hyq_dense_prefill), wall-clock tok/s;
   cpu_baseline    the reference's x86 decode step (f32 activations, scalar
@@ -182,6 +185,24 @@ def sized_read_ceiling(hyq, ctx, ev, nbytes, pool=2 << 30) -> dict:
 
 MFMA_F16_PEAK_TFLOPS = 2500.0
 HIP_ATTR_CLOCK_KHZ, HIP_ATTR_CUS = 5, 63  # hipDeviceAttributeClockRate, ...MultiprocessorCount
+
+
+def mfma_ceiling(hyq, ctx, ev, iters: int = 2048) -> dict:
+    """The sustained f16 MFMA rate of this device: 8 workgroups of 4 waves per
+    CU, each wave issuing back-to-back independent v_mfma_f32_32x32x16_f16 on
+    register operands (hyq_mfma_stream_d), best of 5 launches - the practical
+    ceiling of the batched products, as read_ceiling is of the GEMVs."""
+    cu = ctypes.c_int()
+    ev.hip.hipDeviceGetAttribute(ctypes.byref(cu), HIP_ATTR_CUS, 0)
+    wgs = 8 * cu.value
+    sink = ctx.empty(wgs * 256, np.float32)
+    L = hyq.lib()
+    best = None
+    for _ in range(5):
+        ms = ev.time_ms(lambda i: L.hyq_mfma_stream_d(ctx.handle, wgs, iters, sink.ptr), 1)
+        best = ms if best is None or ms < best else best
+    flop = wgs * 4.0 * iters * 4 * 32768
+    return dict(workgroups=wgs, TFLOPs=round(flop / (best * 1e-3) / 1e12, 1))
 
 
 def mfma_peak_from_clock(ev, device: int = 0) -> dict:
@@ -721,6 +742,8 @@ def main() -> int:
     prefill = {}
     if not args.no_prefill:
         prefill["mfma_peak_from_clock"] = mfma_peak_from_clock(ev)
+        prefill["mfma_ceiling"] = mfma_ceiling(hyq, ctx, ev)
+        log(f"sustained f16 MFMA rate: {prefill['mfma_ceiling']['TFLOPs']:.0f} TFLOP/s")
         for name, (dt_, rows, cols) in {
             "C4_Q4_K_gate_up_14336x4096x512": (Q4_K, 14336, 4096),
             "C4_Q6_K_down_4096x14336x512": (Q6_K, 4096, 14336),
@@ -728,9 +751,11 @@ def main() -> int:
         }.items():
             us, tf = prefill_rate(hyq, ctx, ev, dt_, rows, cols, 512)
             clk = prefill["mfma_peak_from_clock"]["TFLOPs"]
+            ceil = prefill["mfma_ceiling"]["TFLOPs"]
             prefill[name] = dict(us=round(us, 2), TFLOPs=round(tf, 1),
                                  frac=round(tf / MFMA_F16_PEAK_TFLOPS, 4),
-                                 frac_of_clock_peak=round(tf / clk, 4) if clk else None)
+                                 frac_of_clock_peak=round(tf / clk, 4) if clk else None,
+                                 of_mfma_ceiling=round(tf / ceil, 4) if ceil else None)
             log(f"{name}: {us:.1f} us {tf:.0f} TFLOP/s")
 
     pf = None

@@ -62,6 +62,7 @@ SIGNATURES = {
     "hyq_matmul_d": (I, [P, P, P, SZ, P]),
     "hyq_matmul_noalloc_d": (I, [P, P, P, SZ, P]),
     "hyq_hbm_read_d": (I, [P, P, SZ, I, P]),
+    "hyq_mfma_stream_d": (I, [P, I, I, P]),
     "hyq_dequant_rows_d": (I, [P, P, SZ, SZ, P]),
     "hyq_moe_scratch_bytes": (SZ, [SZ, SZ, SZ, SZ, SZ]),
     "hyq_moe_experts_d": (I, [P, P, P, P, P, SZ, P, P, P, SZ, P, SZ, P]),

@@ -782,6 +782,16 @@ int hyq_hbm_read_d(hyq_ctx *ctx, const void *buf_d, size_t bytes, int workgroups
     return HYQ_OK;
 }
 
+int hyq_mfma_stream_d(hyq_ctx *ctx, int workgroups, int iters, float *sink_d)
+{
+    if (!ctx || !sink_d) return fail(HYQ_EINVAL, "mfma_stream: null argument");
+    if (workgroups <= 0 || workgroups > (1 << 20) || iters <= 0 || iters > (1 << 24))
+        return fail(HYQ_EINVAL, "mfma_stream: bad workgroup or iteration count");
+    DeviceGuard g(ctx->device);
+    HYQ_LAUNCH(launch_mfma_stream(workgroups, iters, sink_d, ctx->stream), "mfma_stream");
+    return HYQ_OK;
+}
+
 int hyq_dequant_rows_d(hyq_ctx *ctx, const hyq_weight *w, size_t row0, size_t nrows,
                        float *out_d)
 {

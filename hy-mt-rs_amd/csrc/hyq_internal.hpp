@@ -250,6 +250,9 @@ int launch_ffn_combine(const float *residual, const float *shared, const float *
 // A read-only stream of `bytes` (16-byte aligned) by `workgroups` workgroups,
 // one float per workgroup into sink.
 int launch_hbm_read(const void *buf, size_t bytes, int workgroups, float *sink, void *stream);
+// `workgroups` x 256 threads issuing `iters` x 4 f16 MFMAs each per wave;
+// sink holds workgroups * 256 floats.
+int launch_mfma_stream(int workgroups, int iters, float *sink, void *stream);
 // rms_norm_into of `rows` rows of width H into y (f32).
 int launch_rms_rows(const float *x, const float *w, int rows, int H, float eps, float *y,
                     void *stream);

@@ -236,6 +236,12 @@ int hyq_moe_forward_d(hyq_ctx *ctx, const hyq_moe_config *mc, const hyq_weight *
  * the read-only HBM rate the HBM-bound products are compared with. */
 int hyq_hbm_read_d(hyq_ctx *ctx, const void *buf_d, size_t bytes, int workgroups,
                    float *sink_d);
+/* Measurement aid (no counterpart in the reference): `workgroups`
+ * workgroups of 256 threads, each wave issuing `iters` rounds of four
+ * independent f16 MFMAs (v_mfma_f32_32x32x16_f16, 32768 flop each) on
+ * register operands; sink_d receives workgroups * 256 floats - the
+ * sustained matrix-core rate the batched products are compared with. */
+int hyq_mfma_stream_d(hyq_ctx *ctx, int workgroups, int iters, float *sink_d);
 
 /* decode of rows [row0, row0+nrows) to f32 on the device (Weight::row_into /
  * to_vec, src/quant.rs:99-142). */
