@@ -90,9 +90,9 @@ def test_batched_rows_are_independent_of_batch(gpu_ctx):
                          ids=["q80_shared_64", "q4k_16", "q2c_5", "stq_128"])
 def test_matmul_few_tokens_split_k(gpu_ctx, oracle, dtype, rows, cols, batch):
     """Batches of at most 128 tokens on weights of few row tiles run with K cut
-    into up to 8 slices (the MoE shared projection [2048x2048] Q8_0 at 64
-    tokens: 8 slices of 256 columns); parity with the oracle as every batched
-    product."""
+    into up to 8 slices (Q8_0 in whole 256-column sets takes the one-launch
+    register-operand product instead: the MoE shared projection [2048x2048]
+    at 64 tokens); parity with the oracle as every batched product."""
     _print("gemm few tokens", NAMES[dtype], rows, cols, batch)
     w = random_matrix(dtype, rows, cols, seed=rows + batch)
     x = np.random.default_rng(batch).normal(0, 1, batch * cols).astype(np.float32)
@@ -100,6 +100,27 @@ def test_matmul_few_tokens_split_k(gpu_ctx, oracle, dtype, rows, cols, batch):
     y = W.matmul(x, batch).reshape(batch, rows)
     y_ref, mag = oracle.matmul_f64(dtype, w, rows, cols, x, batch)
     check_prefill_path(y, y_ref, mag, f"{NAMES[dtype]} batch {batch}")
+    W.release()
+
+
+@pytest.mark.parametrize("rows,cols", [(1000, 256), (48, 768), (2048, 2048), (130, 4352)],
+                         ids=["1000x256", "48x768", "2048x2048", "130x4352"])
+def test_q80_few_tokens(gpu_ctx, oracle, rows, cols):
+    """Q8_0 at 2..128 tokens (widths in 256-column sets) takes the one-launch
+    register-operand product: parity with the oracle at 2, 17, 64 and 128
+    tokens (one set, so that most waves have no share of K, and three sets,
+    split unevenly; rows not a multiple of 16; two chunk groups), and every
+    token's row bit-identical across those batches."""
+    _print("q80 few tokens", rows, cols)
+    w = random_matrix(Q8_0, rows, cols, seed=rows + cols)
+    x = np.random.default_rng(cols).normal(0, 1, 128 * cols).astype(np.float32)
+    W = gpu_ctx.upload(Q8_0, w, (cols, rows))
+    full = W.matmul(x, 128).reshape(128, rows)
+    y_ref, mag = oracle.matmul_f64(Q8_0, w, rows, cols, x, 128)
+    check_prefill_path(full, y_ref, mag, f"Q8_0 {rows}x{cols} batch 128")
+    for lo, hi in ((0, 2), (30, 47), (64, 128), (100, 101 + 27)):
+        part = W.matmul(x[lo * cols:hi * cols], hi - lo).reshape(hi - lo, rows)
+        assert np.array_equal(part, full[lo:hi]), (lo, hi)
     W.release()
 
 
