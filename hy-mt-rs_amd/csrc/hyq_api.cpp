@@ -429,9 +429,10 @@ int matmul_dev(hyq_ctx *ctx, const hyq_weight *w, const float *x_d, size_t batch
     if ((uintptr_t)x_d % 16 || (uintptr_t)y_d % 16)
         return fail(HYQ_EINVAL, "matmul: device buffers must be 16-byte aligned");
     if (batch > 65535) return fail(HYQ_EINVAL, "matmul: batch %zu exceeds 65535", batch);
-    const size_t xh_bytes = align_up(batch * w->cols * 2, 256);
     // Q8_0 at up to 128 tokens: one register-operand launch (no K split)
     const bool few = w->dtype == Q8_0 && few_q80_fits((int)w->rows, (int)w->cols, (int)batch);
+    const size_t xh_bytes =
+        align_up(few ? few_q80_operand_bytes((int)w->cols, (int)batch) : batch * w->cols * 2, 256);
     const int ks = few ? 1 : matmul_kslices(w->dtype, (int)w->rows, (int)w->cols, (int)batch);
     const size_t part = ks > 1 ? (size_t)ks * batch * w->rows : 0;
     void *xh_mem = nullptr, *part_mem = nullptr;
@@ -449,12 +450,13 @@ int matmul_dev(hyq_ctx *ctx, const hyq_weight *w, const float *x_d, size_t batch
     }
     _Float16 *xh = (_Float16 *)xh_mem;
     float *rscale = (float *)((uint8_t *)xh_mem + xh_bytes);
-    HYQ_LAUNCH(launch_to_f16(x_d, (int)batch, (int)w->cols, xh, rscale, ctx->stream), "to_f16");
     if (few) {
-        HYQ_LAUNCH(launch_few_q80(w->view, (int)w->cols, xh, rscale, (int)batch, y_d, ctx->stream),
+        HYQ_LAUNCH(launch_few_q80(w->view, (int)w->cols, x_d, xh, rscale, (int)batch, y_d,
+                                  ctx->stream),
                    "few_q80");
         return HYQ_OK;
     }
+    HYQ_LAUNCH(launch_to_f16(x_d, (int)batch, (int)w->cols, xh, rscale, ctx->stream), "to_f16");
     HYQ_LAUNCH(launch_gemm_f16(w->dtype, w->view, (int)w->cols, xh, rscale, (int)batch, y_d,
                                nullptr, ctx->stream, (float *)part_mem, part, ks),
                "gemm_f16");

@@ -14,14 +14,17 @@
 // exactly and only the activations are rounded.
 //
 // Operands. MFMA lane l = 16 g + c holds, of a block, columns 8 g .. 8 g + 7:
-// as the A operand token c of the 16-token chunk (16 contiguous bytes of its
-// f16 row), as the B operand weight row c of the wave's 16 rows (8
-// contiguous code bytes). Output lane l holds tokens 4 g + i, i = 0..3, of
-// row c. Every token's result depends on its own row only, so any batch of
-// at most 128 tokens gives each row the same bits.
+// as the A operand token c of the 16-token chunk, as the B operand weight row
+// c of the wave's 16 rows (8 contiguous code bytes). The activations are laid
+// out by few_rows_kernel in that lane order, [chunk][block][lane][8 halves],
+// so each A operand is one 1 KiB load. Output lane l holds tokens 4 g + i,
+// i = 0..3, of row c. Every token's result depends on its own row only, so
+// any batch of at most 128 tokens gives each row the same bits.
 #include <hip/hip_runtime.h>
 
+#include "hyq_f16rows.hpp"
 #include "hyq_internal.hpp"
+#include "hyq_wave.hpp"
 
 #pragma clang fp contract(off)
 
@@ -55,6 +58,46 @@ __device__ __forceinline__ h8 codes_f16(uint32_t lo, uint32_t hi)
     return h8{q0.x, q0.y, q1.x, q1.y, q2.x, q2.y, q3.x, q3.y};
 }
 
+// One workgroup per token row n of the chunks (n < chunks * 16): its f16
+// values (x[n] scaled by 2^-e, e from the row's largest magnitude as
+// launch_to_f16 forms it; zeros for n >= N) into the fragment layout, and
+// rscale[n] = 2^e.
+__global__ __launch_bounds__(256) void few_rows_kernel(const float *__restrict__ x, int K, int N,
+                                                       _Float16 *__restrict__ xf,
+                                                       float *__restrict__ rscale)
+{
+    __shared__ float wred[4];
+    const int n = (int)blockIdx.x, t = (int)threadIdx.x, nb = K / 32;
+    const int ck = n / FEW_CHUNK, c = n % FEW_CHUNK;
+    const bool live = n < N;
+    const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)(live ? n : 0) * K);
+    float m = 0.f;
+    if (live)
+        for (int i = t; i < K / 4; i += 256) {
+            const float4 v = x4[i];
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+            if (v.x != v.x || v.y != v.y || v.z != v.z || v.w != v.w) m = INFINITY;
+        }
+    m = wave::max64(m);
+    if ((t & 63) == 0) wred[t >> 6] = m;
+    __syncthreads();
+    const int e = f16_row_exponent(fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3])));
+    const float inv = ldexpf(1.0f, -e);
+    if (t == 0 && live) rscale[n] = ldexpf(1.0f, e);
+    // piece (block b, lane group g): columns 32 b + 8 g .. + 7
+    for (int p = t; p < 4 * nb; p += 256) {
+        const int b = p >> 2, g = p & 3;
+        h8 o = {};
+        if (live) {
+            const float4 lo = x4[8 * b + 2 * g], hi = x4[8 * b + 2 * g + 1];
+            o = h8{(_Float16)(lo.x * inv), (_Float16)(lo.y * inv), (_Float16)(lo.z * inv),
+                   (_Float16)(lo.w * inv), (_Float16)(hi.x * inv), (_Float16)(hi.y * inv),
+                   (_Float16)(hi.z * inv), (_Float16)(hi.w * inv)};
+        }
+        *reinterpret_cast<h8 *>(xf + (((size_t)ck * nb + b) * 64 + 16 * g + c) * 8) = o;
+    }
+}
+
 constexpr int FEW_CHUNKS = 4;  // chunks a workgroup multiplies against one weight load
 constexpr int FEW_WAVES = 8;   // waves per workgroup, each a share of K
 
@@ -81,10 +124,12 @@ __global__ __launch_bounds__(64 * FEW_WAVES) void few_q80_kernel(WView w, int K,
     const int rowc = min(row, M - 1);
     const uint8_t *wq = w.p0 + (size_t)rowc * nb * 32 + 8 * g;
     const uint4 *wd = reinterpret_cast<const uint4 *>(w.p1 + (size_t)rowc * nb * 2);
+    // chunk k's fragments (chunks past the batch read the last one, unused)
+    const int nck = (N + FEW_CHUNK - 1) / FEW_CHUNK;
     const _Float16 *xa[FEW_CHUNKS];
 #pragma unroll
     for (int k = 0; k < FEW_CHUNKS; ++k)
-        xa[k] = xh + (size_t)min(n0 + FEW_CHUNK * k + c, N - 1) * K + 8 * g;
+        xa[k] = xh + ((size_t)min(n0 / FEW_CHUNK + k, nck - 1) * nb * 64 + lane) * 8;
     f4 acc[FEW_CHUNKS];
 #pragma unroll
     for (int k = 0; k < FEW_CHUNKS; ++k) acc[k] = f4{0.f, 0.f, 0.f, 0.f};
@@ -99,7 +144,7 @@ __global__ __launch_bounds__(64 * FEW_WAVES) void few_q80_kernel(WView w, int K,
         for (int k = 0; k < FEW_CHUNKS; ++k)
 #pragma unroll
             for (int j = 0; j < FEW_SET; ++j)
-                x[k][j] = *reinterpret_cast<const h8 *>(xa[k] + (size_t)(FEW_SET * s + j) * 32);
+                x[k][j] = *reinterpret_cast<const h8 *>(xa[k] + (size_t)(FEW_SET * s + j) * 512);
         // (all of the set's loads issued before the compute that waits for them)
         __builtin_amdgcn_sched_barrier(0);
         const uint32_t dw[4] = {d4.x, d4.y, d4.z, d4.w};
@@ -145,10 +190,18 @@ bool few_q80_fits(int rows, int cols, int batch)
     return batch >= 1 && batch <= FEW_Q80_MAX_TOKENS && cols % 256 == 0 && rows >= 1;
 }
 
-int launch_few_q80(WView w, int cols, const _Float16 *xh, const float *rscale, int batch,
+size_t few_q80_operand_bytes(int cols, int batch)
+{
+    return (size_t)((batch + FEW_CHUNK - 1) / FEW_CHUNK) * FEW_CHUNK * cols * 2;
+}
+
+int launch_few_q80(WView w, int cols, const float *x, _Float16 *xh, float *rscale, int batch,
                    float *y, void *stream)
 {
     if (!few_q80_fits(w.rows, cols, batch)) return (int)hipErrorInvalidValue;
+    const int nrows = (batch + FEW_CHUNK - 1) / FEW_CHUNK * FEW_CHUNK;
+    hipLaunchKernelGGL(few_rows_kernel, dim3(nrows), dim3(256), 0, (hipStream_t)stream, x, cols,
+                       batch, xh, rscale);
     const int rgroups = (w.rows + 15) / 16;
     const int cgroups = (batch + FEW_CHUNKS * FEW_CHUNK - 1) / (FEW_CHUNKS * FEW_CHUNK);
     hipLaunchKernelGGL(few_q80_kernel, dim3(rgroups * cgroups), dim3(64 * FEW_WAVES), 0,

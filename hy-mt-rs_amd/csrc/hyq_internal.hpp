@@ -168,11 +168,14 @@ int launch_decode_gguf(int fmt, const uint8_t *bytes, size_t nblocks, float *out
 // silu(gate . x) * (up . x).
 int launch_to_f16(const float *x, int rows, int K, _Float16 *xh, float *rscale, void *stream);
 // Q8_0 weights at batch 2..FEW_Q80_MAX_TOKENS with cols a multiple of 256
-// (hyq_gemm_few.hip): y[n][m] = (xh[n] . W[m]) * rscale[n], one launch, the
+// (hyq_gemm_few.hip): y[n][m] = x[n] . W[m], the activations rounded to f16
+// with a power-of-two row scale into xh (few_q80_operand_bytes, in MFMA
+// fragment order) and rscale (batch floats), then one product launch with the
 // codes exact in the f16 MFMA operands and the block scales applied in f32.
 constexpr int FEW_Q80_MAX_TOKENS = 128;
 bool few_q80_fits(int rows, int cols, int batch);
-int launch_few_q80(WView w, int cols, const _Float16 *xh, const float *rscale, int batch,
+size_t few_q80_operand_bytes(int cols, int batch);
+int launch_few_q80(WView w, int cols, const float *x, _Float16 *xh, float *rscale, int batch,
                    float *y, void *stream);
 int launch_norm_to_f16(const float *x, int rows, int K, const float *norm, float eps,
                        _Float16 *xh, float *rscale, void *stream);
