@@ -30,7 +30,8 @@ Also reported, from live HIP-event timings on the context stream:
                   the 1.8B Q2_0C/STQ1_0 set; Q6_K lm_head; the 7B shapes), Q8
                   input, weights rotated over >= 1 GiB of distinct copies:
                   back-to-back launches, and (graph_GBs) one HIP graph that
-                  launches every copy once;
+                  launches every copy once; for STQ1_0 the synthetic codes'
+                  measured zero fraction;
   prefill, moe    the batched f16-MFMA GEMM (TFLOP/s) and the MoE expert layer;
                   mfma_ceiling (in prefill) the sustained rate of back-to-back
                   independent f16 MFMAs on every CU: the practical ceiling of
@@ -42,7 +43,8 @@ Also reported, from live HIP-event timings on the context stream:
                   this host's cores (median of 5 tokens after 2 warm-ups);
   cpu_baselines   the same restatement on every other workload (C1/C2 GEMVs,
                   a 256-row sample of each C4 GEMM, the C5 MoE layer), with the
-                  host's CPU model and core count.
+                  host's CPU model and core count; beside them the GPU path's
+                  int8 algorithm in portable C (not a reference path on x86).
 """
 from __future__ import annotations
 
@@ -142,6 +144,16 @@ def gemv_rate(hyq, ctx, ev, dtype, rows, cols, seed=1, min_bytes=ROTATE_BYTES, g
         W.release()
     agg = alg * copies / (gms * 1e-3) / 1e9 if gms else None
     return ms * 1e3, alg / (ms * 1e-3) / 1e9, agg, copies, alg
+
+
+def stq_zero_fraction(ctx, rows, cols, seed=1, sample=64) -> float:
+    """Fraction of zero weights in the first `sample` rows of the synthetic
+    STQ1_0 matrix gemv_rate uploads, decoded on the device."""
+    from synth import STQ1_0, random_matrix
+    W = ctx.upload(STQ1_0, random_matrix(STQ1_0, rows, cols, seed=seed), (cols, rows))
+    vals = np.concatenate([W.row(r) for r in range(min(sample, rows))])
+    W.release()
+    return round(float(np.mean(vals == 0.0)), 4)
 
 
 def read_ceiling(hyq, ctx, ev, nbytes=2 << 30):
@@ -527,6 +539,16 @@ def cpu_baselines(model, kv) -> dict:
     t = _median_s(step)
     out["C3_decode"] = dict(tok_s=round(1.0 / t, 3), ms=round(t * 1e3, 2),
                             sample="1 token at positions 1024..1031 per run")
+
+    # the int8 algorithm of the GPU path restated in portable C (Q8
+    # activations, integer block sums): not a reference path on x86
+    def step8():
+        o.step(k, v, pos[0], 5, int8_path=True)
+        pos[0] = PREFILLED + (pos[0] - PREFILLED + 1) % 8
+    t8 = _median_s(step8)
+    out["C3_decode_int8_algorithm"] = dict(
+        tok_s=round(1.0 / t8, 3), ms=round(t8 * 1e3, 2),
+        note="the GPU path's int8 algorithm in portable C; not a reference path on x86")
     # C1 / C2 GEMVs at batch 1
     gemv = {}
     for name, (dt_, rows, cols) in {
@@ -735,6 +757,11 @@ def main() -> int:
                               graph_frac=round(agg / HBM_PEAK_GBS, 4) if agg else None,
                               read_ceiling_same_bytes=ceil,
                               of_read_ceiling=round(gbs / ceil["GBs"], 4))
+            if dt_ == STQ1_0:
+                # the synthetic codes' zero fraction (uniform index and sign
+                # bytes; every codebook entry has one zero digit), measured
+                # on 64 rows decoded by the device (Weight::row)
+                gemv[name]["zero_fraction"] = stq_zero_fraction(ctx, rows, cols)
             log(f"{name}: {us:.2f} us {gbs:.0f} GB/s; graph of {copies} copies "
                 f"{agg or 0:.0f} GB/s; a read-only launch of the same bytes {ceil['us']:.2f} us "
                 f"{ceil['GBs']:.0f} GB/s")
