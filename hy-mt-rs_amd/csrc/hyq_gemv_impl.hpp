@@ -247,9 +247,9 @@ __device__ __forceinline__ void stage_loop(const GemvArgs &a, const float *xin, 
 // into registers before the weights' loads are issued, then copied to LDS.
 // With several rows per lane (the large launches) so are the row's scales
 // and the integer sums the format's dot reads (up to Q8_META words per
-// thread), which the dots then read from LDS instead of global memory; the
-// small launches read them from global memory, where their latency hides
-// behind the weights'.
+// thread), which the dots then read from LDS instead of global memory; with
+// one row per lane each lane loads its groups' words from global memory into
+// registers just before each group's weights.
 constexpr int Q8_REG = 8;
 constexpr int Q8_META = 8;
 // (a clang vector type: an array of HIP's int4 struct is not promoted to
@@ -341,6 +341,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
         if constexpr (H) G::load_half(D, w, row, gbase + g, hh);
         else G::load(D, w, row, gbase + g);
     };
+    // The Q8 words a group's dot reads besides the activations: from LDS
+    // where an input stage or the Q8 copy puts them there, read at their use
+    // (Q8At); else from global memory into registers (G::Meta), loaded just
+    // before the group's weights so that their latency overlaps the
+    // weights' instead of following it.
+    using Mt = typename G::Meta;
+    constexpr bool STAGE_META = IN == 0 && NR >= 2;
+    constexpr bool META_PRE = IN == 0 && !STAGE_META;
     Dt d[NR];
     Dt d2[MODE == GEMV_SILU ? NR : 1];
     auto load_group = [&](int g) {
@@ -371,7 +379,6 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
                    N32 = G::QSUMS & Q8_SUM32;
     const int m1 = groups, m2 = m1 + (N256 ? groups : 0), m3 = m2 + (N16 ? 16 * groups : 0);
     const int mwords = m3 + (N32 ? 8 * groups : 0);
-    constexpr bool STAGE_META = IN == 0 && NR >= 2;
     const bool meta_reg = STAGE_META && mwords <= Q8_META * (int)blockDim.x;
     auto meta_src = [&](int i) -> const int * {
         const int *p = reinterpret_cast<const int *>(a.x.s) + i;
@@ -404,10 +411,17 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     }
     static_assert(P == 0 || (NR == 1 && MODE == GEMV_PLAIN), "preload: plain, one row per lane");
     Dt dp[P > 0 ? P : 1];
+    Mt mp[P > 0 ? P : 1];
+    Mt md; // the current group's (P == 0)
     if (P > 0) {
 #pragma unroll
-        for (int u = 0; u < P; ++u) load(dp[u], a.seg[0].w, wrow[0], min(gi + GSTEP * u, groups - 1));
+        for (int u = 0; u < P; ++u) {
+            const int gu = min(gi + GSTEP * u, groups - 1);
+            if constexpr (META_PRE) mp[u] = G::meta(a.x, gu);
+            load(dp[u], a.seg[0].w, wrow[0], gu);
+        }
     } else {
+        if constexpr (META_PRE) md = G::meta(a.x, min(gi, groups - 1));
         load_group(min(gi, groups - 1));
     }
     // the plain epilogue's residual and partial rows, loaded now (after the
@@ -490,17 +504,23 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     // the two halves' integer sums meet by DPP and lane hh == 0 accumulates
     // the group (as the full-group mode of the same format does, one fused
     // multiply-add per group), lane hh == 1 keeps zero.
-    auto accum = [&](float acc, const Dt &D, const int (&act)[NACT], int g) -> float {
+    auto accum = [&](float acc, const Dt &D, const auto &m, const int (&act)[NACT],
+                     int g) -> float {
         if constexpr (H) {
             int is = G::isum_half(D, act, xq, g, hh);
             is += wave::dpp<wave::DPP_XOR1>(is);
             const float r = G::finish_acc(acc, is, D.d, xq, g);
             return hh ? acc : r;
         } else if constexpr (HasHalf<F>::value) {
-            return G::dot_acc(acc, D, act, xq, g);
+            return G::dot_acc(acc, D, act, m);
         } else {
-            return acc + G::template dot<false>(D, act, xq, g, nullptr);
+            return acc + G::template dot<false>(D, act, m, nullptr);
         }
+    };
+    // group g's Q8 words: the preloaded ones, or an accessor of the LDS copy
+    auto meta_of = [&](const Mt &pre, int g) {
+        if constexpr (META_PRE) return pre;
+        else return Q8At{xq, g};
     };
     if constexpr (P > 0) {
 #pragma unroll
@@ -510,7 +530,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
             if (g >= groups || !valid[0]) continue;
             int act[NACT];
             stage_act(g, act);
-            acc[0] = accum(acc[0], dp[u], act, g);
+            acc[0] = accum(acc[0], dp[u], meta_of(mp[u], g), act, g);
         }
     } else if constexpr (NR == 1 && MODE != GEMV_SILU) {
         // The lane's next group is in flight while the current one is used:
@@ -518,7 +538,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
         // lane's last group re-reads group groups - 1 (in bounds, unused).
         Dt e[NR];
         Dt e2[MODE == GEMV_SILU ? NR : 1];
-        auto load_into = [&](Dt *dd, Dt *dd2, int g) {
+        Mt me;
+        auto load_into = [&](Dt *dd, Dt *dd2, Mt &mm, int g) {
+            if constexpr (META_PRE) mm = G::meta(a.x, g);
 #pragma unroll
             for (int i = 0; i < NR; ++i) {
                 const WView &w = MODE == GEMV_MULTI ? a.seg[seg[i]].w : a.seg[0].w;
@@ -526,43 +548,48 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
                 if (MODE == GEMV_SILU) load(dd2[i], a.seg[1].w, wrow[i], g);
             }
         };
-        auto step = [&](const Dt *dc, const Dt *dc2, int g) {
+        auto step = [&](const Dt *dc, const Dt *dc2, const Mt &mm, int g) {
             int act[NACT];
             stage_act(g, act);
+            const auto m = meta_of(mm, g);
 #pragma unroll
             for (int i = 0; i < NR; ++i) {
                 if (!valid[i]) continue;
                 if constexpr (MODE == GEMV_ISUMS && !H) {
                     int32_t *out = a.isums + ((size_t)lrow[i] * groups + g) * G::ISUMS;
-                    acc[i] += G::template dot<true>(dc[i], act, xq, g, out);
+                    acc[i] += G::template dot<true>(dc[i], act, m, out);
                 } else {
-                    acc[i] = accum(acc[i], dc[i], act, g);
-                    if (MODE == GEMV_SILU) acc2[i] = accum(acc2[i], dc2[i], act, g);
+                    acc[i] = accum(acc[i], dc[i], m, act, g);
+                    if (MODE == GEMV_SILU) acc2[i] = accum(acc2[i], dc2[i], m, act, g);
                 }
             }
         };
         int g = gi;
         for (; g + GSTEP < groups; g += 2 * GSTEP) {
-            load_into(e, e2, g + GSTEP);
-            step(d, d2, g);
-            load_into(d, d2, min(g + 2 * GSTEP, groups - 1));
-            step(e, e2, g + GSTEP);
+            load_into(e, e2, me, g + GSTEP);
+            step(d, d2, md, g);
+            load_into(d, d2, md, min(g + 2 * GSTEP, groups - 1));
+            step(e, e2, me, g + GSTEP);
         }
-        if (g < groups) step(d, d2, g);
+        if (g < groups) step(d, d2, md, g);
     } else {
         for (int g = gi; g < groups; g += GSTEP) {
             int act[NACT];
             stage_act(g, act);
-            if (g != gi) load_group(g);
+            if (g != gi) {
+                if constexpr (META_PRE) md = G::meta(a.x, g);
+                load_group(g);
+            }
+            const auto m = meta_of(md, g);
 #pragma unroll
             for (int i = 0; i < NR; ++i) {
                 if (!valid[i]) continue;
                 if constexpr (MODE == GEMV_ISUMS && !H) {
                     int32_t *out = a.isums + ((size_t)lrow[i] * groups + g) * G::ISUMS;
-                    acc[i] += G::template dot<true>(d[i], act, xq, g, out);
+                    acc[i] += G::template dot<true>(d[i], act, m, out);
                 } else {
-                    acc[i] = accum(acc[i], d[i], act, g);
-                    if (MODE == GEMV_SILU) acc2[i] = accum(acc2[i], d2[i], act, g);
+                    acc[i] = accum(acc[i], d[i], m, act, g);
+                    if (MODE == GEMV_SILU) acc2[i] = accum(acc2[i], d2[i], m, act, g);
                 }
             }
         }

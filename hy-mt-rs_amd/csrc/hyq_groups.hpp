@@ -9,7 +9,12 @@
 //
 // Each `dot` returns the group's f32 contribution and, when EMIT is set,
 // writes the group's integer block sums in the granularity the reference's
-// SDOT kernels accumulate them (see hyq.h, hyq_gemv_isums_d).
+// SDOT kernels accumulate them (see hyq.h, hyq_gemv_isums_d). The Q8 words a
+// group's dot reads besides the codes (the group scale and the integer sums
+// the format folds its offsets with) come through an accessor object: a
+// format's `Meta`, loaded into registers by `meta` (so that a kernel can
+// issue those loads with the group's weights), or a `Q8At`, which reads
+// them where they lie at the dot (the LDS copies of an input stage).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -64,9 +69,29 @@ __device__ __forceinline__ void hold(uint16_t &v)
 // The Q8 integer sums a format's dot reads (QSUMS: a mask of these).
 constexpr int Q8_SUM256 = 1, Q8_SUM16 = 2, Q8_SUM32 = 4;
 
+// Group g's Q8 words, read at each use.
+struct Q8At {
+    Q8View x;
+    int g;
+    __device__ __forceinline__ float scale() const { return x.s[g]; }
+    __device__ __forceinline__ int sum256() const { return x.sum256[g]; }
+    __device__ __forceinline__ int sum16(int k) const { return x.sum16[16 * g + k]; }
+    __device__ __forceinline__ int sum32(int j) const { return x.sum32[8 * g + j]; }
+};
+
 struct GroupQ2C {
     static constexpr int ISUMS = 1;
     static constexpr int QSUMS = Q8_SUM256 | Q8_SUM32; // full / half-group dots
+    struct Meta {
+        float s;
+        int s256;
+        __device__ __forceinline__ float scale() const { return s; }
+        __device__ __forceinline__ int sum256() const { return s256; }
+    };
+    __device__ __forceinline__ static Meta meta(const Q8View &x, int g)
+    {
+        return Meta{x.s[g], x.sum256[g]};
+    }
     struct Data {
         uint4 w[4];
         uint16_t d;
@@ -85,9 +110,9 @@ struct GroupQ2C {
         for (int u = 0; u < 4; ++u) D.w[u] = p[u];
         D.d = reinterpret_cast<const uint16_t *>(w.p1)[blk];
     }
-    template <bool EMIT>
-    __device__ __forceinline__ static float dot(const Data &Din, const int *act,
-                                                const Q8View &x, int g, int32_t *out)
+    template <bool EMIT, class M>
+    __device__ __forceinline__ static float dot(const Data &Din, const int *act, const M &x,
+                                                int32_t *out)
     {
         Data D = Din;
         D.hold_all();
@@ -103,9 +128,9 @@ struct GroupQ2C {
                 raw = sdot4((c[m] >> 6) & 0x03030303u, act[16 * u + 12 + m], raw);
             }
         }
-        int isum = 2 * raw - 3 * x.sum256[g];
+        int isum = 2 * raw - 3 * x.sum256();
         if (EMIT) out[0] = isum;
-        return (float)isum * (h2f(D.d) * x.s[g]);
+        return (float)isum * (h2f(D.d) * x.scale());
     }
 
     // Half of a group (weights 128h .. 128h + 127: code units 2h, 2h + 1) for
@@ -160,8 +185,9 @@ struct GroupQ2C {
     {
         return fmaf(h2f(d) * x.s[g], (float)isum, acc);
     }
+    template <class M>
     __device__ __forceinline__ static float dot_acc(float acc, const Data &Din, const int *act,
-                                                    const Q8View &x, int g)
+                                                    const M &x)
     {
         Data D = Din;
         D.hold_all();
@@ -177,7 +203,7 @@ struct GroupQ2C {
                 raw = sdot4((c[m] >> 6) & 0x03030303u, act[16 * u + 12 + m], raw);
             }
         }
-        return finish_acc(acc, 2 * raw - 3 * x.sum256[g], D.d, x, g);
+        return fmaf(h2f(D.d) * x.scale(), (float)(2 * raw - 3 * x.sum256()), acc);
     }
 };
 
@@ -189,6 +215,16 @@ struct GroupQ2C {
 struct GroupSTQ {
     static constexpr int ISUMS = 1;
     static constexpr int QSUMS = Q8_SUM256;
+    struct Meta {
+        float s;
+        int s256;
+        __device__ __forceinline__ float scale() const { return s; }
+        __device__ __forceinline__ int sum256() const { return s256; }
+    };
+    __device__ __forceinline__ static Meta meta(const Q8View &x, int g)
+    {
+        return Meta{x.s[g], x.sum256[g]};
+    }
     struct Data {
         uint4 nib[2];
         uint2 sgn;
@@ -242,9 +278,9 @@ struct GroupSTQ {
     {
         return codes(idx & 0x0F0F0F0Fu, byte_mask(idx << 3));
     }
-    template <bool EMIT>
-    __device__ __forceinline__ static float dot(const Data &Din, const int *act,
-                                                const Q8View &x, int g, int32_t *out)
+    template <bool EMIT, class M>
+    __device__ __forceinline__ static float dot(const Data &Din, const int *act, const M &x,
+                                                int32_t *out)
     {
         Data D = Din;
         D.hold_all();
@@ -266,9 +302,9 @@ struct GroupSTQ {
                     raw = sdot4((e >> (2 * p)) & 0x03030303u, act[16 * c + 4 * p + qi], raw);
             }
         }
-        int isum = raw - x.sum256[g];
+        int isum = raw - x.sum256();
         if (EMIT) out[0] = isum;
-        return (float)isum * (h2f(D.d) * x.s[g]);
+        return (float)isum * (h2f(D.d) * x.scale());
     }
 };
 
@@ -282,6 +318,20 @@ struct GroupSTQ {
 struct GroupQ4K {
     static constexpr int ISUMS = 2;
     static constexpr int QSUMS = Q8_SUM32;
+    struct Meta {
+        float s;
+        int s32[8];
+        __device__ __forceinline__ float scale() const { return s; }
+        __device__ __forceinline__ int sum32(int j) const { return s32[j]; }
+    };
+    __device__ __forceinline__ static Meta meta(const Q8View &x, int g)
+    {
+        Meta m;
+        m.s = x.s[g];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) m.s32[j] = x.sum32[8 * g + j];
+        return m;
+    }
     struct Data {
         uint4 qs[8];
         uint4 meta;
@@ -300,9 +350,9 @@ struct GroupQ4K {
         for (int i = 0; i < 8; ++i) D.qs[i] = p[i];
         D.meta = reinterpret_cast<const uint4 *>(w.p1)[blk];
     }
-    template <bool EMIT>
-    __device__ __forceinline__ static float dot(const Data &Din, const int *act,
-                                                const Q8View &x, int g, int32_t *out)
+    template <bool EMIT, class M>
+    __device__ __forceinline__ static float dot(const Data &Din, const int *act, const M &x,
+                                                int32_t *out)
     {
         Data D = Din;
         D.hold_all();
@@ -339,14 +389,14 @@ struct GroupQ4K {
                 qx = sdot4(nb, act[16 * grp + 8 * hi + i4], qx);
             }
             A += s * qx;
-            B += m * x.sum32[8 * g + j];
+            B += m * x.sum32(j);
         }
         if (EMIT) {
             out[0] = A;
             out[1] = B;
         }
         const float d = h2f((uint16_t)m0), dmin = h2f((uint16_t)(m0 >> 16));
-        return x.s[g] * (d * (float)A - dmin * (float)B);
+        return x.scale() * (d * (float)A - dmin * (float)B);
     }
 };
 
@@ -358,6 +408,20 @@ struct GroupQ4K {
 struct GroupQ6K {
     static constexpr int ISUMS = 16;
     static constexpr int QSUMS = Q8_SUM16;
+    struct Meta {
+        float s;
+        int s16[16];
+        __device__ __forceinline__ float scale() const { return s; }
+        __device__ __forceinline__ int sum16(int k) const { return s16[k]; }
+    };
+    __device__ __forceinline__ static Meta meta(const Q8View &x, int g)
+    {
+        Meta m;
+        m.s = x.s[g];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) m.s16[k] = x.sum16[16 * g + k];
+        return m;
+    }
     struct Data {
         uint4 q[12];
         uint4 sc;
@@ -379,9 +443,9 @@ struct GroupQ6K {
         D.sc = reinterpret_cast<const uint4 *>(w.p1)[blk];
         D.d = reinterpret_cast<const uint16_t *>(w.p2)[blk];
     }
-    template <bool EMIT>
-    __device__ __forceinline__ static float dot(const Data &Din, const int *act,
-                                                const Q8View &x, int g, int32_t *out)
+    template <bool EMIT, class M>
+    __device__ __forceinline__ static float dot(const Data &Din, const int *act, const M &x,
+                                                int32_t *out)
     {
         Data D = Din;
         D.hold_all();
@@ -396,7 +460,7 @@ struct GroupQ6K {
         const uint32_t *ql = v;      // 32 dwords
         const uint32_t *qh = v + 32; // 16 dwords
         const uint32_t scw[4] = {D.sc.x, D.sc.y, D.sc.z, D.sc.w};
-        const float dd = h2f(D.d) * x.s[g];
+        const float dd = h2f(D.d) * x.scale();
         float acc = 0.f;
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
@@ -421,7 +485,7 @@ struct GroupQ6K {
 #pragma unroll
                 for (int p = 0; p < 4; ++p) {
                     const int k = 8 * c + 2 * p + h; // plane = sub-scale index
-                    const int isum = rr[p] - 32 * x.sum16[16 * g + k];
+                    const int isum = rr[p] - 32 * x.sum16(k);
                     if (EMIT) out[k] = isum;
                     const int8_t s8 = (int8_t)(scw[k >> 2] >> (8 * (k & 3)));
                     acc += (float)isum * (dd * (float)s8);
@@ -439,6 +503,11 @@ struct GroupQ6K {
 struct GroupQ80 {
     static constexpr int ISUMS = 8;
     static constexpr int QSUMS = 0;
+    struct Meta {
+        float s;
+        __device__ __forceinline__ float scale() const { return s; }
+    };
+    __device__ __forceinline__ static Meta meta(const Q8View &x, int g) { return Meta{x.s[g]}; }
     struct Data {
         uint4 q[16];
         uint4 d;
@@ -457,14 +526,14 @@ struct GroupQ80 {
         for (int i = 0; i < 16; ++i) D.q[i] = p[i];
         D.d = *reinterpret_cast<const uint4 *>(w.p1 + blk * 2);
     }
-    template <bool EMIT>
-    __device__ __forceinline__ static float dot(const Data &Din, const int *act,
-                                                const Q8View &x, int g, int32_t *out)
+    template <bool EMIT, class M>
+    __device__ __forceinline__ static float dot(const Data &Din, const int *act, const M &x,
+                                                int32_t *out)
     {
         Data D = Din;
         D.hold_all();
         const uint32_t dw[4] = {D.d.x, D.d.y, D.d.z, D.d.w};
-        const float sg = x.s[g];
+        const float sg = x.scale();
         float acc = 0.f;
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
