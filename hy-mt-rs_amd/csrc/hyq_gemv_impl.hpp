@@ -274,8 +274,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     static_assert(!SLOT || (NR == 1 && !H && SL == 0 && P == 0 &&
                             (MODE == GEMV_SILU || MODE == GEMV_PLAIN)),
                   "expert slots: one row per lane, gate/up or plain");
-    static_assert(SL == 0 || (SL == 32 && !H && NR == 1 && MODE == GEMV_PLAIN && (P == 0 || P == 2)),
-                  "wide rows: 32 lanes per row, plain, one row per lane");
+    static_assert(SL == 0 || ((SL == 32 || SL == 16) && !H && NR == 1 && MODE == GEMV_PLAIN),
+                  "wide rows: 16 or 32 lanes per row, plain, one row per lane");
     using G = typename GroupOf<F>::T;
     using Dt = typename GemvData<G, H>::T;
     constexpr int SUBL = SL ? SL : H ? 16 : 8; // lanes per row
@@ -597,7 +597,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
 
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
-        const float v = H ? wave::sum16(acc[i]) : SUBL == 32 ? sum32(acc[i]) : reduce8(acc[i]);
+        const float v = (H || SUBL == 16) ? wave::sum16(acc[i])
+                        : SUBL == 32              ? sum32(acc[i])
+                                                  : reduce8(acc[i]);
         const float v2 = MODE == GEMV_SILU ? (H ? wave::sum16(acc2[i]) : reduce8(acc2[i])) : 0.f;
         if (sub != 0 || !valid[i] || MODE == GEMV_ISUMS) continue;
         if (MODE == GEMV_SILU) {
@@ -700,14 +702,19 @@ template <int F> int launch_gemv_format(int mode, const GemvArgs &a, void *strea
     // input alike, so that both launches sum in the same order
     const bool wide = mode == GEMV_PLAIN && nr == 1 && ks == 1 && a.norm == nullptr &&
                       a.groups >= 32 && rows < 8 * 2048;
+    // 16 lanes per row (four rows per wave), on the same terms, for 16-31
+    // groups per row on fewer than 4096 rows, where 8-lane row-sets give
+    // under two workgroups per CU and three or four groups per lane
+    const bool w16 = mode == GEMV_PLAIN && nr == 1 && ks == 1 && a.norm == nullptr &&
+                     a.groups >= 16 && a.groups < 32 && rows < 4096;
     // half-group mode (Q2_0C, f32 stage, one row per lane; 4 rows per wave)
     // when its workgroups (twice the full-group count) still fit the 256 CUs
     // one each: a CU holding two would be the launch's tail
     const int half_wgs = (rows + 4 * waves - 1) / (4 * waves) * ks;
     const bool half = HasHalf<F>::value && a.xin && nr == 1 && mode != GEMV_ISUMS && !wide &&
-                      half_wgs <= HALF_MAX_WORKGROUPS;
+                      !w16 && half_wgs <= HALF_MAX_WORKGROUPS;
     if (wide) waves = 4;
-    const int rows_per_block = (wide ? 2 : half ? 4 : 8) * nr * waves;
+    const int rows_per_block = (wide ? 2 : w16 || half ? 4 : 8) * nr * waves;
     // a K split is a plain GEMV of an f32 row without norm, residual or
     // partial-row inputs (each slice writes its own partial row)
     if ((ks > 1 || a.nslots) &&
@@ -755,6 +762,20 @@ template <int F> int launch_gemv_format(int mode, const GemvArgs &a, void *strea
             hipLaunchKernelGGL((gemv_kernel<F, 1, GEMV_PLAIN, 0, 0, false, 32>), grid, block, lds, st, a);
         } else {
             hipLaunchKernelGGL((gemv_kernel<F, 1, GEMV_PLAIN, 1, 0, false, 32>), grid, block, lds, st, a);
+        }
+        return (int)hipGetLastError();
+    }
+    if (w16) {
+        // one or two groups per lane, all preloaded
+        if (a.groups <= 16) {
+            if (!a.xin)
+                hipLaunchKernelGGL((gemv_kernel<F, 1, GEMV_PLAIN, 0, 1, false, 16>), grid, block, lds, st, a);
+            else
+                hipLaunchKernelGGL((gemv_kernel<F, 1, GEMV_PLAIN, 1, 1, false, 16>), grid, block, lds, st, a);
+        } else if (!a.xin) {
+            hipLaunchKernelGGL((gemv_kernel<F, 1, GEMV_PLAIN, 0, 2, false, 16>), grid, block, lds, st, a);
+        } else {
+            hipLaunchKernelGGL((gemv_kernel<F, 1, GEMV_PLAIN, 1, 2, false, 16>), grid, block, lds, st, a);
         }
         return (int)hipGetLastError();
     }

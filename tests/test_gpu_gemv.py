@@ -122,10 +122,12 @@ def test_gemv_matches_oracle(gpu_ctx, oracle, dtype):
     check_decode_path(y, y_ref, mag, NAMES[dtype])
 
 
-@pytest.mark.parametrize("dtype", [Q2_0C, STQ1_0], ids=lambda d: NAMES[d])
-def test_gemv_k6144_down_shape(gpu_ctx, oracle, dtype):
-    rows, cols = 2048, 6144
-    _print("down", NAMES[dtype])
+@pytest.mark.parametrize("dtype", QUANT, ids=lambda d: NAMES[d])
+@pytest.mark.parametrize("rows,cols", [(2048, 6144), (3071, 4096)], ids=["2048x6144", "3071x4096"])
+def test_gemv_k6144_down_shape(gpu_ctx, oracle, dtype, rows, cols):
+    """Under 4096 rows of 16-31 groups the GEMV gives each row 16 lanes (one
+    or two groups each; the 1.8B down projection's shape and a ragged one)."""
+    _print("down", NAMES[dtype], rows, cols)
     w = random_matrix(dtype, rows, cols, seed=5)
     x = np.random.default_rng(9).normal(0, 1, cols).astype(np.float32)
     y = gpu_ctx.upload(dtype, w, (cols, rows)).matmul(x, 1)
