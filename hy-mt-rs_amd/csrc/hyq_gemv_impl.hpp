@@ -368,9 +368,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     // of its groups at once; otherwise the first group is preloaded and the
     // others load at the top of their iteration.
     StageRegs sr;
-    i32x4 qv[Q8_REG];
+    // int4 loads per thread: a preloading kernel covers at most GSTEP * P
+    // groups (16 int4 each) with at least 64 threads, so it issues no more
+    // than those need (the surplus would re-read the clamped last int4)
+    constexpr int NQ = P > 0 && GSTEP * P / 4 < Q8_REG ? GSTEP * P / 4 : Q8_REG;
+    i32x4 qv[NQ];
     const bool stage_reg = IN != 0 && groups <= 8 * STAGE_PASSES && (a.nsparts == 0 || groups <= 8);
-    const bool q8_reg = IN == 0 && groups * 16 <= Q8_REG * (int)blockDim.x;
+    const bool q8_reg = IN == 0 && groups * 16 <= NQ * (int)blockDim.x;
     // The words staged for the dots: the scales, then each sum array the
     // format reads, numbered [s | sum256 | sum16 | sum32] over the arrays
     // present; word i's source and LDS index are chosen by selects, so its
@@ -401,7 +405,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
         // clamped into bounds; the copy to LDS keeps the in-range ones
         const i32x4 *src = reinterpret_cast<const i32x4 *>(a.x.q);
 #pragma unroll
-        for (int j = 0; j < Q8_REG; ++j)
+        for (int j = 0; j < NQ; ++j)
             qv[j] = src[min((int)threadIdx.x + j * (int)blockDim.x, groups * 16 - 1)];
     }
     if (IN == 0 && meta_reg) {
@@ -454,7 +458,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
         int4 *dst = reinterpret_cast<int4 *>(lds);
         if (q8_reg) {
 #pragma unroll
-            for (int j = 0; j < Q8_REG; ++j) {
+            for (int j = 0; j < NQ; ++j) {
                 const int i = threadIdx.x + j * (int)blockDim.x;
                 if (i < groups * 16)
                     reinterpret_cast<i32x4 *>(dst)[(i >> 4) * (SLOT_INTS / 4) + (i & 15)] = qv[j];
