@@ -688,7 +688,10 @@ template <int F> int launch_gemv_format(int mode, const GemvArgs &a, void *strea
     if (mode != GEMV_ISUMS) {
         const bool heavy = F == Q6_K || F == Q8_0 || F == Q4_K || mode == GEMV_SILU;
         if (rows >= 8 * 4 * 4 * 1024 && !heavy) nr = 4;
-        else if (rows >= 8 * 2 * 4 * 1024) nr = 2;
+        // (with Q8 input Q6_K keeps one row per lane: measured faster, lm_head
+        // [120818 x 2048] 42.3 -> 33.5 us; with an input stage, which every
+        // workgroup repeats, two rows per lane halve that work)
+        else if (rows >= 8 * 2 * 4 * 1024 && (F != Q6_K || a.xin)) nr = 2;
         // one row per lane with Q8 input: single-wave workgroups measured
         // fastest (7B shapes, 6144-28672 rows); otherwise the largest tiles
         // that keep ~2 workgroups per CU

@@ -183,15 +183,24 @@ def test_gemv_zero_activation_group(gpu_ctx, oracle):
     check_decode_path(y, y_ref, mag)
 
 
-def test_lm_head_q6k_full_size(gpu_ctx, oracle):
+def test_lm_head_q6k_full_size(gpu_ctx, hyq, oracle):
+    """The f32 row (quantized in the launch, two rows per lane) and the Q8
+    row (one row per lane) give the same bits, within the oracle's bound."""
     rows, cols = 120818, 2048
     _print("lm_head")
     w = random_matrix(Q6_K, rows, cols, seed=77)
     x = np.random.default_rng(77).normal(0, 1, cols).astype(np.float32)
-    y = gpu_ctx.upload(Q6_K, w, (cols, rows)).matmul(x, 1)
+    W = gpu_ctx.upload(Q6_K, w, (cols, rows))
+    y = W.matmul(x, 1)
     q, s = oracle.q8_quantize(x)
     y_ref, mag = oracle.gemv_q8_f64(Q6_K, w, rows, cols, q, s)
     check_decode_path(y, y_ref, mag, "lm_head")
+    q8 = gpu_ctx.q8(cols)
+    xd = gpu_ctx.array(x)
+    q8.quantize_into(xd.ptr)
+    yd = gpu_ctx.empty(rows, np.float32)
+    hyq.check(hyq.lib().hyq_gemv_q8_d(gpu_ctx.handle, W.handle, q8.handle, None, yd.ptr))
+    assert np.array_equal(yd.numpy().view(np.uint32), y.view(np.uint32))
 
 
 # ---- fused entry points ----
