@@ -244,14 +244,11 @@ __device__ __forceinline__ void stage_loop(const GemvArgs &a, const float *xin, 
 }
 
 // Q8 input rows (no input stage) of up to Q8_REG int4 per thread are read
-// into registers before the weights' loads are issued, then copied to LDS.
-// With several rows per lane (the large launches) so are the row's scales
-// and the integer sums the format's dot reads (up to Q8_META words per
-// thread), which the dots then read from LDS instead of global memory; with
-// one row per lane each lane loads its groups' words from global memory into
-// registers just before each group's weights.
+// into registers before the weights' loads are issued, then copied to LDS;
+// the row's scales and the integer sums a group's dot reads are loaded by
+// each lane from global memory into registers just before the group's
+// weights (one row per lane with Q8 input).
 constexpr int Q8_REG = 8;
-constexpr int Q8_META = 8;
 // (a clang vector type: an array of HIP's int4 struct is not promoted to
 // registers here)
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -342,13 +339,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
         else G::load(D, w, row, gbase + g);
     };
     // The Q8 words a group's dot reads besides the activations: from LDS
-    // where an input stage or the Q8 copy puts them there, read at their use
-    // (Q8At); else from global memory into registers (G::Meta), loaded just
-    // before the group's weights so that their latency overlaps the
-    // weights' instead of following it.
+    // where an input stage puts them, read at their use (Q8At); with Q8
+    // input from global memory into registers (G::Meta), loaded just before
+    // the group's weights so that their latency overlaps the weights'
+    // instead of following it.
+    static_assert(IN != 0 || NR == 1, "Q8 input: one row per lane");
     using Mt = typename G::Meta;
-    constexpr bool STAGE_META = IN == 0 && NR >= 2;
-    constexpr bool META_PRE = IN == 0 && !STAGE_META;
+    constexpr bool META_PRE = IN == 0;
     Dt d[NR];
     Dt d2[MODE == GEMV_SILU ? NR : 1];
     auto load_group = [&](int g) {
@@ -375,31 +372,6 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     i32x4 qv[NQ];
     const bool stage_reg = IN != 0 && groups <= 8 * STAGE_PASSES && (a.nsparts == 0 || groups <= 8);
     const bool q8_reg = IN == 0 && groups * 16 <= NQ * (int)blockDim.x;
-    // The words staged for the dots: the scales, then each sum array the
-    // format reads, numbered [s | sum256 | sum16 | sum32] over the arrays
-    // present; word i's source and LDS index are chosen by selects, so its
-    // load is unconditional.
-    constexpr bool N256 = G::QSUMS & Q8_SUM256, N16 = G::QSUMS & Q8_SUM16,
-                   N32 = G::QSUMS & Q8_SUM32;
-    const int m1 = groups, m2 = m1 + (N256 ? groups : 0), m3 = m2 + (N16 ? 16 * groups : 0);
-    const int mwords = m3 + (N32 ? 8 * groups : 0);
-    const bool meta_reg = STAGE_META && mwords <= Q8_META * (int)blockDim.x;
-    auto meta_src = [&](int i) -> const int * {
-        const int *p = reinterpret_cast<const int *>(a.x.s) + i;
-        if (N256) p = i >= m1 ? a.x.sum256 + (i - m1) : p;
-        if (N16) p = i >= m2 ? a.x.sum16 + (i - m2) : p;
-        if (N32) p = i >= m3 ? a.x.sum32 + (i - m3) : p;
-        return p;
-    };
-    // LDS index (in words from the scales) of word i
-    auto meta_dst = [&](int i) -> int {
-        int d = i;
-        if (N256) d = i >= m1 ? groups + (i - m1) : d;
-        if (N16) d = i >= m2 ? 2 * groups + (i - m2) : d;
-        if (N32) d = i >= m3 ? 18 * groups + (i - m3) : d;
-        return d;
-    };
-    int mv[Q8_META];
     if (IN != 0 && stage_reg) stage_load<IN>(a, xin, a.norm, sr);
     if (IN == 0 && q8_reg) {
         // clamped into bounds; the copy to LDS keeps the in-range ones
@@ -407,11 +379,6 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
 #pragma unroll
         for (int j = 0; j < NQ; ++j)
             qv[j] = src[min((int)threadIdx.x + j * (int)blockDim.x, groups * 16 - 1)];
-    }
-    if (IN == 0 && meta_reg) {
-#pragma unroll
-        for (int j = 0; j < Q8_META; ++j)
-            mv[j] = *meta_src(min((int)threadIdx.x + j * (int)blockDim.x, mwords - 1));
     }
     static_assert(P == 0 || (NR == 1 && MODE == GEMV_PLAIN), "preload: plain, one row per lane");
     Dt dp[P > 0 ? P : 1];
@@ -441,13 +408,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
         }
     }
     Q8View xq = a.x;
-    // scales, then 256/16/32-value sums after the slots (contiguous, in the
-    // order meta_word numbers them)
+    // (input stage) scales, then 256/16/32-value sums after the slots
     float *sc = reinterpret_cast<float *>(lds + groups * SLOT_INTS);
     int *s256 = reinterpret_cast<int *>(sc + groups);
     int *s16 = s256 + groups;
     int *s32 = s16 + groups * 16;
-    if (IN != 0 || STAGE_META) {
+    if (IN != 0) {
         xq.s = sc;
         xq.sum256 = s256;
         xq.sum16 = s16;
@@ -466,17 +432,6 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
         } else {
             for (int i = threadIdx.x; i < groups * 16; i += blockDim.x)
                 dst[(i >> 4) * (SLOT_INTS / 4) + (i & 15)] = src[i];
-        }
-        int *meta = reinterpret_cast<int *>(sc);
-        if (!STAGE_META) {
-        } else if (meta_reg) {
-#pragma unroll
-            for (int j = 0; j < Q8_META; ++j) {
-                const int i = threadIdx.x + j * (int)blockDim.x;
-                if (i < mwords) meta[meta_dst(i)] = mv[j];
-            }
-        } else {
-            for (int i = threadIdx.x; i < mwords; i += blockDim.x) meta[meta_dst(i)] = *meta_src(i);
         }
     } else {
         float *gss = reinterpret_cast<float *>(s32 + groups * 8);
@@ -653,10 +608,16 @@ int launch_nr(int nr, int pre, const GemvArgs &a, dim3 grid, dim3 block, size_t 
             }
             if (nr == 1) return (int)hipGetLastError();
         }
-        switch (nr) {
-        case 1: hipLaunchKernelGGL((gemv_kernel<F, 1, MODE, IN, 0, false>), grid, block, lds, st, a); break;
-        case 2: hipLaunchKernelGGL((gemv_kernel<F, 2, MODE, IN, 0, false>), grid, block, lds, st, a); break;
-        default: hipLaunchKernelGGL((gemv_kernel<F, 4, MODE, IN, 0, false>), grid, block, lds, st, a); break;
+        if constexpr (IN == 2) {
+            switch (nr) {
+            case 1: hipLaunchKernelGGL((gemv_kernel<F, 1, MODE, IN, 0, false>), grid, block, lds, st, a); break;
+            case 2: hipLaunchKernelGGL((gemv_kernel<F, 2, MODE, IN, 0, false>), grid, block, lds, st, a); break;
+            default: hipLaunchKernelGGL((gemv_kernel<F, 4, MODE, IN, 0, false>), grid, block, lds, st, a); break;
+            }
+        } else {
+            // (several rows per lane only under an RMSNorm stage)
+            if (nr != 1) return (int)hipErrorInvalidValue;
+            hipLaunchKernelGGL((gemv_kernel<F, 1, MODE, IN, 0, false>), grid, block, lds, st, a);
         }
         return (int)hipGetLastError();
     }
@@ -684,24 +645,23 @@ int launch_in(int mode, int nr, int pre, const GemvArgs &a, dim3 grid, dim3 bloc
 template <int F> int launch_gemv_format(int mode, const GemvArgs &a, void *stream)
 {
     const int rows = a.rows_total;
-    int nr = 1, waves = 1;
-    if (mode != GEMV_ISUMS) {
+    // One row per lane, measured fastest with Q8 input or a plain f32 stage
+    // at every size (e.g. vocabulary-sized rows against two per lane: Q6_K
+    // [120818 x 2048] 42.3 -> 33.5 us with Q8 input, 40.4 -> 34.0 us from an
+    // f32 row; Q2_0C [131072 x 2048] 18.8 -> 13.1 us, against four). An
+    // RMSNorm stage costs each workgroup more, so there matrices of 64Ki
+    // rows and more take two (four for the lighter formats) rows per lane
+    // (the decode step's lm_head: ~5 us per token faster than with one).
+    int nr = 1;
+    if (mode != GEMV_ISUMS && a.norm) {
         const bool heavy = F == Q6_K || F == Q8_0 || F == Q4_K || mode == GEMV_SILU;
         if (rows >= 8 * 4 * 4 * 1024 && !heavy) nr = 4;
-        // (with Q8 input Q6_K keeps one row per lane: measured faster, lm_head
-        // [120818 x 2048] 42.3 -> 33.5 us; with an input stage, which every
-        // workgroup repeats, two rows per lane halve that work)
-        else if (rows >= 8 * 2 * 4 * 1024 && (F != Q6_K || a.xin)) nr = 2;
-        // one row per lane with Q8 input: single-wave workgroups measured
-        // fastest (7B shapes, 6144-28672 rows); otherwise the largest tiles
-        // that keep ~2 workgroups per CU
-        if (nr == 1 && !a.xin) waves = 1;
-        else if (rows >= 8 * nr * 4 * 512) waves = 4;
-        else if (rows >= 8 * nr * 2 * 512) waves = 2;
+        else if (rows >= 8 * 2 * 4 * 1024) nr = 2;
     }
-    // With an f32 input stage every workgroup quantizes the whole input row,
+    // Q8 input: single-wave workgroups (measured fastest, 7B shapes of
+    // 6144-28672 rows). An f32 input stage is repeated by every workgroup,
     // so fewer, wider workgroups (4 waves) share that work.
-    if (a.xin) waves = 4;
+    int waves = a.xin ? 4 : 1;
     const int ks = a.nslots > 0 ? a.nslots : a.kslices > 1 ? a.kslices : 1;
     // wide rows (32 lanes per row, two rows per wave): a plain GEMV of at
     // least 32 groups per row whose 8-lane row-sets would leave most SIMDs
