@@ -247,6 +247,8 @@ struct hyq_dense {
     std::unique_ptr<DeviceBuffer> moe_mem;
     float *moe_xn = nullptr;
     Q8Ref moe_q8;
+    // the output row's normalised Q8 (the lm_head GEMV's input)
+    Q8Ref out_q8;
     MoeRowBuf moe_row{};
     const hyq_weight *embedding = nullptr, *output = nullptr;
     float *output_norm = nullptr;
@@ -344,6 +346,23 @@ GemvArgs staged(const hyq_weight *w, const float *xin, const float *norm, float 
     return a;
 }
 
+// The output norm and lm_head (src/model.rs:374-380): the row (plus the
+// last down projection's nparts partial rows) normalised and quantized to Q8
+// once, then the Q8-input GEMV (one row per lane, no input stage repeated by
+// each of its workgroups).
+int lm_head(hyq_dense *m, const float *x, const float *parts, int nparts, hipStream_t st)
+{
+    const hyq_dense_config &c = m->cfg;
+    const Q8Ref &q = m->out_q8;
+    HYQ_LAUNCH(launch_rms_norm_q8(x, m->output_norm, c.hidden, c.rms_eps, nullptr, q.q, q.s,
+                                  q.sum16, q.sum32, q.sum256, st, parts, nparts, c.hidden),
+               "output_norm_q8");
+    HYQ_LAUNCH(launch_gemv(m->output->dtype, GEMV_PLAIN, gemv_args(m->output, q, m->logits, nullptr),
+                           st),
+               "gemv_lm_head");
+    return HYQ_OK;
+}
+
 int enqueue_step(hyq_dense *m, bool trace = false)
 {
     const hyq_dense_config &c = m->cfg;
@@ -430,13 +449,7 @@ int enqueue_step(hyq_dense *m, bool trace = false)
                                         m->trace + (size_t)(l + 1) * c.hidden, st),
                        "trace");
     }
-    {
-        GemvArgs a = staged(m->output, m->hidden, m->output_norm, c.rms_eps, m->logits, nullptr);
-        a.sparts = m->parts;
-        a.nsparts = np;
-        a.parts_stride = c.hidden;
-        HYQ_LAUNCH(launch_gemv(m->output->dtype, GEMV_PLAIN, a, st), "gemv_lm_head");
-    }
+    if (int rc = lm_head(m, m->hidden, m->parts, np, st)) return rc;
     HYQ_LAUNCH(launch_argmax(m->logits, c.vocab, m->argmax_scratch,
                              (int *)(m->argmax_scratch + 64), m->token, m->state, m->history, st),
                "argmax");
@@ -596,9 +609,7 @@ int enqueue_prefill_chunk(hyq_dense *m, int n)
                                    hipMemcpyDeviceToDevice, st),
                     "trace");
     }
-    GemvArgs a = staged(m->output, m->pf_hid + (size_t)(n - 1) * H, m->output_norm, c.rms_eps,
-                        m->logits, nullptr);
-    HYQ_LAUNCH(launch_gemv(m->output->dtype, GEMV_PLAIN, a, st), "gemv_lm_head");
+    if (int rc = lm_head(m, m->pf_hid + (size_t)(n - 1) * H, nullptr, 0, st)) return rc;
     HYQ_LAUNCH(launch_argmax(m->logits, c.vocab, m->argmax_scratch,
                              (int *)(m->argmax_scratch + 64), m->token, m->state, nullptr, st),
                "argmax");
@@ -687,6 +698,9 @@ int hyq_dense_create(hyq_ctx *ctx, const hyq_dense_config *cfg, size_t context, 
     const size_t o_att_out = take(QL);
     const size_t o_parts = take((size_t)GEMV_MAX_PARTS * H);
     const size_t o_arg = take(128), o_tok = take(4), o_state = take(4);
+    const size_t ng = (H + 255) / 256;
+    const size_t o_oq = take((H + 3) / 4), o_os = take(ng), o_o16 = take(16 * ng);
+    const size_t o_o32 = take(8 * ng), o_o256 = take(ng);
     rc = m->mem.alloc(ctx->device, off);
     if (rc) return rc;
     uint8_t *base = (uint8_t *)m->mem.ptr;
@@ -713,6 +727,12 @@ int hyq_dense_create(hyq_ctx *ctx, const hyq_dense_config *cfg, size_t context, 
     m->argmax_scratch = (float *)(base + o_arg);
     m->token = (int32_t *)(base + o_tok);
     m->state = (StepState *)(base + o_state);
+    m->out_q8.q = (int8_t *)(base + o_oq);
+    m->out_q8.s = (float *)(base + o_os);
+    m->out_q8.sum16 = (int32_t *)(base + o_o16);
+    m->out_q8.sum32 = (int32_t *)(base + o_o32);
+    m->out_q8.sum256 = (int32_t *)(base + o_o256);
+    m->out_q8.n = H;
     // rope_frequencies (src/model.rs:263-269): base^(-2j/head_dim) in f32
     std::vector<float> freq(D / 2);
     for (size_t j = 0; j < D / 2; ++j)

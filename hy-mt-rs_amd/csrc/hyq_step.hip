@@ -46,34 +46,58 @@ __global__ __launch_bounds__(256) void embed_kernel(WView w, int cols, const int
 // row (n <= 64 Ki values, read from L2) so that no cross-workgroup sync is
 // needed. y = x * scale * w with scale = 1 / sqrt(mean(x^2) + eps), the x86
 // arm's operation order (src/model.rs:825-829).
+// x is the row ((x + p_0) + p_1) + ... with nparts partial rows p_k at
+// parts + k * pstride (a K-split product's slices, added in the order the
+// GEMV input stage adds them).
 __global__ __launch_bounds__(256) void rms_norm_q8_kernel(const float *__restrict__ x,
                                                           const float *__restrict__ w, int n,
                                                           float eps, float *__restrict__ y,
                                                           int8_t *q, float *s, int32_t *s16,
-                                                          int32_t *s32, int32_t *s256)
+                                                          int32_t *s32, int32_t *s256,
+                                                          const float *__restrict__ parts,
+                                                          int nparts, int pstride)
 {
     __shared__ float part[4];
     const int t = threadIdx.x;
+    auto row4 = [&](int i) {
+        float4 v = reinterpret_cast<const float4 *>(x)[i];
+        for (int k = 0; k < nparts; ++k) {
+            const float4 p = reinterpret_cast<const float4 *>(parts + (size_t)k * pstride)[i];
+            v = make_float4(v.x + p.x, v.y + p.y, v.z + p.z, v.w + p.w);
+        }
+        return v;
+    };
+    auto row1 = [&](int i) {
+        float v = x[i];
+        for (int k = 0; k < nparts; ++k) v = v + parts[(size_t)k * pstride + i];
+        return v;
+    };
     float ss = 0.f;
-    if ((reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+    if ((reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+        (nparts == 0 || ((reinterpret_cast<uintptr_t>(parts) & 15) == 0 && pstride % 4 == 0))) {
         // all of this thread's float4 loads in flight together
-        const float4 *x4 = reinterpret_cast<const float4 *>(x);
         const int n4 = n / 4;
         int i = t;
         for (; i + 768 < n4; i += 1024) {
-            const float4 a = x4[i], b = x4[i + 256], c = x4[i + 512], d = x4[i + 768];
+            const float4 a = row4(i), b = row4(i + 256), c = row4(i + 512), d = row4(i + 768);
             ss += (a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w) +
                   (b.x * b.x + b.y * b.y + b.z * b.z + b.w * b.w) +
                   (c.x * c.x + c.y * c.y + c.z * c.z + c.w * c.w) +
                   (d.x * d.x + d.y * d.y + d.z * d.z + d.w * d.w);
         }
         for (; i < n4; i += 256) {
-            const float4 a = x4[i];
+            const float4 a = row4(i);
             ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
         }
-        for (int j = n4 * 4 + t; j < n; j += 256) ss += x[j] * x[j];
+        for (int j = n4 * 4 + t; j < n; j += 256) {
+            const float v = row1(j);
+            ss += v * v;
+        }
     } else {
-        for (int i = t; i < n; i += 256) ss += x[i] * x[i];
+        for (int i = t; i < n; i += 256) {
+            const float v = row1(i);
+            ss += v * v;
+        }
     }
     ss = wave_sum(ss);
     if ((t & 63) == 0) part[t >> 6] = ss;
@@ -86,7 +110,7 @@ __global__ __launch_bounds__(256) void rms_norm_q8_kernel(const float *__restric
     float v = 0.f;
     if (t < len) {
         const int i = g * 256 + t;
-        v = x[i] * scale * w[i];
+        v = row1(i) * scale * w[i];
         if (y) y[i] = v;
     }
     q8_quantize_group(v, g, len, q, s, s16, s32, s256);
@@ -618,10 +642,12 @@ int launch_embed_rows(int fmt, WView w, int cols, const int *tokens, int n, floa
 }
 
 int launch_rms_norm_q8(const float *x, const float *w, int n, float eps, float *y, int8_t *q,
-                       float *s, int32_t *s16, int32_t *s32, int32_t *s256, void *stream)
+                       float *s, int32_t *s16, int32_t *s32, int32_t *s256, void *stream,
+                       const float *parts, int nparts, int pstride)
 {
     hipLaunchKernelGGL(rms_norm_q8_kernel, dim3((n + 255) / 256), dim3(256), 0,
-                       (hipStream_t)stream, x, w, n, eps, y, q, s, s16, s32, s256);
+                       (hipStream_t)stream, x, w, n, eps, y, q, s, s16, s32, s256, parts, nparts,
+                       pstride);
     return (int)hipGetLastError();
 }
 

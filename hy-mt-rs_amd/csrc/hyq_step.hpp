@@ -21,8 +21,10 @@ int launch_embed_row(int fmt, WView w, int cols, const int *token, float *out, v
 // Rows out[i] = embedding row tokens[i] for i < n (tokens in device memory).
 int launch_embed_rows(int fmt, WView w, int cols, const int *tokens, int n, float *out,
                       void *stream);
+// x may carry nparts partial rows at parts + k * pstride, added to it first
 int launch_rms_norm_q8(const float *x, const float *w, int n, float eps, float *y, int8_t *q,
-                       float *s, int32_t *s16, int32_t *s32, int32_t *s256, void *stream);
+                       float *s, int32_t *s16, int32_t *s32, int32_t *s256, void *stream,
+                       const float *parts = nullptr, int nparts = 0, int pstride = 0);
 // norm_first: the hy_v3 order (per-head rms_norm, then RoPE); otherwise the
 // dense one (src/model.rs:425-446).
 int launch_rope_norm_kv(float *q, const float *k, const float *v, const float *qn,
