@@ -366,9 +366,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     // others load at the top of their iteration.
     StageRegs sr;
     // int4 loads per thread: a preloading kernel covers at most GSTEP * P
-    // groups (16 int4 each) with at least 64 threads, so it issues no more
-    // than those need (the surplus would re-read the clamped last int4)
-    constexpr int NQ = P > 0 && GSTEP * P / 4 < Q8_REG ? GSTEP * P / 4 : Q8_REG;
+    // groups (16 int4 each) with 64 threads (256 in the 32-lane form), so it
+    // issues no more than those need (the surplus would re-read the clamped
+    // last int4); other block sizes take the loop below
+    constexpr int QW = SL == 32 ? 4 : 1;
+    constexpr int NQ = P > 0 && GSTEP * P / (4 * QW) < Q8_REG ? GSTEP * P / (4 * QW) : Q8_REG;
     i32x4 qv[NQ];
     const bool stage_reg = IN != 0 && groups <= 8 * STAGE_PASSES && (a.nsparts == 0 || groups <= 8);
     const bool q8_reg = IN == 0 && groups * 16 <= NQ * (int)blockDim.x;
