@@ -295,6 +295,35 @@ def test_non_finite_logits_poison_the_session(gpu_ctx, hyq):
     dec.close()
 
 
+def test_step_argmax_ties_take_the_first_row(gpu_ctx, hyq):
+    """The step's greedy token reduces the logits in two passes (per-block
+    maxima, then the blocks). Rows 0..776 of the output matrix have zero
+    block scales (logits exactly 0) and every later row is a copy of row
+    777, so the maximum is tied across many blocks: the token is 777 when
+    that logit is positive, else 0 (the first maximum), in forward, the graph
+    decode loop and prefill alike."""
+    c = SMALL
+    model = make_dense_model(c, linear=Q2_0C, seed=13)
+    rows = random_matrix(Q6_K, c["vocab"], c["hidden"], seed=130).reshape(c["vocab"], -1)
+    rows[777:] = rows[777]
+    blocks = rows[:777].reshape(777, -1, 210)  # 210-byte Q6_K blocks, d at 208
+    blocks[:, :, 208:210] = np.array([0.0], np.float16).view(np.uint8)
+    model["output"] = rows.reshape(-1)
+    dec = load_dense(hyq, gpu_ctx, model, 32)
+    for token in (3, 5, 8):
+        dec.position = 0
+        logits, nxt = dec.forward(token)
+        assert np.all(logits[:777] == 0) and np.all(logits[777:] == logits[777])
+        assert nxt == (777 if logits[777] > 0 else 0), (token, logits[777], nxt)
+    dec.position = 0
+    toks = dec.generate(3, 6, use_graph=True)
+    assert set(int(t) for t in toks) <= {0, 777}
+    dec.position = 0
+    logits, nxt = dec.prefill([1, 2, 3])
+    assert nxt == (777 if logits[777] > 0 else 0)
+    dec.close()
+
+
 @pytest.mark.parametrize("pos,norm_first", [(0, False), (1087, False), (1151, False),
                                             (1087, True), (40, True)])
 def test_attention_rope_fused(gpu_ctx, hyq, oracle, pos, norm_first):
