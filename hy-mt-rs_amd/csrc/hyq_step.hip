@@ -554,10 +554,19 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float *__rest
     float v = -INFINITY;
     int idx = 0x7fffffff;
     bool nonfinite = false;
-    for (int i = blockIdx.x * 256 + t; i < n; i += gridDim.x * 256) {
-        const float xi = x[i];
-        nonfinite |= !isfinite(xi);
-        if (!isnan(xi)) better(v, idx, xi, i);
+    // eight values per thread in flight at once (clamped into bounds, the
+    // surplus ignored); the grid makes one round enough up to 131072 values
+    const int stride = gridDim.x * 256;
+    for (int base = blockIdx.x * 256 + t; base < n; base += 8 * stride) {
+        float xv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) xv[u] = x[min(base + u * stride, n - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (base + u * stride < n) {
+                nonfinite |= !isfinite(xv[u]);
+                if (!isnan(xv[u])) better(v, idx, xv[u], base + u * stride);
+            }
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1)
@@ -775,7 +784,7 @@ int launch_attention_rope(const float *q, const float *k, const float *v, const 
     return (int)hipGetLastError();
 }
 
-int argmax_partials(int n) { return std::min(64, (n + 4095) / 4096 > 0 ? (n + 4095) / 4096 : 1); }
+int argmax_partials(int n) { return std::min(64, std::max(1, (n + 2047) / 2048)); }
 
 int launch_argmax(const float *x, int n, float *pv, int *pi, int *token, StepState *st,
                   int *history, void *stream)
