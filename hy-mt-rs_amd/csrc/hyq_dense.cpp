@@ -363,13 +363,18 @@ int lm_head(hyq_dense *m, const float *x, const float *parts, int nparts, hipStr
     return HYQ_OK;
 }
 
-int enqueue_step(hyq_dense *m, bool trace = false)
+// One decode step. It ends with the greedy token, whose final pass also
+// writes that token's embedding row to the hidden row; embed = false starts
+// from that row (the decode loop after its first step), embed = true embeds
+// the state's token first.
+int enqueue_step(hyq_dense *m, bool trace = false, bool embed = true)
 {
     const hyq_dense_config &c = m->cfg;
     hipStream_t st = m->ctx->stream;
-    HYQ_LAUNCH(launch_embed_row(m->embedding->dtype, m->embedding->view, c.hidden, m->token,
-                                m->hidden, st),
-               "embed_row");
+    if (embed)
+        HYQ_LAUNCH(launch_embed_row(m->embedding->dtype, m->embedding->view, c.hidden, m->token,
+                                    m->hidden, st),
+                   "embed_row");
     const int *pos = &m->state->pos;
     const int ks = m->down_ks;
     const bool norm_first = m->arch == HYQ_ARCH_HYV3;
@@ -450,8 +455,10 @@ int enqueue_step(hyq_dense *m, bool trace = false)
                        "trace");
     }
     if (int rc = lm_head(m, m->hidden, m->parts, np, st)) return rc;
-    HYQ_LAUNCH(launch_argmax(m->logits, c.vocab, m->argmax_scratch,
-                             (int *)(m->argmax_scratch + 64), m->token, m->state, m->history, st),
+    HYQ_LAUNCH(launch_argmax_embed(m->logits, c.vocab, m->argmax_scratch,
+                                   (int *)(m->argmax_scratch + 64), m->token, m->state, m->history,
+                                   m->embedding->dtype, m->embedding->view, c.hidden, m->hidden,
+                                   st),
                "argmax");
     return HYQ_OK;
 }
@@ -1088,11 +1095,15 @@ int hyq_dense_generate(hyq_dense *m, int32_t token, size_t steps, int use_graph,
         m->history_cap = steps;
     }
     if ((rc = write_state(m, token, 0, (int)steps))) return rc;
+    // the first step's input row; every step's argmax then writes the next
+    HYQ_LAUNCH(launch_embed_row(m->embedding->dtype, m->embedding->view, m->cfg.hidden, m->token,
+                                m->hidden, st),
+               "embed_row");
     if (use_graph) {
         if (!m->exec) {
             HYQ_HIP(hipStreamSynchronize(st), "hipStreamSynchronize");
             HYQ_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "BeginCapture");
-            rc = enqueue_step(m);
+            rc = enqueue_step(m, false, false);
             hipGraph_t graph = nullptr;
             hipError_t e = hipStreamEndCapture(st, &graph);
             if (rc) {
@@ -1107,7 +1118,7 @@ int hyq_dense_generate(hyq_dense *m, int32_t token, size_t steps, int use_graph,
         for (size_t i = 0; i < steps; ++i) HYQ_HIP(hipGraphLaunch(m->exec, st), "hipGraphLaunch");
     } else {
         for (size_t i = 0; i < steps; ++i)
-            if ((rc = enqueue_step(m))) return rc;
+            if ((rc = enqueue_step(m, false, false))) return rc;
     }
     HYQ_HIP(hipMemcpyAsync(tokens, m->history, steps * 4, hipMemcpyDeviceToHost, st),
             "hipMemcpy(tokens)");

@@ -621,7 +621,81 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float *__restric
     }
 }
 
+// The argmax's final pass fused with the next step's embedding row: every
+// workgroup's first wave reduces the np partials (as argmax_final_kernel),
+// workgroup 0 alone stores the token and advances the step state, and each
+// workgroup decodes 256 values of the token's row of w into out (as
+// embed_kernel does), so the decode loop needs no embedding launch.
+template <int F>
+__global__ __launch_bounds__(256) void argmax_final_embed_kernel(
+    const float *__restrict__ x, int n, const float *__restrict__ pv, const int *__restrict__ pi,
+    int np, int *__restrict__ token, StepState *st, int *history, WView w, int cols,
+    float *__restrict__ out)
+{
+    __shared__ int s_idx;
+    const int t = threadIdx.x;
+    if (t < 64) {
+        float v = -INFINITY;
+        int idx = 0x7fffffff;
+        bool nonfinite = false;
+        for (int i = t; i < np; i += 64) {
+            const int pii = pi[i];
+            nonfinite |= (pii & ARGMAX_NONFINITE) != 0;
+            better(v, idx, pv[i], pii & ~ARGMAX_NONFINITE);
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1)
+            better(v, idx, __shfl_xor(v, off, 64), __shfl_xor(idx, off, 64));
+        const bool any_nf = __any(nonfinite);
+        if (t == 0) {
+            if (isnan(x[0])) idx = 0;
+            idx = min(max(idx, 0), n - 1);
+            s_idx = idx;
+            if (blockIdx.x == 0) {
+                *token = idx;
+                if (st) {
+                    if (history && st->step < st->history_cap) history[st->step] = idx;
+                    st->step += 1;
+                    st->pos += 1;
+                    if (any_nf) st->nonfinite = 1;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    const int i = blockIdx.x * 256 + t;
+    if (i >= cols) return;
+    const size_t row = (size_t)min(s_idx, w.rows - 1);
+    const size_t blk = row * (size_t)w.nb + i / block_len(F);
+    out[i] = dec::decode_plane_value<F>(w, blk, i % block_len(F));
+}
+
 } // namespace
+
+int launch_argmax_embed(const float *x, int n, float *pv, int *pi, int *token, StepState *st,
+                        int *history, int fmt, WView w, int cols, float *out, void *stream)
+{
+    const int np = argmax_partials(n);
+    hipStream_t s = (hipStream_t)stream;
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(np), dim3(256), 0, s, x, n, pv, pi);
+    const dim3 grid((cols + 255) / 256), block(256);
+#define HYQ_AE(F)                                                                              \
+    case F: hipLaunchKernelGGL(argmax_final_embed_kernel<F>, grid, block, 0, s, x, n, pv, pi,     \
+                               np, token, st, history, w, cols, out);                            \
+        break;
+    switch (fmt) {
+        HYQ_AE(Q2_0C)
+        HYQ_AE(STQ1_0)
+        HYQ_AE(Q4_K)
+        HYQ_AE(Q6_K)
+        HYQ_AE(Q8_0)
+        HYQ_AE(F32)
+        HYQ_AE(F16)
+    default: return (int)hipErrorInvalidValue;
+    }
+#undef HYQ_AE
+    return (int)hipGetLastError();
+}
 
 int launch_embed_row(int fmt, WView w, int cols, const int *token, float *out, void *stream)
 {

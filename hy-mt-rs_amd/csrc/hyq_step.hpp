@@ -91,5 +91,10 @@ int launch_attention_rope(const float *q, const float *k, const float *v, const 
 int argmax_partials(int n);
 int launch_argmax(const float *x, int n, float *pv, int *pi, int *token, StepState *st,
                   int *history, void *stream);
+// The same argmax, whose final pass also writes the chosen token's row of
+// the embedding w (format fmt, cols values) to out: the next decode step's
+// input.
+int launch_argmax_embed(const float *x, int n, float *pv, int *pi, int *token, StepState *st,
+                        int *history, int fmt, WView w, int cols, float *out, void *stream);
 
 } // namespace hyq
