@@ -271,8 +271,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     static_assert(!SLOT || (NR == 1 && !H && SL == 0 && P == 0 &&
                             (MODE == GEMV_SILU || MODE == GEMV_PLAIN)),
                   "expert slots: one row per lane, gate/up or plain");
-    static_assert(SL == 0 || ((SL == 32 || SL == 16) && !H && NR == 1 && MODE == GEMV_PLAIN),
-                  "wide rows: 16 or 32 lanes per row, plain, one row per lane");
+    static_assert(SL == 0 || ((SL == 64 || SL == 32 || SL == 16) && !H && NR == 1 &&
+                              MODE == GEMV_PLAIN),
+                  "wide rows: 16, 32 or 64 lanes per row, plain, one row per lane");
     using G = typename GroupOf<F>::T;
     using Dt = typename GemvData<G, H>::T;
     constexpr int SUBL = SL ? SL : H ? 16 : 8; // lanes per row
@@ -366,10 +367,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     // others load at the top of their iteration.
     StageRegs sr;
     // int4 loads per thread: a preloading kernel covers at most GSTEP * P
-    // groups (16 int4 each) with 64 threads (256 in the 32-lane form), so it
-    // issues no more than those need (the surplus would re-read the clamped
-    // last int4); other block sizes take the loop below
-    constexpr int QW = SL == 32 ? 4 : 1;
+    // groups (16 int4 each) with 64 threads (256 in the 32- and 64-lane
+    // forms), so it issues no more than those need (the surplus would re-read
+    // the clamped last int4); other block sizes take the loop below
+    constexpr int QW = SL >= 32 ? 4 : 1;
     constexpr int NQ = P > 0 && GSTEP * P / (4 * QW) < Q8_REG ? GSTEP * P / (4 * QW) : Q8_REG;
     i32x4 qv[NQ];
     const bool stage_reg = IN != 0 && groups <= 8 * STAGE_PASSES && (a.nsparts == 0 || groups <= 8);
@@ -559,6 +560,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
         const float v = (H || SUBL == 16) ? wave::sum16(acc[i])
+                        : SUBL == 64              ? wave::sum64(acc[i])
                         : SUBL == 32              ? sum32(acc[i])
                                                   : reduce8(acc[i]);
         const float v2 = MODE == GEMV_SILU ? (H ? wave::sum16(acc2[i]) : reduce8(acc2[i])) : 0.f;
@@ -673,9 +675,16 @@ template <int F> int launch_gemv_format(int mode, const GemvArgs &a, void *strea
                       a.groups >= 32 && rows < 8 * 2048;
     // 16 lanes per row (four rows per wave), on the same terms, for 16-31
     // groups per row on fewer than 4096 rows, where 8-lane row-sets give
-    // under two workgroups per CU and three or four groups per lane
+    // under two workgroups per CU and three or four groups per lane; at any
+    // row count for Q6_K, whose dot is the heaviest per byte ([32000 x 4096]
+    // 25.0 -> 20.0 us; Q4_K [6144 x 4096] measured 3 % slower so)
     const bool w16 = mode == GEMV_PLAIN && nr == 1 && ks == 1 && a.norm == nullptr &&
-                     a.groups >= 16 && a.groups < 32 && rows < 4096;
+                     a.groups >= 16 && a.groups < 32 && (rows < 4096 || F == Q6_K);
+    // 64 lanes per row (one group each, one row per wave, 4-wave workgroups)
+    // for the long rows of the two formats with the heaviest dots: the 7B
+    // down [4096 x 14336] Q6_K 13.9 -> 11.9 us, STQ1_0 6.5 -> 6.4 us (Q4_K
+    // and Q8_0 measured 4-5 % slower so)
+    const bool w64 = wide && a.groups > 32 && a.groups <= 64 && (F == Q6_K || F == STQ1_0);
     // half-group mode (Q2_0C, f32 stage, one row per lane; 4 rows per wave)
     // when its workgroups (twice the full-group count) still fit the 256 CUs
     // one each: a CU holding two would be the launch's tail
@@ -683,7 +692,7 @@ template <int F> int launch_gemv_format(int mode, const GemvArgs &a, void *strea
     const bool half = HasHalf<F>::value && a.xin && nr == 1 && mode != GEMV_ISUMS && !wide &&
                       !w16 && half_wgs <= HALF_MAX_WORKGROUPS;
     if (wide) waves = 4;
-    const int rows_per_block = (wide ? 2 : w16 || half ? 4 : 8) * nr * waves;
+    const int rows_per_block = (w64 ? 1 : wide ? 2 : w16 || half ? 4 : 8) * nr * waves;
     // a K split is a plain GEMV of an f32 row without norm, residual or
     // partial-row inputs (each slice writes its own partial row)
     if ((ks > 1 || a.nslots) &&
@@ -719,6 +728,13 @@ template <int F> int launch_gemv_format(int mode, const GemvArgs &a, void *strea
     // groups per lane preloaded by the plain one-row-per-lane kernel
     const int pre = a.groups <= 32 ? (a.groups + 7) / 8 : 0;
     hipStream_t st = (hipStream_t)stream;
+    if (w64) {
+        if (!a.xin)
+            hipLaunchKernelGGL((gemv_kernel<F, 1, GEMV_PLAIN, 0, 1, false, 64>), grid, block, lds, st, a);
+        else
+            hipLaunchKernelGGL((gemv_kernel<F, 1, GEMV_PLAIN, 1, 1, false, 64>), grid, block, lds, st, a);
+        return (int)hipGetLastError();
+    }
     if (wide) {
         // rows of at most 64 groups: both of a lane's groups preloaded
         // before the input stage (the same sums in the same order)

@@ -123,10 +123,12 @@ def test_gemv_matches_oracle(gpu_ctx, oracle, dtype):
 
 
 @pytest.mark.parametrize("dtype", QUANT, ids=lambda d: NAMES[d])
-@pytest.mark.parametrize("rows,cols", [(2048, 6144), (3071, 4096)], ids=["2048x6144", "3071x4096"])
+@pytest.mark.parametrize("rows,cols", [(2048, 6144), (3071, 4096), (4100, 4096)],
+                         ids=["2048x6144", "3071x4096", "4100x4096"])
 def test_gemv_k6144_down_shape(gpu_ctx, oracle, dtype, rows, cols):
     """Under 4096 rows of 16-31 groups the GEMV gives each row 16 lanes (one
-    or two groups each; the 1.8B down projection's shape and a ragged one)."""
+    or two groups each; the 1.8B down projection's shape and a ragged one);
+    Q6_K does so at any row count (4100 rows), the other formats keep 8."""
     _print("down", NAMES[dtype], rows, cols)
     w = random_matrix(dtype, rows, cols, seed=5)
     x = np.random.default_rng(9).normal(0, 1, cols).astype(np.float32)
