@@ -263,12 +263,16 @@ struct GroupSTQ {
     // the sign picks e or 0xAA - e per byte (no borrows: every code is <= 2).
     __device__ __forceinline__ static uint32_t codes(uint32_t nb, uint32_t ms)
     {
+        return codes_sel(nb & 0x07070707u, byte_mask(nb << 4), ms);
+    }
+    // The same from the nibbles' low three bits (sel, one per byte) and the
+    // 0xFF / 0x00 byte mask of their bit 3 (m3).
+    __device__ __forceinline__ static uint32_t codes_sel(uint32_t sel, uint32_t m3, uint32_t ms)
+    {
         constexpr uint32_t CB0 = 0x092989a9u, CB1 = 0x062686a6u, CB2 = 0x121a929au,
                            CB3 = 0x424a626au;
-        const uint32_t sel = nb & 0x07070707u;
         const uint32_t r0 = __builtin_amdgcn_perm(CB1, CB0, sel);
         const uint32_t r1 = __builtin_amdgcn_perm(CB3, CB2, sel);
-        const uint32_t m3 = byte_mask(nb << 4); // nibble bit 3
         const uint32_t e = (r1 & m3) | (r0 & ~m3);
         const uint32_t en = 0xAAAAAAAAu - e;
         return (en & ms) | (e & ~ms);
@@ -287,21 +291,30 @@ struct GroupSTQ {
         const uint32_t nib[8] = {D.nib[0].x, D.nib[0].y, D.nib[0].z, D.nib[0].w,
                                  D.nib[1].x, D.nib[1].y, D.nib[1].z, D.nib[1].w};
         const uint32_t sg[2] = {D.sgn.x, D.sgn.y};
-        int raw = 0;
+        // The four 2-bit codes of each codebook byte are dotted at their
+        // place values (code p as 4^p code, bytes at most 48, for p = 3 via
+        // one shift: 16 code) into four accumulators, each then an exact
+        // multiple of its place value.
+        int r0 = 0, r1 = 0, r2 = 0, r3 = 0;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
 #pragma unroll
             for (int qi = 0; qi < 4; ++qi) {
                 const uint32_t dw = nib[2 * c + (qi >> 1)];
-                const uint32_t nb = (qi & 1) ? (dw >> 4) & 0x0F0F0F0Fu : dw & 0x0F0F0F0Fu;
+                // the nibbles' selector bits, and bit 3 moved to bit 7
+                const uint32_t sel = (qi & 1) ? (dw >> 4) & 0x07070707u : dw & 0x07070707u;
+                const uint32_t m3 = byte_mask((qi & 1) ? dw : dw << 4);
                 const int q = (c & 1) * 4 + qi; // quad index inside the sign dword
                 // sign bit q of each byte of S moved to bit 7
-                const uint32_t e = codes(nb, byte_mask(sg[c >> 1] << (7 - q)));
-#pragma unroll
-                for (int p = 0; p < 4; ++p)
-                    raw = sdot4((e >> (2 * p)) & 0x03030303u, act[16 * c + 4 * p + qi], raw);
+                const uint32_t e = codes_sel(sel, m3, byte_mask(sg[c >> 1] << (7 - q)));
+                const int *a = act + 16 * c + qi;
+                r0 = sdot4(e & 0x03030303u, a[0], r0);
+                r1 = sdot4(e & 0x0C0C0C0Cu, a[4], r1);
+                r2 = sdot4(e & 0x30303030u, a[8], r2);
+                r3 = sdot4((e >> 2) & 0x30303030u, a[12], r3);
             }
         }
+        const int raw = (r0 + (r1 >> 2)) + ((r2 + r3) >> 4);
         int isum = raw - x.sum256();
         if (EMIT) out[0] = isum;
         return (float)isum * (h2f(D.d) * x.scale());
