@@ -80,6 +80,28 @@ struct Q8At {
 };
 
 struct GroupQ2C {
+    // sum c q over U 16-byte code units: byte b of unit dword m holds codes
+    // k = 0..3 (bits 2k, 2k + 1) of weights 64 u + 16 k + 4 m + b. The codes
+    // are dotted at their place values (code k as 4^k c for k < 3, and k = 3
+    // via one shift as 16 c, so every byte stays below 64) into three
+    // accumulators, each an exact multiple of its place value.
+    template <int U>
+    __device__ __forceinline__ static int code_dot(const uint4 *w, const int *act)
+    {
+        int r0 = 0, r1 = 0, r23 = 0;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t c[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                r0 = sdot4(c[m] & 0x03030303u, act[16 * u + m], r0);
+                r1 = sdot4(c[m] & 0x0C0C0C0Cu, act[16 * u + 4 + m], r1);
+                r23 = sdot4(c[m] & 0x30303030u, act[16 * u + 8 + m], r23);
+                r23 = sdot4((c[m] >> 2) & 0x30303030u, act[16 * u + 12 + m], r23);
+            }
+        }
+        return (r0 + (r1 >> 2)) + (r23 >> 4);
+    }
     static constexpr int ISUMS = 1;
     static constexpr int QSUMS = Q8_SUM256 | Q8_SUM32; // full / half-group dots
     struct Meta {
@@ -116,18 +138,7 @@ struct GroupQ2C {
     {
         Data D = Din;
         D.hold_all();
-        int raw = 0;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint32_t c[4] = {D.w[u].x, D.w[u].y, D.w[u].z, D.w[u].w};
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                raw = sdot4(c[m] & 0x03030303u, act[16 * u + m], raw);
-                raw = sdot4((c[m] >> 2) & 0x03030303u, act[16 * u + 4 + m], raw);
-                raw = sdot4((c[m] >> 4) & 0x03030303u, act[16 * u + 8 + m], raw);
-                raw = sdot4((c[m] >> 6) & 0x03030303u, act[16 * u + 12 + m], raw);
-            }
-        }
+        const int raw = code_dot<4>(D.w, act);
         int isum = 2 * raw - 3 * x.sum256();
         if (EMIT) out[0] = isum;
         return (float)isum * (h2f(D.d) * x.scale());
@@ -163,18 +174,7 @@ struct GroupQ2C {
     {
         Half D = Din;
         D.hold_all();
-        int raw = 0;
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const uint32_t c[4] = {D.w[u].x, D.w[u].y, D.w[u].z, D.w[u].w};
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                raw = sdot4(c[m] & 0x03030303u, act[16 * u + m], raw);
-                raw = sdot4((c[m] >> 2) & 0x03030303u, act[16 * u + 4 + m], raw);
-                raw = sdot4((c[m] >> 4) & 0x03030303u, act[16 * u + 8 + m], raw);
-                raw = sdot4((c[m] >> 6) & 0x03030303u, act[16 * u + 12 + m], raw);
-            }
-        }
+        const int raw = code_dot<2>(D.w, act);
         const int *s32 = x.sum32 + g * 8 + 4 * h;
         return 2 * raw - 3 * ((s32[0] + s32[1]) + (s32[2] + s32[3]));
     }
@@ -191,18 +191,7 @@ struct GroupQ2C {
     {
         Data D = Din;
         D.hold_all();
-        int raw = 0;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint32_t c[4] = {D.w[u].x, D.w[u].y, D.w[u].z, D.w[u].w};
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                raw = sdot4(c[m] & 0x03030303u, act[16 * u + m], raw);
-                raw = sdot4((c[m] >> 2) & 0x03030303u, act[16 * u + 4 + m], raw);
-                raw = sdot4((c[m] >> 4) & 0x03030303u, act[16 * u + 8 + m], raw);
-                raw = sdot4((c[m] >> 6) & 0x03030303u, act[16 * u + 12 + m], raw);
-            }
-        }
+        const int raw = code_dot<4>(D.w, act);
         return fmaf(h2f(D.d) * x.scale(), (float)(2 * raw - 3 * x.sum256()), acc);
     }
 };
