@@ -676,10 +676,12 @@ template <int F> int launch_gemv_format(int mode, const GemvArgs &a, void *strea
     // 16 lanes per row (four rows per wave), on the same terms, for 16-31
     // groups per row on fewer than 4096 rows, where 8-lane row-sets give
     // under two workgroups per CU and three or four groups per lane; at any
-    // row count for Q6_K, whose dot is the heaviest per byte ([32000 x 4096]
-    // 25.0 -> 20.0 us; Q4_K [6144 x 4096] measured 3 % slower so)
+    // row count for Q6_K and STQ1_0, whose dots are the heaviest per byte
+    // ([32000 x 4096] Q6_K 25.0 -> 20.0 us, [28672 x 4096] STQ1_0 9.17 ->
+    // 9.04 us; Q4_K [6144 x 4096] measured 3 % slower so)
     const bool w16 = mode == GEMV_PLAIN && nr == 1 && ks == 1 && a.norm == nullptr &&
-                     a.groups >= 16 && a.groups < 32 && (rows < 4096 || F == Q6_K);
+                     a.groups >= 16 && a.groups < 32 &&
+                     (rows < 4096 || F == Q6_K || F == STQ1_0);
     // 64 lanes per row (one group each, one row per wave, 4-wave workgroups)
     // for the long rows of the two formats with the heaviest dots: the 7B
     // down [4096 x 14336] Q6_K 13.9 -> 11.9 us, STQ1_0 6.5 -> 6.4 us (Q4_K
