@@ -1,8 +1,8 @@
 /*
  * CPU oracle for the quantized matrix-product path of hy-mt-rs.
  *
- * TEST INFRASTRUCTURE ONLY: the checker for tests/, __graft_entry__.smoke()
- * and bench.py's cpu_baseline leg. Nothing in the product library links it.
+ * TEST INFRASTRUCTURE ONLY: the reference results for tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg. Nothing in the product library links it.
  * The pinning of each function is listed in hyq_oracle.h.
  *
  * Build: oracle/Makefile (gcc, -ffp-contract=off so that a*b+c stays two

@@ -1,7 +1,7 @@
 /*
  * CPU oracle for the quantized matrix-product path of hy-mt-rs.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker: it is loaded by
+ * TEST INFRASTRUCTURE ONLY. This library gives the reference results: it is loaded by
  * tests/, by __graft_entry__.smoke() and by bench.py's cpu_baseline leg, never
  * by the product library (hy-mt-rs_amd/libhyq.so), which has no CPU fallback.
  *

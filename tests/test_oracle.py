@@ -1,5 +1,5 @@
 """CPU tests: pin the oracle against the reference's golden vectors, closed
-forms and invariants before it is trusted as the checker of the GPU path."""
+forms and invariants before the GPU path is compared with it."""
 import json
 import math
 import os
