@@ -1,9 +1,10 @@
 /*
  * CPU oracle for the quantized matrix-product path of hy-mt-rs.
  *
- * TEST INFRASTRUCTURE ONLY. This library gives the reference results: it is loaded by
- * tests/, by __graft_entry__.smoke() and by bench.py's cpu_baseline leg, never
- * by the product library (hy-mt-rs_amd/libhyq.so), which has no CPU fallback.
+ * TEST INFRASTRUCTURE ONLY. This library gives the reference results: it is
+ * loaded by tests/, by __graft_entry__.smoke() and by bench.py's cpu_baseline
+ * leg, never by the product library (hy-mt-rs_amd/libhyq.so), which has no
+ * CPU fallback.
  *
  * Every function restates an algorithm of the reference (Rust, not buildable
  * here: no cargo/rustc, git dependency on candle-core, and src/quant.rs:1460
