@@ -36,6 +36,8 @@ SIGNATURES = {
     "hyq_ctx_destroy": (None, [P]),
     "hyq_ctx_stream": (P, [P]),
     "hyq_sync": (I, [P]),
+    "hyq_ctx_set_q8_trace": (I, [P, P, SZ]),
+    "hyq_ctx_q8_trace_records": (I, [P, P, SZ, P, P]),
     "hyq_device_alloc": (I, [P, SZ, ctypes.POINTER(P)]),
     "hyq_device_free": (I, [P, P]),
     "hyq_memcpy_h2d": (I, [P, P, P, SZ]),
@@ -189,6 +191,7 @@ class Context:
         self.device = device
         # objects that use the context's stream (decoders): closed first
         self._dependents = weakref.WeakSet()
+        self._q8trace = None
 
     @property
     def stream(self) -> int:
@@ -232,6 +235,44 @@ class Context:
 
     def q8(self, n: int) -> "Q8":
         return Q8(self, n)
+
+    def set_q8_trace(self, nbytes: int | None) -> None:
+        """Record the int8 codes and scales the decode path's launches form
+        (hyq_ctx_set_q8_trace) into a device buffer of `nbytes`; None stops
+        recording. Each call starts an empty record list."""
+        if not nbytes:
+            check(lib().hyq_ctx_set_q8_trace(self.handle, None, 0))
+            self._q8trace = None
+            return
+        self._q8trace = self.empty(nbytes, np.uint8)
+        check(lib().hyq_ctx_set_q8_trace(self.handle, self._q8trace.ptr, nbytes))
+
+    def clear_q8_trace(self) -> None:
+        """Empty the record list, keeping the buffer."""
+        check(lib().hyq_ctx_set_q8_trace(self.handle, self._q8trace.ptr, self._q8trace.nbytes))
+
+    def q8_trace(self) -> list:
+        """(codes int8 [n], scales f32 [n / 256], values f32 [n]) of every
+        record since the list was emptied, in launch order: the codes and
+        scales a launch formed and the f32 values it quantized."""
+        count, dropped = ctypes.c_size_t(), ctypes.c_size_t()
+        check(lib().hyq_ctx_q8_trace_records(self.handle, None, 0, ctypes.byref(count),
+                                             ctypes.byref(dropped)))
+        if dropped.value:
+            raise RuntimeError(f"q8 trace: {dropped.value} records did not fit")
+        pairs = (ctypes.c_size_t * (2 * count.value + 2))()
+        check(lib().hyq_ctx_q8_trace_records(self.handle, pairs, count.value,
+                                             ctypes.byref(count), None))
+        self.sync()
+        raw = self._q8trace.numpy()
+        out = []
+        for i in range(count.value):
+            o, n = pairs[2 * i], pairs[2 * i + 1]
+            xo = o + (n + n // 64 + 255) // 256 * 256
+            out.append((raw[o:o + n].view(np.int8).copy(),
+                        raw[o + n:o + n + n // 64].view(np.float32).copy(),
+                        raw[xo:xo + 4 * n].view(np.float32).copy()))
+        return out
 
 
 class DeviceArray:

@@ -6,6 +6,8 @@
 
 #include <memory>
 #include <string>
+#include <utility>
+#include <vector>
 
 #include "../../include/hyq.h"
 #include "hyq_internal.hpp"
@@ -116,6 +118,25 @@ struct Q8Ref {
     }
 };
 
+// The Q8 record of a context (hyq_ctx_set_q8_trace, a test hook): each
+// traced launch takes the next record of n values (a multiple of 256):
+// n int8 codes, n / 256 f32 scales, then (from the next 256-byte boundary)
+// the n f32 values that were quantized; every record starts on a 256-byte
+// boundary. Records that do not fit are counted and dropped.
+struct Q8Trace {
+    uint8_t *base = nullptr;
+    size_t bytes = 0, used = 0, dropped = 0;
+    std::vector<std::pair<size_t, size_t>> records; // (offset, n)
+    // the next record of n values, or false
+    bool take(size_t n, int8_t **codes, float **scales, float **values);
+};
+// Gives a launch with an f32 input stage its record (when t is set): the
+// launch's groups over all of its K slices or slots.
+void q8_trace_gemv(Q8Trace *t, GemvArgs &a);
+// Records the first n values of a Q8 row already in device memory and the
+// f32 row x it was quantized from (copies on st; t may be null).
+int q8_trace_copy(Q8Trace *t, const Q8Ref &q, const float *x, size_t n, hipStream_t st);
+
 int q8_alloc(int device, size_t n, hyq_q8 **out);
 // Hands a weight to a dense decoder, which releases it when destroyed (the
 // weights a GGUF loader uploads for it).
@@ -134,6 +155,9 @@ struct hyq_ctx {
     hipStream_t stream = nullptr;
     hyq::Scratch x, y, bytes, xh, moe, kpart; // kpart: K-slice partials of batched products
     hyq_q8 *q8 = nullptr; // grown on demand for host-pointer calls
+    hyq::Q8Trace q8trace;  // hyq_ctx_set_q8_trace
+    // the record the traced launches use (null while the trace is off)
+    hyq::Q8Trace *q8t() { return q8trace.base ? &q8trace : nullptr; }
 };
 
 struct hyq_weight {

@@ -138,6 +138,44 @@ int q8_alloc(int device, size_t n, hyq_q8 **out)
     return HYQ_OK;
 }
 
+bool Q8Trace::take(size_t n, int8_t **codes, float **scales, float **values)
+{
+    const size_t xoff = align_up(n + n / 64, 256);
+    const size_t need = xoff + align_up(4 * n, 256);
+    if (!base || n % 256 || used + need > bytes) {
+        if (base) ++dropped;
+        return false;
+    }
+    *codes = (int8_t *)(base + used);
+    *scales = (float *)(base + used + n);
+    *values = (float *)(base + used + xoff);
+    records.emplace_back(used, n);
+    used += need;
+    return true;
+}
+
+void q8_trace_gemv(Q8Trace *t, GemvArgs &a)
+{
+    if (!t || !a.xin) return;
+    const size_t parts = a.nslots > 0 ? (size_t)a.nslots : a.kslices > 1 ? (size_t)a.kslices : 1;
+    if (!t->take((size_t)a.groups * 256 * parts, &a.q8t_codes, &a.q8t_scales, &a.q8t_x)) {
+        a.q8t_codes = nullptr;
+        a.q8t_scales = nullptr;
+        a.q8t_x = nullptr;
+    }
+}
+
+int q8_trace_copy(Q8Trace *t, const Q8Ref &q, const float *x, size_t n, hipStream_t st)
+{
+    int8_t *codes;
+    float *scales, *values;
+    if (!t || !t->take(n, &codes, &scales, &values)) return HYQ_OK;
+    HYQ_HIP(hipMemcpyAsync(codes, q.q, n, hipMemcpyDeviceToDevice, st), "q8 trace");
+    HYQ_HIP(hipMemcpyAsync(scales, q.s, n / 256 * 4, hipMemcpyDeviceToDevice, st), "q8 trace");
+    HYQ_HIP(hipMemcpyAsync(values, x, n * 4, hipMemcpyDeviceToDevice, st), "q8 trace");
+    return HYQ_OK;
+}
+
 } // namespace hyq
 
 namespace {
@@ -509,6 +547,34 @@ void hyq_ctx_destroy(hyq_ctx *ctx)
 }
 
 void *hyq_ctx_stream(hyq_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+int hyq_ctx_set_q8_trace(hyq_ctx *ctx, void *trace_d, size_t bytes)
+{
+    if (!ctx) return fail(HYQ_EINVAL, "ctx_set_q8_trace: null context");
+    if (trace_d && (uintptr_t)trace_d % 256)
+        return fail(HYQ_EINVAL, "ctx_set_q8_trace: buffer must be 256-byte aligned");
+    ctx->q8trace = Q8Trace{};
+    if (trace_d) {
+        ctx->q8trace.base = (uint8_t *)trace_d;
+        ctx->q8trace.bytes = bytes;
+    }
+    return HYQ_OK;
+}
+
+int hyq_ctx_q8_trace_records(hyq_ctx *ctx, size_t *pairs, size_t max_records, size_t *count,
+                             size_t *dropped)
+{
+    if (!ctx || !count) return fail(HYQ_EINVAL, "ctx_q8_trace_records: null argument");
+    const Q8Trace &t = ctx->q8trace;
+    *count = t.records.size();
+    if (dropped) *dropped = t.dropped;
+    if (pairs)
+        for (size_t i = 0; i < t.records.size() && i < max_records; ++i) {
+            pairs[2 * i] = t.records[i].first;
+            pairs[2 * i + 1] = t.records[i].second;
+        }
+    return HYQ_OK;
+}
 
 int hyq_sync(hyq_ctx *ctx)
 {

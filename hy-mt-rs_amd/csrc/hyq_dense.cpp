@@ -350,13 +350,22 @@ GemvArgs staged(const hyq_weight *w, const float *xin, const float *norm, float 
 // last down projection's nparts partial rows) normalised and quantized to Q8
 // once, then the Q8-input GEMV (one row per lane, no input stage repeated by
 // each of its workgroups).
-int lm_head(hyq_dense *m, const float *x, const float *parts, int nparts, hipStream_t st)
+int lm_head(hyq_dense *m, const float *x, const float *parts, int nparts, hipStream_t st,
+            Q8Trace *q8t)
 {
     const hyq_dense_config &c = m->cfg;
     const Q8Ref &q = m->out_q8;
-    HYQ_LAUNCH(launch_rms_norm_q8(x, m->output_norm, c.hidden, c.rms_eps, nullptr, q.q, q.s,
-                                  q.sum16, q.sum32, q.sum256, st, parts, nparts, c.hidden),
+    // (traced: the normalized row goes straight into the record)
+    int8_t *tq = nullptr;
+    float *ts = nullptr, *tx = nullptr;
+    const bool tr = q8t && q8t->take((size_t)c.hidden, &tq, &ts, &tx);
+    HYQ_LAUNCH(launch_rms_norm_q8(x, m->output_norm, c.hidden, c.rms_eps, tr ? tx : nullptr, q.q,
+                                  q.s, q.sum16, q.sum32, q.sum256, st, parts, nparts, c.hidden),
                "output_norm_q8");
+    if (tr) {
+        HYQ_HIP(hipMemcpyAsync(tq, q.q, c.hidden, hipMemcpyDeviceToDevice, st), "q8 trace");
+        HYQ_HIP(hipMemcpyAsync(ts, q.s, c.hidden / 64, hipMemcpyDeviceToDevice, st), "q8 trace");
+    }
     HYQ_LAUNCH(launch_gemv(m->output->dtype, GEMV_PLAIN, gemv_args(m->output, q, m->logits, nullptr),
                            st),
                "gemv_lm_head");
@@ -378,6 +387,8 @@ int enqueue_step(hyq_dense *m, bool trace = false, bool embed = true)
     const int *pos = &m->state->pos;
     const int ks = m->down_ks;
     const bool norm_first = m->arch == HYQ_ARCH_HYV3;
+    // the context's Q8 record (eager steps only: a captured graph keeps none)
+    Q8Trace *q8t = trace ? m->ctx->q8t() : nullptr;
     trace = trace && m->trace;
     if (trace)
         HYQ_LAUNCH(launch_sum_parts(m->hidden, nullptr, 0, 0, c.hidden, m->trace, st), "trace");
@@ -402,6 +413,7 @@ int enqueue_step(hyq_dense *m, bool trace = false, bool embed = true)
             }
             a.nseg = 3;
             a.rows_total = start;
+            q8_trace_gemv(q8t, a);
             HYQ_LAUNCH(launch_gemv(L.q->dtype, GEMV_MULTI, a, st), "gemv_qkv");
         }
         HYQ_LAUNCH(launch_attention_rope(m->qb, m->kb, m->vb, L.q_norm, L.k_norm, m->freq,
@@ -417,6 +429,7 @@ int enqueue_step(hyq_dense *m, bool trace = false, bool embed = true)
             a.rparts = m->parts;
             a.nrparts = np;
             a.parts_stride = c.hidden;
+            q8_trace_gemv(q8t, a);
             HYQ_LAUNCH(launch_gemv(L.o->dtype, GEMV_PLAIN, a, st), "gemv_attn_output");
         }
         if (L.moe) {
@@ -426,8 +439,9 @@ int enqueue_step(hyq_dense *m, bool trace = false, bool embed = true)
             HYQ_LAUNCH(launch_rms_norm_q8(m->hidden, L.ffn_norm, c.hidden, c.rms_eps, m->moe_xn,
                                           q.q, q.s, q.sum16, q.sum32, q.sum256, st),
                        "rms_norm_q8");
+            if (int rc = q8_trace_copy(q8t, q, m->moe_xn, (size_t)c.hidden, st)) return rc;
             int rc = moe_ffn_row(st, *L.moe, m->moe_xn, q, m->moe_row, m->hidden, m->hidden,
-                                 trace ? m->trace + (size_t)(l + 1) * c.hidden : nullptr);
+                                 trace ? m->trace + (size_t)(l + 1) * c.hidden : nullptr, q8t);
             if (rc) return rc;
             np = 0;
             continue;
@@ -436,17 +450,19 @@ int enqueue_step(hyq_dense *m, bool trace = false, bool embed = true)
             GemvArgs a = staged(L.gate, m->hidden, L.ffn_norm, c.rms_eps, m->gb, nullptr);
             a.nseg = 2;
             a.seg[1].w = L.up->view;
+            q8_trace_gemv(q8t, a);
             HYQ_LAUNCH(launch_gemv(L.gate->dtype, GEMV_SILU, a, st), "gemv_gate_up_silu");
         }
         if (ks > 1) {
             GemvArgs a = staged(L.down, m->gb, nullptr, 0.f, m->parts, nullptr);
             a.groups /= ks;
             a.kslices = ks;
+            q8_trace_gemv(q8t, a);
             HYQ_LAUNCH(launch_gemv(L.down->dtype, GEMV_PLAIN, a, st), "gemv_down");
         } else {
-            HYQ_LAUNCH(launch_gemv(L.down->dtype, GEMV_PLAIN,
-                                   staged(L.down, m->gb, nullptr, 0.f, m->hidden, m->hidden), st),
-                       "gemv_down");
+            GemvArgs a = staged(L.down, m->gb, nullptr, 0.f, m->hidden, m->hidden);
+            q8_trace_gemv(q8t, a);
+            HYQ_LAUNCH(launch_gemv(L.down->dtype, GEMV_PLAIN, a, st), "gemv_down");
         }
         np = ks > 1 ? ks : 0;
         if (trace)
@@ -454,7 +470,7 @@ int enqueue_step(hyq_dense *m, bool trace = false, bool embed = true)
                                         m->trace + (size_t)(l + 1) * c.hidden, st),
                        "trace");
     }
-    if (int rc = lm_head(m, m->hidden, m->parts, np, st)) return rc;
+    if (int rc = lm_head(m, m->hidden, m->parts, np, st, q8t)) return rc;
     HYQ_LAUNCH(launch_argmax_embed(m->logits, c.vocab, m->argmax_scratch,
                                    (int *)(m->argmax_scratch + 64), m->token, m->state, m->history,
                                    m->embedding->dtype, m->embedding->view, c.hidden, m->hidden,
@@ -616,7 +632,8 @@ int enqueue_prefill_chunk(hyq_dense *m, int n)
                                    hipMemcpyDeviceToDevice, st),
                     "trace");
     }
-    if (int rc = lm_head(m, m->pf_hid + (size_t)(n - 1) * H, nullptr, 0, st)) return rc;
+    if (int rc = lm_head(m, m->pf_hid + (size_t)(n - 1) * H, nullptr, 0, st, m->ctx->q8t()))
+        return rc;
     HYQ_LAUNCH(launch_argmax(m->logits, c.vocab, m->argmax_scratch,
                              (int *)(m->argmax_scratch + 64), m->token, m->state, nullptr, st),
                "argmax");

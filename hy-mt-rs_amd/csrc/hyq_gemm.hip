@@ -35,8 +35,9 @@ __device__ __forceinline__ int xcd_tile(int total)
 }
 
 // One workgroup per row: xh[r][k] = f16(v[k] * 2^-e) and rscale[r] = 2^e,
-// where v = x[src] (or, with `norm`, its RMSNorm v[k] = x[k] * s * norm[k],
-// s = 1 / sqrt(mean(x^2) + eps), the order of src/model.rs:832-870) and
+// where v = x[src] (or, with `norm`, its RMSNorm v[k] = x[k] * (norm[k] * s)
+// over whole 16-value steps and x[k] * s * norm[k] over a tail, s = 1 /
+// sqrt(mean(x^2) + eps), the aarch64 arm of src/model.rs:832-870) and
 // e = ceil(log2(max_k |v[k]|)) - 14 puts the row's largest magnitude at or
 // below 2^14, so no value overflows f16 or drops into its subnormals; the
 // power-of-two scale is exact and the GEMM epilogues multiply it back.
@@ -77,7 +78,11 @@ __global__ __launch_bounds__(256) void rows_to_f16_kernel(const float *__restric
         float4 v = x4[i];
         if (norm) {
             const float4 w = n4p[i];
-            v = make_float4(v.x * s * w.x, v.y * s * w.y, v.z * s * w.z, v.w * s * w.w);
+            if (4 * i < (K & ~15))
+                v = make_float4(v.x * (w.x * s), v.y * (w.y * s), v.z * (w.z * s),
+                                v.w * (w.w * s));
+            else
+                v = make_float4(v.x * s * w.x, v.y * s * w.y, v.z * s * w.z, v.w * s * w.w);
         }
         return v;
     };

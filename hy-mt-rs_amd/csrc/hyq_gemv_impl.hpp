@@ -49,7 +49,7 @@ __device__ __forceinline__ float sum32(float v)
 // sums are reduced over a 16-lane row by DPP and across the half wave's two
 // rows by v_permlane16_swap, with no readlane or LDS round trip, and the
 // divisions are branch-free. With a norm vector the values are
-// rms_norm_into's x * (1/sqrt(mean(x^2) + eps)) * w (src/model.rs:825-829);
+// rms_norm_into's x * (w * (1/sqrt(mean(x^2) + eps))) (src/model.rs:785-815);
 // the sum of squares is formed per group by a fixed tree and then over the
 // groups in ascending order. Rows of up to 8 * STAGE_PASSES groups are loaded
 // with all loads in flight at once (before the weights'); longer rows take a
@@ -69,7 +69,6 @@ __device__ __forceinline__ float4 add4(float4 v, float4 p)
 
 __device__ __forceinline__ float sum_rows(float v) { return wave::sum_rows2(v); }
 __device__ __forceinline__ int sum_rows(int v) { return wave::sum_rows2(v); }
-__device__ __forceinline__ float max_rows(float v) { return wave::max_rows2(v); }
 
 __device__ __forceinline__ float sq8(const float4 &a, const float4 &b)
 {
@@ -77,10 +76,12 @@ __device__ __forceinline__ float sq8(const float4 &a, const float4 &b)
            ((b.x * b.x + b.y * b.y) + (b.z * b.z + b.w * b.w));
 }
 
+// rms_norm_into's aarch64 arm over whole 16-value steps (src/model.rs:809):
+// x * (w * scale)
 __device__ __forceinline__ float4 scale_by(float4 v, float scale, float4 w)
 {
-    return make_float4(v.x * scale * w.x, v.y * scale * w.y, v.z * scale * w.z,
-                       v.w * scale * w.w);
+    return make_float4(v.x * (w.x * scale), v.y * (w.y * scale), v.z * (w.z * scale),
+                       v.w * (w.w * scale));
 }
 
 __device__ __forceinline__ uint32_t pack4(int q0, int q1, int q2, int q3)
@@ -89,13 +90,22 @@ __device__ __forceinline__ uint32_t pack4(int q0, int q1, int q2, int q3)
            ((uint32_t)(q3 & 0xff) << 24);
 }
 
-// Group g's 8 values of this lane (c = lane of the half wave).
+// Group g's 8 values of this lane (c = lane of the half wave); xt (the
+// trace hook, workgroup 0 only) receives the values.
 __device__ __forceinline__ void quantize_half(float4 a, float4 b, int g, int c, int *slots,
-                                              float *sc, int *s256, int *s16, int *s32)
+                                              float *sc, int *s256, int *s16, int *s32,
+                                              float *xt)
 {
-    const float la = fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w)));
-    const float lb = fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)));
-    const float m = max_rows(wave::max16(fmaxf(la, lb)));
+    if (xt) {
+        reinterpret_cast<float4 *>(xt + g * 256 + 8 * c)[0] = a;
+        reinterpret_cast<float4 *>(xt + g * 256 + 8 * c)[1] = b;
+    }
+    // the group maximum propagates NaN (max_abs_neon's FMAX): a NaN in the
+    // group gives scale 0 and zero codes
+    using wave::nmax;
+    const float la = nmax(nmax(fabsf(a.x), fabsf(a.y)), nmax(fabsf(a.z), fabsf(a.w)));
+    const float lb = nmax(nmax(fabsf(b.x), fabsf(b.y)), nmax(fabsf(b.z), fabsf(b.w)));
+    const float m = wave::nmax_rows2(wave::nmax16(nmax(la, lb)));
     const bool pos = m > 0.f;
     const float md = pos ? m : 1.f;
     const float s = pos ? md / 127.f : 0.f;
@@ -164,7 +174,8 @@ __device__ __forceinline__ void stage_load(const GemvArgs &a, const float *xin, 
 
 template <int IN>
 __device__ __forceinline__ void stage_regs(const GemvArgs &a, StageRegs &r, int *slots,
-                                           float *sc, int *s256, int *s16, int *s32, float *gss)
+                                           float *sc, int *s256, int *s16, int *s32, float *gss,
+                                           float *xt)
 {
     const int hw = threadIdx.x >> 5, c = threadIdx.x & 31;
     const int groups = a.groups;
@@ -195,9 +206,9 @@ __device__ __forceinline__ void stage_regs(const GemvArgs &a, StageRegs &r, int 
             if (IN == 2)
                 quantize_half(scale_by(r.x[p][0], scale, r.w[p][0]),
                               scale_by(r.x[p][1], scale, r.w[p][1]), g, c, slots, sc, s256, s16,
-                              s32);
+                              s32, xt);
             else
-                quantize_half(r.x[p][0], r.x[p][1], g, c, slots, sc, s256, s16, s32);
+                quantize_half(r.x[p][0], r.x[p][1], g, c, slots, sc, s256, s16, s32, xt);
         }
     }
 }
@@ -206,7 +217,7 @@ __device__ __forceinline__ void stage_regs(const GemvArgs &a, StageRegs &r, int 
 template <int IN>
 __device__ __forceinline__ void stage_loop(const GemvArgs &a, const float *xin, const float *norm,
                                            int *slots, float *sc, int *s256, int *s16, int *s32,
-                                           float *gss)
+                                           float *gss, float *xt)
 {
     const int hw = threadIdx.x >> 5, c = threadIdx.x & 31;
     const int groups = a.groups;
@@ -239,7 +250,7 @@ __device__ __forceinline__ void stage_loop(const GemvArgs &a, const float *xin, 
             va = scale_by(va, scale, n4[g * 64 + 2 * c]);
             vb = scale_by(vb, scale, n4[g * 64 + 2 * c + 1]);
         }
-        quantize_half(va, vb, g, c, slots, sc, s256, s16, s32);
+        quantize_half(va, vb, g, c, slots, sc, s256, s16, s32, xt);
     }
 }
 
@@ -438,10 +449,25 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
         }
     } else {
         float *gss = reinterpret_cast<float *>(s32 + groups * 8);
-        if (stage_reg) stage_regs<IN>(a, sr, lds, sc, s256, s16, s32, gss);
-        else stage_loop<IN>(a, xin, a.norm, lds, sc, s256, s16, s32, gss);
+        // (test hook) workgroup 0 of the slice or slot records its values
+        float *xt = a.q8t_x && blockIdx.x == 0
+                        ? a.q8t_x + (size_t)(SLOT ? (int)blockIdx.y * groups : gbase) * 256
+                        : nullptr;
+        if (stage_reg) stage_regs<IN>(a, sr, lds, sc, s256, s16, s32, gss, xt);
+        else stage_loop<IN>(a, xin, a.norm, lds, sc, s256, s16, s32, gss, xt);
     }
     __syncthreads();
+    if constexpr (IN != 0) {
+        // (test hook) the codes and scales this stage formed, as they sit in
+        // LDS, from workgroup 0 of the slice or slot
+        if (a.q8t_codes && blockIdx.x == 0) {
+            const int gb = SLOT ? (int)blockIdx.y * groups : gbase;
+            int *codes = reinterpret_cast<int *>(a.q8t_codes) + (size_t)gb * 64;
+            for (int i = threadIdx.x; i < groups * 64; i += blockDim.x)
+                codes[i] = lds[(i >> 6) * SLOT_INTS + (i & 63)];
+            for (int g = threadIdx.x; g < groups; g += blockDim.x) a.q8t_scales[gb + g] = sc[g];
+        }
+    }
 
     float acc[NR];
     float acc2[NR];

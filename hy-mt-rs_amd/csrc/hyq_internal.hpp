@@ -145,6 +145,15 @@ struct GemvArgs {
     int slot_rows;
     int nslots;
     int slot_xin_stride;
+    // A test hook (the parity tests' record of the int8 codes): with an f32
+    // input stage and q8t_codes set, workgroup 0 of each K slice (or slot)
+    // writes the f32 values its stage quantized (after the norm), the codes
+    // and the scales to q8t_x + 256 * g, q8t_codes + 256 * g and
+    // q8t_scales + g for the slice's (slot's) groups g, counted over the
+    // launch's K range (slot s: from s * groups).
+    int8_t *q8t_codes;
+    float *q8t_scales;
+    float *q8t_x;
 };
 constexpr int GEMV_MAX_PARTS = 4;
 

@@ -96,7 +96,8 @@ MoeRowBuf moe_row_carve(const MoeFfn &f, uint8_t *base)
 }
 
 int moe_ffn_row(hipStream_t st, const MoeFfn &f, const float *xn, const Q8Ref &xq,
-                const MoeRowBuf &b, const float *residual, float *out, float *trace)
+                const MoeRowBuf &b, const float *residual, float *out, float *trace,
+                Q8Trace *q8t)
 {
     const int H = f.hidden;
     // router logits (F32 decoded rows, src/model.rs:691) and route (:694)
@@ -139,6 +140,7 @@ int moe_ffn_row(hipStream_t st, const MoeFfn &f, const float *xn, const Q8Ref &x
         a.rows_total = H;
         a.groups = f.smid / 256;
         a.xin = b.hs;
+        q8_trace_gemv(q8t, a);
         HYQ_LAUNCH(launch_gemv(f.sdown->dtype, GEMV_PLAIN, a, st), "moe_shared_down");
     }
     {
@@ -153,6 +155,7 @@ int moe_ffn_row(hipStream_t st, const MoeFfn &f, const float *xn, const Q8Ref &x
         a.slot_experts = f.experts;
         a.nslots = f.used;
         a.slot_xin_stride = f.mid;
+        q8_trace_gemv(q8t, a);
         HYQ_LAUNCH(launch_gemv(f.down->dtype, GEMV_PLAIN, a, st), "moe_experts_down");
     }
     HYQ_LAUNCH(launch_ffn_combine(residual, b.ps, b.pe, b.sw, f.used, H, 1, out, trace, st),
@@ -354,8 +357,9 @@ int hyq_moe_forward_d(hyq_ctx *ctx, const hyq_moe_config *mc, const hyq_weight *
         HYQ_LAUNCH(launch_quantize_q8(x_d, f.hidden, q.q, q.s, q.sum16, q.sum32, q.sum256,
                                       ctx->stream),
                    "quantize_q8");
+        if ((rc = q8_trace_copy(ctx->q8t(), q, x_d, (size_t)f.hidden, ctx->stream))) return rc;
         return moe_ffn_row(ctx->stream, f, x_d, q, moe_row_carve(f, base + off), nullptr, out_d,
-                           nullptr);
+                           nullptr, ctx->q8t());
     }
     return moe_ffn_rows(ctx->stream, f, x_d, (int)tokens, moe_rows_carve(f, (int)tokens, base),
                         nullptr, out_d);

@@ -46,9 +46,11 @@ size_t moe_row_bytes(const MoeFfn &f);
 MoeRowBuf moe_row_carve(const MoeFfn &f, uint8_t *base);
 // out = residual + Moe::forward(xn) (out alone when residual is null) for
 // one normalized row xn (f32, 16-byte aligned) and its Q8 xq; trace, when
-// set, gets a copy of out.
+// set, gets a copy of out; q8t, when set, records the down projections'
+// input stages (the shared expert's, then the slots').
 int moe_ffn_row(hipStream_t st, const MoeFfn &f, const float *xn, const Q8Ref &xq,
-                const MoeRowBuf &b, const float *residual, float *out, float *trace);
+                const MoeRowBuf &b, const float *residual, float *out, float *trace,
+                Q8Trace *q8t = nullptr);
 
 // n-row temporaries: logits [n][E], pairs [n * used], f16 rows with scales,
 // the shared SiLU rows [n][smid], the FFN output [n][H], the grouped expert

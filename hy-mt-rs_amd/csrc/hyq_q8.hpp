@@ -3,12 +3,16 @@
 // :965-991): one 256-value group per 256-thread workgroup, one value per
 // thread.
 //
-// scale = max/127 and inverse = 127/max (IEEE divisions, or 0/0 for an
-// all-zero group); q = saturate_i8(round_half_even(x * inverse)) over whole
-// 16-value steps and clamp(round_half_away(x * inverse), -127, 127) over a
-// group's tail, as the NEON body and its scalar tail do. It also writes the
-// integer sums of q over 16-, 32- and 256-value spans that the GEMV kernels
-// use to fold code offsets (exact integers, so their order is free).
+// max = max|x| over the group's whole 16-value steps by FMAX (a NaN there
+// makes it NaN), then folded with the tail's |x| by f32::max (a NaN operand
+// yields the other one); scale = max/127 and inverse = 127/max (IEEE
+// divisions), or 0/0 unless max > 0 (an all-zero group, or a NaN maximum:
+// every code of such a group is 0); q = saturate_i8(round_half_even(x *
+// inverse)) over whole 16-value steps and clamp(round_half_away(x *
+// inverse), -127, 127) over a group's tail, as the NEON body and its scalar
+// tail do. It also writes the integer sums of q over 16-, 32- and 256-value
+// spans that the GEMV kernels use to fold code offsets (exact integers, so
+// their order is free).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -42,21 +46,27 @@ __device__ __forceinline__ void q8_quantize_group(float v, int g, int len, int8_
                                                   int32_t *__restrict__ sum32,
                                                   int32_t *__restrict__ sum256)
 {
-    __shared__ float wmax[4];
+    __shared__ float wmax[4], wtail[4];
     __shared__ int wsum[4];
     const int t = threadIdx.x;
     const int base = g * 256;
-    float m = wave::max64(fabsf(v));
-    if ((t & 63) == 0) wmax[t >> 6] = m;
+    const int vec = len / 16 * 16;
+    // the body's maximum propagates NaN, the tail's ignores it
+    const float mb = wave::nmax64(t < vec ? fabsf(v) : 0.f);
+    const float mt = wave::max64(t >= vec && t < len ? fabsf(v) : 0.f);
+    if ((t & 63) == 0) {
+        wmax[t >> 6] = mb;
+        wtail[t >> 6] = mt;
+    }
     __syncthreads();
-    m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const float m = fmaxf(wave::nmax(wave::nmax(wmax[0], wmax[1]), wave::nmax(wmax[2], wmax[3])),
+                          fmaxf(fmaxf(wtail[0], wtail[1]), fmaxf(wtail[2], wtail[3])));
 
     float scale = 0.f, inverse = 0.f;
     if (m > 0.f) {
         scale = m / 127.f;
         inverse = 127.f / m;
     }
-    const int vec = len / 16 * 16;
     int qi = 0;
     if (t < vec) qi = q8_sat_rne(v * inverse);
     else if (t < len) qi = q8_tail_round(v * inverse);

@@ -141,8 +141,9 @@ __global__ __launch_bounds__(256) void ffn_combine_kernel(const float *residual,
     if (trace) trace[row + i] = h;
 }
 
-// rms_norm_into of n rows (src/model.rs:785-830): y = x * (1/sqrt(mean(x^2)
-// + eps)) * w, one workgroup per row.
+// rms_norm_into of n rows (src/model.rs:785-830): y = x * (w * scale) over
+// whole 16-value steps and x * scale * w over a tail (the aarch64 arm), scale
+// = 1/sqrt(mean(x^2) + eps), one workgroup per row.
 __global__ __launch_bounds__(256) void rms_rows_kernel(const float *__restrict__ x,
                                                        const float *__restrict__ w, int H,
                                                        float eps, float *__restrict__ y)
@@ -158,7 +159,8 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(const float *__restrict__
     __syncthreads();
     ss = (part[0] + part[1]) + (part[2] + part[3]);
     const float scale = 1.0f / sqrtf(ss / (float)H + eps);
-    for (int i = t; i < H; i += 256) y[i] = x[i] * scale * w[i];
+    const int body = H & ~15;
+    for (int i = t; i < H; i += 256) y[i] = i < body ? x[i] * (w[i] * scale) : x[i] * scale * w[i];
 }
 
 } // namespace

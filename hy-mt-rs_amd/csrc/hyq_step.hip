@@ -44,8 +44,9 @@ __global__ __launch_bounds__(256) void embed_kernel(WView w, int cols, const int
 // ---- rms_norm_into fused with the Q8 quantizer ----
 // One workgroup per 256-value group; each recomputes sum(x^2) over the whole
 // row (n <= 64 Ki values, read from L2) so that no cross-workgroup sync is
-// needed. y = x * scale * w with scale = 1 / sqrt(mean(x^2) + eps), the x86
-// arm's operation order (src/model.rs:825-829).
+// needed. y = x * (w * scale) with scale = 1 / sqrt(mean(x^2) + eps) over
+// whole 16-value steps and x * scale * w over the tail, the aarch64 arm's
+// operation order (src/model.rs:791-822).
 // x is the row ((x + p_0) + p_1) + ... with nparts partial rows p_k at
 // parts + k * pstride (a K-split product's slices, added in the order the
 // GEMV input stage adds them).
@@ -110,7 +111,7 @@ __global__ __launch_bounds__(256) void rms_norm_q8_kernel(const float *__restric
     float v = 0.f;
     if (t < len) {
         const int i = g * 256 + t;
-        v = row1(i) * scale * w[i];
+        v = i < (n & ~15) ? row1(i) * (w[i] * scale) : row1(i) * scale * w[i];
         if (y) y[i] = v;
     }
     q8_quantize_group(v, g, len, q, s, s16, s32, s256);
@@ -166,18 +167,24 @@ __global__ void rope_norm_kv_kernel(float *__restrict__ q, const float *__restri
         for (int i = 0; i < (half + 63) / 64; ++i) ss += part[i];
         return 1.0f / sqrtf(ss / (float)dim + eps);
     };
+    // the aarch64 arm's x * (w * scale) over whole 16-value steps, x * scale
+    // * w over a tail (src/model.rs:837-865)
+    const int body = dim & ~15;
+    auto nrm = [&](float x, int i, float scale) {
+        return i < body ? x * (nw[i] * scale) : x * scale * nw[i];
+    };
     float o0, o1;
     if (norm_first) {
         const float scale = head_scale(a, c2);
-        const float n0 = a * scale * nw[j], n1 = c2 * scale * nw[j + half];
+        const float n0 = nrm(a, j, scale), n1 = nrm(c2, j + half, scale);
         o0 = n0 * cs - n1 * sn;
         o1 = n0 * sn + n1 * cs;
     } else {
         const float r0 = a * cs - c2 * sn;
         const float r1 = a * sn + c2 * cs;
         const float scale = head_scale(r0, r1);
-        o0 = r0 * scale * nw[j];
-        o1 = r1 * scale * nw[j + half];
+        o0 = nrm(r0, j, scale);
+        o1 = nrm(r1, j + half, scale);
     }
     if (is_q) {
         q[(size_t)h * dim + j] = o0;
@@ -221,9 +228,10 @@ __global__ void rope_norm_kv_kernel(float *__restrict__ q, const float *__restri
 // new key (RoPE + norm) and value, appends them to the caches
 // (KvCache::append, src/model.rs:650-669) and uses them from LDS.
 
-// RoPE (NeoX halves j, j+64) of one 128-wide head and its rms_norm, in the
-// dense order (RoPE first) or the hy_v3 one (norm first); lane j of a full
-// wave owns the pair.
+// RoPE (NeoX halves j, j+64) of one 128-wide head and its rms_norm (the
+// aarch64 arm's x * (w * scale), src/model.rs:837-865), in the dense order
+// (RoPE first) or the hy_v3 one (norm first); lane j of a full wave owns the
+// pair.
 __device__ __forceinline__ void rope_norm_pair(float a, float c2, float cs, float sn, float n0,
                                                float n1, float eps, bool norm_first, float &o0,
                                                float &o1)
@@ -231,7 +239,7 @@ __device__ __forceinline__ void rope_norm_pair(float a, float c2, float cs, floa
     if (norm_first) {
         const float ss = wave_sum(a * a + c2 * c2);
         const float scale = 1.0f / sqrtf(ss / (float)ATT_D + eps);
-        const float u0 = a * scale * n0, u1 = c2 * scale * n1;
+        const float u0 = a * (n0 * scale), u1 = c2 * (n1 * scale);
         o0 = u0 * cs - u1 * sn;
         o1 = u0 * sn + u1 * cs;
         return;
@@ -240,8 +248,8 @@ __device__ __forceinline__ void rope_norm_pair(float a, float c2, float cs, floa
     const float r1 = a * sn + c2 * cs;
     const float ss = wave_sum(r0 * r0 + r1 * r1);
     const float scale = 1.0f / sqrtf(ss / (float)ATT_D + eps);
-    o0 = r0 * scale * n0;
-    o1 = r1 * scale * n1;
+    o0 = r0 * (n0 * scale);
+    o1 = r1 * (n1 * scale);
 }
 
 constexpr int ATT_WAVES = 8;

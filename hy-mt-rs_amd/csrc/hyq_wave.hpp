@@ -58,6 +58,22 @@ __device__ __forceinline__ float max16(float v)
     return fmaxf(v, dpp<DPP_MIRROR>(v));
 }
 
+// NaN-propagating maxima (IEEE 754-2019 maximum, v_maximum3_f32): NaN when
+// any operand is NaN, as NEON's FMAX / FMAXV are, which form the Q8
+// quantizer's group maximum in the reference (src/quant.rs:869-892). fmaxf
+// (IEEE maxNum) returns the other operand instead.
+__device__ __forceinline__ float nmax(float a, float b)
+{
+    return __builtin_elementwise_maximum(a, b);
+}
+__device__ __forceinline__ float nmax16(float v)
+{
+    v = nmax(v, dpp<DPP_XOR1>(v));
+    v = nmax(v, dpp<DPP_XOR2>(v));
+    v = nmax(v, dpp<DPP_HALF_MIRROR>(v));
+    return nmax(v, dpp<DPP_MIRROR>(v));
+}
+
 template <class T> __device__ __forceinline__ T lane(T v, int l)
 {
     return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
@@ -78,6 +94,11 @@ __device__ __forceinline__ float max64(float v)
 {
     v = max16(v);
     return fmaxf(fmaxf(lane(v, 0), lane(v, 16)), fmaxf(lane(v, 32), lane(v, 48)));
+}
+__device__ __forceinline__ float nmax64(float v)
+{
+    v = nmax16(v);
+    return nmax(nmax(lane(v, 0), lane(v, 16)), nmax(lane(v, 32), lane(v, 48)));
 }
 
 // v_permlane16_swap / v_permlane32_swap of v with itself. swap16: `even`
@@ -119,6 +140,12 @@ __device__ __forceinline__ float max_rows2(float v)
     int e, o;
     swap16(__builtin_bit_cast(int, v), e, o);
     return fmaxf(__builtin_bit_cast(float, e), __builtin_bit_cast(float, o));
+}
+__device__ __forceinline__ float nmax_rows2(float v)
+{
+    int e, o;
+    swap16(__builtin_bit_cast(int, v), e, o);
+    return nmax(__builtin_bit_cast(float, e), __builtin_bit_cast(float, o));
 }
 __device__ __forceinline__ float sum_halves(float v)
 {

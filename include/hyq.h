@@ -70,6 +70,23 @@ void hyq_ctx_destroy(hyq_ctx *ctx);
 /* The context's hipStream_t, for callers that enqueue their own work. */
 void *hyq_ctx_stream(hyq_ctx *ctx);
 int hyq_sync(hyq_ctx *ctx);
+/* Q8 tracing (no counterpart in the reference: it exposes the int8 codes
+ * that Q8::quantize_into, src/quant.rs:904-922, forms inside the products).
+ * While trace_d (256-byte aligned device memory of `bytes` bytes) is set,
+ * every launch of the dense decoder's eager step (hyq_dense_forward) and of
+ * hyq_moe_forward_d at one token that quantizes an f32 row to Q8 - a GEMV
+ * input stage, the RMSNorm+Q8 and quantize kernels - also writes what it
+ * quantized and formed to trace_d, one record of n values after another:
+ * n int8 codes, n / 256 f32 scales and, from the next 256-byte boundary, the
+ * n f32 values quantized (after any RMSNorm); each record starts on a
+ * 256-byte boundary.
+ * Setting a buffer (or NULL, which switches tracing off) clears the list.
+ * hyq_ctx_q8_trace_records returns the number of records written since
+ * (*count), the number dropped for want of space (*dropped, may be NULL)
+ * and, for the first max_records of them, (byte offset, n) pairs. */
+int hyq_ctx_set_q8_trace(hyq_ctx *ctx, void *trace_d, size_t bytes);
+int hyq_ctx_q8_trace_records(hyq_ctx *ctx, size_t *pairs, size_t max_records, size_t *count,
+                             size_t *dropped);
 
 /* ---- device buffers for the _d entry points (no reference counterpart: the
  * reference is host-only; a host that drives the device-pointer calls needs

@@ -41,6 +41,7 @@ def lib() -> ctypes.CDLL:
 
 P = ctypes.c_void_p
 SZ = ctypes.c_size_t
+I = ctypes.c_int
 
 
 def _declare(L: ctypes.CDLL) -> None:
@@ -65,8 +66,8 @@ def _declare(L: ctypes.CDLL) -> None:
         "hyqo_route": (None, [P, P, SZ, SZ, ctypes.c_int, ctypes.c_float, P, P]),
         "hyqo_moe_experts": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, P, P, P, SZ, SZ, SZ,
                                             P, SZ, P, P, P, SZ, P, ctypes.c_int]),
-        "hyqo_rms_norm_into": (None, [P, P, SZ, ctypes.c_float, P]),
-        "hyqo_rms_norm_rows": (None, [P, P, SZ, SZ, ctypes.c_float]),
+        "hyqo_rms_norm_into": (None, [P, P, SZ, ctypes.c_float, P, I]),
+        "hyqo_rms_norm_rows": (None, [P, P, SZ, SZ, ctypes.c_float, I]),
         "hyqo_rope_tables": (None, [SZ, ctypes.c_float, SZ, P, P]),
         "hyqo_rope": (None, [P, SZ, SZ, P, P]),
         "hyqo_attention": (None, [P, P, P, SZ, SZ, SZ, SZ, P]),
@@ -81,6 +82,10 @@ def _declare(L: ctypes.CDLL) -> None:
         "hyqo_output_logits": (None, [P, P, ctypes.c_int, P, ctypes.c_int]),
         "hyqo_argmax": (ctypes.c_int, [P, SZ]),
         "hyqo_moe_forward": (None, [P, SZ, P, SZ, P, ctypes.c_int, ctypes.c_int]),
+        "hyqo_moe_forward_tap": (None, [P, SZ, P, P, ctypes.c_int, P]),
+        "hyqo_layer_step_tap": (ctypes.c_int, [P, ctypes.c_int, P, P, P, SZ, SZ, ctypes.c_int,
+                                               P]),
+        "hyqo_output_logits_tap": (None, [P, P, P, ctypes.c_int, P]),
         "hyqo_max_threads": (ctypes.c_int, []),
     }
     for name, (res, args) in sig.items():
@@ -251,6 +256,61 @@ class _Model(ctypes.Structure):
                 ("k_norm", P), ("arch", ctypes.c_int), ("moe", P)]
 
 
+# Q8 stages of the int8 path (oracle/hyq_oracle_step.h: hyqo_q8_tap)
+STAGE_ATTN_IN, STAGE_OUT_IN, STAGE_FFN_IN, STAGE_DOWN_IN, STAGE_EXPERT_DOWN_IN = range(5)
+
+
+class _Tap(ctypes.Structure):
+    _fields_ = [("stride", SZ), ("own_x", P), ("own_q", P), ("own_s", P), ("use_q", P),
+                ("use_s", P)]
+
+
+class Q8Tap:
+    """The oracle's own quantized inputs stage by stage (x, q, s: [stages,
+    stride], [stages, stride], [stages, stride / 256]) and, for the stages in
+    `use` ({stage: (codes, scales, ...)}), the codes and scales that replace
+    them in the products."""
+
+    def __init__(self, stages: int, width: int, use: dict | None = None, required=()):
+        self.stride = (width + 255) // 256 * 256
+        self.x = np.zeros((stages, self.stride), np.float32)
+        self.q = np.zeros((stages, self.stride), np.int8)
+        self.s = np.zeros((stages, self.stride // 256), np.float32)
+        self.use_q = np.zeros((stages, self.stride), np.int8)
+        self.use_s = np.zeros((stages, self.stride // 256), np.float32)
+        # the C tap replaces every stage the run reaches, or none
+        if use is not None and not set(required) <= set(use):
+            raise ValueError("Q8Tap: codes for stages %s are missing"
+                             % sorted(set(required) - set(use)))
+        self._uses = bool(use)
+        for st, rec in (use or {}).items():
+            q, sc = rec[0], rec[1]
+            self.use_q[st, :q.size] = q
+            self.use_s[st, :sc.size] = sc
+        self.st = _Tap(self.stride, _p(self.x), _p(self.q), _p(self.s),
+                       _p(self.use_q) if self._uses else None,
+                       _p(self.use_s) if self._uses else None)
+
+    def own(self, stage: int, n: int):
+        """The oracle's input, codes and scales of one stage's n values."""
+        return self.x[stage, :n], self.q[stage, :n], self.s[stage, :(n + 255) // 256]
+
+
+def moe_forward_tap(e: dict, hidden: int, x: np.ndarray, use: dict | None = None,
+                    threads: int = 0):
+    """Moe::forward of one row on the int8 path with its Q8 stages (FFN_IN,
+    DOWN_IN, EXPERT_DOWN_IN + j) recorded and, with `use`, replaced."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    out = np.empty(hidden, np.float32)
+    st = moe_struct(e)
+    tap = Q8Tap(STAGE_EXPERT_DOWN_IN + e["used"], max(hidden, e["mid"], e["shared_mid"]), use,
+                [STAGE_FFN_IN, STAGE_DOWN_IN] +
+                [STAGE_EXPERT_DOWN_IN + j for j in range(e["used"])])
+    lib().hyqo_moe_forward_tap(ctypes.byref(st), hidden, _p(x), _p(out), threads,
+                               ctypes.byref(tap.st))
+    return out, tap
+
+
 class _Moe(ctypes.Structure):
     _fields_ = [("experts", ctypes.c_int), ("used", ctypes.c_int), ("mid", ctypes.c_int),
                 ("shared_mid", ctypes.c_int), ("normalize", ctypes.c_int),
@@ -330,6 +390,40 @@ class DenseOracle:
         if rc != 0:
             raise ValueError("layer_step: bad layer or position")
         return h
+
+    def stages(self, l: int) -> list[int]:
+        """Widths of layer l's Q8 stages (STAGE_*), in stage order."""
+        c = self.model["cfg"]
+        layer = self.model["layers"][l]
+        w = [c["hidden"], c["heads"] * c["head_dim"], c["hidden"]]
+        if "moe" in layer:
+            e = layer["moe"]
+            return w + [e["shared_mid"]] + [e["mid"]] * e["used"]
+        return w + [c["ffn"]]
+
+    def layer_tap(self, l: int, hidden: np.ndarray, kc: np.ndarray, vc: np.ndarray, pos: int,
+                  use: dict | None = None, threads: int = 0):
+        """layer() on the int8 path with the Q8 stages recorded and, with
+        `use`, replaced: (output row, Q8Tap)."""
+        h = np.ascontiguousarray(hidden, np.float32).copy()
+        assert kc.flags["C_CONTIGUOUS"] and vc.flags["C_CONTIGUOUS"]
+        widths = self.stages(l)
+        tap = Q8Tap(len(widths), max(widths), use, range(len(widths)))
+        rc = lib().hyqo_layer_step_tap(ctypes.byref(self.m), l, _p(h), _p(kc), _p(vc),
+                                       kc.shape[0], pos, threads, ctypes.byref(tap.st))
+        if rc != 0:
+            raise ValueError("layer_step: bad layer or position")
+        return h, tap
+
+    def output_tap(self, hidden: np.ndarray, use: dict | None = None, threads: int = 0):
+        """output() on the int8 path with its one Q8 stage (STAGE_ATTN_IN)
+        recorded and, with `use`, replaced: (logits, Q8Tap)."""
+        h = np.ascontiguousarray(hidden, np.float32).copy()
+        logits = np.empty(self.model["cfg"]["vocab"], np.float32)
+        tap = Q8Tap(1, self.model["cfg"]["hidden"], use, [STAGE_ATTN_IN])
+        lib().hyqo_output_logits_tap(ctypes.byref(self.m), _p(h), _p(logits), threads,
+                                     ctypes.byref(tap.st))
+        return logits, tap
 
     def prefill_layer(self, l: int, hidden: np.ndarray, kc: np.ndarray, vc: np.ndarray,
                       pos: int, threads: int = 0) -> np.ndarray:

@@ -233,15 +233,32 @@ static int8_t tail_round(float v)
     return (int8_t)r;
 }
 
+/* max_abs_neon (src/quant.rs:869-892): vmaxq_f32 / vmaxvq_f32 (FMAX,
+ * FMAXV) over the whole 16-value steps, starting from 0: any NaN there makes
+ * the maximum NaN. The tail then folds in with f32::max, which returns the
+ * other operand when one is NaN (fmaxf), so a tail value replaces a NaN
+ * maximum. With max NaN (or 0), `max > 0.` fails: scale and inverse are 0
+ * and every code of the group is 0 (NaN * 0 converts to 0). */
+static float group_max_abs(const float *x, size_t len)
+{
+    size_t vec = len / 16 * 16;
+    float max = 0.f;
+    int nan = 0;
+    for (size_t i = 0; i < vec; ++i) {
+        float a = fabsf(x[i]);
+        if (a != a) nan = 1;
+        else if (a > max) max = a;
+    }
+    if (nan) max = NAN;
+    for (size_t i = vec; i < len; ++i) max = fmaxf(max, fabsf(x[i]));
+    return max;
+}
+
 void hyqo_q8_quantize(const float *x, size_t n, int8_t *q, float *scales)
 {
     for (size_t g0 = 0, gi = 0; g0 < n; g0 += 256, ++gi) {
         size_t len = n - g0 < 256 ? n - g0 : 256;
-        float max = 0.f;
-        for (size_t i = 0; i < len; ++i) {
-            float a = fabsf(x[g0 + i]);
-            if (a > max) max = a;
-        }
+        float max = group_max_abs(x + g0, len);
         float scale = 0.f, inverse = 0.f;
         if (max > 0.f) {
             scale = max / 127.f;

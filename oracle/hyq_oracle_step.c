@@ -9,10 +9,15 @@
  *   int8_path = 1  the int8 path the reference takes with SDOT
  *                  (src/model.rs:403-416, 461-471, 487-501, 522-531): every
  *                  matmul input is Q8-quantized and each output is the exact
- *                  value of the integer formula rounded once to f32.
- * The glue follows the x86 arms of rms_norm_into (src/model.rs:785-830),
- * rms_norm (:832-870), rope_with_cache (:874-917), attention_into
- * (:949-1035) and add (:1043-1077). hyqo_prefill_chunk is the batch > 1
+ *                  value of the integer formula rounded once to f32. The
+ *                  int8 path exists only in the aarch64 build, so its
+ *                  RMSNorms take that arm's operation order (x * (w *
+ *                  scale), src/model.rs:791-822, 837-865).
+ * The rest of the glue follows rope_with_cache (src/model.rs:874-917),
+ * attention_into (:949-1035), add (:1043-1077) and, with int8_path = 0, the
+ * x86 arms of rms_norm_into (:824-829) and rms_norm (:866-869); the
+ * hyqo_q8_tap of hyqo_layer_step_tap records and replaces the int8 path's
+ * quantized inputs stage by stage. hyqo_prefill_chunk is the batch > 1
  * arm of forward_into (src/model.rs:549-616): f32 activations through the
  * batched Weight::matmul (src/quant.rs:272-343), and the last row's logits
  * through the batch-1 matmul of the chosen arm.
@@ -33,20 +38,33 @@ static size_t rb_of(int dtype, size_t cols)
     return cols / (size_t)hyqo_block_len(dtype) * (size_t)hyqo_block_bytes(dtype);
 }
 
-void hyqo_rms_norm_into(const float *x, const float *w, size_t n, float eps, float *out)
+/* One normalized value. The aarch64 arm multiplies x by (w * scale) over
+ * whole 16-value steps (src/model.rs:791-815, :837-860) and by scale, then
+ * w, over the tail (:816-822, :861-864); the x86 arm always x * scale * w
+ * (:824-829, :866-869). */
+static float rms_value(float x, float w, float scale, size_t i, size_t n, int aarch64)
+{
+    if (aarch64 && i < n / 16 * 16) return x * (w * scale);
+    return x * scale * w;
+}
+
+void hyqo_rms_norm_into(const float *x, const float *w, size_t n, float eps, float *out,
+                        int aarch64)
 {
     float variance = hyqo_dot(x, x, n) / (float)n;
     float scale = 1.0f / sqrtf(variance + eps);
-    for (size_t i = 0; i < n; ++i) out[i] = x[i] * scale * w[i];
+    for (size_t i = 0; i < n; ++i) out[i] = rms_value(x[i], w[i], scale, i, n, aarch64);
 }
 
-void hyqo_rms_norm_rows(float *x, const float *w, size_t total, size_t wlen, float eps)
+void hyqo_rms_norm_rows(float *x, const float *w, size_t total, size_t wlen, float eps,
+                        int aarch64)
 {
     for (size_t r = 0; r + wlen <= total; r += wlen) {
         float *row = x + r;
         float variance = hyqo_dot(row, row, wlen) / (float)wlen;
         float scale = 1.0f / sqrtf(variance + eps);
-        for (size_t i = 0; i < wlen; ++i) row[i] = row[i] * scale * w[i];
+        for (size_t i = 0; i < wlen; ++i)
+            row[i] = rms_value(row[i], w[i], scale, i, wlen, aarch64);
     }
 }
 
@@ -119,14 +137,23 @@ int hyqo_max_threads(void)
 #endif
 }
 
-/* One int8-path GEMV: y = round_f32(exact integer formula) (see hyq_oracle.h). */
+/* One int8-path GEMV: y = round_f32(exact integer formula) (see hyq_oracle.h),
+ * its input being quantized stage `stage` of the tap (when set). */
 static void gemv_int8(int dtype, const uint8_t *w, size_t rows, size_t cols, const float *x,
-                      float *y)
+                      float *y, const hyqo_q8_tap *tap, int stage)
 {
     int8_t *q = (int8_t *)malloc(cols);
     float *s = (float *)malloc(sizeof(float) * (cols / 256 + 1));
     double *yd = (double *)malloc(sizeof(double) * rows);
     hyqo_q8_quantize(x, cols, q, s);
+    if (tap) {
+        size_t o = (size_t)stage * tap->stride, os = o / 256;
+        if (tap->own_x) memcpy(tap->own_x + o, x, sizeof(float) * cols);
+        if (tap->own_q) memcpy(tap->own_q + o, q, cols);
+        if (tap->own_s) memcpy(tap->own_s + os, s, sizeof(float) * ((cols + 255) / 256));
+        if (tap->use_q) memcpy(q, tap->use_q + o, cols);
+        if (tap->use_s) memcpy(s, tap->use_s + os, sizeof(float) * ((cols + 255) / 256));
+    }
     hyqo_gemv_q8_f64(dtype, w, rows, cols, q, s, yd, NULL);
     for (size_t r = 0; r < rows; ++r) y[r] = (float)yd[r];
     free(q);
@@ -135,29 +162,32 @@ static void gemv_int8(int dtype, const uint8_t *w, size_t rows, size_t cols, con
 }
 
 static void linear(const hyqo_model *m, int dtype, const uint8_t *w, size_t rows, size_t cols,
-                   const float *x, float *y, int int8_path, int threads)
+                   const float *x, float *y, int int8_path, int threads, const hyqo_q8_tap *tap,
+                   int stage)
 {
     if (int8_path)
-        gemv_int8(dtype, w, rows, cols, x, y);
+        gemv_int8(dtype, w, rows, cols, x, y, tap, stage);
     else
         hyqo_matmul(dtype, w, rows, cols, x, 1, y, threads);
     (void)m;
 }
 
 /* DenseFfn::forward at batch 1 on the int8 path (src/model.rs:487-501):
- * silu(gate x) * (up x) from Q8 inputs, then down of the product's Q8. */
+ * silu(gate x) * (up x) from Q8 inputs, then down of the product's Q8 (tap
+ * stages in_stage and down_stage). */
 static void ffn_int8(int dtype_gu, int dtype_down, const uint8_t *gate, const uint8_t *up,
-                     const uint8_t *down, size_t hidden, size_t mid, const float *x, float *out)
+                     const uint8_t *down, size_t hidden, size_t mid, const float *x, float *out,
+                     const hyqo_q8_tap *tap, int in_stage, int down_stage)
 {
     float *g = (float *)malloc(sizeof(float) * mid);
     float *u = (float *)malloc(sizeof(float) * mid);
-    gemv_int8(dtype_gu, gate, mid, hidden, x, g);
-    gemv_int8(dtype_gu, up, mid, hidden, x, u);
+    gemv_int8(dtype_gu, gate, mid, hidden, x, g, tap, in_stage);
+    gemv_int8(dtype_gu, up, mid, hidden, x, u, tap, in_stage);
     for (size_t i = 0; i < mid; ++i) {
         float v = g[i];
         g[i] = (v / (1.0f + expf(-v))) * u[i];
     }
-    gemv_int8(dtype_down, down, hidden, mid, g, out);
+    gemv_int8(dtype_down, down, hidden, mid, g, out, tap, down_stage);
     free(g);
     free(u);
 }
@@ -182,8 +212,8 @@ static void ffn_f32(int dtype_gu, int dtype_down, const uint8_t *gate, const uin
     free(g);
 }
 
-void hyqo_moe_forward(const hyqo_moe *e, size_t hidden, const float *x, size_t n, float *out,
-                      int int8_path, int threads)
+static void moe_forward(const hyqo_moe *e, size_t hidden, const float *x, size_t n, float *out,
+                        int int8_path, int threads, const hyqo_q8_tap *tap)
 {
     size_t E = (size_t)e->experts, U = (size_t)e->used, mid = (size_t)e->mid;
     /* router.matmul (F32, src/model.rs:691) and route per token (:692-698);
@@ -200,7 +230,7 @@ void hyqo_moe_forward(const hyqo_moe *e, size_t hidden, const float *x, size_t n
     /* output = shared.forward(input, batch) (:699) */
     if (int8_path && n == 1)
         ffn_int8(e->dtype_shared, e->dtype_shared_down, e->sgate, e->sup, e->sdown, hidden,
-                 (size_t)e->shared_mid, x, out);
+                 (size_t)e->shared_mid, x, out, tap, HYQO_STAGE_FFN_IN, HYQO_STAGE_DOWN_IN);
     else
         ffn_f32(e->dtype_shared, e->dtype_shared_down, e->sgate, e->sup, e->sdown, hidden,
                 (size_t)e->shared_mid, x, n, out, threads);
@@ -211,11 +241,13 @@ void hyqo_moe_forward(const hyqo_moe *e, size_t hidden, const float *x, size_t n
         size_t db = hidden * (size_t)hyqo_block_bytes(e->dtype_down) * mid /
                     (size_t)hyqo_block_len(e->dtype_down);
         float *res = (float *)malloc(sizeof(float) * hidden);
+        int visited = 0;
         for (size_t ex = 0; ex < E; ++ex)
             for (size_t k = 0; k < U; ++k) {
                 if ((size_t)pe[k] != ex) continue;
                 ffn_int8(e->dtype_gate, e->dtype_down, e->gate + ex * gb, e->up + ex * gb,
-                         e->down + ex * db, hidden, mid, x, res);
+                         e->down + ex * db, hidden, mid, x, res, tap, HYQO_STAGE_FFN_IN,
+                         HYQO_STAGE_EXPERT_DOWN_IN + visited++);
                 for (size_t i = 0; i < hidden; ++i) out[i] += pw[k] * res[i];
             }
         free(res);
@@ -229,8 +261,20 @@ void hyqo_moe_forward(const hyqo_moe *e, size_t hidden, const float *x, size_t n
     free(pw);
 }
 
-int hyqo_layer_step(const hyqo_model *m, int l, float *hidden, float *kc, float *vc, size_t ctx,
-                    size_t pos, int int8_path, int threads)
+void hyqo_moe_forward(const hyqo_moe *e, size_t hidden, const float *x, size_t n, float *out,
+                      int int8_path, int threads)
+{
+    moe_forward(e, hidden, x, n, out, int8_path, threads, NULL);
+}
+
+void hyqo_moe_forward_tap(const hyqo_moe *e, size_t hidden, const float *x, float *out,
+                          int threads, const hyqo_q8_tap *tap)
+{
+    moe_forward(e, hidden, x, 1, out, 1, threads, tap);
+}
+
+static int layer_step(const hyqo_model *m, int l, float *hidden, float *kc, float *vc,
+                      size_t ctx, size_t pos, int int8_path, int threads, const hyqo_q8_tap *tap)
 {
     size_t H = (size_t)m->hidden, D = (size_t)m->head_dim;
     size_t qlen = (size_t)m->heads * D, kvw = (size_t)m->kv_heads * D, F = (size_t)m->ffn;
@@ -247,34 +291,38 @@ int hyqo_layer_step(const hyqo_model *m, int l, float *hidden, float *kc, float 
     /* the step's RoPE tables at `pos` (src/model.rs:378-392) */
     hyqo_rope_tables(D, m->rope_base, pos, cos_s, sin_s);
 
-    hyqo_rms_norm_into(hidden, m->attn_norm[l], H, m->eps, xn);
-    linear(m, m->dtype_linear, m->wq[l], qlen, H, xn, q, int8_path, threads);
-    linear(m, m->dtype_linear, m->wk[l], kvw, H, xn, k, int8_path, threads);
-    linear(m, m->dtype_linear, m->wv[l], kvw, H, xn, v, int8_path, threads);
+    hyqo_rms_norm_into(hidden, m->attn_norm[l], H, m->eps, xn, int8_path);
+    linear(m, m->dtype_linear, m->wq[l], qlen, H, xn, q, int8_path, threads, tap,
+           HYQO_STAGE_ATTN_IN);
+    linear(m, m->dtype_linear, m->wk[l], kvw, H, xn, k, int8_path, threads, tap,
+           HYQO_STAGE_ATTN_IN);
+    linear(m, m->dtype_linear, m->wv[l], kvw, H, xn, v, int8_path, threads, tap,
+           HYQO_STAGE_ATTN_IN);
     /* per-head Q/K RMSNorm before RoPE (hy_v3) or after it (dense)
      * (src/model.rs:425-446) */
     if (m->arch == 1) {
-        hyqo_rms_norm_rows(q, m->q_norm[l], qlen, D, m->eps);
-        hyqo_rms_norm_rows(k, m->k_norm[l], kvw, D, m->eps);
+        hyqo_rms_norm_rows(q, m->q_norm[l], qlen, D, m->eps, int8_path);
+        hyqo_rms_norm_rows(k, m->k_norm[l], kvw, D, m->eps, int8_path);
     }
     hyqo_rope(q, (size_t)m->heads, D, cos_s, sin_s);
     hyqo_rope(k, (size_t)m->kv_heads, D, cos_s, sin_s);
     if (m->arch != 1) {
-        hyqo_rms_norm_rows(q, m->q_norm[l], qlen, D, m->eps);
-        hyqo_rms_norm_rows(k, m->k_norm[l], kvw, D, m->eps);
+        hyqo_rms_norm_rows(q, m->q_norm[l], qlen, D, m->eps, int8_path);
+        hyqo_rms_norm_rows(k, m->k_norm[l], kvw, D, m->eps, int8_path);
     }
     memcpy(kc + pos * kvw, k, sizeof(float) * kvw);
     memcpy(vc + pos * kvw, v, sizeof(float) * kvw);
     hyqo_attention(q, kc, vc, (size_t)m->heads, (size_t)m->kv_heads, D, pos + 1, att);
-    linear(m, m->dtype_linear, m->wo[l], H, qlen, att, proj, int8_path, threads);
+    linear(m, m->dtype_linear, m->wo[l], H, qlen, att, proj, int8_path, threads, tap,
+           HYQO_STAGE_OUT_IN);
     for (size_t i = 0; i < H; ++i) hidden[i] += proj[i];
-    hyqo_rms_norm_into(hidden, m->ffn_norm[l], H, m->eps, xn);
+    hyqo_rms_norm_into(hidden, m->ffn_norm[l], H, m->eps, xn, int8_path);
     if (m->moe && m->moe[l]) {
         /* Ffn::Moe (src/model.rs:507-510) */
-        hyqo_moe_forward(m->moe[l], H, xn, 1, proj, int8_path, threads);
+        moe_forward(m->moe[l], H, xn, 1, proj, int8_path, threads, tap);
     } else if (int8_path) {
-        gemv_int8(m->dtype_linear, m->wgate[l], F, H, xn, gate);
-        gemv_int8(m->dtype_linear, m->wup[l], F, H, xn, up);
+        gemv_int8(m->dtype_linear, m->wgate[l], F, H, xn, gate, tap, HYQO_STAGE_FFN_IN);
+        gemv_int8(m->dtype_linear, m->wup[l], F, H, xn, up, tap, HYQO_STAGE_FFN_IN);
         for (size_t i = 0; i < F; ++i) {
             float g = gate[i];
             float silu = g / (1.0f + expf(-g));
@@ -284,7 +332,8 @@ int hyqo_layer_step(const hyqo_model *m, int l, float *hidden, float *kc, float 
         hyqo_gate_up_silu(m->dtype_linear, m->wgate[l], m->wup[l], F, H, xn, gate, threads);
     }
     if (!(m->moe && m->moe[l]))
-        linear(m, m->dtype_down, m->wdown[l], H, F, gate, proj, int8_path, threads);
+        linear(m, m->dtype_down, m->wdown[l], H, F, gate, proj, int8_path, threads, tap,
+               HYQO_STAGE_DOWN_IN);
     for (size_t i = 0; i < H; ++i) hidden[i] += proj[i];
 
     free(xn);
@@ -298,14 +347,38 @@ int hyqo_layer_step(const hyqo_model *m, int l, float *hidden, float *kc, float 
     return 0;
 }
 
-void hyqo_output_logits(const hyqo_model *m, float *hidden, int int8_path, float *logits,
-                        int threads)
+int hyqo_layer_step(const hyqo_model *m, int l, float *hidden, float *kc, float *vc, size_t ctx,
+                    size_t pos, int int8_path, int threads)
+{
+    return layer_step(m, l, hidden, kc, vc, ctx, pos, int8_path, threads, NULL);
+}
+
+int hyqo_layer_step_tap(const hyqo_model *m, int l, float *hidden, float *kc, float *vc,
+                        size_t ctx, size_t pos, int threads, const hyqo_q8_tap *tap)
+{
+    return layer_step(m, l, hidden, kc, vc, ctx, pos, 1, threads, tap);
+}
+
+static void output_logits(const hyqo_model *m, float *hidden, int int8_path, float *logits,
+                          int threads, const hyqo_q8_tap *tap)
 {
     size_t H = (size_t)m->hidden;
     /* rms_norm(hidden, output_norm), then the output matmul (src/model.rs:515-538) */
-    hyqo_rms_norm_rows(hidden, m->output_norm, H, H, m->eps);
+    hyqo_rms_norm_rows(hidden, m->output_norm, H, H, m->eps, int8_path);
     linear(m, m->dtype_embed, m->output ? m->output : m->embed, (size_t)m->vocab, H, hidden,
-           logits, int8_path, threads);
+           logits, int8_path, threads, tap, HYQO_STAGE_ATTN_IN);
+}
+
+void hyqo_output_logits(const hyqo_model *m, float *hidden, int int8_path, float *logits,
+                        int threads)
+{
+    output_logits(m, hidden, int8_path, logits, threads, NULL);
+}
+
+void hyqo_output_logits_tap(const hyqo_model *m, float *hidden, float *logits, int threads,
+                            const hyqo_q8_tap *tap)
+{
+    output_logits(m, hidden, 1, logits, threads, tap);
 }
 
 int hyqo_decode_step(const hyqo_model *m, float *kcache, float *vcache, size_t ctx, size_t pos,
@@ -343,15 +416,15 @@ int hyqo_prefill_layer(const hyqo_model *m, int l, float *hidden, float *kc, flo
 
     /* normalized = rms_norm(hidden) row by row; q/k/v = matmul(., batch) (:555-564) */
     memcpy(xn, hidden, sizeof(float) * n * H);
-    hyqo_rms_norm_rows(xn, m->attn_norm[l], n * H, H, m->eps);
+    hyqo_rms_norm_rows(xn, m->attn_norm[l], n * H, H, m->eps, 0);
     hyqo_matmul(m->dtype_linear, m->wq[l], qlen, H, xn, n, q, threads);
     hyqo_matmul(m->dtype_linear, m->wk[l], kvw, H, xn, n, k, threads);
     hyqo_matmul(m->dtype_linear, m->wv[l], kvw, H, xn, n, v, threads);
     /* rope at start + token (src/model.rs:570-583, 919-947), then the dense
      * order's per-head norms (:584-587) */
     if (m->arch == 1) {
-        hyqo_rms_norm_rows(q, m->q_norm[l], n * qlen, D, m->eps);
-        hyqo_rms_norm_rows(k, m->k_norm[l], n * kvw, D, m->eps);
+        hyqo_rms_norm_rows(q, m->q_norm[l], n * qlen, D, m->eps, 0);
+        hyqo_rms_norm_rows(k, m->k_norm[l], n * kvw, D, m->eps, 0);
     }
     for (size_t t = 0; t < n; ++t) {
         hyqo_rope_tables(D, m->rope_base, pos + t, cos_s, sin_s);
@@ -359,8 +432,8 @@ int hyqo_prefill_layer(const hyqo_model *m, int l, float *hidden, float *kc, flo
         hyqo_rope(k + t * kvw, (size_t)m->kv_heads, D, cos_s, sin_s);
     }
     if (m->arch != 1) {
-        hyqo_rms_norm_rows(q, m->q_norm[l], n * qlen, D, m->eps);
-        hyqo_rms_norm_rows(k, m->k_norm[l], n * kvw, D, m->eps);
+        hyqo_rms_norm_rows(q, m->q_norm[l], n * qlen, D, m->eps, 0);
+        hyqo_rms_norm_rows(k, m->k_norm[l], n * kvw, D, m->eps, 0);
     }
     /* cache.append (:588-593, 650-669), then causal attention: token t sees
      * positions 0..=pos+t (src/model.rs:956-961) */
@@ -374,7 +447,7 @@ int hyqo_prefill_layer(const hyqo_model *m, int l, float *hidden, float *kc, flo
     /* DenseFfn::forward at batch n (src/model.rs:672-685): two matmuls,
      * silu(g) * u, down */
     memcpy(xn, hidden, sizeof(float) * n * H);
-    hyqo_rms_norm_rows(xn, m->ffn_norm[l], n * H, H, m->eps);
+    hyqo_rms_norm_rows(xn, m->ffn_norm[l], n * H, H, m->eps, 0);
     if (m->moe && m->moe[l]) {
         /* Moe::forward at batch n (src/model.rs:598-601) */
         hyqo_moe_forward(m->moe[l], H, xn, n, proj, 0, threads);

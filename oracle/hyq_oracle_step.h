@@ -52,8 +52,49 @@ typedef struct {
 void hyqo_moe_forward(const hyqo_moe *e, size_t hidden, const float *x, size_t n, float *out,
                       int int8_path, int threads);
 
-void hyqo_rms_norm_into(const float *x, const float *w, size_t n, float eps, float *out);
-void hyqo_rms_norm_rows(float *x, const float *w, size_t total, size_t wlen, float eps);
+/* The int8 path's quantized inputs, stage by stage, for the parity tests of
+ * the device's decode step. The stages of one layer (values per stage):
+ *   HYQO_STAGE_ATTN_IN        the normalized hidden row (Q/K/V input)    hidden
+ *   HYQO_STAGE_OUT_IN         the attention row (attention-output input) heads*head_dim
+ *   HYQO_STAGE_FFN_IN         the normalized row (FFN input)             hidden
+ *   HYQO_STAGE_DOWN_IN        silu(g) * u of the dense FFN, or of the MoE's
+ *                             shared expert (down input)                 ffn / shared_mid
+ *   HYQO_STAGE_EXPERT_DOWN_IN + j  the j-th routed expert's silu(g) * u,
+ *                             experts in ascending order                 mid
+ * and the output's one: HYQO_STAGE_ATTN_IN, the output-normalized row.
+ * Stage i's values sit at own_x / own_q / use_q + i * stride and its scales
+ * at own_s / use_s + i * stride / 256 (stride a multiple of 256). own_* (each
+ * when set) receive the oracle's own f32 input, codes and scales; use_q and
+ * use_s (each when set) replace the codes and scales that enter the
+ * product. */
+enum {
+    HYQO_STAGE_ATTN_IN = 0,
+    HYQO_STAGE_OUT_IN = 1,
+    HYQO_STAGE_FFN_IN = 2,
+    HYQO_STAGE_DOWN_IN = 3,
+    HYQO_STAGE_EXPERT_DOWN_IN = 4
+};
+typedef struct {
+    size_t stride;
+    float *own_x;
+    int8_t *own_q;
+    float *own_s;
+    const int8_t *use_q;
+    const float *use_s;
+} hyqo_q8_tap;
+
+/* Moe::forward of one row on the int8 path with a tap (its stages FFN_IN,
+ * DOWN_IN and EXPERT_DOWN_IN + j). */
+void hyqo_moe_forward_tap(const hyqo_moe *e, size_t hidden, const float *x, float *out,
+                          int threads, const hyqo_q8_tap *tap);
+
+/* rms_norm_into / rms_norm (src/model.rs:785-870) in the operation order of
+ * the aarch64 arm (aarch64 = 1: x * (w * scale) over whole 16-value steps) or
+ * the x86 arm (0: x * scale * w). */
+void hyqo_rms_norm_into(const float *x, const float *w, size_t n, float eps, float *out,
+                        int aarch64);
+void hyqo_rms_norm_rows(float *x, const float *w, size_t total, size_t wlen, float eps,
+                        int aarch64);
 void hyqo_rope_tables(size_t head_dim, float base, size_t pos, float *cos_s, float *sin_s);
 void hyqo_rope(float *values, size_t heads, size_t dim, const float *cos_s, const float *sin_s);
 void hyqo_attention(const float *q, const float *keys, const float *values, size_t heads,
@@ -80,6 +121,11 @@ int hyqo_prefill_layer(const hyqo_model *m, int l, float *hidden, float *kc, flo
                        size_t ctx, size_t pos, size_t n, int threads);
 void hyqo_output_logits(const hyqo_model *m, float *hidden, int int8_path, float *logits,
                         int threads);
+/* hyqo_layer_step and hyqo_output_logits on the int8 path with a tap. */
+int hyqo_layer_step_tap(const hyqo_model *m, int l, float *hidden, float *kc, float *vc,
+                        size_t ctx, size_t pos, int threads, const hyqo_q8_tap *tap);
+void hyqo_output_logits_tap(const hyqo_model *m, float *hidden, float *logits, int threads,
+                            const hyqo_q8_tap *tap);
 int hyqo_argmax(const float *x, size_t n);
 /* OpenMP threads the matmul/attention loops use when threads <= 0. */
 int hyqo_max_threads(void);

@@ -63,7 +63,8 @@ def test_stq_all_patterns_on_gpu(gpu_ctx, oracle):
 def test_quantize_q8_bit_exact(gpu_ctx, hyq, oracle):
     cases = json.load(open(os.path.join(GOLDEN, "q8_vectors.json")))
     rng = np.random.default_rng(0)
-    inputs = [np.array(c["x"], np.float32) for c in cases]
+    inputs = [np.array([int(b, 16) for b in c["x_bits"]], np.uint32).view(np.float32)
+              for c in cases]
     inputs += [rng.normal(0, 1, 2048).astype(np.float32),
                (rng.normal(0, 3, 6144) * (np.arange(6144) % 7)).astype(np.float32),
                rng.normal(0, 1, 264).astype(np.float32)]
@@ -79,6 +80,16 @@ def test_quantize_q8_bit_exact(gpu_ctx, hyq, oracle):
         q_ref, s_ref = oracle.q8_quantize(x)
         assert np.array_equal(q_dev.view(np.int8), q_ref)
         assert np.array_equal(s_dev.view(np.uint32), s_ref.view(np.uint32))
+    # the golden cases' own answers too (the NaN and infinity rules included)
+    for c, x in zip(cases, inputs):
+        q8 = gpu_ctx.q8(x.size)
+        q8.quantize_into(gpu_ctx.array(x).ptr)
+        gpu_ctx.sync()
+        q_dev = device_bytes(hyq, gpu_ctx, q8.values_ptr, x.size).view(np.int8)
+        s_dev = device_bytes(hyq, gpu_ctx, q8.scales_ptr, 4 * ((x.size + 255) // 256))
+        assert np.array_equal(q_dev, np.array(c["q"], np.int8)), c["name"]
+        s_ref = np.array([int(b, 16) for b in c["scales_bits"]], np.uint32)
+        assert np.array_equal(s_dev.view(np.uint32), s_ref), c["name"]
 
 
 # ---- integer block sums ----
@@ -248,7 +259,10 @@ def test_staged_gemv_equals_quantize_then_gemv(gpu_ctx, hyq, dtype, cols):
     looped stage). Its output equals hyq_quantize_q8_d + hyq_gemv_q8_d bit for
     bit: the same maxima, IEEE divisions, round-half-even and exact integer
     sums. A row 4 bytes off float4 alignment takes the two-launch path and
-    must agree as well. An all-zero group (scale 0) is included."""
+    must agree as well. An all-zero group (scale 0) is included, and from
+    three groups on a group holding a NaN: the reference's NEON maximum
+    (FMAX) makes that group's maximum NaN, so its scale and codes are 0 and
+    the product equals that of the same row with the group zeroed."""
     if cols % hyq.lib().hyq_block_len(dtype):
         pytest.skip("width is not a whole number of blocks")
     rows = 200
@@ -257,6 +271,9 @@ def test_staged_gemv_equals_quantize_then_gemv(gpu_ctx, hyq, dtype, cols):
     rng = np.random.default_rng(cols)
     x = (rng.normal(0, 1, cols) * rng.choice([1e-3, 1.0, 40.0], cols)).astype(np.float32)
     x[256:512] = 0.0
+    nan_group = cols >= 768
+    if nan_group:
+        x[600] = np.nan
     W = gpu_ctx.upload(dtype, w, (cols, rows))
     xd = gpu_ctx.array(np.concatenate([x, x[:4]]))
     xo = gpu_ctx.array(np.concatenate([np.zeros(1, np.float32), x]))  # x at byte offset 4
@@ -270,6 +287,13 @@ def test_staged_gemv_equals_quantize_then_gemv(gpu_ctx, hyq, dtype, cols):
     a, b, c = y_staged.numpy(), y_two.numpy(), y_off.numpy()
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     assert np.array_equal(c.view(np.uint32), b.view(np.uint32))
+    if nan_group:
+        assert np.isfinite(a).all()
+        xz = x.copy()
+        xz[512:768] = 0.0
+        yz = gpu_ctx.empty(rows, np.float32)
+        hyq.check(L.hyq_matmul_d(gpu_ctx.handle, W.handle, gpu_ctx.array(xz).ptr, 1, yz.ptr))
+        assert np.array_equal(a.view(np.uint32), yz.numpy().view(np.uint32))
 
 
 def test_residual_epilogue(gpu_ctx, hyq, oracle):

@@ -5,13 +5,17 @@ site, :507-510 and :598-601) with the hy_v3 Q/K-norm order (:425-446).
 
 Bars: expert selections equal; route weights within 2 f32 ulps (the GPU's
 expf and glibc's differ by an ulp); a batch-1 MoE FFN within 1e-4 relative
-unless one of its Q8 inputs hit a rounding midpoint (a flip moves one int8
-code, ~6e-4 of a product; at most one such case per test); an f16-MFMA batch
-within 2e-3; decoder layers teacher-forced as in test_gpu_c3.py."""
+on the device's int8 codes, every code where they differ from the oracle's
+shown to be a rounding-midpoint flip (tests/q8_proof.py); an f16-MFMA batch
+within 2e-3; decoder layers teacher-forced and free-running as in
+test_gpu_c3.py."""
 import numpy as np
 import pytest
 
+import q8_proof as P
 from synth import Q4_K, Q8_0, make_hyv3_model, make_kv_cache, load_hyv3, upload_moe
+
+TRACE_BYTES = 4 << 20
 
 pytestmark = pytest.mark.gpu
 
@@ -70,15 +74,26 @@ def test_moe_forward_one_token(gpu_ctx, hyq, oracle):
     e = model["layers"][1]["moe"]
     H = HYV3["hidden"]
     ffn = upload_moe(hyq, gpu_ctx, e, H)
-    errs = []
+    gpu_ctx.set_q8_trace(TRACE_BYTES)
+    errs, flips = [], []
     for s in range(4):
         x = np.random.default_rng(s).normal(0, 1, (1, H)).astype(np.float32)
+        gpu_ctx.clear_q8_trace()
         got = ffn.forward(x)
-        ref = oracle.moe_forward(e, H, x, 1, int8_path=True)
-        errs.append(_rel(got, ref))
-    _print("moe batch-1 rel", ["%.1e" % v for v in errs])
-    assert max(errs) <= 2e-3, errs
-    assert sum(v > 1e-4 for v in errs) <= 1, errs
+        # the records: the row's Q8, the shared expert's down input, the
+        # routed experts' down inputs (one record, slot after slot)
+        rx, rs, (qe, se, xe) = gpu_ctx.q8_trace()
+        m, used = e["mid"], e["used"]
+        assert qe.size == m * used
+        stages = {oracle.STAGE_FFN_IN: rx, oracle.STAGE_DOWN_IN: rs}
+        for j in range(used):
+            stages[oracle.STAGE_EXPERT_DOWN_IN + j] = (
+                qe[j * m:(j + 1) * m], se[j * m // 256:(j + 1) * m // 256], xe[j * m:(j + 1) * m])
+        ref, tap = oracle.moe_forward_tap(e, H, x, use=stages)
+        errs.append(P.prove(f"moe row {s}", [(got, ref)], tap, stages, flips))
+    gpu_ctx.set_q8_trace(None)
+    _print("moe batch-1 rel on the GPU's codes", ["%.1e" % v for v in errs])
+    P.print_flips("moe batch-1", flips)
 
 
 @pytest.mark.parametrize("n", [5, 64])
@@ -98,22 +113,25 @@ def test_moe_forward_batch(gpu_ctx, hyq, oracle, n):
     assert rel <= 2e-3
 
 
-def _teacher_forced(ref, dec, cfg, pos, logits, label):
+def _teacher_forced(ref, dec, stages, final, cfg, pos, logits, label):
+    """Each layer (dense or MoE) on the GPU's input row, cache and int8 codes,
+    then the output: every flip explained, everything within 1e-4."""
     tr = dec.trace(1)[:, 0]
-    errs = []
+    errs, flips = [], []
     for l in range(cfg["layers"]):
         kc, vc = dec.read_kv(l, pos + 1)
         kref = np.zeros((pos + 1, kc.shape[1]), np.float32)
         vref = kref.copy()
         kref[:pos] = kc[:pos]
         vref[:pos] = vc[:pos]
-        out = ref.layer(l, tr[l], kref, vref, pos, int8_path=True)
-        errs.append(max(_rel(tr[l + 1], out), _rel(kc[pos], kref[pos]),
-                        _rel(vc[pos], vref[pos])))
-    errs.append(_rel(logits, ref.output(tr[-1], int8_path=True)))
-    _print(label, "per-layer rel (last: logits)", ["%.1e" % e for e in errs])
-    assert max(errs) <= 2e-3, (label, errs)
-    assert sum(e > 1e-4 for e in errs) <= max(1, len(errs) // 4), (label, errs)
+        out, tap = ref.layer_tap(l, tr[l], kref, vref, pos, use=stages[l])
+        errs.append(P.prove((label, l), [(tr[l + 1], out), (kc[pos], kref[pos]),
+                                         (vc[pos], vref[pos])], tap, stages[l], flips))
+    lg, tap = ref.output_tap(tr[-1], use=final)
+    errs.append(P.prove((label, "output"), [(logits, lg)], tap, final, flips))
+    _print(label, "per-layer rel on the GPU's codes (last: logits)",
+           ["%.1e" % e for e in errs])
+    P.print_flips(label, flips)
 
 
 def test_hyv3_decoder_matches_oracle(gpu_ctx, hyq, oracle):
@@ -132,20 +150,28 @@ def test_hyv3_decoder_matches_oracle(gpu_ctx, hyq, oracle):
     k0, v0 = k.copy(), v.copy()
     ref = oracle.DenseOracle(model)
     dec.set_trace(1)
+    gpu_ctx.set_q8_trace(TRACE_BYTES)
     token, toks = 11, []
     for i in range(4):
         pos = prefilled + i
+        gpu_ctx.clear_q8_trace()
         logits, nxt = dec.forward(token)
-        _teacher_forced(ref, dec, cfg, pos, logits, f"hyv3 step {i}")
-        ref_logits = ref.step(k, v, pos, token, int8_path=True)
-        rel = _rel(logits, ref_logits)
-        _print(f"hyv3 step {i}: free-running logits rel {rel:.2e}")
-        assert rel <= 5e-3, (i, rel)
+        stages, final = P.split_step_records(gpu_ctx.q8_trace(), ref, cfg["layers"])
+        _teacher_forced(ref, dec, stages, final, cfg, pos, logits, f"hyv3 step {i}")
+        # free-running: the oracle's own chain on the GPU's codes
+        flips = []
+        ref_logits = P.step_with_device_codes(ref, cfg, P.embed_row(model, cfg, token), k, v,
+                                              pos, stages, final, f"hyv3 step {i}", flips)
+        rel = P.rel(logits, ref_logits)
+        _print(f"hyv3 step {i}: free-running logits rel {rel:.2e} on the GPU's codes "
+               f"({len(flips)} flipped codes explained)")
+        assert rel <= P.DECODE_BAR, (i, rel)
         top = np.sort(ref_logits)[-2:]
         if top[1] - top[0] > 1e-3 * np.abs(ref_logits).max():
             assert nxt == int(np.argmax(ref_logits))
         toks.append(nxt)
         token = nxt
+    gpu_ctx.set_q8_trace(None)
     dec.set_trace(None)
     for l in range(cfg["layers"]):
         dec.load_kv(l, k0[l, :prefilled], v0[l, :prefilled])
@@ -169,8 +195,11 @@ def test_hyv3_prefill_matches_oracle(gpu_ctx, hyq, oracle):
     dec.position = prefilled
     ref = oracle.DenseOracle(model)
     dec.set_trace(n)
+    gpu_ctx.set_q8_trace(TRACE_BYTES)
     toks = np.random.default_rng(n).integers(0, cfg["vocab"], n).astype(np.int32)
     logits, _ = dec.prefill(toks)
+    recs = gpu_ctx.q8_trace()
+    gpu_ctx.set_q8_trace(None)
     tr = dec.trace(n)
     errs = []
     for l in range(cfg["layers"]):
@@ -182,10 +211,14 @@ def test_hyv3_prefill_matches_oracle(gpu_ctx, hyq, oracle):
         out = ref.prefill_layer(l, tr[l], kref, vref, prefilled).reshape(n, -1)
         errs.append(_rel(tr[l + 1], out))
         assert _rel(kc[prefilled:], kref[prefilled:]) <= 2e-3, (l, "K rows")
-    lerr = _rel(logits, ref.output(tr[-1, -1], int8_path=True))
+    # the logits: one batch-1 product of the GPU's final row on its codes
+    assert len(recs) == 1, len(recs)
+    flips = []
+    lg, tap = ref.output_tap(tr[-1, -1], use={0: recs[0]})
+    lerr = P.prove("hyv3 prefill output", [(logits, lg)], tap, {0: recs[0]}, flips)
     _print("hyv3 prefill per-layer rel", ["%.1e" % e for e in errs], "logits %.1e" % lerr)
+    P.print_flips("hyv3 prefill output", flips)
     assert max(errs) <= 2e-3, errs
-    assert lerr <= 2e-3, lerr
     dec.set_trace(None)
     dec.close()
 

@@ -38,7 +38,7 @@ def test_rms_norm_q8(gpu_ctx, hyq, oracle):
         y = yd.numpy()
         y_ref = np.empty(n, np.float32)
         oracle.lib().hyqo_rms_norm_into(x.ctypes.data, w.ctypes.data, n, _f(1e-5),
-                                        y_ref.ctypes.data)
+                                        y_ref.ctypes.data, 1)
         assert np.allclose(y, y_ref, rtol=4e-7, atol=0), n
         q = device_bytes(hyq, gpu_ctx, q8.values_ptr, n).view(np.int8)
         q_ref, _ = oracle.q8_quantize(y)  # the GPU's own f32 row, quantized by the oracle
@@ -52,7 +52,7 @@ def _rope_ref(oracle, x, heads, pos, base, norm, eps):
     L.hyqo_rope_tables(128, _f(base), pos, c.ctypes.data, s.ctypes.data)
     x = x.copy()
     L.hyqo_rope(x.ctypes.data, heads, 128, c.ctypes.data, s.ctypes.data)
-    L.hyqo_rms_norm_rows(x.ctypes.data, norm.ctypes.data, x.size, 128, _f(eps))
+    L.hyqo_rms_norm_rows(x.ctypes.data, norm.ctypes.data, x.size, 128, _f(eps), 1)
     return x
 
 
@@ -365,10 +365,10 @@ def test_attention_rope_fused(gpu_ctx, hyq, oracle, pos, norm_first):
         def rot(x, n, w):
             x = x.copy()
             if norm_first:
-                O.hyqo_rms_norm_rows(x.ctypes.data, w.ctypes.data, x.size, 128, _f(eps))
+                O.hyqo_rms_norm_rows(x.ctypes.data, w.ctypes.data, x.size, 128, _f(eps), 1)
             O.hyqo_rope(x.ctypes.data, n, 128, c.ctypes.data, s.ctypes.data)
             if not norm_first:
-                O.hyqo_rms_norm_rows(x.ctypes.data, w.ctypes.data, x.size, 128, _f(eps))
+                O.hyqo_rms_norm_rows(x.ctypes.data, w.ctypes.data, x.size, 128, _f(eps), 1)
             return x
         q_ref, k_ref = rot(q, heads, qn), rot(k, kvh, kn)
         kc_ref[p], vc_ref[p] = k_ref, v

@@ -115,13 +115,25 @@ def test_fused_row_dot_matches_decode(oracle, dtype):
 
 # ---- Q8 activations: src/quant.rs:2955-2978 plus constructed vectors ----
 
+def q8_case_arrays(c):
+    """Inputs and scales of a q8_vectors.json case from their f32 bit patterns."""
+    x = np.array([int(b, 16) for b in c["x_bits"]], np.uint32).view(np.float32)
+    s = np.array([int(b, 16) for b in c["scales_bits"]], np.uint32).view(np.float32)
+    return x, np.array(c["q"], np.int8), s
+
+
 def test_q8_constructed_vectors(oracle):
+    """Ties, saturation, zero groups, tails, and NaN / infinity in the steps
+    and in the tail (max_abs_neon's FMAX propagates NaN, f32::max skips it)."""
     with open(os.path.join(GOLDEN, "q8_vectors.json")) as f:
         cases = json.load(f)
+    names = {c["name"] for c in cases}
+    assert {"nan_in_body", "nan_in_tail", "nan_in_body_with_tail", "infinity"} <= names
     for c in cases:
-        q, s = oracle.q8_quantize(np.array(c["x"], dtype=np.float32))
-        assert np.array_equal(q, np.array(c["q"], dtype=np.int8)), c["name"]
-        assert np.array_equal(s, np.array(c["scales"], dtype=np.float32)), c["name"]
+        x, q_ref, s_ref = q8_case_arrays(c)
+        q, s = oracle.q8_quantize(x)
+        assert np.array_equal(q, q_ref), c["name"]
+        assert np.array_equal(s.view(np.uint32), s_ref.view(np.uint32)), c["name"]
 
 
 def test_q8_round_trip_invariant(oracle):

@@ -111,27 +111,56 @@ def test_prefill_errors(oracle):
 
 # ---- pins of the step glue by what the mathematics fixes ----
 
-def test_rms_norm_constant_row_closed_form(oracle):
+@pytest.mark.parametrize("arm", [0, 1], ids=["x86", "aarch64"])
+def test_rms_norm_constant_row_closed_form(oracle, arm):
     """rms_norm_into (src/model.rs:785-830): a constant row c has mean square
-    c^2, so every output is c * (1/sqrt(c^2 + eps)) * w_i; a wrong divisor
-    (n - 1, or the sum instead of the mean) or a missing eps changes it."""
+    c^2, so every output is c * w_i / sqrt(c^2 + eps) up to the rounding of
+    the products (each arm rounds twice); a wrong divisor (n - 1, or the sum
+    instead of the mean) or a missing eps changes it. The width has a tail
+    past the last 16-value step."""
     L = oracle.lib()
-    n = 2048
+    n = 2048 + 5
     w = np.random.default_rng(1).normal(1, 0.02, n).astype(np.float32)
     for c, eps in ((0.75, 1e-5), (3.0, 1e-5), (1e-3, 1e-5), (0.5, 0.0)):
         x = np.full(n, c, np.float32)
         out = np.empty(n, np.float32)
-        L.hyqo_rms_norm_into(_p(x), _p(w), n, _f(eps), _p(out))
-        scale = np.float32(1.0) / np.sqrt(np.float32(c) * np.float32(c) + np.float32(eps))
-        exp = (np.float32(c) * scale) * w
-        assert np.allclose(out, exp, rtol=2e-7, atol=0), (c, eps)
+        L.hyqo_rms_norm_into(_p(x), _p(w), n, _f(eps), _p(out), arm)
+        exp = c * w.astype(np.float64) / np.sqrt(np.float64(np.float32(c)) ** 2 + eps)
+        assert np.allclose(out, exp, rtol=2.5e-7, atol=0), (c, eps)
         # the rows form equals the single-row form row by row
         rows = np.tile(x, 3)
-        L.hyqo_rms_norm_rows(_p(rows), _p(w), rows.size, n, _f(eps))
+        L.hyqo_rms_norm_rows(_p(rows), _p(w), rows.size, n, _f(eps), arm)
         assert np.array_equal(rows.reshape(3, n), np.tile(out, (3, 1)))
 
 
-def test_rms_norm_power_of_two_invariance(oracle):
+def test_rms_norm_arms_differ_only_in_rounding(oracle):
+    """The aarch64 arm forms x * (w * scale) over whole 16-value steps and
+    the x86 arm (x * scale) * w (src/model.rs:809, :828): with every w_i a
+    power of two both products are exact scalings of one rounded product,
+    so the arms agree bit for bit; with general w they differ by at most one
+    rounding each (2 ulps); past the last 16-value step the aarch64 arm also
+    takes x * scale * w, so the tail agrees bit for bit."""
+    L = oracle.lib()
+    rng = np.random.default_rng(3)
+    n = 2048 + 11
+    x = rng.normal(0, 1, n).astype(np.float32)
+    out0, out1 = np.empty(n, np.float32), np.empty(n, np.float32)
+    w2 = (2.0 ** rng.integers(-3, 4, n)).astype(np.float32)
+    L.hyqo_rms_norm_into(_p(x), _p(w2), n, _f(1e-5), _p(out0), 0)
+    L.hyqo_rms_norm_into(_p(x), _p(w2), n, _f(1e-5), _p(out1), 1)
+    assert np.array_equal(out0.view(np.uint32), out1.view(np.uint32))
+    w = rng.normal(1, 0.02, n).astype(np.float32)
+    L.hyqo_rms_norm_into(_p(x), _p(w), n, _f(1e-5), _p(out0), 0)
+    L.hyqo_rms_norm_into(_p(x), _p(w), n, _f(1e-5), _p(out1), 1)
+    body = n // 16 * 16
+    assert np.array_equal(out0[body:].view(np.uint32), out1[body:].view(np.uint32))
+    ulp = np.spacing(np.abs(out0[:body]))
+    assert np.all(np.abs(out0[:body] - out1[:body]) <= 2 * ulp)
+    assert not np.array_equal(out0[:body], out1[:body])  # the orders do differ
+
+
+@pytest.mark.parametrize("arm", [0, 1], ids=["x86", "aarch64"])
+def test_rms_norm_power_of_two_invariance(oracle, arm):
     """With eps = 0, scaling the row by 2^k scales the mean square by 4^k and
     its root by 2^k, all exactly, so the output is unchanged bit for bit."""
     L = oracle.lib()
@@ -140,16 +169,16 @@ def test_rms_norm_power_of_two_invariance(oracle):
     x = rng.normal(0, 1, n).astype(np.float32)
     w = rng.normal(1, 0.02, n).astype(np.float32)
     base = np.empty(n, np.float32)
-    L.hyqo_rms_norm_into(_p(x), _p(w), n, _f(0.0), _p(base))
+    L.hyqo_rms_norm_into(_p(x), _p(w), n, _f(0.0), _p(base), arm)
     for k in (-20, -3, 5, 30):
         xs = (x * np.float32(2.0 ** k)).astype(np.float32)
         out = np.empty(n, np.float32)
-        L.hyqo_rms_norm_into(_p(xs), _p(w), n, _f(0.0), _p(out))
+        L.hyqo_rms_norm_into(_p(xs), _p(w), n, _f(0.0), _p(out), arm)
         assert np.array_equal(out.view(np.uint32), base.view(np.uint32)), k
     # and against float64 within f32 rounding
     ref = x.astype(np.float64) / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-5) * w
     out = np.empty(n, np.float32)
-    L.hyqo_rms_norm_into(_p(x), _p(w), n, _f(1e-5), _p(out))
+    L.hyqo_rms_norm_into(_p(x), _p(w), n, _f(1e-5), _p(out), arm)
     assert np.allclose(out, ref, rtol=1e-5, atol=1e-6)
 
 
@@ -409,3 +438,68 @@ def test_qk_norm_order_by_architecture(oracle, arch):
     other = norm(rope(k)) if arch == 1 else rope(norm(k))
     assert _rel(kc[pos], exp) <= 1e-5
     assert _rel(kc[pos], other) > 1e-3
+
+
+# ---- the Q8 tap the decode-path parity tests replace codes through ----
+
+@pytest.mark.parametrize("moe", [False, True])
+def test_q8_tap_records_and_replays_the_int8_path(oracle, moe):
+    """hyqo_layer_step_tap / hyqo_output_logits_tap / hyqo_moe_forward_tap:
+    each recorded stage's codes and scales are the quantizer's output on the
+    recorded input; replaying the recorded codes gives the untapped layer,
+    output and MoE FFN bit for bit; and one replaced code reaches the
+    product: it moves the layer's output, its K/V row or a later stage's
+    recorded input (with every stage replaced, a later stage's codes absorb
+    an earlier stage's change, which its recorded input still shows)."""
+    c = HYV3_SMALL if moe else SMALL
+    model = _hyv3(seed=7) if moe else make_dense_model(c, linear=Q2_0C, seed=7)
+    ref = oracle.DenseOracle(model)
+    k, v = make_kv_cache(c, 24, 9, seed=7)
+    h = np.random.default_rng(7).normal(0, 1, c["hidden"]).astype(np.float32)
+    for l in range(c["layers"]):
+        widths = ref.stages(l)
+        kk, vv = k[l].copy(), v[l].copy()
+        plain = ref.layer(l, h, kk, vv, 9, int8_path=True)
+        out, tap = ref.layer_tap(l, h, k[l].copy(), v[l].copy(), 9)
+        assert np.array_equal(out.view(np.uint32), plain.view(np.uint32))
+        use = {}
+        for st, n in enumerate(widths):
+            x, q, s = tap.own(st, n)
+            q_ref, s_ref = oracle.q8_quantize(x)
+            assert np.array_equal(q, q_ref) and np.array_equal(s, s_ref), (l, st)
+            use[st] = (q.copy(), s.copy())
+        again, _ = ref.layer_tap(l, h, k[l].copy(), v[l].copy(), 9, use=use)
+        assert np.array_equal(again.view(np.uint32), plain.view(np.uint32))
+        for st in range(len(widths)):
+            moved = {a: (b[0].copy(), b[1]) for a, b in use.items()}
+            q = moved[st][0]
+            j = int(np.argmax(np.abs(q) < 120))
+            q[j] += 1
+            kk2, vv2 = k[l].copy(), v[l].copy()
+            changed, tap2 = ref.layer_tap(l, h, kk2, vv2, 9, use=moved)
+            later = [not np.array_equal(tap2.own(a, widths[a])[0], tap.own(a, widths[a])[0])
+                     for a in range(st + 1, len(widths))]
+            assert (not np.array_equal(changed, plain) or any(later) or
+                    not np.array_equal(kk2, kk) or not np.array_equal(vv2, vv)), (l, st)
+        with pytest.raises(ValueError):
+            ref.layer_tap(l, h, k[l].copy(), v[l].copy(), 9,
+                          use={a: b for a, b in use.items() if a != 1})
+        h = plain
+    logits = ref.output(h, int8_path=True)
+    lg, tap = ref.output_tap(h)
+    assert np.array_equal(lg.view(np.uint32), logits.view(np.uint32))
+    x, q, s = tap.own(0, c["hidden"])
+    lg2, _ = ref.output_tap(h, use={0: (q.copy(), s.copy())})
+    assert np.array_equal(lg2.view(np.uint32), logits.view(np.uint32))
+    if moe:
+        e = model["layers"][1]["moe"]
+        xr = np.random.default_rng(8).normal(0, 1, (1, c["hidden"])).astype(np.float32)
+        plain = oracle.moe_forward(e, c["hidden"], xr, 1, int8_path=True)[0]
+        out, tap = oracle.moe_forward_tap(e, c["hidden"], xr)
+        assert np.array_equal(out.view(np.uint32), plain.view(np.uint32))
+        st = [oracle.STAGE_FFN_IN, oracle.STAGE_DOWN_IN] + \
+            [oracle.STAGE_EXPERT_DOWN_IN + j for j in range(e["used"])]
+        n = [c["hidden"], e["shared_mid"]] + [e["mid"]] * e["used"]
+        use = {a: tuple(t.copy() for t in tap.own(a, w)[1:]) for a, w in zip(st, n)}
+        again, _ = oracle.moe_forward_tap(e, c["hidden"], xr, use=use)
+        assert np.array_equal(again.view(np.uint32), plain.view(np.uint32))
