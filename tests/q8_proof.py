@@ -136,3 +136,23 @@ def step_with_device_codes(ref, cfg, hidden, kcache, vcache, pos, layer_stages, 
 def embed_row(model, cfg, token):
     rb = model["embed"].size // cfg["vocab"]
     return O.decode(model["embed_dtype"], model["embed"][token * rb:(token + 1) * rb])
+
+
+def check_step(ctx, ref, model, cfg, kf, vf, pos, token, logits, nxt, label):
+    """One traced decode step (ctx's record holds exactly that step's) against
+    the oracle's own chain on caches kf/vf with the device's codes: every
+    stage proved as above, the logits within the decode bar, and the same
+    greedy token where the oracle's top-2 gap is clear. Returns the relative
+    error of the logits."""
+    stages, final = split_step_records(ctx.q8_trace(), ref, cfg["layers"])
+    flips = []
+    ref_logits = step_with_device_codes(ref, cfg, embed_row(model, cfg, token), kf, vf, pos,
+                                        stages, final, label, flips)
+    r = rel(logits, ref_logits)
+    print(f"{label}: logits rel {r:.2e} on the device's codes "
+          f"({len(flips)} flipped codes explained)", flush=True)
+    assert r <= DECODE_BAR, (label, r)
+    top = np.sort(ref_logits)[-2:]
+    if top[1] - top[0] > 1e-3 * np.abs(ref_logits).max():
+        assert nxt == int(np.argmax(ref_logits)), label
+    return r

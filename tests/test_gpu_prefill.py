@@ -13,6 +13,8 @@ hyq_dense_forward."""
 import numpy as np
 import pytest
 
+import q8_proof as P
+
 from synth import (Q2_0C, Q4_K, Q6_K, Q8_0, STQ1_0, load_dense, make_dense_model, make_kv_cache,
                    random_matrix)
 
@@ -178,8 +180,8 @@ def test_prefill_of_one_token_is_the_decode_step(gpu_ctx, hyq):
 
 def test_decode_continues_after_prefill(gpu_ctx, hyq, oracle):
     """Batch-1 steps after a prefill attend to the prefilled rows: each
-    step's logits match the oracle's int8 step on the GPU's own cache (the
-    decode-step tolerance, 5e-3 relative)."""
+    step's logits match the oracle's int8 step on the GPU's own cache and
+    int8 codes (the decode bar, 1e-4 relative; tests/q8_proof.py)."""
     c = SMALL
     context, past, n = 64, 3, 40
     model = _model(Q2_0C, seed=9)
@@ -188,17 +190,18 @@ def test_decode_continues_after_prefill(gpu_ctx, hyq, oracle):
     _, token = dec.prefill(tokens)
     ref = oracle.DenseOracle(model)
     kvw = c["kv_heads"] * c["head_dim"]
+    gpu_ctx.set_q8_trace(1 << 20)
     for i in range(3):
         pos = past + n + i
         k = np.zeros((c["layers"], context, kvw), np.float32)
         v = np.zeros_like(k)
         for l in range(c["layers"]):
             k[l, :pos], v[l, :pos] = dec.read_kv(l, pos)
+        gpu_ctx.clear_q8_trace()
         logits, nxt = dec.forward(token)
-        ref_logits = ref.step(k, v, pos, token, int8_path=True)
-        rel = _rel(logits, ref_logits)
-        assert rel <= 5e-3, (i, rel)
+        P.check_step(gpu_ctx, ref, model, c, k, v, pos, token, logits, nxt, f"step {i}")
         token = nxt
+    gpu_ctx.set_q8_trace(None)
     assert dec.position == past + n + 3
     dec.close()
 
@@ -225,8 +228,8 @@ MIXED = dict(SMALL, ffn=6144)  # 24 groups: the down projection runs as three K 
 @pytest.mark.parametrize("linear,down", [(Q4_K, Q6_K), (Q8_0, Q8_0), (Q6_K, Q6_K)])
 def test_mixed_formats_prefill_and_decode(gpu_ctx, hyq, oracle, linear, down):
     """The Q4_K_M mix (Q4_K linears, Q6_K down) and single-format Q8_0 / Q6_K
-    models: prefill within 1e-2 and the following decode steps within 5e-3
-    (on the GPU's own cache) of the oracle."""
+    models: prefill within 1e-2 and the following decode steps within 1e-4
+    (on the GPU's own cache and int8 codes) of the oracle."""
     c = MIXED
     _print("mixed", linear, down)
     model = make_dense_model(c, linear=linear, down=down, seed=31)
@@ -240,15 +243,17 @@ def test_mixed_formats_prefill_and_decode(gpu_ctx, hyq, oracle, linear, down):
     _print("  prefill rel", rel)
     assert rel <= 1e-2, rel
     kvw = c["kv_heads"] * c["head_dim"]
+    gpu_ctx.set_q8_trace(1 << 20)
     for i in range(2):
         pos = past + n + i
         kc = np.zeros((c["layers"], context, kvw), np.float32)
         vc = np.zeros_like(kc)
         for l in range(c["layers"]):
             kc[l, :pos], vc[l, :pos] = dec.read_kv(l, pos)
+        gpu_ctx.clear_q8_trace()
         step_logits, nxt = dec.forward(token)
-        rel = _rel(step_logits, ref.step(kc, vc, pos, token, int8_path=True))
-        _print("  step", i, "rel", rel)
-        assert rel <= 5e-3, (i, rel)
+        P.check_step(gpu_ctx, ref, model, c, kc, vc, pos, token, step_logits, nxt,
+                     f"mixed step {i}")
         token = nxt
+    gpu_ctx.set_q8_trace(None)
     dec.close()
