@@ -10,16 +10,16 @@ whole forward pass plus argmax); warmup W and timed K steps run at positions
 1024 .. 1024+W+K-1 (128 positions at the defaults).
 
 Also reported, from live HIP-event timings on the context stream:
-  roofline        the kernel with the largest time share of a decode step (the
-                  Q2_0C GEMV with its f32 input stage that the step runs for the
-                  attention output and, as three K slices, for the down
-                  projection), launched alone through the C ABI as the very
-                  instantiation the step launches, on the attention-output
-                  shape [2048 x 2048], weights rotated over 1 GiB and inputs
-                  over 64 rows so that both come from HBM:
-                  algorithmic bytes per launch / average launch time; `traffic`
-                  is the counter-measured HBM bytes per launch of the same
-                  kernel (profiles/*_traffic.json);
+  roofline        the kernel with the largest time share of a decode step among
+                  those decode_kernels times as the very instantiation the step
+                  launches (the step's attention launch: RoPE, q/k norms, KV
+                  append and split softmax partials over the 1032 cached
+                  positions, K/V rotated over 64 layer caches so that they come
+                  from HBM), launched alone through the C ABI: algorithmic bytes
+                  per launch / average launch time (HIP events on the context
+                  stream); `traffic` and `fetch_bytes` are the counter-measured
+                  HBM bytes per launch of the same kernel
+                  (profiles/*_traffic.json);
   step_hbm        the bytes a token streams (weights + KV cache) / time per token;
   device_copy_GBs (in roofline) a 1 GiB device-to-device copy's read + write
                   bytes / time;
@@ -27,11 +27,18 @@ Also reported, from live HIP-event timings on the context stream:
                   practical ceiling of the HBM-bound (read-dominated) kernels;
   decode_kernels  the step's other kernels timed the same way;
   gemv            GB/s of every matrix of the GEMV workloads (Q4_K [6144x2048];
-                  the 1.8B Q2_0C/STQ1_0 set; Q6_K lm_head; the 7B shapes), Q8
-                  input, weights rotated over >= 1 GiB of distinct copies:
+                  the 1.8B Q2_0C/STQ1_0 set; Q6_K lm_head; the 7B shapes, and
+                  the 7B gate/up pair as the step launches it: one fused
+                  SiLU launch of both [14336 x 4096] matrices), Q8 input,
+                  weights rotated over >= 1 GiB of distinct copies:
                   back-to-back launches, and (graph_GBs) one HIP graph that
-                  launches every copy once; for STQ1_0 the synthetic codes'
-                  measured zero fraction;
+                  launches every copy once, each beside a read-only launch of
+                  the same bytes; for STQ1_0 the synthetic codes' measured zero
+                  fraction;
+  decode_models   the same decode measurement for the 1.8B 1.25Bit (STQ1_0)
+                  model and a 7B Q4_K_M model (hidden 4096, 32/8 heads, FFN
+                  14336, Q4_K linears, Q6_K down and tied embedding/lm_head of
+                  128167 rows): tok/s and step_hbm;
   prefill, moe    the batched f16-MFMA GEMM (TFLOP/s) and the MoE expert layer;
                   mfma_ceiling (in prefill) the sustained rate of back-to-back
                   independent f16 MFMAs on every CU: the practical ceiling of
@@ -144,6 +151,70 @@ def gemv_rate(hyq, ctx, ev, dtype, rows, cols, seed=1, min_bytes=ROTATE_BYTES, g
         W.release()
     agg = alg * copies / (gms * 1e-3) / 1e9 if gms else None
     return ms * 1e3, alg / (ms * 1e-3) / 1e9, agg, copies, alg
+
+
+def gemv_silu_rate(hyq, ctx, ev, dtype, rows, cols, seed=1, min_bytes=ROTATE_BYTES):
+    """The fused gate/up launch of a decode step (GEMV_SILU: gate and up
+    [rows x cols] each, y = silu(gate x) * (up x), Weight::
+    matmul_gate_up_silu_fast) with Q8 input, over >= 1 GiB of distinct weight
+    pairs: (us per launch, algorithmic GB/s, algorithmic bytes)."""
+    from synth import random_matrix
+    g = random_matrix(dtype, rows, cols, seed=seed)
+    u = random_matrix(dtype, rows, cols, seed=seed + 1)
+    pairs = int(min(1024, max(2, np.ceil(min_bytes / (2 * g.size)))))
+    Gs = [ctx.upload(dtype, g, (cols, rows)) for _ in range(pairs)]
+    Us = [ctx.upload(dtype, u, (cols, rows)) for _ in range(pairs)]
+    x = np.random.default_rng(seed).normal(0, 1, cols).astype(np.float32)
+    q8 = ctx.q8(cols)
+    xd = ctx.array(x)
+    q8.quantize_into(xd.ptr)
+    y = ctx.empty(rows, np.float32)
+    L = hyq.lib()
+
+    def launch(i):
+        L.hyq_gate_up_silu_q8_d(ctx.handle, Gs[i % pairs].handle, Us[i % pairs].handle,
+                                q8.handle, y.ptr)
+
+    ms = ev.time_ms(launch, max(64, 2 * pairs))
+    alg = 2 * g.size + cols + 4 * (cols // 256) + 4 * rows
+    for W in Gs + Us:
+        W.release()
+    q8.release()
+    return ms * 1e3, alg / (ms * 1e-3) / 1e9, alg
+
+
+def decode_line(hyq, ctx, model, prefilled, warmup, steps, use_graph, seed=0) -> dict:
+    """Greedy decode of a synthetic dense model: `warmup` untimed steps, then
+    `steps` timed ones (hyq_dense_generate, one HIP graph replay per token,
+    synchronised before it returns) from a KV cache pre-filled with N(0,1) to
+    `prefilled` positions; tok/s and the HBM rate of the bytes a token
+    streams (packed weights, the tied lm_head once, K/V at the mid position)."""
+    from synth import dense_weight_bytes, load_dense, make_kv_cache
+    cfg = model["cfg"]
+    context = prefilled + warmup + steps + 1
+    kv = make_kv_cache(cfg, context, prefilled, seed=seed)
+    dec = load_dense(hyq, ctx, model, context)
+    for l in range(cfg["layers"]):
+        dec.load_kv(l, kv[0][l, :prefilled], kv[1][l, :prefilled])
+    dec.position = prefilled
+    toks = dec.generate(1, warmup, use_graph=use_graph) if warmup else [1]
+    t0 = time.perf_counter()
+    dec.generate(int(toks[-1]), steps, use_graph=use_graph)
+    dt = time.perf_counter() - t0
+    dec.close()
+    tok_s = steps / dt
+    kvw = cfg["kv_heads"] * cfg["head_dim"]
+    mid = prefilled + warmup + steps // 2
+    step_bytes = dense_weight_bytes(model) + cfg["layers"] * 2 * (mid + 1) * kvw * 4
+    return dict(tok_s=round(tok_s, 2), ms_per_token=round(dt / steps * 1e3, 4), steps=steps,
+                warmup=warmup, positions=[prefilled + warmup, prefilled + warmup + steps - 1],
+                step_hbm=dict(bytes_per_token=int(step_bytes),
+                              GBs=round(step_bytes * tok_s / 1e9, 1),
+                              frac=round(step_bytes * tok_s / 1e9 / HBM_PEAK_GBS, 4)))
+
+
+DENSE_7B = dict(layers=32, hidden=4096, heads=32, kv_heads=8, head_dim=128, ffn=14336,
+                vocab=128167, rope_base=11158840.0, rms_eps=1e-5)
 
 
 def stq_zero_fraction(ctx, rows, cols, seed=1, sample=64) -> float:
@@ -485,6 +556,9 @@ def roofline_loop(hyq, ctx, ev, model, kv, pos, iters):
     a, b = ctx.empty(nb, np.uint8), ctx.empty(nb, np.uint8)
     hyq.check(L.hyq_memcpy_d2d(ctx.handle, b.ptr, a.ptr, nb))
     ctx.sync()
+    # every buffer released here, before the context and the process end
+    for d in ks + vs + [qd, kd, vd, qn, kn, freq, posd, scratch, a, b]:
+        d.free()
     return ms * 1e3
 
 
@@ -624,6 +698,9 @@ ONLY = {
     "gemv_stq1_0_gate_up_28672x4096": ("gemv", "STQ1_0", 28672, 4096),
     "gemv_q4k_gate_14336x4096": ("gemv", "Q4_K", 14336, 4096),
     "c5_moe_layer_64tok_top8of64": ("moe", None, 0, 0),
+    "decode_7b_q4km": ("decode", "7B", 0, 0),
+    "decode_1p8b_stq1_0": ("decode", "STQ1_0", 0, 0),
+    "decode_1p8b_q2c": ("decode", "Q2_0C", 0, 0),
 }
 
 
@@ -636,6 +713,8 @@ def main() -> int:
     ap.add_argument("--no-gemv", action="store_true", help="skip the standalone GEMV table")
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the batched (prefill) GEMM table")
+    ap.add_argument("--no-models", action="store_true",
+                    help="skip the 1.8B 1.25Bit and 7B Q4_K_M decode lines")
     ap.add_argument("--roofline-only", action="store_true",
                     help="run only the roofline kernel loop and a 256 MiB copy (for hardware "
                          "counter runs), print its time and exit")
@@ -652,8 +731,8 @@ def main() -> int:
               "(the path has no multi-GPU runtime in this build)", file=sys.stderr)
         return 2
     import __graft_entry__ as ge
-    from synth import DENSE_1P8B, Q2_0C, Q4_K, Q6_K, STQ1_0, dense_weight_bytes, load_dense, \
-        make_dense_model, make_kv_cache
+    from synth import DENSE_1P8B, NAMES, Q2_0C, Q4_K, Q6_K, STQ1_0, dense_weight_bytes, \
+        load_dense, make_dense_model, make_kv_cache
 
     hyq = ge.package()
     if args.only:
@@ -665,6 +744,13 @@ def main() -> int:
             m = moe_rate(hyq, ctx, ev)
             print(json.dumps({"kernel": args.only, "avg_us": m["us"], "GBs": m["GBs"]}),
                   flush=True)
+        elif kind == "decode":
+            mcfg, lin, down = ((DENSE_7B, Q4_K, Q6_K) if dt_name == "7B" else
+                               (DENSE_1P8B, STQ1_0 if dt_name == "STQ1_0" else Q2_0C, None))
+            m = make_dense_model(mcfg, linear=lin, embed=Q6_K, seed=2, down=down)
+            r = decode_line(hyq, ctx, m, PREFILLED, args.warmup, args.steps,
+                            not args.no_graph, seed=2)
+            print(json.dumps({"decode": args.only, **r}), flush=True)
         elif kind == "gemm":
             us, tf = prefill_rate(hyq, ctx, ev, dt_, rows, cols, 512)
             print(json.dumps({"kernel": args.only, "avg_us": round(us, 3),
@@ -686,8 +772,9 @@ def main() -> int:
     if args.roofline_only:
         us = roofline_loop(hyq, ctx, ev, model, kv, PREFILLED + args.warmup,
                            max(args.steps, 64))
-        print(json.dumps({"kernel": "attention", "avg_us": round(us, 3)}), flush=True)
         ctx.close()
+        assert ev.hip.hipDeviceSynchronize() == 0
+        print(json.dumps({"kernel": "attention", "avg_us": round(us, 3)}), flush=True)
         return 0
     dec = load_dense(hyq, ctx, model, context)
     for l in range(cfg["layers"]):
@@ -708,14 +795,17 @@ def main() -> int:
               key=lambda n: table[n]["us_per_step"])
     dk = table[dom]
     achieved = dk["bytes"] / (dk["us"] * 1e-6) / 1e9
-    traffic = None
+    traffic, fetch = None, None
     tf = os.path.join(ROOT, "profiles", f"{ROOFLINE_PROFILE}_traffic.json")
     if os.path.exists(tf):
         with open(tf) as f:
-            traffic = json.load(f).get("bytes_per_launch")
+            rec = json.load(f)
+        traffic = rec.get("bytes_per_launch")
+        fetch = rec.get("fetch_bytes_per_launch")
     roofline = dict(kernel=f"{dom}: {dk['launch']}", bound="hbm", achieved=round(achieved, 1),
                     peak=HBM_PEAK_GBS, unit="GB/s", frac=round(achieved / HBM_PEAK_GBS, 4),
-                    traffic=traffic, algorithmic_bytes=dk["bytes"], avg_us=dk["us"])
+                    traffic=traffic, fetch_bytes=fetch, algorithmic_bytes=dk["bytes"],
+                    avg_us=dk["us"])
     copy = copy_rate(hyq, ctx, ev)
     roofline["device_copy_GBs"] = copy["GBs"]
     ceiling = read_ceiling(hyq, ctx, ev)
@@ -765,6 +855,19 @@ def main() -> int:
             log(f"{name}: {us:.2f} us {gbs:.0f} GB/s; graph of {copies} copies "
                 f"{agg or 0:.0f} GB/s; a read-only launch of the same bytes {ceil['us']:.2f} us "
                 f"{ceil['GBs']:.0f} GB/s")
+        # the 7B gate/up product as a decode step launches it: one fused
+        # launch of both [14336 x 4096] matrices and the SiLU epilogue
+        for name, dt_ in {"7B_Q4_K_gate_up_silu_2x14336x4096": Q4_K,
+                          "7B_Q2_0C_gate_up_silu_2x14336x4096": Q2_0C,
+                          "7B_STQ1_0_gate_up_silu_2x14336x4096": STQ1_0}.items():
+            us, gbs, alg = gemv_silu_rate(hyq, ctx, ev, dt_, 14336, 4096)
+            ceil = sized_read_ceiling(hyq, ctx, ev, alg)
+            gemv[name] = dict(us=round(us, 3), GBs=round(gbs, 1),
+                              frac=round(gbs / HBM_PEAK_GBS, 4), bytes=int(alg),
+                              read_ceiling_same_bytes=ceil,
+                              of_read_ceiling=round(gbs / ceil["GBs"], 4))
+            log(f"{name}: {us:.2f} us {gbs:.0f} GB/s; a read-only launch of the same bytes "
+                f"{ceil['us']:.2f} us {ceil['GBs']:.0f} GB/s")
 
     prefill = {}
     if not args.no_prefill:
@@ -797,6 +900,29 @@ def main() -> int:
         log(f"C5 MoE layer (64 tokens, top-8 of 64 Q4_K experts + Q8_0 shared): "
             f"{moe['us']:.1f} us {moe['GBs']:.0f} GB/s")
 
+    # the other decode workloads the reference publishes CPU rates for
+    # (docs/validation.md:68,72): the 1.8B 1.25Bit (STQ1_0) model and the 7B
+    # Q4_K_M mix (Q4_K linears, Q6_K down and tied Q6_K embedding/lm_head)
+    models = {}
+    if not args.no_models:
+        for name, (mcfg, lin, down, ref_tok_s) in {
+            "1.8B_1.25Bit_STQ1_0": (cfg, STQ1_0, None, 99.32),
+            "7B_Q4_K_M": (DENSE_7B, Q4_K, Q6_K, 2.96),
+        }.items():
+            log(f"building the synthetic {name} model")
+            m = make_dense_model(mcfg, linear=lin, embed=Q6_K, seed=2, down=down)
+            models[name] = decode_line(hyq, ctx, m, PREFILLED, args.warmup, args.steps,
+                                       use_graph, seed=2)
+            models[name]["config"] = dict(mcfg, linear=NAMES[lin], down=NAMES[down or lin],
+                                          embed="Q6_K (tied)")
+            models[name]["reference_published"] = dict(
+                value=ref_tok_s, unit="tok/s",
+                note="Apple M2 Pro 8 threads, real weights (docs/validation.md); not this config")
+            del m
+            log(f"decode {name}: {models[name]['tok_s']:.1f} tok/s "
+                f"({models[name]['ms_per_token']:.3f} ms/token), "
+                f"{models[name]['step_hbm']['GBs']:.0f} GB/s of a token's bytes")
+
     cpu, cpus = None, None
     if not args.no_cpu:
         log("cpu baselines")
@@ -822,6 +948,7 @@ def main() -> int:
         "step_hbm": step,
         "decode_kernels": table,
         "gemv": gemv,
+        "decode_models": models,
         "prefill": prefill,
         "prefill_1p8b": pf,
         "moe": moe,

@@ -191,6 +191,9 @@ class Context:
         self.device = device
         # objects that use the context's stream (decoders): closed first
         self._dependents = weakref.WeakSet()
+        # device buffers allocated through the context: freed by close(), so
+        # that none is left to the HIP runtime's own teardown at process exit
+        self._buffers = weakref.WeakSet()
         self._q8trace = None
 
     @property
@@ -201,9 +204,17 @@ class Context:
         check(lib().hyq_sync(self.handle))
 
     def close(self) -> None:
+        """Closes the decoders on the context, synchronises its stream, frees
+        every device buffer allocated through it, then destroys it."""
         if self.handle:
             for d in list(self._dependents):
                 d.close()
+            check(lib().hyq_sync(self.handle))
+            if self._q8trace is not None:
+                check(lib().hyq_ctx_set_q8_trace(self.handle, None, 0))
+            for b in list(self._buffers):
+                b.free()
+            self._q8trace = None
             lib().hyq_ctx_destroy(self.handle)
             self.handle = None
 
@@ -286,6 +297,7 @@ class DeviceArray:
         h = P()
         check(lib().hyq_device_alloc(ctx.handle, self.nbytes, ctypes.byref(h)))
         self.ptr = h.value
+        ctx._buffers.add(self)
 
     @classmethod
     def from_host(cls, ctx: Context, a: np.ndarray) -> "DeviceArray":
