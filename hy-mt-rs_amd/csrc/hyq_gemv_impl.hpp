@@ -213,6 +213,74 @@ __device__ __forceinline__ void stage_regs(const GemvArgs &a, StageRegs &r, int 
     }
 }
 
+// IN 3: IN 2 whose partial rows span two passes (rows of 9-16 groups: a
+// 4096-wide QKV input after a K-split down projection), so that they stay in
+// registers instead of taking the loop below; its own instantiation, so
+// the other stages keep their registers and code.
+constexpr int STAGE3_PASSES = 2;
+struct StageRegs3 {
+    float4 x[STAGE3_PASSES][2];
+    float4 w[STAGE3_PASSES][2];
+    float4 pt[GEMV_MAX_PARTS][STAGE3_PASSES][2];
+};
+
+__device__ __forceinline__ void stage_load3(const GemvArgs &a, const float *xin, const float *norm,
+                                            StageRegs3 &r)
+{
+    const int hw = threadIdx.x >> 5, c = threadIdx.x & 31;
+    const float4 *x4 = reinterpret_cast<const float4 *>(xin);
+    const float4 *n4 = reinterpret_cast<const float4 *>(norm);
+#pragma unroll
+    for (int p = 0; p < STAGE3_PASSES; ++p) {
+        const int g = 8 * p + hw;
+        if (g < a.groups) {
+            r.x[p][0] = x4[g * 64 + 2 * c];
+            r.x[p][1] = x4[g * 64 + 2 * c + 1];
+            r.w[p][0] = n4[g * 64 + 2 * c];
+            r.w[p][1] = n4[g * 64 + 2 * c + 1];
+#pragma unroll
+            for (int k = 0; k < GEMV_MAX_PARTS; ++k)
+                if (k < a.nsparts) {
+                    const float4 *p4 =
+                        reinterpret_cast<const float4 *>(a.sparts + (size_t)k * a.parts_stride);
+                    r.pt[k][p][0] = p4[g * 64 + 2 * c];
+                    r.pt[k][p][1] = p4[g * 64 + 2 * c + 1];
+                }
+        }
+    }
+}
+
+__device__ __forceinline__ void stage_regs3(const GemvArgs &a, StageRegs3 &r, int *slots,
+                                            float *sc, int *s256, int *s16, int *s32, float *gss,
+                                            float *xt)
+{
+    const int hw = threadIdx.x >> 5, c = threadIdx.x & 31;
+    const int groups = a.groups;
+#pragma unroll
+    for (int p = 0; p < STAGE3_PASSES; ++p) {
+        const int g = 8 * p + hw;
+        if (g < groups) {
+#pragma unroll
+            for (int k = 0; k < GEMV_MAX_PARTS; ++k)
+                if (k < a.nsparts) {
+                    r.x[p][0] = add4(r.x[p][0], r.pt[k][p][0]);
+                    r.x[p][1] = add4(r.x[p][1], r.pt[k][p][1]);
+                }
+            const float ss = sum_rows(wave::sum16(sq8(r.x[p][0], r.x[p][1])));
+            if (c == 0) gss[g] = ss;
+        }
+    }
+    const float scale = finish_norm(gss, groups, a.eps);
+#pragma unroll
+    for (int p = 0; p < STAGE3_PASSES; ++p) {
+        const int g = 8 * p + hw;
+        if (g < groups)
+            quantize_half(scale_by(r.x[p][0], scale, r.w[p][0]),
+                          scale_by(r.x[p][1], scale, r.w[p][1]), g, c, slots, sc, s256, s16, s32,
+                          xt);
+    }
+}
+
 // Longer rows: a loop over the passes (loads at the top of each).
 template <int IN>
 __device__ __forceinline__ void stage_loop(const GemvArgs &a, const float *xin, const float *norm,
@@ -377,6 +445,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     // of its groups at once; otherwise the first group is preloaded and the
     // others load at the top of their iteration.
     StageRegs sr;
+    StageRegs3 sr3;
     // int4 loads per thread: a preloading kernel covers at most GSTEP * P
     // groups (16 int4 each) with 64 threads (256 in the 32- and 64-lane
     // forms), so it issues no more than those need (the surplus would re-read
@@ -384,9 +453,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
     constexpr int QW = SL >= 32 ? 4 : 1;
     constexpr int NQ = P > 0 && GSTEP * P / (4 * QW) < Q8_REG ? GSTEP * P / (4 * QW) : Q8_REG;
     i32x4 qv[NQ];
-    const bool stage_reg = IN != 0 && groups <= 8 * STAGE_PASSES && (a.nsparts == 0 || groups <= 8);
+    const bool stage_reg =
+        IN == 3 ? groups <= 8 * STAGE3_PASSES
+                : IN != 0 && groups <= 8 * STAGE_PASSES && (a.nsparts == 0 || groups <= 8);
     const bool q8_reg = IN == 0 && groups * 16 <= NQ * (int)blockDim.x;
-    if (IN != 0 && stage_reg) stage_load<IN>(a, xin, a.norm, sr);
+    if constexpr (IN == 3) {
+        if (stage_reg) stage_load3(a, xin, a.norm, sr3);
+    } else if (IN != 0 && stage_reg) {
+        stage_load<IN>(a, xin, a.norm, sr);
+    }
     if (IN == 0 && q8_reg) {
         // clamped into bounds; the copy to LDS keeps the in-range ones
         const i32x4 *src = reinterpret_cast<const i32x4 *>(a.x.q);
@@ -453,8 +528,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
         float *xt = a.q8t_x && blockIdx.x == 0
                         ? a.q8t_x + (size_t)(SLOT ? (int)blockIdx.y * groups : gbase) * 256
                         : nullptr;
-        if (stage_reg) stage_regs<IN>(a, sr, lds, sc, s256, s16, s32, gss, xt);
-        else stage_loop<IN>(a, xin, a.norm, lds, sc, s256, s16, s32, gss, xt);
+        if constexpr (IN == 3) {
+            if (stage_reg) stage_regs3(a, sr3, lds, sc, s256, s16, s32, gss, xt);
+            else stage_loop<2>(a, xin, a.norm, lds, sc, s256, s16, s32, gss, xt);
+        } else {
+            if (stage_reg) stage_regs<IN>(a, sr, lds, sc, s256, s16, s32, gss, xt);
+            else stage_loop<IN>(a, xin, a.norm, lds, sc, s256, s16, s32, gss, xt);
+        }
     }
     __syncthreads();
     if constexpr (IN != 0) {
@@ -793,13 +873,20 @@ template <int F> int launch_gemv_format(int mode, const GemvArgs &a, void *strea
         return (int)hipGetLastError();
     }
     if (!a.xin) return launch_in<F, 0, false>(mode, nr, pre, a, grid, block, lds, st);
+    // the fused QKV launch with an RMSNorm stage over 9-16 groups that adds
+    // partial rows: IN 3 keeps them in registers for both passes
+    const bool two_pass_parts =
+        mode == GEMV_MULTI && nr == 1 && a.nsparts > 0 && a.groups > 8 && a.groups <= 16;
     if constexpr (HasHalf<F>::value) {
         if (half) {
             if (!a.norm) return launch_in<F, 1, true>(mode, nr, pre, a, grid, block, lds, st);
+            if (two_pass_parts)
+                return launch_nr<F, GEMV_MULTI, 3, true>(1, 0, a, grid, block, lds, st);
             return launch_in<F, 2, true>(mode, nr, pre, a, grid, block, lds, st);
         }
     }
     if (!a.norm) return launch_in<F, 1, false>(mode, nr, pre, a, grid, block, lds, st);
+    if (two_pass_parts) return launch_nr<F, GEMV_MULTI, 3, false>(1, 0, a, grid, block, lds, st);
     return launch_in<F, 2, false>(mode, nr, pre, a, grid, block, lds, st);
 }
 

@@ -31,7 +31,7 @@ import numpy as np
 import pytest
 
 import q8_proof as P
-from synth import (DENSE_1P8B, Q2_0C, Q6_K, load_dense, make_dense_model, make_kv_cache,
+from synth import (DENSE_1P8B, Q2_0C, Q4_K, Q6_K, load_dense, make_dense_model, make_kv_cache,
                    random_matrix)
 
 pytestmark = pytest.mark.gpu
@@ -155,6 +155,45 @@ def test_c3_full_model_matches_oracle(gpu_ctx, hyq, oracle):
     dec.position = prefilled
     got = dec.generate(5, 4, use_graph=True)
     assert list(got) == toks, (list(got), toks)
+    dec.close()
+
+
+SHAPES_7B = dict(layers=2, hidden=4096, heads=32, kv_heads=8, head_dim=128, ffn=14336,
+                 vocab=4096, rope_base=11158840.0, rms_eps=1e-5)
+
+
+def test_7b_shapes_layers_match_oracle(gpu_ctx, hyq, oracle):
+    """Two layers at the 7B Q4_K_M shapes (hidden 4096, 32/8 heads of 128,
+    FFN 14336; Q4_K linears, Q6_K down and output): the down projection runs
+    as four K slices of 14 groups, and the next layer's QKV input stage adds
+    their partial rows over 16 groups (the two-pass register stage); the
+    gate/up pair has two groups per lane. Cache pre-filled to 80 of 96
+    positions; three tokens, each layer by layer and free-running, on the
+    GPU's codes (1e-4)."""
+    cfg = SHAPES_7B
+    context, prefilled = 96, 80
+    model = make_dense_model(cfg, linear=Q4_K, embed=Q6_K, seed=3, down=Q6_K)
+    model["output"] = random_matrix(Q6_K, cfg["vocab"], cfg["hidden"], 53)
+    dec = load_dense(hyq, gpu_ctx, model, context)
+    k, v = make_kv_cache(cfg, context, prefilled, seed=3)
+    for l in range(cfg["layers"]):
+        dec.load_kv(l, k[l, :prefilled], v[l, :prefilled])
+    dec.position = prefilled
+    ref = oracle.DenseOracle(model)
+    dec.set_trace(1)
+    gpu_ctx.set_q8_trace(TRACE_BYTES)
+    token = 9
+    for i in range(3):
+        pos = prefilled + i
+        gpu_ctx.clear_q8_trace()
+        logits, nxt = dec.forward(token)
+        stages, final = P.split_step_records(gpu_ctx.q8_trace(), ref, cfg["layers"])
+        _teacher_forced_step(ref, dec, stages, final, cfg, pos, logits, f"7b step {i}")
+        _free_running(ref, model, cfg, k, v, pos, token, stages, final, logits, nxt,
+                      f"7b step {i}")
+        token = nxt
+    gpu_ctx.set_q8_trace(None)
+    dec.set_trace(None)
     dec.close()
 
 
