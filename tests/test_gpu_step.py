@@ -398,6 +398,62 @@ def test_attention_rope_fused(gpu_ctx, hyq, oracle, pos, norm_first):
     assert np.allclose(out2.numpy(), got, rtol=2e-5, atol=2e-6)
 
 
+@pytest.mark.parametrize("kvh,pos", [(4, 0), (4, 31), (4, 32), (4, 1032), (4, 1151), (8, 700),
+                                     (1, 500)])
+def test_attention_rope_positions_and_repeats(gpu_ctx, hyq, oracle, kvh, pos):
+    """hyq_attention_rope_d with its merge at positions that end a split
+    (31), start one (32), fill one row (0) and the bench's positions, on 1,
+    4 and 8 KV heads: repeated 40 times on the same inputs (the append
+    rewrites the same row), every output is bit-identical to the first, and
+    it agrees with the oracle's attention (1 to 36 splits)."""
+    heads, D, ctxlen = 4 * kvh, 128, 1152
+    base, eps = 11158840.0, 1e-5
+    rng = np.random.default_rng(pos + kvh)
+    qn = rng.normal(1, 0.02, D).astype(np.float32)
+    kn = rng.normal(1, 0.02, D).astype(np.float32)
+    kc = rng.normal(0, 1, (ctxlen, kvh * D)).astype(np.float32)
+    vc = rng.normal(0, 1, (ctxlen, kvh * D)).astype(np.float32)
+    q = rng.normal(0, 1, heads * D).astype(np.float32)
+    k = rng.normal(0, 1, kvh * D).astype(np.float32)
+    v = rng.normal(0, 1, kvh * D).astype(np.float32)
+    freq = np.array([np.float32(base) ** np.float32(-2.0 * j / D) for j in range(64)],
+                    np.float32)
+    d = {n: gpu_ctx.array(a) for n, a in dict(q=q, k=k, v=v, qn=qn, kn=kn, freq=freq, kc=kc,
+                                               vc=vc, pos=np.array([pos], np.int32)).items()}
+    L = hyq.lib()
+    scratch = gpu_ctx.empty(L.hyq_attention_scratch_floats(ctxlen, heads), np.float32)
+    out = gpu_ctx.empty(heads * D, np.float32)
+    first = None
+    for i in range(40):
+        hyq.check(L.hyq_attention_rope_d(gpu_ctx.handle, d["q"].ptr, d["k"].ptr, d["v"].ptr,
+                                         d["qn"].ptr, d["kn"].ptr, d["freq"].ptr, d["pos"].ptr,
+                                         ctxlen, heads, kvh, D, _f(eps), 0, d["kc"].ptr,
+                                         d["vc"].ptr, scratch.ptr, out.ptr))
+        got = out.numpy()
+        if first is None:
+            first = got
+        assert np.array_equal(got.view(np.uint32), first.view(np.uint32)), (i, pos)
+    O = oracle.lib()
+    c = np.empty(64, np.float32)
+    sn = np.empty(64, np.float32)
+    O.hyqo_rope_tables(128, _f(base), pos, c.ctypes.data, sn.ctypes.data)
+
+    def rot(x, n, w):
+        x = x.copy()
+        O.hyqo_rope(x.ctypes.data, n, 128, c.ctypes.data, sn.ctypes.data)
+        O.hyqo_rms_norm_rows(x.ctypes.data, w.ctypes.data, x.size, 128, _f(eps), 1)
+        return x
+    kc_ref = kc.copy()
+    kc_ref[pos] = rot(k, kvh, kn)
+    vc_ref = vc.copy()
+    vc_ref[pos] = v
+    ref = np.empty(heads * D, np.float32)
+    q_ref = rot(q, heads, qn)  # (kept alive across the call that reads it)
+    O.hyqo_attention(q_ref.ctypes.data, kc_ref.ctypes.data, vc_ref.ctypes.data, heads, kvh, D,
+                     pos + 1, ref.ctypes.data)
+    assert np.allclose(first, ref, rtol=2e-5, atol=2e-6), np.abs(first - ref).max()
+
+
 def test_attention_rope_position_at_context_appends_nothing(gpu_ctx, hyq):
     """A device position equal to `context` (which the library cannot check
     on the host) must not be appended past the caches' `context` rows. The
