@@ -343,7 +343,10 @@ def prefill_e2e(dec, cfg, tokens: int, runs: int = 3) -> dict:
 def moe_rate(hyq, ctx, ev, tokens=64, experts=64, used=8, hidden=2048, mid=1536, seed=5):
     """MoE layer at 30B-A3B-style shapes: the dense Q8_0 shared projection
     [2048x2048] seeds the output (batched matmul), then the Q4_K expert loop
-    (softmax top-8 routing of N(0,1) logits, weights renormalized)."""
+    (softmax top-8 routing of N(0,1) logits, weights renormalized).
+    hyq_moe_shared_experts_d runs the shared product inside the expert
+    launches (`us`); `us_two_calls` times hyq_matmul_d then
+    hyq_moe_experts_d."""
     from synth import Q4_K, Q8_0, random_matrix
     rng = np.random.default_rng(seed)
     G = ctx.upload(Q4_K, random_matrix(Q4_K, experts * mid, hidden, seed), (hidden, mid, experts))
@@ -370,18 +373,25 @@ def moe_rate(hyq, ctx, ev, tokens=64, experts=64, used=8, hidden=2048, mid=1536,
     nbytes = L.hyq_moe_scratch_bytes(tokens, len(pt), experts, hidden, mid)
     scratch = ctx.empty(nbytes, np.uint8)
 
-    def launch(i):
+    def sequential(i):
         L.hyq_matmul_d(ctx.handle, S.handle, x.ptr, tokens, out.ptr)
         L.hyq_moe_experts_d(ctx.handle, G.handle, U.handle, D.handle, x.ptr, tokens, ptd.ptr,
                             ped.ptr, pwd.ptr, len(pt), scratch.ptr, nbytes, out.ptr)
 
-    ms = ev.time_ms(launch, 20)
+    def layer(i):
+        L.hyq_moe_shared_experts_d(ctx.handle, S.handle, G.handle, U.handle, D.handle, x.ptr,
+                                   tokens, ptd.ptr, ped.ptr, pwd.ptr, len(pt), scratch.ptr,
+                                   nbytes, out.ptr)
+
+    ms_seq = ev.time_ms(sequential, 20)
+    ms = ev.time_ms(layer, 20)
     touched = len(set(pe))
     wbytes = touched * (2 * mid * hidden // 256 * 144 + hidden * mid // 256 * 144) + \
         hidden * hidden // 32 * 34
     for w in (G, U, D, S):
         w.release()
-    return dict(us=round(ms * 1e3, 2), experts_touched=touched, weight_bytes=wbytes,
+    return dict(us=round(ms * 1e3, 2), us_two_calls=round(ms_seq * 1e3, 2),
+                experts_touched=touched, weight_bytes=wbytes,
                 GBs=round(wbytes / (ms * 1e-3) / 1e9, 1),
                 frac=round(wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
 
@@ -742,8 +752,8 @@ def main() -> int:
         dt_ = dict(Q4_K=Q4_K, Q6_K=Q6_K, STQ1_0=STQ1_0, Q2_0C=Q2_0C).get(dt_name)
         if kind == "moe":
             m = moe_rate(hyq, ctx, ev)
-            print(json.dumps({"kernel": args.only, "avg_us": m["us"], "GBs": m["GBs"]}),
-                  flush=True)
+            print(json.dumps({"kernel": args.only, "avg_us": m["us"], "GBs": m["GBs"],
+                              "two_calls_us": m["us_two_calls"]}), flush=True)
         elif kind == "decode":
             mcfg, lin, down = ((DENSE_7B, Q4_K, Q6_K) if dt_name == "7B" else
                                (DENSE_1P8B, STQ1_0 if dt_name == "STQ1_0" else Q2_0C, None))

@@ -69,6 +69,7 @@ SIGNATURES = {
     "hyq_moe_scratch_bytes": (SZ, [SZ, SZ, SZ, SZ, SZ]),
     "hyq_moe_experts_d": (I, [P, P, P, P, P, SZ, P, P, P, SZ, P, SZ, P]),
     "hyq_moe_experts": (I, [P, P, P, P, P, SZ, P, P, P, SZ, P]),
+    "hyq_moe_shared_experts_d": (I, [P, P, P, P, P, P, SZ, P, P, P, SZ, P, SZ, P]),
     "hyq_decode_d": (I, [P, I, P, SZ, P, SZ]),
     "hyq_embed_row_d": (I, [P, P, P, P]),
     "hyq_rms_norm_q8_d": (I, [P, P, P, SZ, ctypes.c_float, P, P]),

@@ -16,6 +16,7 @@
 #include <algorithm>
 
 #include "hyq_f16rows.hpp"
+#include "hyq_few_q80.hpp"
 #include "hyq_moe_operand.hpp"
 #include "hyq_tile.hpp"
 #include "hyq_wave.hpp"
@@ -518,19 +519,33 @@ __host__ __device__ inline bool plan_fast_fits(int P, int T, int E)
 // of x [T, K] (wave_row_operand: xop, xhs, xsc), one wave per row, and the
 // plan also writes, per chunk column (ti, col), the pair position it takes
 // (cpos: the chunk's last pair for columns past its pairs) and that pair's
-// token (ctok).
+// token (ctok). With xf given, a second wave per row writes the row's f16
+// fragments for a few-token Q8_0 product (hyq_few_q80.hpp; zeros for the rows
+// past T of the last 16-row chunk), scaled by the same 2^-e (its own
+// maximum of the row): xsc is then that product's row scale too.
 __global__ __launch_bounds__(1024) void moe_plan_fast_kernel(
     const int *__restrict__ ptok, const int *__restrict__ pexp, int P, int T, int E, int *eoff,
     int *order, int *toff, int *tlist, int *tiles, int *ntiles, int chunk,
     const float *__restrict__ x, int K, uint4 *__restrict__ xop, uint2 *__restrict__ xhs,
-    float *__restrict__ xsc, int *__restrict__ cpos, int *__restrict__ ctok)
+    float *__restrict__ xsc, int *__restrict__ cpos, int *__restrict__ ctok,
+    _Float16 *__restrict__ xf)
 {
     const int t = threadIdx.x;
     if (blockIdx.x > 0) {
-        const int r = 16 * (blockIdx.x - 1) + (t >> 6);
-        if (r >= T) return;
-        wave_row_operand(x + (size_t)r * K, K, xop + (size_t)r * (K / 8),
-                         xhs + (size_t)r * (K / 64), xsc + r);
+        // one wave per row, or with xf two: the row operand and the fragments
+        const int w = t >> 6;
+        const int r = (xf ? 8 * (blockIdx.x - 1) + (w >> 1) : 16 * (blockIdx.x - 1) + w);
+        if (!xf || !(w & 1)) {
+            if (r < T)
+                wave_row_operand(x + (size_t)r * K, K, xop + (size_t)r * (K / 8),
+                                 xhs + (size_t)r * (K / 64), xsc + r);
+            return;
+        }
+        const float *xr = r < T ? x + (size_t)r * K : nullptr;
+        const int e = xr ? f16_row_exponent(wave_row_absmax(xr, K)) : 0;
+        const float4 *x4 = reinterpret_cast<const float4 *>(xr);
+        for (int p = t & 63; p < K / 8; p += 64)
+            few::fragment_piece(x4, ldexpf(1.0f, -e), r, p, K, xf);
         return;
     }
     __shared__ int key[PLAN_FAST];
@@ -961,18 +976,44 @@ MoeLayout moe_layout(int tokens, int npairs, int experts, int hidden, int mid)
     L.gpart = take(4 * 2 * (size_t)npairs * mid);
     L.upart = take(4 * 2 * (size_t)npairs * mid);
     L.outp2 = take(4 * (size_t)npairs * hidden);
+    // f16 fragments of the token rows for a fused Q8_0 shared projection
+    L.xf = take(tokens <= FEW_Q80_MAX_TOKENS ? few_q80_operand_bytes(hidden, tokens) : 0);
     L.bytes = off;
     return L;
 }
 
 int moe_plan_max() { return PLAN_MAX; }
 
+namespace {
+
+// Register-operand Q4_K kernels while the pairs average at most one
+// 16-token chunk per expert (weight-bound); the LDS-tiled GEMM otherwise.
+bool few_path(int fmt_gu, int fmt_down, const WView &gate, const WView &up, const WView &down,
+              int hidden, int mid, int npairs, int experts)
+{
+    return fmt_gu == Q4_K && fmt_down == Q4_K && moe_q4k_fits(hidden, mid) && gate.p2 && up.p2 &&
+           down.p2 && npairs <= moe_q4k_chunk() * experts;
+}
+
+} // namespace
+
+bool moe_fuses_shared(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int hidden,
+                      int mid, int tokens, int npairs, int experts)
+{
+    return npairs > 0 && tokens >= 2 && few_path(fmt_gu, fmt_down, gate, up, down, hidden, mid, npairs, experts) &&
+           plan_fast_fits(npairs, tokens, experts) && few_q80_fits(hidden, hidden, tokens);
+}
+
 int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int hidden, int mid,
                const float *x, int tokens, const int *ptok, const int *pexp, const float *pw,
                int npairs, int experts, uint8_t *scratch, const MoeLayout &L, float *out,
-               void *stream)
+               void *stream, const WView *shared)
 {
     if (hidden % BK || mid % BK || hidden % 4 || tokens > PLAN_MAX || experts > PLAN_MAX)
+        return (int)hipErrorInvalidValue;
+    if (shared && (shared->rows != hidden ||
+                   !moe_fuses_shared(fmt_gu, fmt_down, gate, up, down, hidden, mid, tokens,
+                                     npairs, experts)))
         return (int)hipErrorInvalidValue;
     hipStream_t st = (hipStream_t)stream;
     int *eoff = (int *)(scratch + L.eoff), *order = (int *)(scratch + L.order);
@@ -984,10 +1025,7 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
     float *h32 = (float *)(scratch + L.h32), *outp = (float *)(scratch + L.outp);
     if (npairs == 0) return 0;
 
-    // Register-operand Q4_K kernels while the pairs average at most one
-    // 16-token chunk per expert (weight-bound); the LDS-tiled GEMM otherwise.
-    const bool few = fmt_gu == Q4_K && fmt_down == Q4_K && moe_q4k_fits(hidden, mid) &&
-                     gate.p2 && up.p2 && down.p2 && npairs <= moe_q4k_chunk() * experts;
+    const bool few = few_path(fmt_gu, fmt_down, gate, up, down, hidden, mid, npairs, experts);
     // (the few-token kernels take the token rows' largest magnitudes from the
     // plan's launch)
     const bool fast = plan_fast_fits(npairs, tokens, experts);
@@ -995,12 +1033,14 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
     uint2 *xhs = (uint2 *)(scratch + L.xhs);
     float *xsc = (float *)(scratch + L.xsc);
     int *cpos = (int *)(scratch + L.cpos), *ctok = (int *)(scratch + L.ctok);
+    _Float16 *xf = shared ? (_Float16 *)(scratch + L.xf) : nullptr;
     if (fast)
-        hipLaunchKernelGGL(moe_plan_fast_kernel, dim3(few ? 1 + (tokens + 15) / 16 : 1),
+        hipLaunchKernelGGL(moe_plan_fast_kernel,
+                           dim3(few ? 1 + (xf ? 2 : 1) * ((tokens + 15) / 16) : 1),
                            dim3(1024), 0, st, ptok, pexp, npairs, tokens, experts, eoff, order,
                            toff, tlist, tiles, ntiles, few ? moe_q4k_chunk() : BN,
                            few ? x : nullptr, hidden, xop, xhs, xsc, few ? cpos : nullptr,
-                           ctok);
+                           ctok, xf);
     else if (npairs <= PLAN_SMALL && tokens <= PLAN_SMALL && experts <= PLAN_SMALL)
         hipLaunchKernelGGL(moe_plan_small_kernel, dim3(1), dim3(256), 0, st, ptok, pexp, npairs,
                            tokens, experts, eoff, order, toff, tlist, tiles, ntiles,
@@ -1016,7 +1056,7 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
                                 xsc, cpos, ctok, (float *)(scratch + L.gpart),
                                 (float *)(scratch + L.upart), (uint4 *)(scratch + L.hop),
                                 (uint2 *)(scratch + L.hhs), (float *)(scratch + L.hsc), outp,
-                                outp2, stream);
+                                outp2, stream, shared, xf, out);
         if (rc) return rc;
         hipLaunchKernelGGL(moe_combine_kernel, dim3((hidden + 255) / 256, tokens), dim3(256), 0,
                            st, out, hidden, toff, tlist, order, pw, outp,

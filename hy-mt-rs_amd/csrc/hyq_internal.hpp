@@ -219,7 +219,7 @@ int launch_gate_up_f16(int fmt, WView gate, WView up, int cols, const _Float16 *
 // Byte offsets of the MoE scratch regions (hyq_gemm.hip: moe_layout).
 struct MoeLayout {
     size_t eoff, order, rank, toff, tlist, tiles, ntiles, xg, xscale, h32, h, hscale, outp;
-    size_t xop, xhs, xsc, hop, hhs, hsc, cpos, ctok, gpart, upart, outp2, bytes;
+    size_t xop, xhs, xsc, hop, hhs, hsc, cpos, ctok, gpart, upart, outp2, xf, bytes;
     int max_tiles, max_tiles_few;
 };
 MoeLayout moe_layout(int tokens, int npairs, int experts, int hidden, int mid);
@@ -228,7 +228,13 @@ int moe_plan_max();
 int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int hidden, int mid,
                const float *x, int tokens, const int *ptok, const int *pexp, const float *pw,
                int npairs, int experts, uint8_t *scratch, const MoeLayout &L, float *out,
-               void *stream);
+               void *stream, const WView *shared = nullptr);
+// Whether launch_moe takes a Q8_0 shared projection [hidden, hidden] (`shared`)
+// for these shapes: out = x shared^T then the routed sum, the shared product
+// run inside the expert launches (the register-operand path with the
+// single-workgroup plan, 2..FEW_Q80_MAX_TOKENS tokens).
+bool moe_fuses_shared(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int hidden,
+                      int mid, int tokens, int npairs, int experts);
 // The Q4_K register-operand expert kernels (hyq_moe_q4k.hip) after a plan
 // of moe_q4k_chunk()-token chunks. xop/xhs/xsc hold the row operands of the
 // token rows of x and hop/hhs/hsc those of the pairs' SiLU rows
@@ -236,12 +242,16 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
 // token (the column's rows), gpart / upart the gate and up partial rows of
 // the K slices [2][npairs][mid], outp2 the down product's second K slice.
 // have_ops: the plan's launch already wrote xop/xhs/xsc and cpos/ctok.
+// With `shared` (Q8_0, hidden columns, at most FEW_Q80_MAX_TOKENS tokens,
+// have_ops, and the plan's launch given xf) the SiLU-rows launch also runs
+// y = x shared^T on the f16 fragments xf with the row scales xsc.
 int launch_moe_q4k(WView gate, WView up, WView down, int hidden, int mid, const float *x,
                    int tokens, const int *ptok, const int *eoff, const int *valid,
                    const int *order, const int *tiles, const int *ntiles, int max_tiles,
                    int npairs, bool have_ops, uint4 *xop, uint2 *xhs, float *xsc, int *cpos,
                    int *ctok, float *gpart, float *upart, uint4 *hop, uint2 *hhs, float *hsc,
-                   float *outp, float *outp2, void *stream);
+                   float *outp, float *outp2, void *stream, const WView *shared = nullptr,
+                   const _Float16 *xf = nullptr, float *y = nullptr);
 // whether the register-operand kernels take these expert shapes
 bool moe_q4k_fits(int hidden, int mid);
 // K slices of the down product (1 or 2): outp2 is read when 2

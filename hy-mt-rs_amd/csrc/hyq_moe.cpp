@@ -50,6 +50,34 @@ int check_counts(size_t tokens, size_t npairs)
     return HYQ_OK;
 }
 
+int check_device_args(const float *x_d, const float *out_d, const int32_t *pt, const int32_t *pe,
+                      const float *pw, const void *scratch_d)
+{
+    if (!x_d || !out_d || !pt || !pe || !pw || !scratch_d)
+        return fail(HYQ_EINVAL, "moe: null buffer");
+    if ((uintptr_t)x_d % 16 || (uintptr_t)scratch_d % 256)
+        return fail(HYQ_EINVAL, "moe: x must be 16-byte and scratch 256-byte aligned");
+    return HYQ_OK;
+}
+
+// The expert loop on the context's stream (buffers checked); with `shared`
+// (moe_fuses_shared holds) its product seeds out inside the same launches.
+int experts_into(hyq_ctx *ctx, const hyq_weight *gate, const hyq_weight *up,
+                 const hyq_weight *down, const MoeShape &s, const float *x_d, size_t tokens,
+                 const int32_t *pt, const int32_t *pe, const float *pw, size_t npairs,
+                 void *scratch_d, size_t scratch_bytes, float *out_d, const WView *shared)
+{
+    const MoeLayout L =
+        moe_layout((int)tokens, (int)npairs, (int)s.experts, (int)s.hidden, (int)s.mid);
+    if (scratch_bytes < L.bytes)
+        return fail(HYQ_EINVAL, "moe: scratch %zu bytes < %zu", scratch_bytes, L.bytes);
+    HYQ_LAUNCH(launch_moe(gate->dtype, down->dtype, gate->view, up->view, down->view,
+                          (int)s.hidden, (int)s.mid, x_d, (int)tokens, pt, pe, pw, (int)npairs,
+                          (int)s.experts, (uint8_t *)scratch_d, L, out_d, ctx->stream, shared),
+               "moe");
+    return HYQ_OK;
+}
+
 } // namespace
 
 extern "C" {
@@ -72,23 +100,47 @@ int hyq_moe_experts_d(hyq_ctx *ctx, const hyq_weight *gate, const hyq_weight *up
     MoeShape s;
     int rc = check_experts(ctx, gate, up, down, &s);
     if (!rc) rc = check_counts(tokens, npairs);
-    if (rc) return rc;
-    if (npairs == 0) return HYQ_OK;
-    if (!x_d || !out_d || !pair_token_d || !pair_expert_d || !pair_weight_d || !scratch_d)
-        return fail(HYQ_EINVAL, "moe: null buffer");
-    if ((uintptr_t)x_d % 16 || (uintptr_t)scratch_d % 256)
-        return fail(HYQ_EINVAL, "moe: x must be 16-byte and scratch 256-byte aligned");
-    const MoeLayout L =
-        moe_layout((int)tokens, (int)npairs, (int)s.experts, (int)s.hidden, (int)s.mid);
-    if (scratch_bytes < L.bytes)
-        return fail(HYQ_EINVAL, "moe: scratch %zu bytes < %zu", scratch_bytes, L.bytes);
+    if (!rc && npairs)
+        rc = check_device_args(x_d, out_d, pair_token_d, pair_expert_d, pair_weight_d, scratch_d);
+    if (rc || npairs == 0) return rc;
     DeviceGuard g(ctx->device);
-    HYQ_LAUNCH(launch_moe(gate->dtype, down->dtype, gate->view, up->view, down->view,
-                          (int)s.hidden, (int)s.mid, x_d, (int)tokens, pair_token_d,
-                          pair_expert_d, pair_weight_d, (int)npairs, (int)s.experts,
-                          (uint8_t *)scratch_d, L, out_d, ctx->stream),
-               "moe");
-    return HYQ_OK;
+    return experts_into(ctx, gate, up, down, s, x_d, tokens, pair_token_d, pair_expert_d,
+                        pair_weight_d, npairs, scratch_d, scratch_bytes, out_d, nullptr);
+}
+
+int hyq_moe_shared_experts_d(hyq_ctx *ctx, const hyq_weight *shared, const hyq_weight *gate,
+                             const hyq_weight *up, const hyq_weight *down, const float *x_d,
+                             size_t tokens, const int32_t *pair_token_d,
+                             const int32_t *pair_expert_d, const float *pair_weight_d,
+                             size_t npairs, void *scratch_d, size_t scratch_bytes, float *out_d)
+{
+    MoeShape s;
+    int rc = check_experts(ctx, gate, up, down, &s);
+    if (!rc) rc = check_counts(tokens, npairs);
+    if (rc) return rc;
+    if (!shared) return fail(HYQ_EINVAL, "moe: null shared weight");
+    if (shared->rank != 2 || shared->cols != s.hidden || shared->rows != s.hidden)
+        return fail(HYQ_EINVAL, "moe: the shared projection must be [%zu, %zu]", s.hidden,
+                    s.hidden);
+    if (shared->device != ctx->device) return fail(HYQ_EINVAL, "moe: shared weight on another device");
+    if (npairs &&
+        (rc = check_device_args(x_d, out_d, pair_token_d, pair_expert_d, pair_weight_d, scratch_d)))
+        return rc;
+    DeviceGuard g(ctx->device);
+    if (shared->dtype == Q8_0 && !check_f16_range(shared, "moe") &&
+        moe_fuses_shared(gate->dtype, down->dtype, gate->view, up->view, down->view,
+                         (int)s.hidden, (int)s.mid, (int)tokens, (int)npairs, (int)s.experts))
+        // the shared product's tiles run in the expert launches (its f16
+        // rows formed with the experts' row operands, its tiles beside the
+        // SiLU rows), before the routed sum
+        return experts_into(ctx, gate, up, down, s, x_d, tokens, pair_token_d, pair_expert_d,
+                            pair_weight_d, npairs, scratch_d, scratch_bytes, out_d,
+                            &shared->view);
+    // else the two calls: the seed (src/model.rs:699), then the loop
+    rc = hyq_matmul_d(ctx, shared, x_d, tokens, out_d);
+    if (rc || npairs == 0) return rc;
+    return experts_into(ctx, gate, up, down, s, x_d, tokens, pair_token_d, pair_expert_d,
+                        pair_weight_d, npairs, scratch_d, scratch_bytes, out_d, nullptr);
 }
 
 int hyq_moe_experts(hyq_ctx *ctx, const hyq_weight *gate, const hyq_weight *up,

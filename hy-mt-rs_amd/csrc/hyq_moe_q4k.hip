@@ -42,6 +42,7 @@
 #include <hip/hip_runtime.h>
 
 #include "hyq_f16rows.hpp"
+#include "hyq_few_q80.hpp"
 #include "hyq_internal.hpp"
 #include "hyq_moe_operand.hpp"
 #include "hyq_wave.hpp"
@@ -382,22 +383,38 @@ __global__ __launch_bounds__(256, 2) void moe_q4k_gate_up_kernel(
 // K slices' partial rows (in slice order), formed as pair q's row operand
 // (hop, hhs, hsc: hyq_moe_operand.hpp, scaled by the row's largest |h|,
 // infinity when it holds a NaN); one workgroup per valid pair position q.
-__global__ __launch_bounds__(256) void silu_rows_kernel(const float *__restrict__ gpart,
-                                                        const float *__restrict__ upart,
-                                                        int ks, size_t part_stride, int mid,
-                                                        const int *__restrict__ valid,
-                                                        uint4 *__restrict__ hop,
-                                                        uint2 *__restrict__ hhs,
-                                                        float *__restrict__ hsc)
+// The first `stiles` workgroups take the tiles of a few-token Q8_0 product
+// y = x W^T (hyq_few_q80.hpp: the shared projection that seeds the routed
+// sum, its fragments xf and row scales xsc formed in the plan's launch),
+// which needs nothing the SiLU rows make. They come first so that they are
+// dispatched while the SiLU rows are: their registers hold one workgroup
+// per CU, and the SiLU rows fill the other CUs.
+__global__ __launch_bounds__(64 * few::WAVES) void silu_rows_kernel(
+    const float *__restrict__ gpart, const float *__restrict__ upart, int ks, size_t part_stride,
+    int mid, const int *__restrict__ valid, uint4 *__restrict__ hop, uint2 *__restrict__ hhs,
+    float *__restrict__ hsc, int stiles, WView shared, int K, const _Float16 *__restrict__ xf,
+    const float *__restrict__ xsc, int T, float *__restrict__ y, int cgroups)
 {
-    __shared__ __align__(16) float hl[MOE_Q4K_MAX_K];
-    __shared__ float wred[4];
-    const int q = blockIdx.x;
+    constexpr int NT = 64 * few::WAVES;
+    union Lds {
+        struct {
+            float hl[MOE_Q4K_MAX_K];
+            float wred[few::WAVES];
+        } s;
+        few::Red red;
+    };
+    __shared__ __align__(16) Lds lds;
+    if ((int)blockIdx.x < stiles) {
+        few::q80_tile((int)blockIdx.x, shared, K, xf, xsc, T, y, cgroups, lds.red);
+        return;
+    }
+    const int q = blockIdx.x - stiles;
     if (q >= *valid) return;
     const int t = threadIdx.x;
     const size_t row = (size_t)q * mid;
+    float *hl = lds.s.hl;
     float m = 0.f;
-    for (int i = t; i < mid; i += 256) {
+    for (int i = t; i < mid; i += NT) {
         float gv = gpart[row + i], uv = upart[row + i];
         if (ks > 1) {
             gv = gv + gpart[part_stride + row + i];
@@ -409,15 +426,18 @@ __global__ __launch_bounds__(256) void silu_rows_kernel(const float *__restrict_
         if (v != v) m = INFINITY;
     }
     m = wave::max64(m);
-    if ((t & 63) == 0) wred[t >> 6] = m;
+    if ((t & 63) == 0) lds.s.wred[t >> 6] = m;
     __syncthreads();
-    const int e = f16_row_exponent(fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3])));
+    float mm = lds.s.wred[0];
+#pragma unroll
+    for (int w = 1; w < few::WAVES; ++w) mm = fmaxf(mm, lds.s.wred[w]);
+    const int e = f16_row_exponent(mm);
     const float inv = ldexpf(1.0f, -e);
     if (t == 0) hsc[q] = ldexpf(1.0f, e);
     auto val = [&](int i) { return hl[i]; };
     uint4 *op = hop + (size_t)q * (mid / 8);
     uint32_t *hs = reinterpret_cast<uint32_t *>(hhs + (size_t)q * (mid / 64));
-    for (int it = t; it < 8 * (mid / 256); it += 256)
+    for (int it = t; it < 8 * (mid / 256); it += NT)
         row_operand_item(val, inv, it >> 3, (it >> 1) & 3, it & 1, op, hs);
 }
 
@@ -507,9 +527,12 @@ int launch_moe_q4k(WView gate, WView up, WView down, int hidden, int mid, const 
                    const int *order, const int *tiles, const int *ntiles, int max_tiles,
                    int npairs, bool have_ops, uint4 *xop, uint2 *xhs, float *xsc, int *cpos,
                    int *ctok, float *gpart, float *upart, uint4 *hop, uint2 *hhs, float *hsc,
-                   float *outp, float *outp2, void *stream)
+                   float *outp, float *outp2, void *stream, const WView *shared,
+                   const _Float16 *xf, float *y)
 {
     if (!moe_q4k_fits(hidden, mid)) return (int)hipErrorInvalidValue;
+    if (shared && (!have_ops || !xf || !few_q80_fits(shared->rows, hidden, tokens)))
+        return (int)hipErrorInvalidValue;
     hipStream_t st = (hipStream_t)stream;
     const size_t gstride = (size_t)npairs * mid;
     if (!have_ops) {
@@ -525,8 +548,11 @@ int launch_moe_q4k(WView gate, WView up, WView down, int hidden, int mid, const 
     hipLaunchKernelGGL(moe_q4k_gate_up_kernel, grid, dim3(256),
                        (size_t)34 * (hidden / moe_kslices(hidden)), st, gate, up, mid, hidden,
                        eoff, tiles, ntiles, ctok, xop, xhs, xsc, gpart, upart, gstride, mid / 64);
-    hipLaunchKernelGGL(silu_rows_kernel, dim3(npairs), dim3(256), 0, st, gpart, upart,
-                       moe_kslices(hidden), gstride, mid, valid, hop, hhs, hsc);
+    int cgroups = 0;
+    const int stiles = shared ? few::q80_tiles(shared->rows, tokens, &cgroups) : 0;
+    hipLaunchKernelGGL(silu_rows_kernel, dim3(npairs + stiles), dim3(64 * few::WAVES), 0, st,
+                       gpart, upart, moe_kslices(hidden), gstride, mid, valid, hop, hhs, hsc,
+                       stiles, shared ? *shared : WView{}, hidden, xf, xsc, tokens, y, cgroups);
     hipLaunchKernelGGL(moe_q4k_down_kernel, grid, dim3(256), (size_t)34 * mid, st, down, hidden,
                        mid, eoff, tiles, ntiles, cpos, hop, hhs, hsc, outp, hidden / 64);
     return (int)hipGetLastError();

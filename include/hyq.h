@@ -208,6 +208,21 @@ int hyq_moe_experts(hyq_ctx *ctx, const hyq_weight *gate, const hyq_weight *up,
                     const hyq_weight *down, const float *x, size_t tokens,
                     const int32_t *pair_token, const int32_t *pair_expert,
                     const float *pair_weight, size_t npairs, float *out);
+/* The expert loop with its seed: out_d = shared x_d (Weight::matmul of the
+ * [hidden, hidden] shared projection at batch `tokens`, in the place of
+ * Moe::forward's shared expert, src/model.rs:699), then the loop of
+ * hyq_moe_experts_d adds into it. For a Q8_0 projection at 2..128 tokens
+ * beside Q4_K experts of at most 16 tokens each on average, the shared
+ * product runs inside the expert launches: its f16 rows are formed with the
+ * experts' token operands and its tiles run beside the SiLU rows, with the
+ * same arithmetic as hyq_matmul_d, so out_d holds the same bits as the two
+ * calls in sequence (which is what other shapes run). Same pairs, scratch
+ * and limits as hyq_moe_experts_d. */
+int hyq_moe_shared_experts_d(hyq_ctx *ctx, const hyq_weight *shared, const hyq_weight *gate,
+                             const hyq_weight *up, const hyq_weight *down, const float *x_d,
+                             size_t tokens, const int32_t *pair_token_d,
+                             const int32_t *pair_expert_d, const float *pair_weight_d,
+                             size_t npairs, void *scratch_d, size_t scratch_bytes, float *out_d);
 
 /* ---- the whole MoE FFN of a HyV3 layer: Moe::forward (src/model.rs:687-726)
  * ---- */

@@ -259,6 +259,73 @@ def test_moe_device_entry_point_and_rerun(gpu_ctx, hyq):
         assert np.array_equal(od.numpy(), host)
 
 
+@pytest.mark.parametrize("tokens,used", [(64, 8), (100, 8), (1, 8), (16, 0)])
+def test_moe_shared_experts_matches_two_calls(gpu_ctx, hyq, oracle, tokens, used):
+    """hyq_moe_shared_experts_d at the 30B-A3B layer shape (Q8_0 shared
+    projection [2048x2048], top-`used` of 64 Q4_K experts): at 64 and 100
+    tokens the shared product's tiles run inside the expert launches (one and
+    two 64-token chunk groups), at one token or with no pairs the two calls
+    run. Five calls in a row, the output refilled with NaN before each (a
+    seed the shared tiles failed to write would keep them), each equal bit for
+    bit to hyq_matmul_d followed by hyq_moe_experts_d; three tokens against
+    the f64 chain seeded with the oracle's shared product. Token rows 5 and 9
+    are scaled by 1e6 and 1e-6."""
+    hidden, mid, experts = 2048, 1536, 64
+    _print("moe shared + experts", tokens, used)
+    gate = random_matrix(Q4_K, experts * mid, hidden, seed=41)
+    up = random_matrix(Q4_K, experts * mid, hidden, seed=42)
+    down = random_matrix(Q4_K, experts * hidden, mid, seed=43)
+    shared = random_matrix(Q8_0, hidden, hidden, seed=44)
+    x = np.random.default_rng(45).normal(0, 1, (tokens, hidden)).astype(np.float32)
+    if tokens > 10:  # the f16 row scales of both products' operands
+        x[5] *= 1e6
+        x[9] *= 1e-6
+    x = x.ravel()
+    if used:
+        pt, pe, pw = routed_pairs(tokens, experts, used, seed=46)
+    else:
+        pt = pe = np.zeros(0, np.int32)
+        pw = np.zeros(0, np.float32)
+    G = gpu_ctx.upload(Q4_K, gate, (hidden, mid, experts))
+    U = gpu_ctx.upload(Q4_K, up, (hidden, mid, experts))
+    D = gpu_ctx.upload(Q4_K, down, (mid, hidden, experts))
+    S = gpu_ctx.upload(Q8_0, shared, (hidden, hidden))
+    L = hyq.lib()
+    n = len(pt)
+    nbytes = L.hyq_moe_scratch_bytes(tokens, max(n, 1), experts, hidden, mid)
+    scratch = gpu_ctx.empty(nbytes, np.uint8)
+    xd = gpu_ctx.array(x)
+    ptd, ped, pwd = (gpu_ctx.array(a if n else np.zeros(1, a.dtype)) for a in (pt, pe, pw))
+    seq = gpu_ctx.empty(tokens * hidden, np.float32)
+    hyq.check(L.hyq_matmul_d(gpu_ctx.handle, S.handle, xd.ptr, tokens, seq.ptr))
+    hyq.check(L.hyq_moe_experts_d(gpu_ctx.handle, G.handle, U.handle, D.handle, xd.ptr, tokens,
+                                  ptd.ptr, ped.ptr, pwd.ptr, n, scratch.ptr, nbytes, seq.ptr))
+    want = seq.numpy()
+    nan = np.full(tokens * hidden, np.nan, np.float32)
+    od = gpu_ctx.array(nan)
+    for i in range(5):
+        od.copy_from(nan)
+        hyq.check(L.hyq_moe_shared_experts_d(gpu_ctx.handle, S.handle, G.handle, U.handle,
+                                             D.handle, xd.ptr, tokens, ptd.ptr, ped.ptr, pwd.ptr,
+                                             n, scratch.ptr, nbytes, od.ptr))
+        got = od.numpy()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (tokens, used, i)
+    pick = sorted(np.random.default_rng(47).choice(tokens, min(3, tokens),
+                                                   replace=False).tolist())
+    seed = np.zeros((tokens, hidden), np.float64)
+    smag = np.zeros((tokens, hidden))
+    for t in pick:
+        y, m = oracle.matmul_f64(Q8_0, shared, hidden, hidden, x[t * hidden:(t + 1) * hidden], 1)
+        seed[t], smag[t] = y[0], m[0]
+    ref, mag = chain_f64(oracle, Q4_K, Q4_K, gate, up, down, hidden, mid, x, pt, pe, pw, seed,
+                         pick)
+    got = want.reshape(tokens, hidden)
+    check_moe(got[pick], np.stack([ref[t] for t in pick]),
+              np.stack([mag[t] + smag[t] for t in pick]), f"shared + experts {tokens}")
+    for w in (G, U, D, S):
+        w.release()
+
+
 def test_moe_errors(gpu_ctx, hyq):
     hidden, mid, experts = 256, 512, 4
     G = gpu_ctx.upload(Q4_K, random_matrix(Q4_K, experts * mid, hidden, seed=1),
