@@ -266,6 +266,26 @@ struct GroupSTQ {
         const uint32_t en = 0xAAAAAAAAu - e;
         return (en & ms) | (e & ~ms);
     }
+    // The codebook bytes of the four groups of nibble dword dw (its low
+    // nibbles, or with hi its high ones) with sign bit q of each byte of S:
+    // the low three bits select from the sign-0 entries 0-7 and 8-15 (two
+    // v_perm_b32), and each of the two remaining choices (bit 3: the upper
+    // entries; the sign: 0xAA - e) is a v_perm_b32 between two candidate
+    // dwords whose selector is kb = 0x03020100 plus 4 in every byte whose bit
+    // is set (byte b of the first source or of the second).
+    __device__ __forceinline__ static uint32_t codes_perm(uint32_t dw, int hi, uint32_t S, int q,
+                                                          uint32_t kb)
+    {
+        constexpr uint32_t CB0 = 0x092989a9u, CB1 = 0x062686a6u, CB2 = 0x121a929au,
+                           CB3 = 0x424a626au;
+        const uint32_t sel = hi ? (dw >> 4) & 0x07070707u : dw & 0x07070707u;
+        const uint32_t s3 = ((hi ? dw >> 5 : dw >> 1) & 0x04040404u) | kb;
+        const uint32_t ss = ((q >= 2 ? S >> (q - 2) : S << (2 - q)) & 0x04040404u) | kb;
+        const uint32_t r0 = __builtin_amdgcn_perm(CB1, CB0, sel);
+        const uint32_t r1 = __builtin_amdgcn_perm(CB3, CB2, sel);
+        const uint32_t e = __builtin_amdgcn_perm(r1, r0, s3);
+        return __builtin_amdgcn_perm(0xAAAAAAAAu - e, e, ss);
+    }
     // 5-bit index bytes (sign<<4 | nibble) -> codebook bytes, four at a time.
     __device__ __forceinline__ static uint32_t lut(uint32_t idx)
     {
@@ -285,17 +305,17 @@ struct GroupSTQ {
         // one shift: 16 code) into four accumulators, each then an exact
         // multiple of its place value.
         int r0 = 0, r1 = 0, r2 = 0, r3 = 0;
+        // (the byte-select base in a register, so that each selector is one
+        // v_and_or_b32)
+        uint32_t kb = 0x03020100u;
+        asm volatile("" : "+v"(kb));
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
 #pragma unroll
             for (int qi = 0; qi < 4; ++qi) {
                 const uint32_t dw = nib[2 * c + (qi >> 1)];
-                // the nibbles' selector bits, and bit 3 moved to bit 7
-                const uint32_t sel = (qi & 1) ? (dw >> 4) & 0x07070707u : dw & 0x07070707u;
-                const uint32_t m3 = byte_mask((qi & 1) ? dw : dw << 4);
                 const int q = (c & 1) * 4 + qi; // quad index inside the sign dword
-                // sign bit q of each byte of S moved to bit 7
-                const uint32_t e = codes_sel(sel, m3, byte_mask(sg[c >> 1] << (7 - q)));
+                const uint32_t e = codes_perm(dw, qi & 1, sg[c >> 1], q, kb);
                 const int *a = act + 16 * c + qi;
                 r0 = sdot4(e & 0x03030303u, a[0], r0);
                 r1 = sdot4(e & 0x0C0C0C0Cu, a[4], r1);
