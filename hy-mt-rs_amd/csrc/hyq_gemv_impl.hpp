@@ -351,8 +351,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
                             (MODE == GEMV_SILU || MODE == GEMV_PLAIN)),
                   "expert slots: one row per lane, gate/up or plain");
     static_assert(SL == 0 || ((SL == 64 || SL == 32 || SL == 16) && !H && NR == 1 &&
-                              MODE == GEMV_PLAIN),
-                  "wide rows: 16, 32 or 64 lanes per row, plain, one row per lane");
+                              (MODE == GEMV_PLAIN || (MODE == GEMV_SILU && SL == 16))),
+                  "wide rows: 16, 32 or 64 lanes per row (16 for gate/up), one row per lane");
     using G = typename GroupOf<F>::T;
     using Dt = typename GemvData<G, H>::T;
     constexpr int SUBL = SL ? SL : H ? 16 : 8; // lanes per row
@@ -669,7 +669,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
                         : SUBL == 64              ? wave::sum64(acc[i])
                         : SUBL == 32              ? sum32(acc[i])
                                                   : reduce8(acc[i]);
-        const float v2 = MODE == GEMV_SILU ? (H ? wave::sum16(acc2[i]) : reduce8(acc2[i])) : 0.f;
+        const float v2 =
+            MODE == GEMV_SILU ? ((H || SUBL == 16) ? wave::sum16(acc2[i]) : reduce8(acc2[i])) : 0.f;
         if (sub != 0 || !valid[i] || MODE == GEMV_ISUMS) continue;
         if (MODE == GEMV_SILU) {
             a.seg[0].y[lrow[i]] = silu_mul(v, v2);
@@ -800,7 +801,16 @@ template <int F> int launch_gemv_format(int mode, const GemvArgs &a, void *strea
     const bool half = HasHalf<F>::value && a.xin && nr == 1 && mode != GEMV_ISUMS && !wide &&
                       !w16 && half_wgs <= HALF_MAX_WORKGROUPS;
     if (wide) waves = 4;
-    const int rows_per_block = (w64 ? 1 : wide ? 2 : w16 || half ? 4 : 8) * nr * waves;
+    // gate/up from Q8 input, 9-16 groups per row: 16 lanes per row, so that
+    // each lane's one group of both matrices is loaded before the activations
+    // are staged (with 8 lanes the second group loads after the first's dots);
+    // for the formats with the heaviest dots ([2 x 14336 x 4096] Q4_K 14.7 ->
+    // 14.5 us, STQ1_0 9.8 -> 9.4 us; Q2_0C 8.1 -> 8.5 us, and under an
+    // RMSNorm stage the 7B decode step 1.77 -> 1.82 ms per token, so not
+    // there)
+    const bool s16 = mode == GEMV_SILU && !a.xin && nr == 1 && ks == 1 && a.groups > 8 &&
+                     a.groups <= 16 && (F == Q4_K || F == STQ1_0 || F == Q6_K);
+    const int rows_per_block = (w64 ? 1 : wide ? 2 : w16 || half || s16 ? 4 : 8) * nr * waves;
     // a K split is a plain GEMV of an f32 row without norm, residual or
     // partial-row inputs (each slice writes its own partial row)
     if ((ks > 1 || a.nslots) &&
@@ -856,6 +866,10 @@ template <int F> int launch_gemv_format(int mode, const GemvArgs &a, void *strea
         } else {
             hipLaunchKernelGGL((gemv_kernel<F, 1, GEMV_PLAIN, 1, 0, false, 32>), grid, block, lds, st, a);
         }
+        return (int)hipGetLastError();
+    }
+    if (s16) {
+        hipLaunchKernelGGL((gemv_kernel<F, 1, GEMV_SILU, 0, 0, false, 16>), grid, block, lds, st, a);
         return (int)hipGetLastError();
     }
     if (w16) {

@@ -231,24 +231,35 @@ def test_fused_qkv_equals_three_products(gpu_ctx, hyq, dtype):
 
 
 @pytest.mark.parametrize("dtype", QUANT, ids=lambda d: NAMES[d])
-def test_gate_up_silu(gpu_ctx, oracle, dtype):
-    rows, cols = 1536, 2048
+@pytest.mark.parametrize("cols", [2048, 4096])
+def test_gate_up_silu(gpu_ctx, oracle, dtype, cols):
+    """8 groups per row and 16. At 8 groups the fused launch and the plain
+    GEMV both give a row 8 lanes, so each half of the product equals the
+    plain GEMV (the SiLU within 2e-6); at 16 the plain GEMV gives a row 16
+    lanes and the fused one 8 or 16 by format, so the sums may round in
+    another order. Either way the product is checked against the oracle's
+    f64 halves on the same Q8 input (relative 2-norm 1e-4)."""
+    rows = 1536
     g = random_matrix(dtype, rows, cols, seed=31)
     u = random_matrix(dtype, rows, cols, seed=32)
     x = np.random.default_rng(33).normal(0, 1, cols).astype(np.float32)
     G = gpu_ctx.upload(dtype, g, (cols, rows))
     U = gpu_ctx.upload(dtype, u, (cols, rows))
     y = G.matmul_gate_up_silu(U, x)
-    # each half equals the plain GEMV bit for bit
     gy, uy = G.matmul(x, 1), U.matmul(x, 1)
-    with np.errstate(over="ignore"):
-        exp = ((gy / (np.float32(1) + np.exp(-gy))) * uy).astype(np.float32)
-    assert np.allclose(y, exp, rtol=2e-6, atol=0), NAMES[dtype]
+    if cols == 2048:
+        with np.errstate(over="ignore"):
+            exp = ((gy / (np.float32(1) + np.exp(-gy))) * uy).astype(np.float32)
+        assert np.allclose(y, exp, rtol=2e-6, atol=0), NAMES[dtype]
     q, s = oracle.q8_quantize(x)
     gr, gm = oracle.gemv_q8_f64(dtype, g, rows, cols, q, s)
     ur, um = oracle.gemv_q8_f64(dtype, u, rows, cols, q, s)
     check_decode_path(gy, gr, gm)
     check_decode_path(uy, ur, um)
+    with np.errstate(over="ignore"):
+        ref = gr / (1 + np.exp(-gr)) * ur
+    rel = np.linalg.norm(y - ref) / np.linalg.norm(ref)
+    assert rel <= 1e-4, (NAMES[dtype], cols, rel)
 
 
 @pytest.mark.parametrize("dtype", QUANT, ids=lambda d: NAMES[d])
