@@ -133,6 +133,22 @@ def test_gemv_matches_oracle(gpu_ctx, oracle, dtype):
     check_decode_path(y, y_ref, mag, NAMES[dtype])
 
 
+@pytest.mark.parametrize("dtype", [Q2_0C, STQ1_0], ids=lambda d: NAMES[d])
+@pytest.mark.parametrize("rows,cols", [(2048, 2048), (12288, 2048)],
+                         ids=["attn_out_2048x2048", "gate_up_12288x2048"])
+def test_gemv_c2_shapes(gpu_ctx, oracle, dtype, rows, cols):
+    """The 1.8B attention output and stacked gate+up matrices at their own
+    sizes (the QKV and down shapes are above), Q8 input, against the
+    oracle's f64 dot on the same codes."""
+    _print("c2", NAMES[dtype], rows, cols)
+    w = random_matrix(dtype, rows, cols, seed=61)
+    x = np.random.default_rng(62).normal(0, 1, cols).astype(np.float32)
+    y = gpu_ctx.upload(dtype, w, (cols, rows)).matmul(x, 1)
+    q, s = oracle.q8_quantize(x)
+    y_ref, mag = oracle.gemv_q8_f64(dtype, w, rows, cols, q, s)
+    check_decode_path(y, y_ref, mag, NAMES[dtype])
+
+
 @pytest.mark.parametrize("dtype", QUANT, ids=lambda d: NAMES[d])
 @pytest.mark.parametrize("rows,cols", [(2048, 6144), (3071, 4096), (4100, 4096)],
                          ids=["2048x6144", "3071x4096", "4100x4096"])
