@@ -848,6 +848,12 @@ def main() -> int:
             "7B_Q6_K_down_4096x14336": (Q6_K, 4096, 14336),
             "7B_Q2_0C_gate_up_28672x4096": (Q2_0C, 28672, 4096),
             "7B_STQ1_0_gate_up_28672x4096": (STQ1_0, 28672, 4096),
+            # the target formats at the 7B vocabulary projection's shape
+            # (an lm_head in that format): sizes where the HBM stream, not
+            # the ~3 us launch ramp, decides
+            "7B_vocab_Q4_K_128167x4096": (Q4_K, 128167, 4096),
+            "7B_vocab_Q2_0C_128167x4096": (Q2_0C, 128167, 4096),
+            "7B_vocab_STQ1_0_128167x4096": (STQ1_0, 128167, 4096),
         }.items():
             us, gbs, agg, copies, alg = gemv_rate(hyq, ctx, ev, dt_, rows, cols, graph=use_graph)
             ceil = sized_read_ceiling(hyq, ctx, ev, alg)
