@@ -514,10 +514,11 @@ __host__ __device__ inline bool plan_fast_fits(int P, int T, int E)
            nb * T <= PLAN_FAST_TAB;
 }
 
-// Workgroup 0 makes the plan. With x given (the Q4_K register-operand
-// kernels), workgroups 1, 2, ... also form the row operand of each token row
-// of x [T, K] (wave_row_operand: xop, xhs, xsc), one wave per row, and the
-// plan also writes, per chunk column (ti, col), the pair position it takes
+// Workgroups 0 and 1 make the plan, each grouping the pairs by expert: 0
+// writes eoff, order and the tiles, 1 the per-token lists (toff, tlist). With
+// x given (the Q4_K register-operand kernels), workgroups 2, 3, ... also form
+// the row operand of each token row of x [T, K] (wave_row_operand: xop, xhs,
+// xsc), one wave per row, and the plan also writes, per chunk column (ti, col), the pair position it takes
 // (cpos: the chunk's last pair for columns past its pairs) and that pair's
 // token (ctok). With xf given, a second wave per row writes the row's f16
 // fragments for a few-token Q8_0 product (hyq_few_q80.hpp; zeros for the rows
@@ -531,10 +532,10 @@ __global__ __launch_bounds__(1024) void moe_plan_fast_kernel(
     _Float16 *__restrict__ xf)
 {
     const int t = threadIdx.x;
-    if (blockIdx.x > 0) {
+    if (blockIdx.x > 1) {
         // one wave per row, or with xf two: the row operand and the fragments
         const int w = t >> 6;
-        const int r = (xf ? 8 * (blockIdx.x - 1) + (w >> 1) : 16 * (blockIdx.x - 1) + w);
+        const int r = (xf ? 8 * (blockIdx.x - 2) + (w >> 1) : 16 * (blockIdx.x - 2) + w);
         if (!xf || !(w & 1)) {
             if (r < T)
                 wave_row_operand(x + (size_t)r * K, K, xop + (size_t)r * (K / 8),
@@ -555,6 +556,10 @@ __global__ __launch_bounds__(1024) void moe_plan_fast_kernel(
     __shared__ unsigned long long tab[PLAN_FAST_TAB];
     __shared__ int off[PLAN_FAST + 1];
     __shared__ int lsum[16];
+    // tile -> expert: at most P / chunk + min(E, P) tiles for chunk >= 16
+    __shared__ int tle[PLAN_FAST + PLAN_FAST / 16 + 1];
+    // workgroup 1 forms the per-token lists; both group the pairs by expert
+    const bool tokens_wg = blockIdx.x == 1;
     for (int p = t; p < P; p += 1024) {
         const int tk = ptok[p], e = pexp[p];
         key[p] = tk >= 0 && tk < T && e >= 0 && e < E ? e : -1;
@@ -563,32 +568,42 @@ __global__ __launch_bounds__(1024) void moe_plan_fast_kernel(
     __syncthreads();
     // group pairs by expert (stable)
     lds_group_1024(key, P, E, tab, rk, off, lsum);
-    for (int e = t; e <= E; e += 1024) eoff[e] = off[e];
+    if (!tokens_wg)
+        for (int e = t; e <= E; e += 1024) eoff[e] = off[e];
     for (int p = t; p < P; p += 1024) {
         const int e = key[p];
         if (e >= 0) ord[off[e] + (int)tab[(p >> 6) * E + e] + rk[p]] = p;
     }
     __syncthreads();
     const int nv = off[E];
-    for (int q = t; q < nv; q += 1024) order[q] = ord[q];
-    // chunk-token chunks of every expert (counts in rk, scanned)
-    for (int e = t; e < E; e += 1024) rk[e] = (off[e + 1] - off[e] + chunk - 1) / chunk;
-    __syncthreads();
-    lds_scan_1024(rk, E, lsum);
-    for (int e = t; e < E; e += 1024)
-        for (int c = 0; c < rk[e + 1] - rk[e]; ++c) {
-            tiles[2 * (rk[e] + c)] = e;
-            tiles[2 * (rk[e] + c) + 1] = c;
-            if (cpos) {
-                const int nb = off[e] + c * chunk, last = min(chunk, off[e + 1] - nb) - 1;
-                for (int col = 0; col < chunk; ++col) {
-                    const int q = nb + min(col, last);
-                    cpos[(rk[e] + c) * chunk + col] = q;
-                    ctok[(rk[e] + c) * chunk + col] = tok[ord[q]];
-                }
+    if (!tokens_wg) {
+        for (int q = t; q < nv; q += 1024) order[q] = ord[q];
+        // chunk-token chunks of every expert (counts in rk, scanned)
+        for (int e = t; e < E; e += 1024) rk[e] = (off[e + 1] - off[e] + chunk - 1) / chunk;
+        __syncthreads();
+        lds_scan_1024(rk, E, lsum);
+        for (int e = t; e < E; e += 1024)
+            for (int c = 0; c < rk[e + 1] - rk[e]; ++c) {
+                tiles[2 * (rk[e] + c)] = e;
+                tiles[2 * (rk[e] + c) + 1] = c;
+                tle[rk[e] + c] = e;
+            }
+        const int nt = rk[E];
+        if (t == 0) *ntiles = nt;
+        if (cpos) {
+            __syncthreads();
+            // each chunk column's pair position (the chunk's last pair past
+            // its pairs) and token, one column per thread
+            for (int i = t; i < nt * chunk; i += 1024) {
+                const int ti = i / chunk, col = i - ti * chunk, e = tle[ti];
+                const int nb = off[e] + (ti - rk[e]) * chunk, last = min(chunk, off[e + 1] - nb) - 1;
+                const int q = nb + min(col, last);
+                cpos[i] = q;
+                ctok[i] = tok[ord[q]];
             }
         }
-    if (t == 0) *ntiles = rk[E];
+        return;
+    }
     // for each token, its positions in ascending expert order
     for (int q = t; q < nv; q += 1024) key[q] = tok[ord[q]];
     __syncthreads();
@@ -1036,7 +1051,7 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
     _Float16 *xf = shared ? (_Float16 *)(scratch + L.xf) : nullptr;
     if (fast)
         hipLaunchKernelGGL(moe_plan_fast_kernel,
-                           dim3(few ? 1 + (xf ? 2 : 1) * ((tokens + 15) / 16) : 1),
+                           dim3(few ? 2 + (xf ? 2 : 1) * ((tokens + 15) / 16) : 2),
                            dim3(1024), 0, st, ptok, pexp, npairs, tokens, experts, eoff, order,
                            toff, tlist, tiles, ntiles, few ? moe_q4k_chunk() : BN,
                            few ? x : nullptr, hidden, xop, xhs, xsc, few ? cpos : nullptr,

@@ -35,11 +35,23 @@ constexpr int MOE_OP_U2_PER_SB = 4;  // hs uint2 per superblock of a row
 __device__ __forceinline__ float wave_row_absmax(const float *x, int n)
 {
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    const int lane = threadIdx.x & 63, n4 = n / 4;
     float m = 0.f;
-    for (int i = threadIdx.x & 63; i < n / 4; i += 64) {
-        const float4 v = x4[i];
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-        if (v.x != v.x || v.y != v.y || v.z != v.z || v.w != v.w) m = INFINITY;
+    // eight float4 loads in flight per pass (clamped in bounds, past the end
+    // masked to zero), so that the row costs one memory round trip per 2048
+    // values rather than one per float4
+    for (int i0 = 0; i0 < n4; i0 += 512) {
+        float4 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = x4[min(i0 + lane + 64 * j, n4 - 1)];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (i0 + lane + 64 * j >= n4) v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)),
+                               fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+            if (v[j].x != v[j].x || v[j].y != v[j].y || v[j].z != v[j].z || v[j].w != v[j].w)
+                m = INFINITY;
+        }
     }
     return wave::max64(m);
 }
