@@ -38,6 +38,11 @@ int fail(int code, const char *fmt, ...)
 
 int hip_fail(hipError_t e, const char *what)
 {
+    // A failed runtime call (an allocation past the device's memory, say)
+    // stays the thread's last error until read, and every launcher reports
+    // hipGetLastError after its launch: read it here, so that the next launch
+    // is not reported as this call's failure.
+    (void)hipGetLastError();
     return fail(e == hipErrorOutOfMemory ? HYQ_ENOMEM : HYQ_EDEVICE, "%s: %s", what,
                 hipGetErrorString(e));
 }

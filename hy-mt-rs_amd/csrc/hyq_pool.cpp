@@ -48,7 +48,10 @@ void *pool_alloc(int device, size_t bytes, PoolChunk **chunk)
     if (hipMalloc(&base, size) != hipSuccess) {
         (void)hipGetLastError(); // clear the failed allocation's error
         size = align_up(need, PAGE);
-        if (hipMalloc(&base, size) != hipSuccess) return nullptr;
+        if (hipMalloc(&base, size) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
     }
     auto *c = new PoolChunk{device, (uint8_t *)base, Ranges{}, 1};
     c->ranges.size = size;

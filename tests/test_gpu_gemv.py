@@ -354,6 +354,23 @@ def test_expert_view_equals_separate_upload(gpu_ctx):
         W.expert(E)
 
 
+def test_failed_allocation_leaves_later_launches_alone(gpu_ctx, hyq):
+    """A device allocation past the device's memory fails with HYQ_ENOMEM, and
+    the runtime error it leaves is not reported by the next (good) launch:
+    every launcher checks the runtime's last error after launching."""
+    w = random_matrix(Q2_0C, 64, 512, seed=3)
+    W = gpu_ctx.upload(Q2_0C, w, (512, 64))
+    x = np.random.default_rng(3).normal(0, 1, 512).astype(np.float32)
+    y0 = W.matmul(x, 1)
+    for attempt in range(2):
+        _print("allocation of 2^50 bytes, attempt", attempt)
+        with pytest.raises(hyq.HyqError) as e:
+            gpu_ctx.empty(1 << 48, np.float32)
+        assert e.value.code == hyq.ENOMEM
+        assert np.array_equal(W.matmul(x, 1), y0)
+    W.release()
+
+
 def test_shape_errors(gpu_ctx, hyq):
     w = random_matrix(Q2_0C, 8, 512, seed=0)
     with pytest.raises(ValueError):
