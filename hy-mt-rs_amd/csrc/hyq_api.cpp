@@ -655,7 +655,8 @@ int hyq_weight_upload(hyq_ctx *ctx, int dtype, const uint8_t *gguf_bytes, size_t
         return fail(HYQ_EINVAL, "wrong byte count for dtype %d: %zu != %llu", dtype, byte_len,
                     (unsigned long long)(nblocks * (uint64_t)bb));
     if (!gguf_bytes) return fail(HYQ_EINVAL, "hyq_weight_upload: null bytes");
-    if (rows * experts > 0x7fffffffull || nb > 0x7fffffffull)
+    // (every launch takes rows and columns as int)
+    if (rows * experts > 0x7fffffffull || cols > 0x7fffffffull)
         return fail(HYQ_EINVAL, "hyq_weight_upload: shape too large");
     DeviceGuard g(ctx->device);
 
