@@ -478,5 +478,131 @@ __device__ __forceinline__ void k_loop(const WSrc &wsrc, const XRow &xrow, const
     }
 }
 
+// ---------------------------------------------------------------------------
+// Producer/consumer form of k_loop for 512 threads (tiles of BM weight rows by
+// 256 tokens): waves 0-3 (one per SIMD) fetch and dequantize the weight slice
+// as k_loop's first 256 threads do; waves 4-7 (the other wave of each SIMD)
+// multiply, each 2 blocks of 32 weight rows (LDS rows arow(0), arow(1) ..
+// + 31, a function of the wave) by 128 tokens, wave 4 + c taking tokens
+// 128 (c % 2): 2 weight and 4 token fragments per 16-deep step feed 8
+// MFMAs (0.75 KB of LDS reads per MFMA against k_loop's 1 KB); all eight
+// copy the activation slice as k_loop does (four 16-byte pieces each). Every output
+// element sees the same operands in the same k order as in k_loop, so the
+// results are bit-identical. acc[i][j]: weight block i, token block j.
+// ---------------------------------------------------------------------------
+constexpr int PC_THREADS = 512;
+
+template <class ARow>
+__device__ __forceinline__ void mma_step_pc(const _Float16 *Ws, const _Float16 *Xs,
+                                            const ARow &arow, int wn, f32x16 (&acc)[2][4])
+{
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 31, kq = 8 * (lane >> 5);
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 16) {
+        half8 a[2], b[4];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            a[i] = *reinterpret_cast<const half8 *>(Ws + (arow(i) + r) * LDK + kk + kq);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            b[j] = *reinterpret_cast<const half8 *>(Xs + (wn * 128 + 32 * j + r) * LDK + kk + kq);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+}
+
+template <int F, class WSrc, class XRow, class ARow>
+__device__ __forceinline__ void k_loop_pc(const WSrc &wsrc, const XRow &xrow, const ARow &arow,
+                                          int K, _Float16 *lds, f32x16 (&acc)[2][4],
+                                          int kbase = 0)
+{
+    using D = Deq<F>;
+    constexpr int BUF = buf_halves<8>();
+    const int t = threadIdx.x;
+    // waves 0-3 produce, waves 4-7 consume (a wave-uniform test); both copy
+    // activation rows: thread t the four rows (t % 256) / 8 + 32 i + 128 (t / 256)
+    const bool prod = __builtin_amdgcn_readfirstlane(t) < 256;
+    const int lrow = (t & 255) >> 1, h = t & 1;
+    const int wn = (t >> 6) & 1;
+    WView wv{};
+    int row = -1;
+    if (prod) wsrc(lrow, wv, row);
+    const _Float16 *xp[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const _Float16 *p = xrow(((t & 255) >> 3) + 32 * i + 128 * (t >> 8));
+        xp[i] = p ? p + 8 * (t & 7) : nullptr;
+    }
+    const RowPtr rp = D::rows(wv, row < 0 ? 0 : row);
+    typename D::Raw raw;
+    uint4 xr[4];
+    auto fetch_x = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            xr[i] = xp[i] ? *reinterpret_cast<const uint4 *>(xp[i] + kbase + k0)
+                          : make_uint4(0, 0, 0, 0);
+    };
+    auto put_x = [&](int b) {
+        _Float16 *Xs = lds + b * BUF + TILE_HALVES;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<uint4 *>(
+                Xs + (((t & 255) >> 3) + 32 * i + 128 * (t >> 8)) * LDK + 8 * (t & 7)) = xr[i];
+    };
+    auto fetch_w = [&](int k0) {
+        if (row >= 0) D::load(raw, rp, kbase + k0, h);
+    };
+    auto put_w = [&](int k0, int b) {
+        _Float16 *Ws = lds + b * BUF;
+        if (row >= 0) D::convert(raw, ((kbase + k0) >> 6) & 3, h, Ws + lrow * LDK);
+        else zero_half(Ws + lrow * LDK, h);
+    };
+    // Two loops, one per role, each passing the same 1 + steps barriers (a
+    // barrier counts waves, whichever instruction they reach it at), so that
+    // neither role keeps the other's registers live: the producers' staged
+    // weights, the consumers' 128 accumulators.
+    const int steps = K / BK;
+    if (prod) {
+        fetch_w(0);
+        fetch_x(0);
+        put_w(0, 0);
+        put_x(0);
+        if (steps > 1) {
+            fetch_w(BK);
+            fetch_x(BK);
+        }
+        __syncthreads();
+        for (int s = 0; s < steps; ++s) {
+            if (s + 1 < steps) {
+                put_w((s + 1) * BK, (s & 1) ^ 1);
+                put_x((s & 1) ^ 1);
+                if (s + 2 < steps) {
+                    fetch_w((s + 2) * BK);
+                    fetch_x((s + 2) * BK);
+                }
+            }
+            __syncthreads();
+        }
+    } else {
+        fetch_x(0);
+        put_x(0);
+        if (steps > 1) fetch_x(BK);
+        __syncthreads();
+        for (int s = 0; s < steps; ++s) {
+            const _Float16 *Ws = lds + (s & 1) * BUF;
+            mma_step_pc(Ws, Ws + TILE_HALVES, arow, wn, acc);
+            if (s + 1 < steps) {
+                put_x((s & 1) ^ 1);
+                if (s + 2 < steps) fetch_x((s + 2) * BK);
+            }
+            __syncthreads();
+        }
+    }
+}
+
 } // namespace tile
 } // namespace hyq
