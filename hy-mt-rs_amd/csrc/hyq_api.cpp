@@ -474,9 +474,14 @@ int matmul_dev(hyq_ctx *ctx, const hyq_weight *w, const float *x_d, size_t batch
     if (batch > 65535) return fail(HYQ_EINVAL, "matmul: batch %zu exceeds 65535", batch);
     // Q8_0 at up to 128 tokens: one register-operand launch (no K split)
     const bool few = w->dtype == Q8_0 && few_q80_fits((int)w->rows, (int)w->cols, (int)batch);
-    const size_t xh_bytes =
-        align_up(few ? few_q80_operand_bytes((int)w->cols, (int)batch) : batch * w->cols * 2, 256);
     const int ks = few ? 1 : matmul_kslices(w->dtype, (int)w->rows, (int)w->cols, (int)batch);
+    // the 256-token tiles take their f16 rows in MFMA fragment order
+    const bool frag =
+        !few && gemm_frag_operand(w->dtype, (int)w->rows, (int)w->cols, (int)batch, ks);
+    const size_t xh_bytes =
+        align_up(few ? few_q80_operand_bytes((int)w->cols, (int)batch)
+                     : (frag ? frag_rows((int)batch) : batch) * w->cols * 2,
+                 256);
     const size_t part = ks > 1 ? (size_t)ks * batch * w->rows : 0;
     void *xh_mem = nullptr, *part_mem = nullptr;
     if (fs) {
@@ -499,9 +504,10 @@ int matmul_dev(hyq_ctx *ctx, const hyq_weight *w, const float *x_d, size_t batch
                    "few_q80");
         return HYQ_OK;
     }
-    HYQ_LAUNCH(launch_to_f16(x_d, (int)batch, (int)w->cols, xh, rscale, ctx->stream), "to_f16");
+    HYQ_LAUNCH(launch_to_f16(x_d, (int)batch, (int)w->cols, xh, rscale, ctx->stream, frag),
+               "to_f16");
     HYQ_LAUNCH(launch_gemm_f16(w->dtype, w->view, (int)w->cols, xh, rscale, (int)batch, y_d,
-                               nullptr, ctx->stream, (float *)part_mem, part, ks),
+                               nullptr, ctx->stream, (float *)part_mem, part, ks, frag),
                "gemm_f16");
     return HYQ_OK;
 }

@@ -52,7 +52,8 @@ __global__ __launch_bounds__(256) void rows_to_f16_kernel(const float *__restric
                                                           const float *__restrict__ norm,
                                                           float eps,
                                                           _Float16 *__restrict__ xh,
-                                                          float *__restrict__ rscale)
+                                                          float *__restrict__ rscale,
+                                                          bool frag = false)
 {
     __shared__ float wred[4];
     const int r = blockIdx.x;
@@ -100,13 +101,16 @@ __global__ __launch_bounds__(256) void rows_to_f16_kernel(const float *__restric
     const int e = f16_row_exponent(m);
     const float inv = ldexpf(1.0f, -e);
     if (t == 0) rscale[r] = ldexpf(1.0f, e);
-    _Float16 *o = xh + (size_t)r * K;
+    // (fragment order: values 4i .. 4i + 3 stay together, k % 8 being 0 or 4)
+    _Float16 *o = frag ? xh + (size_t)(r / 32) * 32 * K + (size_t)(r % 32) * 8 : xh + (size_t)r * K;
     for (int i = t; i < n4; i += 256) {
         const float4 v = value(i);
         const half2v a = __builtin_convertvector((float2v){v.x * inv, v.y * inv}, half2v);
         const half2v b = __builtin_convertvector((float2v){v.z * inv, v.w * inv}, half2v);
-        *reinterpret_cast<half2v *>(o + 4 * i) = a;
-        *reinterpret_cast<half2v *>(o + 4 * i + 2) = b;
+        const int k = 4 * i;
+        _Float16 *q = frag ? o + (size_t)(k / 16) * 512 + 256 * ((k / 8) & 1) + (k & 4) : o + k;
+        *reinterpret_cast<half2v *>(q) = a;
+        *reinterpret_cast<half2v *>(q + 2) = b;
     }
 }
 
@@ -236,6 +240,79 @@ __global__ __launch_bounds__(PC_THREADS, 1) void gemm_f16_pc_kernel(
 #pragma unroll
             for (int g4 = 0; g4 < 4; ++g4) {
                 const int m = m0 + wm * 64 + 32 * i + acc_row_in_block(4 * g4);
+                if (m + 3 < M && (M & 3) == 0) {
+                    float4 v = make_float4(acc[i][j][4 * g4] * sc, acc[i][j][4 * g4 + 1] * sc,
+                                           acc[i][j][4 * g4 + 2] * sc, acc[i][j][4 * g4 + 3] * sc);
+                    if (rr) {
+                        const float4 a = *reinterpret_cast<const float4 *>(rr + m);
+                        v = make_float4(a.x + v.x, a.y + v.y, a.z + v.z, a.w + v.w);
+                    }
+                    *reinterpret_cast<float4 *>(yr + m) = v;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (m + e < M) {
+                            const float v = acc[i][j][4 * g4 + e] * sc;
+                            yr[m + e] = rr ? rr[m + e] + v : v;
+                        }
+                }
+            }
+        }
+}
+
+// The 256-token tiles with the activations, in fragment order
+// (launch_to_f16 with frag), straight into the consumers' registers
+// (k_loop_pcx): same grid and tile order as gemm_f16_pc_kernel, bit-identical
+// results; consumer wave 4 + c writes tokens 64 c ...
+template <int F>
+__global__ __launch_bounds__(PC_THREADS, 1) void gemm_f16_pcx_kernel(
+    GemmSegs g, int K, const _Float16 *__restrict__ xh, const float *__restrict__ rscale, int N,
+    int mtiles, int ntiles, int kslices, float *__restrict__ part)
+{
+    __shared__ __attribute__((aligned(16))) _Float16 lds[2 * TILE_HALVES];
+    const int T = xcd_tile(mtiles * ntiles);
+    if (T >= mtiles * ntiles) return;
+    int mt = T / ntiles, sg = 0;
+    while (sg + 1 < g.nseg && mt >= g.s[sg].tiles) mt -= g.s[sg++].tiles;
+    const GemmSeg &S = g.s[sg];
+    const int M = S.rows;
+    const int m0 = mt * BM, n0 = (T % ntiles) * 256;
+
+    f32x16 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+    auto wsrc = [&](int lrow, WView &v, int &row) {
+        v = S.w;
+        row = m0 + lrow < M ? m0 + lrow : -1;
+    };
+    // the fragment-order run of the 32-token block holding tile token r
+    // (clamped into the batch's blocks)
+    auto xsrc = [&](int r) -> const _Float16 * {
+        return xh + (size_t)min((n0 + r) / 32, (N - 1) / 32) * 32 * K;
+    };
+    const int kslice = K / kslices;
+    k_loop_pcx<F>(wsrc, xsrc, kslice, lds, acc, blockIdx.y * kslice);
+    if (threadIdx.x < 256) return; // the producers
+    const int c = (threadIdx.x >> 6) & 3;
+
+    float *y = kslices > 1 ? part + (size_t)blockIdx.y * N * M : S.y;
+    const float *residual = kslices > 1 ? nullptr : S.residual;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int n = n0 + 64 * c + 32 * j + (threadIdx.x & 31);
+            if (n >= N) continue;
+            float *yr = y + (size_t)n * M;
+            const float *rr = residual ? residual + (size_t)n * M : nullptr;
+            const float sc = rscale[n];
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const int m = m0 + 32 * i + acc_row_in_block(4 * g4);
                 if (m + 3 < M && (M & 3) == 0) {
                     float4 v = make_float4(acc[i][j][4 * g4] * sc, acc[i][j][4 * g4 + 1] * sc,
                                            acc[i][j][4 * g4 + 2] * sc, acc[i][j][4 * g4 + 3] * sc);
@@ -863,9 +940,15 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(float *__restrict__ ou
 
 } // namespace
 
-int launch_to_f16(const float *x, int rows, int K, _Float16 *xh, float *rscale, void *stream)
+int launch_to_f16(const float *x, int rows, int K, _Float16 *xh, float *rscale, void *stream,
+                  bool frag)
 {
-    return launch_norm_to_f16(x, rows, K, nullptr, 0.f, xh, rscale, stream);
+    if (!frag) return launch_norm_to_f16(x, rows, K, nullptr, 0.f, xh, rscale, stream);
+    if (rows <= 0) return 0;
+    if (K % 16) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(rows_to_f16_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream, x, K,
+                       nullptr, nullptr, nullptr, nullptr, 0.f, xh, rscale, true);
+    return (int)hipGetLastError();
 }
 
 int launch_norm_to_f16(const float *x, int rows, int K, const float *norm, float eps,
@@ -966,9 +1049,17 @@ int matmul_kslices(int fmt, int M, int K, int batch)
     return base;
 }
 
+bool gemm_frag_operand(int fmt, int rows, int cols, int batch, int kslices)
+{
+    (void)fmt;
+    (void)cols;
+    const int mtiles = (rows + BM - 1) / BM;
+    return gemm_waves(batch, mtiles * (kslices > 1 ? kslices : 1)) == 8;
+}
+
 int launch_gemm_f16(int fmt, WView w, int cols, const _Float16 *xh, const float *rscale,
                     int batch, float *y, const float *residual, void *stream, float *part,
-                    size_t part_floats, int kslices)
+                    size_t part_floats, int kslices, bool xfrag)
 {
     GemmSegs g{};
     g.nseg = 1;
@@ -978,7 +1069,7 @@ int launch_gemm_f16(int fmt, WView w, int cols, const _Float16 *xh, const float 
     g.s[0].rows = w.rows;
     const int ks = kslices > 0 ? kslices : gemm_kslices(fmt, w.rows, cols);
     if (ks > 1 && part && part_floats >= (size_t)ks * batch * w.rows) {
-        int rc = launch_gemm_f16_segs(fmt, g, cols, xh, rscale, batch, stream, ks, part);
+        int rc = launch_gemm_f16_segs(fmt, g, cols, xh, rscale, batch, stream, ks, part, xfrag);
         if (rc) return rc;
         const size_t count4 = (size_t)batch * w.rows / 4;
         hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((count4 + 255) / 256)), dim3(256),
@@ -987,11 +1078,11 @@ int launch_gemm_f16(int fmt, WView w, int cols, const _Float16 *xh, const float 
                            reinterpret_cast<float4 *>(y));
         return (int)hipGetLastError();
     }
-    return launch_gemm_f16_segs(fmt, g, cols, xh, rscale, batch, stream);
+    return launch_gemm_f16_segs(fmt, g, cols, xh, rscale, batch, stream, 1, nullptr, xfrag);
 }
 
 int launch_gemm_f16_segs(int fmt, GemmSegs g, int cols, const _Float16 *xh, const float *rscale,
-                         int batch, void *stream, int kslices, float *part)
+                         int batch, void *stream, int kslices, float *part, bool xfrag)
 {
     if (cols % BK || g.nseg < 1 || g.nseg > 3) return (int)hipErrorInvalidValue;
     if (kslices < 1 || (kslices > 1 && (g.nseg != 1 || !part || cols % kslices)))
@@ -1003,13 +1094,18 @@ int launch_gemm_f16_segs(int fmt, GemmSegs g, int cols, const _Float16 *xh, cons
         mtiles += g.s[i].tiles;
     }
     const int nw = gemm_waves(batch, mtiles * kslices), bn = 32 * nw;
+    // fragment-order activations: only the 256-token tiles of one weight
+    if (xfrag && (nw != 8 || g.nseg != 1 || cols % 16)) return (int)hipErrorInvalidValue;
     const int ntiles = (batch + bn - 1) / bn;
     const int per = (mtiles * ntiles + 7) / 8;
     dim3 grid(8 * per, kslices), block(64 * nw);
     hipStream_t st = (hipStream_t)stream;
 #define HYQ_GEMM(F)                                                                            \
     case F:                                                                                    \
-        if (nw == 8)                                                                           \
+        if (xfrag)                                                                             \
+            hipLaunchKernelGGL((gemm_f16_pcx_kernel<F>), grid, block, 0, st, g, cols, xh,       \
+                               rscale, batch, mtiles, ntiles, kslices, part);                  \
+        else if (nw == 8)                                                                      \
             hipLaunchKernelGGL((gemm_f16_pc_kernel<F>), grid, block, 0, st, g, cols, xh,        \
                                rscale, batch, mtiles, ntiles, kslices, part);                  \
         else                                                                                   \

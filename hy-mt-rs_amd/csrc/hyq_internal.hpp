@@ -175,7 +175,13 @@ int launch_decode_gguf(int fmt, const uint8_t *bytes, size_t nblocks, float *out
 // y[batch][w.rows] = rscale[batch] * (xh[batch][cols] W^T) (+ residual, which
 // may alias y), or the dense gate/up product h[batch][gate.rows] =
 // silu(gate . x) * (up . x).
-int launch_to_f16(const float *x, int rows, int K, _Float16 *xh, float *rscale, void *stream);
+// frag: xh in MFMA fragment order (gemm_frag_operand) instead of rows: the
+// 8 halves k = 16 b + 8 h .. + 7 of token t at
+// ((t / 32 * (K / 16) + b) * 64 + t % 32 + 32 h) * 8, each 32-token block
+// (frag_rows: the batch rounded up to whole blocks) one 64 K-byte run.
+int launch_to_f16(const float *x, int rows, int K, _Float16 *xh, float *rscale, void *stream,
+                  bool frag = false);
+inline size_t frag_rows(int batch) { return (size_t)(batch + 31) / 32 * 32; }
 // Q8_0 weights at batch 2..FEW_Q80_MAX_TOKENS with cols a multiple of 256
 // (hyq_gemm_few.hip): y[n][m] = x[n] . W[m], the activations rounded to f16
 // with a power-of-two row scale into xh (few_q80_operand_bytes, in MFMA
@@ -191,9 +197,15 @@ int launch_norm_to_f16(const float *x, int rows, int K, const float *norm, float
 // With `part` (part_floats >= kslices * batch * w.rows) a GEMM of few row
 // tiles runs as K slices into part, added in slice order: `kslices` of them,
 // or gemm_kslices when kslices is 0.
+// xfrag: xh is in fragment order, which only the 256-token tiles take (a
+// launch for which gemm_frag_operand holds).
 int launch_gemm_f16(int fmt, WView w, int cols, const _Float16 *xh, const float *rscale,
                     int batch, float *y, const float *residual, void *stream,
-                    float *part = nullptr, size_t part_floats = 0, int kslices = 0);
+                    float *part = nullptr, size_t part_floats = 0, int kslices = 0,
+                    bool xfrag = false);
+// Whether a one-weight product of this shape at `kslices` runs as 256-token
+// tiles (and can take its activations in fragment order).
+bool gemm_frag_operand(int fmt, int rows, int cols, int batch, int kslices);
 int gemm_kslices(int fmt, int M, int K);
 size_t gemm_split_floats(int fmt, int M, int N, int K);
 int matmul_kslices(int fmt, int M, int K, int batch);
@@ -212,7 +224,8 @@ struct GemmSegs {
     int nseg;
 };
 int launch_gemm_f16_segs(int fmt, GemmSegs g, int cols, const _Float16 *xh, const float *rscale,
-                         int batch, void *stream, int kslices = 1, float *part = nullptr);
+                         int batch, void *stream, int kslices = 1, float *part = nullptr,
+                         bool xfrag = false);
 int launch_gate_up_f16(int fmt, WView gate, WView up, int cols, const _Float16 *xh,
                        const float *rscale, int batch, float *h, void *stream);
 

@@ -604,5 +604,95 @@ __device__ __forceinline__ void k_loop_pc(const WSrc &wsrc, const XRow &xrow, co
     }
 }
 
+// The producer/consumer loop with the activations, in fragment order
+// (launch_to_f16 with frag), taken straight into the consumers' registers (no
+// LDS copy): consumer wave 4 + c owns tokens 64 c .. 64 c + 63 of the tile
+// against all BM weight rows (4 weight and 2 token fragments per 16-deep step
+// feed 8 MFMAs), loading its token fragments one step ahead into a two-set
+// register ring, each a contiguous KiB (lane l: 8 consecutive k of token
+// 32 j + l % 32); LDS holds only the dequantized weights. xsrc(r): the
+// fragment-order run of the 32-token block of tile token r (clamped into the
+// batch: tokens past it produce sums nobody writes). Same operands, same k
+// order per element as k_loop: bit-identical results. acc[i][j]: weight
+// block i, token block j.
+template <int F, class WSrc, class XSrc>
+__device__ __forceinline__ void k_loop_pcx(const WSrc &wsrc, const XSrc &xsrc, int K,
+                                           _Float16 *lds, f32x16 (&acc)[4][2], int kbase = 0)
+{
+    using D = Deq<F>;
+    const int t = threadIdx.x;
+    const bool prod = __builtin_amdgcn_readfirstlane(t) < 256;
+    const int steps = K / BK;
+    if (prod) {
+        const int lrow = t >> 1, h = t & 1;
+        WView wv{};
+        int row = -1;
+        wsrc(lrow, wv, row);
+        const RowPtr rp = D::rows(wv, row < 0 ? 0 : row);
+        typename D::Raw raw;
+        auto fetch = [&](int k0) {
+            if (row >= 0) D::load(raw, rp, kbase + k0, h);
+        };
+        auto put = [&](int k0, int b) {
+            _Float16 *Ws = lds + b * TILE_HALVES + lrow * LDK;
+            if (row >= 0) D::convert(raw, ((kbase + k0) >> 6) & 3, h, Ws);
+            else zero_half(Ws, h);
+        };
+        fetch(0);
+        put(0, 0);
+        if (steps > 1) fetch(BK);
+        __syncthreads();
+        for (int s = 0; s < steps; ++s) {
+            if (s + 1 < steps) {
+                put((s + 1) * BK, (s & 1) ^ 1);
+                if (s + 2 < steps) fetch((s + 2) * BK);
+            }
+            __syncthreads();
+        }
+        return;
+    }
+    const int lane = t & 63, c = (t >> 6) & 3;
+    const int r = lane & 31, kq = 8 * (lane >> 5);
+    // lane l's 8 halves of 16-deep step b in the block's fragment-order run
+    const _Float16 *xb[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) xb[j] = xsrc(64 * c + 32 * j) + (size_t)(kbase / 16) * 512 + lane * 8;
+    half8 B0[4][2], B1[4][2];
+    auto loadB = [&](half8 (&b)[4][2], int k0) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                b[kk][j] = *reinterpret_cast<const half8 *>(xb[j] + (size_t)(k0 / 16 + kk) * 512);
+    };
+    auto mma = [&](const _Float16 *Ws, const half8 (&b)[4][2]) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            half8 a[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                a[i] = *reinterpret_cast<const half8 *>(Ws + (32 * i + r) * LDK + 16 * kk + kq);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] =
+                        __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[kk][j], acc[i][j], 0, 0, 0);
+        }
+    };
+    loadB(B0, 0);
+    __syncthreads();
+    for (int s = 0; s < steps; s += 2) {
+        if (s + 1 < steps) loadB(B1, (s + 1) * BK);
+        mma(lds, B0);
+        __syncthreads();
+        if (s + 1 < steps) {
+            if (s + 2 < steps) loadB(B0, (s + 2) * BK);
+            mma(lds + TILE_HALVES, B1);
+            __syncthreads();
+        }
+    }
+}
+
 } // namespace tile
 } // namespace hyq
