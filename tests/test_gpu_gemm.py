@@ -63,6 +63,43 @@ def test_prefill_7b_full_size_sampled_rows(gpu_ctx, oracle, dtype, rows, cols):
     check_prefill_path(y[:, pick], y_ref, mag, NAMES[dtype])
 
 
+@pytest.mark.parametrize("dtype,rows,cols,batch", [(Q4_K, 14336, 4096, 300), (Q6_K, 4096, 14336, 270),
+                                                   (Q4_K, 6144, 4096, 257)],
+                         ids=["gate_up_q4k_300", "down_q6k_270", "qkv_q4k_257"])
+def test_prefill_7b_ragged_token_blocks(gpu_ctx, oracle, dtype, rows, cols, batch):
+    """The 256-token tiles with their activations in fragment order at token
+    counts that end inside a 32-token block (and inside a 256-token tile):
+    sampled weight rows, all tokens, against the oracle; the partial block's
+    rows past the batch feed sums that are never written."""
+    _print("gemm ragged", NAMES[dtype], rows, cols, batch)
+    w = random_matrix(dtype, rows, cols, seed=rows + batch)
+    x = np.random.default_rng(batch).normal(0, 1, batch * cols).astype(np.float32)
+    y = gpu_ctx.upload(dtype, w, (cols, rows)).matmul(x, batch).reshape(batch, rows)
+    assert np.all(np.isfinite(y))
+    rb = row_bytes(dtype, cols)
+    pick = np.sort(np.random.default_rng(6).choice(rows, 64, replace=False))
+    pick[-1] = rows - 1
+    sub = np.concatenate([w[r * rb:(r + 1) * rb] for r in pick])
+    y_ref, mag = oracle.matmul_f64(dtype, sub, len(pick), cols, x, batch)
+    check_prefill_path(y[:, pick], y_ref, mag, NAMES[dtype])
+
+
+def test_fragment_tiles_equal_row_tiles(gpu_ctx):
+    """At 300 tokens a [14336 x 4096] product runs as 256-token tiles with its
+    activations in fragment order; at 200 tokens the same weight runs as
+    128-token tiles with its activations copied through LDS. The same
+    operands meet in the same k order either way, so the first 200 token rows
+    agree bit for bit."""
+    rows, cols = 14336, 4096
+    w = random_matrix(Q4_K, rows, cols, seed=11)
+    x = np.random.default_rng(11).normal(0, 1, 300 * cols).astype(np.float32)
+    W = gpu_ctx.upload(Q4_K, w, (cols, rows))
+    big = W.matmul(x, 300).reshape(300, rows)
+    small = W.matmul(x[:200 * cols], 200).reshape(200, rows)
+    assert np.array_equal(big[:200].view(np.uint32), small.view(np.uint32))
+    W.release()
+
+
 def test_batched_rows_are_independent_of_batch(gpu_ctx):
     """Each token's output row does not depend on the other tokens of the
     batch, for batches on the same side of one 128-token tile: above it the
