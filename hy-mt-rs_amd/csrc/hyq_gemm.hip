@@ -45,6 +45,15 @@ __device__ __forceinline__ int xcd_tile(int total)
 // src = r, or ptok[order[r]] when order is given; rows r >= *count (when
 // count is given) are left alone. A row with a zero, infinite or NaN maximum
 // keeps scale 1 (and its infinities / NaNs propagate).
+//
+// R > 0 (rows of at most 1024 R values): thread t holds float4s t + 256 j,
+// j < R, of the row (and of the norm vector) in registers, all their loads
+// issued at once (clamped into the row) before the first is used, so a row
+// costs one memory latency instead of one per float4 of a thread, and the
+// passes (sum of squares, maximum, conversion) read the registers. R = 0
+// loops over the row in global memory (any length). Every value is formed
+// by the same operations in the same order either way.
+template <int R>
 __global__ __launch_bounds__(256) void rows_to_f16_kernel(const float *__restrict__ x, int K,
                                                           const int *__restrict__ order,
                                                           const int *__restrict__ ptok,
@@ -53,7 +62,7 @@ __global__ __launch_bounds__(256) void rows_to_f16_kernel(const float *__restric
                                                           float eps,
                                                           _Float16 *__restrict__ xh,
                                                           float *__restrict__ rscale,
-                                                          bool frag = false)
+                                                          bool frag)
 {
     __shared__ float wred[4];
     const int r = blockIdx.x;
@@ -62,13 +71,36 @@ __global__ __launch_bounds__(256) void rows_to_f16_kernel(const float *__restric
     const float4 *x4 = reinterpret_cast<const float4 *>(x + src * K);
     const float4 *n4p = reinterpret_cast<const float4 *>(norm);
     const int t = threadIdx.x, n4 = K / 4;
+    constexpr int NJ = R > 0 ? R : 1;
+    float4 xv[NJ], wv[NJ];
+    if constexpr (R > 0) {
+#pragma unroll
+        for (int j = 0; j < R; ++j) xv[j] = x4[min(t + 256 * j, n4 - 1)];
+        if (norm) {
+#pragma unroll
+            for (int j = 0; j < R; ++j) wv[j] = n4p[min(t + 256 * j, n4 - 1)];
+        }
+    }
+    // float4 i = t + 256 j of the row, before the norm
+    auto raw = [&](int j, int i) { return R > 0 ? xv[j] : x4[i]; };
+    // The passes below visit i = t + 256 j for j = 0, 1, ... while i < n4:
+    // unrolled over the registers for R > 0, a loop for R = 0.
+    auto each = [&](auto &&f) {
+        if constexpr (R > 0) {
+#pragma unroll
+            for (int j = 0; j < R; ++j)
+                if (t + 256 * j < n4) f(j, t + 256 * j);
+        } else {
+            for (int i = t; i < n4; i += 256) f(0, i);
+        }
+    };
     float s = 1.f;
     if (norm) {
         float ss = 0.f;
-        for (int i = t; i < n4; i += 256) {
-            const float4 v = x4[i];
+        each([&](int j, int i) {
+            const float4 v = raw(j, i);
             ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
-        }
+        });
         ss = wave::sum64(ss);
         if ((t & 63) == 0) wred[t >> 6] = ss;
         __syncthreads();
@@ -76,10 +108,10 @@ __global__ __launch_bounds__(256) void rows_to_f16_kernel(const float *__restric
         __syncthreads();
         s = 1.0f / sqrtf(ss / (float)K + eps);
     }
-    auto value = [&](int i) {
-        float4 v = x4[i];
+    auto value = [&](int j, int i) {
+        float4 v = raw(j, i);
         if (norm) {
-            const float4 w = n4p[i];
+            const float4 w = R > 0 ? wv[j] : n4p[i];
             if (4 * i < (K & ~15))
                 v = make_float4(v.x * (w.x * s), v.y * (w.y * s), v.z * (w.z * s),
                                 v.w * (w.w * s));
@@ -89,11 +121,11 @@ __global__ __launch_bounds__(256) void rows_to_f16_kernel(const float *__restric
         return v;
     };
     float m = 0.f;
-    for (int i = t; i < n4; i += 256) {
-        const float4 v = value(i);
+    each([&](int j, int i) {
+        const float4 v = value(j, i);
         m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         if (v.x != v.x || v.y != v.y || v.z != v.z || v.w != v.w) m = INFINITY;
-    }
+    });
     m = wave::max64(m);
     if ((t & 63) == 0) wred[t >> 6] = m;
     __syncthreads();
@@ -103,15 +135,34 @@ __global__ __launch_bounds__(256) void rows_to_f16_kernel(const float *__restric
     if (t == 0) rscale[r] = ldexpf(1.0f, e);
     // (fragment order: values 4i .. 4i + 3 stay together, k % 8 being 0 or 4)
     _Float16 *o = frag ? xh + (size_t)(r / 32) * 32 * K + (size_t)(r % 32) * 8 : xh + (size_t)r * K;
-    for (int i = t; i < n4; i += 256) {
-        const float4 v = value(i);
+    each([&](int j, int i) {
+        const float4 v = value(j, i);
         const half2v a = __builtin_convertvector((float2v){v.x * inv, v.y * inv}, half2v);
         const half2v b = __builtin_convertvector((float2v){v.z * inv, v.w * inv}, half2v);
         const int k = 4 * i;
         _Float16 *q = frag ? o + (size_t)(k / 16) * 512 + 256 * ((k / 8) & 1) + (k & 4) : o + k;
         *reinterpret_cast<half2v *>(q) = a;
         *reinterpret_cast<half2v *>(q + 2) = b;
-    }
+    });
+}
+
+// rows_to_f16_kernel for rows of K values on `rows` workgroups: the
+// register form with the fewest registers that holds the row, else the loop.
+void launch_rows_to_f16(int rows, int K, hipStream_t st, const float *x, const int *order,
+                        const int *ptok, const int *count, const float *norm, float eps,
+                        _Float16 *xh, float *rscale, bool frag)
+{
+    const int need = K < 4 ? 1 << 30 : (K + 1023) / 1024;
+#define HYQ_ROWS_F16(RR)                                                                           hipLaunchKernelGGL(rows_to_f16_kernel<RR>, dim3(rows), dim3(256), 0, st, x, K, order, ptok, \
+                       count, norm, eps, xh, rscale, frag)
+    if (need <= 2) HYQ_ROWS_F16(2);
+    else if (need <= 4) HYQ_ROWS_F16(4);
+    else if (need <= 6) HYQ_ROWS_F16(6);
+    else if (need <= 8) HYQ_ROWS_F16(8);
+    else if (need <= 12) HYQ_ROWS_F16(12);
+    else if (need <= 16) HYQ_ROWS_F16(16);
+    else HYQ_ROWS_F16(0);
+#undef HYQ_ROWS_F16
 }
 
 // Y[n][m] = (X[n] . W[m]) * rscale[n], plus residual[n][m] when given (the
@@ -262,9 +313,10 @@ __global__ __launch_bounds__(PC_THREADS, 1) void gemm_f16_pc_kernel(
 
 // The 256-token tiles with the activations, in fragment order
 // (launch_to_f16 with frag), straight into the consumers' registers
-// (k_loop_pcx): same grid and tile order as gemm_f16_pc_kernel, bit-identical
+// (k_loop_pcx): the tile order of gemm_f16_pc_kernel over tiles of 32 NI
+// weight rows (128, or 96 where that fills more of the CUs), bit-identical
 // results; consumer wave 4 + c writes tokens 64 c ...
-template <int F>
+template <int F, int NI>
 __global__ __launch_bounds__(PC_THREADS, 1) void gemm_f16_pcx_kernel(
     GemmSegs g, int K, const _Float16 *__restrict__ xh, const float *__restrict__ rscale, int N,
     int mtiles, int ntiles, int kslices, float *__restrict__ part)
@@ -276,11 +328,11 @@ __global__ __launch_bounds__(PC_THREADS, 1) void gemm_f16_pcx_kernel(
     while (sg + 1 < g.nseg && mt >= g.s[sg].tiles) mt -= g.s[sg++].tiles;
     const GemmSeg &S = g.s[sg];
     const int M = S.rows;
-    const int m0 = mt * BM, n0 = (T % ntiles) * 256;
+    const int m0 = mt * (32 * NI), n0 = (T % ntiles) * 256;
 
-    f32x16 acc[4][2];
+    f32x16 acc[NI][2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -295,14 +347,14 @@ __global__ __launch_bounds__(PC_THREADS, 1) void gemm_f16_pcx_kernel(
         return xh + (size_t)min((n0 + r) / 32, (N - 1) / 32) * 32 * K;
     };
     const int kslice = K / kslices;
-    k_loop_pcx<F>(wsrc, xsrc, kslice, lds, acc, blockIdx.y * kslice);
+    k_loop_pcx<F, NI>(wsrc, xsrc, kslice, lds, acc, blockIdx.y * kslice);
     if (threadIdx.x < 256) return; // the producers
     const int c = (threadIdx.x >> 6) & 3;
 
     float *y = kslices > 1 ? part + (size_t)blockIdx.y * N * M : S.y;
     const float *residual = kslices > 1 ? nullptr : S.residual;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int n = n0 + 64 * c + 32 * j + (threadIdx.x & 31);
@@ -946,8 +998,8 @@ int launch_to_f16(const float *x, int rows, int K, _Float16 *xh, float *rscale, 
     if (!frag) return launch_norm_to_f16(x, rows, K, nullptr, 0.f, xh, rscale, stream);
     if (rows <= 0) return 0;
     if (K % 16) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(rows_to_f16_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream, x, K,
-                       nullptr, nullptr, nullptr, nullptr, 0.f, xh, rscale, true);
+    launch_rows_to_f16(rows, K, (hipStream_t)stream, x, nullptr, nullptr, nullptr, nullptr, 0.f,
+                       xh, rscale, true);
     return (int)hipGetLastError();
 }
 
@@ -956,8 +1008,8 @@ int launch_norm_to_f16(const float *x, int rows, int K, const float *norm, float
 {
     if (rows <= 0) return 0;
     if (K % 4) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(rows_to_f16_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream, x, K,
-                       nullptr, nullptr, nullptr, norm, eps, xh, rscale);
+    launch_rows_to_f16(rows, K, (hipStream_t)stream, x, nullptr, nullptr, nullptr, norm, eps, xh,
+                       rscale, false);
     return (int)hipGetLastError();
 }
 
@@ -1097,13 +1149,29 @@ int launch_gemm_f16_segs(int fmt, GemmSegs g, int cols, const _Float16 *xh, cons
     // fragment-order activations: only the 256-token tiles of one weight
     if (xfrag && (nw != 8 || g.nseg != 1 || cols % 16)) return (int)hipErrorInvalidValue;
     const int ntiles = (batch + bn - 1) / bn;
+    // The fragment-order kernel takes 96-row tiles where they need fewer
+    // rounds of workgroups over the 256 CUs per row of a tile (rounds x tile
+    // rows): a [6144 x 4096] product in two K slices at 512 tokens runs as
+    // 64 x 2 x 2 = 256 workgroups of 96 rows instead of 192 of 128.
+    bool rows96 = false;
+    if (xfrag) {
+        const int m96 = (g.s[0].rows + 95) / 96;
+        auto rounds = [&](int mt) { return (mt * ntiles * kslices + 255) / 256; };
+        if (rounds(m96) * 96 < rounds(mtiles) * BM) {
+            rows96 = true;
+            mtiles = g.s[0].tiles = m96;
+        }
+    }
     const int per = (mtiles * ntiles + 7) / 8;
     dim3 grid(8 * per, kslices), block(64 * nw);
     hipStream_t st = (hipStream_t)stream;
 #define HYQ_GEMM(F)                                                                            \
     case F:                                                                                    \
-        if (xfrag)                                                                             \
-            hipLaunchKernelGGL((gemm_f16_pcx_kernel<F>), grid, block, 0, st, g, cols, xh,       \
+        if (xfrag && rows96)                                                                   \
+            hipLaunchKernelGGL((gemm_f16_pcx_kernel<F, 3>), grid, block, 0, st, g, cols, xh,    \
+                               rscale, batch, mtiles, ntiles, kslices, part);                  \
+        else if (xfrag)                                                                        \
+            hipLaunchKernelGGL((gemm_f16_pcx_kernel<F, 4>), grid, block, 0, st, g, cols, xh,    \
                                rscale, batch, mtiles, ntiles, kslices, part);                  \
         else if (nw == 8)                                                                      \
             hipLaunchKernelGGL((gemm_f16_pc_kernel<F>), grid, block, 0, st, g, cols, xh,        \
@@ -1248,8 +1316,8 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
                            moe_q4k_down_slices(mid) > 1 ? outp2 : nullptr);
         return (int)hipGetLastError();
     }
-    hipLaunchKernelGGL(rows_to_f16_kernel, dim3(npairs), dim3(256), 0, st, x, hidden, order,
-                       ptok, eoff + experts, nullptr, 0.f, xg, xscale);
+    launch_rows_to_f16(npairs, hidden, st, x, order, ptok, eoff + experts, nullptr, 0.f, xg,
+                       xscale, false);
     {
         const int mtiles = (mid + 63) / 64;
         const int per = (mtiles * L.max_tiles + 7) / 8;
@@ -1269,8 +1337,8 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
         }
 #undef HYQ_MOE_GU
     }
-    hipLaunchKernelGGL(rows_to_f16_kernel, dim3(npairs), dim3(256), 0, st, h32, mid, nullptr,
-                       nullptr, eoff + experts, nullptr, 0.f, H, hscale);
+    launch_rows_to_f16(npairs, mid, st, h32, nullptr, nullptr, eoff + experts, nullptr, 0.f, H,
+                       hscale, false);
     {
         const int mtiles = (hidden + BM - 1) / BM;
         const int per = (mtiles * L.max_tiles + 7) / 8;

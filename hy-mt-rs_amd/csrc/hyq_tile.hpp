@@ -607,27 +607,31 @@ __device__ __forceinline__ void k_loop_pc(const WSrc &wsrc, const XRow &xrow, co
 // The producer/consumer loop with the activations, in fragment order
 // (launch_to_f16 with frag), taken straight into the consumers' registers (no
 // LDS copy): consumer wave 4 + c owns tokens 64 c .. 64 c + 63 of the tile
-// against all BM weight rows (4 weight and 2 token fragments per 16-deep step
-// feed 8 MFMAs), loading its token fragments one step ahead into a two-set
-// register ring, each a contiguous KiB (lane l: 8 consecutive k of token
-// 32 j + l % 32); LDS holds only the dequantized weights. xsrc(r): the
-// fragment-order run of the 32-token block of tile token r (clamped into the
-// batch: tokens past it produce sums nobody writes). Same operands, same k
-// order per element as k_loop: bit-identical results. acc[i][j]: weight
-// block i, token block j.
-template <int F, class WSrc, class XSrc>
+// against all 32 NI weight rows (NI weight and 2 token fragments per 16-deep
+// step feed 2 NI MFMAs), loading its token fragments one step ahead into a
+// two-set register ring, each a contiguous KiB (lane l: 8 consecutive k of
+// token 32 j + l % 32); LDS holds only the dequantized weights. NI = 4 is
+// the 128-row tile; NI = 3 a 96-row tile (producer threads of rows 96-127
+// idle), for grids that 128-row tiles would leave short of the CUs.
+// xsrc(r): the fragment-order run of the 32-token block of tile token r
+// (clamped into the batch: tokens past it produce sums nobody writes). Same
+// operands, same k order per element as k_loop: bit-identical results.
+// acc[i][j]: weight block i, token block j.
+template <int F, int NI, class WSrc, class XSrc>
 __device__ __forceinline__ void k_loop_pcx(const WSrc &wsrc, const XSrc &xsrc, int K,
-                                           _Float16 *lds, f32x16 (&acc)[4][2], int kbase = 0)
+                                           _Float16 *lds, f32x16 (&acc)[NI][2], int kbase = 0)
 {
+    static_assert(NI == 3 || NI == 4, "96- or 128-row tiles");
     using D = Deq<F>;
     const int t = threadIdx.x;
     const bool prod = __builtin_amdgcn_readfirstlane(t) < 256;
     const int steps = K / BK;
     if (prod) {
         const int lrow = t >> 1, h = t & 1;
+        const bool used = lrow < 32 * NI;
         WView wv{};
         int row = -1;
-        wsrc(lrow, wv, row);
+        if (used) wsrc(lrow, wv, row);
         const RowPtr rp = D::rows(wv, row < 0 ? 0 : row);
         typename D::Raw raw;
         auto fetch = [&](int k0) {
@@ -636,7 +640,7 @@ __device__ __forceinline__ void k_loop_pcx(const WSrc &wsrc, const XSrc &xsrc, i
         auto put = [&](int k0, int b) {
             _Float16 *Ws = lds + b * TILE_HALVES + lrow * LDK;
             if (row >= 0) D::convert(raw, ((kbase + k0) >> 6) & 3, h, Ws);
-            else zero_half(Ws, h);
+            else if (used) zero_half(Ws, h);
         };
         fetch(0);
         put(0, 0);
@@ -668,12 +672,12 @@ __device__ __forceinline__ void k_loop_pcx(const WSrc &wsrc, const XSrc &xsrc, i
     auto mma = [&](const _Float16 *Ws, const half8 (&b)[4][2]) {
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-            half8 a[4];
+            half8 a[NI];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < NI; ++i)
                 a[i] = *reinterpret_cast<const half8 *>(Ws + (32 * i + r) * LDK + 16 * kk + kq);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < NI; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
                     acc[i][j] =
