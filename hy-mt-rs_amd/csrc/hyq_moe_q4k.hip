@@ -389,6 +389,7 @@ __global__ __launch_bounds__(256, 2) void moe_q4k_gate_up_kernel(
 // which needs nothing the SiLU rows make. They come first so that they are
 // dispatched while the SiLU rows are: their registers hold one workgroup
 // per CU, and the SiLU rows fill the other CUs.
+template <int RS>
 __global__ __launch_bounds__(64 * few::WAVES) void silu_rows_kernel(
     const float *__restrict__ gpart, const float *__restrict__ upart, int ks, size_t part_stride,
     int mid, const int *__restrict__ valid, uint4 *__restrict__ hop, uint2 *__restrict__ hhs,
@@ -413,14 +414,34 @@ __global__ __launch_bounds__(64 * few::WAVES) void silu_rows_kernel(
     const int t = threadIdx.x;
     const size_t row = (size_t)q * mid;
     float *hl = lds.s.hl;
-    float m = 0.f;
-    for (int i = t; i < mid; i += NT) {
-        float gv = gpart[row + i], uv = upart[row + i];
-        if (ks > 1) {
-            gv = gv + gpart[part_stride + row + i];
-            uv = uv + upart[part_stride + row + i];
+    // values t + NT j, j < RS (mid <= NT RS): every load issued (clamped
+    // into the row) before the first is used
+    float gv[RS], uv[RS], g2[RS], u2[RS];
+#pragma unroll
+    for (int j = 0; j < RS; ++j) {
+        const size_t i = row + min(t + NT * j, mid - 1);
+        gv[j] = gpart[i];
+        uv[j] = upart[i];
+    }
+    if (ks > 1) {
+#pragma unroll
+        for (int j = 0; j < RS; ++j) {
+            const size_t i = part_stride + row + min(t + NT * j, mid - 1);
+            g2[j] = gpart[i];
+            u2[j] = upart[i];
         }
-        const float v = silu_mul(gv, uv);
+    }
+    float m = 0.f;
+#pragma unroll
+    for (int j = 0; j < RS; ++j) {
+        const int i = t + NT * j;
+        if (i >= mid) break;
+        float g = gv[j], u = uv[j];
+        if (ks > 1) {
+            g = g + g2[j];
+            u = u + u2[j];
+        }
+        const float v = silu_mul(g, u);
         hl[i] = v;
         m = fmaxf(m, fabsf(v));
         if (v != v) m = INFINITY;
@@ -550,9 +571,12 @@ int launch_moe_q4k(WView gate, WView up, WView down, int hidden, int mid, const 
                        eoff, tiles, ntiles, ctok, xop, xhs, xsc, gpart, upart, gstride, mid / 64);
     int cgroups = 0;
     const int stiles = shared ? few::q80_tiles(shared->rows, tokens, &cgroups) : 0;
-    hipLaunchKernelGGL(silu_rows_kernel, dim3(npairs + stiles), dim3(64 * few::WAVES), 0, st,
-                       gpart, upart, moe_kslices(hidden), gstride, mid, valid, hop, hhs, hsc,
-                       stiles, shared ? *shared : WView{}, hidden, xf, xsc, tokens, y, cgroups);
+    // the SiLU rows' widths: mid <= MOE_Q4K_MAX_KL (moe_q4k_fits)
+    static_assert(MOE_Q4K_MAX_KL <= 4 * 64 * few::WAVES, "four values per SiLU-row thread");
+    auto silu = mid <= 3 * 64 * few::WAVES ? silu_rows_kernel<3> : silu_rows_kernel<4>;
+    hipLaunchKernelGGL(silu, dim3(npairs + stiles), dim3(64 * few::WAVES), 0, st, gpart, upart,
+                       moe_kslices(hidden), gstride, mid, valid, hop, hhs, hsc, stiles,
+                       shared ? *shared : WView{}, hidden, xf, xsc, tokens, y, cgroups);
     hipLaunchKernelGGL(moe_q4k_down_kernel, grid, dim3(256), (size_t)34 * mid, st, down, hidden,
                        mid, eoff, tiles, ntiles, cpos, hop, hhs, hsc, outp, hidden / 64);
     return (int)hipGetLastError();
