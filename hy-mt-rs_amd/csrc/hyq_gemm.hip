@@ -35,6 +35,18 @@ __device__ __forceinline__ int xcd_tile(int total)
     return (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
 }
 
+// The token row of workgroup b when the rows are written in fragment order.
+// There a 128-byte line holds 16 bytes of each of 8 consecutive rows
+// (r / 8 equal), and workgroup b runs on XCD b % 8: with row
+// 8 (8 (j / 8) + b % 8) + j % 8, j = b / 8, the 8 rows of a line run on one
+// XCD, whose L2 merges their pieces into whole lines, instead of on eight.
+// A bijection of [0, 64 n) onto itself.
+__device__ __forceinline__ int frag_row(int b)
+{
+    const int j = b >> 3;
+    return 8 * (8 * (j >> 3) + (b & 7)) + (j & 7);
+}
+
 // One workgroup per row: xh[r][k] = f16(v[k] * 2^-e) and rscale[r] = 2^e,
 // where v = x[src] (or, with `norm`, its RMSNorm v[k] = x[k] * (norm[k] * s)
 // over whole 16-value steps and x[k] * s * norm[k] over a tail, s = 1 /
@@ -55,6 +67,7 @@ __device__ __forceinline__ int xcd_tile(int total)
 // by the same operations in the same order either way.
 template <int R>
 __global__ __launch_bounds__(256) void rows_to_f16_kernel(const float *__restrict__ x, int K,
+                                                          int nrows,
                                                           const int *__restrict__ order,
                                                           const int *__restrict__ ptok,
                                                           const int *__restrict__ count,
@@ -65,8 +78,8 @@ __global__ __launch_bounds__(256) void rows_to_f16_kernel(const float *__restric
                                                           bool frag)
 {
     __shared__ float wred[4];
-    const int r = blockIdx.x;
-    if (count && r >= *count) return;
+    const int r = frag ? frag_row((int)blockIdx.x) : (int)blockIdx.x;
+    if (r >= nrows || (count && r >= *count)) return;
     const size_t src = order ? (size_t)ptok[order[r]] : (size_t)r;
     const float4 *x4 = reinterpret_cast<const float4 *>(x + src * K);
     const float4 *n4p = reinterpret_cast<const float4 *>(norm);
@@ -146,14 +159,17 @@ __global__ __launch_bounds__(256) void rows_to_f16_kernel(const float *__restric
     });
 }
 
-// rows_to_f16_kernel for rows of K values on `rows` workgroups: the
-// register form with the fewest registers that holds the row, else the loop.
+// rows_to_f16_kernel for rows of K values: the register form with the fewest
+// registers that holds the row, else the loop. In fragment order the grid
+// is the rows rounded up to 64 (see frag_row).
 void launch_rows_to_f16(int rows, int K, hipStream_t st, const float *x, const int *order,
                         const int *ptok, const int *count, const float *norm, float eps,
                         _Float16 *xh, float *rscale, bool frag)
 {
     const int need = K < 4 ? 1 << 30 : (K + 1023) / 1024;
-#define HYQ_ROWS_F16(RR)                                                                           hipLaunchKernelGGL(rows_to_f16_kernel<RR>, dim3(rows), dim3(256), 0, st, x, K, order, ptok, \
+    const dim3 grid(frag ? (rows + 63) / 64 * 64 : rows);
+#define HYQ_ROWS_F16(RR)                                                                       \
+    hipLaunchKernelGGL(rows_to_f16_kernel<RR>, grid, dim3(256), 0, st, x, K, rows, order, ptok, \
                        count, norm, eps, xh, rscale, frag)
     if (need <= 2) HYQ_ROWS_F16(2);
     else if (need <= 4) HYQ_ROWS_F16(4);
