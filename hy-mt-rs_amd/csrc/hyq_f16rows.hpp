@@ -21,4 +21,16 @@ __device__ __forceinline__ int f16_row_exponent(float m)
     return e;
 }
 
+// The token row of workgroup b when the rows are written in an MFMA
+// fragment order whose 128-byte lines hold 16 bytes of each of 8
+// consecutive rows (r / 8 equal), and workgroup b runs on XCD b % 8: with row
+// 8 (8 (j / 8) + b % 8) + j % 8, j = b / 8, the 8 rows of a line run on one
+// XCD, whose L2 merges their pieces into whole lines, instead of on eight.
+// A bijection of [0, 64 n) onto itself.
+__device__ __forceinline__ int frag_row(int b)
+{
+    const int j = b >> 3;
+    return 8 * (8 * (j >> 3) + (b & 7)) + (j & 7);
+}
+
 } // namespace hyq

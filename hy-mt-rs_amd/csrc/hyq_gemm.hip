@@ -35,18 +35,6 @@ __device__ __forceinline__ int xcd_tile(int total)
     return (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
 }
 
-// The token row of workgroup b when the rows are written in fragment order.
-// There a 128-byte line holds 16 bytes of each of 8 consecutive rows
-// (r / 8 equal), and workgroup b runs on XCD b % 8: with row
-// 8 (8 (j / 8) + b % 8) + j % 8, j = b / 8, the 8 rows of a line run on one
-// XCD, whose L2 merges their pieces into whole lines, instead of on eight.
-// A bijection of [0, 64 n) onto itself.
-__device__ __forceinline__ int frag_row(int b)
-{
-    const int j = b >> 3;
-    return 8 * (8 * (j >> 3) + (b & 7)) + (j & 7);
-}
-
 // One workgroup per row: xh[r][k] = f16(v[k] * 2^-e) and rscale[r] = 2^e,
 // where v = x[src] (or, with `norm`, its RMSNorm v[k] = x[k] * (norm[k] * s)
 // over whole 16-value steps and x[k] * s * norm[k] over a tail, s = 1 /

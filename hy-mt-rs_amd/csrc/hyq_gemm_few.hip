@@ -16,16 +16,18 @@ namespace hyq {
 
 namespace {
 
-// One workgroup per token row n of the chunks (n < chunks * 16): its f16
+// One workgroup per token row n of the chunks (n < nrows = chunks * 16;
+// workgroup b takes row frag_row(b), so a line's 8 tokens share an XCD): its f16
 // values (x[n] scaled by 2^-e, e from the row's largest magnitude as
 // launch_to_f16 forms it; zeros for n >= N) into the fragment layout, and
 // rscale[n] = 2^e.
 __global__ __launch_bounds__(256) void few_rows_kernel(const float *__restrict__ x, int K, int N,
-                                                       _Float16 *__restrict__ xf,
+                                                       int nrows, _Float16 *__restrict__ xf,
                                                        float *__restrict__ rscale)
 {
     __shared__ float wred[4];
-    const int n = (int)blockIdx.x, t = (int)threadIdx.x, nb = K / 32;
+    const int n = frag_row((int)blockIdx.x), t = (int)threadIdx.x, nb = K / 32;
+    if (n >= nrows) return;
     const bool live = n < N;
     const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)(live ? n : 0) * K);
     float m = 0.f;
@@ -71,8 +73,9 @@ int launch_few_q80(WView w, int cols, const float *x, _Float16 *xh, float *rscal
 {
     if (!few_q80_fits(w.rows, cols, batch)) return (int)hipErrorInvalidValue;
     const int nrows = (batch + few::CHUNK - 1) / few::CHUNK * few::CHUNK;
-    hipLaunchKernelGGL(few_rows_kernel, dim3(nrows), dim3(256), 0, (hipStream_t)stream, x, cols,
-                       batch, xh, rscale);
+    // rows n < nrows, on workgroups frag_row^-1(n): a line's 8 tokens on one XCD
+    hipLaunchKernelGGL(few_rows_kernel, dim3((nrows + 63) / 64 * 64), dim3(256), 0,
+                       (hipStream_t)stream, x, cols, batch, nrows, xh, rscale);
     int cgroups = 0;
     const int tiles = few::q80_tiles(w.rows, batch, &cgroups);
     hipLaunchKernelGGL(few_q80_kernel, dim3(tiles), dim3(64 * few::WAVES), 0,
