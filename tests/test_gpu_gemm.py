@@ -64,13 +64,14 @@ def test_prefill_7b_full_size_sampled_rows(gpu_ctx, oracle, dtype, rows, cols):
 
 
 @pytest.mark.parametrize("dtype,rows,cols,batch", [(Q4_K, 14336, 4096, 300), (Q6_K, 4096, 14336, 270),
-                                                   (Q4_K, 6144, 4096, 257)],
-                         ids=["gate_up_q4k_300", "down_q6k_270", "qkv_q4k_257"])
+                                                   (Q4_K, 6144, 4096, 257), (Q4_K, 6112, 4096, 300)],
+                         ids=["gate_up_q4k_300", "down_q6k_270", "qkv_q4k_257", "rows96_partial_300"])
 def test_prefill_7b_ragged_token_blocks(gpu_ctx, oracle, dtype, rows, cols, batch):
     """The 256-token tiles with their activations in fragment order at token
     counts that end inside a 32-token block (and inside a 256-token tile):
     sampled weight rows, all tokens, against the oracle; the partial block's
-    rows past the batch feed sums that are never written."""
+    rows past the batch feed sums that are never written. [6144 x 4096] and
+    [6112 x 4096] run as 96-row tiles (the latter's last tile 64 rows)."""
     _print("gemm ragged", NAMES[dtype], rows, cols, batch)
     w = random_matrix(dtype, rows, cols, seed=rows + batch)
     x = np.random.default_rng(batch).normal(0, 1, batch * cols).astype(np.float32)
