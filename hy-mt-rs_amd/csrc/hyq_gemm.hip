@@ -978,8 +978,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(float *__restrict__ ou
                                                           const int *__restrict__ tlist,
                                                           const int *__restrict__ order,
                                                           const float *__restrict__ pw,
-                                                          const float *__restrict__ outp,
-                                                          const float *__restrict__ outp2)
+                                                          const float *__restrict__ outp)
 {
     const int t = blockIdx.y;
     const int col = blockIdx.x * 256 + threadIdx.x;
@@ -987,9 +986,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(float *__restrict__ ou
     float acc = out[(size_t)t * hidden + col];
     for (int i = toff[t]; i < toff[t + 1]; ++i) {
         const int q = tlist[i];
-        float v = outp[(size_t)q * hidden + col];
-        if (outp2) v = v + outp2[(size_t)q * hidden + col]; // the second K slice
-        acc = acc + pw[order[q]] * v;
+        acc = acc + pw[order[q]] * outp[(size_t)q * hidden + col];
     }
     out[(size_t)t * hidden + col] = acc;
 }
@@ -1232,7 +1229,6 @@ MoeLayout moe_layout(int tokens, int npairs, int experts, int hidden, int mid)
     L.ctok = take(4 * cols);
     L.gpart = take(4 * 2 * (size_t)npairs * mid);
     L.upart = take(4 * 2 * (size_t)npairs * mid);
-    L.outp2 = take(4 * (size_t)npairs * hidden);
     // f16 fragments of the token rows for a fused Q8_0 shared projection
     L.xf = take(tokens <= FEW_Q80_MAX_TOKENS ? few_q80_operand_bytes(hidden, tokens) : 0);
     L.bytes = off;
@@ -1307,17 +1303,15 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
                            experts, eoff, order, rank, toff, tlist, tiles, ntiles,
                            few ? moe_q4k_chunk() : BN);
     if (few) {
-        float *outp2 = (float *)(scratch + L.outp2);
         int rc = launch_moe_q4k(gate, up, down, hidden, mid, x, tokens, ptok, eoff, eoff + experts,
                                 order, tiles, ntiles, L.max_tiles_few, npairs, fast, xop, xhs,
                                 xsc, cpos, ctok, (float *)(scratch + L.gpart),
                                 (float *)(scratch + L.upart), (uint4 *)(scratch + L.hop),
                                 (uint2 *)(scratch + L.hhs), (float *)(scratch + L.hsc), outp,
-                                outp2, stream, shared, xf, out);
+                                stream, shared, xf, out);
         if (rc) return rc;
         hipLaunchKernelGGL(moe_combine_kernel, dim3((hidden + 255) / 256, tokens), dim3(256), 0,
-                           st, out, hidden, toff, tlist, order, pw, outp,
-                           moe_q4k_down_slices(mid) > 1 ? outp2 : nullptr);
+                           st, out, hidden, toff, tlist, order, pw, outp);
         return (int)hipGetLastError();
     }
     launch_rows_to_f16(npairs, hidden, st, x, order, ptok, eoff + experts, nullptr, 0.f, xg,
@@ -1363,7 +1357,7 @@ int launch_moe(int fmt_gu, int fmt_down, WView gate, WView up, WView down, int h
 #undef HYQ_MOE_DN
     }
     hipLaunchKernelGGL(moe_combine_kernel, dim3((hidden + 255) / 256, tokens), dim3(256), 0, st,
-                       out, hidden, toff, tlist, order, pw, outp, (const float *)nullptr);
+                       out, hidden, toff, tlist, order, pw, outp);
     return (int)hipGetLastError();
 }
 

@@ -232,7 +232,7 @@ int launch_gate_up_f16(int fmt, WView gate, WView up, int cols, const _Float16 *
 // Byte offsets of the MoE scratch regions (hyq_gemm.hip: moe_layout).
 struct MoeLayout {
     size_t eoff, order, rank, toff, tlist, tiles, ntiles, xg, xscale, h32, h, hscale, outp;
-    size_t xop, xhs, xsc, hop, hhs, hsc, cpos, ctok, gpart, upart, outp2, xf, bytes;
+    size_t xop, xhs, xsc, hop, hhs, hsc, cpos, ctok, gpart, upart, xf, bytes;
     int max_tiles, max_tiles_few;
 };
 MoeLayout moe_layout(int tokens, int npairs, int experts, int hidden, int mid);
@@ -253,7 +253,7 @@ bool moe_fuses_shared(int fmt_gu, int fmt_down, WView gate, WView up, WView down
 // token rows of x and hop/hhs/hsc those of the pairs' SiLU rows
 // (hyq_moe_operand.hpp), cpos / ctok each chunk column's pair position and
 // token (the column's rows), gpart / upart the gate and up partial rows of
-// the K slices [2][npairs][mid], outp2 the down product's second K slice.
+// the K slices [2][npairs][mid], outp the down product's rows [npairs][hidden].
 // have_ops: the plan's launch already wrote xop/xhs/xsc and cpos/ctok.
 // With `shared` (Q8_0, hidden columns, at most FEW_Q80_MAX_TOKENS tokens,
 // have_ops, and the plan's launch given xf) the SiLU-rows launch also runs
@@ -263,12 +263,10 @@ int launch_moe_q4k(WView gate, WView up, WView down, int hidden, int mid, const 
                    const int *order, const int *tiles, const int *ntiles, int max_tiles,
                    int npairs, bool have_ops, uint4 *xop, uint2 *xhs, float *xsc, int *cpos,
                    int *ctok, float *gpart, float *upart, uint4 *hop, uint2 *hhs, float *hsc,
-                   float *outp, float *outp2, void *stream, const WView *shared = nullptr,
+                   float *outp, void *stream, const WView *shared = nullptr,
                    const _Float16 *xf = nullptr, float *y = nullptr);
 // whether the register-operand kernels take these expert shapes
 bool moe_q4k_fits(int hidden, int mid);
-// K slices of the down product (1 or 2): outp2 is read when 2
-int moe_q4k_down_slices(int mid);
 int moe_q4k_chunk();
 int isums_per_group(int fmt);
 // F32/F16 weights (hyq_f32mm.hip): y[rows] = W x in f32, or silu(W x) *

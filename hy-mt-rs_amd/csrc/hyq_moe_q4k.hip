@@ -100,11 +100,6 @@ __device__ __forceinline__ uint32_t dword(const uint4 &v, int i)
 
 __device__ __forceinline__ h2 pair_bits(uint32_t b) { return __builtin_bit_cast(h2, b); }
 
-__device__ __forceinline__ _Float16 f16i(uint32_t v, float scale)
-{
-    return (_Float16)(scale * (float)v);
-}
-
 // acc += d * P - dmin * M for one superblock of one row tile. `magic` holds
 // 0x64006400 in a VGPR, so each nibble pair is one v_and_or_b32 (whose mask
 // then takes the one scalar operand gfx9's VOP3 allows). The activations are
@@ -548,7 +543,7 @@ int launch_moe_q4k(WView gate, WView up, WView down, int hidden, int mid, const 
                    const int *order, const int *tiles, const int *ntiles, int max_tiles,
                    int npairs, bool have_ops, uint4 *xop, uint2 *xhs, float *xsc, int *cpos,
                    int *ctok, float *gpart, float *upart, uint4 *hop, uint2 *hhs, float *hsc,
-                   float *outp, float *outp2, void *stream, const WView *shared,
+                   float *outp, void *stream, const WView *shared,
                    const _Float16 *xf, float *y)
 {
     if (!moe_q4k_fits(hidden, mid)) return (int)hipErrorInvalidValue;
@@ -563,8 +558,11 @@ int launch_moe_q4k(WView gate, WView up, WView down, int hidden, int mid, const 
                            st, tiles, ntiles, eoff, order, ptok, max_tiles, cpos, ctok);
     }
     int dev = 0, cus = 0;
-    hipGetDevice(&dev);
-    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    hipError_t err = hipGetDevice(&dev);
+    if (err == hipSuccess)
+        err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (err != hipSuccess) return (int)err;
+    if (cus <= 0) return (int)hipErrorInvalidDevice;
     const dim3 grid(unit_grid(cus));
     hipLaunchKernelGGL(moe_q4k_gate_up_kernel, grid, dim3(256),
                        (size_t)34 * (hidden / moe_kslices(hidden)), st, gate, up, mid, hidden,
@@ -588,8 +586,6 @@ bool moe_q4k_fits(int hidden, int mid)
            mid <= MOE_Q4K_MAX_K && hidden / moe_kslices(hidden) <= MOE_Q4K_MAX_KL &&
            mid <= MOE_Q4K_MAX_KL && hidden % 128 == 0;
 }
-
-int moe_q4k_down_slices(int) { return 1; }
 
 int moe_q4k_chunk() { return CHUNK; }
 

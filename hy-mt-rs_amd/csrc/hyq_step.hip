@@ -22,7 +22,6 @@ namespace hyq {
 namespace {
 
 __device__ __forceinline__ float wave_sum(float v) { return wave::sum64(v); }
-__device__ __forceinline__ float wave_max(float v) { return wave::max64(v); }
 
 // ---- embedding rows (Weight::row_into with device-resident token ids) ----
 // Grid (cols / 256, tokens): row blockIdx.y of out takes token[blockIdx.y]
