@@ -223,3 +223,49 @@ def test_metadata_accessors(hyq):
 def test_tensors_are_listed_in_name_order(hyq):
     g = gg(hyq, build([], [F32_T("zeta"), F32_T("alpha"), F32_T("mid")]))
     assert list(g.tensors()) == ["alpha", "mid", "zeta"]
+
+
+def test_mutated_files_open_or_fail_cleanly(hyq):
+    """Seeded byte mutations of a file with metadata of every kind and two
+    tensors (single bytes set, runs overwritten, cut or extended): each one
+    either opens, and then every accessor answers or raises ValueError, or is
+    rejected with ValueError. The reader takes untrusted files; under a
+    host-AddressSanitizer build of the library this also checks that no
+    mutation reads outside the file."""
+    base = build([("general.architecture", STR, "hunyuan"), ("u", U32, 7), ("i", I32, -3),
+                  ("f", F32, 0.5), ("d", F64, 2.5), ("b", BOOL, True), ("big", U64, 2**40),
+                  ("a", ARR, (STR, ["x", "yz", ""])), ("n", ARR, (U32, [1, 2, 3]))],
+                 [("w0", [4, 2], 0, struct.pack("<8f", *range(8))),
+                  ("w1", [3], 0, struct.pack("<3f", 1.0, 2.0, 3.0))])
+    gg(hyq, base).close()
+    rng = np.random.default_rng(2024)
+    opened = 0
+    for _ in range(1500):
+        b = bytearray(base)
+        kind = rng.integers(4)
+        if kind == 0:
+            b[rng.integers(len(b))] = int(rng.integers(256))
+        elif kind == 1:
+            at = int(rng.integers(len(b)))
+            run = rng.integers(0, 256, int(rng.integers(1, 9)), dtype=np.uint8).tobytes()
+            b[at:at + len(run)] = run
+        elif kind == 2:
+            del b[int(rng.integers(len(b))):]
+        else:
+            b += rng.integers(0, 256, int(rng.integers(1, 64)), dtype=np.uint8).tobytes()
+        try:
+            g = gg(hyq, bytes(b))
+        except ValueError:
+            continue
+        opened += 1
+        for name in g.tensors():
+            g.tensor_bytes(name)
+        for key, get in (("u", g.u64), ("i", g.f64), ("d", g.f64), ("b", g.boolean),
+                         ("general.architecture", g.string), ("a", g.array_len),
+                         ("n", g.array_len), ("big", g.u64)):
+            try:
+                get(key)
+            except ValueError:
+                pass
+        g.close()
+    assert opened > 0  # some mutations leave a valid file (tensor data, string bytes)
